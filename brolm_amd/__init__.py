@@ -1,0 +1,236 @@
+"""brolm_amd — MI355X-native implementation of brolm's quantized Qwen3 decode path.
+
+Python mirror of the C++ API (reference include/brolm/qwen.h,
+include/brolm/qwen_generate.h, include/brolm/detail/generate.h) over the C ABI
+of libbrolm.so.  All compute runs in the native libraries on a gfx950 device;
+there is no Python or CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _native
+from ._native import check
+
+GGML = {"F32": 0, "F16": 1, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "BF16": 30}
+
+__all__ = ["Qwen3Config", "Qwen3Model", "SamplingParams", "GenerateOptions", "generate", "sample_token",
+           "qwen3_hf_to_ggml", "SynthSpec", "write_synth_qwen3", "init", "GGML"]
+
+
+def init() -> None:
+    """brotensor::init(): register the gfx950 device (raises without one)."""
+    check(_native.lib().brolm_init(), "init")
+
+
+def _i32(a) -> "C.Array":
+    arr = np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+    return arr, arr.ctypes.data_as(_native.P_i32)
+
+
+@dataclass
+class Qwen3Config:
+    """Qwen3Config (include/brolm/qwen.h:35-56)."""
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    intermediate_size: int = 3072
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1000000.0
+    tie_word_embeddings: bool = True
+    max_position_embeddings: int = 40960
+
+    def _c(self) -> _native.Qwen3ConfigC:
+        c = _native.Qwen3ConfigC()
+        for f in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+                  "num_key_value_heads", "head_dim", "max_position_embeddings"):
+            setattr(c, f, int(getattr(self, f)))
+        c.rms_norm_eps = float(self.rms_norm_eps)
+        c.rope_theta = float(self.rope_theta)
+        c.tie_word_embeddings = 1 if self.tie_word_embeddings else 0
+        return c
+
+    @staticmethod
+    def from_gguf(path: str) -> "Qwen3Config":
+        c = _native.Qwen3ConfigC()
+        check(_native.lib().brolm_qwen3_config_from_gguf(str(path).encode(), C.byref(c)), "from_gguf")
+        return Qwen3Config(c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
+                           c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.rms_norm_eps, c.rope_theta,
+                           bool(c.tie_word_embeddings), c.max_position_embeddings)
+
+
+def qwen3_hf_to_ggml(hf_name: str) -> str:
+    buf = C.create_string_buffer(256)
+    n = _native.lib().brolm_qwen3_hf_to_ggml(hf_name.encode(), buf, 256)
+    return buf.value.decode() if n > 0 else ""
+
+
+class Qwen3Model:
+    """Qwen3Model (include/brolm/qwen.h:58-157); logits are returned as float32
+    copies of the FP16 device logits."""
+
+    def __init__(self, cfg: Qwen3Config):
+        self.cfg = cfg
+        self._h = _native.lib().brolm_qwen3_create(C.byref(cfg._c()))
+        if not self._h:
+            raise _native.NativeError(_native.lib().brolm_last_error().decode())
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            _native.lib().brolm_qwen3_free(h)
+            self._h = None
+
+    def config(self) -> Qwen3Config:
+        return self.cfg
+
+    def load_weights(self, gguf_path: str) -> None:
+        check(_native.lib().brolm_qwen3_load_gguf(self._h, str(gguf_path).encode()), "load_weights")
+
+    def allocate_cache(self, max_seq_len: int) -> None:
+        check(_native.lib().brolm_qwen3_allocate_cache(self._h, int(max_seq_len)), "allocate_cache")
+
+    def reset_cache(self) -> None:
+        check(_native.lib().brolm_qwen3_reset_cache(self._h), "reset_cache")
+
+    def truncate_cache(self, length: int) -> None:
+        check(_native.lib().brolm_qwen3_truncate_cache(self._h, int(length)), "truncate_cache")
+
+    def cache_len(self) -> int:
+        return _native.lib().brolm_qwen3_cache_len(self._h)
+
+    def forward(self, ids: Sequence[int], want_hidden: bool = False):
+        arr, p = _i32(ids)
+        L = arr.size
+        logits = np.empty((L, self.cfg.vocab_size), np.float32)
+        hidden = np.empty((L, self.cfg.hidden_size), np.float32) if want_hidden else None
+        check(_native.lib().brolm_qwen3_forward(self._h, p, L, logits.ctypes.data_as(_native.P_f32),
+                                                hidden.ctypes.data_as(_native.P_f32) if want_hidden else None),
+              "forward")
+        return (logits, hidden) if want_hidden else logits
+
+    def forward_last(self, ids: Sequence[int]) -> np.ndarray:
+        arr, p = _i32(ids)
+        logits = np.empty((self.cfg.vocab_size,), np.float32)
+        check(_native.lib().brolm_qwen3_forward_last(self._h, p, arr.size, logits.ctypes.data_as(_native.P_f32)),
+              "forward_last")
+        return logits
+
+    def embed_tokens(self, ids: Sequence[int]) -> np.ndarray:
+        arr, p = _i32(ids)
+        out = np.empty((arr.size, self.cfg.hidden_size), np.float16)
+        check(_native.lib().brolm_qwen3_embed_tokens(self._h, p, arr.size, out.ctypes.data_as(_native.P_u16)),
+              "embed_tokens")
+        return out
+
+    def forward_embeds(self, embeds: np.ndarray, want_hidden: bool = False):
+        e = np.ascontiguousarray(embeds, dtype=np.float16)
+        L = e.shape[0]
+        logits = np.empty((L, self.cfg.vocab_size), np.float32)
+        hidden = np.empty((L, self.cfg.hidden_size), np.float32) if want_hidden else None
+        check(_native.lib().brolm_qwen3_forward_embeds(self._h, e.ctypes.data_as(_native.P_u16), L,
+                                                       logits.ctypes.data_as(_native.P_f32),
+                                                       hidden.ctypes.data_as(_native.P_f32) if want_hidden else None),
+              "forward_embeds")
+        return (logits, hidden) if want_hidden else logits
+
+    def decode_greedy(self, token: int, n: int, eos_id: int = -1) -> list[int]:
+        out = np.empty((max(n, 1),), np.int32)
+        k = check(_native.lib().brolm_qwen3_decode_greedy(self._h, int(token), int(n),
+                                                          out.ctypes.data_as(_native.P_i32), int(eos_id)),
+                  "decode_greedy")
+        return out[:k].tolist()
+
+    def time_decode_steps(self, token: int, n: int) -> float:
+        ms = _native.lib().brolm_qwen3_time_decode_steps(self._h, int(token), int(n))
+        if ms < 0:
+            raise _native.NativeError(_native.lib().brolm_last_error().decode())
+        return ms
+
+    def decode_weight_bytes(self) -> int:
+        return int(_native.lib().brolm_qwen3_decode_weight_bytes(self._h))
+
+
+@dataclass
+class SamplingParams:
+    """SamplingParams (include/brolm/detail/generate.h:29-34)."""
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 1.0
+    seed: int = 0
+
+
+@dataclass
+class GenerateOptions:
+    """GenerateOptions (include/brolm/detail/generate.h:57-61)."""
+    max_new_tokens: int = 64
+    sampling: SamplingParams = field(default_factory=SamplingParams)
+    stop_on_eos: bool = True
+    device_greedy: bool = True
+
+
+def generate(model: Qwen3Model, prompt_ids: Sequence[int], eos_id: int, opts: GenerateOptions) -> list[int]:
+    """qwen::generate (include/brolm/qwen_generate.h:45-47): only the new ids."""
+    arr, p = _i32(list(prompt_ids) if len(prompt_ids) else [0])
+    n_prompt = len(prompt_ids)
+    out = np.empty((max(opts.max_new_tokens, 1),), np.int32)
+    s = opts.sampling
+    k = check(_native.lib().brolm_qwen3_generate(model._h, p, n_prompt, int(opts.max_new_tokens), int(eos_id),
+                                                 1 if opts.stop_on_eos else 0, float(s.temperature), int(s.top_k),
+                                                 float(s.top_p), int(s.seed), 1 if opts.device_greedy else 0,
+                                                 out.ctypes.data_as(_native.P_i32)),
+              "generate")
+    return out[:k].tolist()
+
+
+def sample_token(logits: np.ndarray, params: SamplingParams, seed: int) -> int:
+    """sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142)."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    return _native.lib().brolm_sample_token(a.ctypes.data_as(_native.P_f32), a.size, float(params.temperature),
+                                            int(params.top_k), float(params.top_p), int(seed))
+
+
+@dataclass
+class SynthSpec:
+    """Synthetic Qwen3 checkpoint (include/brolm/synth.h)."""
+    vocab: int = 151936
+    hidden: int = 1024
+    intermediate: int = 3072
+    layers: int = 28
+    n_q: int = 16
+    n_kv: int = 8
+    head_dim: int = 128
+    eps: float = 1e-6
+    theta: float = 1000000.0
+    context: int = 40960
+    tied: bool = True
+    embed: str = "Q8_0"
+    q: str = "Q8_0"
+    k: str = "Q8_0"
+    v: str = "Q8_0"
+    o: str = "Q8_0"
+    gate: str = "Q8_0"
+    up: str = "Q8_0"
+    down: str = "Q8_0"
+    output: str = "Q6_K"
+    stddev: float = 0.02
+    seed: int = 0
+
+
+def write_synth_qwen3(spec: SynthSpec, path: str) -> None:
+    s = _native.SynthSpecC()
+    for f in ("vocab", "hidden", "intermediate", "layers", "n_q", "n_kv", "head_dim", "context"):
+        setattr(s, f, int(getattr(spec, f)))
+    s.eps, s.theta, s.stddev = float(spec.eps), float(spec.theta), float(spec.stddev)
+    s.tied = 1 if spec.tied else 0
+    for f in ("embed", "q", "k", "v", "o", "gate", "up", "down", "output"):
+        setattr(s, f + "_type", GGML[getattr(spec, f)])
+    s.seed = int(spec.seed)
+    check(_native.lib().brolm_synth_qwen3_write(C.byref(s), str(path).encode()), "write_synth_qwen3")

@@ -1,0 +1,94 @@
+"""Build the native libraries in-tree.
+
+libbrolm_hip.so  HIP kernels for gfx950 + their C ABI (include/brolm_hip.h)
+libbrolm.so      C++20 host stack (brotensor op surface, GGUF, Qwen3 decoder,
+                 generate, synthetic checkpoints) + its C ABI (include/brolm_c.h)
+
+Both land in brolm_amd/lib/.  Run `python -m brolm_amd.build` or call
+build_all().  Every call recompiles (objects go to _build/).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+PKG = ROOT / "brolm_amd"
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "lib"
+OBJDIR = ROOT / "_build"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+HIPCC = str(ROCM / "bin" / "hipcc")
+ARCH = "gfx950"
+# Packed-FP32 instructions are kept out of every kernel.
+HIP_FLAGS = [
+    "-O3", f"--offload-arch={ARCH}", "-fPIC", "-std=c++20",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+    f"-I{ROOT / 'include'}",
+]
+CXX = os.environ.get("CXX", "g++")
+CXX_FLAGS = [
+    "-O2", "-fPIC", "-std=c++20", "-Wall", "-Wextra", "-Wno-unused-parameter",
+    "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", f"-I{ROOT / 'include'}",
+    f"-I{CSRC / 'host'}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed: {' '.join(cmd[:3])} ... ({r.returncode})")
+
+
+def _jobs() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 4
+    return max(1, min(n, 16))
+
+
+def build_kernels() -> Path:
+    srcs = sorted((CSRC / "kernels").glob("*.hip"))
+    OBJDIR.mkdir(parents=True, exist_ok=True)
+    objs = [OBJDIR / (s.stem + ".hip.o") for s in srcs]
+    with cf.ThreadPoolExecutor(_jobs()) as ex:
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", str(so[0]), "-o", str(so[1])]), zip(srcs, objs)))
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    out = LIBDIR / "libbrolm_hip.so"
+    tmp = out.with_suffix(".so.tmp")
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
+def build_host() -> Path:
+    srcs = sorted((CSRC / "host").glob("*.cpp"))
+    OBJDIR.mkdir(parents=True, exist_ok=True)
+    objs = [OBJDIR / (s.stem + ".cpp.o") for s in srcs]
+    with cf.ThreadPoolExecutor(_jobs()) as ex:
+        list(ex.map(lambda so: _run([CXX, *CXX_FLAGS, "-c", str(so[0]), "-o", str(so[1])]), zip(srcs, objs)))
+    out = LIBDIR / "libbrolm.so"
+    tmp = out.with_suffix(".so.tmp")
+    _run([CXX, "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
+          f"-L{LIBDIR}", "-lbrolm_hip", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}", "-pthread"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all() -> list[Path]:
+    k = build_kernels()
+    h = build_host()
+    return [k, h]
+
+
+if __name__ == "__main__":
+    for p in build_all():
+        print(p)

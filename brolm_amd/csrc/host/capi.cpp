@@ -1,0 +1,270 @@
+// C facade of the Qwen3 stack (include/brolm_c.h).
+#include "brolm_c.h"
+
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "brolm/detail/profile.h"
+#include "brolm/qwen.h"
+#include "brolm/qwen_generate.h"
+#include "brolm/synth.h"
+#include "brotensor/gguf.h"
+#include "brotensor/runtime.h"
+
+struct brolm_qwen3 {
+    std::unique_ptr<brolm::qwen::Qwen3Model> model;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <typename F>
+int guard(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+    } catch (...) {
+        g_err = "unknown C++ exception";
+    }
+    return -1;
+}
+
+brolm::qwen::Qwen3Config to_cfg(const brolm_qwen3_config& c) {
+    brolm::qwen::Qwen3Config q;
+    q.vocab_size = c.vocab_size;
+    q.hidden_size = c.hidden_size;
+    q.intermediate_size = c.intermediate_size;
+    q.num_hidden_layers = c.num_hidden_layers;
+    q.num_attention_heads = c.num_attention_heads;
+    q.num_key_value_heads = c.num_key_value_heads;
+    q.head_dim = c.head_dim;
+    q.rms_norm_eps = c.rms_norm_eps;
+    q.rope_theta = c.rope_theta;
+    q.tie_word_embeddings = c.tie_word_embeddings != 0;
+    q.max_position_embeddings = c.max_position_embeddings;
+    return q;
+}
+
+void from_cfg(const brolm::qwen::Qwen3Config& q, brolm_qwen3_config* c) {
+    c->vocab_size = q.vocab_size;
+    c->hidden_size = q.hidden_size;
+    c->intermediate_size = q.intermediate_size;
+    c->num_hidden_layers = q.num_hidden_layers;
+    c->num_attention_heads = q.num_attention_heads;
+    c->num_key_value_heads = q.num_key_value_heads;
+    c->head_dim = q.head_dim;
+    c->rms_norm_eps = q.rms_norm_eps;
+    c->rope_theta = q.rope_theta;
+    c->tie_word_embeddings = q.tie_word_embeddings ? 1 : 0;
+    c->max_position_embeddings = q.max_position_embeddings;
+}
+
+void to_host_f32(const brotensor::Tensor& t, float* dst) {
+    const std::vector<float> v = t.to_host_vector();
+    std::memcpy(dst, v.data(), v.size() * sizeof(float));
+}
+
+brolm::qwen::Qwen3Model& model_of(brolm_qwen3* m) {
+    if (!m || !m->model) throw std::runtime_error("null model handle");
+    return *m->model;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* brolm_last_error(void) { return g_err.c_str(); }
+
+int brolm_init(void) {
+    return guard([] { brotensor::init(); });
+}
+
+int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* s, const char* path) {
+    return guard([&] {
+        if (!s || !path) throw std::runtime_error("synth: null argument");
+        brolm::synth::Qwen3Spec q;
+        q.vocab = s->vocab; q.hidden = s->hidden; q.intermediate = s->intermediate; q.layers = s->layers;
+        q.n_q = s->n_q; q.n_kv = s->n_kv; q.head_dim = s->head_dim; q.eps = s->eps; q.theta = s->theta;
+        q.context = s->context; q.tied = s->tied != 0;
+        q.embed = brotensor::dtype_from_ggml(s->embed_type);
+        q.q = brotensor::dtype_from_ggml(s->q_type);
+        q.k = brotensor::dtype_from_ggml(s->k_type);
+        q.v = brotensor::dtype_from_ggml(s->v_type);
+        q.o = brotensor::dtype_from_ggml(s->o_type);
+        q.gate = brotensor::dtype_from_ggml(s->gate_type);
+        q.up = brotensor::dtype_from_ggml(s->up_type);
+        q.down = brotensor::dtype_from_ggml(s->down_type);
+        q.output = brotensor::dtype_from_ggml(s->output_type);
+        q.stddev = s->stddev;
+        q.seed = s->seed;
+        brolm::synth::write_qwen3_gguf(q, path);
+    });
+}
+
+int brolm_synth_normal_bf16(uint64_t key, int64_t n, float stddev, float* out) {
+    return guard([&] { brolm::synth::normal_bf16(key, n, stddev, out); });
+}
+
+uint64_t brolm_synth_tensor_key(uint64_t seed, const char* name) { return brolm::synth::tensor_key(seed, name); }
+
+int brolm_synth_quantize(int ggml_type, const float* src, int64_t n, uint8_t* dst) {
+    return guard([&] { brolm::synth::quantize(brotensor::dtype_from_ggml(ggml_type), src, n, dst); });
+}
+
+int brolm_qwen3_hf_to_ggml(const char* hf_name, char* out, int cap) {
+    const std::string s = brolm::qwen::qwen3_hf_to_ggml(hf_name ? hf_name : "");
+    if (out && cap > 0) {
+        const std::size_t n = std::min<std::size_t>(s.size(), static_cast<std::size_t>(cap - 1));
+        std::memcpy(out, s.data(), n);
+        out[n] = 0;
+    }
+    return static_cast<int>(s.size());
+}
+
+int brolm_qwen3_config_from_gguf(const char* path, brolm_qwen3_config* out) {
+    return guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        from_cfg(brolm::qwen::Qwen3Config::from_gguf(f), out);
+    });
+}
+
+int brolm_gguf_tensor_count(const char* path, int64_t* out) {
+    return guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        *out = static_cast<int64_t>(f.tensor_count());
+    });
+}
+
+int brolm_gguf_tensor_info(const char* path, const char* name, int* ggml_type, int64_t* dims4, int* ndims,
+                           int64_t* nbytes) {
+    return guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto* t = f.find_tensor(name);
+        if (!t) throw std::runtime_error(std::string("gguf: no tensor '") + name + "'");
+        *ggml_type = brotensor::dtype_to_ggml(t->dtype);
+        *ndims = static_cast<int>(t->dims.size());
+        for (int i = 0; i < 4; ++i) dims4[i] = i < *ndims ? t->dims[static_cast<std::size_t>(i)] : 1;
+        *nbytes = static_cast<int64_t>(t->nbytes);
+    });
+}
+
+brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg) {
+    brolm_qwen3* out = nullptr;
+    const int rc = guard([&] {
+        if (!cfg) throw std::runtime_error("null config");
+        auto h = std::make_unique<brolm_qwen3>();
+        h->model = std::make_unique<brolm::qwen::Qwen3Model>(to_cfg(*cfg));
+        out = h.release();
+    });
+    return rc == 0 ? out : nullptr;
+}
+
+void brolm_qwen3_free(brolm_qwen3* m) { delete m; }
+
+int brolm_qwen3_load_gguf(brolm_qwen3* m, const char* path) {
+    return guard([&] {
+        brotensor::init();
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        model_of(m).load_weights(f);
+    });
+}
+
+int brolm_qwen3_allocate_cache(brolm_qwen3* m, int n) { return guard([&] { model_of(m).allocate_cache(n); }); }
+int brolm_qwen3_reset_cache(brolm_qwen3* m) { return guard([&] { model_of(m).reset_cache(); }); }
+int brolm_qwen3_truncate_cache(brolm_qwen3* m, int n) { return guard([&] { model_of(m).truncate_cache(n); }); }
+int brolm_qwen3_cache_len(const brolm_qwen3* m) { return (m && m->model) ? m->model->cache_len() : -1; }
+
+int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits, float* hidden) {
+    return guard([&] {
+        brotensor::Tensor lg, hd;
+        model_of(m).forward(ids, L, lg, hidden ? &hd : nullptr);
+        if (logits) to_host_f32(lg, logits);
+        if (hidden) to_host_f32(hd, hidden);
+    });
+}
+
+int brolm_qwen3_forward_last(brolm_qwen3* m, const int32_t* ids, int L, float* logits) {
+    return guard([&] {
+        brotensor::Tensor lg;
+        model_of(m).forward_last(ids, L, lg);
+        if (logits) to_host_f32(lg, logits);
+    });
+}
+
+int brolm_qwen3_embed_tokens(brolm_qwen3* m, const int32_t* ids, int L, uint16_t* out) {
+    return guard([&] {
+        brotensor::Tensor e;
+        model_of(m).embed_tokens(ids, L, e);
+        e.copy_to_host_fp16(out);
+    });
+}
+
+int brolm_qwen3_forward_embeds(brolm_qwen3* m, const uint16_t* embeds, int L, float* logits, float* hidden) {
+    return guard([&] {
+        brolm::qwen::Qwen3Model& q = model_of(m);
+        brotensor::Tensor e = brotensor::Tensor::from_host_fp16(embeds, L, q.config().hidden_size);
+        brotensor::Tensor lg, hd;
+        q.forward_embeds(e, L, lg, hidden ? &hd : nullptr);
+        if (logits) to_host_f32(lg, logits);
+        if (hidden) to_host_f32(hd, hidden);
+    });
+}
+
+int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, int max_new, int eos_id,
+                         int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
+                         int device_greedy, int32_t* out) {
+    int count = -1;
+    const int rc = guard([&] {
+        brolm::qwen::GenerateOptions o;
+        o.max_new_tokens = max_new;
+        o.stop_on_eos = stop_on_eos != 0;
+        o.sampling.temperature = temperature;
+        o.sampling.top_k = top_k;
+        o.sampling.top_p = top_p;
+        o.sampling.seed = seed;
+        o.device_greedy = device_greedy != 0;
+        const std::vector<int32_t> p(prompt, prompt + (n_prompt > 0 ? n_prompt : 0));
+        const std::vector<int32_t> g = brolm::qwen::generate(model_of(m), p, eos_id, o);
+        std::memcpy(out, g.data(), g.size() * sizeof(int32_t));
+        count = static_cast<int>(g.size());
+    });
+    return rc == 0 ? count : -1;
+}
+
+int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id) {
+    int count = -1;
+    const int rc = guard([&] { count = model_of(m).core().decode_greedy(token, n, out, eos_id); });
+    return rc == 0 ? count : -1;
+}
+
+double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n) {
+    double ms = -1.0;
+    const int rc = guard([&] { ms = model_of(m).core().time_decode_steps(token, n); });
+    return rc == 0 ? ms : -1.0;
+}
+
+int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m) {
+    return (m && m->model) ? const_cast<brolm::qwen::Qwen3Model&>(*m->model).core().decode_weight_bytes() : -1;
+}
+
+int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed) {
+    brolm::detail::SamplingParams p;
+    p.temperature = temperature;
+    p.top_k = top_k;
+    p.top_p = top_p;
+    std::mt19937_64 rng(seed);
+    return brolm::detail::sample_token(logits, vocab, p, rng);
+}
+
+void brolm_profile_reset(void) { brolm::detail::profile::reset(); }
+void brolm_profile_report(void) { brolm::detail::profile::report(); }
+int brolm_profile_enabled(void) { return brolm::detail::profile::enabled() ? 1 : 0; }
+
+}  // extern "C"

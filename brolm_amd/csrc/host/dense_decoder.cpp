@@ -1,0 +1,512 @@
+// DenseDecoder (reference src/detail/dense_decoder.cpp), MI355X structure:
+// FP32 residual stream, op-surface prefill, fused + graph-captured decode step.
+#include "brolm/detail/dense_decoder.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "brolm/detail/compute.h"
+#include "brolm/detail/device.h"
+#include "brolm/detail/profile.h"
+#include "brolm/detail/weights.h"
+#include "brolm_hip.h"
+#include "brotensor/ops.h"
+#include "brotensor/runtime.h"
+#include "hip_util.h"
+
+namespace brolm::detail {
+
+namespace bt = ::brotensor;
+
+namespace {
+
+[[noreturn]] void fail(const std::string& msg) { throw std::runtime_error("DenseDecoder: " + msg); }
+
+bt::Tensor make_idx_device(const int32_t* host, int n) {
+    bt::Tensor t = bt::Tensor::empty_on(bt::Device::ROCm, n, 1, bt::Dtype::INT32);
+    hipx::h2d(t.data, host, static_cast<std::size_t>(n) * sizeof(int32_t));
+    return t;
+}
+
+bool env_flag(const char* name) {
+    const char* v = std::getenv(name);
+    return v != nullptr && *v != '\0' && !(v[0] == '0' && v[1] == '\0');
+}
+
+int ggml_of(const bt::Tensor& t) { return bt::dtype_to_ggml(t.dtype); }
+
+std::int64_t tensor_bytes(const bt::Tensor& t) { return static_cast<std::int64_t>(t.bytes()); }
+
+}  // namespace
+
+// ─── decode session ──────────────────────────────────────────────────────────
+//
+// Device scalars (scal): [0] token fed this step, [1] its position, [2] argmax
+// of this step's logits, [3] history count, [4 ..) history of argmax ids.
+// The captured step ends with the advance kernel (token <- argmax, pos += 1),
+// so back-to-back replays decode greedily with no host round trip; the host
+// re-stages token/pos whenever it drives the step itself.
+
+struct DecodeGraphSession {
+    static constexpr int kHist = 4096;
+    int cap = 0;
+    bx_decode_dims dims{};
+    std::vector<bx_decode_layer> layers;
+    void* ws = nullptr;
+    int32_t* scal = nullptr;
+    uint16_t* logits = nullptr;
+    void* argmax_ws = nullptr;
+    int32_t* pinned = nullptr;  // host staging {tok, pos, next, count}
+    hipEvent_t staged = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool use_graph = true;
+
+    ~DecodeGraphSession() {
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (staged) (void)hipEventDestroy(staged);
+        if (pinned) (void)hipHostFree(pinned);
+        if (ws) (void)hipFree(ws);
+        if (scal) (void)hipFree(scal);
+        if (logits) (void)hipFree(logits);
+        if (argmax_ws) (void)hipFree(argmax_ws);
+    }
+};
+
+// ─── ctor / dtor ─────────────────────────────────────────────────────────────
+
+DenseDecoder::DenseDecoder(const DenseDecoderConfig& cfg) : cfg_(cfg) {
+    if (cfg_.hidden_size <= 0 || cfg_.intermediate_size <= 0 || cfg_.num_hidden_layers <= 0 ||
+        cfg_.vocab_size <= 0 || cfg_.head_dim <= 0)
+        fail("config has non-positive dimension");
+    if (cfg_.num_attention_heads <= 0 || cfg_.num_key_value_heads <= 0)
+        fail("num_attention_heads / num_key_value_heads must be positive");
+    if (cfg_.num_attention_heads % cfg_.num_key_value_heads != 0)
+        fail("num_attention_heads must be a multiple of num_key_value_heads");
+    if (cfg_.head_dim % 2 != 0) fail("head_dim must be even (RoPE rotates dimension pairs)");
+    layers_.resize(static_cast<std::size_t>(cfg_.num_hidden_layers));
+}
+
+DenseDecoder::~DenseDecoder() = default;
+DenseDecoder::DenseDecoder(DenseDecoder&&) noexcept = default;
+DenseDecoder& DenseDecoder::operator=(DenseDecoder&&) noexcept = default;
+
+// ─── load_weights (dense_decoder.cpp:121-192) ───────────────────────────────
+
+void DenseDecoder::load_weights(const weights::Source& src) {
+    invalidate_graph_();
+    const int V = cfg_.vocab_size, H = cfg_.hidden_size, F = cfg_.intermediate_size, HD = cfg_.head_dim;
+    const int n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
+    const int q_dim = n_q * HD, kv_dim = n_kv * HD;
+
+    src.upload_compute_dequant("model.embed_tokens.weight", V, H, embed_tokens_, "embed_tokens.weight");
+    for (int i = 0; i < cfg_.num_hidden_layers; ++i) {
+        const std::string p = "model.layers." + std::to_string(i) + ".";
+        Layer& L = layers_[static_cast<std::size_t>(i)];
+        src.upload_compute_dequant(p + "input_layernorm.weight", H, 1, L.input_ln, "input_layernorm.weight");
+        src.upload_compute_rope_permuted(p + "self_attn.q_proj.weight", q_dim, H, n_q, HD, L.Wq, "q_proj.weight");
+        src.upload_compute_rope_permuted(p + "self_attn.k_proj.weight", kv_dim, H, n_kv, HD, L.Wk, "k_proj.weight");
+        src.upload_compute_checked(p + "self_attn.v_proj.weight", kv_dim, H, L.Wv, "v_proj.weight");
+        src.upload_compute_checked(p + "self_attn.o_proj.weight", H, q_dim, L.Wo, "o_proj.weight");
+        if (cfg_.use_qk_norm) {
+            src.upload_compute_rope_permuted(p + "self_attn.q_norm.weight", HD, 1, 1, HD, L.q_norm, "q_norm.weight");
+            src.upload_compute_rope_permuted(p + "self_attn.k_norm.weight", HD, 1, 1, HD, L.k_norm, "k_norm.weight");
+        }
+        src.upload_compute_dequant(p + "post_attention_layernorm.weight", H, 1, L.post_attn_ln,
+                                   "post_attention_layernorm.weight");
+        src.upload_compute_checked(p + "mlp.gate_proj.weight", F, H, L.gate_W, "gate_proj.weight");
+        src.upload_compute_checked(p + "mlp.up_proj.weight", F, H, L.up_W, "up_proj.weight");
+        src.upload_compute_checked(p + "mlp.down_proj.weight", H, F, L.down_W, "down_proj.weight");
+    }
+    src.upload_compute_dequant("model.norm.weight", H, 1, final_norm_, "model.norm.weight");
+    if (src.has("lm_head.weight")) {
+        src.upload_compute_checked("lm_head.weight", V, H, lm_head_, "lm_head.weight");
+    } else {
+        if (!cfg_.tie_word_embeddings) fail("load_weights: lm_head.weight missing and tie_word_embeddings is false");
+        lm_head_ = embed_tokens_.clone();
+    }
+    bt::sync_all();
+}
+
+// ─── cache management (dense_decoder.cpp:196-227) ───────────────────────────
+
+void DenseDecoder::allocate_cache(int max_seq_len) {
+    if (max_seq_len <= 0) fail("allocate_cache: max_seq_len must be positive");
+    if (max_seq_len != max_seq_len_) invalidate_graph_();
+    const int cols = cfg_.num_key_value_heads * cfg_.head_dim;
+    for (Layer& L : layers_) {
+        resize_like(L.K_cache, max_seq_len, cols, bt::Dtype::FP16, bt::Device::ROCm);
+        resize_like(L.V_cache, max_seq_len, cols, bt::Dtype::FP16, bt::Device::ROCm);
+    }
+    max_seq_len_ = max_seq_len;
+    cache_len_ = 0;
+    ensure_rope_table_();
+}
+
+void DenseDecoder::ensure_rope_table_() {
+    const int half = cfg_.head_dim / 2;
+    if (rope_cos_.data && rope_cos_.rows == max_seq_len_) return;
+    std::vector<float> c(static_cast<std::size_t>(max_seq_len_) * half), s(c.size());
+    bx_rope_table_host(c.data(), s.data(), max_seq_len_, cfg_.head_dim, cfg_.rope_theta);
+    rope_cos_ = bt::Tensor::from_host_on(bt::Device::ROCm, c.data(), max_seq_len_, half);
+    rope_sin_ = bt::Tensor::from_host_on(bt::Device::ROCm, s.data(), max_seq_len_, half);
+}
+
+void DenseDecoder::reset_cache() { cache_len_ = 0; }
+
+void DenseDecoder::truncate_cache(int len) {
+    if (len < 0) fail("truncate_cache: len must be non-negative");
+    if (len > cache_len_) fail("truncate_cache: len exceeds current cache_len");
+    cache_len_ = len;
+}
+
+// ─── forward (dense_decoder.cpp:231-329) ────────────────────────────────────
+
+void DenseDecoder::embed_tokens(const int32_t* ids, int L, bt::Tensor& out) {
+    if (!ids) fail("embed_tokens: ids pointer is null");
+    if (L <= 0) fail("embed_tokens: L must be positive");
+    if (embed_tokens_.size() == 0) fail("embed_tokens: weights not loaded");
+    for (int i = 0; i < L; ++i)
+        if (ids[i] < 0 || ids[i] >= cfg_.vocab_size) fail("embed_tokens: token id out of range");
+    bt::Tensor idx = make_idx_device(ids, L);
+    bt::embedding_lookup_forward(embed_tokens_, static_cast<const int32_t*>(idx.data), L, out);
+    out = out.clone();
+}
+
+static void check_forward(const char* what, const int32_t* ids, int L, bool loaded, int max_seq, int cache_len,
+                          int vocab) {
+    if (!ids) fail(std::string(what) + ": ids pointer is null");
+    if (L <= 0) fail(std::string(what) + ": L must be positive");
+    if (!loaded) fail(std::string(what) + ": weights not loaded");
+    if (max_seq == 0) fail(std::string(what) + ": cache not allocated");
+    if (cache_len + L > max_seq) fail(std::string(what) + ": cache_len + L exceeds allocated cache capacity");
+    for (int i = 0; i < L; ++i)
+        if (ids[i] < 0 || ids[i] >= vocab) fail(std::string(what) + ": token id out of range");
+}
+
+void DenseDecoder::forward(const int32_t* ids, int L, bt::Tensor& logits_out, bt::Tensor* hidden_out) {
+    check_forward("forward", ids, L, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
+    {
+        profile::ScopedStage ps(profile::Stage::idx_upload);
+        ids_dev_ = make_idx_device(ids, L);
+    }
+    {
+        profile::ScopedStage ps(profile::Stage::embed);
+        resize_like(h_, L, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+        hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                                  embed_tokens_.cols, static_cast<const int32_t*>(ids_dev_.data), L,
+                                  static_cast<float*>(h_.data), bt::stream()),
+                 "embedding");
+    }
+    run_layers_(L, logits_out, hidden_out);
+}
+
+void DenseDecoder::forward_last(const int32_t* ids, int L, bt::Tensor& logits_out) {
+    check_forward("forward_last", ids, L, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
+    if (L == 1 && !profile::enabled()) {
+        bx_decode_dims d{};
+        d.hidden = cfg_.hidden_size; d.intermediate = cfg_.intermediate_size;
+        d.n_q = cfg_.num_attention_heads; d.n_kv = cfg_.num_key_value_heads; d.head_dim = cfg_.head_dim;
+        d.vocab = cfg_.vocab_size; d.cap = max_seq_len_; d.eps = cfg_.rms_norm_eps;
+        d.qkv_type_q = ggml_of(layers_[0].Wq); d.qkv_type_k = ggml_of(layers_[0].Wk);
+        d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
+        d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
+        d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
+        if (cfg_.use_qk_norm && bx_decode_ws_bytes(&d) != 0) {
+            decode_step_(ids[0], logits_out);
+            return;
+        }
+    }
+    {
+        profile::ScopedStage ps(profile::Stage::idx_upload);
+        ids_dev_ = make_idx_device(ids, L);
+    }
+    {
+        profile::ScopedStage ps(profile::Stage::embed);
+        resize_like(h_, L, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+        hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                                  embed_tokens_.cols, static_cast<const int32_t*>(ids_dev_.data), L,
+                                  static_cast<float*>(h_.data), bt::stream()),
+                 "embedding");
+    }
+    run_layers_(L, logits_out, nullptr, /*logits_last_row_only=*/true);
+}
+
+void DenseDecoder::forward_embeds(const bt::Tensor& embeds, int L, bt::Tensor& logits_out, bt::Tensor* hidden_out) {
+    if (L <= 0) fail("forward_embeds: L must be positive");
+    if (embed_tokens_.size() == 0) fail("forward_embeds: weights not loaded");
+    if (max_seq_len_ == 0) fail("forward_embeds: cache not allocated");
+    if (cache_len_ + L > max_seq_len_) fail("forward_embeds: cache_len + L exceeds allocated cache capacity");
+    if (embeds.rows != L || embeds.cols != cfg_.hidden_size) fail("forward_embeds: embeds must be (L, hidden_size)");
+    if (embeds.dtype != bt::Dtype::FP16 || embeds.device != bt::Device::ROCm)
+        fail("forward_embeds: embeds must be FP16 on the ROCm device");
+    resize_like(h_, L, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+    hipx::bx(bx_dequant_to_f32(BX_TYPE_F16, embeds.data, static_cast<float*>(h_.data), L, cfg_.hidden_size,
+                               bt::stream()),
+             "forward_embeds");
+    run_layers_(L, logits_out, hidden_out);
+}
+
+// ─── op-surface layer stack (dense_decoder.cpp:526-681) ─────────────────────
+
+void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden_out, bool logits_last_row_only) {
+    const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
+    const float eps = cfg_.rms_norm_eps;
+    const int seq_offset = cache_len_;
+
+    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst) {
+        const int rows = src.rows;
+        bt::Tensor v = bt::Tensor::view(src.device, src.data, rows * num_heads, HD, src.dtype);
+        bt::rms_norm_forward(v, gain, eps, dst);
+        dst.rows = rows;
+        dst.cols = num_heads * HD;
+    };
+
+    namespace prof = profile;
+    using PS = profile::Stage;
+    for (Layer& layer : layers_) {
+        { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.input_ln, eps, norm_); }
+        {
+            prof::ScopedStage ps(PS::qkv_proj);
+            linear_batched(layer.Wq, nullptr, norm_, q_);
+            linear_batched(layer.Wk, nullptr, norm_, k_);
+            linear_batched(layer.Wv, nullptr, norm_, v_);
+        }
+        bt::Tensor* q_attn = &q_;
+        bt::Tensor* k_attn = &k_;
+        if (cfg_.use_qk_norm) {
+            prof::ScopedStage ps(PS::qk_norm);
+            headnorm(q_, n_q, layer.q_norm, qn_);
+            headnorm(k_, n_kv, layer.k_norm, kn_);
+            q_attn = &qn_;
+            k_attn = &kn_;
+        }
+        {
+            prof::ScopedStage ps(PS::rope);
+            bt::rope_forward(*q_attn, HD, n_q, seq_offset, cfg_.rope_theta, *q_attn);
+            bt::rope_forward(*k_attn, HD, n_kv, seq_offset, cfg_.rope_theta, *k_attn);
+        }
+        { prof::ScopedStage ps(PS::kv_append); bt::kv_cache_append(*k_attn, v_, cache_len_, layer.K_cache, layer.V_cache); }
+        {
+            prof::ScopedStage ps(PS::attention);
+            bt::flash_attention_decode(*q_attn, layer.K_cache, layer.V_cache, cache_len_ + L, n_q, n_kv, attn_);
+        }
+        { prof::ScopedStage ps(PS::o_proj); linear_batched(layer.Wo, nullptr, attn_, proj_); }
+        { prof::ScopedStage ps(PS::residual_add); bt::add_inplace(h_, proj_); }
+        { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_); }
+        {
+            prof::ScopedStage ps(PS::mlp_proj);
+            linear_batched(layer.gate_W, nullptr, norm_, gate_);
+            linear_batched(layer.up_W, nullptr, norm_, up_);
+        }
+        {
+            prof::ScopedStage ps(PS::swiglu);
+            bt::silu_forward(gate_, gate_);
+            bt::mul_inplace(gate_, up_);
+        }
+        { prof::ScopedStage ps(PS::mlp_proj); linear_batched(layer.down_W, nullptr, gate_, proj_); }
+        { prof::ScopedStage ps(PS::residual_add); bt::add_inplace(h_, proj_); }
+    }
+    {
+        prof::ScopedStage ps(PS::final_norm);
+        bt::rms_norm_forward(h_, final_norm_, eps, norm_);
+        if (hidden_out) *hidden_out = norm_.clone();
+    }
+    {
+        prof::ScopedStage ps(PS::lm_head);
+        if (logits_last_row_only && L > 1) {
+            bt::Tensor last = bt::Tensor::view(
+                norm_.device,
+                static_cast<char*>(norm_.data) + static_cast<std::size_t>(L - 1) * norm_.cols * 2, 1, norm_.cols,
+                norm_.dtype);
+            linear_batched(lm_head_, nullptr, last, logits_out);
+        } else {
+            linear_batched(lm_head_, nullptr, norm_, logits_out);
+        }
+    }
+    cache_len_ += L;
+}
+
+// ─── fused decode step ──────────────────────────────────────────────────────
+
+void DenseDecoder::invalidate_graph_() { graph_.reset(); }
+
+DecodeGraphSession& DenseDecoder::session_() {
+    if (graph_ && graph_->cap == max_seq_len_) return *graph_;
+    graph_.reset();
+    auto s = std::make_unique<DecodeGraphSession>();
+    s->cap = max_seq_len_;
+    bx_decode_dims& d = s->dims;
+    d.hidden = cfg_.hidden_size; d.intermediate = cfg_.intermediate_size;
+    d.n_q = cfg_.num_attention_heads; d.n_kv = cfg_.num_key_value_heads; d.head_dim = cfg_.head_dim;
+    d.vocab = cfg_.vocab_size; d.cap = max_seq_len_; d.eps = cfg_.rms_norm_eps;
+    d.qkv_type_q = ggml_of(layers_[0].Wq); d.qkv_type_k = ggml_of(layers_[0].Wk);
+    d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
+    d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
+    d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
+    for (const Layer& L : layers_) {
+        if (ggml_of(L.Wq) != d.qkv_type_q || ggml_of(L.Wk) != d.qkv_type_k || ggml_of(L.Wv) != d.qkv_type_v ||
+            ggml_of(L.Wo) != d.o_type || ggml_of(L.gate_W) != d.gate_type || ggml_of(L.up_W) != d.up_type ||
+            ggml_of(L.down_W) != d.down_type)
+            fail("decode step: per-layer weight types must match across layers");
+        bx_decode_layer bl{};
+        bl.in_ln = L.input_ln.data; bl.q_norm = L.q_norm.data; bl.k_norm = L.k_norm.data;
+        bl.post_ln = L.post_attn_ln.data;
+        bl.Wq = L.Wq.data; bl.Wk = L.Wk.data; bl.Wv = L.Wv.data; bl.Wo = L.Wo.data;
+        bl.Wg = L.gate_W.data; bl.Wu = L.up_W.data; bl.Wd = L.down_W.data;
+        bl.Kc = L.K_cache.data; bl.Vc = L.V_cache.data;
+        s->layers.push_back(bl);
+    }
+    const std::size_t wsb = bx_decode_ws_bytes(&d);
+    if (wsb == 0) fail(std::string("decode step: unsupported shape: ") + bx_last_error());
+    hipx::check(hipMalloc(&s->ws, wsb), "hipMalloc decode ws");
+    hipx::check(hipMalloc(reinterpret_cast<void**>(&s->scal), (4 + DecodeGraphSession::kHist) * sizeof(int32_t)),
+                "hipMalloc decode scalars");
+    hipx::check(hipMemsetAsync(s->scal, 0, (4 + DecodeGraphSession::kHist) * sizeof(int32_t), hipx::stream()),
+                "memset scalars");
+    hipx::check(hipMalloc(reinterpret_cast<void**>(&s->logits), static_cast<std::size_t>(cfg_.vocab_size) * 2),
+                "hipMalloc logits");
+    hipx::check(hipMalloc(&s->argmax_ws, bx_argmax_workspace_bytes(cfg_.vocab_size)), "hipMalloc argmax ws");
+    hipx::check(hipHostMalloc(reinterpret_cast<void**>(&s->pinned), 4 * sizeof(int32_t), hipHostMallocDefault),
+                "hipHostMalloc");
+    hipx::check(hipEventCreateWithFlags(&s->staged, hipEventDisableTiming), "hipEventCreate");
+    s->use_graph = !env_flag("BROLM_NO_GRAPH");
+    hipx::sync();
+    graph_ = std::move(s);
+    return *graph_;
+}
+
+// Enqueue one fused step on the stream (captured or eager).
+static void enqueue_step(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
+                         const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
+    void* st = bt::stream();
+    int32_t* tok = s.scal + 0;
+    int32_t* pos = s.scal + 1;
+    int32_t* next = s.scal + 2;
+    int32_t* count = s.scal + 3;
+    int32_t* hist = s.scal + 4;
+    hipx::bx(bx_decode_embed(&s.dims, static_cast<const uint16_t*>(embed.data), tok, s.ws, st), "decode_embed");
+    for (const bx_decode_layer& L : s.layers)
+        hipx::bx(bx_decode_layer_run(&s.dims, &L, pos, static_cast<const float*>(cos.data),
+                                     static_cast<const float*>(sin.data), s.ws, st),
+                 "decode_layer");
+    hipx::bx(bx_decode_head(&s.dims, static_cast<const uint16_t*>(final_norm.data), lm_head.data, s.logits, s.ws, st),
+             "decode_head");
+    hipx::bx(bx_argmax_f16(s.logits, s.dims.vocab, next, s.argmax_ws, st), "decode_argmax");
+    hipx::bx(bx_decode_advance(tok, pos, next, hist, count, st), "decode_advance");
+}
+
+static void stage_step(DecodeGraphSession& s, int32_t token, int32_t pos) {
+    // The previous staging copy must have consumed the pinned buffer.
+    hipx::check(hipEventSynchronize(s.staged), "hipEventSynchronize");
+    s.pinned[0] = token;
+    s.pinned[1] = pos;
+    s.pinned[2] = 0;
+    s.pinned[3] = 0;
+    hipx::check(hipMemcpyAsync(s.scal, s.pinned, 4 * sizeof(int32_t), hipMemcpyHostToDevice, hipx::stream()),
+                "stage step");
+    hipx::check(hipEventRecord(s.staged, hipx::stream()), "hipEventRecord");
+}
+
+static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, const bt::Tensor& final_norm,
+                         const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
+    if (s.use_graph && !s.exec) {
+        hipStream_t st = hipx::stream();
+        hipx::check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            enqueue_step(s, embed, final_norm, lm_head, cos, sin);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(st, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        hipx::check(hipStreamEndCapture(st, &s.graph), "hipStreamEndCapture");
+        hipx::check(hipGraphInstantiate(&s.exec, s.graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    for (int i = 0; i < n; ++i) {
+        if (s.use_graph) hipx::check(hipGraphLaunch(s.exec, hipx::stream()), "hipGraphLaunch");
+        else enqueue_step(s, embed, final_norm, lm_head, cos, sin);
+    }
+}
+
+void DenseDecoder::decode_step_(int32_t token, bt::Tensor& logits_out) {
+    DecodeGraphSession& s = session_();
+    stage_step(s, token, cache_len_);
+    launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+    resize_like(logits_out, 1, cfg_.vocab_size, bt::Dtype::FP16, bt::Device::ROCm);
+    hipx::check(hipMemcpyAsync(logits_out.data, s.logits, static_cast<std::size_t>(cfg_.vocab_size) * 2,
+                               hipMemcpyDeviceToDevice, hipx::stream()),
+                "copy logits");
+    cache_len_ += 1;
+}
+
+int DenseDecoder::decode_greedy(int32_t token, int n, int32_t* out, int eos_id) {
+    if (n <= 0) return 0;
+    check_forward("decode_greedy", &token, 1, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
+    if (cache_len_ + n > max_seq_len_) fail("decode_greedy: cache_len + n exceeds allocated cache capacity");
+    DecodeGraphSession& s = session_();
+    int done = 0;
+    int32_t cur = token;
+    while (done < n) {
+        const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
+        stage_step(s, cur, cache_len_);
+        launch_steps(s, chunk, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+        hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
+        for (int i = 0; i < chunk; ++i) {
+            if (eos_id >= 0 && out[done + i] == eos_id) {
+                cache_len_ += i + 1;
+                return done + i + 1;
+            }
+        }
+        cache_len_ += chunk;
+        done += chunk;
+        cur = out[done - 1];
+    }
+    return done;
+}
+
+double DenseDecoder::time_decode_steps(int32_t token, int n) {
+    if (n <= 0) return 0.0;
+    check_forward("time_decode_steps", &token, 1, embed_tokens_.size() != 0, max_seq_len_, cache_len_,
+                  cfg_.vocab_size);
+    if (cache_len_ + n > max_seq_len_) fail("time_decode_steps: cache_len + n exceeds allocated cache capacity");
+    DecodeGraphSession& s = session_();
+    stage_step(s, token, cache_len_);
+    launch_steps(s, 0, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);  // capture outside timing
+    hipEvent_t e0, e1;
+    hipx::check(hipEventCreate(&e0), "hipEventCreate");
+    hipx::check(hipEventCreate(&e1), "hipEventCreate");
+    hipx::check(hipEventRecord(e0, hipx::stream()), "hipEventRecord");
+    launch_steps(s, n, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+    hipx::check(hipEventRecord(e1, hipx::stream()), "hipEventRecord");
+    hipx::check(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.f;
+    hipx::check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    cache_len_ += n;
+    return static_cast<double>(ms) / n;
+}
+
+std::int64_t DenseDecoder::decode_weight_bytes() const {
+    std::int64_t b = 0;
+    for (const Layer& L : layers_) {
+        b += tensor_bytes(L.Wq) + tensor_bytes(L.Wk) + tensor_bytes(L.Wv) + tensor_bytes(L.Wo);
+        b += tensor_bytes(L.gate_W) + tensor_bytes(L.up_W) + tensor_bytes(L.down_W);
+        b += tensor_bytes(L.input_ln) + tensor_bytes(L.post_attn_ln) + tensor_bytes(L.q_norm) + tensor_bytes(L.k_norm);
+    }
+    b += tensor_bytes(lm_head_) + tensor_bytes(final_norm_);
+    b += static_cast<std::int64_t>(cfg_.hidden_size) * 2;  // one embedding row
+    return b;
+}
+
+}  // namespace brolm::detail

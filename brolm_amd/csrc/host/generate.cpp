@@ -1,0 +1,100 @@
+// Sampler and logits download (reference src/detail/generate.cpp:38-142) and
+// the Qwen3 binding (src/qwen_generate.cpp:12-17).
+#include "brolm/detail/generate.h"
+
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+
+#include "brolm/detail/profile.h"
+#include "brolm/qwen_generate.h"
+#include "brotensor/runtime.h"
+
+namespace brolm::detail {
+
+namespace {
+
+std::vector<float> download_fp32(const brotensor::Tensor& t) { return t.to_host_vector(); }
+
+// Strict '>' scan: the lowest index wins ties.
+int argmax(const float* logits, int vocab) {
+    int best = 0;
+    float best_v = logits[0];
+    for (int i = 1; i < vocab; ++i) {
+        if (logits[i] > best_v) {
+            best_v = logits[i];
+            best = i;
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+std::vector<float> last_row_fp32(const brotensor::Tensor& logits) {
+    profile::ScopedStage ps(profile::Stage::logits_download);
+    if (logits.rows == 1) return download_fp32(logits);
+    const int es = brotensor::dtype_size_bytes(logits.dtype);
+    brotensor::Tensor last = brotensor::Tensor::view(
+        logits.device,
+        static_cast<char*>(logits.data) + static_cast<std::size_t>(logits.rows - 1) * logits.cols * es, 1,
+        logits.cols, logits.dtype);
+    return download_fp32(last);
+}
+
+int sample_token(const float* logits, int vocab, const SamplingParams& p, std::mt19937_64& rng) {
+    profile::ScopedStage ps(profile::Stage::sample);
+    if (vocab <= 0) return 0;
+    if (p.temperature <= 0.0f || p.top_k == 1) return argmax(logits, vocab);
+    const float inv_t = 1.0f / p.temperature;
+    float max_logit = logits[0] * inv_t;
+    for (int i = 1; i < vocab; ++i) max_logit = std::max(max_logit, logits[i] * inv_t);
+    std::vector<float> probs(static_cast<std::size_t>(vocab));
+    double sum = 0.0;
+    for (int i = 0; i < vocab; ++i) {
+        const float e = std::exp(logits[i] * inv_t - max_logit);
+        probs[static_cast<std::size_t>(i)] = e;
+        sum += e;
+    }
+    const float norm = sum > 0.0 ? static_cast<float>(1.0 / sum) : 0.0f;
+    for (float& v : probs) v *= norm;
+    std::vector<int> order(static_cast<std::size_t>(vocab));
+    std::iota(order.begin(), order.end(), 0);
+    std::sort(order.begin(), order.end(), [&](int a, int b) {
+        return probs[static_cast<std::size_t>(a)] > probs[static_cast<std::size_t>(b)];
+    });
+    std::size_t keep = static_cast<std::size_t>(vocab);
+    if (p.top_k > 0 && static_cast<std::size_t>(p.top_k) < keep) keep = static_cast<std::size_t>(p.top_k);
+    if (p.top_p < 1.0f) {
+        double cum = 0.0;
+        std::size_t nucleus = 0;
+        for (std::size_t i = 0; i < keep; ++i) {
+            cum += probs[static_cast<std::size_t>(order[i])];
+            ++nucleus;
+            if (cum >= static_cast<double>(p.top_p)) break;
+        }
+        keep = std::max<std::size_t>(nucleus, 1);
+    }
+    double kept = 0.0;
+    for (std::size_t i = 0; i < keep; ++i) kept += probs[static_cast<std::size_t>(order[i])];
+    if (kept <= 0.0) return order[0];
+    std::uniform_real_distribution<double> dist(0.0, 1.0);
+    const double r = dist(rng) * kept;
+    double acc = 0.0;
+    for (std::size_t i = 0; i < keep; ++i) {
+        acc += probs[static_cast<std::size_t>(order[i])];
+        if (r < acc) return order[i];
+    }
+    return order[keep - 1];
+}
+
+}  // namespace brolm::detail
+
+namespace brolm::qwen {
+
+std::vector<int32_t> generate(Qwen3Model& model, const std::vector<int32_t>& prompt_ids, int eos_id,
+                              const GenerateOptions& opts) {
+    return brolm::detail::generate(model, prompt_ids, eos_id, opts);
+}
+
+}  // namespace brolm::qwen

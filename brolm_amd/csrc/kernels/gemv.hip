@@ -1,0 +1,136 @@
+// Quant-carrier / FP16 batched linear (brotensor linear_forward_batched_*_fp16,
+// dispatched at include/brolm/detail/compute.h:54-86): Y[M,N] = X[M,K] W[N,K]^T.
+// M <= 16: GEMV kernels (one wavefront per weight row, lanes across K).
+// M > 16: the prefill GEMM (gemm.hip).
+#include "gemv_core.h"
+
+namespace bx {
+
+int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+             hipStream_t st);
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+template <int FMT, int M, int RB>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
+                                                       int64_t ldx, const uint16_t* __restrict__ bias,
+                                                       uint16_t* __restrict__ Y, int64_t ldy, int N, int K) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    const int xstride = K / 2;
+    const int sstride = K / 16;
+    uint32_t* xs = smem;
+    float* xsum = reinterpret_cast<float*>(smem + M * xstride);
+    stage_x_f16<XLayout<FMT>::swizzled, XLayout<FMT>::needs_sums>(X, ldx, M, K, xs, xstride, xsum, sstride);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int U = K / 32;
+    for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wave) * RB; r0 < N; r0 += (int64_t)gridDim.x * kWaves * RB) {
+        float acc[RB][M];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[rb][m] = 0.f;
+        for (int u = lane; u < U; u += 64) {
+            typename RawOf<FMT>::T raw[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const int64_t row = r0 + rb < N ? r0 + rb : N - 1;
+                raw[rb] = load_unit<FMT>(W, N, K, row, u);
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) dot_unit<M>(raw[rb], u, xs, xstride, xsum, sstride, acc[rb]);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int64_t row = r0 + rb;
+            const float b = (bias && row < N) ? h2f(bias[row]) : 0.f;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float v = wave_sum(acc[rb][m]);
+                if (lane == 0 && row < N) Y[m * ldy + row] = f2h(v + b);
+            }
+        }
+    }
+}
+
+size_t gemv_lds_bytes(int fmt, int M, int K) {
+    size_t b = (size_t)M * K * 2;
+    if (fmt == FMT_Q4_K) b += (size_t)M * (K / 16) * 4;
+    return b;
+}
+
+template <int FMT, int M>
+int launch_gemv(const void* W, const uint16_t* X, int64_t ldx, const uint16_t* bias, uint16_t* Y, int64_t ldy, int N,
+                int K, hipStream_t st) {
+    constexpr int RB = M <= 2 ? 2 : 1;
+    const int64_t rows_per_block = (int64_t)kWaves * RB;
+    int64_t blocks = ((int64_t)N + rows_per_block - 1) / rows_per_block;
+    const int64_t cap = (int64_t)num_cus() * 16;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = gemv_lds_bytes(FMT, M, K);
+    gemv_kernel<FMT, M, RB><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, ldx, bias, Y, ldy, N, K);
+    return launch_check("gemv");
+}
+
+template <int FMT>
+int gemv_dispatch(int M, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int N, int K,
+                  hipStream_t st) {
+    // Largest row chunk whose staged activations fit in 64 KB of LDS.
+    int m0 = 0;
+    while (m0 < M) {
+        const int rem = M - m0;
+        int mc = 16;
+        while (mc > 1 && (mc > rem || gemv_lds_bytes(FMT, mc, K) > 65536)) mc >>= 1;
+        if (gemv_lds_bytes(FMT, mc, K) > 65536) return fail(BX_EUNSUPPORTED, "gemv: K too large for LDS staging");
+        const uint16_t* Xc = X + (int64_t)m0 * K;
+        uint16_t* Yc = Y + (int64_t)m0 * N;
+        int rc;
+        switch (mc) {
+            case 16: rc = launch_gemv<FMT, 16>(W, Xc, K, bias, Yc, N, N, K, st); break;
+            case 8: rc = launch_gemv<FMT, 8>(W, Xc, K, bias, Yc, N, N, K, st); break;
+            case 4: rc = launch_gemv<FMT, 4>(W, Xc, K, bias, Yc, N, N, K, st); break;
+            case 2: rc = launch_gemv<FMT, 2>(W, Xc, K, bias, Yc, N, N, K, st); break;
+            default: rc = launch_gemv<FMT, 1>(W, Xc, K, bias, Yc, N, N, K, st); break;
+        }
+        if (rc) return rc;
+        m0 += mc;
+    }
+    return BX_OK;
+}
+
+}  // namespace
+
+int check_linear_shape(int wtype, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail(BX_EINVAL, "linear: non-positive shape");
+    const int64_t be = type_block_elems(wtype);
+    if (wtype != BX_TYPE_F16 && wtype != BX_TYPE_Q8_0 && wtype != BX_TYPE_Q4_K && wtype != BX_TYPE_Q6_K)
+        return fail(BX_EUNSUPPORTED, "linear: unsupported weight type " + std::to_string(wtype));
+    if (K % 32 != 0 || K % be != 0)
+        return fail(BX_EINVAL, "linear: K=" + std::to_string(K) + " must be a multiple of 32 and of the block size");
+    return BX_OK;
+}
+
+int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+             hipStream_t st) {
+    switch (wtype) {
+        case BX_TYPE_Q4_K: return gemv_dispatch<FMT_Q4_K>(M, W, X, bias, Y, N, K, st);
+        case BX_TYPE_Q6_K: return gemv_dispatch<FMT_Q6_K>(M, W, X, bias, Y, N, K, st);
+        case BX_TYPE_Q8_0: return gemv_dispatch<FMT_Q8_0>(M, W, X, bias, Y, N, K, st);
+        case BX_TYPE_F16: return gemv_dispatch<FMT_F16>(M, W, X, bias, Y, N, K, st);
+        default: return fail(BX_EUNSUPPORTED, "gemv: unsupported type");
+    }
+}
+
+}  // namespace bx
+
+extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M,
+                             int N, int K, void* stream) {
+    if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
+    if (!W || !X || !Y) return bx::fail(BX_EINVAL, "linear: null pointer");
+    hipStream_t st = bx::as_stream(stream);
+    if (M <= 16) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
+    return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
+}

@@ -1,0 +1,117 @@
+#pragma once
+
+// Dense GQA / SwiGLU / RoPE causal decoder core (reference
+// include/brolm/detail/dense_decoder.h:84-239, src/detail/dense_decoder.cpp).
+//
+// Same public surface and semantics as the reference: load_weights through a
+// Source, a per-layer FP16 KV cache of (max_seq, n_kv*head_dim),
+// forward / forward_last / embed_tokens / forward_embeds, truncate_cache as
+// the speculative-draft seam.  MI355X-specific structure:
+//   - the residual stream is FP32 in HBM (H*4 bytes per row);
+//   - L > 1 (prefill) runs the op surface (MFMA GEMM + split-K attention);
+//   - L == 1 runs the fused decode step (six kernels per layer), captured
+//     once into a hipGraph and replayed with the token id and position read
+//     from device memory (BROLM_NO_GRAPH=1 launches the same kernels eagerly,
+//     so graph and eager decode are bit-identical);
+//   - decode_greedy() keeps greedy generation on the device: argmax and the
+//     next token feed the following replay without a host round trip.
+
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "brotensor/tensor.h"
+
+namespace brolm::detail::weights { class Source; }
+
+namespace brolm::detail {
+
+struct DecodeGraphSession;
+
+struct DenseDecoderConfig {
+    int vocab_size = 0;
+    int hidden_size = 0;
+    int intermediate_size = 0;
+    int num_hidden_layers = 0;
+    int num_attention_heads = 0;
+    int num_key_value_heads = 0;
+    int head_dim = 0;
+    float rms_norm_eps = 1e-6f;
+    float rope_theta = 1000000.0f;
+    bool use_qk_norm = false;
+    bool tie_word_embeddings = true;
+};
+
+class DenseDecoder {
+public:
+    explicit DenseDecoder(const DenseDecoderConfig& cfg);
+    ~DenseDecoder();
+    DenseDecoder(const DenseDecoder&) = delete;
+    DenseDecoder& operator=(const DenseDecoder&) = delete;
+    DenseDecoder(DenseDecoder&&) noexcept;
+    DenseDecoder& operator=(DenseDecoder&&) noexcept;
+
+    void load_weights(const brolm::detail::weights::Source& src);
+    void allocate_cache(int max_seq_len);
+    void reset_cache();
+    void truncate_cache(int len);
+    int cache_len() const { return cache_len_; }
+    int max_seq_len() const { return max_seq_len_; }
+
+    void forward(const int32_t* ids, int L, brotensor::Tensor& logits_out, brotensor::Tensor* hidden_out = nullptr);
+    void forward_last(const int32_t* ids, int L, brotensor::Tensor& logits_out);
+    void embed_tokens(const int32_t* ids, int L, brotensor::Tensor& out);
+    void forward_embeds(const brotensor::Tensor& embeds, int L, brotensor::Tensor& logits_out,
+                        brotensor::Tensor* hidden_out = nullptr);
+
+    // Greedy decode of up to n tokens starting from `token` at position
+    // cache_len(), entirely on the device (argmax feeds the next step).
+    // Writes the n sampled ids to out; stops after eos_id when eos_id >= 0.
+    // Returns the number of ids written; cache_len advances by that count.
+    int decode_greedy(int32_t token, int n, int32_t* out, int eos_id);
+
+    // Replays the captured step n times from `token` at cache_len() and
+    // returns the GPU time per step in milliseconds (hipEvents around the
+    // replays); cache_len advances by n.  Used by bench.py.
+    double time_decode_steps(int32_t token, int n);
+
+    // Bytes of weights one decode step streams (carrier bytes of every
+    // per-layer matrix + lm_head + one embedding row + norm gammas).
+    std::int64_t decode_weight_bytes() const;
+
+    const DenseDecoderConfig& config() const { return cfg_; }
+
+private:
+    struct Layer {
+        brotensor::Tensor input_ln;
+        brotensor::Tensor Wq, Wk, Wv, Wo;
+        brotensor::Tensor q_norm, k_norm;
+        brotensor::Tensor post_attn_ln;
+        brotensor::Tensor gate_W, up_W, down_W;
+        brotensor::Tensor K_cache, V_cache;
+    };
+
+    void run_layers_(int L, brotensor::Tensor& logits_out, brotensor::Tensor* hidden_out,
+                     bool logits_last_row_only = false);
+    void decode_step_(int32_t token, brotensor::Tensor& logits_out);
+    DecodeGraphSession& session_();
+    void invalidate_graph_();
+    void ensure_rope_table_();
+
+    DenseDecoderConfig cfg_;
+    brotensor::Tensor embed_tokens_;
+    std::vector<Layer> layers_;
+    brotensor::Tensor final_norm_;
+    brotensor::Tensor lm_head_;
+
+    int cache_len_ = 0;
+    int max_seq_len_ = 0;
+
+    brotensor::Tensor rope_cos_, rope_sin_;  // (cap, hd/2) FP32
+    brotensor::Tensor ids_dev_, h_, norm_, q_, k_, v_, qn_, kn_, attn_, proj_, gate_, up_;
+    brotensor::Tensor attn_ws_;
+
+    std::unique_ptr<DecodeGraphSession> graph_;
+};
+
+}  // namespace brolm::detail

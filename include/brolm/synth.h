@@ -1,0 +1,54 @@
+#pragma once
+
+// Synthetic Qwen3 GGUF checkpoints for benchmarks and parity tests (no network,
+// no real weights).  Every linear weight is drawn N(0, stddev) from a
+// counter-based splitmix64 stream keyed by (seed, tensor name), Box-Muller in
+// double, rounded to BF16 (RNE), then stored as the requested GGUF type.
+// Norm gammas are 1 (F32).
+//
+// The quantizers here are this project's own (round-to-nearest per block with
+// the ggml block layouts); they are not ggml's iterative quantizers.  They
+// only produce inputs: parity is checked on the dequantized values of the
+// blocks they write.
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "brotensor/tensor.h"
+
+namespace brolm::synth {
+
+struct Qwen3Spec {
+    int vocab = 151936;
+    int hidden = 1024;
+    int intermediate = 3072;
+    int layers = 28;
+    int n_q = 16;
+    int n_kv = 8;
+    int head_dim = 128;
+    float eps = 1e-6f;
+    float theta = 1000000.0f;
+    int context = 40960;
+    bool tied = true;  // no output.weight
+    brotensor::Dtype embed = brotensor::Dtype::Q8_0;
+    brotensor::Dtype q = brotensor::Dtype::Q8_0, k = brotensor::Dtype::Q8_0, v = brotensor::Dtype::Q8_0,
+                     o = brotensor::Dtype::Q8_0;
+    brotensor::Dtype gate = brotensor::Dtype::Q8_0, up = brotensor::Dtype::Q8_0, down = brotensor::Dtype::Q8_0;
+    brotensor::Dtype output = brotensor::Dtype::Q6_K;
+    float stddev = 0.02f;
+    std::uint64_t seed = 0;
+};
+
+// Key of a tensor's random stream: seed mixed with the FNV-1a hash of its name.
+std::uint64_t tensor_key(std::uint64_t seed, const std::string& name);
+// out[i] = bf16(stddev * z_i), z the i-th standard normal of stream `key`.
+void normal_bf16(std::uint64_t key, std::int64_t n, float stddev, float* out);
+// Quantize n values (multiple of the block size) into GGUF blocks of `dt`
+// (Q8_0, Q4_K, Q6_K, or dense FP16 / BF16 / FP32).
+void quantize(brotensor::Dtype dt, const float* src, std::int64_t n, std::uint8_t* dst);
+
+std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& spec);
+void write_qwen3_gguf(const Qwen3Spec& spec, const std::string& path);
+
+}  // namespace brolm::synth

@@ -1,0 +1,98 @@
+/*
+ * brolm_c.h — C ABI of libbrolm.so, the C++20 Qwen3 decode stack
+ * (include/brolm/qwen.h, include/brolm/qwen_generate.h) for FFI callers
+ * (Python ctypes, cgo, ...).  Each entry point forwards to the C++ API named
+ * beside it, which mirrors the reference's (paths in wlejon/brolm).
+ *
+ * Conventions: int returns are 0 on success, -1 on failure with a
+ * thread-local message from brolm_last_error(); host buffers are caller-owned;
+ * logits come back as FP32 values of the FP16 device logits.
+ */
+#ifndef BROLM_C_H
+#define BROLM_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct brolm_qwen3 brolm_qwen3;
+
+/* Qwen3Config (include/brolm/qwen.h:35-47). */
+typedef struct {
+    int vocab_size, hidden_size, intermediate_size, num_hidden_layers;
+    int num_attention_heads, num_key_value_heads, head_dim;
+    float rms_norm_eps, rope_theta;
+    int tie_word_embeddings, max_position_embeddings;
+} brolm_qwen3_config;
+
+/* Synthetic checkpoint spec (include/brolm/synth.h); *_type are ggml ids. */
+typedef struct {
+    int vocab, hidden, intermediate, layers, n_q, n_kv, head_dim;
+    float eps, theta;
+    int context, tied;
+    int embed_type, q_type, k_type, v_type, o_type, gate_type, up_type, down_type, output_type;
+    float stddev;
+    uint64_t seed;
+} brolm_synth_qwen3_spec;
+
+const char* brolm_last_error(void);
+/* brotensor::init(): registers the gfx950 device (fails without one). */
+int brolm_init(void);
+
+/* synth::write_qwen3_gguf */
+int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* spec, const char* path);
+/* synth::normal_bf16 / synth::quantize (test hooks for the generator). */
+int brolm_synth_normal_bf16(uint64_t key, int64_t n, float stddev, float* out);
+uint64_t brolm_synth_tensor_key(uint64_t seed, const char* name);
+int brolm_synth_quantize(int ggml_type, const float* src, int64_t n, uint8_t* dst);
+
+/* qwen3_hf_to_ggml (src/qwen.cpp:173-208): writes the ggml name to out
+ * (NUL-terminated, cap bytes) and returns its length; 0 if unmapped. */
+int brolm_qwen3_hf_to_ggml(const char* hf_name, char* out, int cap);
+/* Qwen3Config::from_gguf (src/qwen.cpp:88-149). */
+int brolm_qwen3_config_from_gguf(const char* path, brolm_qwen3_config* out);
+/* GGUF metadata / tensor directory of the product reader (gguf::File). */
+int brolm_gguf_tensor_count(const char* path, int64_t* out);
+int brolm_gguf_tensor_info(const char* path, const char* name, int* ggml_type, int64_t* dims4, int* ndims,
+                           int64_t* nbytes);
+
+/* Qwen3Model (include/brolm/qwen.h:58-157). */
+brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg);
+void brolm_qwen3_free(brolm_qwen3* m);
+int brolm_qwen3_load_gguf(brolm_qwen3* m, const char* path);
+int brolm_qwen3_allocate_cache(brolm_qwen3* m, int max_seq_len);
+int brolm_qwen3_reset_cache(brolm_qwen3* m);
+int brolm_qwen3_truncate_cache(brolm_qwen3* m, int len);
+int brolm_qwen3_cache_len(const brolm_qwen3* m);
+/* forward: logits (L, vocab); hidden (L, hidden) or NULL. */
+int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits, float* hidden);
+/* forward_last: logits (1, vocab). */
+int brolm_qwen3_forward_last(brolm_qwen3* m, const int32_t* ids, int L, float* logits);
+/* embed_tokens: out (L, hidden) FP16 bits. */
+int brolm_qwen3_embed_tokens(brolm_qwen3* m, const int32_t* ids, int L, uint16_t* out);
+/* forward_embeds: embeds (L, hidden) FP16 bits from the host. */
+int brolm_qwen3_forward_embeds(brolm_qwen3* m, const uint16_t* embeds, int L, float* logits, float* hidden);
+/* qwen::generate (include/brolm/qwen_generate.h:45-47); returns the count. */
+int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, int max_new, int eos_id,
+                         int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
+                         int device_greedy, int32_t* out);
+/* DenseDecoder::decode_greedy / time_decode_steps / decode_weight_bytes. */
+int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id);
+double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n);
+int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m);
+
+/* sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142). */
+int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed);
+
+/* BROLM_PROFILE stage table (src/detail/profile.cpp). */
+void brolm_profile_reset(void);
+void brolm_profile_report(void);
+int brolm_profile_enabled(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

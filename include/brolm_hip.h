@@ -1,0 +1,180 @@
+/*
+ * brolm_hip.h — C ABI of the MI355X (gfx950) kernel library libbrolm_hip.so.
+ *
+ * This is the thin layer between the C++20 host (the brotensor-shaped op
+ * surface in include/brotensor/ops.h and brolm's DenseDecoder) and the
+ * hand-written HIP kernels.  Plain pointers and sizes only; no C++ types.
+ *
+ * Contract for every entry point:
+ *   - Pointers are device pointers (hipMalloc'd or torch-owned) unless stated.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Nothing here allocates device memory; scratch is passed in by the
+ *     caller, sized by the matching *_workspace_bytes query.
+ *   - Return 0 on success or a negative BX_E* code; bx_last_error() gives a
+ *     thread-local message.  Shapes are validated on the host before any
+ *     launch, so an invalid shape is an error return, never a device fault.
+ *   - FP16 values travel as uint16_t bit patterns (IEEE binary16).
+ *
+ * Quantized weights ("carriers") live on the device in a repacked layout that
+ * is a byte permutation of the GGUF blocks (same byte count; see
+ * bx_repack_gguf_rows).  The reference interface each entry point replaces is
+ * cited beside it (paths relative to wlejon/brolm; the ops themselves live in
+ * the absent sibling brotensor, so the citation is brolm's call site).
+ */
+#ifndef BROLM_HIP_H
+#define BROLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BX_OK 0
+#define BX_EINVAL (-1)     /* bad argument or shape */
+#define BX_ELAUNCH (-2)    /* HIP runtime error */
+#define BX_EUNSUPPORTED (-3)
+
+/* ggml tensor type ids accepted by the carrier entry points. */
+#define BX_TYPE_F32 0
+#define BX_TYPE_F16 1
+#define BX_TYPE_Q8_0 8
+#define BX_TYPE_Q4_K 12
+#define BX_TYPE_Q6_K 14
+
+const char* bx_last_error(void);
+int bx_abi_version(void);
+/* 1 if a gfx950 device is present and the code objects load. */
+int bx_device_ok(void);
+
+/* ---------------------------------------------------------------- carriers */
+
+/* Repack `rows` GGUF rows of `cols` elements (src: device copy of the GGUF
+ * bytes, row-major) into the device carrier layout at dst (same byte count).
+ * Replaces the layout handed over by gguf::upload_raw
+ * (include/brolm/detail/weights.h:294-305, :324). */
+int bx_repack_gguf_rows(int type, const void* src, void* dst, int64_t rows, int64_t cols, void* stream);
+/* Inverse of bx_repack_gguf_rows (carrier -> GGUF bytes). */
+int bx_unpack_carrier_rows(int type, const void* src, void* dst, int64_t rows, int64_t cols, void* stream);
+/* Carrier byte count for (rows, cols) of `type`; -1 if cols is ragged. */
+int64_t bx_carrier_bytes(int type, int64_t rows, int64_t cols);
+
+/* K6: dequant_{q8_0,q4k,q6k}_to_fp16 (weights.h:325-339). FP32 values are
+ * d*sc*q - dmin*m exactly as the GGUF formula, then RNE to binary16 with
+ * subnormals kept. */
+int bx_dequant_to_f16(int type, const void* carrier, uint16_t* dst, int64_t rows, int64_t cols, void* stream);
+/* Unpack-only debug entry: the same values before the FP16 rounding. */
+int bx_dequant_to_f32(int type, const void* carrier, float* dst, int64_t rows, int64_t cols, void* stream);
+
+/* ------------------------------------------------------------------ linear */
+
+/* K1-K4: linear_forward_batched_{q4k,q6k,q8_0,}_fp16(W, bias, X, Y)
+ * (include/brolm/detail/compute.h:54-86).  Y[M,N] = X[M,K] . W[N,K]^T (+bias[N]).
+ * X, Y, bias FP16; FP32 accumulation.  W is a carrier of `wtype` or dense FP16
+ * (wtype BX_TYPE_F16).  M <= 16 runs the GEMV kernels, larger M the prefill
+ * GEMM. */
+int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y,
+                  int M, int N, int K, void* stream);
+
+/* ------------------------------------------------------------- elementwise */
+
+/* K7: embedding_lookup_forward(W, idx_dev, L, out) (dense_decoder.cpp:259-261).
+ * W FP16 (V, H); ids must be in [0, V) (checked by the caller on the host). */
+int bx_embedding_f16(const uint16_t* W, int V, int H, const int32_t* ids, int L, uint16_t* out, void* stream);
+/* Same gather into an FP32 residual stream. */
+int bx_embedding_f32(const uint16_t* W, int V, int H, const int32_t* ids, int L, float* out, void* stream);
+
+/* K8/K9: rms_norm_forward(X, gamma, eps, Y) (dense_decoder.cpp:559, :540-550).
+ * x_is_f32 selects an FP32 input (the residual stream); Y is FP16. */
+int bx_rms_norm(const void* X, int x_is_f32, const uint16_t* gamma, float eps, uint16_t* Y, int rows, int cols,
+                void* stream);
+
+/* K10: rope_forward(X, hd, n_heads, seq_offset, theta, Y) (dense_decoder.cpp:587-590),
+ * in place allowed (X == Y).  Row r rotates at position seq_offset + r using
+ * the FP32 cos/sin table (cap, hd/2) built by bx_rope_table on the host side. */
+int bx_rope_f16(const uint16_t* X, uint16_t* Y, int rows, int hd, int n_heads, int seq_offset,
+                const float* cos_tab, const float* sin_tab, int tab_rows, void* stream);
+/* Host helper: cos/sin table of pos*theta^(-2i/hd), computed in double. */
+void bx_rope_table_host(float* cos_out, float* sin_out, int rows, int hd, float theta);
+
+/* K12: kv_cache_append(k, v, cur_len, Kc, Vc) (dense_decoder.cpp:597-598). */
+int bx_kv_append_f16(const uint16_t* k, const uint16_t* v, int L, int cols, int cur_len, uint16_t* Kc,
+                     uint16_t* Vc, int cap, void* stream);
+
+/* K14: flash_attention_decode(q, Kc, Vc, valid_len, n_q, n_kv, out[, softcap, window])
+ * (dense_decoder.cpp:606-607; Gemma form src/gemma2.cpp:365-367).
+ * q (L, n_q*hd) FP16, caches (cap, n_kv*hd) FP16, out (L, n_q*hd) FP16.
+ * Row r attends keys [max(0, p-window+1), p] with p = valid_len - L + r.
+ * workspace: bx_attention_workspace_bytes(L, n_q, hd, valid_len) bytes. */
+size_t bx_attention_workspace_bytes(int L, int n_q, int hd, int valid_len);
+int bx_attention_decode_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, int L, int valid_len,
+                            int n_q, int n_kv, int hd, float softcap, int window, uint16_t* out,
+                            void* workspace, void* stream);
+
+/* K15: flash_attention_decode_masked(q, Kc, Vc, mask, n_q, n_kv, out)
+ * (dense_decoder.cpp:476-478): one query row attends the keys j < n_keys
+ * whose FP32 mask[j] (device) is non-zero.  workspace as above with L = 1,
+ * valid_len = n_keys. */
+int bx_attention_masked_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, const float* mask, int n_keys,
+                            int n_q, int n_kv, int hd, uint16_t* out, void* workspace, void* stream);
+
+/* K13: scatter_rows(src, idx_row, dst) (dense_decoder.cpp:473-474):
+ * dst row *idx_dev (device int32, must be < dst_rows) = src (one row of
+ * `row_bytes` bytes). */
+int bx_scatter_row(const void* src, const int32_t* idx_dev, void* dst, int64_t row_bytes, int dst_rows,
+                   void* stream);
+
+/* K16: silu_forward(g, g) + mul_inplace(g, u) (dense_decoder.cpp:635-636). */
+int bx_silu_mul_f16(uint16_t* g, const uint16_t* u, int64_t n, void* stream);
+int bx_silu_f16(const uint16_t* x, uint16_t* y, int64_t n, void* stream);
+int bx_mul_f16(uint16_t* a, const uint16_t* b, int64_t n, void* stream);
+/* K17: add_inplace(h, proj) (dense_decoder.cpp:616, :645); h FP32 or FP16. */
+int bx_add_inplace(void* h, int h_is_f32, const uint16_t* x, int64_t n, void* stream);
+/* FP32 -> FP16 copy (RNE). */
+int bx_f32_to_f16(const float* x, uint16_t* y, int64_t n, void* stream);
+
+/* ------------------------------------------------------------ decode step */
+
+/* Fused single-token decode kernels (the captured step of
+ * dense_decoder.cpp:335-524, restructured).  Per-step scalars (token id,
+ * position) are read from device memory so the step can be graph-captured
+ * once and replayed.  All activations are in `ws` (bx_decode_ws_bytes). */
+typedef struct {
+    int hidden, intermediate, n_q, n_kv, head_dim, vocab, cap;
+    float eps;
+    int qkv_type_q, qkv_type_k, qkv_type_v, o_type, gate_type, up_type, down_type, lm_type;
+} bx_decode_dims;
+
+typedef struct {
+    const void *in_ln, *q_norm, *k_norm, *post_ln;  /* FP16 gammas (q/k norms permuted) */
+    const void *Wq, *Wk, *Wv, *Wo, *Wg, *Wu, *Wd;   /* carriers or FP16 */
+    void *Kc, *Vc;                                  /* FP16 (cap, n_kv*hd) */
+} bx_decode_layer;
+
+size_t bx_decode_ws_bytes(const bx_decode_dims* d);
+/* Embedding row of *tok_dev into the FP32 residual (ws). */
+int bx_decode_embed(const bx_decode_dims* d, const uint16_t* embed, const int32_t* tok_dev, void* ws, void* stream);
+/* One layer at position *pos_dev (cos/sin table rows pos). */
+int bx_decode_layer_run(const bx_decode_dims* d, const bx_decode_layer* L, const int32_t* pos_dev,
+                        const float* cos_tab, const float* sin_tab, void* ws, void* stream);
+/* Final norm + lm_head -> logits (FP16, vocab). */
+int bx_decode_head(const bx_decode_dims* d, const uint16_t* final_norm, const void* lm_head, uint16_t* logits,
+                   void* ws, void* stream);
+
+/* Step feedback for device-side greedy decoding: *tok = *next, *pos += 1,
+ * hist[*count] = *next, *count += 1 (hist may be NULL; count must then be
+ * NULL too; hist must hold at least as many ids as steps between resets). */
+int bx_decode_advance(int32_t* tok_dev, int32_t* pos_dev, const int32_t* next_dev, int32_t* hist, int32_t* count,
+                      void* stream);
+
+/* Device greedy argmax over FP16 logits, lowest index wins ties
+ * (src/detail/generate.cpp:38-48).  Writes the id to *out (device int32).
+ * workspace: bx_argmax_workspace_bytes(n). */
+size_t bx_argmax_workspace_bytes(int64_t n);
+int bx_argmax_f16(const uint16_t* logits, int64_t n, int32_t* out, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
