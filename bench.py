@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the quantized Qwen3 hot path on one MI355X.
+
+Workload: Qwen3-1.7B shape, Q4_K linears with Q6_K
+attn_v / ffn_down / output (untied), synthetic seeded N(0, 0.02) weights;
+prefill a 1024-token prompt (std::mt19937_64(42) % vocab, as
+tools/bench_decode.cpp:208-213), then greedy decode at positions 1024..,
+KV cache capacity 4096.
+
+A step is one decode token: the captured hipGraph of the fused decode step
+(embedding, 28 layers, final norm + lm_head, device argmax feeding the next
+token).  W warm-up steps run first; then K steps are timed with host wall
+clock around (sync, K replays, sync), and HIP events on the decode stream
+give the GPU time per step used for the roofline.  Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+CONFIGS = {
+    # BASELINE.json configs[2]
+    "qwen3-1.7b-q4k": dict(vocab=151936, hidden=2048, intermediate=6144, layers=28, n_q=16, n_kv=8, head_dim=128,
+                           tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K", gate="Q4_K",
+                           up="Q4_K", down="Q6_K", output="Q6_K", prompt=1024, decode=512, cap=4096),
+    # BASELINE.json configs[1]
+    "qwen3-0.6b-q8_0": dict(vocab=151936, hidden=1024, intermediate=3072, layers=28, n_q=16, n_kv=8, head_dim=128,
+                            tied=True, embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0",
+                            up="Q8_0", down="Q8_0", output="Q8_0", prompt=512, decode=256, cap=2048),
+    # BASELINE.json configs[4]
+    "qwen3-8b-q4k": dict(vocab=151936, hidden=4096, intermediate=12288, layers=36, n_q=32, n_kv=8, head_dim=128,
+                         tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K",
+                         up="Q4_K", down="Q4_K", output="Q6_K", prompt=2048, decode=256, cap=2304),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synth_path(name: str, seed: int) -> Path:
+    d = Path(os.environ.get("BROLM_BENCH_DIR", "/tmp"))
+    return d / f"brolm_synth_{name}_s{seed}.gguf"
+
+
+def make_model_file(name: str, seed: int) -> Path:
+    import brolm_amd as ba
+
+    c = CONFIGS[name]
+    path = synth_path(name, seed)
+    if not path.exists():
+        spec = ba.SynthSpec(**{k: v for k, v in c.items() if k not in ("prompt", "decode", "cap")}, seed=seed)
+        t0 = time.time()
+        tmp = path.with_suffix(".tmp")
+        ba.write_synth_qwen3(spec, str(tmp))
+        os.replace(tmp, path)
+        log(f"synthetic checkpoint {path.name}: {path.stat().st_size / 1e9:.3f} GB in {time.time() - t0:.1f} s")
+    return path
+
+
+def cpu_baseline(path: Path, vocab: int, prompt: list[int], seconds: float) -> dict:
+    """The oracle (C, FP32 on dequantized weights, OpenMP) on the host cores:
+    prefill a short prompt, then greedy decode until ~`seconds` of decode work."""
+    import oracle
+
+    t0 = time.time()
+    m = oracle.Model(str(path))
+    load_s = time.time() - t0
+    n_prompt = 32
+    m.allocate_cache(n_prompt + 256)
+    t0 = time.time()
+    lg = m.forward(prompt[:n_prompt], last_only=True)
+    prefill_s = time.time() - t0
+    tok, _ = oracle.argmax(lg[0])
+    steps = 0
+    t0 = time.time()
+    while steps < 256:
+        lg = m.forward([tok], last_only=True)
+        tok, _ = oracle.argmax(lg[0])
+        steps += 1
+        if time.time() - t0 > seconds:
+            break
+    dec_s = time.time() - t0
+    return {
+        "value": steps / dec_s,
+        "unit": "tok/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"oracle FP32 decode of {steps} tokens after a {n_prompt}-token prefill "
+                  f"(prefill {prefill_s:.1f} s, weight dequant/load {load_s:.1f} s excluded)",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default: the config's decode)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="qwen3-1.7b-q4k", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU decode is not part of this build", file=sys.stderr)
+        return 2
+
+    import brolm_amd as ba
+
+    c = CONFIGS[args.config]
+    steps = args.steps if args.steps is not None else c["decode"]
+    path = make_model_file(args.config, args.seed)
+    ba.init()
+    cfg = ba.Qwen3Config.from_gguf(str(path))
+    model = ba.Qwen3Model(cfg)
+    t0 = time.time()
+    model.load_weights(str(path))
+    log(f"loaded in {time.time() - t0:.1f} s")
+    prompt = ba.prompt_ids(c["prompt"], cfg.vocab_size, seed=42)
+    cap = max(c["cap"], c["prompt"] + args.warmup + steps + 1)
+    model.allocate_cache(cap)
+
+    # prefill (timed separately, reported as an extra field)
+    t0 = time.perf_counter()
+    logits = model.forward_last(prompt)
+    prefill_s = time.perf_counter() - t0
+    first = int(logits.argmax())
+    t0 = time.perf_counter()
+    model.truncate_cache(0)
+    logits = model.forward_last(prompt)
+    prefill_s = min(prefill_s, time.perf_counter() - t0)
+    log(f"prefill {c['prompt']} tokens: {prefill_s * 1e3:.1f} ms")
+
+    # warm-up steps, then roll back to the end of the prompt
+    if args.warmup > 0:
+        model.time_decode_steps(first, args.warmup)
+    model.truncate_cache(len(prompt))
+
+    # timed region: K captured decode steps
+    t0 = time.perf_counter()
+    gpu_ms = model.time_decode_steps(first, steps)
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / steps
+    tok_s = steps / wall
+
+    # reference-shaped loop (forward_last + logits download + host argmax)
+    model.truncate_cache(len(prompt))
+    n_ref = min(64, steps)
+    tok = first
+    t0 = time.perf_counter()
+    for _ in range(n_ref):
+        tok = int(model.forward_last([tok]).argmax())
+    ref_tok_s = n_ref / (time.perf_counter() - t0)
+
+    wbytes = model.decode_weight_bytes()
+    achieved = wbytes / (gpu_ms * 1e-3) / 1e9
+    kvd = cfg.num_key_value_heads * cfg.head_dim
+    avg_ctx = len(prompt) + steps / 2
+    kv_bytes = 2 * cfg.num_hidden_layers * avg_ctx * kvd * 2
+    result = {
+        "metric": "decode tok/s bs=1 Qwen3-1.7B Q4_K; quant-GEMV HBM GB/s as % of peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 activations / Q4_K+Q6_K weights, fp32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to GGUF blocks, mt19937_64(42) prompt",
+        "config": {"workload": args.config, "prompt_tokens": c["prompt"], "decode_tokens": steps, "kv_cap": cap,
+                   "batch": 1, "sampling": "greedy (device argmax)", "graph": "hipGraph, one launch per token"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "captured decode step (hipGraph launch)",
+                     "algorithmic_bytes_per_launch": wbytes, "gpu_ms_per_launch": round(gpu_ms, 5)},
+        "gpu_ms_per_step_events": round(gpu_ms, 5),
+        "weight_bytes_per_token": wbytes,
+        "kv_bytes_per_token_avg": int(kv_bytes),
+        "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
+        "ref_loop_tok_s": round(ref_tok_s, 2),
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) ...")
+        result["cpu_baseline"] = cpu_baseline(path, cfg.vocab_size, prompt, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -197,6 +197,14 @@ def sample_token(logits: np.ndarray, params: SamplingParams, seed: int) -> int:
                                             int(params.top_k), float(params.top_p), int(seed))
 
 
+def prompt_ids(n: int, vocab: int, seed: int = 42) -> list[int]:
+    """bench_decode's synthetic prompt: std::mt19937_64(seed)() % vocab (tools/bench_decode.cpp:208-213)."""
+    out = np.empty((max(n, 1),), np.int32)
+    check(_native.lib().brolm_prompt_ids(int(seed), int(n), int(vocab), out.ctypes.data_as(_native.P_i32)),
+          "prompt_ids")
+    return out[:n].tolist()
+
+
 @dataclass
 class SynthSpec:
     """Synthetic Qwen3 checkpoint (include/brolm/synth.h)."""

@@ -106,6 +106,7 @@ C_SYMBOLS = {
     "brolm_qwen3_time_decode_steps": (f64, [vp, i32, C.c_int]),
     "brolm_qwen3_decode_weight_bytes": (i64, [vp]),
     "brolm_sample_token": (C.c_int, [P_f32, C.c_int, f32, C.c_int, f32, u64]),
+    "brolm_prompt_ids": (C.c_int, [u64, C.c_int, C.c_int, P_i32]),
     "brolm_profile_reset": (None, []),
     "brolm_profile_report": (None, []),
     "brolm_profile_enabled": (C.c_int, []),

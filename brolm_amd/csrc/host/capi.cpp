@@ -268,3 +268,14 @@ void brolm_profile_report(void) { brolm::detail::profile::report(); }
 int brolm_profile_enabled(void) { return brolm::detail::profile::enabled() ? 1 : 0; }
 
 }  // extern "C"
+
+extern "C" int brolm_prompt_ids(uint64_t seed, int n, int vocab, int32_t* out) {
+    // tools/bench_decode.cpp:208-213: std::mt19937_64(seed)() % vocab
+    if (n < 0 || vocab <= 0 || (!out && n > 0)) {
+        g_err = "prompt_ids: bad arguments";
+        return -1;
+    }
+    std::mt19937_64 rng(seed);
+    for (int i = 0; i < n; ++i) out[i] = static_cast<int32_t>(rng() % static_cast<uint64_t>(vocab));
+    return 0;
+}

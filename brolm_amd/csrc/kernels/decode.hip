@@ -5,19 +5,23 @@
 //   1 norm_qkv   rms_norm(h) in the prologue, GEMV over [Wq; Wk; Wv] (mixed
 //                carrier formats by row segment), FP32 q/k/v out
 //   2 attn       per (KV head, split): QK-norm + RoPE of q and k, KV-cache
-//                write of position pos, split-K attention partials
+//                write of position pos, split-K attention partials (K/V tiles
+//                staged in LDS)
 //   3 combine    merge splits -> FP16 attention output
 //   4 o_proj     GEMV + residual add into the FP32 residual stream
 //   5 norm_mlp   rms_norm(h) prologue, gate and up rows of the same index in
 //                one wavefront, SwiGLU epilogue -> FP16 activation
 //   6 down       GEMV + residual add
 //
+// GEMVs use the M = 1 core of gemv_core.h: activations staged once per block
+// in LDS, then held in registers; each wavefront streams R weight rows at a
+// time with all their 16-byte loads in flight.
+//
 // The token id and position are read from device memory (pos_dev, tok_dev),
 // so one capture serves every step; the split count is fixed at capture time
 // and the keys per split follow pos on the device.
 #include <cmath>
 
-#include "attention_core.h"
 #include "gemv_core.h"
 
 namespace bx {
@@ -25,21 +29,27 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMinKeysPerSplit = 32;
+constexpr int kMinKeysPerSplit = 16;
+constexpr int kMaxKeysPerSplit = 64;
+constexpr int kMaxGroup = 8;
 
 struct WsLayout {
     size_t h, qkv, attn, act, part, total;
     int S;
 };
 
+int splits_for(const bx_decode_dims& d) {
+    int S = (2 * num_cus()) / (d.n_kv > 0 ? d.n_kv : 1);
+    const int need = (d.cap + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // keys per split stay <= 64
+    if (S < need) S = need;
+    if (S < 1) S = 1;
+    return S;
+}
+
 WsLayout ws_layout(const bx_decode_dims& d) {
     WsLayout w{};
     const int qd = d.n_q * d.head_dim, kvd = d.n_kv * d.head_dim;
-    int S = (2 * num_cus()) / (d.n_kv > 0 ? d.n_kv : 1);
-    if (S < 1) S = 1;
-    const int smax = (d.cap + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
-    if (S > smax) S = smax;
-    w.S = S;
+    w.S = splits_for(d);
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -50,14 +60,13 @@ WsLayout ws_layout(const bx_decode_dims& d) {
     w.qkv = take((size_t)(qd + 2 * kvd) * 4);
     w.attn = take((size_t)qd * 2);
     w.act = take((size_t)d.intermediate * 2);
-    w.part = take((size_t)d.n_q * S * (d.head_dim + 2) * 4);
+    w.part = take((size_t)d.n_q * w.S * (d.head_dim + 2) * 4);
     w.total = off;
     return w;
 }
 
-// ---- activation staging -------------------------------------------------
+// ---- activation staging (swizzled FP16 pairs + 16-element sums in LDS) ----
 
-// x = fp16(h * rsqrt(mean(h^2) + eps) * gamma), swizzled into LDS (+ sums).
 __device__ void stage_norm(const float* __restrict__ h, const uint16_t* __restrict__ gamma, float eps, int K,
                            uint32_t* xs, float* xsum, float* red) {
     float ss = 0.f;
@@ -91,29 +100,23 @@ __device__ void stage_f16(const uint16_t* __restrict__ x, int K, uint32_t* xs, f
     __syncthreads();
 }
 
-// ---- one weight row (M = 1) against the staged activation ---------------
-
-template <int FMT>
-__device__ __forceinline__ float row_dot_fmt(const void* W, int64_t N, int K, int64_t n, const uint32_t* xs,
-                                             const float* xsum) {
+// Stream rows [0, N) of one matrix; epi(row, value) runs on lane 0.
+template <int FMT, int UPL, class Epi>
+__device__ __forceinline__ void stream_matrix(const void* W, int64_t N, int K, const uint32_t* xs, const float* xsum,
+                                              int64_t task0, int64_t task_stride, Epi epi) {
+    constexpr int R = RowsPer<UPL>::R;
     const int lane = threadIdx.x & 63;
-    const int U = K / 32;
-    float acc[1] = {0.f};
-    for (int u = lane; u < U; u += 64) {
-        const auto raw = load_unit<FMT>(W, N, K, n, u);
-        if constexpr (FMT == FMT_F16) dot_unit_f16_swz<1>(raw, u, xs, K / 2, acc);
-        else dot_unit<1>(raw, u, xs, K / 2, xsum, K / 16, acc);
-    }
-    return wave_sum(acc[0]);
-}
-
-__device__ __forceinline__ float row_dot(int type, const void* W, int64_t N, int K, int64_t n, const uint32_t* xs,
-                                         const float* xsum) {
-    switch (type) {
-        case BX_TYPE_Q4_K: return row_dot_fmt<FMT_Q4_K>(W, N, K, n, xs, xsum);
-        case BX_TYPE_Q6_K: return row_dot_fmt<FMT_Q6_K>(W, N, K, n, xs, xsum);
-        case BX_TYPE_Q8_0: return row_dot_fmt<FMT_Q8_0>(W, N, K, n, xs, xsum);
-        default: return row_dot_fmt<FMT_F16>(W, N, K, n, xs, xsum);
+    XCache<FMT, UPL> xu;
+    xu.init(xs, xsum, K);
+    const int64_t tasks = (N + R - 1) / R;
+    for (int64_t t = task0; t < tasks; t += task_stride) {
+        float o[R];
+        rows_dot_m1<FMT, UPL, R>(W, N, K, t * R, xu, o);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr)
+                if (t * R + rr < N) epi(t * R + rr, o[rr]);
+        }
     }
 }
 
@@ -131,82 +134,101 @@ __global__ void embed_kernel(const uint16_t* __restrict__ E, const int32_t* __re
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x) h[i] = h2f(E[t * H + i]);
 }
 
-// 1: rms_norm + [Wq; Wk; Wv] -> FP32 rows.
-__global__ __launch_bounds__(kThreads) void norm_qkv_kernel(const float* __restrict__ h,
-                                                            const uint16_t* __restrict__ gamma, float eps, int K,
-                                                            Seg3 seg, float* __restrict__ out) {
+// Each GEMV kernel is specialised on the weight format(s) and units per lane
+// so the register budget is that of one path; waves_per_eu(4) caps it at 128.
+#define BX_GEMV_BOUNDS __launch_bounds__(kThreads, 4)
+
+// 1: rms_norm + [Wq; Wk; Wv] -> FP32 rows.  q and k share format FA, v has
+// FB.  Wavefront tasks walk the segments in turn; a task streams R rows.
+template <int FA, int FB, int UPL>
+__global__ BX_GEMV_BOUNDS void norm_qkv_kernel(const float* __restrict__ h, const uint16_t* __restrict__ gamma,
+                                               float eps, int K, Seg3 seg, float* __restrict__ out) {
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
     float* red = xsum + K / 16;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int N = seg.rows[0] + seg.rows[1] + seg.rows[2];
-    for (int r = blockIdx.x * kWaves + wave; r < N; r += gridDim.x * kWaves) {
-        int sgi = 0, n = r;
-        if (n >= seg.rows[0]) { n -= seg.rows[0]; sgi = 1; if (n >= seg.rows[1]) { n -= seg.rows[1]; sgi = 2; } }
-        const float v = row_dot(seg.type[sgi], seg.W[sgi], seg.rows[sgi], K, n, xs, xsum);
-        if (lane == 0) out[r] = v;
+    const int wave = threadIdx.x >> 6;
+    const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
+    constexpr int R = RowsPer<UPL>::R;
+    int64_t base = 0, tbase = 0;
+    for (int sg = 0; sg < 3; ++sg) {
+        const int64_t N = seg.rows[sg];
+        float* o = out + base;
+        int64_t t0 = w0 - (tbase % ws);  // this wavefront's first task inside the segment
+        if (t0 < 0) t0 += ws;
+        if (sg < 2) stream_matrix<FA, UPL>(seg.W[sg], N, K, xs, xsum, t0, ws, [&](int64_t r, float v) { o[r] = v; });
+        else stream_matrix<FB, UPL>(seg.W[sg], N, K, xs, xsum, t0, ws, [&](int64_t r, float v) { o[r] = v; });
+        tbase += (N + R - 1) / R;
+        base += N;
     }
 }
 
 // 4 / 6: FP16 activation x, GEMV, residual add into h.
-__global__ __launch_bounds__(kThreads) void gemv_resid_kernel(const uint16_t* __restrict__ x, int K, const void* W,
-                                                              int type, int N, float* __restrict__ h) {
+template <int FMT, int UPL>
+__global__ BX_GEMV_BOUNDS void gemv_resid_kernel(const uint16_t* __restrict__ x, int K, const void* W, int N,
+                                                 float* __restrict__ h) {
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
     stage_f16(x, K, xs, xsum);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int r = blockIdx.x * kWaves + wave; r < N; r += gridDim.x * kWaves) {
-        const float v = row_dot(type, W, N, K, r, xs, xsum);
-        if (lane == 0) h[r] += v;
-    }
+    const int wave = threadIdx.x >> 6;
+    const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
+    stream_matrix<FMT, UPL>(W, N, K, xs, xsum, w0, ws, [&](int64_t r, float v) { h[r] += v; });
 }
 
 // 5: rms_norm + gate/up rows of index n -> act[n] = fp16(silu(g) * u).
-__global__ __launch_bounds__(kThreads) void norm_mlp_kernel(const float* __restrict__ h,
-                                                            const uint16_t* __restrict__ gamma, float eps, int K,
-                                                            const void* Wg, int tg, const void* Wu, int tu, int F,
-                                                            uint16_t* __restrict__ act) {
+template <int FMT, int UPL>
+__global__ BX_GEMV_BOUNDS void norm_mlp_kernel(const float* __restrict__ h, const uint16_t* __restrict__ gamma,
+                                               float eps, int K, const void* Wg, const void* Wu, int F,
+                                               uint16_t* __restrict__ act) {
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
     float* red = xsum + K / 16;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
+    constexpr int R = RowsPer<UPL>::R > 1 ? RowsPer<UPL>::R / 2 : 1;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int r = blockIdx.x * kWaves + wave; r < F; r += gridDim.x * kWaves) {
-        const float g = row_dot(tg, Wg, F, K, r, xs, xsum);
-        const float u = row_dot(tu, Wu, F, K, r, xs, xsum);
-        if (lane == 0) act[r] = f2h(g / (1.0f + __expf(-g)) * u);
+    const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
+    XCache<FMT, UPL> xu;
+    xu.init(xs, xsum, K);
+    const int64_t tasks = (F + R - 1) / R;
+    for (int64_t t = w0; t < tasks; t += ws) {
+        float g[R], u[R];
+        rows_dot_m1_pair<FMT, UPL, R>(Wg, Wu, F, K, t * R, xu, g, u);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int64_t r = t * R + rr;
+                if (r < F) act[r] = f2h(g[rr] / (1.0f + __expf(-g[rr])) * u[rr]);
+            }
+        }
     }
 }
 
 // Final: rms_norm + lm_head rows -> FP16 logits.
-__global__ __launch_bounds__(kThreads) void norm_head_kernel(const float* __restrict__ h,
-                                                             const uint16_t* __restrict__ gamma, float eps, int K,
-                                                             const void* W, int type, int N,
-                                                             uint16_t* __restrict__ logits) {
+template <int FMT, int UPL>
+__global__ BX_GEMV_BOUNDS void norm_head_kernel(const float* __restrict__ h, const uint16_t* __restrict__ gamma,
+                                                float eps, int K, const void* W, int N,
+                                                uint16_t* __restrict__ logits) {
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
     float* red = xsum + K / 16;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int r = blockIdx.x * kWaves + wave; r < N; r += gridDim.x * kWaves) {
-        const float v = row_dot(type, W, N, K, r, xs, xsum);
-        if (lane == 0) logits[r] = f2h(v);
-    }
+    const int wave = threadIdx.x >> 6;
+    const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
+    stream_matrix<FMT, UPL>(W, N, K, xs, xsum, w0, ws, [&](int64_t r, float v) { logits[r] = f2h(v); });
 }
 
-// Per-head RMSNorm of a 'hd' FP32 vector into dst (LDS) using one wavefront,
-// then the RoPE rotation at table row pos; round to FP16 precision when asked.
+// Per-head RMSNorm of an hd-long FP32 vector (one wavefront), RoPE at the
+// table row, optional FP16 rounding (the value the cache will hold), scale.
 __device__ void head_norm_rope(const float* src, const uint16_t* gamma, float eps, int hd, const float* cos_row,
                                const float* sin_row, float* dst, bool round16, float post_scale) {
     const int lane = threadIdx.x & 63;
     float ss = 0.f;
     for (int d = lane; d < hd; d += 64) ss += src[d] * src[d];
-    ss = wave_sum(ss);
+    ss = wave_allsum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
     for (int p = lane; p < hd / 2; p += 64) {
         float x0 = src[2 * p] * inv * h2f(gamma[2 * p]);
@@ -221,83 +243,170 @@ __device__ void head_norm_rope(const float* src, const uint16_t* gamma, float ep
 }
 
 // 2: attention partials for (split s, KV head g) at position *pos.
+// LDS: q[G][hd] f32 | kt[64][hd+2] f16 | vt[64][hd] f16 | p[G][64] f32 | red.
+template <int HD>
 __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict__ qkv, const uint16_t* q_norm,
-                                                        const uint16_t* k_norm, float eps, int n_q, int n_kv, int hd,
+                                                        const uint16_t* k_norm, float eps, int n_q, int n_kv, int,
                                                         const int32_t* __restrict__ pos_dev,
                                                         const float* __restrict__ cos_t,
                                                         const float* __restrict__ sin_t, uint16_t* Kc, uint16_t* Vc,
                                                         int S, float* __restrict__ part) {
     extern __shared__ __align__(16) float sm[];
+    constexpr int hd = HD;
     const int s = blockIdx.x, g = blockIdx.y;
     const int G = n_q / n_kv;
     const int pos = *pos_dev;
     int kps = (pos + 1 + S - 1) / S;
     if (kps < kMinKeysPerSplit) kps = kMinKeysPerSplit;
     const int kb = s * kps, ke = min(pos + 1, (s + 1) * kps);
-    float* qs = sm;                  // G * hd
-    float* ck = qs + G * hd;         // hd
-    float* cv = ck + hd;             // hd
-    float* sc = cv + hd;             // G * 256
-    float* red = sc + G * 256;       // 64
+    const int nk = ke - kb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int qd = n_q * hd, kvd = n_kv * hd;
+    if (nk <= 0) {  // empty split: a zero record the combine can read without branching
+        for (int i = threadIdx.x; i < G * (hd + 2); i += kThreads) {
+            const int h = i / (hd + 2), e = i % (hd + 2);
+            part[((int64_t)(g * G + h) * S + s) * (hd + 2) + e] = e == hd ? -INFINITY : 0.f;
+        }
+        return;
+    }
+    const int kstride = hd + 8;  // halves per K row in LDS (padding against bank conflicts)
+    float* qs = sm;
+    uint16_t* kt = reinterpret_cast<uint16_t*>(qs + G * hd);
+    uint16_t* vt = kt + kMaxKeysPerSplit * kstride;
+    float* pr = reinterpret_cast<float*>(vt + kMaxKeysPerSplit * hd);
+    float* ck = pr + G * kMaxKeysPerSplit;
+    float* cv = ck + hd;
+
+    // Issue the K/V tile loads first (16 bytes per thread per step).
+    const int chunks = nk * (hd / 8);  // 16-byte chunks per tile
+    constexpr int kMaxChunks = kMaxKeysPerSplit * HD / 8 / kThreads;
+    u4v kreg[kMaxChunks], vreg[kMaxChunks];
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < chunks) {
+            const int j = c / (hd / 8), d8 = c % (hd / 8);
+            const int64_t off = (int64_t)(kb + j) * kvd + (int64_t)g * hd + 8 * d8;
+            kreg[i] = ldg16(Kc + off);
+            vreg[i] = ldg16(Vc + off);
+        }
+    }
     const float* cos_row = cos_t + (int64_t)pos * (hd / 2);
     const float* sin_row = sin_t + (int64_t)pos * (hd / 2);
     const float scale = 1.0f / sqrtf((float)hd);
-    AttnArgs a{};
-    a.Kc = Kc; a.Vc = Vc; a.mask = nullptr; a.L = 1; a.valid_len = pos + 1;
-    a.n_q = n_q; a.n_kv = n_kv; a.hd = hd; a.softcap = 0.f; a.window = 0; a.kps = kps; a.S = S; a.ws = part;
-    if (kb < ke) {
-        // query heads of the group (wave w -> heads w, w+4, ...)
-        for (int i = wave; i < G; i += kWaves)
-            head_norm_rope(qkv + (int64_t)(g * G + i) * hd, q_norm, eps, hd, cos_row, sin_row, qs + i * hd, false,
-                           scale);
-        const bool has_cur = kb <= pos && pos < ke;
-        if (has_cur && wave == 0) {
-            head_norm_rope(qkv + qd + (int64_t)g * hd, k_norm, eps, hd, cos_row, sin_row, ck, true, 1.0f);
-            for (int d = lane; d < hd; d += 64) cv[d] = h2f(f2h(qkv[qd + kvd + (int64_t)g * hd + d]));
+    for (int i = wave; i < G; i += kWaves)
+        head_norm_rope(qkv + (int64_t)(g * G + i) * hd, q_norm, eps, hd, cos_row, sin_row, qs + i * hd, false,
+                       scale);
+    const bool has_cur = pos < ke;  // key pos is the last key of this split
+    if (has_cur && wave == kWaves - 1) {
+        head_norm_rope(qkv + qd + (int64_t)g * hd, k_norm, eps, hd, cos_row, sin_row, ck, true, 1.0f);
+        for (int d = lane; d < hd; d += 64) cv[d] = h2f(f2h(qkv[qd + kvd + (int64_t)g * hd + d]));
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < chunks) {
+            const int j = c / (hd / 8), d8 = c % (hd / 8);
+            *reinterpret_cast<u4v*>(kt + j * kstride + 8 * d8) = kreg[i];
+            *reinterpret_cast<u4v*>(vt + j * hd + 8 * d8) = vreg[i];
+        }
+    }
+    __syncthreads();
+    if (has_cur) {
+        // the current key/value replace the (stale) cache row in the tile and go to the cache
+        for (int d = threadIdx.x; d < hd; d += kThreads) {
+            const uint16_t kh = f2h(ck[d]), vh = f2h(cv[d]);
+            kt[(nk - 1) * kstride + d] = kh;
+            vt[(nk - 1) * hd + d] = vh;
+            Kc[(int64_t)pos * kvd + (int64_t)g * hd + d] = kh;
+            Vc[(int64_t)pos * kvd + (int64_t)g * hd + d] = vh;
         }
         __syncthreads();
-        if (has_cur) {
-            for (int d = threadIdx.x; d < hd; d += kThreads) {
-                Kc[(int64_t)pos * kvd + (int64_t)g * hd + d] = f2h(ck[d]);
-                Vc[(int64_t)pos * kvd + (int64_t)g * hd + d] = f2h(cv[d]);
+    }
+    // scores: wave h handles query head h, lane j handles key j
+    for (int h = wave; h < G; h += kWaves) {
+        float sc = -INFINITY;
+        if (lane < nk) {
+            const float* q = qs + h * hd;
+            const uint16_t* kr = kt + lane * kstride;
+            float a = 0.f;
+            for (int d = 0; d < hd; d += 8) {
+                const u4v kv = *reinterpret_cast<const u4v*>(kr + d);
+                const float4 q0 = *reinterpret_cast<const float4*>(q + d);
+                const float4 q1 = *reinterpret_cast<const float4*>(q + d + 4);
+                a += q0.x * h2f(kv.x & 0xffff) + q0.y * h2f(kv.x >> 16) + q0.z * h2f(kv.y & 0xffff) +
+                     q0.w * h2f(kv.y >> 16) + q1.x * h2f(kv.z & 0xffff) + q1.y * h2f(kv.z >> 16) +
+                     q1.z * h2f(kv.w & 0xffff) + q1.w * h2f(kv.w >> 16);
             }
+            sc = a;
         }
-        AttnState st;
-        attn_state_init(st);
-        attn_range(a, g, kb, ke, qs, sc, red, st, ck, cv, has_cur ? pos : -1);
-        attn_write_partial(a, 0, g, s, st);
-        attn_write_ml(a, 0, g, s, red);
-    } else {
-        // empty split: m = -inf, l = 0 (its o is never read)
-        if (threadIdx.x < G) {
-            float* rec = part + ((int64_t)(g * G + threadIdx.x) * S + s) * (hd + 2);
-            rec[hd] = -INFINITY;
-            rec[hd + 1] = 0.f;
+        const float m = wave_max(sc);
+        const float p = lane < nk ? __expf(sc - m) : 0.f;
+        const float l = wave_allsum(p);
+        if (lane < kMaxKeysPerSplit) pr[h * kMaxKeysPerSplit + lane] = p;
+        if (lane == 0) {
+            float* rec = part + ((int64_t)(g * G + h) * S + s) * (hd + 2);
+            rec[hd] = m;
+            rec[hd + 1] = l;
         }
+    }
+    __syncthreads();
+    // o[h][d] = sum_j p[h][j] * V[j][d]; thread -> (h, dim pair)
+    for (int idx = threadIdx.x; idx < G * (hd / 2); idx += kThreads) {
+        const int h = idx / (hd / 2), dp = idx % (hd / 2);
+        const float* p = pr + h * kMaxKeysPerSplit;
+        float o0 = 0.f, o1 = 0.f;
+        for (int j = 0; j < nk; ++j) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(vt + j * hd + 2 * dp);
+            o0 += p[j] * h2f(v & 0xffff);
+            o1 += p[j] * h2f(v >> 16);
+        }
+        float* rec = part + ((int64_t)(g * G + h) * S + s) * (hd + 2);
+        rec[2 * dp] = o0;
+        rec[2 * dp + 1] = o1;
     }
 }
 
 // 3: merge the S partials of each query head -> FP16 attention output.
-__global__ void combine_kernel(const float* __restrict__ part, int S, int hd, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ part, int S, int hd,
+                                                     uint16_t* __restrict__ out) {
+    __shared__ float w[512];
+    __shared__ float red[2];
     const int h = blockIdx.x;
     const float* base = part + (int64_t)h * S * (hd + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, base[(int64_t)s * (hd + 2) + hd]);
-    float lsum = 0.f;
-    for (int s = 0; s < S; ++s) {
+    float mloc = -INFINITY;
+    for (int s = threadIdx.x; s < S; s += blockDim.x) mloc = fmaxf(mloc, base[(int64_t)s * (hd + 2) + hd]);
+    mloc = wave_max(mloc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mloc;
+    __syncthreads();
+    const float M = fmaxf(red[0], red[1]);
+    float lloc = 0.f;
+    for (int s = threadIdx.x; s < S; s += blockDim.x) {
         const float m = base[(int64_t)s * (hd + 2) + hd];
-        if (m > -INFINITY) lsum += __expf(m - M) * base[(int64_t)s * (hd + 2) + hd + 1];
+        const float ws = m > -INFINITY ? __expf(m - M) : 0.f;
+        w[s] = ws;
+        lloc += ws * base[(int64_t)s * (hd + 2) + hd + 1];
     }
+    lloc = wave_allsum(lloc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = lloc;
+    __syncthreads();
+    const float lsum = red[0] + red[1];
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float o = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float m = base[(int64_t)s * (hd + 2) + hd];
-            if (m > -INFINITY) o += __expf(m - M) * base[(int64_t)s * (hd + 2) + d];
+        // branch-free so the loads of consecutive splits are issued back to back
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+        int s = 0;
+        for (; s + 4 <= S; s += 4) {
+            const float v0 = base[(int64_t)s * (hd + 2) + d], v1 = base[(int64_t)(s + 1) * (hd + 2) + d];
+            const float v2 = base[(int64_t)(s + 2) * (hd + 2) + d], v3 = base[(int64_t)(s + 3) * (hd + 2) + d];
+            o0 += w[s] * v0;
+            o1 += w[s + 1] * v1;
+            o2 += w[s + 2] * v2;
+            o3 += w[s + 3] * v3;
         }
-        out[(int64_t)h * hd + d] = f2h(o * inv);
+        for (; s < S; ++s) o0 += w[s] * base[(int64_t)s * (hd + 2) + d];
+        out[(int64_t)h * hd + d] = f2h((o0 + o1 + o2 + o3) * inv);
     }
 }
 
@@ -314,8 +423,10 @@ __global__ void advance_kernel(int32_t* tok, int32_t* pos, const int32_t* next, 
     }
 }
 
-unsigned gemv_blocks(int64_t rows) {
-    int64_t b = (rows + kWaves - 1) / kWaves;
+unsigned gemv_blocks(int64_t rows, int K) {
+    const int upl = upl_for(K);
+    const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
+    int64_t b = (rows + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
     if (b > cap) b = cap;
     return (unsigned)(b < 1 ? 1 : b);
@@ -323,7 +434,12 @@ unsigned gemv_blocks(int64_t rows) {
 
 size_t norm_lds(int K) { return (size_t)K * 2 + (size_t)(K / 16) * 4 + 64 * 4; }
 
-bool quant_or_f16(int t) {
+size_t attn_lds(int G, int hd) {
+    return (size_t)G * hd * 4 + (size_t)kMaxKeysPerSplit * (hd + 8) * 2 + (size_t)kMaxKeysPerSplit * hd * 2 +
+           (size_t)G * kMaxKeysPerSplit * 4 + (size_t)2 * hd * 4 + 256;
+}
+
+bool known_type(int t) {
     return t == BX_TYPE_Q4_K || t == BX_TYPE_Q6_K || t == BX_TYPE_Q8_0 || t == BX_TYPE_F16;
 }
 
@@ -331,7 +447,9 @@ int check_dims(const bx_decode_dims* d) {
     if (!d) return fail(BX_EINVAL, "decode: null dims");
     if (d->hidden <= 0 || d->hidden % 256 || d->intermediate <= 0 || d->intermediate % 256)
         return fail(BX_EUNSUPPORTED, "decode: hidden and intermediate must be multiples of 256");
-    if (d->n_q <= 0 || d->n_kv <= 0 || d->n_q % d->n_kv || d->n_q / d->n_kv > kAttnMaxGroup)
+    if (d->hidden > 12288 || d->intermediate > 12288 || d->n_q * d->head_dim > 12288)
+        return fail(BX_EUNSUPPORTED, "decode: K above 12288");
+    if (d->n_q <= 0 || d->n_kv <= 0 || d->n_q % d->n_kv || d->n_q / d->n_kv > kMaxGroup)
         return fail(BX_EUNSUPPORTED, "decode: unsupported head counts");
     if (d->head_dim % 8 || d->head_dim > 256 || d->head_dim <= 0)
         return fail(BX_EUNSUPPORTED, "decode: head_dim must be a multiple of 8 and <= 256");
@@ -340,11 +458,61 @@ int check_dims(const bx_decode_dims* d) {
     const int ts[8] = {d->qkv_type_q, d->qkv_type_k, d->qkv_type_v, d->o_type,
                        d->gate_type, d->up_type, d->down_type, d->lm_type};
     for (int t : ts)
-        if (!quant_or_f16(t)) return fail(BX_EUNSUPPORTED, "decode: unsupported weight type");
-    if (norm_lds(d->intermediate) > 65536 || norm_lds(d->hidden) > 65536 ||
-        norm_lds(d->n_q * d->head_dim) > 65536)
-        return fail(BX_EUNSUPPORTED, "decode: activation too large for LDS staging");
+        if (!known_type(t)) return fail(BX_EUNSUPPORTED, "decode: unsupported weight type");
+    if (d->gate_type != d->up_type) return fail(BX_EUNSUPPORTED, "decode: gate and up must share a type");
+    if (d->qkv_type_q != d->qkv_type_k) return fail(BX_EUNSUPPORTED, "decode: q and k must share a type");
+    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256)
+        return fail(BX_EUNSUPPORTED, "decode: head_dim must be 64, 128 or 256");
+    if (attn_lds(d->n_q / d->n_kv, d->head_dim) > 65536)
+        return fail(BX_EUNSUPPORTED, "decode: attention tile too large for LDS");
+    if (splits_for(*d) > 512) return fail(BX_EUNSUPPORTED, "decode: cache capacity too large (> 32768)");
     return BX_OK;
+}
+
+// ---- host-side specialisation dispatch ------------------------------------
+
+template <int FA, int FB>
+int launch_qkv_ab(int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h, const uint16_t* g, float eps,
+                  int K, Seg3 seg, float* out) {
+    BX_DISPATCH_UPL(upl, (norm_qkv_kernel<FA, FB, UPL_><<<blocks, kThreads, lds, st>>>(h, g, eps, K, seg, out)));
+    return launch_check("decode norm_qkv");
+}
+template <int FA>
+int launch_qkv_a(int tb, int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h, const uint16_t* g,
+                 float eps, int K, Seg3 seg, float* out) {
+    switch (tb) {
+        case BX_TYPE_Q4_K: return launch_qkv_ab<FA, FMT_Q4_K>(upl, blocks, lds, st, h, g, eps, K, seg, out);
+        case BX_TYPE_Q6_K: return launch_qkv_ab<FA, FMT_Q6_K>(upl, blocks, lds, st, h, g, eps, K, seg, out);
+        case BX_TYPE_Q8_0: return launch_qkv_ab<FA, FMT_Q8_0>(upl, blocks, lds, st, h, g, eps, K, seg, out);
+        default: return launch_qkv_ab<FA, FMT_F16>(upl, blocks, lds, st, h, g, eps, K, seg, out);
+    }
+}
+int launch_qkv(int ta, int tb, int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h,
+               const uint16_t* g, float eps, int K, Seg3 seg, float* out) {
+    switch (ta) {
+        case BX_TYPE_Q4_K: return launch_qkv_a<FMT_Q4_K>(tb, upl, blocks, lds, st, h, g, eps, K, seg, out);
+        case BX_TYPE_Q6_K: return launch_qkv_a<FMT_Q6_K>(tb, upl, blocks, lds, st, h, g, eps, K, seg, out);
+        case BX_TYPE_Q8_0: return launch_qkv_a<FMT_Q8_0>(tb, upl, blocks, lds, st, h, g, eps, K, seg, out);
+        default: return launch_qkv_a<FMT_F16>(tb, upl, blocks, lds, st, h, g, eps, K, seg, out);
+    }
+}
+int launch_resid(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const uint16_t* x, int K,
+                 const void* W, int N, float* h) {
+    BX_DISPATCH_FMT(type, BX_DISPATCH_UPL(upl, (gemv_resid_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(
+                                                   x, K, W, N, h))));
+    return launch_check("decode gemv_resid");
+}
+int launch_mlp(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h, const uint16_t* g,
+               float eps, int K, const void* Wg, const void* Wu, int F, uint16_t* act) {
+    BX_DISPATCH_FMT(type, BX_DISPATCH_UPL(upl, (norm_mlp_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(
+                                                   h, g, eps, K, Wg, Wu, F, act))));
+    return launch_check("decode norm_mlp");
+}
+int launch_head(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h, const uint16_t* g,
+                float eps, int K, const void* W, int N, uint16_t* logits) {
+    BX_DISPATCH_FMT(type, BX_DISPATCH_UPL(upl, (norm_head_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(
+                                                   h, g, eps, K, W, N, logits))));
+    return launch_check("decode head");
 }
 
 }  // namespace
@@ -387,29 +555,36 @@ int bx_decode_layer_run(const bx_decode_dims* d, const bx_decode_layer* L, const
     seg.W[0] = L->Wq; seg.type[0] = d->qkv_type_q; seg.rows[0] = qd;
     seg.W[1] = L->Wk; seg.type[1] = d->qkv_type_k; seg.rows[1] = kvd;
     seg.W[2] = L->Wv; seg.type[2] = d->qkv_type_v; seg.rows[2] = kvd;
-    norm_qkv_kernel<<<gemv_blocks(qd + 2 * kvd), kThreads, norm_lds(H), st>>>(
-        h, static_cast<const uint16_t*>(L->in_ln), d->eps, H, seg, qkv);
-    if (int rc = launch_check("decode norm_qkv")) return rc;
+    if (int rc = launch_qkv(d->qkv_type_q, d->qkv_type_v, upl_for(H), gemv_blocks(qd + 2 * kvd, H), norm_lds(H), st,
+                            h, static_cast<const uint16_t*>(L->in_ln), d->eps, H, seg, qkv))
+        return rc;
 
     const int G = d->n_q / d->n_kv;
-    const size_t alds = (size_t)(G * hd + 2 * hd + G * 256 + 64) * sizeof(float);
-    attn_kernel<<<dim3(w.S, d->n_kv), kThreads, alds, st>>>(
-        qkv, static_cast<const uint16_t*>(L->q_norm), static_cast<const uint16_t*>(L->k_norm), d->eps, d->n_q,
-        d->n_kv, hd, pos_dev, cos_tab, sin_tab, static_cast<uint16_t*>(L->Kc), static_cast<uint16_t*>(L->Vc), w.S,
-        part);
+    const dim3 agrid(w.S, d->n_kv);
+    const size_t alds = attn_lds(G, hd);
+    const auto* qn = static_cast<const uint16_t*>(L->q_norm);
+    const auto* kn = static_cast<const uint16_t*>(L->k_norm);
+    auto* Kc = static_cast<uint16_t*>(L->Kc);
+    auto* Vc = static_cast<uint16_t*>(L->Vc);
+    if (hd == 64)
+        attn_kernel<64><<<agrid, kThreads, alds, st>>>(qkv, qn, kn, d->eps, d->n_q, d->n_kv, hd, pos_dev, cos_tab,
+                                                       sin_tab, Kc, Vc, w.S, part);
+    else if (hd == 128)
+        attn_kernel<128><<<agrid, kThreads, alds, st>>>(qkv, qn, kn, d->eps, d->n_q, d->n_kv, hd, pos_dev, cos_tab,
+                                                        sin_tab, Kc, Vc, w.S, part);
+    else
+        attn_kernel<256><<<agrid, kThreads, alds, st>>>(qkv, qn, kn, d->eps, d->n_q, d->n_kv, hd, pos_dev, cos_tab,
+                                                        sin_tab, Kc, Vc, w.S, part);
     if (int rc = launch_check("decode attn")) return rc;
     combine_kernel<<<d->n_q, 128, 0, st>>>(part, w.S, hd, attn);
     if (int rc = launch_check("decode combine")) return rc;
 
-    gemv_resid_kernel<<<gemv_blocks(H), kThreads, norm_lds(qd), st>>>(attn, qd, L->Wo, d->o_type, H, h);
-    if (int rc = launch_check("decode o_proj")) return rc;
-
-    norm_mlp_kernel<<<gemv_blocks(F), kThreads, norm_lds(H), st>>>(
-        h, static_cast<const uint16_t*>(L->post_ln), d->eps, H, L->Wg, d->gate_type, L->Wu, d->up_type, F, act);
-    if (int rc = launch_check("decode norm_mlp")) return rc;
-
-    gemv_resid_kernel<<<gemv_blocks(H), kThreads, norm_lds(F), st>>>(act, F, L->Wd, d->down_type, H, h);
-    return launch_check("decode down");
+    if (int rc = launch_resid(d->o_type, upl_for(qd), gemv_blocks(H, qd), norm_lds(qd), st, attn, qd, L->Wo, H, h))
+        return rc;
+    if (int rc = launch_mlp(d->gate_type, upl_for(H), gemv_blocks(2 * F, H), norm_lds(H), st, h,
+                            static_cast<const uint16_t*>(L->post_ln), d->eps, H, L->Wg, L->Wu, F, act))
+        return rc;
+    return launch_resid(d->down_type, upl_for(F), gemv_blocks(H, F), norm_lds(F), st, act, F, L->Wd, H, h);
 }
 
 int bx_decode_head(const bx_decode_dims* d, const uint16_t* final_norm, const void* lm_head, uint16_t* logits,
@@ -418,9 +593,8 @@ int bx_decode_head(const bx_decode_dims* d, const uint16_t* final_norm, const vo
     if (!final_norm || !lm_head || !logits || !ws) return fail(BX_EINVAL, "decode_head: null pointer");
     const WsLayout w = ws_layout(*d);
     const float* h = reinterpret_cast<const float*>(static_cast<char*>(ws) + w.h);
-    norm_head_kernel<<<gemv_blocks(d->vocab), kThreads, norm_lds(d->hidden), as_stream(stream)>>>(
-        h, final_norm, d->eps, d->hidden, lm_head, d->lm_type, d->vocab, logits);
-    return launch_check("decode head");
+    return launch_head(d->lm_type, upl_for(d->hidden), gemv_blocks(d->vocab, d->hidden), norm_lds(d->hidden),
+                       as_stream(stream), h, final_norm, d->eps, d->hidden, lm_head, d->vocab, logits);
 }
 
 int bx_decode_advance(int32_t* tok_dev, int32_t* pos_dev, const int32_t* next_dev, int32_t* hist, int32_t* count,

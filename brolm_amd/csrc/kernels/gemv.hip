@@ -56,6 +56,53 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const void* __restrict__
     }
 }
 
+// M = 1: activations staged swizzled for every format, then held in
+// registers; each wavefront streams R rows per task (gemv_core.h).
+template <int FMT, int UPL>
+__global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restrict__ W,
+                                                          const uint16_t* __restrict__ X,
+                                                          const uint16_t* __restrict__ bias,
+                                                          uint16_t* __restrict__ Y, int N, int K) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    uint32_t* xs = smem;
+    float* xsum = reinterpret_cast<float*>(smem + K / 2);
+    stage_x_f16<true, false>(X, K, 1, K, xs, K / 2, xsum, K / 16);
+    __syncthreads();
+    sums_from_lds(xs, 1, K, K / 2, xsum, K / 16);
+    __syncthreads();
+    constexpr int R = RowsPer<UPL>::R;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    XCache<FMT, UPL> xu;
+    xu.init(xs, xsum, K);
+    const int64_t tasks = ((int64_t)N + R - 1) / R;
+    for (int64_t t = (int64_t)blockIdx.x * kWaves + wave; t < tasks; t += (int64_t)gridDim.x * kWaves) {
+        float o[R];
+        rows_dot_m1<FMT, UPL, R>(W, N, K, t * R, xu, o);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int64_t row = t * R + rr;
+                if (row < N) Y[row] = f2h(o[rr] + (bias ? h2f(bias[row]) : 0.f));
+            }
+        }
+    }
+}
+
+int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int N, int K,
+                   hipStream_t st) {
+    const int upl = upl_for(K);
+    if (upl > 6) return fail(BX_EUNSUPPORTED, "gemv: K above 12288 at M = 1");
+    const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
+    int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
+    const int64_t cap = (int64_t)num_cus() * 8;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = (size_t)K * 2 + (size_t)(K / 16) * 4;
+    BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL(upl, {
+        gemv_m1_kernel<FMT_, UPL_><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
+    }))
+    return launch_check("gemv m1");
+}
+
 size_t gemv_lds_bytes(int fmt, int M, int K) {
     size_t b = (size_t)M * K * 2;
     if (fmt == FMT_Q4_K) b += (size_t)M * (K / 16) * 4;
@@ -115,6 +162,7 @@ int check_linear_shape(int wtype, int M, int N, int K) {
 
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st) {
+    if (M == 1 && upl_for(K) <= 6) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
     switch (wtype) {
         case BX_TYPE_Q4_K: return gemv_dispatch<FMT_Q4_K>(M, W, X, bias, Y, N, K, st);
         case BX_TYPE_Q6_K: return gemv_dispatch<FMT_Q6_K>(M, W, X, bias, Y, N, K, st);

@@ -328,3 +328,277 @@ __device__ __forceinline__ void dot_unit_f16_swz(const RawF16& r, int u, const u
 }
 
 }  // namespace bx
+
+namespace bx {
+
+// ---- M = 1 decode core: activations held in registers ------------------------
+//
+// Each lane owns the units u = lane + 64*i (i < UPL) of every row, so its 32
+// activation values per unit are loaded from LDS once and reused for all rows
+// the wavefront streams.  R rows are loaded before any math so R*UPL 16-byte
+// weight loads are in flight per lane.
+
+struct XU {
+    uint32_t p[16];   // activation pairs in the unit's weight-pair order
+    float s0, s1;     // Q4_K: sums of the low / high 16-element segments
+};
+
+template <int FMT>
+__device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum, int u) {
+    XU x;
+    if constexpr (FMT == FMT_Q4_K) {
+        const int b = u >> 3, t = u & 7, c = t >> 1;
+        const int e_lo = 256 * b + 64 * c + 16 * (t & 1), e_hi = e_lo + 32;
+        const u4v a0 = *reinterpret_cast<const u4v*>(xs + (e_lo >> 1));
+        const u4v a1 = *reinterpret_cast<const u4v*>(xs + (e_lo >> 1) + 4);
+        const u4v b0 = *reinterpret_cast<const u4v*>(xs + (e_hi >> 1));
+        const u4v b1 = *reinterpret_cast<const u4v*>(xs + (e_hi >> 1) + 4);
+        x.p[0] = a0.x; x.p[1] = a0.y; x.p[2] = a0.z; x.p[3] = a0.w;
+        x.p[4] = a1.x; x.p[5] = a1.y; x.p[6] = a1.z; x.p[7] = a1.w;
+        x.p[8] = b0.x; x.p[9] = b0.y; x.p[10] = b0.z; x.p[11] = b0.w;
+        x.p[12] = b1.x; x.p[13] = b1.y; x.p[14] = b1.z; x.p[15] = b1.w;
+        x.s0 = xsum[e_lo >> 4];
+        x.s1 = xsum[e_hi >> 4];
+    } else if constexpr (FMT == FMT_Q6_K) {
+        const int b = u >> 3, t = u & 7, h = t >> 2, l0 = 8 * (t & 3);
+        const int e0 = 256 * b + 128 * h + l0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u4v v = *reinterpret_cast<const u4v*>(xs + ((e0 + 32 * j) >> 1));
+            x.p[4 * j] = v.x; x.p[4 * j + 1] = v.y; x.p[4 * j + 2] = v.z; x.p[4 * j + 3] = v.w;
+        }
+        x.s0 = x.s1 = 0.f;
+    } else {
+        const int e0 = 32 * u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u4v v = *reinterpret_cast<const u4v*>(xs + (e0 >> 1) + 4 * q);
+            x.p[4 * q] = v.x; x.p[4 * q + 1] = v.y; x.p[4 * q + 2] = v.z; x.p[4 * q + 3] = v.w;
+        }
+        x.s0 = x.s1 = 0.f;
+    }
+    return x;
+}
+
+__device__ __forceinline__ float dot_reg(const RawQ4K& r, int u, const XU& x) {
+    const int c = (u & 7) >> 1;
+    const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
+    int sc0, m0, sc1, m1;
+    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c, sc0, m0);
+    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c + 1, sc1, m1);
+    const float s_lo = d * (float)sc0, s_hi = d * (float)sc1;
+    const float c_lo = 8.f * s_lo - dmin * (float)m0, c_hi = 8.f * s_hi - dmin * (float)m1;
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    float al = 0.f, ah = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t w = qw[k];
+        al = dot2(x.p[2 * k], centre(magic_pair(w & 0x000F000Fu), 1032.f), al);
+        al = dot2(x.p[2 * k + 1], centre(magic_pair((w >> 8) & 0x000F000Fu), 1032.f), al);
+        ah = dot2(x.p[8 + 2 * k], centre(magic_pair((w >> 4) & 0x000F000Fu), 1032.f), ah);
+        ah = dot2(x.p[8 + 2 * k + 1], centre(magic_pair((w >> 12) & 0x000F000Fu), 1032.f), ah);
+    }
+    return s_lo * al + c_lo * x.s0 + s_hi * ah + c_hi * x.s1;
+}
+
+__device__ __forceinline__ float dot_reg(const RawQ6K& r, int u, const XU& x) {
+    const int t = u & 7, h = t >> 2, l0 = 8 * (t & 3);
+    const float d = h2f(r.d & 0xffff);
+    const uint32_t slo = h ? r.sc.z : r.sc.x, shi = h ? r.sc.w : r.sc.y;
+    const int sb = (l0 >= 16) ? 8 : 0;
+    const float s0 = d * (float)(int8_t)((slo >> sb) & 0xff), s1 = d * (float)(int8_t)((slo >> (16 + sb)) & 0xff);
+    const float s2 = d * (float)(int8_t)((shi >> sb) & 0xff), s3 = d * (float)(int8_t)((shi >> (16 + sb)) & 0xff);
+    const uint32_t A[2] = {r.ql.x, r.ql.y}, B[2] = {r.ql.z, r.ql.w}, Hq[2] = {r.qh.x, r.qh.y};
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t a = A[k], bb = B[k], q = Hq[k];
+        a0 = dot2(x.p[2 * k], centre(magic_pair((a & 0x000F000Fu) | ((q & 0x00030003u) << 4)), 1056.f), a0);
+        a0 = dot2(x.p[2 * k + 1],
+                  centre(magic_pair(((a >> 8) & 0x000F000Fu) | (((q >> 8) & 0x00030003u) << 4)), 1056.f), a0);
+        a1 = dot2(x.p[4 + 2 * k], centre(magic_pair((bb & 0x000F000Fu) | (((q >> 2) & 0x00030003u) << 4)), 1056.f), a1);
+        a1 = dot2(x.p[4 + 2 * k + 1],
+                  centre(magic_pair(((bb >> 8) & 0x000F000Fu) | (((q >> 10) & 0x00030003u) << 4)), 1056.f), a1);
+        a2 = dot2(x.p[8 + 2 * k],
+                  centre(magic_pair(((a >> 4) & 0x000F000Fu) | (((q >> 4) & 0x00030003u) << 4)), 1056.f), a2);
+        a2 = dot2(x.p[8 + 2 * k + 1],
+                  centre(magic_pair(((a >> 12) & 0x000F000Fu) | (((q >> 12) & 0x00030003u) << 4)), 1056.f), a2);
+        a3 = dot2(x.p[12 + 2 * k],
+                  centre(magic_pair(((bb >> 4) & 0x000F000Fu) | (((q >> 6) & 0x00030003u) << 4)), 1056.f), a3);
+        a3 = dot2(x.p[12 + 2 * k + 1],
+                  centre(magic_pair(((bb >> 12) & 0x000F000Fu) | (((q >> 14) & 0x00030003u) << 4)), 1056.f), a3);
+    }
+    return s0 * a0 + s1 * a1 + s2 * a2 + s3 * a3;
+}
+
+__device__ __forceinline__ float dot_reg(const RawQ8& r, int, const XU& x) {
+    const float d = h2f(r.d & 0xffff);
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        s = dot2(x.p[2 * k], centre(magic_pair((qw[k] & 0x00FF00FFu) ^ 0x00800080u), 1152.f), s);
+        s = dot2(x.p[2 * k + 1], centre(magic_pair(((qw[k] >> 8) & 0x00FF00FFu) ^ 0x00800080u), 1152.f), s);
+    }
+    return d * s;
+}
+
+// FP16 weights against swizzled activations: re-pair (w0,w1),(w2,w3) -> (w0,w2),(w1,w3).
+__device__ __forceinline__ float dot_reg(const RawF16& r, int, const XU& x) {
+    const uint32_t w[16] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w,
+                            r.w2.x, r.w2.y, r.w2.z, r.w2.w, r.w3.x, r.w3.y, r.w3.z, r.w3.w};
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const uint32_t a = w[2 * g], b = w[2 * g + 1];
+        s = dot2(x.p[2 * g], __builtin_amdgcn_perm(b, a, 0x05040100u), s);
+        s = dot2(x.p[2 * g + 1], __builtin_amdgcn_perm(b, a, 0x07060302u), s);
+    }
+    return s;
+}
+
+// 64-lane all-reduce: DPP within rows of 16 (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror), shuffles across rows.
+__device__ __forceinline__ float wave_allsum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Dot products of rows row0 .. row0+R-1 (clamped to N-1 for loads) with the
+// activation held in xu; every lane returns the R sums.
+// Activation source for rows_dot_m1: registers when a lane owns at most two
+// units (K <= 4096), otherwise re-read from LDS per unit to stay in budget.
+template <int FMT, int UPL>
+struct XCache {
+    static constexpr bool kRegs = UPL <= 2;
+    XU x[kRegs ? UPL : 1];
+    const uint32_t* xs;
+    const float* xsum;
+    __device__ __forceinline__ void init(const uint32_t* xs_, const float* xsum_, int K);
+    __device__ __forceinline__ XU get(int i, int u) const;
+};
+
+// Rows per wavefront task for a given units-per-lane count.
+template <int UPL>
+struct RowsPer {
+    static constexpr int R = UPL == 1 ? 4 : (UPL == 2 ? 2 : 1);
+};
+
+template <int FMT, int UPL, int R>
+__device__ __forceinline__ void rows_dot_m1(const void* W, int64_t N, int K, int64_t row0,
+                                            const XCache<FMT, UPL>& xu, float (&out)[R]) {
+    const int lane = threadIdx.x & 63;
+    const int U = K / 32;
+    typename RawOf<FMT>::T raw[R][UPL];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        const int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = lane + 64 * i;
+            if (u < U) raw[rr][i] = load_unit<FMT>(W, N, K, row, u);
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = lane + 64 * i;
+            if (u < U) a += dot_reg(raw[rr][i], u, xu.get(i, u));
+        }
+        out[rr] = wave_allsum(a);
+    }
+}
+
+template <int FMT, int UPL>
+__device__ __forceinline__ void XCache<FMT, UPL>::init(const uint32_t* xs_, const float* xsum_, int K) {
+    xs = xs_;
+    xsum = xsum_;
+    if constexpr (kRegs) load_xu_all<FMT, UPL>(xs_, xsum_, K, x);
+}
+
+template <int FMT, int UPL>
+__device__ __forceinline__ XU XCache<FMT, UPL>::get(int i, int u) const {
+    if constexpr (kRegs) return x[i];
+    else return load_xu<FMT>(xs, xsum, u);
+}
+
+template <int FMT, int UPL>
+__device__ __forceinline__ void load_xu_all(const uint32_t* xs, const float* xsum, int K, XU (&xu)[UPL]) {
+    const int lane = threadIdx.x & 63;
+    const int U = K / 32;
+#pragma unroll
+    for (int i = 0; i < UPL; ++i) {
+        const int u = lane + 64 * i;
+        if (u < U) xu[i] = load_xu<FMT>(xs, xsum, u);
+    }
+}
+
+}  // namespace bx
+
+namespace bx {
+
+// Same as rows_dot_m1 for two matrices of one format and shape (gate / up):
+// all 2*R rows are in flight before the math.
+template <int FMT, int UPL, int R>
+__device__ __forceinline__ void rows_dot_m1_pair(const void* Wa, const void* Wb, int64_t N, int K, int64_t row0,
+                                                 const XCache<FMT, UPL>& xu, float (&oa)[R], float (&ob)[R]) {
+    const int lane = threadIdx.x & 63;
+    const int U = K / 32;
+    typename RawOf<FMT>::T ra[R][UPL], rb[R][UPL];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        const int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = lane + 64 * i;
+            if (u < U) {
+                ra[rr][i] = load_unit<FMT>(Wa, N, K, row, u);
+                rb[rr][i] = load_unit<FMT>(Wb, N, K, row, u);
+            }
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = lane + 64 * i;
+            if (u < U) {
+                a += dot_reg(ra[rr][i], u, xu.get(i, u));
+                b += dot_reg(rb[rr][i], u, xu.get(i, u));
+            }
+        }
+        oa[rr] = wave_allsum(a);
+        ob[rr] = wave_allsum(b);
+    }
+}
+
+// Units per lane for K (32-element units spread over 64 lanes).
+__host__ __device__ constexpr int upl_for(int K) { return (K / 32 + 63) / 64; }
+
+}  // namespace bx
+
+// Dispatch `BODY` with constexpr FMT_ (from a runtime ggml type) and UPL_ (from
+// a runtime units-per-lane count in {1,2,3,4,6}).
+#define BX_DISPATCH_UPL(upl, ...)                                  \
+    switch (upl) {                                                 \
+        case 1: { constexpr int UPL_ = 1; __VA_ARGS__; } break;    \
+        case 2: { constexpr int UPL_ = 2; __VA_ARGS__; } break;    \
+        case 3: { constexpr int UPL_ = 3; __VA_ARGS__; } break;    \
+        case 4: { constexpr int UPL_ = 4; __VA_ARGS__; } break;    \
+        default: { constexpr int UPL_ = 6; __VA_ARGS__; } break;   \
+    }
+#define BX_DISPATCH_FMT(type, ...)                                                 \
+    switch (type) {                                                                \
+        case BX_TYPE_Q4_K: { constexpr int FMT_ = bx::FMT_Q4_K; __VA_ARGS__; } break; \
+        case BX_TYPE_Q6_K: { constexpr int FMT_ = bx::FMT_Q6_K; __VA_ARGS__; } break; \
+        case BX_TYPE_Q8_0: { constexpr int FMT_ = bx::FMT_Q8_0; __VA_ARGS__; } break; \
+        default: { constexpr int FMT_ = bx::FMT_F16; __VA_ARGS__; } break;         \
+    }

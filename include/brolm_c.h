@@ -87,6 +87,9 @@ int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m);
 /* sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142). */
 int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed);
 
+/* Synthetic prompt of tools/bench_decode.cpp:208-213: std::mt19937_64(seed)() % vocab. */
+int brolm_prompt_ids(uint64_t seed, int n, int vocab, int32_t* out);
+
 /* BROLM_PROFILE stage table (src/detail/profile.cpp). */
 void brolm_profile_reset(void);
 void brolm_profile_report(void);
