@@ -1,0 +1,321 @@
+"""Kernel parity on the device, through the C ABI of libbrolm_hip.so, against
+the CPU oracle and the independent block encoder.  Integer/byte work is
+bit-exact; floating-point results carry the tolerance stated in each test."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+import spec_blocks as sb
+from gpu_util import call, carrier, dev, empty, f16_dev, f16_host, host, hip, ptr, release, stream, torch
+
+pytestmark = pytest.mark.gpu
+
+QTYPES = [8, 12, 14]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    import brolm_amd as ba
+    ba.init()
+    assert hip().bx_device_ok() == 1
+
+
+@pytest.fixture(autouse=True)
+def _keep_buffers_until_done():
+    yield
+    release()
+
+
+def _f16(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+# ----------------------------------------------------------------- carriers and dequant (bit-exact)
+
+@pytest.mark.parametrize("t", QTYPES)
+@pytest.mark.parametrize("rows,cols", [(1, 256), (3, 512), (37, 1024), (5, 6144)])
+def test_repack_roundtrip_and_dequant_bit_exact(t, rows, cols):
+    print(f"[dequant] type={t} rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows * cols + t)
+    raw, want = sb.random_matrix(rng, t, rows, cols)
+    assert hip().bx_carrier_bytes(t, rows, cols) == len(raw)
+    car = carrier(t, raw, rows, cols)
+    back = empty(len(raw))
+    call("bx_unpack_carrier_rows", t, ptr(car), ptr(back), rows, cols, stream())
+    assert host(back).tobytes() == raw
+    f32 = torch().empty(rows * cols, dtype=torch().float32, device="cuda")
+    call("bx_dequant_to_f32", t, ptr(car), ptr(f32), rows, cols, stream())
+    assert np.array_equal(host(f32).view(np.uint32), want.reshape(-1).view(np.uint32))
+    f16 = torch().empty(rows * cols, dtype=torch().int16, device="cuda")
+    call("bx_dequant_to_f16", t, ptr(car), ptr(f16), rows, cols, stream())
+    assert np.array_equal(host(f16).view(np.uint16), want.reshape(-1).astype(np.float16).view(np.uint16))
+
+
+def test_dequant_golden_fixture():
+    from golden import load_blocks
+    for t, raw, f32_bits, f16_bits in load_blocks():
+        cols = sb.QK[t] * 4
+        rows = f32_bits.size // cols
+        car = carrier(t, raw, rows, cols)
+        f32 = torch().empty(f32_bits.size, dtype=torch().float32, device="cuda")
+        call("bx_dequant_to_f32", t, ptr(car), ptr(f32), rows, cols, stream())
+        assert np.array_equal(host(f32).view(np.uint32), f32_bits)
+        f16 = torch().empty(f32_bits.size, dtype=torch().int16, device="cuda")
+        call("bx_dequant_to_f16", t, ptr(car), ptr(f16), rows, cols, stream())
+        assert np.array_equal(host(f16).view(np.uint16), f16_bits)
+
+
+# ----------------------------------------------------------------- linear (GEMV M<=16, GEMM above)
+
+def _linear_tol(W: np.ndarray, X: np.ndarray, ref: np.ndarray) -> np.ndarray:
+    """FP16 output rounding (2^-11 relative, doubled) plus an FP32
+    accumulation allowance of 2^-14 of the absolute dot-product mass.  For
+    M > 16 the prefill GEMM feeds the MFMA dequantized weights rounded to FP16
+    (relative error <= 2^-11 per product), so its bound adds 2^-11 of the mass."""
+    mass = np.abs(X.astype(np.float64)) @ np.abs(W.astype(np.float64)).T
+    gemm = 2.0 ** -11 if X.shape[0] > 16 else 0.0
+    return 2.0 ** -10 * np.abs(ref) + (2.0 ** -14 + gemm) * mass + 1e-6
+
+
+def _run_linear(t, Wdev, X, N, K, bias=None):
+    M = X.shape[0]
+    x = f16_dev(X)
+    y = torch().empty(M * N, dtype=torch().int16, device="cuda")
+    b = f16_dev(bias) if bias is not None else None
+    call("bx_linear_f16", t, ptr(Wdev), ptr(b), ptr(x), ptr(y), M, N, K, stream())
+    return f16_host(y).reshape(M, N)
+
+
+@pytest.mark.parametrize("t", QTYPES)
+@pytest.mark.parametrize("N,K", [(1, 256), (7, 512), (96, 1024), (300, 2048), (64, 3072), (33, 6144), (40, 8192),
+                                 (9, 12288)])
+def test_linear_quant_vs_oracle(t, N, K):
+    rng = np.random.default_rng(N * 31 + K + t)
+    raw, Wv = sb.random_matrix(rng, t, N, K)
+    car = carrier(t, raw, N, K)
+    for M in (1, 2, 3, 4, 5, 8, 16, 17, 64, 130):
+        print(f"[linear] type={t} N={N} K={K} M={M}", flush=True)
+        X = _f16(rng.standard_normal((M, K)))
+        got = _run_linear(t, car, X, N, K)
+        ref = oracle.linear(Wv, X)
+        err = np.abs(got - ref)
+        tol = _linear_tol(Wv, X, ref)
+        assert np.all(err <= tol), (M, float((err / tol).max()))
+
+
+@pytest.mark.parametrize("t", [1, 12])
+def test_linear_bias_and_dense_f16(t):
+    rng = np.random.default_rng(5)
+    N, K = 200, 1024
+    if t == 1:
+        Wv = _f16(rng.standard_normal((N, K)) * 0.05)
+        Wdev = f16_dev(Wv)
+    else:
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        Wdev = carrier(t, raw, N, K)
+    bias = _f16(rng.standard_normal(N))
+    for M in (1, 4, 33):
+        X = _f16(rng.standard_normal((M, K)))
+        got = _run_linear(t, Wdev, X, N, K, bias)
+        ref = oracle.linear(Wv, X) + bias
+        assert np.all(np.abs(got - ref) <= _linear_tol(Wv, X, ref) + 2.0 ** -10 * np.abs(bias)), M
+
+
+def test_linear_onehot_selects_dequantized_column():
+    """X = e_k makes Y the k-th dequantized column, rounded once to FP16."""
+    rng = np.random.default_rng(9)
+    for t in QTYPES:
+        N, K = 64, 512
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        car = carrier(t, raw, N, K)
+        for k in (0, 31, 32, 255, 256, 511):
+            X = np.zeros((1, K), np.float32)
+            X[0, k] = 1.0
+            got = _run_linear(t, car, X, N, K)
+            assert np.array_equal(got[0], _f16(Wv[:, k])), (t, k)
+
+
+# ----------------------------------------------------------------- norms, rope, kv
+
+@pytest.mark.parametrize("x_is_f32", [0, 1])
+def test_rms_norm(x_is_f32):
+    rng = np.random.default_rng(11)
+    rows, cols = 9, 2048
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 2
+    if not x_is_f32:
+        x = _f16(x)
+    g = _f16(rng.uniform(0.5, 1.5, cols))
+    xd = dev(x) if x_is_f32 else f16_dev(x)
+    y = torch().empty(rows * cols, dtype=torch().int16, device="cuda")
+    call("bx_rms_norm", ptr(xd), x_is_f32, ptr(f16_dev(g)), C.c_float(1e-6), ptr(y), rows, cols, stream())
+    ref = oracle.rms_norm(x, g, 1e-6)
+    np.testing.assert_allclose(f16_host(y).reshape(rows, cols), ref, atol=2e-3 * np.abs(ref).max(), rtol=2 ** -10)
+
+
+@pytest.mark.parametrize("hd,pos0", [(64, 0), (128, 1023), (128, 40000)])
+def test_rope(hd, pos0):
+    rng = np.random.default_rng(hd + pos0)
+    n_heads, L, theta = 4, 3, 1e6
+    cap = pos0 + L + 5
+    cos = np.empty((cap, hd // 2), np.float32)
+    sin = np.empty((cap, hd // 2), np.float32)
+    hip().bx_rope_table_host(cos.ctypes.data_as(C.POINTER(C.c_float)), sin.ctypes.data_as(C.POINTER(C.c_float)),
+                             cap, hd, C.c_float(theta))
+    x = _f16(rng.standard_normal((L, n_heads * hd)))
+    xd = f16_dev(x)
+    call("bx_rope_f16", ptr(xd), ptr(xd), L, hd, n_heads, pos0, ptr(dev(cos)), ptr(dev(sin)), cap, stream())
+    ref = oracle.rope(x, hd, n_heads, pos0, theta)
+    np.testing.assert_allclose(f16_host(xd).reshape(L, -1), ref, atol=4e-3)
+
+
+def test_kv_append_and_scatter_row():
+    rng = np.random.default_rng(12)
+    cap, cols, L, cur = 16, 256, 3, 5
+    Kc = torch().zeros(cap * cols, dtype=torch().int16, device="cuda")
+    Vc = torch().zeros(cap * cols, dtype=torch().int16, device="cuda")
+    k = rng.integers(0, 1 << 15, (L, cols)).astype(np.uint16)
+    v = rng.integers(0, 1 << 15, (L, cols)).astype(np.uint16)
+    call("bx_kv_append_f16", ptr(dev(k)), ptr(dev(v)), L, cols, cur, ptr(Kc), ptr(Vc), cap, stream())
+    kh, vh = host(Kc).view(np.uint16).reshape(cap, cols), host(Vc).view(np.uint16).reshape(cap, cols)
+    assert np.array_equal(kh[cur:cur + L], k) and np.array_equal(vh[cur:cur + L], v)
+    assert not kh[:cur].any() and not kh[cur + L:].any()
+    row = rng.integers(0, 1 << 15, cols).astype(np.uint16)
+    idx = dev(np.array([11], np.int32))
+    call("bx_scatter_row", ptr(dev(row)), ptr(idx), ptr(Kc), cols * 2, cap, stream())
+    assert np.array_equal(host(Kc).view(np.uint16).reshape(cap, cols)[11], row)
+
+
+# ----------------------------------------------------------------- attention
+
+def _attn_ref(q, K, V, L, valid, n_q, n_kv, hd, softcap=0.0, window=0, mask=None):
+    """float64 softmax attention with GQA map h -> h // (n_q / n_kv)."""
+    out = np.zeros((L, n_q * hd))
+    G = n_q // n_kv
+    for r in range(L):
+        p = valid - L + r
+        lo = max(0, p - window + 1) if window > 0 else 0
+        keys = np.arange(lo, p + 1)
+        if mask is not None:
+            keys = np.nonzero(mask[:valid])[0]
+        for h in range(n_q):
+            g = h // G
+            s = K[keys, g * hd:(g + 1) * hd].astype(np.float64) @ q[r, h * hd:(h + 1) * hd].astype(np.float64)
+            s /= np.sqrt(hd)
+            if softcap > 0:
+                s = softcap * np.tanh(s / softcap)
+            w = np.exp(s - s.max())
+            out[r, h * hd:(h + 1) * hd] = (w / w.sum()) @ V[keys, g * hd:(g + 1) * hd].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("L,valid,n_q,n_kv,hd", [
+    (1, 1, 4, 2, 64), (1, 5, 16, 8, 128), (1, 64, 16, 8, 128), (1, 65, 16, 8, 128), (1, 300, 8, 8, 64),
+    (1, 2049, 16, 8, 128), (1, 4096, 32, 8, 128), (4, 70, 4, 2, 64), (16, 600, 16, 8, 128)])
+def test_attention_decode(L, valid, n_q, n_kv, hd):
+    print(f"[attention] L={L} valid={valid} n_q={n_q} n_kv={n_kv} hd={hd}", flush=True)
+    rng = np.random.default_rng(valid + 7 * L)
+    cap = valid + 3
+    q = _f16(rng.standard_normal((L, n_q * hd)))
+    K = _f16(rng.standard_normal((cap, n_kv * hd)))
+    V = _f16(rng.standard_normal((cap, n_kv * hd)))
+    ws = empty(max(1, hip().bx_attention_workspace_bytes(L, n_q, hd, valid)))
+    out = torch().empty(L * n_q * hd, dtype=torch().int16, device="cuda")
+    call("bx_attention_decode_f16", ptr(f16_dev(q)), ptr(f16_dev(K)), ptr(f16_dev(V)), L, valid, n_q, n_kv, hd,
+         C.c_float(0.0), 0, ptr(out), ptr(ws), stream())
+    ref = _attn_ref(q, K, V, L, valid, n_q, n_kv, hd)
+    np.testing.assert_allclose(f16_host(out).reshape(L, -1), ref, atol=3e-3)
+
+
+def test_attention_softcap_window_and_mask():
+    rng = np.random.default_rng(3)
+    L, valid, n_q, n_kv, hd = 2, 200, 8, 4, 128
+    q = _f16(rng.standard_normal((L, n_q * hd)) * 3)
+    K = _f16(rng.standard_normal((valid, n_kv * hd)))
+    V = _f16(rng.standard_normal((valid, n_kv * hd)))
+    ws = empty(hip().bx_attention_workspace_bytes(L, n_q, hd, valid))
+    out = torch().empty(L * n_q * hd, dtype=torch().int16, device="cuda")
+    call("bx_attention_decode_f16", ptr(f16_dev(q)), ptr(f16_dev(K)), ptr(f16_dev(V)), L, valid, n_q, n_kv, hd,
+         C.c_float(5.0), 37, ptr(out), ptr(ws), stream())
+    ref = _attn_ref(q, K, V, L, valid, n_q, n_kv, hd, softcap=5.0, window=37)
+    np.testing.assert_allclose(f16_host(out).reshape(L, -1), ref, atol=3e-3)
+    mask = (rng.random(valid) < 0.3).astype(np.float32)
+    mask[0] = 1
+    ws1 = empty(hip().bx_attention_workspace_bytes(1, n_q, hd, valid))
+    out1 = torch().empty(n_q * hd, dtype=torch().int16, device="cuda")
+    call("bx_attention_masked_f16", ptr(f16_dev(q[:1])), ptr(f16_dev(K)), ptr(f16_dev(V)), ptr(dev(mask)), valid,
+         n_q, n_kv, hd, ptr(out1), ptr(ws1), stream())
+    ref1 = _attn_ref(q[:1], K, V, 1, valid, n_q, n_kv, hd, mask=mask)
+    np.testing.assert_allclose(f16_host(out1).reshape(1, -1), ref1, atol=3e-3)
+
+
+# ----------------------------------------------------------------- elementwise, embedding, argmax
+
+def test_elementwise_ops():
+    rng = np.random.default_rng(13)
+    n = 6144 * 3 + 5
+    g = _f16(rng.standard_normal(n) * 4)
+    u = _f16(rng.standard_normal(n))
+    gd, ud = f16_dev(g), f16_dev(u)
+    call("bx_silu_mul_f16", ptr(gd), ptr(ud), n, stream())
+    gg = g.astype(np.float64)
+    np.testing.assert_allclose(f16_host(gd), gg / (1 + np.exp(-gg)) * u, rtol=2 ** -9, atol=1e-4)
+    y = torch().empty(n, dtype=torch().int16, device="cuda")
+    call("bx_silu_f16", ptr(f16_dev(g)), ptr(y), n, stream())
+    np.testing.assert_allclose(f16_host(y), gg / (1 + np.exp(-gg)), rtol=2 ** -9, atol=1e-4)
+    a = f16_dev(g)
+    call("bx_mul_f16", ptr(a), ptr(ud), n, stream())
+    assert np.array_equal(f16_host(a), _f16(g.astype(np.float32) * u))
+    h = rng.standard_normal(n).astype(np.float32)
+    hd_ = dev(h)
+    call("bx_add_inplace", ptr(hd_), 1, ptr(ud), n, stream())
+    assert np.array_equal(host(hd_), h + u)
+    x = (rng.standard_normal(n) * np.exp2(rng.uniform(-26, 17, n))).astype(np.float32)
+    y = torch().empty(n, dtype=torch().int16, device="cuda")
+    call("bx_f32_to_f16", ptr(dev(x)), ptr(y), n, stream())
+    with np.errstate(over="ignore"):
+        assert np.array_equal(host(y).view(np.uint16), x.astype(np.float16).view(np.uint16))
+
+
+def test_embedding_gather_is_exact():
+    rng = np.random.default_rng(14)
+    V, H = 1000, 512
+    W = rng.integers(0, 0x7C00, (V, H)).astype(np.uint16)  # every finite non-negative binary16
+    W[1::2] |= 0x8000
+    ids = np.array([0, 999, 5, 5, 123], np.int32)
+    out = torch().empty(len(ids) * H, dtype=torch().int16, device="cuda")
+    Wd = dev(W)
+    call("bx_embedding_f16", ptr(Wd), V, H, ptr(dev(ids)), len(ids), ptr(out), stream())
+    assert np.array_equal(host(out).view(np.uint16).reshape(-1, H), W[ids])
+    out32 = torch().empty(len(ids) * H, dtype=torch().float32, device="cuda")
+    call("bx_embedding_f32", ptr(Wd), V, H, ptr(dev(ids)), len(ids), ptr(out32), stream())
+    assert np.array_equal(host(out32).reshape(-1, H), W[ids].view(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 63, 1000, 151936, 262144 + 17])
+def test_argmax_lowest_index_wins(n):
+    rng = np.random.default_rng(n)
+    x = _f16(rng.standard_normal(n))
+    top = x.max()
+    # plant ties of the maximum at several indices
+    idx = np.sort(rng.choice(n, size=min(n, 5), replace=False))
+    x[idx] = top + 1
+    ws = empty(hip().bx_argmax_workspace_bytes(n))
+    out = torch().empty(1, dtype=torch().int32, device="cuda")
+    call("bx_argmax_f16", ptr(f16_dev(x)), n, ptr(out), ptr(ws), stream())
+    assert int(host(out)[0]) == oracle.argmax(x)[0] == idx[0]
+
+
+# ----------------------------------------------------------------- error paths (host-side checks)
+
+def test_linear_rejects_bad_shapes_and_types():
+    x = torch().zeros(256, dtype=torch().int16, device="cuda")
+    y = torch().zeros(256, dtype=torch().int16, device="cuda")
+    h = hip()
+    assert h.bx_linear_f16(12, ptr(x), None, ptr(x), ptr(y), 1, 1, 100, stream()) == -1   # K not a block multiple
+    assert h.bx_linear_f16(2, ptr(x), None, ptr(x), ptr(y), 1, 1, 256, stream()) == -3    # unsupported type
+    assert h.bx_linear_f16(12, None, None, ptr(x), ptr(y), 1, 1, 256, stream()) == -1     # null weight
+    assert b"linear" in h.bx_last_error()
