@@ -76,27 +76,37 @@ def cpu_baseline(path: Path, vocab: int, prompt: list[int], seconds: float) -> d
     m = oracle.Model(str(path))
     load_s = time.time() - t0
     n_prompt = 32
-    m.allocate_cache(n_prompt + 256)
+    max_steps = 4096
+    m.allocate_cache(n_prompt + max_steps)
     t0 = time.time()
     lg = m.forward(prompt[:n_prompt], last_only=True)
     prefill_s = time.time() - t0
     tok, _ = oracle.argmax(lg[0])
     steps = 0
     t0 = time.time()
-    while steps < 256:
+    while steps < max_steps:
         lg = m.forward([tok], last_only=True)
         tok, _ = oracle.argmax(lg[0])
         steps += 1
         if time.time() - t0 > seconds:
             break
     dec_s = time.time() - t0
+    cpu = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {
-        "value": steps / dec_s,
+        "value": round(steps / dec_s, 3),
         "unit": "tok/s",
         "cores": oracle.num_threads(),
         "kind": "port",
         "sample": f"oracle FP32 decode of {steps} tokens after a {n_prompt}-token prefill "
-                  f"(prefill {prefill_s:.1f} s, weight dequant/load {load_s:.1f} s excluded)",
+                  f"(prefill {prefill_s:.1f} s, weight dequant/load {load_s:.1f} s excluded); "
+                  f"{oracle.num_threads()} OpenMP threads of {os.cpu_count()} visible, {cpu}",
     }
 
 
