@@ -157,6 +157,11 @@ class Qwen3Model:
     def decode_weight_bytes(self) -> int:
         return int(_native.lib().brolm_qwen3_decode_weight_bytes(self._h))
 
+    def decode_mode(self) -> str:
+        """Which single-token step path runs: "persistent", "graph" or "eager"."""
+        m = check(_native.lib().brolm_qwen3_decode_mode(self._h), "decode_mode")
+        return ("eager", "graph", "persistent")[m]
+
 
 @dataclass
 class SamplingParams:

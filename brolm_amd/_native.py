@@ -73,6 +73,11 @@ HIP_SYMBOLS = {
     "bx_decode_layer_run": (C.c_int, [C.POINTER(DecodeDimsC), vp, vp, vp, vp, vp, vp]),
     "bx_decode_head": (C.c_int, [C.POINTER(DecodeDimsC), vp, vp, vp, vp, vp]),
     "bx_decode_advance": (C.c_int, [vp, vp, vp, vp, vp, vp]),
+    "bx_persist_ws_bytes": (C.c_size_t, [C.POINTER(DecodeDimsC)]),
+    "bx_persist_step": (C.c_int, [C.POINTER(DecodeDimsC), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_uint32,
+                                  vp]),
+    "bx_persist_status": (C.c_int, [vp, C.POINTER(C.c_uint32)]),
+    "bx_persist_trace": (C.c_int, [vp, C.c_int]),
     "bx_argmax_workspace_bytes": (C.c_size_t, [i64]),
     "bx_argmax_f16": (C.c_int, [vp, i64, vp, vp, vp]),
 }
@@ -105,6 +110,7 @@ C_SYMBOLS = {
     "brolm_qwen3_decode_greedy": (C.c_int, [vp, i32, C.c_int, P_i32, C.c_int]),
     "brolm_qwen3_time_decode_steps": (f64, [vp, i32, C.c_int]),
     "brolm_qwen3_decode_weight_bytes": (i64, [vp]),
+    "brolm_qwen3_decode_mode": (C.c_int, [vp]),
     "brolm_sample_token": (C.c_int, [P_f32, C.c_int, f32, C.c_int, f32, u64]),
     "brolm_prompt_ids": (C.c_int, [u64, C.c_int, C.c_int, P_i32]),
     "brolm_profile_reset": (None, []),

@@ -254,6 +254,12 @@ int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m) {
     return (m && m->model) ? const_cast<brolm::qwen::Qwen3Model&>(*m->model).core().decode_weight_bytes() : -1;
 }
 
+int brolm_qwen3_decode_mode(brolm_qwen3* m) {
+    int mode = -1;
+    const int rc = guard([&] { mode = model_of(m).core().decode_mode(); });
+    return rc == 0 ? mode : -1;
+}
+
 int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed) {
     brolm::detail::SamplingParams p;
     p.temperature = temperature;

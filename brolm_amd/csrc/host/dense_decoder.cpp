@@ -67,9 +67,17 @@ struct DecodeGraphSession {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
+    // persistent single-launch step (bx_persist_step), used when it covers the shape
+    bool use_persist = false;
+    void* pws = nullptr;
+    std::size_t pws_bytes = 0;
+    bx_decode_layer* layers_dev = nullptr;
+    uint32_t epoch = 0;
 
     ~DecodeGraphSession() {
         (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
+        if (pws) (void)hipFree(pws);
+        if (layers_dev) (void)hipFree(layers_dev);
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
         if (staged) (void)hipEventDestroy(staged);
@@ -379,6 +387,18 @@ DecodeGraphSession& DenseDecoder::session_() {
                 "hipHostMalloc");
     hipx::check(hipEventCreateWithFlags(&s->staged, hipEventDisableTiming), "hipEventCreate");
     s->use_graph = !env_flag("BROLM_NO_GRAPH");
+    if (s->use_graph && !env_flag("BROLM_NO_PERSIST")) {
+        s->pws_bytes = bx_persist_ws_bytes(&d);
+        if (s->pws_bytes != 0) {
+            hipx::check(hipMalloc(&s->pws, s->pws_bytes), "hipMalloc persist ws");
+            hipx::check(hipMemsetAsync(s->pws, 0, s->pws_bytes, hipx::stream()), "memset persist ws");
+            const std::size_t lb = s->layers.size() * sizeof(bx_decode_layer);
+            hipx::check(hipMalloc(reinterpret_cast<void**>(&s->layers_dev), lb), "hipMalloc layer table");
+            hipx::check(hipMemcpyAsync(s->layers_dev, s->layers.data(), lb, hipMemcpyHostToDevice, hipx::stream()),
+                        "upload layer table");
+            s->use_persist = true;
+        }
+    }
     hipx::sync();
     graph_ = std::move(s);
     return *graph_;
@@ -416,8 +436,41 @@ static void stage_step(DecodeGraphSession& s, int32_t token, int32_t pos) {
     hipx::check(hipEventRecord(s.staged, hipx::stream()), "hipEventRecord");
 }
 
+static void launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
+                           const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
+    if (++s.epoch >= (1u << 22)) {  // tags ran out: clear the words and restart
+        hipx::check(hipMemsetAsync(s.pws, 0, s.pws_bytes, hipx::stream()), "memset persist ws");
+        s.epoch = 1;
+    }
+    hipx::bx(bx_persist_step(&s.dims, static_cast<int>(s.layers.size()), s.layers_dev,
+                             static_cast<const uint16_t*>(embed.data), static_cast<const uint16_t*>(final_norm.data),
+                             lm_head.data, static_cast<const float*>(cos.data), static_cast<const float*>(sin.data),
+                             s.scal, s.logits, s.pws, s.epoch, bt::stream()),
+             "persist step");
+}
+
+// After the launches completed: a persistent step that gave up on a wait
+// leaves its abort flag set.
+static void check_persist(DecodeGraphSession& s) {
+    if (!s.use_persist) return;
+    hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
+    uint32_t site = 0;
+    const int st = bx_persist_status(s.pws, &site);
+    if (st < 0) hipx::bx(st, "persist status");
+    if (st == 1) {
+        // the words now hold a partial step: clear them so the next step starts clean
+        hipx::check(hipMemset(s.pws, 0, s.pws_bytes), "memset persist ws");
+        s.epoch = 0;
+        fail("persistent decode step aborted waiting at site " + std::to_string(site));
+    }
+}
+
 static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, const bt::Tensor& final_norm,
                          const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
+    if (s.use_persist) {
+        for (int i = 0; i < n; ++i) launch_persist(s, embed, final_norm, lm_head, cos, sin);
+        return;
+    }
     if (s.use_graph && !s.exec) {
         hipStream_t st = hipx::stream();
         hipx::check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -446,6 +499,7 @@ void DenseDecoder::decode_step_(int32_t token, bt::Tensor& logits_out) {
     hipx::check(hipMemcpyAsync(logits_out.data, s.logits, static_cast<std::size_t>(cfg_.vocab_size) * 2,
                                hipMemcpyDeviceToDevice, hipx::stream()),
                 "copy logits");
+    check_persist(s);
     cache_len_ += 1;
 }
 
@@ -460,6 +514,7 @@ int DenseDecoder::decode_greedy(int32_t token, int n, int32_t* out, int eos_id) 
         const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
         stage_step(s, cur, cache_len_);
         launch_steps(s, chunk, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+        check_persist(s);
         hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
         for (int i = 0; i < chunk; ++i) {
             if (eos_id >= 0 && out[done + i] == eos_id) {
@@ -493,8 +548,16 @@ double DenseDecoder::time_decode_steps(int32_t token, int n) {
     hipx::check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    check_persist(s);
     cache_len_ += n;
     return static_cast<double>(ms) / n;
+}
+
+int DenseDecoder::decode_mode() {
+    if (embed_tokens_.size() == 0) fail("decode_mode: weights not loaded");
+    if (max_seq_len_ == 0) fail("decode_mode: cache not allocated");
+    DecodeGraphSession& s = session_();
+    return s.use_persist ? 2 : (s.use_graph ? 1 : 0);
 }
 
 std::int64_t DenseDecoder::decode_weight_bytes() const {

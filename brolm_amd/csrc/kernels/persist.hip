@@ -1,0 +1,1180 @@
+// Persistent single-launch decode step.
+//
+// The whole L = 1 step of src/detail/dense_decoder.cpp:439-496 (run_layers_,
+// :526-681, at one token) — embedding, every layer, final norm, lm_head,
+// greedy argmax and the token feedback — runs as ONE cooperative launch with
+// one workgroup per CU.  Stages that the multi-kernel step separates with a
+// kernel boundary are separated here by dataflow: every vector a stage hands
+// to the next is written as 64-bit words {value bits, tag} with device-scope
+// relaxed atomic stores, and consumers poll those words (device-scope relaxed
+// atomic loads, coherent across XCDs) until every tag equals the tag of the
+// (step, layer, stage) they wait for.  Tags grow monotonically with the
+// launch epoch, so buffers are never cleared between steps.  A poll gives up
+// after a bounded number of rounds and raises a shared abort flag that every
+// other poll checks, so all waves leave the kernel on any failure.
+//
+// Per layer (WG w of G):
+//   A  rms_norm(h) -> rows of [Wq; Wk; Wv] (segments spread over G by bytes)
+//   B  WGs (group g, split s): QK-norm, RoPE, KV-cache write of position pos,
+//      split-K attention partial over keys [kb, ke); split 0 of each group
+//      combines the partials of its group -> FP16 attention output
+//   C  rows of Wo owned by w (H/G rows) + residual kept in the WG's LDS
+//   D  rms_norm(h) -> gate/up row pairs -> FP16 silu(g)*u
+//   E  rows of Wd owned by w + residual
+// Head: rms_norm(h) -> lm_head rows -> FP16 logits + per-WG argmax; WG 0
+// reduces the candidates (lowest index on ties) and advances tok/pos.
+#include <cmath>
+
+#include "gemv_core.h"
+
+namespace bx {
+namespace {
+
+constexpr int kPT = 256;            // threads per workgroup
+constexpr int kPW = kPT / 64;       // waves
+constexpr int kMaxGq = 8;           // query heads per KV head
+constexpr int kTile = 128;          // keys per attention tile
+constexpr int kMaxOwn = 64;         // residual rows owned per WG
+constexpr uint32_t kSpinCheck = 128;        // poll rounds between abort checks
+constexpr uint32_t kSpinLimit = 1u << 21;   // poll rounds before giving up (~1 s)
+constexpr int kTraceSlots = 1024;           // per WG: 1 + 10 per layer + 4
+
+struct PArgs {
+    int H, F, n_q, n_kv, hd, V, cap, L;
+    float eps;
+    int g_q, g_k;                    // WGs of the q and k segments of stage A (v gets the rest)
+    uint32_t epoch;
+    const bx_decode_layer* layers;   // device array of L layers
+    const uint16_t* embed;
+    const uint16_t* final_norm;
+    const void* lm_head;
+    const float* cos_t;
+    const float* sin_t;
+    int32_t* scal;                   // tok, pos, next, count, hist[...]
+    uint16_t* logits;
+    uint32_t* ctrl;                  // [0] abort flag, [1] failure site
+    uint64_t* hbuf;                  // H words: FP32 residual
+    uint64_t* qkv;                   // qd + 2 kvd words: FP32 GEMV outputs
+    uint64_t* attn;                  // qd / 2 words: FP16 pairs
+    uint64_t* act;                   // F / 2 words: FP16 pairs
+    uint64_t* part;                  // n_kv * Smax * Gq * (hd + 2) words: FP32 split records
+    uint64_t* cand;                  // 2 G words: per-WG argmax value / index
+    uint64_t* trace;                 // optional wall-clock stamps [G][kTraceSlots] (bx_persist_trace)
+};
+
+__device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_word(uint64_t* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t tag_of(const PArgs& a, int layer, int stage) {
+    return a.epoch * 1024u + (uint32_t)layer * 8u + (uint32_t)stage;
+}
+
+// The thread index through an opaque move: values derived from it (per-lane
+// addresses) cannot be hoisted out of the layer loop, where dozens of them
+// would outlive the register file and spill.
+__device__ __forceinline__ int tidx() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
+
+// A zero the compiler cannot see through.  Added to the per-lane address
+// terms inside the layer loop, it keeps those addresses from being hoisted
+// out of the loop, where dozens of loop-invariant 64-bit addresses would
+// outlive the register file and spill.
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    return z;
+}
+
+// Wall-clock stamp of a stage boundary (thread 0) when tracing is on.
+__device__ __forceinline__ void stamp(const PArgs& a, int slot) {
+    if (a.trace && tidx() == 0) a.trace[(size_t)blockIdx.x * kTraceSlots + slot] = wall_clock64();
+}
+
+__device__ __forceinline__ bool aborted(const PArgs& a) {
+    return __hip_atomic_load(a.ctrl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+__device__ __forceinline__ void raise_abort(const PArgs& a, uint32_t site) {
+    __hip_atomic_store(a.ctrl + 1, site, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.ctrl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll words [0, n) of buf (thread t owns t, t + kPT, ...), E in flight per
+// thread; sink(i, value) for each word once its tag matches.  false on abort.
+template <int E, class Sink>
+__device__ __forceinline__ bool poll_words(const PArgs& a, const uint64_t* buf, int n, uint32_t tag, uint32_t site,
+                                           Sink sink) {
+    for (int base = 0; base < n; base += E * kPT) {
+        uint32_t pend = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (base + tidx() + e * kPT < n) pend |= 1u << e;
+        uint32_t rounds = 0;
+        while (pend) {
+            uint64_t w[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if (pend & (1u << e)) w[e] = ld_word(buf + base + tidx() + e * kPT);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if ((pend & (1u << e)) && (uint32_t)(w[e] >> 32) == tag) {
+                    pend &= ~(1u << e);
+                    sink(base + tidx() + e * kPT, (uint32_t)w[e]);
+                }
+            }
+            if (pend) {
+                ++rounds;
+                if (rounds % kSpinCheck == 0) {
+                    if (aborted(a)) return false;
+                    if (rounds >= kSpinLimit) {
+                        raise_abort(a, site);
+                        return false;
+                    }
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    return true;
+}
+
+// ---- LDS arena -------------------------------------------------------------
+
+struct Arena {
+    uint32_t* xs;     // swizzled FP16 pairs, Kmax / 2
+    float* xsum;      // Kmax / 16
+    float* hv;        // H (full residual for the norms)
+    float* own;       // kMaxOwn residual rows owned by this WG
+    float* red;       // 64 reduction scratch
+    float* att;       // attention scratch (see attention_stage)
+};
+
+__host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq);
+
+__host__ __device__ inline size_t arena_bytes(int H, int F, int qd, int hd, int Gq) {
+    const int kmax = H > F ? (H > qd ? H : qd) : (F > qd ? F : qd);
+    return (size_t)kmax * 2 + (size_t)(kmax / 16) * 4 + (size_t)H * 4 + kMaxOwn * 4 + 64 * 4 +
+           att_scratch_bytes(hd, Gq);
+}
+
+__device__ __forceinline__ Arena make_arena(unsigned char* base, int H, int F, int qd) {
+    const int kmax = H > F ? (H > qd ? H : qd) : (F > qd ? F : qd);
+    Arena r;
+    size_t o = 0;
+    r.xs = reinterpret_cast<uint32_t*>(base + o); o += (size_t)kmax * 2;
+    r.xsum = reinterpret_cast<float*>(base + o); o += (size_t)(kmax / 16) * 4;
+    r.hv = reinterpret_cast<float*>(base + o); o += (size_t)H * 4;
+    r.own = reinterpret_cast<float*>(base + o); o += kMaxOwn * 4;
+    r.red = reinterpret_cast<float*>(base + o); o += 64 * 4;
+    r.att = reinterpret_cast<float*>(base + o);
+    return r;
+}
+
+__device__ __forceinline__ float block_sum_p(float v, float* red) {
+    v = wave_allsum(v);
+    const int wave = tidx() >> 6;
+    __syncthreads();
+    if ((tidx() & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPW; ++i) s += red[i];
+    return s;
+}
+
+// A norm's FP16 gamma, groups g = t + kPT i of 4 values, loaded into registers
+// before the normalized vector's input arrives.
+constexpr int kGammaRegs = 4;   // hidden <= 4 * 4 * kPT
+struct GammaRegs {
+    u2v v[kGammaRegs];
+    __device__ __forceinline__ void load(const void* gamma, int K) {
+#pragma unroll
+        for (int i = 0; i < kGammaRegs; ++i) {
+            const int g = tidx() + i * kPT;
+            if (4 * g < K) v[i] = reinterpret_cast<const u2v*>(gamma)[g];
+        }
+    }
+};
+
+// rms_norm of hv (FP32, K) with FP16 gamma -> swizzled FP16 xs + 16-sums.
+__device__ __forceinline__ void norm_to_xs(const Arena& ar, const GammaRegs& gam, float eps, int K) {
+    float ss = 0.f;
+    for (int i = tidx(); i < K; i += kPT) ss += ar.hv[i] * ar.hv[i];
+    ss = block_sum_p(ss, ar.red);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < kGammaRegs; ++i) {
+        const int g = tidx() + i * kPT;
+        if (4 * g < K) {
+            const float4 v = *reinterpret_cast<const float4*>(ar.hv + 4 * g);
+            const u2v gm = gam.v[i];
+            store_group<true>(ar.xs, g, f2h(v.x * inv * h2f(gm.x & 0xffff)), f2h(v.y * inv * h2f(gm.x >> 16)),
+                              f2h(v.z * inv * h2f(gm.y & 0xffff)), f2h(v.w * inv * h2f(gm.y >> 16)));
+        }
+    }
+    __syncthreads();
+    sums_from_lds(ar.xs, 1, K, K / 2, ar.xsum, K / 16);
+    __syncthreads();
+}
+
+// Poll FP16-pair words (K / 2 of them) into the swizzled xs + 16-sums.
+template <int E>
+__device__ __forceinline__ bool poll_pairs_to_xs(const PArgs& a, const Arena& ar, const uint64_t* buf, int K, uint32_t tag,
+                                 uint32_t site) {
+    const bool ok = poll_words<E>(a, buf, K / 2, tag, site, [&](int i, uint32_t v) {
+        // pair i holds x[2i], x[2i+1]; group g = i / 2 of 4 elements
+        const int g = i >> 1;
+        uint32_t* row = ar.xs + 2 * g;
+        uint16_t* h16 = reinterpret_cast<uint16_t*>(row);
+        // swizzled: dword 2g = (x0, x2), dword 2g+1 = (x1, x3)
+        if (i & 1) { h16[1] = (uint16_t)(v & 0xffff); h16[3] = (uint16_t)(v >> 16); }   // x2, x3
+        else { h16[0] = (uint16_t)(v & 0xffff); h16[2] = (uint16_t)(v >> 16); }         // x0, x1
+    });
+    if (!__syncthreads_and(ok)) return false;
+    sums_from_lds(ar.xs, 1, K, K / 2, ar.xsum, K / 16);
+    __syncthreads();
+    return true;
+}
+
+// R rows x UPL units of one matrix held in a wave's registers: loaded ahead
+// of the activation they meet (the weights do not depend on it), dotted later.
+template <int FMT, int UPL, int R>
+struct RowBlock {
+    typename RawOf<FMT>::T raw[R][UPL];
+
+    // Every load is issued unconditionally (rows and units clamped into the
+    // matrix, the extras ignored by dot): the compiler then counts the loads in
+    // flight exactly and waits only for the ones a later use needs, not for
+    // loads issued after these.
+    __device__ __forceinline__ void load(const void* W, int64_t N, int K, int64_t row0) {
+        const int lane = tidx() & 63;
+        const int U = K / 32;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+            if (row < 0) row = 0;
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = lane + 64 * i;
+                raw[rr][i] = load_unit<FMT>(W, N, K, row, u < U ? u : U - 1);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void dot(int K, const XCache<FMT, UPL>& xu, float (&out)[R]) const {
+        const int lane = tidx() & 63;
+        const int U = K / 32;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < UPL; ++i) {
+                const int u = lane + 64 * i;
+                if (u < U) acc += dot_reg(raw[rr][i], u, xu.get(i, u));
+            }
+            out[rr] = wave_allsum(acc);
+        }
+    }
+};
+
+// Rows [r0, r1) of W (N x K): wave w takes tasks of R rows starting at
+// r0 + w R with stride kPW R.  prefetch() loads the first task before the
+// caller waits for the activation; finish() computes every task (later tasks
+// load in turn) and calls epi(row, value) on lane 0.
+template <int FMT, int UPL, int R>
+struct WgRows {
+    RowBlock<FMT, UPL, R> blk;
+    int first;
+
+    __device__ __forceinline__ void prefetch(const void* W, int64_t N, int K, int r0, int r1) {
+        first = r0 + (int)(tidx() >> 6) * R;
+        if (first < r1) blk.load(W, N, K, first);
+    }
+
+    template <class Epi>
+    __device__ __forceinline__ void finish(const void* W, int64_t N, int K, int r1, const Arena& ar, Epi epi) {
+        if (first >= r1) return;
+        const int lane = tidx() & 63;
+        XCache<FMT, UPL> xu;
+        xu.init(ar.xs, ar.xsum, K);
+        for (int t = first; t < r1; t += kPW * R) {
+            if (t != first) blk.load(W, N, K, t);
+            float o[R];
+            blk.dot(K, xu, o);
+            if (lane == 0) {
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr)
+                    if (t + rr < r1) epi(t + rr, o[rr]);
+            }
+        }
+    }
+};
+
+// lm_head rows [r0, r1): two blocks in flight per wave, the next task's loads
+// issued before the current task's math.  The first task is loaded by the
+// caller (before the final norm's input arrives).
+template <int FMT, int UPL, int R, class Epi>
+__device__ __forceinline__ void head_rows(RowBlock<FMT, UPL, R>& b0, RowBlock<FMT, UPL, R>& b1, const void* W,
+                                          int64_t N, int K, int r0, int r1, const Arena& ar, Epi epi) {
+    const int lane = tidx() & 63;
+    const int step = kPW * R;
+    XCache<FMT, UPL> xu;
+    xu.init(ar.xs, ar.xsum, K);
+    auto emit = [&](int t, const float (&o)[R]) {
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr)
+                if (t + rr < r1) epi(t + rr, o[rr]);
+        }
+    };
+    for (int t = r0 + (int)(tidx() >> 6) * R; t < r1; t += 2 * step) {
+        const int t1 = t + step;
+        if (t1 < r1) b1.load(W, N, K, t1);
+        float o[R];
+        b0.dot(K, xu, o);
+        emit(t, o);
+        if (t1 >= r1) break;
+        const int t2 = t1 + step;
+        if (t2 < r1) b0.load(W, N, K, t2);
+        b1.dot(K, xu, o);
+        emit(t1, o);
+    }
+}
+
+__device__ __forceinline__ void range_of(int n, int parts, int i, int& b, int& e) {
+    b = (int)((int64_t)n * i / parts);
+    e = (int)((int64_t)n * (i + 1) / parts);
+}
+
+// ---- attention (stage B) ---------------------------------------------------
+
+// Keys per split and split count for context length n: splits <= smax, keys
+// a multiple of kSplitQ (short splits keep each workgroup's chain short).
+constexpr int kSplitQ = 16;
+__device__ __forceinline__ void split_plan(int n, int smax, int& kps, int& S) {
+    kps = (n + smax - 1) / smax;
+    kps = (kps + kSplitQ - 1) / kSplitQ * kSplitQ;
+    if (kps < kSplitQ) kps = kSplitQ;
+    S = (n + kps - 1) / kps;
+}
+
+// Head dims each of a group's combining WGs merges: an even count so output
+// pairs stay whole; ceil(hd / dsl) <= S combiners.
+__device__ __forceinline__ int comb_slice(int hd, int S) { return 2 * ((hd / 2 + S - 1) / S); }
+
+// Attention scratch inside the arena (host and device agree on this size).
+__host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq) {
+    return (size_t)Gq * hd * 6             // q16 pairs, qraw
+           + (size_t)hd * 12               // kraw, vraw, kcur, vcur
+           + (size_t)kTile * hd * 4        // kt, vt
+           + (size_t)Gq * kTile * 6        // sc, p16
+           + (size_t)Gq * 12               // mrun, lrun, alph
+           + (size_t)kPT * 8               // slice partials
+           + 256;
+}
+
+// HBM -> LDS copies (global_load_lds_dwordx4): lane L of a wave writes the 16
+// bytes at its own source address to lds_base + 16 L.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// Keys [c0, c0 + nk) of one KV head into LDS: K with its 16-byte chunks XOR-
+// swizzled by the key (chunk d8 of key j at position d8 ^ (j mod HD/8), so
+// lanes reading consecutive keys hit distinct banks), V in natural order.
+// Slots past nk in the last copy repeat key nk - 1 (in bounds, finite).
+template <int HD>
+__device__ __forceinline__ void dma_tile(const uint16_t* Kc, const uint16_t* Vc, int64_t kvd, int64_t krow0, int c0,
+                                         int nk, uint16_t* kt, uint16_t* vt) {
+    constexpr int CPK = HD / 8;
+    const int ninst = (nk * CPK + 63) / 64;
+    const int wave = tidx() >> 6, lane = tidx() & 63;
+    for (int i = wave; i < ninst; i += kPW) {
+        const int slot = 64 * i + lane;
+        int j = slot / CPK;
+        const int pc = slot % CPK;
+        if (j >= nk) j = nk - 1;
+        const int64_t row = (int64_t)(c0 + j) * kvd + krow0;
+        dma16(Kc + row + 8 * (pc ^ (j & (CPK - 1))), kt + 512 * i);
+        dma16(Vc + row + 8 * pc, vt + 512 * i);
+    }
+}
+
+// Words of the split records per KV group (any S <= smax).
+__host__ __device__ inline size_t part_words_per_group(int hd, int Gq, int smax) {
+    return (size_t)(smax + 1) * Gq * (2 * hd + 4 * smax + 4);
+}
+
+// Per-lane static vectors of one head row (pairs p = lane + 64 i): q_norm and
+// k_norm gamma pairs, RoPE cos / sin of row pos.  Loaded before q is ready.
+template <int HD>
+struct RopeRegs {
+    static constexpr int kP = (HD / 2 + 63) / 64;
+    uint32_t qg[kP], kg[kP];
+    float c[kP], s[kP];
+    __device__ __forceinline__ void load(const bx_decode_layer& Ly, const float* cos_row, const float* sin_row) {
+        const int lane = tidx() & 63;
+#pragma unroll
+        for (int i = 0; i < kP; ++i) {
+            const int p = lane + 64 * i;
+            if (p < HD / 2) {
+                qg[i] = static_cast<const uint32_t*>(Ly.q_norm)[p];
+                kg[i] = static_cast<const uint32_t*>(Ly.k_norm)[p];
+                c[i] = cos_row[p];
+                s[i] = sin_row[p];
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ float r16(float x) { return h2f(f2h(x)); }
+__device__ __forceinline__ uint32_t pack16(float lo, float hi) {
+    return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+}
+
+// RMSNorm of one HD-long FP32 head (one wave) with gamma pairs gm, RoPE with
+// the lane's cos/sin, FP16 rounding after each step as the op path stores
+// them (q/k-norm into FP16, RoPE in place on FP16) -> FP16 pairs at dst.
+template <int HD>
+__device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t (&gm)[RopeRegs<HD>::kP],
+                                               const RopeRegs<HD>& rr, float eps, uint32_t* dst) {
+    const int lane = tidx() & 63;
+    constexpr int kP = RopeRegs<HD>::kP;
+    float x0[kP], x1[kP];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kP; ++i) {
+        const int p = lane + 64 * i;
+        x0[i] = x1[i] = 0.f;
+        if (p < HD / 2) {
+            x0[i] = src[2 * p];
+            x1[i] = src[2 * p + 1];
+            ss += x0[i] * x0[i] + x1[i] * x1[i];
+        }
+    }
+    ss = wave_allsum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int i = 0; i < kP; ++i) {
+        const int p = lane + 64 * i;
+        if (p < HD / 2) {
+            const float a0 = r16(x0[i] * inv * h2f(gm[i] & 0xffff));
+            const float a1 = r16(x1[i] * inv * h2f(gm[i] >> 16));
+            dst[p] = pack16(a0 * rr.c[i] - a1 * rr.s[i], a0 * rr.s[i] + a1 * rr.c[i]);
+        }
+    }
+}
+
+// Stage B for (KV group g, split s) = (w % n_kv, w / n_kv).  The first tile of
+// cached keys / values and the static per-row vectors are requested before q
+// is polled.  Scores: FP16 q . K via v_dot2 over all waves, scaled in FP32;
+// softmax per head with the running max / sum across tiles; P.V via v_dot2
+// over key pairs (V staged as (v_2j[d], v_2j+1[d]) pairs).  Each split writes
+// its record in ncomb slices of head dims; split c < ncomb merges slice c of
+// all splits and writes those dims of the group's FP16 attention output.
+template <int HD>
+__device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar, const bx_decode_layer& Ly,
+                                                int layer, int pos, int zl) {
+    constexpr int CPK = HD / 8;                     // 16-byte chunks per key row
+    constexpr int kMaxItems = 4;                    // Gq * HD / 2 <= kPT * kMaxItems
+    const int G = gridDim.x, w = blockIdx.x;
+    const int Gq = a.n_q / a.n_kv, qd = a.n_q * HD, kvd = a.n_kv * HD;
+    const int smax = G / a.n_kv;
+    const int g = w % a.n_kv, s = w / a.n_kv;
+    if (s >= smax) return true;
+    int kps, S;
+    split_plan(pos + 1, smax, kps, S);
+    if (s >= S) return true;
+    const int kb = s * kps + zl, ke = min(pos + 1, kb + kps);
+    const bool has_cur = ke == pos + 1;
+    const int wave = tidx() >> 6, lane = tidx() & 63;
+    const uint32_t tin = tag_of(a, layer, 0), tout = tag_of(a, layer, 1);
+    if (layer == 14) stamp(a, 900 + 0);
+
+    uint32_t* q16 = reinterpret_cast<uint32_t*>(ar.att);          // Gq * HD/2
+    float* qraw = ar.att + Gq * HD / 2;                            // Gq * HD
+    float* kraw = qraw + Gq * HD;                                  // HD
+    float* vraw = kraw + HD;                                       // HD
+    uint32_t* kcur = reinterpret_cast<uint32_t*>(vraw + HD);      // HD/2
+    uint32_t* vcur = kcur + HD / 2;                                // HD/2
+    uint16_t* kt = reinterpret_cast<uint16_t*>(vcur + HD / 2);    // kTile x HD, 16-byte chunks XOR-swizzled
+    uint16_t* vt = kt + kTile * HD;                                // kTile x HD
+    float* sc = reinterpret_cast<float*>(vt + kTile * HD);        // Gq x kTile
+    uint32_t* p16 = reinterpret_cast<uint32_t*>(sc + Gq * kTile); // Gq x kTile/2
+    float* mrun = reinterpret_cast<float*>(p16 + Gq * kTile / 2); // Gq
+    float* lrun = mrun + Gq;
+    float* alph = lrun + Gq;
+    float* osl = alph + Gq;                                        // 2 kPT
+
+    const uint16_t* Kc = static_cast<const uint16_t*>(Ly.Kc);
+    const uint16_t* Vc = static_cast<const uint16_t*>(Ly.Vc);
+    const int64_t krow0 = (int64_t)g * HD;
+    // the first tile of cached rows goes straight to LDS while q is computed elsewhere
+    dma_tile<HD>(Kc, Vc, kvd, krow0, kb, min(kTile, ke - kb), kt, vt);
+    RopeRegs<HD> rr;
+    rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2));
+    if (layer == 14) stamp(a, 900 + 1);
+
+    // q rows of the group's heads, then (split holding pos) k and v rows.  Each
+    // wave's polls complete after its own tile copies (in-order counters).
+    bool ok = poll_words<4>(a, a.qkv + zl + (int64_t)g * Gq * HD, Gq * HD, tin, 10,
+                            [&](int i, uint32_t v) { qraw[i] = __uint_as_float(v); });
+    if (ok && has_cur) {
+        ok = poll_words<1>(a, a.qkv + zl + qd + krow0, HD, tin, 11,
+                           [&](int i, uint32_t v) { kraw[i] = __uint_as_float(v); });
+        if (ok)
+            ok = poll_words<1>(a, a.qkv + zl + qd + kvd + krow0, HD, tin, 12,
+                               [&](int i, uint32_t v) { vraw[i] = __uint_as_float(v); });
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // tile copies of this wave landed (also without polls)
+    if (!__syncthreads_and(ok)) return false;
+    if (layer == 14) stamp(a, 900 + 2);
+
+    for (int h = wave; h < Gq; h += kPW) norm_rope_head<HD>(qraw + h * HD, rr.qg, rr, a.eps, q16 + h * HD / 2);
+    if (has_cur && wave == kPW - 1) {
+        norm_rope_head<HD>(kraw, rr.kg, rr, a.eps, kcur);
+        for (int p = lane; p < HD / 2; p += 64) vcur[p] = pack16(vraw[2 * p], vraw[2 * p + 1]);
+    }
+    if (tidx() < Gq) {
+        mrun[tidx()] = -INFINITY;
+        lrun[tidx()] = 0.f;
+    }
+    __syncthreads();
+    if (has_cur) {
+        uint16_t* Kw = static_cast<uint16_t*>(Ly.Kc);
+        uint16_t* Vw = static_cast<uint16_t*>(Ly.Vc);
+        for (int p = tidx(); p < HD / 2; p += kPT) {
+            reinterpret_cast<uint32_t*>(Kw + (int64_t)pos * kvd + krow0)[p] = kcur[p];
+            reinterpret_cast<uint32_t*>(Vw + (int64_t)pos * kvd + krow0)[p] = vcur[p];
+        }
+    }
+
+    // P.V items (head, dim pair) x key-pair slices
+    const int items = Gq * HD / 2;
+    const int nsl = items < kPT ? kPT / items : 1;
+    const int sl = items < kPT ? tidx() / items : 0;
+    const bool pv_on = tidx() < (items < kPT ? items * nsl : kPT);
+    float o0[kMaxItems], o1[kMaxItems];
+#pragma unroll
+    for (int i = 0; i < kMaxItems; ++i) o0[i] = o1[i] = 0.f;
+    const float scale = 1.0f / sqrtf((float)HD);
+
+    int ti = 0;
+    for (int c0 = kb; c0 < ke; c0 += kTile, ++ti) {
+        const int nk = min(kTile, ke - c0);
+        if (ti > 0) {   // later tiles (splits longer than one tile)
+            __syncthreads();
+            dma_tile<HD>(Kc, Vc, kvd, krow0, c0, nk, kt, vt);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        // the current key / value replace the stale cache row pos in the tile
+        if (pos >= c0 && pos < c0 + nk) {
+            const int j = pos - c0;
+            for (int d8 = tidx(); d8 < CPK; d8 += kPT) {
+                *reinterpret_cast<u4v*>(kt + j * HD + 8 * (d8 ^ (j & (CPK - 1)))) =
+                    *reinterpret_cast<const u4v*>(kcur + 4 * d8);
+                *reinterpret_cast<u4v*>(vt + j * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vcur + 4 * d8);
+            }
+        }
+        __syncthreads();
+        if (layer == 14 && ti == 0) stamp(a, 900 + 3);
+        // scores of (head, key) items over all threads
+        for (int it = tidx(); it < Gq * kTile; it += kPT) {
+            const int h = it / kTile, j = it % kTile;
+            float acc = -INFINITY;
+            if (j < nk) {
+                const uint32_t* q = q16 + h * HD / 2;
+                const uint16_t* kr = kt + j * HD;
+                acc = 0.f;
+#pragma unroll
+                for (int d8 = 0; d8 < CPK; ++d8) {
+                    const u4v kk = *reinterpret_cast<const u4v*>(kr + 8 * (d8 ^ (j & (CPK - 1))));
+                    const u4v qq = *reinterpret_cast<const u4v*>(q + 4 * d8);
+                    acc = dot2(qq.x, kk.x, acc);
+                    acc = dot2(qq.y, kk.y, acc);
+                    acc = dot2(qq.z, kk.z, acc);
+                    acc = dot2(qq.w, kk.w, acc);
+                }
+                acc *= scale;
+            }
+            sc[it] = acc;
+        }
+        __syncthreads();
+        // softmax update per head: lane owns keys 2 lane, 2 lane + 1 (kTile = 128)
+        for (int h = wave; h < Gq; h += kPW) {
+            const float s0 = sc[h * kTile + 2 * lane], s1 = sc[h * kTile + 2 * lane + 1];
+            const float mc = wave_max(fmaxf(s0, s1));
+            const float mo = mrun[h];
+            const float mn = fmaxf(mo, mc);
+            const float p0 = 2 * lane < nk ? r16(__expf(s0 - mn)) : 0.f;
+            const float p1 = 2 * lane + 1 < nk ? r16(__expf(s1 - mn)) : 0.f;
+            const float ps = wave_allsum(p0 + p1);
+            p16[h * kTile / 2 + lane] = pack16(p0, p1);
+            if (lane == 0) {
+                const float al = mo == -INFINITY ? 0.f : __expf(mo - mn);
+                alph[h] = al;
+                lrun[h] = lrun[h] * al + ps;
+                mrun[h] = mn;
+            }
+        }
+        __syncthreads();
+        // P.V: (p_2j, p_2j+1) . (v_2j[d], v_2j+1[d]) by v_dot2 on v_perm-paired rows.
+        // The row past nk (odd nk) is a copy of row nk - 1, which in the split
+        // holding pos is the cache row not written yet: read as zero.
+        if (pv_on) {
+            const int npair = (nk + 1) / 2;
+#pragma unroll
+            for (int i = 0; i < kMaxItems; ++i) {
+                const int idx = items < kPT ? tidx() % items : tidx() + i * kPT;
+                if ((items < kPT && i == 0) || (items >= kPT && idx < items)) {
+                    const int h = idx / (HD / 2), dp = idx % (HD / 2);
+                    const uint32_t* pp = p16 + h * kTile / 2;
+                    const float al = alph[h];
+                    float a0 = o0[i] * al, a1 = o1[i] * al;
+#pragma unroll 8
+                    for (int jp = sl; jp < npair; jp += nsl) {
+                        const uint32_t v0 = *reinterpret_cast<const uint32_t*>(vt + (2 * jp) * HD + 2 * dp);
+                        const uint32_t v1 =
+                            2 * jp + 1 < nk ? *reinterpret_cast<const uint32_t*>(vt + (2 * jp + 1) * HD + 2 * dp) : 0u;
+                        const uint32_t p = pp[jp];
+                        a0 = dot2(p, __builtin_amdgcn_perm(v1, v0, 0x05040100u), a0);
+                        a1 = dot2(p, __builtin_amdgcn_perm(v1, v0, 0x07060302u), a1);
+                    }
+                    o0[i] = a0;
+                    o1[i] = a1;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (layer == 14) stamp(a, 900 + 4);
+    // fold the key slices
+    if (nsl > 1) {
+        if (pv_on) {
+            osl[2 * tidx()] = o0[0];
+            osl[2 * tidx() + 1] = o1[0];
+        }
+        __syncthreads();
+        if (tidx() < items) {
+            float a0 = 0.f, a1 = 0.f;
+            for (int t = 0; t < nsl; ++t) {
+                a0 += osl[2 * (t * items + tidx())];
+                a1 += osl[2 * (t * items + tidx()) + 1];
+            }
+            o0[0] = a0;
+            o1[0] = a1;
+        }
+    }
+    // split record, in ncomb slices of dsl head dims: [o[dsl], m, l] per (slice, split, head)
+    const int dsl = comb_slice(HD, S), ncomb = (HD + dsl - 1) / dsl, rec = dsl + 2;
+    uint64_t* gbase = a.part + zl + (int64_t)g * part_words_per_group(HD, Gq, smax);
+#pragma unroll
+    for (int i = 0; i < kMaxItems; ++i) {
+        const int idx = tidx() + i * kPT;
+        if (idx < items && (nsl == 1 || i == 0)) {
+            const int h = idx / (HD / 2), d = 2 * (idx % (HD / 2)), c = d / dsl;   // dsl is even
+            uint64_t* r = gbase + ((int64_t)(c * S + s) * Gq + h) * rec + (d - c * dsl);
+            st_word(r, tout, __float_as_uint(o0[i]));
+            st_word(r + 1, tout, __float_as_uint(o1[i]));
+        }
+    }
+    for (int it = tidx(); it < ncomb * Gq; it += kPT) {
+        const int c = it / Gq, h = it % Gq;
+        uint64_t* r = gbase + ((int64_t)(c * S + s) * Gq + h) * rec;
+        st_word(r + dsl, tout, __float_as_uint(mrun[h]));
+        st_word(r + dsl + 1, tout, __float_as_uint(lrun[h]));
+        // the last slice may hold fewer than dsl dims: its unused slots are still
+        // polled by the combiner, so they carry the tag too
+        for (int dd = HD - c * dsl; dd < dsl; ++dd) st_word(r + dd, tout, 0u);
+    }
+    if (layer == 14) stamp(a, 900 + 5);
+    if (s >= ncomb) return true;
+
+    // combiner s: dims [s dsl, s dsl + dsl) of every head of the group
+    __syncthreads();
+    float* recs = ar.att;   // S * Gq * rec floats (checked on the host)
+    const uint64_t* mine = gbase + (int64_t)s * S * Gq * rec;
+    ok = poll_words<4>(a, mine, S * Gq * rec, tout, 13, [&](int i, uint32_t v) { recs[i] = __uint_as_float(v); });
+    if (layer == 14) stamp(a, 900 + 6);
+    if (!__syncthreads_and(ok)) return false;
+    const int dlen = min(dsl, HD - s * dsl);
+    for (int it = tidx(); it < Gq * (dlen / 2); it += kPT) {
+        const int h = it / (dlen / 2), dp = it % (dlen / 2);
+        float M = -INFINITY;
+        for (int t = 0; t < S; ++t) M = fmaxf(M, recs[(t * Gq + h) * rec + dsl]);
+        float lsum = 0.f, a0 = 0.f, a1 = 0.f;
+        for (int t = 0; t < S; ++t) {
+            const float* r = recs + (t * Gq + h) * rec;
+            const float wt = r[dsl] == -INFINITY ? 0.f : __expf(r[dsl] - M);
+            lsum += wt * r[dsl + 1];
+            a0 += wt * r[2 * dp];
+            a1 += wt * r[2 * dp + 1];
+        }
+        const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+        const int64_t word = ((int64_t)(g * Gq + h) * HD + s * dsl) / 2 + dp;
+        st_word(a.attn + word, tout, pack16(a0 * inv, a1 * inv));
+    }
+    if (layer == 14) stamp(a, 900 + 7);
+    return true;
+}
+
+// ---- the kernel ---------------------------------------------------------------
+
+// Poll the FP32 residual words into hv.
+__device__ __forceinline__ bool poll_h(const PArgs& a, const Arena& ar, const uint64_t* hbuf, uint32_t tag, uint32_t site) {
+    const bool ok = poll_words<16>(a, hbuf, a.H, tag, site, [&](int i, uint32_t v) { ar.hv[i] = __uint_as_float(v); });
+    return __syncthreads_and(ok);
+}
+
+template <int FQ, int FV, int FO, int FGU, int FD, int FH, int UH, int UO, int UF, int RA, int RC, int RD, int RE,
+          int RH, int HD>
+__global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
+    extern __shared__ __align__(16) unsigned char psm[];
+    const int H = a.H, F = a.F, qd = a.n_q * HD, kvd = a.n_kv * HD;
+    const Arena ar = make_arena(psm, H, F, qd);
+    const int G = gridDim.x, w = blockIdx.x;
+    const int wave = tidx() >> 6, lane = tidx() & 63;
+    const int tok = a.scal[0], pos = a.scal[1];
+    stamp(a, 0);
+
+    // residual rows owned by this WG (rows of Wo and Wd)
+    int hb, he;
+    range_of(H, G, w, hb, he);
+
+    // embedding row -> hv (all) and own rows
+    for (int i = tidx(); i < H; i += kPT) ar.hv[i] = h2f(a.embed[(int64_t)tok * H + i]);
+    __syncthreads();
+    for (int i = tidx(); i < he - hb; i += kPT) ar.own[i] = ar.hv[hb + i];
+    __syncthreads();
+
+    // stage A partition: q / k / v segments spread over WGs in proportion to bytes
+    const int g_v = G - a.g_q - a.g_k;
+    int seg, segw, segn;
+    if (w < a.g_q) { seg = 0; segw = w; segn = a.g_q; }
+    else if (w < a.g_q + a.g_k) { seg = 1; segw = w - a.g_q; segn = a.g_k; }
+    else { seg = 2; segw = w - a.g_q - a.g_k; segn = g_v; }
+    const int seg_rows = seg == 0 ? qd : kvd;
+    const int seg_base = seg == 0 ? 0 : (seg == 1 ? qd : qd + kvd);
+    int ab, ae;
+    range_of(seg_rows, segn, segw, ab, ae);
+    int fb, fe;   // gate/up rows, in pairs
+    range_of(F / 2, G, w, fb, fe);
+    fb *= 2;
+    fe *= 2;
+
+    // Weight blocks of each wave's first task per stage, requested ahead of
+    // their input: A(l) before its residual poll, C(l) while A(l) computes,
+    // D(l) while C(l) computes, E(l) while D(l) computes.  Further tasks (rows
+    // beyond one task per wave) load in place.
+    const int a0 = ab + wave * RA, c0r = hb + wave * RC, d0 = fb + wave * RD, e0 = hb + wave * RE;
+
+    for (int l = 0; l < a.L; ++l) {
+        const bx_decode_layer& Ly = a.layers[l];
+        const int zl = opaque_zero();
+        // declared per layer: a block is live only from its load to its use
+        RowBlock<FQ, UH, RA> wa_qk;
+        RowBlock<FV, UH, RA> wa_v;
+        RowBlock<FO, UO, RC> wc;
+        RowBlock<FGU, UH, RD> wg, wu;
+        RowBlock<FD, UF, RE> we;
+        auto issue_a = [&](const bx_decode_layer& L, int z) {
+            if (a0 < ae) {
+                if (seg == 2) wa_v.load(L.Wv, kvd, H, a0 + z);
+                else wa_qk.load(seg == 0 ? L.Wq : L.Wk, seg_rows, H, a0 + z);
+            }
+        };
+        const int sl = 1 + 10 * l;
+        // ---- A: norm + q/k/v rows
+        {
+            issue_a(Ly, zl);
+            GammaRegs gam;
+            gam.load(Ly.in_ln, H);
+            if (l > 0 && !poll_h(a, ar, a.hbuf + zl, tag_of(a, l - 1, 4), 1)) return;
+            stamp(a, sl + 0);
+            wc.load(Ly.Wo, H, qd, c0r + zl);
+            if (l == 14) stamp(a, 920);
+            norm_to_xs(ar, gam, a.eps, H);
+            if (l == 14) stamp(a, 921);
+            const uint32_t t = tag_of(a, l, 0);
+            uint64_t* out = a.qkv + seg_base;
+            if (a0 < ae) {
+                if (seg == 2) {
+                    XCache<FV, UH> xu;
+                    xu.init(ar.xs, ar.xsum, H);
+                    for (int r = a0; r < ae; r += kPW * RA) {
+                        if (r != a0) wa_v.load(Ly.Wv, kvd, H, r + zl);
+                        float o[RA];
+                        wa_v.dot(H, xu, o);
+                        if (lane == 0) {
+#pragma unroll
+                            for (int rr = 0; rr < RA; ++rr)
+                                if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
+                        }
+                    }
+                } else {
+                    const void* W = seg == 0 ? Ly.Wq : Ly.Wk;
+                    XCache<FQ, UH> xu;
+                    xu.init(ar.xs, ar.xsum, H);
+                    for (int r = a0; r < ae; r += kPW * RA) {
+                        if (r != a0) wa_qk.load(W, seg_rows, H, r + zl);
+                        float o[RA];
+                        wa_qk.dot(H, xu, o);
+                        if (lane == 0) {
+#pragma unroll
+                            for (int rr = 0; rr < RA; ++rr)
+                                if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        stamp(a, sl + 1);
+        // ---- B: attention
+        if (!__syncthreads_and(attention_stage<HD>(a, ar, Ly, l, pos, zl))) return;
+        stamp(a, sl + 2);
+        // ---- C: o-proj + residual
+        {
+            if (!poll_pairs_to_xs<4>(a, ar, a.attn + zl, qd, tag_of(a, l, 1), 2)) return;
+            stamp(a, sl + 3);
+            wg.load(Ly.Wg, F, H, d0 + zl);
+            wu.load(Ly.Wu, F, H, d0 + zl);
+            const uint32_t t = tag_of(a, l, 2);
+            if (c0r < he) {
+                XCache<FO, UO> xu;
+                xu.init(ar.xs, ar.xsum, qd);
+                for (int r = c0r; r < he; r += kPW * RC) {
+                    if (r != c0r) wc.load(Ly.Wo, H, qd, r + zl);
+                    float o[RC];
+                    wc.dot(qd, xu, o);
+                    if (lane == 0) {
+#pragma unroll
+                        for (int rr = 0; rr < RC; ++rr) {
+                            if (r + rr < he) {
+                                const float nv = ar.own[r + rr - hb] + o[rr];
+                                ar.own[r + rr - hb] = nv;
+                                st_word(a.hbuf + r + rr, t, __float_as_uint(nv));
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        stamp(a, sl + 4);
+        // ---- D: norm + gate/up row pairs
+        {
+            GammaRegs gam;
+            gam.load(Ly.post_ln, H);
+            if (!poll_h(a, ar, a.hbuf + zl, tag_of(a, l, 2), 3)) return;
+            stamp(a, sl + 5);
+            we.load(Ly.Wd, H, F, e0 + zl);
+            if (l == 14) stamp(a, 922);
+            norm_to_xs(ar, gam, a.eps, H);
+            if (l == 14) stamp(a, 923);
+            const uint32_t t = tag_of(a, l, 3);
+            if (d0 < fe) {
+                XCache<FGU, UH> xu;
+                xu.init(ar.xs, ar.xsum, H);
+                for (int r = d0; r < fe; r += kPW * RD) {
+                    if (r != d0) {
+                        wg.load(Ly.Wg, F, H, r + zl);
+                        wu.load(Ly.Wu, F, H, r + zl);
+                    }
+                    float gg[RD], uu[RD];
+                    wg.dot(H, xu, gg);
+                    wu.dot(H, xu, uu);
+                    if (lane == 0) {
+#pragma unroll
+                        for (int rr = 0; rr < RD; rr += 2) {
+                            if (r + rr < fe) {
+                                const uint32_t lo = (uint32_t)f2h(gg[rr] / (1.0f + __expf(-gg[rr])) * uu[rr]);
+                                const uint32_t hi =
+                                    (uint32_t)f2h(gg[rr + 1] / (1.0f + __expf(-gg[rr + 1])) * uu[rr + 1]);
+                                st_word(a.act + (r + rr) / 2, t, lo | (hi << 16));
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        stamp(a, sl + 6);
+        // ---- E: down + residual
+        {
+            if (!poll_pairs_to_xs<16>(a, ar, a.act + zl, F, tag_of(a, l, 3), 4)) return;
+            stamp(a, sl + 7);
+            const uint32_t t = tag_of(a, l, 4);
+            if (e0 < he) {
+                XCache<FD, UF> xu;
+                xu.init(ar.xs, ar.xsum, F);
+                for (int r = e0; r < he; r += kPW * RE) {
+                    if (r != e0) we.load(Ly.Wd, H, F, r + zl);
+                    float o[RE];
+                    we.dot(F, xu, o);
+                    if (lane == 0) {
+#pragma unroll
+                        for (int rr = 0; rr < RE; ++rr) {
+                            if (r + rr < he) {
+                                const float nv = ar.own[r + rr - hb] + o[rr];
+                                ar.own[r + rr - hb] = nv;
+                                st_word(a.hbuf + r + rr, t, __float_as_uint(nv));
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        stamp(a, sl + 8);
+    }
+
+    // ---- head: final norm, lm_head rows, per-WG argmax
+    const int sh = 1 + 10 * a.L;
+    int vb, ve;
+    range_of(a.V, G, w, vb, ve);
+    float best = -INFINITY;
+    int besti = -1;
+    {
+        RowBlock<FH, UH, RH> b0, b1;
+        const int first = vb + wave * RH;
+        if (first < ve) b0.load(a.lm_head, a.V, H, first);
+        GammaRegs gam;
+        gam.load(a.final_norm, H);
+        if (!poll_h(a, ar, a.hbuf, tag_of(a, a.L - 1, 4), 5)) return;
+        stamp(a, sh + 0);
+        norm_to_xs(ar, gam, a.eps, H);
+        head_rows<FH, UH, RH>(b0, b1, a.lm_head, a.V, H, vb, ve, ar, [&](int r, float v) {
+            const uint16_t hv16 = f2h(v);
+            a.logits[r] = hv16;
+            const float q = h2f(hv16);
+            if (besti < 0 || q > best) { best = q; besti = r; }
+        });
+    }
+    stamp(a, sh + 1);
+    // WG argmax: lane 0 of each wave holds its best (lowest index among equal values).
+    float* rv = ar.red;
+    int* ri = reinterpret_cast<int*>(ar.red + 8);
+    __syncthreads();
+    if (lane == 0) {
+        rv[wave] = best;
+        ri[wave] = besti;
+    }
+    __syncthreads();
+    const uint32_t tc = tag_of(a, a.L, 0);
+    if (tidx() == 0) {
+        float bv = -INFINITY;
+        int bi = -1;
+        for (int i = 0; i < kPW; ++i) {
+            if (ri[i] < 0) continue;
+            if (bi < 0 || rv[i] > bv || (rv[i] == bv && ri[i] < bi)) { bv = rv[i]; bi = ri[i]; }
+        }
+        st_word(a.cand + 2 * w, tc, __float_as_uint(bv));
+        st_word(a.cand + 2 * w + 1, tc, (uint32_t)bi);
+    }
+    if (w != 0) return;
+    float* cv = ar.att;  // 2G values
+    const bool ok = poll_words<4>(a, a.cand, 2 * G, tc, 6, [&](int i, uint32_t v) { cv[i] = __uint_as_float(v); });
+    if (!__syncthreads_and(ok)) return;
+    if (wave == 0) {
+        // lanes scan strided candidates, then a shuffle tree keeps (max value, lowest index)
+        float bv = -INFINITY;
+        int bi = -1;
+        for (int i = lane; i < G; i += 64) {
+            const int idx = (int)__float_as_uint(cv[2 * i + 1]);
+            const float v = cv[2 * i];
+            if (idx < 0) continue;
+            if (bi < 0 || v > bv || (v == bv && idx < bi)) { bv = v; bi = idx; }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+        }
+        if (lane != 0) return;
+        int32_t* scal = a.scal;
+        scal[2] = bi;
+        scal[0] = bi;
+        scal[1] = pos + 1;
+        const int32_t c = scal[3];
+        scal[4 + c] = bi;
+        scal[3] = c + 1;
+    }
+    stamp(a, sh + 2);
+}
+
+struct PKey {
+    int fq, fv, fo, fgu, fd, fh, uh, uo, uf, hd;
+};
+
+using PFn = void (*)(PArgs);
+
+#define BX_PK(FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD)           \
+    {{FQ, FV, FO, FGU, FD, FH, UH, UO, UF, HD},                                      \
+     persist_kernel<FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD>}
+
+struct PEntry {
+    PKey k;
+    PFn fn;
+};
+
+// Instantiated shapes: the BASELINE format mixes at their widths and the small
+// test models of the same mixes.  RA..RH: rows per wave task of stages A, C, D
+// (per matrix), E and the head.
+const PEntry kPersistTable[] = {
+    // Q4_K with Q6_K v/down/output (1.7B: H 2048, F 6144; test: H 256, F 768)
+    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 3, 4, 2, 6, 2, 8, 128),
+    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 1, 4, 2, 6, 2, 8, 64),
+    // all Q8_0, tied FP16 lm_head (0.6B: H 1024, F 3072, qd 2048; test: H 512, F 1024, qd 512)
+    BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 2, 4, 2, 6, 2, 4, 128),
+    BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 1, 4, 2, 6, 2, 4, 64),
+    // Q4_K everywhere with Q6_K output (8B: H 4096, F 12288)
+    BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 4, 4, 4, 2, 4, 128),
+};
+
+struct PLayout {
+    size_t ctrl, hbuf, qkv, attn, act, part, cand, total;
+    size_t lds;
+    int smax;
+    PFn fn;
+};
+
+int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
+    const int hd = d.head_dim, qd = d.n_q * hd, kvd = d.n_kv * hd;
+    if (d.n_kv <= 0 || d.n_q % d.n_kv) return fail(BX_EINVAL, "persist: bad head counts");
+    const int Gq = d.n_q / d.n_kv;
+    if (Gq > kMaxGq) return fail(BX_EUNSUPPORTED, "persist: more than 8 query heads per KV head");
+    if (hd != 64 && hd != 128) return fail(BX_EUNSUPPORTED, "persist: head_dim must be 64 or 128");
+    if (Gq * hd > kPT * 4) return fail(BX_EUNSUPPORTED, "persist: too many query heads per KV head for head_dim");
+    if (d.hidden > 4 * 4 * kPT) return fail(BX_EUNSUPPORTED, "persist: hidden above 4096");
+    if (d.qkv_type_q != d.qkv_type_k || d.gate_type != d.up_type)
+        return fail(BX_EUNSUPPORTED, "persist: q/k or gate/up formats differ");
+    if (d.hidden % 256 || d.intermediate % 256 || qd % 256) return fail(BX_EUNSUPPORTED, "persist: widths");
+    const int smax = G / d.n_kv;
+    if (smax < 1 || G < 3) return fail(BX_EUNSUPPORTED, "persist: too few CUs");
+    if ((d.hidden + G - 1) / G > kMaxOwn) return fail(BX_EUNSUPPORTED, "persist: hidden too wide for the grid");
+    // a combiner holds S * Gq * (dsl + 2) floats of the attention scratch, S <= smax, dsl <= hd / S + 2
+    const size_t att_bytes = att_scratch_bytes(hd, Gq);
+    const size_t rec_bytes = (size_t)Gq * (hd + 4 * smax) * 4;
+    size_t lds = arena_bytes(d.hidden, d.intermediate, qd, hd, Gq);
+    if (rec_bytes > att_bytes) lds += rec_bytes - att_bytes;
+    if ((size_t)2 * G * 4 > att_bytes) return fail(BX_EUNSUPPORTED, "persist: candidate buffer");
+    if (lds > 160 * 1024) return fail(BX_EUNSUPPORTED, "persist: LDS budget exceeded");
+    const PKey want{d.qkv_type_q, d.qkv_type_v, d.o_type, d.gate_type, d.down_type, d.lm_type,
+                    upl_for(d.hidden), upl_for(qd), upl_for(d.intermediate), hd};
+    o.fn = nullptr;
+    for (const PEntry& e : kPersistTable) {
+        if (e.k.fq == want.fq && e.k.fv == want.fv && e.k.fo == want.fo && e.k.fgu == want.fgu &&
+            e.k.fd == want.fd && e.k.fh == want.fh && e.k.uh == want.uh && e.k.uo == want.uo && e.k.uf == want.uf &&
+            e.k.hd == want.hd)
+            o.fn = e.fn;
+    }
+    if (!o.fn) return fail(BX_EUNSUPPORTED, "persist: no instantiation for this format mix / width");
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t r = off;
+        off += (bytes + 255) / 256 * 256;
+        return r;
+    };
+    o.ctrl = take(256);
+    o.hbuf = take((size_t)d.hidden * 8);
+    o.qkv = take((size_t)(qd + 2 * kvd) * 8);
+    o.attn = take((size_t)qd / 2 * 8);
+    o.act = take((size_t)d.intermediate / 2 * 8);
+    o.part = take((size_t)d.n_kv * part_words_per_group(hd, Gq, smax) * 8);
+    o.cand = take((size_t)2 * G * 8);
+    o.total = off;
+    o.lds = lds;
+    o.smax = smax;
+    return BX_OK;
+}
+
+int persist_grid() { return num_cus(); }
+
+uint64_t* g_trace = nullptr;   // set by bx_persist_trace
+
+}  // namespace
+}  // namespace bx
+
+extern "C" size_t bx_persist_ws_bytes(const bx_decode_dims* d) {
+    if (!d) return 0;
+    bx::PLayout o{};
+    if (bx::persist_layout(*d, bx::persist_grid(), o) != BX_OK) return 0;
+    return o.total;
+}
+
+extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev,
+                               const uint16_t* embed, const uint16_t* final_norm, const void* lm_head,
+                               const float* cos_tab, const float* sin_tab, int32_t* scal, uint16_t* logits,
+                               void* ws, uint32_t epoch, void* stream) {
+    if (!d || !layers_dev || !embed || !final_norm || !lm_head || !cos_tab || !sin_tab || !scal || !logits || !ws)
+        return bx::fail(BX_EINVAL, "persist: null pointer");
+    if (n_layers <= 0 || n_layers > 127) return bx::fail(BX_EINVAL, "persist: layer count");
+    if (epoch == 0 || epoch >= (1u << 22)) return bx::fail(BX_EINVAL, "persist: epoch out of range");
+    const int G = bx::persist_grid();
+    bx::PLayout o{};
+    if (int rc = bx::persist_layout(*d, G, o)) return rc;
+    const int hd = d->head_dim, qd = d->n_q * hd, kvd = d->n_kv * hd;
+    bx::PArgs a{};
+    a.H = d->hidden; a.F = d->intermediate; a.n_q = d->n_q; a.n_kv = d->n_kv; a.hd = hd; a.V = d->vocab;
+    a.cap = d->cap; a.L = n_layers; a.eps = d->eps;
+    // stage A: split G over the q / k / v segments in proportion to their bytes
+    auto row_bytes = [&](int t) {
+        return (double)bx::type_block_bytes(t) * (double)(d->hidden / bx::type_block_elems(t));
+    };
+    const double bq = row_bytes(d->qkv_type_q) * qd;
+    const double bk = row_bytes(d->qkv_type_k) * kvd;
+    const double bv = row_bytes(d->qkv_type_v) * kvd;
+    int gq = (int)(G * bq / (bq + bk + bv) + 0.5), gk = (int)(G * bk / (bq + bk + bv) + 0.5);
+    if (gq < 1) gq = 1;
+    if (gk < 1) gk = 1;
+    if (gq + gk > G - 1) gk = G - 1 - gq;
+    if (gk < 1) return bx::fail(BX_EUNSUPPORTED, "persist: grid too small");
+    a.g_q = gq; a.g_k = gk;
+    a.epoch = epoch;
+    a.layers = layers_dev;
+    a.embed = embed; a.final_norm = final_norm; a.lm_head = lm_head; a.cos_t = cos_tab; a.sin_t = sin_tab;
+    a.scal = scal; a.logits = logits;
+    unsigned char* base = static_cast<unsigned char*>(ws);
+    a.ctrl = reinterpret_cast<uint32_t*>(base + o.ctrl);
+    a.hbuf = reinterpret_cast<uint64_t*>(base + o.hbuf);
+    a.qkv = reinterpret_cast<uint64_t*>(base + o.qkv);
+    a.attn = reinterpret_cast<uint64_t*>(base + o.attn);
+    a.act = reinterpret_cast<uint64_t*>(base + o.act);
+    a.part = reinterpret_cast<uint64_t*>(base + o.part);
+    a.cand = reinterpret_cast<uint64_t*>(base + o.cand);
+    a.trace = bx::g_trace;
+    hipStream_t st = bx::as_stream(stream);
+    if (o.lds > 64 * 1024) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(o.fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)o.lds) != hipSuccess)
+            return bx::fail(BX_ELAUNCH, "persist: cannot raise the LDS limit");
+    }
+    void* args[] = {&a};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(o.fn), dim3(G), dim3(bx::kPT),
+                                                    args, (unsigned)o.lds, st);
+    if (e != hipSuccess) return bx::fail(BX_ELAUNCH, std::string("persist: launch failed: ") + hipGetErrorString(e));
+    return BX_OK;
+}
+
+extern "C" int bx_persist_status(const void* ws, uint32_t* site) {
+    if (!ws) return bx::fail(BX_EINVAL, "persist_status: null workspace");
+    uint32_t c[2] = {0, 0};
+    if (hipMemcpy(c, ws, sizeof(c), hipMemcpyDeviceToHost) != hipSuccess)
+        return bx::fail(BX_ELAUNCH, "persist_status: copy failed");
+    if (site) *site = c[1];
+    return c[0] ? 1 : 0;
+}
+
+extern "C" int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg) {
+    if (buf_dev && slots_per_wg < bx::kTraceSlots) return bx::fail(BX_EINVAL, "persist_trace: need 1024 slots per workgroup");
+    bx::g_trace = buf_dev;
+    return BX_OK;
+}

@@ -79,6 +79,11 @@ public:
     // per-layer matrix + lm_head + one embedding row + norm gammas).
     std::int64_t decode_weight_bytes() const;
 
+    // How single-token steps run: 2 = persistent single launch, 1 = replayed
+    // hipGraph of per-stage kernels, 0 = the same kernels launched eagerly.
+    // Needs loaded weights and an allocated cache (creates the step session).
+    int decode_mode();
+
     const DenseDecoderConfig& config() const { return cfg_; }
 
 private:

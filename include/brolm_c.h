@@ -83,6 +83,9 @@ int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, in
 int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id);
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n);
 int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m);
+/* DenseDecoder::decode_mode: 2 persistent single launch, 1 captured graph, 0 eager; -1 on error
+ * (no counterpart in the reference: reports which of this build's step paths runs). */
+int brolm_qwen3_decode_mode(brolm_qwen3* m);
 
 /* sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142). */
 int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed);

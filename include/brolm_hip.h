@@ -168,6 +168,33 @@ int bx_decode_head(const bx_decode_dims* d, const uint16_t* final_norm, const vo
 int bx_decode_advance(int32_t* tok_dev, int32_t* pos_dev, const int32_t* next_dev, int32_t* hist, int32_t* count,
                       void* stream);
 
+/* Persistent decode step: the same single-token step (embedding, all layers,
+ * final norm, lm_head, greedy argmax, the feedback of bx_decode_advance) as
+ * ONE cooperative launch with one workgroup per CU; stages hand vectors to
+ * each other through tagged words in `ws` instead of kernel boundaries
+ * (replaces the captured step of dense_decoder.cpp:335-524 as a whole).
+ * bx_persist_ws_bytes returns 0 (with a message) for shapes/format mixes it
+ * does not cover.  `ws` must be zeroed once before the first step; `epoch`
+ * must grow by one per launch on that ws (1 <= epoch < 2^22; re-zero ws and
+ * restart at 1 when it runs out).  `layers_dev` is a device array of
+ * n_layers bx_decode_layer.  scal = {tok, pos, next, count, hist[...]} as for
+ * bx_decode_advance.  bx_persist_status reads the abort flag after the
+ * launches completed (caller synchronizes): 0 ok, 1 aborted (`site` names the
+ * wait that timed out). */
+size_t bx_persist_ws_bytes(const bx_decode_dims* d);
+int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev,
+                    const uint16_t* embed, const uint16_t* final_norm, const void* lm_head, const float* cos_tab,
+                    const float* sin_tab, int32_t* scal, uint16_t* logits, void* ws, uint32_t epoch, void* stream);
+int bx_persist_status(const void* ws, uint32_t* site);
+/* Debug timing (no counterpart in the reference): while buf_dev is non-null,
+ * every later bx_persist_step writes the device wall clock (wall_clock64, the
+ * constant-rate counter) at each stage boundary of each workgroup into
+ * buf_dev[wg * 1024 + slot]: slot 0 start, 1 + 10 l + {0 A input, 1 A done,
+ * 2 B done, 3 C input, 4 C done, 5 D input, 6 D done, 7 E input, 8 E done},
+ * 1 + 10 L + {0 head input, 1 head rows done, 2 step done (workgroup 0)}.
+ * slots_per_wg must be >= 1024.  NULL switches it off. */
+int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg);
+
 /* Device greedy argmax over FP16 logits, lowest index wins ties
  * (src/detail/generate.cpp:38-48).  Writes the id to *out (device int32).
  * workspace: bx_argmax_workspace_bytes(n). */

@@ -40,6 +40,7 @@ def test_prefill_and_decode_logits_vs_oracle(ba, which, request):
     om.allocate_cache(128)
     V = m.cfg.vocab_size
     ids = [1, 2, 3, 4, V - 1, 17, 0, 300]
+    assert m.decode_mode() == "persistent"
     got = m.forward(ids)
     want = om.forward(ids)
     assert got.shape == (len(ids), V) and np.isfinite(got).all()
@@ -147,21 +148,71 @@ def test_generate_lengths_eos_and_sampling(ba, small_gguf):
     assert o1 == o2 and len(o1) == 10
 
 
+def _session(m, env: dict) -> str:
+    """Create the model's step session under `env` (the switches are read when
+    the session is created) and return its mode."""
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return m.decode_mode()
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
 def test_graph_step_equals_eager_step(ba, small_gguf):
     """dense_decoder.cpp:335-524: the captured step replays the same kernels as
     the eager step (BROLM_NO_GRAPH), so logits agree bitwise."""
     g = _load(ba, small_gguf)
-    os.environ["BROLM_NO_GRAPH"] = "1"
-    try:
-        e = _load(ba, small_gguf)
-        ids = [3, 1, 4, 1, 5]
-        g.forward(ids)
-        e.forward(ids)
-        for t in (9, 2, 6, 5):
-            assert np.array_equal(g.forward_last([t]), e.forward_last([t]))
-        assert g.decode_greedy(3, 12) == e.decode_greedy(3, 12)
-    finally:
-        del os.environ["BROLM_NO_GRAPH"]
+    assert _session(g, {"BROLM_NO_PERSIST": "1"}) == "graph"
+    e = _load(ba, small_gguf)
+    assert _session(e, {"BROLM_NO_GRAPH": "1"}) == "eager"
+    ids = [3, 1, 4, 1, 5]
+    g.forward(ids)
+    e.forward(ids)
+    for t in (9, 2, 6, 5):
+        assert np.array_equal(g.forward_last([t]), e.forward_last([t]))
+    assert g.decode_greedy(3, 12) == e.decode_greedy(3, 12)
+
+
+@pytest.mark.parametrize("which", ["small_gguf", "small_q8_gguf"])
+def test_persistent_step_matches_graph_step(ba, which, request):
+    """The single-launch step computes the same step as the per-stage kernels
+    (same GEMV cores; attention splits differ, so FP rounding may too)."""
+    path = request.getfixturevalue(which)
+    p = _load(ba, path)
+    assert _session(p, {}) == "persistent"
+    g = _load(ba, path)
+    assert _session(g, {"BROLM_NO_PERSIST": "1"}) == "graph"
+    ids = [3, 1, 4, 1, 5, 9, 2, 6]
+    p.forward(ids)
+    g.forward(ids)
+    for t in (5, 3, 5, 8, 9, 7):
+        a, b = p.forward_last([t]), g.forward_last([t])
+        assert np.abs(a - b).max() <= LOGIT_TOL / 4
+    assert p.decode_greedy(3, 16) == g.decode_greedy(3, 16)
+    assert p.cache_len() == g.cache_len() == len(ids) + 6 + 16
+
+
+def test_persistent_step_many_splits_vs_oracle(ba, small_gguf):
+    """Context beyond one 64-key tile: several attention splits per KV head,
+    merged by split 0 of each group, against the oracle."""
+    m = _load(ba, small_gguf, cap=700)
+    assert m.decode_mode() == "persistent"
+    om = oracle.Model(str(small_gguf))
+    om.allocate_cache(700)
+    prompt = ba.prompt_ids(600, m.cfg.vocab_size, seed=42)
+    m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    tok = int(b.argmax())
+    for _ in range(6):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
 
 
 def test_cache_errors_raise(ba, small_gguf):
