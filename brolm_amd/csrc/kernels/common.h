@@ -31,6 +31,7 @@ int num_cus();
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 typedef unsigned u2v __attribute__((ext_vector_type(2)));
+typedef float f2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 // FP32 -> FP16 with round-to-nearest-even (v_cvt_f16_f32 under the default
@@ -54,16 +55,57 @@ __device__ __forceinline__ u2v ldg_nt8(const void* p) {
 }
 __device__ __forceinline__ u4v ldg16(const void* p) { return *reinterpret_cast<const u4v*>(p); }
 
-// Full 64-lane wavefront sum.
+// Cross-lane value by DPP (no LDS traffic): CTRL selects the source lane
+// (quad_perm within 4 lanes, row_half_mirror 0x141 / row_mirror 0x140 within
+// a row of 16, row_bcast:15 0x142 / row_bcast:31 0x143 from lane 15 / 31 into
+// later rows); rows outside ROWS take `ident`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float v, float ident) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ident),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Full 64-lane wavefront sum / max, returned in every lane: four steps give
+// every lane its row's result, the two broadcasts fold the rows into lane 63.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_f<0xB1>(v, 0.f);
+    v += dpp_f<0x4E>(v, 0.f);
+    v += dpp_f<0x141>(v, 0.f);
+    v += dpp_f<0x140>(v, 0.f);
+    v += dpp_f<0x142, 0xA>(v, 0.f);
+    v += dpp_f<0x143, 0xC>(v, 0.f);
+    return lane63(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x141>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x140>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v, -INFINITY));
+    return lane63(v);
+}
+// R independent sums reduced step by step together, so the steps of
+// different rows overlap instead of waiting on each other.
+template <int R>
+__device__ __forceinline__ void wave_sum_n(float (&v)[R]) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0xB1>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0x4E>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0x141>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0x140>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0x142, 0xA>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] += dpp_f<0x143, 0xC>(v[r], 0.f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = lane63(v[r]);
 }
 
 // Block-wide sum for blockDim.x == NT (multiple of 64); `red` is >= NT/64 floats of LDS.

@@ -86,7 +86,7 @@ __device__ void stage_norm(const float* __restrict__ h, const uint16_t* __restri
         store_group<true>(xs, g, x0, x1, x2, x3);
     }
     __syncthreads();
-    sums_from_lds(xs, 1, K, K / 2, xsum, K / 16);
+    sums8_from_lds(xs, K, xsum);
     __syncthreads();
 }
 
@@ -96,7 +96,7 @@ __device__ void stage_f16(const uint16_t* __restrict__ x, int K, uint32_t* xs, f
         store_group<true>(xs, g, v.x & 0xffff, v.x >> 16, v.y & 0xffff, v.y >> 16);
     }
     __syncthreads();
-    sums_from_lds(xs, 1, K, K / 2, xsum, K / 16);
+    sums8_from_lds(xs, K, xsum);
     __syncthreads();
 }
 
@@ -146,7 +146,7 @@ __global__ BX_GEMV_BOUNDS void norm_qkv_kernel(const float* __restrict__ h, cons
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
-    float* red = xsum + K / 16;
+    float* red = xsum + K / 8;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
     const int wave = threadIdx.x >> 6;
     const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
@@ -185,7 +185,7 @@ __global__ BX_GEMV_BOUNDS void norm_mlp_kernel(const float* __restrict__ h, cons
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
-    float* red = xsum + K / 16;
+    float* red = xsum + K / 8;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
     constexpr int R = RowsPer<UPL>::R > 1 ? RowsPer<UPL>::R / 2 : 1;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -214,7 +214,7 @@ __global__ BX_GEMV_BOUNDS void norm_head_kernel(const float* __restrict__ h, con
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
-    float* red = xsum + K / 16;
+    float* red = xsum + K / 8;
     stage_norm(h, gamma, eps, K, xs, xsum, red);
     const int wave = threadIdx.x >> 6;
     const int64_t w0 = (int64_t)blockIdx.x * kWaves + wave, ws = (int64_t)gridDim.x * kWaves;
@@ -432,7 +432,7 @@ unsigned gemv_blocks(int64_t rows, int K) {
     return (unsigned)(b < 1 ? 1 : b);
 }
 
-size_t norm_lds(int K) { return (size_t)K * 2 + (size_t)(K / 16) * 4 + 64 * 4; }
+size_t norm_lds(int K) { return (size_t)K * 2 + (size_t)(K / 8) * 4 + 64 * 4; }
 
 size_t attn_lds(int G, int hd) {
     return (size_t)G * hd * 4 + (size_t)kMaxKeysPerSplit * (hd + 8) * 2 + (size_t)kMaxKeysPerSplit * hd * 2 +

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
     float* xsum = reinterpret_cast<float*>(smem + K / 2);
     stage_x_f16<true, false>(X, K, 1, K, xs, K / 2, xsum, K / 16);
     __syncthreads();
-    sums_from_lds(xs, 1, K, K / 2, xsum, K / 16);
+    sums8_from_lds(xs, K, xsum);
     __syncthreads();
     constexpr int R = RowsPer<UPL>::R;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -96,7 +96,7 @@ int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* 
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
     if (blocks > cap) blocks = cap;
-    const size_t lds = (size_t)K * 2 + (size_t)(K / 16) * 4;
+    const size_t lds = (size_t)K * 2 + (size_t)(K / 8) * 4;
     BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL(upl, {
         gemv_m1_kernel<FMT_, UPL_><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
     }))

@@ -278,20 +278,6 @@ __device__ void stage_x_f16(const uint16_t* __restrict__ X, int64_t ldx, int M, 
     }
 }
 
-// Sums of 16-element segments from an LDS-staged row (any layout: the pairs of
-// a 16-aligned segment are a permutation of its elements).
-__device__ __forceinline__ void sums_from_lds(const uint32_t* xs, int M, int K, int xstride, float* xsum, int sstride) {
-    const int S = K / 16;
-    for (int i = threadIdx.x; i < M * S; i += blockDim.x) {
-        const int m = i / S, j = i - m * S;
-        const uint32_t* p = xs + m * xstride + 8 * j;
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s += h2f(p[e] & 0xffff) + h2f(p[e] >> 16);
-        xsum[m * sstride + j] = s;
-    }
-}
-
 }  // namespace bx
 
 namespace bx {
@@ -337,14 +323,33 @@ namespace bx {
 // activation values per unit are loaded from LDS once and reused for all rows
 // the wavefront streams.  R rows are loaded before any math so R*UPL 16-byte
 // weight loads are in flight per lane.
+//
+// The M = 1 dots leave the magic-exponent offset in the weights: a pair is
+// built by one v_and_or_b32 per field, (w & mask) | 0x64006400, giving
+// 1024 + q (nibble at bits 0-3) or 1024 + 16 q (nibble at bits 4-7), and the
+// offsets come off once per segment as offset * sum(x) from 8-element sums of
+// the staged activations (xsum8[j] = x[8j] + ... + x[8j+7], FP32).  Products
+// stay exact; the FP32 accumulator carries the offset's magnitude, which adds
+// about 2^-24 * 1040 * |x| per accumulation, an order below the FP16 rounding
+// of x itself.
 
 struct XU {
     uint32_t p[16];   // activation pairs in the unit's weight-pair order
-    float s0, s1;     // Q4_K: sums of the low / high 16-element segments
+    float s[4];       // sums of the unit's x segments (Q4_K: low / high 16, Q6_K: four 8s)
 };
 
+// 8-element sums of an LDS-staged row (any layout: the pairs of an 8-aligned
+// segment are a permutation of its elements).
+__device__ __forceinline__ void sums8_from_lds(const uint32_t* xs, int K, float* xsum8) {
+    for (int j = threadIdx.x; j < K / 8; j += blockDim.x) {
+        const u4v v = *reinterpret_cast<const u4v*>(xs + 4 * j);
+        xsum8[j] = ((h2f(v.x & 0xffff) + h2f(v.x >> 16)) + (h2f(v.y & 0xffff) + h2f(v.y >> 16))) +
+                   ((h2f(v.z & 0xffff) + h2f(v.z >> 16)) + (h2f(v.w & 0xffff) + h2f(v.w >> 16)));
+    }
+}
+
 template <int FMT>
-__device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum, int u) {
+__device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum8, int u) {
     XU x;
     if constexpr (FMT == FMT_Q4_K) {
         const int b = u >> 3, t = u & 7, c = t >> 1;
@@ -357,8 +362,11 @@ __device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum, int
         x.p[4] = a1.x; x.p[5] = a1.y; x.p[6] = a1.z; x.p[7] = a1.w;
         x.p[8] = b0.x; x.p[9] = b0.y; x.p[10] = b0.z; x.p[11] = b0.w;
         x.p[12] = b1.x; x.p[13] = b1.y; x.p[14] = b1.z; x.p[15] = b1.w;
-        x.s0 = xsum[e_lo >> 4];
-        x.s1 = xsum[e_hi >> 4];
+        const f2v sl = *reinterpret_cast<const f2v*>(xsum8 + (e_lo >> 3));
+        const f2v sh = *reinterpret_cast<const f2v*>(xsum8 + (e_hi >> 3));
+        x.s[0] = sl.x + sl.y;
+        x.s[1] = sh.x + sh.y;
+        x.s[2] = x.s[3] = 0.f;
     } else if constexpr (FMT == FMT_Q6_K) {
         const int b = u >> 3, t = u & 7, h = t >> 2, l0 = 8 * (t & 3);
         const int e0 = 256 * b + 128 * h + l0;
@@ -366,8 +374,8 @@ __device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum, int
         for (int j = 0; j < 4; ++j) {
             const u4v v = *reinterpret_cast<const u4v*>(xs + ((e0 + 32 * j) >> 1));
             x.p[4 * j] = v.x; x.p[4 * j + 1] = v.y; x.p[4 * j + 2] = v.z; x.p[4 * j + 3] = v.w;
+            x.s[j] = xsum8[(e0 + 32 * j) >> 3];
         }
-        x.s0 = x.s1 = 0.f;
     } else {
         const int e0 = 32 * u;
 #pragma unroll
@@ -375,60 +383,76 @@ __device__ __forceinline__ XU load_xu(const uint32_t* xs, const float* xsum, int
             const u4v v = *reinterpret_cast<const u4v*>(xs + (e0 >> 1) + 4 * q);
             x.p[4 * q] = v.x; x.p[4 * q + 1] = v.y; x.p[4 * q + 2] = v.z; x.p[4 * q + 3] = v.w;
         }
-        x.s0 = x.s1 = 0.f;
+        x.s[0] = x.s[1] = x.s[2] = x.s[3] = 0.f;
     }
     return x;
 }
 
+// 0x64006400 in a VGPR: v_and_or_b32 on gfx9 reads at most one scalar operand
+// and no literal, so the masks go in SGPRs and the magic pair in a register.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+    uint32_t r;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
+    return r;
+}
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
+
+// Q4_K unit: low nibbles (bits 0-3 of each byte) give 1024 + q, high nibbles
+// masked in place (bits 4-7) give 1024 + 16 q, so
+//   sum x w = s_lo (al - 1024 X_lo) - dmin m_lo X_lo
+//           + s_hi / 16 (ah - 1024 X_hi) - dmin m_hi X_hi.
 __device__ __forceinline__ float dot_reg(const RawQ4K& r, int u, const XU& x) {
     const int c = (u & 7) >> 1;
     const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
     int sc0, m0, sc1, m1;
     q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c, sc0, m0);
     q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c + 1, sc1, m1);
-    const float s_lo = d * (float)sc0, s_hi = d * (float)sc1;
-    const float c_lo = 8.f * s_lo - dmin * (float)m0, c_hi = 8.f * s_hi - dmin * (float)m1;
+    const uint32_t mg = magic_vgpr();
     const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float al = 0.f, ah = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t w = qw[k];
-        al = dot2(x.p[2 * k], centre(magic_pair(w & 0x000F000Fu), 1032.f), al);
-        al = dot2(x.p[2 * k + 1], centre(magic_pair((w >> 8) & 0x000F000Fu), 1032.f), al);
-        ah = dot2(x.p[8 + 2 * k], centre(magic_pair((w >> 4) & 0x000F000Fu), 1032.f), ah);
-        ah = dot2(x.p[8 + 2 * k + 1], centre(magic_pair((w >> 12) & 0x000F000Fu), 1032.f), ah);
+        const uint32_t w = qw[k], w8 = w >> 8;
+        al = dot2(x.p[2 * k], and_or(w, 0x000F000Fu, mg), al);
+        al = dot2(x.p[2 * k + 1], and_or(w8, 0x000F000Fu, mg), al);
+        ah = dot2(x.p[8 + 2 * k], and_or(w, 0x00F000F0u, mg), ah);
+        ah = dot2(x.p[8 + 2 * k + 1], and_or(w8, 0x00F000F0u, mg), ah);
     }
-    return s_lo * al + c_lo * x.s0 + s_hi * ah + c_hi * x.s1;
+    const float s_lo = d * (float)sc0, s_hi = d * (float)sc1;
+    return s_lo * __builtin_fmaf(-1024.f, x.s[0], al) - dmin * (float)m0 * x.s[0] +
+           (s_hi * 0.0625f) * __builtin_fmaf(-1024.f, x.s[1], ah) - dmin * (float)m1 * x.s[1];
 }
 
+// Q6_K unit: groups 0 and 1 place the 6-bit q at bits 0-5 (1024 + q), groups
+// 2 and 3 take the high nibble in place and the two high bits at 8-9
+// (1024 + 16 q); with q centred on 32,
+//   group 0/1: s_j (a_j - 1056 X_j),  group 2/3: s_j / 16 (a_j - 1536 X_j).
 __device__ __forceinline__ float dot_reg(const RawQ6K& r, int u, const XU& x) {
     const int t = u & 7, h = t >> 2, l0 = 8 * (t & 3);
     const float d = h2f(r.d & 0xffff);
     const uint32_t slo = h ? r.sc.z : r.sc.x, shi = h ? r.sc.w : r.sc.y;
     const int sb = (l0 >= 16) ? 8 : 0;
-    const float s0 = d * (float)(int8_t)((slo >> sb) & 0xff), s1 = d * (float)(int8_t)((slo >> (16 + sb)) & 0xff);
-    const float s2 = d * (float)(int8_t)((shi >> sb) & 0xff), s3 = d * (float)(int8_t)((shi >> (16 + sb)) & 0xff);
+    const uint32_t mg = magic_vgpr();
     const uint32_t A[2] = {r.ql.x, r.ql.y}, B[2] = {r.ql.z, r.ql.w}, Hq[2] = {r.qh.x, r.qh.y};
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const uint32_t a = A[k], bb = B[k], q = Hq[k];
-        a0 = dot2(x.p[2 * k], centre(magic_pair((a & 0x000F000Fu) | ((q & 0x00030003u) << 4)), 1056.f), a0);
-        a0 = dot2(x.p[2 * k + 1],
-                  centre(magic_pair(((a >> 8) & 0x000F000Fu) | (((q >> 8) & 0x00030003u) << 4)), 1056.f), a0);
-        a1 = dot2(x.p[4 + 2 * k], centre(magic_pair((bb & 0x000F000Fu) | (((q >> 2) & 0x00030003u) << 4)), 1056.f), a1);
-        a1 = dot2(x.p[4 + 2 * k + 1],
-                  centre(magic_pair(((bb >> 8) & 0x000F000Fu) | (((q >> 10) & 0x00030003u) << 4)), 1056.f), a1);
-        a2 = dot2(x.p[8 + 2 * k],
-                  centre(magic_pair(((a >> 4) & 0x000F000Fu) | (((q >> 4) & 0x00030003u) << 4)), 1056.f), a2);
-        a2 = dot2(x.p[8 + 2 * k + 1],
-                  centre(magic_pair(((a >> 12) & 0x000F000Fu) | (((q >> 12) & 0x00030003u) << 4)), 1056.f), a2);
-        a3 = dot2(x.p[12 + 2 * k],
-                  centre(magic_pair(((bb >> 4) & 0x000F000Fu) | (((q >> 6) & 0x00030003u) << 4)), 1056.f), a3);
-        a3 = dot2(x.p[12 + 2 * k + 1],
-                  centre(magic_pair(((bb >> 12) & 0x000F000Fu) | (((q >> 14) & 0x00030003u) << 4)), 1056.f), a3);
+        const uint32_t a8 = a >> 8, b8 = bb >> 8;
+        const uint32_t ql4 = q << 4, qr4 = q >> 4, ql2 = q << 2, qr6 = q >> 6;
+        a0 = dot2(x.p[2 * k], and_or(ql4, 0x00300030u, and_or(a, 0x000F000Fu, mg)), a0);
+        a0 = dot2(x.p[2 * k + 1], and_or(qr4, 0x00300030u, and_or(a8, 0x000F000Fu, mg)), a0);
+        a1 = dot2(x.p[4 + 2 * k], and_or(ql2, 0x00300030u, and_or(bb, 0x000F000Fu, mg)), a1);
+        a1 = dot2(x.p[4 + 2 * k + 1], and_or(qr6, 0x00300030u, and_or(b8, 0x000F000Fu, mg)), a1);
+        a2 = dot2(x.p[8 + 2 * k], and_or(ql4, 0x03000300u, and_or(a, 0x00F000F0u, mg)), a2);
+        a2 = dot2(x.p[8 + 2 * k + 1], and_or(qr4, 0x03000300u, and_or(a8, 0x00F000F0u, mg)), a2);
+        a3 = dot2(x.p[12 + 2 * k], and_or(ql2, 0x03000300u, and_or(bb, 0x00F000F0u, mg)), a3);
+        a3 = dot2(x.p[12 + 2 * k + 1], and_or(qr6, 0x03000300u, and_or(b8, 0x00F000F0u, mg)), a3);
     }
-    return s0 * a0 + s1 * a1 + s2 * a2 + s3 * a3;
+    const float s0 = d * (float)(int8_t)((slo >> sb) & 0xff), s1 = d * (float)(int8_t)((slo >> (16 + sb)) & 0xff);
+    const float s2 = d * (float)(int8_t)((shi >> sb) & 0xff), s3 = d * (float)(int8_t)((shi >> (16 + sb)) & 0xff);
+    return s0 * __builtin_fmaf(-1056.f, x.s[0], a0) + s1 * __builtin_fmaf(-1056.f, x.s[1], a1) +
+           (s2 * 0.0625f) * __builtin_fmaf(-1536.f, x.s[2], a2) + (s3 * 0.0625f) * __builtin_fmaf(-1536.f, x.s[3], a3);
 }
 
 __device__ __forceinline__ float dot_reg(const RawQ8& r, int, const XU& x) {
@@ -457,17 +481,8 @@ __device__ __forceinline__ float dot_reg(const RawF16& r, int, const XU& x) {
     return s;
 }
 
-// 64-lane all-reduce: DPP within rows of 16 (quad_perm [1,0,3,2], [2,3,0,1],
-// row_half_mirror, row_mirror), shuffles across rows.
-__device__ __forceinline__ float wave_allsum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
+// 64-lane all-reduce (DPP only).
+__device__ __forceinline__ float wave_allsum(float v) { return wave_sum(v); }
 
 // Dot products of rows row0 .. row0+R-1 (clamped to N-1 for loads) with the
 // activation held in xu; every lane returns the R sums.

@@ -37,7 +37,8 @@ constexpr int kTile = 128;          // keys per attention tile
 constexpr int kMaxOwn = 64;         // residual rows owned per WG
 constexpr uint32_t kSpinCheck = 128;        // poll rounds between abort checks
 constexpr uint32_t kSpinLimit = 1u << 21;   // poll rounds before giving up (~1 s)
-constexpr int kTraceSlots = 1024;           // per WG: 1 + 10 per layer + 4
+constexpr int kTraceSlots = 1024;          // per WG: 1 + 10 per layer + 4
+constexpr int kTraceLayer = 14;            // attention sub-stage stamps (slots 900-907) of this layer
 
 struct PArgs {
     int H, F, n_q, n_kv, hd, V, cap, L;
@@ -147,7 +148,7 @@ __device__ __forceinline__ bool poll_words(const PArgs& a, const uint64_t* buf, 
 
 struct Arena {
     uint32_t* xs;     // swizzled FP16 pairs, Kmax / 2
-    float* xsum;      // Kmax / 16
+    float* xsum;      // Kmax / 8 sums of 8 consecutive elements
     float* hv;        // H (full residual for the norms)
     float* own;       // kMaxOwn residual rows owned by this WG
     float* red;       // 64 reduction scratch
@@ -158,7 +159,7 @@ __host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq);
 
 __host__ __device__ inline size_t arena_bytes(int H, int F, int qd, int hd, int Gq) {
     const int kmax = H > F ? (H > qd ? H : qd) : (F > qd ? F : qd);
-    return (size_t)kmax * 2 + (size_t)(kmax / 16) * 4 + (size_t)H * 4 + kMaxOwn * 4 + 64 * 4 +
+    return (size_t)kmax * 2 + (size_t)(kmax / 8) * 4 + (size_t)H * 4 + kMaxOwn * 4 + 64 * 4 +
            att_scratch_bytes(hd, Gq);
 }
 
@@ -167,7 +168,7 @@ __device__ __forceinline__ Arena make_arena(unsigned char* base, int H, int F, i
     Arena r;
     size_t o = 0;
     r.xs = reinterpret_cast<uint32_t*>(base + o); o += (size_t)kmax * 2;
-    r.xsum = reinterpret_cast<float*>(base + o); o += (size_t)(kmax / 16) * 4;
+    r.xsum = reinterpret_cast<float*>(base + o); o += (size_t)(kmax / 8) * 4;
     r.hv = reinterpret_cast<float*>(base + o); o += (size_t)H * 4;
     r.own = reinterpret_cast<float*>(base + o); o += kMaxOwn * 4;
     r.red = reinterpret_cast<float*>(base + o); o += 64 * 4;
@@ -175,54 +176,19 @@ __device__ __forceinline__ Arena make_arena(unsigned char* base, int H, int F, i
     return r;
 }
 
-__device__ __forceinline__ float block_sum_p(float v, float* red) {
-    v = wave_allsum(v);
-    const int wave = tidx() >> 6;
-    __syncthreads();
-    if ((tidx() & 63) == 0) red[wave] = v;
-    __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < kPW; ++i) s += red[i];
-    return s;
-}
-
-// A norm's FP16 gamma, groups g = t + kPT i of 4 values, loaded into registers
-// before the normalized vector's input arrives.
-constexpr int kGammaRegs = 4;   // hidden <= 4 * 4 * kPT
+// A norm's FP16 gamma for the 8-element chunks c = tidx() + j kPT, loaded
+// into registers before the normalized vector's input arrives.
+constexpr int kGammaChunks = 2;   // hidden <= 2 * 8 * kPT
 struct GammaRegs {
-    u2v v[kGammaRegs];
+    u4v v[kGammaChunks];
     __device__ __forceinline__ void load(const void* gamma, int K) {
 #pragma unroll
-        for (int i = 0; i < kGammaRegs; ++i) {
-            const int g = tidx() + i * kPT;
-            if (4 * g < K) v[i] = reinterpret_cast<const u2v*>(gamma)[g];
+        for (int j = 0; j < kGammaChunks; ++j) {
+            const int c = tidx() + j * kPT;
+            if (8 * c < K) v[j] = reinterpret_cast<const u4v*>(gamma)[c];
         }
     }
 };
-
-// rms_norm of hv (FP32, K) with FP16 gamma -> swizzled FP16 xs + 16-sums.
-__device__ __forceinline__ void norm_to_xs(const Arena& ar, const GammaRegs& gam, float eps, int K) {
-    float ss = 0.f;
-    for (int i = tidx(); i < K; i += kPT) ss += ar.hv[i] * ar.hv[i];
-    ss = block_sum_p(ss, ar.red);
-    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-#pragma unroll
-    for (int i = 0; i < kGammaRegs; ++i) {
-        const int g = tidx() + i * kPT;
-        if (4 * g < K) {
-            const float4 v = *reinterpret_cast<const float4*>(ar.hv + 4 * g);
-            const u2v gm = gam.v[i];
-            store_group<true>(ar.xs, g, f2h(v.x * inv * h2f(gm.x & 0xffff)), f2h(v.y * inv * h2f(gm.x >> 16)),
-                              f2h(v.z * inv * h2f(gm.y & 0xffff)), f2h(v.w * inv * h2f(gm.y >> 16)));
-        }
-    }
-    __syncthreads();
-    sums_from_lds(ar.xs, 1, K, K / 2, ar.xsum, K / 16);
-    __syncthreads();
-}
-
-// Poll FP16-pair words (K / 2 of them) into the swizzled xs + 16-sums.
 template <int E>
 __device__ __forceinline__ bool poll_pairs_to_xs(const PArgs& a, const Arena& ar, const uint64_t* buf, int K, uint32_t tag,
                                  uint32_t site) {
@@ -236,7 +202,7 @@ __device__ __forceinline__ bool poll_pairs_to_xs(const PArgs& a, const Arena& ar
         else { h16[0] = (uint16_t)(v & 0xffff); h16[2] = (uint16_t)(v >> 16); }         // x0, x1
     });
     if (!__syncthreads_and(ok)) return false;
-    sums_from_lds(ar.xs, 1, K, K / 2, ar.xsum, K / 16);
+    sums8_from_lds(ar.xs, K, ar.xsum);
     __syncthreads();
     return true;
 }
@@ -274,13 +240,33 @@ struct RowBlock {
             float acc = 0.f;
 #pragma unroll
             for (int i = 0; i < UPL; ++i) {
+                // a select, not a branch: no control flow between the loads and the math
                 const int u = lane + 64 * i;
-                if (u < U) acc += dot_reg(raw[rr][i], u, xu.get(i, u));
+                const int uc = u < U ? u : U - 1;
+                const float c = dot_reg(raw[rr][i], uc, xu.get(i, uc));
+                acc += u < U ? c : 0.f;
             }
-            out[rr] = wave_allsum(acc);
+            out[rr] = acc;
         }
+        wave_sum_n<R>(out);
     }
 };
+
+// A wave's row tasks first, first + stride, ... below end: the first task's
+// block was loaded ahead by the caller, later ones load in place.  The first
+// task is peeled off the loop so that no in-loop load merges into its path:
+// its wait then covers its own loads and the ones issued before them, not the
+// next stage's blocks requested after it.
+template <class Load, class Comp>
+__device__ __forceinline__ void peeled_tasks(int first, int end, int stride, Load&& load, Comp&& comp) {
+    if (first < end) {
+        comp(first);
+        for (int r = first + stride; r < end; r += stride) {
+            load(r);
+            comp(r);
+        }
+    }
+}
 
 // Rows [r0, r1) of W (N x K): wave w takes tasks of R rows starting at
 // r0 + w R with stride kPW R.  prefetch() loads the first task before the
@@ -494,7 +480,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     const bool has_cur = ke == pos + 1;
     const int wave = tidx() >> 6, lane = tidx() & 63;
     const uint32_t tin = tag_of(a, layer, 0), tout = tag_of(a, layer, 1);
-    if (layer == 14) stamp(a, 900 + 0);
+    if (layer == kTraceLayer) stamp(a, 900 + 0);
 
     uint32_t* q16 = reinterpret_cast<uint32_t*>(ar.att);          // Gq * HD/2
     float* qraw = ar.att + Gq * HD / 2;                            // Gq * HD
@@ -518,7 +504,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     dma_tile<HD>(Kc, Vc, kvd, krow0, kb, min(kTile, ke - kb), kt, vt);
     RopeRegs<HD> rr;
     rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2));
-    if (layer == 14) stamp(a, 900 + 1);
+    if (layer == kTraceLayer) stamp(a, 900 + 1);
 
     // q rows of the group's heads, then (split holding pos) k and v rows.  Each
     // wave's polls complete after its own tile copies (in-order counters).
@@ -533,7 +519,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     }
     __builtin_amdgcn_s_waitcnt(0);   // tile copies of this wave landed (also without polls)
     if (!__syncthreads_and(ok)) return false;
-    if (layer == 14) stamp(a, 900 + 2);
+    if (layer == kTraceLayer) stamp(a, 900 + 2);
 
     for (int h = wave; h < Gq; h += kPW) norm_rope_head<HD>(qraw + h * HD, rr.qg, rr, a.eps, q16 + h * HD / 2);
     if (has_cur && wave == kPW - 1) {
@@ -583,32 +569,43 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
             }
         }
         __syncthreads();
-        if (layer == 14 && ti == 0) stamp(a, 900 + 3);
-        // scores of (head, key) items over all threads
-        for (int it = tidx(); it < Gq * kTile; it += kPT) {
-            const int h = it / kTile, j = it % kTile;
-            float acc = -INFINITY;
-            if (j < nk) {
+        if (layer == kTraceLayer && ti == 0) stamp(a, 900 + 3);
+        // scores of the (head, key < nk) items: a quad of lanes per item, each
+        // lane a quarter of the head dim with all its LDS reads issued at once,
+        // then a quad reduction
+        {
+            constexpr int QC = CPK / 4;   // 16-byte chunks per lane
+            const int qt = tidx() & 3;
+            for (int it = tidx() >> 2; it < Gq * nk; it += kPT / 4) {
+                const int h = it / nk, j = it - h * nk;
                 const uint32_t* q = q16 + h * HD / 2;
                 const uint16_t* kr = kt + j * HD;
-                acc = 0.f;
+                u4v kk[QC], qq[QC];
 #pragma unroll
-                for (int d8 = 0; d8 < CPK; ++d8) {
-                    const u4v kk = *reinterpret_cast<const u4v*>(kr + 8 * (d8 ^ (j & (CPK - 1))));
-                    const u4v qq = *reinterpret_cast<const u4v*>(q + 4 * d8);
-                    acc = dot2(qq.x, kk.x, acc);
-                    acc = dot2(qq.y, kk.y, acc);
-                    acc = dot2(qq.z, kk.z, acc);
-                    acc = dot2(qq.w, kk.w, acc);
+                for (int c = 0; c < QC; ++c) {
+                    const int d8 = qt * QC + c;
+                    kk[c] = *reinterpret_cast<const u4v*>(kr + 8 * (d8 ^ (j & (CPK - 1))));
+                    qq[c] = *reinterpret_cast<const u4v*>(q + 4 * d8);
                 }
-                acc *= scale;
+                float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+                for (int c = 0; c < QC; ++c) {
+                    acc = dot2(qq[c].x, kk[c].x, acc);
+                    acc2 = dot2(qq[c].y, kk[c].y, acc2);
+                    acc = dot2(qq[c].z, kk[c].z, acc);
+                    acc2 = dot2(qq[c].w, kk[c].w, acc2);
+                }
+                acc += acc2;
+                acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0xB1, 0xF, 0xF, false));
+                acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x4E, 0xF, 0xF, false));
+                if (qt == 0) sc[h * kTile + j] = acc * scale;
             }
-            sc[it] = acc;
         }
         __syncthreads();
         // softmax update per head: lane owns keys 2 lane, 2 lane + 1 (kTile = 128)
         for (int h = wave; h < Gq; h += kPW) {
-            const float s0 = sc[h * kTile + 2 * lane], s1 = sc[h * kTile + 2 * lane + 1];
+            const float s0 = 2 * lane < nk ? sc[h * kTile + 2 * lane] : -INFINITY;
+            const float s1 = 2 * lane + 1 < nk ? sc[h * kTile + 2 * lane + 1] : -INFINITY;
             const float mc = wave_max(fmaxf(s0, s1));
             const float mo = mrun[h];
             const float mn = fmaxf(mo, mc);
@@ -625,10 +622,13 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         }
         __syncthreads();
         // P.V: (p_2j, p_2j+1) . (v_2j[d], v_2j+1[d]) by v_dot2 on v_perm-paired rows.
-        // The row past nk (odd nk) is a copy of row nk - 1, which in the split
-        // holding pos is the cache row not written yet: read as zero.
+        // The trip count is padded to a multiple of 4 per slice so that each
+        // step issues four pairs' reads at once; rows at or past nk are read
+        // from row nk - 1 (finite) and meet p = 0 (every pair of the tile holds
+        // its p, zero past nk).  4 nsl divides kTile / 2, so pairs stay in the tile.
         if (pv_on) {
             const int npair = (nk + 1) / 2;
+            const int npad = (npair + 4 * nsl - 1) / (4 * nsl) * (4 * nsl);
 #pragma unroll
             for (int i = 0; i < kMaxItems; ++i) {
                 const int idx = items < kPT ? tidx() % items : tidx() + i * kPT;
@@ -637,14 +637,21 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
                     const uint32_t* pp = p16 + h * kTile / 2;
                     const float al = alph[h];
                     float a0 = o0[i] * al, a1 = o1[i] * al;
-#pragma unroll 8
-                    for (int jp = sl; jp < npair; jp += nsl) {
-                        const uint32_t v0 = *reinterpret_cast<const uint32_t*>(vt + (2 * jp) * HD + 2 * dp);
-                        const uint32_t v1 =
-                            2 * jp + 1 < nk ? *reinterpret_cast<const uint32_t*>(vt + (2 * jp + 1) * HD + 2 * dp) : 0u;
-                        const uint32_t p = pp[jp];
-                        a0 = dot2(p, __builtin_amdgcn_perm(v1, v0, 0x05040100u), a0);
-                        a1 = dot2(p, __builtin_amdgcn_perm(v1, v0, 0x07060302u), a1);
+                    for (int jp = sl; jp < npad; jp += 4 * nsl) {
+                        uint32_t v0[4], v1[4], pv[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int j2 = jp + u * nsl;
+                            const int r0 = min(2 * j2, nk - 1), r1 = min(2 * j2 + 1, nk - 1);
+                            v0[u] = *reinterpret_cast<const uint32_t*>(vt + r0 * HD + 2 * dp);
+                            v1[u] = *reinterpret_cast<const uint32_t*>(vt + r1 * HD + 2 * dp);
+                            pv[u] = pp[j2];
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            a0 = dot2(pv[u], __builtin_amdgcn_perm(v1[u], v0[u], 0x05040100u), a0);
+                            a1 = dot2(pv[u], __builtin_amdgcn_perm(v1[u], v0[u], 0x07060302u), a1);
+                        }
                     }
                     o0[i] = a0;
                     o1[i] = a1;
@@ -653,7 +660,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         }
         __syncthreads();
     }
-    if (layer == 14) stamp(a, 900 + 4);
+    if (layer == kTraceLayer) stamp(a, 900 + 4);
     // fold the key slices
     if (nsl > 1) {
         if (pv_on) {
@@ -693,7 +700,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         // polled by the combiner, so they carry the tag too
         for (int dd = HD - c * dsl; dd < dsl; ++dd) st_word(r + dd, tout, 0u);
     }
-    if (layer == 14) stamp(a, 900 + 5);
+    if (layer == kTraceLayer) stamp(a, 900 + 5);
     if (s >= ncomb) return true;
 
     // combiner s: dims [s dsl, s dsl + dsl) of every head of the group
@@ -701,35 +708,88 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     float* recs = ar.att;   // S * Gq * rec floats (checked on the host)
     const uint64_t* mine = gbase + (int64_t)s * S * Gq * rec;
     ok = poll_words<4>(a, mine, S * Gq * rec, tout, 13, [&](int i, uint32_t v) { recs[i] = __uint_as_float(v); });
-    if (layer == 14) stamp(a, 900 + 6);
+    if (layer == kTraceLayer) stamp(a, 900 + 6);
     if (!__syncthreads_and(ok)) return false;
+    // split weights exp(m_t - M) / L, one wavefront per head, splits over lanes
+    float* wgt = recs + S * Gq * rec;   // Gq * S floats
+    for (int h = wave; h < Gq; h += kPW) {
+        float M = -INFINITY;
+        for (int t = lane; t < S; t += 64) M = fmaxf(M, recs[(t * Gq + h) * rec + dsl]);
+        M = wave_max(M);
+        float lsum = 0.f;
+        for (int t = lane; t < S; t += 64) {
+            const float* r = recs + (t * Gq + h) * rec;
+            const float wt = r[dsl] == -INFINITY ? 0.f : __expf(r[dsl] - M);
+            wgt[h * S + t] = wt;
+            lsum += wt * r[dsl + 1];
+        }
+        lsum = wave_allsum(lsum);
+        const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+        for (int t = lane; t < S; t += 64) wgt[h * S + t] *= inv;
+    }
+    __syncthreads();
     const int dlen = min(dsl, HD - s * dsl);
     for (int it = tidx(); it < Gq * (dlen / 2); it += kPT) {
         const int h = it / (dlen / 2), dp = it % (dlen / 2);
-        float M = -INFINITY;
-        for (int t = 0; t < S; ++t) M = fmaxf(M, recs[(t * Gq + h) * rec + dsl]);
-        float lsum = 0.f, a0 = 0.f, a1 = 0.f;
+        float a0 = 0.f, a1 = 0.f;
         for (int t = 0; t < S; ++t) {
             const float* r = recs + (t * Gq + h) * rec;
-            const float wt = r[dsl] == -INFINITY ? 0.f : __expf(r[dsl] - M);
-            lsum += wt * r[dsl + 1];
+            const float wt = wgt[h * S + t];
             a0 += wt * r[2 * dp];
             a1 += wt * r[2 * dp + 1];
         }
-        const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
         const int64_t word = ((int64_t)(g * Gq + h) * HD + s * dsl) / 2 + dp;
-        st_word(a.attn + word, tout, pack16(a0 * inv, a1 * inv));
+        st_word(a.attn + word, tout, pack16(a0, a1));
     }
-    if (layer == 14) stamp(a, 900 + 7);
+    if (layer == kTraceLayer) stamp(a, 900 + 7);
     return true;
 }
 
 // ---- the kernel ---------------------------------------------------------------
 
 // Poll the FP32 residual words into hv.
-__device__ __forceinline__ bool poll_h(const PArgs& a, const Arena& ar, const uint64_t* hbuf, uint32_t tag, uint32_t site) {
-    const bool ok = poll_words<16>(a, hbuf, a.H, tag, site, [&](int i, uint32_t v) { ar.hv[i] = __uint_as_float(v); });
-    return __syncthreads_and(ok);
+// Residual poll fused with RMSNorm into the swizzled FP16 pairs and 8-sums of
+// the dot stages.  hbuf == nullptr: hv already holds the residual (layer 0).
+// Each thread reads back the words it polled itself, in a fixed order, for its
+// partial sum of squares, so one barrier serves both the all-arrived check and
+// the reduction; each thread then converts 8-element chunks c = tidx() + j kPT.
+__device__ __forceinline__ bool poll_norm(const PArgs& a, const Arena& ar, const uint64_t* hbuf, uint32_t tag,
+                                          uint32_t site, const GammaRegs& gam, float eps) {
+    const int K = a.H;
+    bool ok = true;
+    if (hbuf) ok = poll_words<16>(a, hbuf, K, tag, site, [&](int i, uint32_t v) { ar.hv[i] = __uint_as_float(v); });
+    float ss = 0.f;
+    for (int i = tidx(); i < K; i += kPT) ss += ar.hv[i] * ar.hv[i];
+    ss = wave_allsum(ss);
+    if ((tidx() & 63) == 0) ar.red[tidx() >> 6] = ss;
+    if (!__syncthreads_and(ok)) return false;
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPW; ++i) tot += ar.red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int j = 0; j < kGammaChunks; ++j) {
+        const int c = tidx() + j * kPT;
+        if (8 * c < K) {
+            const float4 v0 = *reinterpret_cast<const float4*>(ar.hv + 8 * c);
+            const float4 v1 = *reinterpret_cast<const float4*>(ar.hv + 8 * c + 4);
+            const u4v gm = gam.v[j];
+            const uint32_t h0 = f2h(v0.x * inv * h2f(gm.x & 0xffff)), h1 = f2h(v0.y * inv * h2f(gm.x >> 16));
+            const uint32_t h2 = f2h(v0.z * inv * h2f(gm.y & 0xffff)), h3 = f2h(v0.w * inv * h2f(gm.y >> 16));
+            const uint32_t h4 = f2h(v1.x * inv * h2f(gm.z & 0xffff)), h5 = f2h(v1.y * inv * h2f(gm.z >> 16));
+            const uint32_t h6 = f2h(v1.z * inv * h2f(gm.w & 0xffff)), h7 = f2h(v1.w * inv * h2f(gm.w >> 16));
+            // groups 2c, 2c + 1 swizzled: (x0, x2), (x1, x3), (x4, x6), (x5, x7)
+            u4v d;
+            d.x = h0 | (h2 << 16);
+            d.y = h1 | (h3 << 16);
+            d.z = h4 | (h6 << 16);
+            d.w = h5 | (h7 << 16);
+            *reinterpret_cast<u4v*>(ar.xs + 4 * c) = d;
+            ar.xsum[c] = ((h2f(h0) + h2f(h2)) + (h2f(h1) + h2f(h3))) + ((h2f(h4) + h2f(h6)) + (h2f(h5) + h2f(h7)));
+        }
+    }
+    __syncthreads();
+    return true;
 }
 
 template <int FQ, int FV, int FO, int FGU, int FD, int FH, int UH, int UO, int UF, int RA, int RC, int RD, int RE,
@@ -774,64 +834,64 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     // beyond one task per wave) load in place.
     const int a0 = ab + wave * RA, c0r = hb + wave * RC, d0 = fb + wave * RD, e0 = hb + wave * RE;
 
+    // A blocks are requested during E of the layer before (the first layer's
+    // here), so that they have landed before A's residual poll: loads complete
+    // in issue order, and a poll issued behind fresh weight loads waits for them.
+    RowBlock<FQ, UH, RA> wa_qk;
+    RowBlock<FV, UH, RA> wa_v;
+    auto issue_a = [&](const bx_decode_layer& L, int z) {
+        if (a0 < ae) {
+            if (seg == 2) wa_v.load(L.Wv, kvd, H, a0 + z);
+            else wa_qk.load(seg == 0 ? L.Wq : L.Wk, seg_rows, H, a0 + z);
+        }
+    };
+    issue_a(a.layers[0], opaque_zero());
+
     for (int l = 0; l < a.L; ++l) {
         const bx_decode_layer& Ly = a.layers[l];
         const int zl = opaque_zero();
         // declared per layer: a block is live only from its load to its use
-        RowBlock<FQ, UH, RA> wa_qk;
-        RowBlock<FV, UH, RA> wa_v;
         RowBlock<FO, UO, RC> wc;
         RowBlock<FGU, UH, RD> wg, wu;
         RowBlock<FD, UF, RE> we;
-        auto issue_a = [&](const bx_decode_layer& L, int z) {
-            if (a0 < ae) {
-                if (seg == 2) wa_v.load(L.Wv, kvd, H, a0 + z);
-                else wa_qk.load(seg == 0 ? L.Wq : L.Wk, seg_rows, H, a0 + z);
-            }
-        };
         const int sl = 1 + 10 * l;
         // ---- A: norm + q/k/v rows
         {
-            issue_a(Ly, zl);
             GammaRegs gam;
             gam.load(Ly.in_ln, H);
-            if (l > 0 && !poll_h(a, ar, a.hbuf + zl, tag_of(a, l - 1, 4), 1)) return;
+            if (!poll_norm(a, ar, l > 0 ? a.hbuf + zl : nullptr, tag_of(a, l - 1, 4), 1, gam, a.eps)) return;
             stamp(a, sl + 0);
             wc.load(Ly.Wo, H, qd, c0r + zl);
-            if (l == 14) stamp(a, 920);
-            norm_to_xs(ar, gam, a.eps, H);
-            if (l == 14) stamp(a, 921);
             const uint32_t t = tag_of(a, l, 0);
             uint64_t* out = a.qkv + seg_base;
-            if (a0 < ae) {
-                if (seg == 2) {
-                    XCache<FV, UH> xu;
-                    xu.init(ar.xs, ar.xsum, H);
-                    for (int r = a0; r < ae; r += kPW * RA) {
-                        if (r != a0) wa_v.load(Ly.Wv, kvd, H, r + zl);
+            auto put = [&](int r, const float(&o)[RA]) {
+                if (lane == 0) {
+#pragma unroll
+                    for (int rr = 0; rr < RA; ++rr)
+                        if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
+                }
+            };
+            if (seg == 2) {
+                XCache<FV, UH> xu;
+                xu.init(ar.xs, ar.xsum, H);
+                peeled_tasks(
+                    a0, ae, kPW * RA, [&](int r) { wa_v.load(Ly.Wv, kvd, H, r + zl); },
+                    [&](int r) {
                         float o[RA];
                         wa_v.dot(H, xu, o);
-                        if (lane == 0) {
-#pragma unroll
-                            for (int rr = 0; rr < RA; ++rr)
-                                if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
-                        }
-                    }
-                } else {
-                    const void* W = seg == 0 ? Ly.Wq : Ly.Wk;
-                    XCache<FQ, UH> xu;
-                    xu.init(ar.xs, ar.xsum, H);
-                    for (int r = a0; r < ae; r += kPW * RA) {
-                        if (r != a0) wa_qk.load(W, seg_rows, H, r + zl);
+                        put(r, o);
+                    });
+            } else {
+                const void* W = seg == 0 ? Ly.Wq : Ly.Wk;
+                XCache<FQ, UH> xu;
+                xu.init(ar.xs, ar.xsum, H);
+                peeled_tasks(
+                    a0, ae, kPW * RA, [&](int r) { wa_qk.load(W, seg_rows, H, r + zl); },
+                    [&](int r) {
                         float o[RA];
                         wa_qk.dot(H, xu, o);
-                        if (lane == 0) {
-#pragma unroll
-                            for (int rr = 0; rr < RA; ++rr)
-                                if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
-                        }
-                    }
-                }
+                        put(r, o);
+                    });
             }
         }
         __syncthreads();
@@ -846,11 +906,10 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             wg.load(Ly.Wg, F, H, d0 + zl);
             wu.load(Ly.Wu, F, H, d0 + zl);
             const uint32_t t = tag_of(a, l, 2);
-            if (c0r < he) {
+            {
                 XCache<FO, UO> xu;
                 xu.init(ar.xs, ar.xsum, qd);
-                for (int r = c0r; r < he; r += kPW * RC) {
-                    if (r != c0r) wc.load(Ly.Wo, H, qd, r + zl);
+                peeled_tasks(c0r, he, kPW * RC, [&](int r) { wc.load(Ly.Wo, H, qd, r + zl); }, [&](int r) {
                     float o[RC];
                     wc.dot(qd, xu, o);
                     if (lane == 0) {
@@ -863,7 +922,7 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                             }
                         }
                     }
-                }
+                });
             }
         }
         __syncthreads();
@@ -872,21 +931,18 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
         {
             GammaRegs gam;
             gam.load(Ly.post_ln, H);
-            if (!poll_h(a, ar, a.hbuf + zl, tag_of(a, l, 2), 3)) return;
+            if (!poll_norm(a, ar, a.hbuf + zl, tag_of(a, l, 2), 3, gam, a.eps)) return;
             stamp(a, sl + 5);
             we.load(Ly.Wd, H, F, e0 + zl);
-            if (l == 14) stamp(a, 922);
-            norm_to_xs(ar, gam, a.eps, H);
-            if (l == 14) stamp(a, 923);
             const uint32_t t = tag_of(a, l, 3);
-            if (d0 < fe) {
+            {
                 XCache<FGU, UH> xu;
                 xu.init(ar.xs, ar.xsum, H);
-                for (int r = d0; r < fe; r += kPW * RD) {
-                    if (r != d0) {
-                        wg.load(Ly.Wg, F, H, r + zl);
-                        wu.load(Ly.Wu, F, H, r + zl);
-                    }
+                auto load = [&](int r) {
+                    wg.load(Ly.Wg, F, H, r + zl);
+                    wu.load(Ly.Wu, F, H, r + zl);
+                };
+                peeled_tasks(d0, fe, kPW * RD, load, [&](int r) {
                     float gg[RD], uu[RD];
                     wg.dot(H, xu, gg);
                     wu.dot(H, xu, uu);
@@ -901,7 +957,7 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                             }
                         }
                     }
-                }
+                });
             }
         }
         __syncthreads();
@@ -910,12 +966,12 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
         {
             if (!poll_pairs_to_xs<16>(a, ar, a.act + zl, F, tag_of(a, l, 3), 4)) return;
             stamp(a, sl + 7);
+            if (l + 1 < a.L) issue_a(a.layers[l + 1], zl);
             const uint32_t t = tag_of(a, l, 4);
-            if (e0 < he) {
+            {
                 XCache<FD, UF> xu;
                 xu.init(ar.xs, ar.xsum, F);
-                for (int r = e0; r < he; r += kPW * RE) {
-                    if (r != e0) we.load(Ly.Wd, H, F, r + zl);
+                peeled_tasks(e0, he, kPW * RE, [&](int r) { we.load(Ly.Wd, H, F, r + zl); }, [&](int r) {
                     float o[RE];
                     we.dot(F, xu, o);
                     if (lane == 0) {
@@ -928,7 +984,7 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                             }
                         }
                     }
-                }
+                });
             }
         }
         __syncthreads();
@@ -947,9 +1003,8 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
         if (first < ve) b0.load(a.lm_head, a.V, H, first);
         GammaRegs gam;
         gam.load(a.final_norm, H);
-        if (!poll_h(a, ar, a.hbuf, tag_of(a, a.L - 1, 4), 5)) return;
+        if (!poll_norm(a, ar, a.hbuf, tag_of(a, a.L - 1, 4), 5, gam, a.eps)) return;
         stamp(a, sh + 0);
-        norm_to_xs(ar, gam, a.eps, H);
         head_rows<FH, UH, RH>(b0, b1, a.lm_head, a.V, H, vb, ve, ar, [&](int r, float v) {
             const uint16_t hv16 = f2h(v);
             a.logits[r] = hv16;
@@ -1018,11 +1073,12 @@ using PFn = void (*)(PArgs);
 
 #define BX_PK(FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD)           \
     {{FQ, FV, FO, FGU, FD, FH, UH, UO, UF, HD},                                      \
-     persist_kernel<FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD>}
+     persist_kernel<FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD>, RA}
 
 struct PEntry {
     PKey k;
     PFn fn;
+    int ra;
 };
 
 // Instantiated shapes: the BASELINE format mixes at their widths and the small
@@ -1043,6 +1099,7 @@ struct PLayout {
     size_t ctrl, hbuf, qkv, attn, act, part, cand, total;
     size_t lds;
     int smax;
+    int ra;
     PFn fn;
 };
 
@@ -1060,9 +1117,10 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
     const int smax = G / d.n_kv;
     if (smax < 1 || G < 3) return fail(BX_EUNSUPPORTED, "persist: too few CUs");
     if ((d.hidden + G - 1) / G > kMaxOwn) return fail(BX_EUNSUPPORTED, "persist: hidden too wide for the grid");
-    // a combiner holds S * Gq * (dsl + 2) floats of the attention scratch, S <= smax, dsl <= hd / S + 2
+    // a combiner holds S * Gq * (dsl + 2) floats of the attention scratch, S <= smax, dsl <= hd / S + 2,
+    // and Gq * S split weights
     const size_t att_bytes = att_scratch_bytes(hd, Gq);
-    const size_t rec_bytes = (size_t)Gq * (hd + 4 * smax) * 4;
+    const size_t rec_bytes = (size_t)Gq * (hd + 5 * smax) * 4;   // records + split weights
     size_t lds = arena_bytes(d.hidden, d.intermediate, qd, hd, Gq);
     if (rec_bytes > att_bytes) lds += rec_bytes - att_bytes;
     if ((size_t)2 * G * 4 > att_bytes) return fail(BX_EUNSUPPORTED, "persist: candidate buffer");
@@ -1074,7 +1132,10 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
         if (e.k.fq == want.fq && e.k.fv == want.fv && e.k.fo == want.fo && e.k.fgu == want.fgu &&
             e.k.fd == want.fd && e.k.fh == want.fh && e.k.uh == want.uh && e.k.uo == want.uo && e.k.uf == want.uf &&
             e.k.hd == want.hd)
+        {
             o.fn = e.fn;
+            o.ra = e.ra;
+        }
     }
     if (!o.fn) return fail(BX_EUNSUPPORTED, "persist: no instantiation for this format mix / width");
     size_t off = 0;
@@ -1125,7 +1186,11 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     bx::PArgs a{};
     a.H = d->hidden; a.F = d->intermediate; a.n_q = d->n_q; a.n_kv = d->n_kv; a.hd = hd; a.V = d->vocab;
     a.cap = d->cap; a.L = n_layers; a.eps = d->eps;
-    // stage A: split G over the q / k / v segments in proportion to their bytes
+    // stage A: when the grid has room, give every q / k workgroup at most one
+    // round of rows (kPW waves x RA rows: all of them prefetched before the
+    // residual poll) and v the rest; otherwise split in proportion to bytes.
+    const int rnd = bx::kPW * o.ra;
+    const int nq = (qd + rnd - 1) / rnd, nk = (kvd + rnd - 1) / rnd;
     auto row_bytes = [&](int t) {
         return (double)bx::type_block_bytes(t) * (double)(d->hidden / bx::type_block_elems(t));
     };
@@ -1133,6 +1198,10 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     const double bk = row_bytes(d->qkv_type_k) * kvd;
     const double bv = row_bytes(d->qkv_type_v) * kvd;
     int gq = (int)(G * bq / (bq + bk + bv) + 0.5), gk = (int)(G * bk / (bq + bk + bv) + 0.5);
+    if (nq + 2 * nk <= G) {
+        gq = nq;
+        gk = nk;
+    }
     if (gq < 1) gq = 1;
     if (gk < 1) gk = 1;
     if (gq + gk > G - 1) gk = G - 1 - gq;
