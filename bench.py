@@ -7,11 +7,13 @@ prefill a 1024-token prompt (std::mt19937_64(42) % vocab, as
 tools/bench_decode.cpp:208-213), then greedy decode at positions 1024..,
 KV cache capacity 4096.
 
-A step is one decode token: the captured hipGraph of the fused decode step
-(embedding, 28 layers, final norm + lm_head, device argmax feeding the next
-token).  W warm-up steps run first; then K steps are timed with host wall
-clock around (sync, K replays, sync), and HIP events on the decode stream
-give the GPU time per step used for the roofline.  Prints ONE JSON line.
+A step is one decode token: one launch of the persistent cooperative decode
+kernel (embedding, 28 layers, final norm + lm_head, device argmax feeding the
+next token; one workgroup per CU, stages linked by tagged dataflow words), or
+the captured hipGraph of the per-stage kernels where the persistent kernel has
+no instantiation.  W warm-up steps run first; then K steps are timed with host
+wall clock around (sync, K launches, sync), and HIP events on the decode
+stream give the GPU time per step used for the roofline.  Prints ONE JSON line.
 """
 from __future__ import annotations
 
@@ -26,6 +28,23 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+STEP_DESC = {
+    "persistent": "persistent cooperative kernel, one launch per token",
+    "graph": "hipGraph of the per-stage kernels, one launch per token",
+    "eager": "per-stage kernels launched one by one",
+}
+# HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
+# (FETCH_SIZE x 1.99974 + WRITE_SIZE x 1.0, each scale from a 256 MiB copy in the
+# same run): profiles/persist_kernel_traffic_qwen3-1.7b-q4k.md.
+MEASURED_TRAFFIC = {
+    ("qwen3-1.7b-q4k", "persistent"): 1_372_105_357,
+}
+KERNEL_DESC = {
+    "persistent": "persist_kernel: the whole decode step (all layers, lm_head, argmax) in one launch",
+    "graph": "captured decode step (hipGraph launch)",
+    "eager": "decode step (eager kernel sequence)",
+}
 
 CONFIGS = {
     # BASELINE.json configs[2]
@@ -119,6 +138,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (a reference dispatch of known bytes for "
+                         "hardware-counter runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -127,6 +149,18 @@ def main() -> int:
         return 2
 
     import brolm_amd as ba
+
+    if args.calib_copy_mib > 0:
+        import torch
+
+        n = args.calib_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calib_copy_mib} MiB read + {args.calib_copy_mib} MiB written")
+        del src, dst
 
     c = CONFIGS[args.config]
     steps = args.steps if args.steps is not None else c["decode"]
@@ -157,7 +191,9 @@ def main() -> int:
         model.time_decode_steps(first, args.warmup)
     model.truncate_cache(len(prompt))
 
-    # timed region: K captured decode steps
+    mode = model.decode_mode()
+    log(f"decode step path: {mode}")
+    # timed region: K decode steps
     t0 = time.perf_counter()
     gpu_ms = model.time_decode_steps(first, steps)
     wall = time.perf_counter() - t0
@@ -192,10 +228,11 @@ def main() -> int:
         "dtype": "fp16 activations / Q4_K+Q6_K weights, fp32 accumulate",
         "data": "synthetic: seeded N(0,0.02) weights quantized to GGUF blocks, mt19937_64(42) prompt",
         "config": {"workload": args.config, "prompt_tokens": c["prompt"], "decode_tokens": steps, "kv_cap": cap,
-                   "batch": 1, "sampling": "greedy (device argmax)", "graph": "hipGraph, one launch per token"},
+                   "batch": 1, "sampling": "greedy (device argmax)", "decode_step": STEP_DESC[mode]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "captured decode step (hipGraph launch)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC.get((args.config, mode)),
+                     "kernel": KERNEL_DESC[mode],
                      "algorithmic_bytes_per_launch": wbytes, "gpu_ms_per_launch": round(gpu_ms, 5)},
         "gpu_ms_per_step_events": round(gpu_ms, 5),
         "weight_bytes_per_token": wbytes,
@@ -203,6 +240,9 @@ def main() -> int:
         "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
         "ref_loop_tok_s": round(ref_tok_s, 2),
     }
+    # device state goes before the process exit path (a profiler wrapping this
+    # run finalizes there)
+    model.close()
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline(path, cfg.vocab_size, prompt, args.cpu_seconds)

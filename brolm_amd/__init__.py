@@ -82,11 +82,16 @@ class Qwen3Model:
         if not self._h:
             raise _native.NativeError(_native.lib().brolm_last_error().decode())
 
-    def __del__(self):
+    def close(self) -> None:
+        """Free the device state now (weights, KV cache, decode sessions)
+        rather than at garbage collection."""
         h = getattr(self, "_h", None)
         if h:
             _native.lib().brolm_qwen3_free(h)
             self._h = None
+
+    def __del__(self):
+        self.close()
 
     def config(self) -> Qwen3Config:
         return self.cfg

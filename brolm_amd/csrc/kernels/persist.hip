@@ -24,6 +24,7 @@
 // Head: rms_norm(h) -> lm_head rows -> FP16 logits + per-WG argmax; WG 0
 // reduces the candidates (lowest index on ties) and advances tok/pos.
 #include <cmath>
+#include <cstdlib>
 
 #include "gemv_core.h"
 
@@ -1227,8 +1228,25 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
             return bx::fail(BX_ELAUNCH, "persist: cannot raise the LDS limit");
     }
     void* args[] = {&a};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(o.fn), dim3(G), dim3(bx::kPT),
-                                                    args, (unsigned)o.lds, st);
+    // BROLM_PERSIST_PLAIN_LAUNCH: launch the same grid without the cooperative
+    // API, for profilers that cannot finish a process whose kernels were
+    // launched cooperatively.  The occupancy check below is the one the
+    // cooperative launch makes (one workgroup per CU, grid = CU count), so
+    // the grid is co-resident on an otherwise idle device; every wait is also
+    // bounded and raises the abort flag, so the kernel ends either way.
+    static const bool plain = std::getenv("BROLM_PERSIST_PLAIN_LAUNCH") != nullptr;
+    hipError_t e;
+    if (plain) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(o.fn), bx::kPT,
+                                                          o.lds) != hipSuccess ||
+            per_cu < 1)
+            return bx::fail(BX_ELAUNCH, "persist: workgroup does not fit on a CU");
+        e = hipLaunchKernel(reinterpret_cast<const void*>(o.fn), dim3(G), dim3(bx::kPT), args, o.lds, st);
+    } else {
+        e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(o.fn), dim3(G), dim3(bx::kPT), args,
+                                       (unsigned)o.lds, st);
+    }
     if (e != hipSuccess) return bx::fail(BX_ELAUNCH, std::string("persist: launch failed: ") + hipGetErrorString(e));
     return BX_OK;
 }
