@@ -76,6 +76,7 @@ HIP_SYMBOLS = {
     "bx_persist_ws_bytes": (C.c_size_t, [C.POINTER(DecodeDimsC)]),
     "bx_persist_step": (C.c_int, [C.POINTER(DecodeDimsC), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_uint32,
                                   vp]),
+    "bx_persist_ws_init": (C.c_int, [C.POINTER(DecodeDimsC), vp, vp]),
     "bx_persist_status": (C.c_int, [vp, C.POINTER(C.c_uint32)]),
     "bx_persist_trace": (C.c_int, [vp, C.c_int]),
     "bx_argmax_workspace_bytes": (C.c_size_t, [i64]),

@@ -391,7 +391,7 @@ DecodeGraphSession& DenseDecoder::session_() {
         s->pws_bytes = bx_persist_ws_bytes(&d);
         if (s->pws_bytes != 0) {
             hipx::check(hipMalloc(&s->pws, s->pws_bytes), "hipMalloc persist ws");
-            hipx::check(hipMemsetAsync(s->pws, 0, s->pws_bytes, hipx::stream()), "memset persist ws");
+            hipx::bx(bx_persist_ws_init(&d, s->pws, hipx::stream()), "persist ws init");
             const std::size_t lb = s->layers.size() * sizeof(bx_decode_layer);
             hipx::check(hipMalloc(reinterpret_cast<void**>(&s->layers_dev), lb), "hipMalloc layer table");
             hipx::check(hipMemcpyAsync(s->layers_dev, s->layers.data(), lb, hipMemcpyHostToDevice, hipx::stream()),
@@ -438,8 +438,8 @@ static void stage_step(DecodeGraphSession& s, int32_t token, int32_t pos) {
 
 static void launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
                            const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
-    if (++s.epoch >= (1u << 22)) {  // tags ran out: clear the words and restart
-        hipx::check(hipMemsetAsync(s.pws, 0, s.pws_bytes, hipx::stream()), "memset persist ws");
+    if (++s.epoch >= 64) {  // a cycle of 16-bit tags is used up: re-initialize the words
+        hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
         s.epoch = 1;
     }
     hipx::bx(bx_persist_step(&s.dims, static_cast<int>(s.layers.size()), s.layers_dev,
@@ -458,8 +458,9 @@ static void check_persist(DecodeGraphSession& s) {
     const int st = bx_persist_status(s.pws, &site);
     if (st < 0) hipx::bx(st, "persist status");
     if (st == 1) {
-        // the words now hold a partial step: clear them so the next step starts clean
-        hipx::check(hipMemset(s.pws, 0, s.pws_bytes), "memset persist ws");
+        // the words now hold a partial step: re-initialize them so the next step starts clean
+        hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
+        hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
         s.epoch = 0;
         fail("persistent decode step aborted waiting at site " + std::to_string(site));
     }

@@ -45,15 +45,28 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
+// Global-memory views of generic pointers.  A pointer the compiler cannot
+// trace to a kernel argument (e.g. one read from a device-side table of
+// layers) is generic, and generic accesses become flat instructions, which
+// count against lgkmcnt as well as vmcnt: every later wait for an LDS access
+// would then also wait for them.  An explicit address-space cast keeps weight
+// streams on global_load and out of the LDS counter.
+#define BX_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const BX_GLOBAL T* gptr(const void* p) {
+    return (const BX_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ BX_GLOBAL T* gptr_w(void* p) {
+    return (BX_GLOBAL T*)p;
+}
+
 // Streaming (read-once) loads: the `nt` hint keeps weight streams from
 // thrashing L2/MALL; measured 7.1 TB/s vs 6.3 TB/s for plain loads.
-__device__ __forceinline__ u4v ldg_nt16(const void* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
-}
-__device__ __forceinline__ u2v ldg_nt8(const void* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
-}
-__device__ __forceinline__ u4v ldg16(const void* p) { return *reinterpret_cast<const u4v*>(p); }
+__device__ __forceinline__ u4v ldg_nt16(const void* p) { return __builtin_nontemporal_load(gptr<u4v>(p)); }
+__device__ __forceinline__ u2v ldg_nt8(const void* p) { return __builtin_nontemporal_load(gptr<u2v>(p)); }
+__device__ __forceinline__ u4v ldg16(const void* p) { return *gptr<u4v>(p); }
+__device__ __forceinline__ uint16_t ldg_u16(const void* p) { return *gptr<uint16_t>(p); }
 
 // Cross-lane value by DPP (no LDS traffic): CTRL selects the source lane
 // (quad_perm within 4 lanes, row_half_mirror 0x141 / row_mirror 0x140 within

@@ -66,7 +66,7 @@ __device__ __forceinline__ RawQ6K load_unit<FMT_Q6_K>(const void* W, int64_t N, 
     r.ql = ldg_nt16(c.ql + s * 128 + 16 * t);
     r.qh = ldg_nt8(c.qh + s * 64 + 8 * t);
     r.sc = ldg16(c.sc + s * 16);
-    r.d = *reinterpret_cast<const uint16_t*>(c.d + s * 2);
+    r.d = ldg_u16(c.d + s * 2);
     return r;
 }
 
@@ -77,7 +77,7 @@ __device__ __forceinline__ RawQ8 load_unit<FMT_Q8_0>(const void* W, int64_t N, i
     RawQ8 r;
     r.q0 = ldg_nt16(c.qs + s * 32);
     r.q1 = ldg_nt16(c.qs + s * 32 + 16);
-    r.d = *reinterpret_cast<const uint16_t*>(c.d + s * 2);
+    r.d = ldg_u16(c.d + s * 2);
     return r;
 }
 

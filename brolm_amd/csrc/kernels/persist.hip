@@ -5,13 +5,17 @@
 // greedy argmax and the token feedback — runs as ONE cooperative launch with
 // one workgroup per CU.  Stages that the multi-kernel step separates with a
 // kernel boundary are separated here by dataflow: every vector a stage hands
-// to the next is written as 64-bit words {value bits, tag} with device-scope
-// relaxed atomic stores, and consumers poll those words (device-scope relaxed
-// atomic loads, coherent across XCDs) until every tag equals the tag of the
-// (step, layer, stage) they wait for.  Tags grow monotonically with the
-// launch epoch, so buffers are never cleared between steps.  A poll gives up
-// after a bounded number of rounds and raises a shared abort flag that every
-// other poll checks, so all waves leave the kernel on any failure.
+// to the next is written as 64-bit words {16-bit tag, three FP16 values} (or
+// {tag, one 32-bit value} for split records and argmax candidates) with
+// device-scope relaxed atomic stores, and consumers poll those words
+// (device-scope relaxed atomic loads, coherent across XCDs) until every tag
+// equals the tag of the (epoch, layer, stage) they wait for.  The polled
+// volume is what an all-to-all hand-off costs, hence three values per word.
+// The epoch cycles through 1..63; the host re-initializes the words
+// (bx_persist_ws_init) before each cycle, so a word never holds a stale tag
+// equal to the one awaited.  A poll gives up after a bounded number of rounds
+// and raises a shared abort flag that every other poll checks, so all waves
+// leave the kernel on any failure.
 //
 // Per layer (WG w of G):
 //   A  rms_norm(h) -> rows of [Wq; Wk; Wv] (segments spread over G by bytes)
@@ -55,23 +59,45 @@ struct PArgs {
     int32_t* scal;                   // tok, pos, next, count, hist[...]
     uint16_t* logits;
     uint32_t* ctrl;                  // [0] abort flag, [1] failure site
-    uint64_t* hbuf;                  // H words: FP32 residual
-    uint64_t* qkv;                   // qd + 2 kvd words: FP32 GEMV outputs
-    uint64_t* attn;                  // qd / 2 words: FP16 pairs
-    uint64_t* act;                   // F / 2 words: FP16 pairs
-    uint64_t* part;                  // n_kv * Smax * Gq * (hd + 2) words: FP32 split records
+    uint64_t* hbuf;                  // words3(H) words: FP16 residual triples
+    uint64_t* qw;                    // n_q * hw words: q triples per head (hw = head_words(hd))
+    uint64_t* kw;                    // n_kv * hw words: k triples per head
+    uint64_t* vw;                    // n_kv * hw words: v triples per head
+    uint64_t* attn;                  // n_q * hw words: attention output triples per head
+    uint64_t* act;                   // words3(F) words: SwiGLU output triples
+    uint64_t* part;                  // n_kv * part_words_per_group words: FP32 split records
     uint64_t* cand;                  // 2 G words: per-WG argmax value / index
+    int64_t part_stride;             // words of split records per KV group
     uint64_t* trace;                 // optional wall-clock stamps [G][kTraceSlots] (bx_persist_trace)
 };
+
+// ---- tagged words ----------------------------------------------------------
+// bits 48-63: tag; bits 0-47: three FP16 values (v0 at bit 0, v1 at 16, v2 at
+// 32) or bits 0-31: one 32-bit value.  tag = (epoch mod 64) << 10 | layer << 3
+// | stage with epoch in 1..63 and layer <= 126, so the all-ones pattern the
+// words are initialized to is never a live tag.
+__host__ __device__ constexpr int words3(int n) { return (n + 2) / 3; }
+// Words per head of a per-head triple vector: words3(hd) rounded up to even,
+// so every head (and group of heads) starts 16-byte aligned for the paired
+// polls; a padding word holds no element but is written and polled like the
+// others.
+__host__ __device__ constexpr int head_words(int hd) { return (words3(hd) + 1) & ~1; }
 
 __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_word(uint64_t* p, uint32_t tag, uint32_t v) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_u32(uint64_t* p, uint32_t tag, uint32_t v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 48) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_h3(uint64_t* p, uint32_t tag, uint32_t v0, uint32_t v1, uint32_t v2) {
+    __hip_atomic_store(p, ((uint64_t)tag << 48) | ((uint64_t)v2 << 32) | ((uint64_t)v1 << 16) | (uint64_t)v0,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 48); }
+__device__ __forceinline__ uint32_t word_lo(uint64_t w) { return (uint32_t)w; }
+__device__ __forceinline__ uint32_t word_h(uint64_t w, int j) { return (uint32_t)(w >> (16 * j)) & 0xffffu; }
 __device__ __forceinline__ uint32_t tag_of(const PArgs& a, int layer, int stage) {
-    return a.epoch * 1024u + (uint32_t)layer * 8u + (uint32_t)stage;
+    return ((a.epoch & 63u) << 10) | ((uint32_t)layer << 3) | (uint32_t)stage;
 }
 
 // The thread index through an opaque move: values derived from it (per-lane
@@ -93,6 +119,13 @@ __device__ __forceinline__ int opaque_zero() {
     return z;
 }
 
+// Compiler memory barrier after a prefetch: without it the compiler sinks
+// the weight loads to their first use (past the polls in between) and waits
+// for them there, so nothing is in flight ahead of time.  It emits no
+// instruction and does not wait for the loads.
+template <int ID>
+__device__ __forceinline__ void pin_loads() { asm volatile("; prefetch point %0" ::"i"(ID) : "memory"); }
+
 // Wall-clock stamp of a stage boundary (thread 0) when tracing is on.
 __device__ __forceinline__ void stamp(const PArgs& a, int slot) {
     if (a.trace && tidx() == 0) a.trace[(size_t)blockIdx.x * kTraceSlots + slot] = wall_clock64();
@@ -106,27 +139,92 @@ __device__ __forceinline__ void raise_abort(const PArgs& a, uint32_t site) {
     __hip_atomic_store(a.ctrl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Poll words [0, n) of buf (thread t owns t, t + kPT, ...), E in flight per
-// thread; sink(i, value) for each word once its tag matches.  false on abort.
+// Poll words [0, n) of buf two at a time: 16-byte device-scope loads (sc1
+// buffer loads) of word pairs.  Each 8-byte half carries its own tag, so a
+// load that saw two different writes cannot pass a stale half.  Thread t owns
+// pairs t, t + kPT, ...; E pairs in flight per thread; sink(i, word) for each
+// word once its tag matches.  false on abort.
 template <int E, class Sink>
 __device__ __forceinline__ bool poll_words(const PArgs& a, const uint64_t* buf, int n, uint32_t tag, uint32_t site,
                                            Sink sink) {
-    for (int base = 0; base < n; base += E * kPT) {
-        uint32_t pend = 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(buf), 0, (n + 1) / 2 * 16, 0x00020000);
+    const int np = (n + 1) / 2;
+    for (int base = 0; base < np; base += E * kPT) {
+        uint32_t pend = 0;   // bit 2e + h: word h of pair e
 #pragma unroll
-        for (int e = 0; e < E; ++e)
-            if (base + tidx() + e * kPT < n) pend |= 1u << e;
+        for (int e = 0; e < E; ++e) {
+            const int pi = base + tidx() + e * kPT;
+            if (pi < np) pend |= (2 * pi + 1 < n ? 3u : 1u) << (2 * e);
+        }
         uint32_t rounds = 0;
         while (pend) {
-            uint64_t w[E];
+            u4v v[E];
 #pragma unroll
             for (int e = 0; e < E; ++e)
-                if (pend & (1u << e)) w[e] = ld_word(buf + base + tidx() + e * kPT);
+                if (pend & (3u << (2 * e)))
+                    v[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, (base + tidx() + e * kPT) * 16, 0, 16);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                if ((pend & (1u << e)) && (uint32_t)(w[e] >> 32) == tag) {
-                    pend &= ~(1u << e);
-                    sink(base + tidx() + e * kPT, (uint32_t)w[e]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t bit = 1u << (2 * e + h);
+                    const uint64_t w = ((uint64_t)v[e][2 * h + 1] << 32) | v[e][2 * h];
+                    if ((pend & bit) && word_tag(w) == tag) {
+                        pend &= ~bit;
+                        sink(2 * (base + tidx() + e * kPT) + h, w);
+                    }
+                }
+            }
+            if (pend) {
+                ++rounds;
+                if (rounds % kSpinCheck == 0) {
+                    if (aborted(a)) return false;
+                    if (rounds >= kSpinLimit) {
+                        raise_abort(a, site);
+                        return false;
+                    }
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+    }
+    return true;
+}
+
+// Poll np word pairs at base + off(p) (16-byte aligned, both words live),
+// E pairs in flight per thread; sink(p, h, word) for word h of pair p once its
+// tag matches.  For vectors spread over several buffers of one allocation.
+template <int E, class Off, class Sink>
+__device__ __forceinline__ bool poll_pairs(const PArgs& a, const uint64_t* base, int np, uint32_t tag, uint32_t site,
+                                           Off off, Sink sink) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base), 0, 0x7fffffff,
+                                                                        0x00020000);
+    for (int b = 0; b < np; b += E * kPT) {
+        uint32_t pend = 0;
+        int wo[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int pi = b + tidx() + e * kPT;
+            wo[e] = pi < np ? off(pi) : 0;
+            if (pi < np) pend |= 3u << (2 * e);
+        }
+        uint32_t rounds = 0;
+        while (pend) {
+            u4v v[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if (pend & (3u << (2 * e))) v[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, wo[e] * 8, 0, 16);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t bit = 1u << (2 * e + h);
+                    const uint64_t w = ((uint64_t)v[e][2 * h + 1] << 32) | v[e][2 * h];
+                    if ((pend & bit) && word_tag(w) == tag) {
+                        pend &= ~bit;
+                        sink(b + tidx() + e * kPT, h, w);
+                    }
                 }
             }
             if (pend) {
@@ -152,15 +250,21 @@ struct Arena {
     float* xsum;      // Kmax / 8 sums of 8 consecutive elements
     float* hv;        // H (full residual for the norms)
     float* own;       // kMaxOwn residual rows owned by this WG
+    float* rows;      // kMaxOwn stage outputs of this WG, gathered before they are packed into words
     float* red;       // 64 reduction scratch
     float* att;       // attention scratch (see attention_stage)
 };
 
 __host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq);
 
+// LDS bytes of the kernel's copy of the layer table (ahead of the arena).
+__host__ __device__ inline size_t layer_table_bytes(int L) {
+    return ((size_t)L * sizeof(bx_decode_layer) + 15) / 16 * 16;
+}
+
 __host__ __device__ inline size_t arena_bytes(int H, int F, int qd, int hd, int Gq) {
     const int kmax = H > F ? (H > qd ? H : qd) : (F > qd ? F : qd);
-    return (size_t)kmax * 2 + (size_t)(kmax / 8) * 4 + (size_t)H * 4 + kMaxOwn * 4 + 64 * 4 +
+    return (size_t)kmax * 2 + (size_t)(kmax / 8) * 4 + (size_t)H * 4 + 2 * kMaxOwn * 4 + 64 * 4 +
            att_scratch_bytes(hd, Gq);
 }
 
@@ -172,6 +276,7 @@ __device__ __forceinline__ Arena make_arena(unsigned char* base, int H, int F, i
     r.xsum = reinterpret_cast<float*>(base + o); o += (size_t)(kmax / 8) * 4;
     r.hv = reinterpret_cast<float*>(base + o); o += (size_t)H * 4;
     r.own = reinterpret_cast<float*>(base + o); o += kMaxOwn * 4;
+    r.rows = reinterpret_cast<float*>(base + o); o += kMaxOwn * 4;
     r.red = reinterpret_cast<float*>(base + o); o += 64 * 4;
     r.att = reinterpret_cast<float*>(base + o);
     return r;
@@ -186,26 +291,66 @@ struct GammaRegs {
 #pragma unroll
         for (int j = 0; j < kGammaChunks; ++j) {
             const int c = tidx() + j * kPT;
-            if (8 * c < K) v[j] = reinterpret_cast<const u4v*>(gamma)[c];
+            if (8 * c < K) v[j] = gptr<u4v>(gamma)[c];
         }
     }
 };
-template <int E>
-__device__ __forceinline__ bool poll_pairs_to_xs(const PArgs& a, const Arena& ar, const uint64_t* buf, int K, uint32_t tag,
-                                 uint32_t site) {
-    const bool ok = poll_words<E>(a, buf, K / 2, tag, site, [&](int i, uint32_t v) {
-        // pair i holds x[2i], x[2i+1]; group g = i / 2 of 4 elements
-        const int g = i >> 1;
-        uint32_t* row = ar.xs + 2 * g;
-        uint16_t* h16 = reinterpret_cast<uint16_t*>(row);
-        // swizzled: dword 2g = (x0, x2), dword 2g+1 = (x1, x3)
-        if (i & 1) { h16[1] = (uint16_t)(v & 0xffff); h16[3] = (uint16_t)(v >> 16); }   // x2, x3
-        else { h16[0] = (uint16_t)(v & 0xffff); h16[2] = (uint16_t)(v >> 16); }         // x0, x1
+// One FP16 value (bits v) of element e into the swizzled LDS pairs: group
+// g = e / 4 holds dwords 2g = (x0, x2) and 2g + 1 = (x1, x3).
+__device__ __forceinline__ void put_swz(uint32_t* xs, int e, uint32_t v) {
+    reinterpret_cast<uint16_t*>(xs)[4 * (e >> 2) + 2 * (e & 1) + ((e >> 1) & 1)] = (uint16_t)v;
+}
+
+// Poll nw words of FP16 triples into the swizzled activation of K elements
+// (element of word i, slot j: elem(i, j), skipped when >= K), then the
+// 8-element sums.  E words in flight per thread.
+template <int E, class Elem>
+__device__ __forceinline__ bool poll_triples_to_xs(const PArgs& a, const Arena& ar, const uint64_t* buf, int nw, int K,
+                                                   uint32_t tag, uint32_t site, Elem elem) {
+    const bool ok = poll_words<E>(a, buf, nw, tag, site, [&](int i, uint64_t w) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int e = elem(i, j);
+            if (e >= 0) put_swz(ar.xs, e, word_h(w, j));
+        }
     });
     if (!__syncthreads_and(ok)) return false;
     sums8_from_lds(ar.xs, K, ar.xsum);
     __syncthreads();
     return true;
+}
+
+// Element of slot j of word i in a per-head triple layout (hw words per head
+// of HD elements); -1 for the padding slots at a head's end.
+template <int HD>
+__device__ __forceinline__ int head_elem(int i, int j) {
+    constexpr int hw = head_words(HD);
+    const int h = i / hw, d = 3 * (i - h * hw) + j;
+    return d < HD ? h * HD + d : -1;
+}
+
+// First row of word W in a per-head triple layout (rows of a head are
+// contiguous; words never straddle heads; a padding word starts at the next
+// head's first row and holds none).
+template <int HD>
+__device__ __forceinline__ int head_row(int W) {
+    constexpr int hw = head_words(HD);
+    return (W / hw) * HD + min(3 * (W % hw), HD);
+}
+
+// Pack this WG's stage outputs (src[r - r0] for rows r of words [wb, we),
+// gathered in LDS) into FP16 triples and store them.  row(W) is the first row of
+// word W, nrows(W) its count (<= 3).
+template <class Row, class NRows>
+__device__ __forceinline__ void emit_triples(const float* src, uint64_t* out, int wb, int we, int r0, uint32_t tag,
+                                             Row row, NRows nrows) {
+    for (int W = wb + tidx(); W < we; W += kPT) {
+        const int r = row(W) - r0, n = nrows(W);
+        const uint32_t v0 = n > 0 ? f2h(src[r]) : 0u;
+        const uint32_t v1 = n > 1 ? f2h(src[r + 1]) : 0u;
+        const uint32_t v2 = n > 2 ? f2h(src[r + 2]) : 0u;
+        st_h3(out + W, tag, v0, v1, v2);
+    }
 }
 
 // R rows x UPL units of one matrix held in a wave's registers: loaded ahead
@@ -350,9 +495,12 @@ __device__ __forceinline__ void split_plan(int n, int smax, int& kps, int& S) {
     S = (n + kps - 1) / kps;
 }
 
-// Head dims each of a group's combining WGs merges: an even count so output
-// pairs stay whole; ceil(hd / dsl) <= S combiners.
-__device__ __forceinline__ int comb_slice(int hd, int S) { return 2 * ((hd / 2 + S - 1) / S); }
+// Output words each of a group's combining WGs merges per head: wpc words =
+// dsl = 3 wpc head dims, so a combiner emits whole FP16 triples; ncomb =
+// ceil(head_words(hd) / wpc) <= S combiners.  A split record holds dsl
+// partial sums, m and l, padded to an even word count (paired polls).
+__host__ __device__ inline int comb_words(int hd, int S) { return (head_words(hd) + S - 1) / S; }
+__host__ __device__ inline int rec_words(int wpc) { return (3 * wpc + 2 + 1) & ~1; }
 
 // Attention scratch inside the arena (host and device agree on this size).
 __host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq) {
@@ -392,9 +540,25 @@ __device__ __forceinline__ void dma_tile(const uint16_t* Kc, const uint16_t* Vc,
     }
 }
 
-// Words of the split records per KV group (any S <= smax).
-__host__ __device__ inline size_t part_words_per_group(int hd, int Gq, int smax) {
-    return (size_t)(smax + 1) * Gq * (2 * hd + 4 * smax + 4);
+// Words of the split records per KV group, for the largest of any S <= smax:
+// ncomb slices x S splits x Gq heads x (dsl partial sums + m + l).
+inline size_t part_words_per_group(int hd, int Gq, int smax) {
+    size_t best = 0;
+    for (int S = 1; S <= smax; ++S) {
+        const int wpc = comb_words(hd, S), ncomb = (head_words(hd) + wpc - 1) / wpc;
+        const size_t n = (size_t)ncomb * S * Gq * rec_words(wpc);
+        if (n > best) best = n;
+    }
+    return best;
+}
+// LDS floats a combiner needs: S x Gq records of dsl + 2 and Gq x S weights.
+inline size_t comb_lds_floats(int hd, int Gq, int smax) {
+    size_t best = 0;
+    for (int S = 1; S <= smax; ++S) {
+        const size_t n = (size_t)S * Gq * rec_words(comb_words(hd, S)) + (size_t)Gq * S;
+        if (n > best) best = n;
+    }
+    return best;
 }
 
 // Per-lane static vectors of one head row (pairs p = lane + 64 i): q_norm and
@@ -410,10 +574,10 @@ struct RopeRegs {
         for (int i = 0; i < kP; ++i) {
             const int p = lane + 64 * i;
             if (p < HD / 2) {
-                qg[i] = static_cast<const uint32_t*>(Ly.q_norm)[p];
-                kg[i] = static_cast<const uint32_t*>(Ly.k_norm)[p];
-                c[i] = cos_row[p];
-                s[i] = sin_row[p];
+                qg[i] = gptr<uint32_t>(Ly.q_norm)[p];
+                kg[i] = gptr<uint32_t>(Ly.k_norm)[p];
+                c[i] = gptr<float>(cos_row)[p];
+                s[i] = gptr<float>(sin_row)[p];
             }
         }
     }
@@ -457,9 +621,38 @@ __device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t 
     }
 }
 
+// Key tile of the attention scratch: after q16 [Gq HD/2], qraw [Gq HD],
+// kraw, vraw [HD each], kcur, vcur [HD/2 each] (4-byte units).
+template <int HD>
+__device__ __forceinline__ uint16_t* att_key_tile(const Arena& ar, int Gq) {
+    return reinterpret_cast<uint16_t*>(ar.att + Gq * HD / 2 + Gq * HD + 3 * HD);
+}
+
+// The first tile of cached keys / values of this workgroup's attention split
+// (rows below pos, written by earlier steps) goes straight to LDS.  Issued
+// right after the previous stage's output stores, so the copy overlaps the
+// wait for q / k / v; nothing touches the tile region until stage B.
+template <int HD>
+__device__ __forceinline__ void attn_tile_prefetch(const PArgs& a, const Arena& ar, const bx_decode_layer& Ly,
+                                                   int pos, int zl) {
+    const int G = gridDim.x, w = blockIdx.x;
+    const int Gq = a.n_q / a.n_kv, kvd = a.n_kv * HD;
+    const int smax = G / a.n_kv;
+    const int g = w % a.n_kv, s = w / a.n_kv;
+    if (s >= smax) return;
+    int kps, S;
+    split_plan(pos + 1, smax, kps, S);
+    if (s >= S) return;
+    const int kb = s * kps + zl, ke = min(pos + 1, kb + kps);
+    uint16_t* kt = att_key_tile<HD>(ar, Gq);
+    uint16_t* vt = kt + kTile * HD;
+    dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), kvd, (int64_t)g * HD, kb,
+                 min(kTile, ke - kb), kt, vt);
+}
+
 // Stage B for (KV group g, split s) = (w % n_kv, w / n_kv).  The first tile of
-// cached keys / values and the static per-row vectors are requested before q
-// is polled.  Scores: FP16 q . K via v_dot2 over all waves, scaled in FP32;
+// cached keys / values is already on its way (attn_tile_prefetch); the static
+// per-row vectors are requested before q is polled.  Scores: FP16 q . K via v_dot2 over all waves, scaled in FP32;
 // softmax per head with the running max / sum across tiles; P.V via v_dot2
 // over key pairs (V staged as (v_2j[d], v_2j+1[d]) pairs).  Each split writes
 // its record in ncomb slices of head dims; split c < ncomb merges slice c of
@@ -489,7 +682,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     float* vraw = kraw + HD;                                       // HD
     uint32_t* kcur = reinterpret_cast<uint32_t*>(vraw + HD);      // HD/2
     uint32_t* vcur = kcur + HD / 2;                                // HD/2
-    uint16_t* kt = reinterpret_cast<uint16_t*>(vcur + HD / 2);    // kTile x HD, 16-byte chunks XOR-swizzled
+    uint16_t* kt = att_key_tile<HD>(ar, Gq);                        // kTile x HD, 16-byte chunks XOR-swizzled
     uint16_t* vt = kt + kTile * HD;                                // kTile x HD
     float* sc = reinterpret_cast<float*>(vt + kTile * HD);        // Gq x kTile
     uint32_t* p16 = reinterpret_cast<uint32_t*>(sc + Gq * kTile); // Gq x kTile/2
@@ -501,23 +694,34 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     const uint16_t* Kc = static_cast<const uint16_t*>(Ly.Kc);
     const uint16_t* Vc = static_cast<const uint16_t*>(Ly.Vc);
     const int64_t krow0 = (int64_t)g * HD;
-    // the first tile of cached rows goes straight to LDS while q is computed elsewhere
-    dma_tile<HD>(Kc, Vc, kvd, krow0, kb, min(kTile, ke - kb), kt, vt);
+    // the first tile of cached rows was requested by attn_tile_prefetch
     RopeRegs<HD> rr;
     rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2));
     if (layer == kTraceLayer) stamp(a, 900 + 1);
 
-    // q rows of the group's heads, then (split holding pos) k and v rows.  Each
+    // q triples of the group's heads, then (split holding pos) k and v.  Each
     // wave's polls complete after its own tile copies (in-order counters).
-    bool ok = poll_words<4>(a, a.qkv + zl + (int64_t)g * Gq * HD, Gq * HD, tin, 10,
-                            [&](int i, uint32_t v) { qraw[i] = __uint_as_float(v); });
-    if (ok && has_cur) {
-        ok = poll_words<1>(a, a.qkv + zl + qd + krow0, HD, tin, 11,
-                           [&](int i, uint32_t v) { kraw[i] = __uint_as_float(v); });
-        if (ok)
-            ok = poll_words<1>(a, a.qkv + zl + qd + kvd + krow0, HD, tin, 12,
-                               [&](int i, uint32_t v) { vraw[i] = __uint_as_float(v); });
-    }
+    constexpr int hw = head_words(HD);
+    auto unpack = [](float* dst, int i, uint64_t w) {
+        const int h = i / hw, d = 3 * (i - h * hw);
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            if (d + j < HD) dst[h * HD + d + j] = h2f(word_h(w, j));
+    };
+    // one poll over the group's q words and, for the split holding pos, its k
+    // and v words (pairs: hw is even); word offsets from a.qw
+    const int npq = Gq * hw / 2, npk = has_cur ? hw / 2 : 0;
+    const int kofs = (int)(a.kw - a.qw) + g * hw, vofs = (int)(a.vw - a.qw) + g * hw;
+    bool ok = poll_pairs<1>(
+        a, a.qw + zl, npq + 2 * npk, tin, 10,
+        [&](int p) {
+            return p < npq ? g * Gq * hw + 2 * p : (p < npq + npk ? kofs + 2 * (p - npq) : vofs + 2 * (p - npq - npk));
+        },
+        [&](int p, int h, uint64_t w) {
+            if (p < npq) unpack(qraw, 2 * p + h, w);
+            else if (p < npq + npk) unpack(kraw, 2 * (p - npq) + h, w);
+            else unpack(vraw, 2 * (p - npq - npk) + h, w);
+        });
     __builtin_amdgcn_s_waitcnt(0);   // tile copies of this wave landed (also without polls)
     if (!__syncthreads_and(ok)) return false;
     if (layer == kTraceLayer) stamp(a, 900 + 2);
@@ -536,8 +740,8 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         uint16_t* Kw = static_cast<uint16_t*>(Ly.Kc);
         uint16_t* Vw = static_cast<uint16_t*>(Ly.Vc);
         for (int p = tidx(); p < HD / 2; p += kPT) {
-            reinterpret_cast<uint32_t*>(Kw + (int64_t)pos * kvd + krow0)[p] = kcur[p];
-            reinterpret_cast<uint32_t*>(Vw + (int64_t)pos * kvd + krow0)[p] = vcur[p];
+            gptr_w<uint32_t>(Kw + (int64_t)pos * kvd + krow0)[p] = kcur[p];
+            gptr_w<uint32_t>(Vw + (int64_t)pos * kvd + krow0)[p] = vcur[p];
         }
     }
 
@@ -680,26 +884,28 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         }
     }
     // split record, in ncomb slices of dsl head dims: [o[dsl], m, l] per (slice, split, head)
-    const int dsl = comb_slice(HD, S), ncomb = (HD + dsl - 1) / dsl, rec = dsl + 2;
-    uint64_t* gbase = a.part + zl + (int64_t)g * part_words_per_group(HD, Gq, smax);
+    const int wpc = comb_words(HD, S), dsl = 3 * wpc, ncomb = (hw + wpc - 1) / wpc, rec = rec_words(wpc);
+    uint64_t* gbase = a.part + zl + (int64_t)g * a.part_stride;
+    auto rec_at = [&](int c, int sp, int h) { return gbase + ((int64_t)(c * S + sp) * Gq + h) * rec; };
 #pragma unroll
     for (int i = 0; i < kMaxItems; ++i) {
         const int idx = tidx() + i * kPT;
         if (idx < items && (nsl == 1 || i == 0)) {
-            const int h = idx / (HD / 2), d = 2 * (idx % (HD / 2)), c = d / dsl;   // dsl is even
-            uint64_t* r = gbase + ((int64_t)(c * S + s) * Gq + h) * rec + (d - c * dsl);
-            st_word(r, tout, __float_as_uint(o0[i]));
-            st_word(r + 1, tout, __float_as_uint(o1[i]));
+            const int h = idx / (HD / 2), d = 2 * (idx % (HD / 2));
+            const int c0 = d / dsl, c1 = (d + 1) / dsl;
+            st_u32(rec_at(c0, s, h) + (d - c0 * dsl), tout, __float_as_uint(o0[i]));
+            st_u32(rec_at(c1, s, h) + (d + 1 - c1 * dsl), tout, __float_as_uint(o1[i]));
         }
     }
     for (int it = tidx(); it < ncomb * Gq; it += kPT) {
         const int c = it / Gq, h = it % Gq;
-        uint64_t* r = gbase + ((int64_t)(c * S + s) * Gq + h) * rec;
-        st_word(r + dsl, tout, __float_as_uint(mrun[h]));
-        st_word(r + dsl + 1, tout, __float_as_uint(lrun[h]));
+        uint64_t* r = rec_at(c, s, h);
+        st_u32(r + dsl, tout, __float_as_uint(mrun[h]));
+        st_u32(r + dsl + 1, tout, __float_as_uint(lrun[h]));
+        if (rec > dsl + 2) st_u32(r + dsl + 2, tout, 0u);
         // the last slice may hold fewer than dsl dims: its unused slots are still
         // polled by the combiner, so they carry the tag too
-        for (int dd = HD - c * dsl; dd < dsl; ++dd) st_word(r + dd, tout, 0u);
+        for (int dd = max(0, HD - c * dsl); dd < dsl; ++dd) st_u32(r + dd, tout, 0u);
     }
     if (layer == kTraceLayer) stamp(a, 900 + 5);
     if (s >= ncomb) return true;
@@ -708,7 +914,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     __syncthreads();
     float* recs = ar.att;   // S * Gq * rec floats (checked on the host)
     const uint64_t* mine = gbase + (int64_t)s * S * Gq * rec;
-    ok = poll_words<4>(a, mine, S * Gq * rec, tout, 13, [&](int i, uint32_t v) { recs[i] = __uint_as_float(v); });
+    ok = poll_words<2>(a, mine, S * Gq * rec, tout, 13, [&](int i, uint64_t v) { recs[i] = __uint_as_float(word_lo(v)); });
     if (layer == kTraceLayer) stamp(a, 900 + 6);
     if (!__syncthreads_and(ok)) return false;
     // split weights exp(m_t - M) / L, one wavefront per head, splits over lanes
@@ -729,18 +935,33 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         for (int t = lane; t < S; t += 64) wgt[h * S + t] *= inv;
     }
     __syncthreads();
-    const int dlen = min(dsl, HD - s * dsl);
-    for (int it = tidx(); it < Gq * (dlen / 2); it += kPT) {
-        const int h = it / (dlen / 2), dp = it % (dlen / 2);
-        float a0 = 0.f, a1 = 0.f;
-        for (int t = 0; t < S; ++t) {
-            const float* r = recs + (t * Gq + h) * rec;
-            const float wt = wgt[h * S + t];
-            a0 += wt * r[2 * dp];
-            a1 += wt * r[2 * dp + 1];
+    // output words [s wpc, s wpc + nws) of every head of the group: Q lanes per
+    // word (the power of two >= S, at most 16) sum strided splits, then a
+    // shuffle tree (a fixed order: the result is deterministic)
+    const int nws = min(wpc, hw - s * wpc);
+    const int Q = S > 8 ? 16 : (S > 4 ? 8 : (S > 2 ? 4 : (S > 1 ? 2 : 1)));
+    const int qi = tidx() & (Q - 1);
+    for (int it0 = 0; it0 < Gq * nws; it0 += kPT / Q) {
+        const int it = it0 + tidx() / Q;
+        const bool on = it < Gq * nws;
+        const int h = on ? it / nws : 0, k = on ? it % nws : 0;
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
+        if (on) {
+            for (int t = qi; t < S; t += Q) {
+                const float* r = recs + (t * Gq + h) * rec + 3 * k;
+                const float wt = wgt[h * S + t];
+                acc0 += wt * r[0];
+                acc1 += wt * r[1];
+                acc2 += wt * r[2];
+            }
         }
-        const int64_t word = ((int64_t)(g * Gq + h) * HD + s * dsl) / 2 + dp;
-        st_word(a.attn + word, tout, pack16(a0, a1));
+        for (int m = Q / 2; m >= 1; m >>= 1) {
+            acc0 += __shfl_xor(acc0, m, 64);
+            acc1 += __shfl_xor(acc1, m, 64);
+            acc2 += __shfl_xor(acc2, m, 64);
+        }
+        if (on && qi == 0)
+            st_h3(a.attn + (int64_t)(g * Gq + h) * hw + s * wpc + k, tout, f2h(acc0), f2h(acc1), f2h(acc2));
     }
     if (layer == kTraceLayer) stamp(a, 900 + 7);
     return true;
@@ -748,19 +969,30 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
 
 // ---- the kernel ---------------------------------------------------------------
 
-// Poll the FP32 residual words into hv.
-// Residual poll fused with RMSNorm into the swizzled FP16 pairs and 8-sums of
-// the dot stages.  hbuf == nullptr: hv already holds the residual (layer 0).
-// Each thread reads back the words it polled itself, in a fixed order, for its
-// partial sum of squares, so one barrier serves both the all-arrived check and
-// the reduction; each thread then converts 8-element chunks c = tidx() + j kPT.
+// Residual poll (FP16 triples into hv) fused with RMSNorm into the swizzled
+// FP16 pairs and 8-sums of the dot stages.  hbuf == nullptr: hv already holds
+// the residual (layer 0).  Each thread reads back the words it polled itself,
+// in a fixed order, for its partial sum of squares, so one barrier serves both
+// the all-arrived check and the reduction; each thread then converts 8-element
+// chunks c = tidx() + j kPT.
 __device__ __forceinline__ bool poll_norm(const PArgs& a, const Arena& ar, const uint64_t* hbuf, uint32_t tag,
                                           uint32_t site, const GammaRegs& gam, float eps) {
-    const int K = a.H;
+    const int K = a.H, nw = words3(K);
     bool ok = true;
-    if (hbuf) ok = poll_words<16>(a, hbuf, K, tag, site, [&](int i, uint32_t v) { ar.hv[i] = __uint_as_float(v); });
+    if (hbuf)
+        ok = poll_words<2>(a, hbuf, nw, tag, site, [&](int i, uint64_t w) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                if (3 * i + j < K) ar.hv[3 * i + j] = h2f(word_h(w, j));
+        });
+    // the words this thread polled (pairs tidx() + m kPT), in a fixed order (a
+    // deterministic sum, and no read of another thread's words before the barrier)
     float ss = 0.f;
-    for (int i = tidx(); i < K; i += kPT) ss += ar.hv[i] * ar.hv[i];
+    for (int i = 2 * tidx(); i < nw; i += 2 * kPT) {
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            if (3 * i + j < K) ss += ar.hv[3 * i + j] * ar.hv[3 * i + j];
+    }
     ss = wave_allsum(ss);
     if ((tidx() & 63) == 0) ar.red[tidx() >> 6] = ss;
     if (!__syncthreads_and(ok)) return false;
@@ -798,15 +1030,24 @@ template <int FQ, int FV, int FO, int FGU, int FD, int FH, int UH, int UO, int U
 __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     extern __shared__ __align__(16) unsigned char psm[];
     const int H = a.H, F = a.F, qd = a.n_q * HD, kvd = a.n_kv * HD;
-    const Arena ar = make_arena(psm, H, F, qd);
+    // The layer table goes to LDS first: weight pointers read from global
+    // memory would be vector loads, and the wait for one (vmcnt, in order)
+    // would also wait for every weight prefetch issued before it.
+    bx_decode_layer* const lt = reinterpret_cast<bx_decode_layer*>(psm);
+    for (int i = tidx(); i < a.L * (int)(sizeof(bx_decode_layer) / 8); i += kPT)
+        reinterpret_cast<uint64_t*>(psm)[i] = gptr<uint64_t>(a.layers)[i];
+    __syncthreads();
+    const Arena ar = make_arena(psm + layer_table_bytes(a.L), H, F, qd);
     const int G = gridDim.x, w = blockIdx.x;
     const int wave = tidx() >> 6, lane = tidx() & 63;
     const int tok = a.scal[0], pos = a.scal[1];
     stamp(a, 0);
 
-    // residual rows owned by this WG (rows of Wo and Wd)
-    int hb, he;
-    range_of(H, G, w, hb, he);
+    constexpr int hw = head_words(HD);
+    // residual rows owned by this WG (rows of Wo and Wd): whole triples
+    int hwb, hwe;
+    range_of(words3(H), G, w, hwb, hwe);
+    const int hb = 3 * hwb, he = min(3 * hwe, H);
 
     // embedding row -> hv (all) and own rows
     for (int i = tidx(); i < H; i += kPT) ar.hv[i] = h2f(a.embed[(int64_t)tok * H + i]);
@@ -814,20 +1055,23 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     for (int i = tidx(); i < he - hb; i += kPT) ar.own[i] = ar.hv[hb + i];
     __syncthreads();
 
-    // stage A partition: q / k / v segments spread over WGs in proportion to bytes
+    // stage A partition: q / k / v segments (per-head triples) spread over WGs
+    // (the host balances bytes and keeps each WG to one task round per wave)
     const int g_v = G - a.g_q - a.g_k;
     int seg, segw, segn;
     if (w < a.g_q) { seg = 0; segw = w; segn = a.g_q; }
     else if (w < a.g_q + a.g_k) { seg = 1; segw = w - a.g_q; segn = a.g_k; }
     else { seg = 2; segw = w - a.g_q - a.g_k; segn = g_v; }
     const int seg_rows = seg == 0 ? qd : kvd;
-    const int seg_base = seg == 0 ? 0 : (seg == 1 ? qd : qd + kvd);
-    int ab, ae;
-    range_of(seg_rows, segn, segw, ab, ae);
-    int fb, fe;   // gate/up rows, in pairs
-    range_of(F / 2, G, w, fb, fe);
-    fb *= 2;
-    fe *= 2;
+    uint64_t* const seg_out = seg == 0 ? a.qw : (seg == 1 ? a.kw : a.vw);
+    int awb, awe;
+    range_of(seg_rows / HD * hw, segn, segw, awb, awe);
+    const int ab = head_row<HD>(awb), ae = head_row<HD>(awe);
+    int fwb, fwe;   // SwiGLU outputs (gate/up rows): whole triples
+    range_of(words3(F), G, w, fwb, fwe);
+    const int fb = 3 * fwb, fe = min(3 * fwe, F);
+    auto head_nrows = [](int W) { return max(0, min(3, HD - 3 * (W % hw))); };
+    auto flat_row = [](int W) { return 3 * W; };
 
     // Weight blocks of each wave's first task per stage, requested ahead of
     // their input: A(l) before its residual poll, C(l) while A(l) computes,
@@ -846,10 +1090,12 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             else wa_qk.load(seg == 0 ? L.Wq : L.Wk, seg_rows, H, a0 + z);
         }
     };
-    issue_a(a.layers[0], opaque_zero());
+    attn_tile_prefetch<HD>(a, ar, lt[0], pos, opaque_zero());
+    issue_a(lt[0], opaque_zero());
+    pin_loads<1>();
 
     for (int l = 0; l < a.L; ++l) {
-        const bx_decode_layer& Ly = a.layers[l];
+        const bx_decode_layer& Ly = lt[l];
         const int zl = opaque_zero();
         // declared per layer: a block is live only from its load to its use
         RowBlock<FO, UO, RC> wc;
@@ -862,14 +1108,12 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             gam.load(Ly.in_ln, H);
             if (!poll_norm(a, ar, l > 0 ? a.hbuf + zl : nullptr, tag_of(a, l - 1, 4), 1, gam, a.eps)) return;
             stamp(a, sl + 0);
-            wc.load(Ly.Wo, H, qd, c0r + zl);
             const uint32_t t = tag_of(a, l, 0);
-            uint64_t* out = a.qkv + seg_base;
             auto put = [&](int r, const float(&o)[RA]) {
                 if (lane == 0) {
 #pragma unroll
                     for (int rr = 0; rr < RA; ++rr)
-                        if (r + rr < ae) st_word(out + r + rr, t, __float_as_uint(o[rr]));
+                        if (r + rr < ae) ar.rows[r + rr - ab] = o[rr];
                 }
             };
             if (seg == 2) {
@@ -894,18 +1138,27 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                         put(r, o);
                     });
             }
+            __syncthreads();
+            emit_triples(ar.rows, seg_out + zl, awb, awe, ab, t, [](int W) { return head_row<HD>(W); }, head_nrows);
+            // C's weights stream while q / k / v travel to the attention splits
+            wc.load(Ly.Wo, H, qd, c0r + zl);
+            pin_loads<2>();
         }
         __syncthreads();
         stamp(a, sl + 1);
         // ---- B: attention
         if (!__syncthreads_and(attention_stage<HD>(a, ar, Ly, l, pos, zl))) return;
+        // D's weights stream while the attention output travels to the o-proj
+        wg.load(Ly.Wg, F, H, d0 + zl);
+        wu.load(Ly.Wu, F, H, d0 + zl);
+        pin_loads<3>();
         stamp(a, sl + 2);
         // ---- C: o-proj + residual
         {
-            if (!poll_pairs_to_xs<4>(a, ar, a.attn + zl, qd, tag_of(a, l, 1), 2)) return;
+            if (!poll_triples_to_xs<2>(a, ar, a.attn + zl, a.n_q * hw, qd, tag_of(a, l, 1), 2,
+                                       [](int i, int j) { return head_elem<HD>(i, j); }))
+                return;
             stamp(a, sl + 3);
-            wg.load(Ly.Wg, F, H, d0 + zl);
-            wu.load(Ly.Wu, F, H, d0 + zl);
             const uint32_t t = tag_of(a, l, 2);
             {
                 XCache<FO, UO> xu;
@@ -915,16 +1168,16 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                     wc.dot(qd, xu, o);
                     if (lane == 0) {
 #pragma unroll
-                        for (int rr = 0; rr < RC; ++rr) {
-                            if (r + rr < he) {
-                                const float nv = ar.own[r + rr - hb] + o[rr];
-                                ar.own[r + rr - hb] = nv;
-                                st_word(a.hbuf + r + rr, t, __float_as_uint(nv));
-                            }
-                        }
+                        for (int rr = 0; rr < RC; ++rr)
+                            if (r + rr < he) ar.own[r + rr - hb] += o[rr];
                     }
                 });
             }
+            __syncthreads();
+            emit_triples(ar.own, a.hbuf + zl, hwb, hwe, hb, t, flat_row, [&](int W) { return min(3, H - 3 * W); });
+            // E's weights stream while the residual travels to the norm
+            we.load(Ly.Wd, H, F, e0 + zl);
+            pin_loads<4>();
         }
         __syncthreads();
         stamp(a, sl + 4);
@@ -934,11 +1187,11 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             gam.load(Ly.post_ln, H);
             if (!poll_norm(a, ar, a.hbuf + zl, tag_of(a, l, 2), 3, gam, a.eps)) return;
             stamp(a, sl + 5);
-            we.load(Ly.Wd, H, F, e0 + zl);
             const uint32_t t = tag_of(a, l, 3);
             {
                 XCache<FGU, UH> xu;
                 xu.init(ar.xs, ar.xsum, H);
+                if (l == kTraceLayer) stamp(a, 910);
                 auto load = [&](int r) {
                     wg.load(Ly.Wg, F, H, r + zl);
                     wu.load(Ly.Wu, F, H, r + zl);
@@ -946,28 +1199,28 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                 peeled_tasks(d0, fe, kPW * RD, load, [&](int r) {
                     float gg[RD], uu[RD];
                     wg.dot(H, xu, gg);
+                    if (l == kTraceLayer) stamp(a, 911);
                     wu.dot(H, xu, uu);
+                    if (l == kTraceLayer) stamp(a, 912);
                     if (lane == 0) {
 #pragma unroll
-                        for (int rr = 0; rr < RD; rr += 2) {
-                            if (r + rr < fe) {
-                                const uint32_t lo = (uint32_t)f2h(gg[rr] / (1.0f + __expf(-gg[rr])) * uu[rr]);
-                                const uint32_t hi =
-                                    (uint32_t)f2h(gg[rr + 1] / (1.0f + __expf(-gg[rr + 1])) * uu[rr + 1]);
-                                st_word(a.act + (r + rr) / 2, t, lo | (hi << 16));
-                            }
-                        }
+                        for (int rr = 0; rr < RD; ++rr)
+                            if (r + rr < fe) ar.rows[r + rr - fb] = gg[rr] / (1.0f + __expf(-gg[rr])) * uu[rr];
                     }
                 });
             }
+            __syncthreads();
+            if (l == kTraceLayer) stamp(a, 913);
+            emit_triples(ar.rows, a.act + zl, fwb, fwe, fb, t, flat_row, [&](int W) { return min(3, F - 3 * W); });
         }
         __syncthreads();
         stamp(a, sl + 6);
         // ---- E: down + residual
         {
-            if (!poll_pairs_to_xs<16>(a, ar, a.act + zl, F, tag_of(a, l, 3), 4)) return;
+            if (!poll_triples_to_xs<4>(a, ar, a.act + zl, words3(F), F, tag_of(a, l, 3), 4,
+                                       [&](int i, int j) { return 3 * i + j < F ? 3 * i + j : -1; }))
+                return;
             stamp(a, sl + 7);
-            if (l + 1 < a.L) issue_a(a.layers[l + 1], zl);
             const uint32_t t = tag_of(a, l, 4);
             {
                 XCache<FD, UF> xu;
@@ -977,16 +1230,22 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
                     we.dot(F, xu, o);
                     if (lane == 0) {
 #pragma unroll
-                        for (int rr = 0; rr < RE; ++rr) {
-                            if (r + rr < he) {
-                                const float nv = ar.own[r + rr - hb] + o[rr];
-                                ar.own[r + rr - hb] = nv;
-                                st_word(a.hbuf + r + rr, t, __float_as_uint(nv));
-                            }
-                        }
+                        for (int rr = 0; rr < RE; ++rr)
+                            if (r + rr < he) ar.own[r + rr - hb] += o[rr];
                     }
                 });
             }
+            __syncthreads();
+            emit_triples(ar.own, a.hbuf + zl, hwb, hwe, hb, t, flat_row, [&](int W) { return min(3, H - 3 * W); });
+            // the next layer's A weights and first attention tile stream while
+            // the residual travels to its norm
+            if (l + 1 < a.L) {
+                // the tile first: the compiler waits for every earlier load
+                // before an LDS-DMA issue, and the A weights are not needed yet
+                attn_tile_prefetch<HD>(a, ar, lt[l + 1], pos, zl);
+                issue_a(lt[l + 1], zl);
+            }
+            pin_loads<5>();
         }
         __syncthreads();
         stamp(a, sl + 8);
@@ -1031,12 +1290,12 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             if (ri[i] < 0) continue;
             if (bi < 0 || rv[i] > bv || (rv[i] == bv && ri[i] < bi)) { bv = rv[i]; bi = ri[i]; }
         }
-        st_word(a.cand + 2 * w, tc, __float_as_uint(bv));
-        st_word(a.cand + 2 * w + 1, tc, (uint32_t)bi);
+        st_u32(a.cand + 2 * w, tc, __float_as_uint(bv));
+        st_u32(a.cand + 2 * w + 1, tc, (uint32_t)bi);
     }
     if (w != 0) return;
     float* cv = ar.att;  // 2G values
-    const bool ok = poll_words<4>(a, a.cand, 2 * G, tc, 6, [&](int i, uint32_t v) { cv[i] = __uint_as_float(v); });
+    const bool ok = poll_words<1>(a, a.cand, 2 * G, tc, 6, [&](int i, uint64_t v) { cv[i] = __uint_as_float(word_lo(v)); });
     if (!__syncthreads_and(ok)) return;
     if (wave == 0) {
         // lanes scan strided candidates, then a shuffle tree keeps (max value, lowest index)
@@ -1074,38 +1333,78 @@ using PFn = void (*)(PArgs);
 
 #define BX_PK(FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD)           \
     {{FQ, FV, FO, FGU, FD, FH, UH, UO, UF, HD},                                      \
-     persist_kernel<FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD>, RA}
+     persist_kernel<FQ, FV, FO, FGU, FD, FH, UH, UO, UF, RA, RC, RD, RE, RH, HD>, RA, RC, RD, RE}
 
 struct PEntry {
     PKey k;
     PFn fn;
-    int ra;
+    int ra, rc, rd, re;
 };
 
 // Instantiated shapes: the BASELINE format mixes at their widths and the small
 // test models of the same mixes.  RA..RH: rows per wave task of stages A, C, D
-// (per matrix), E and the head.
+// (per matrix), E and the head.  Rows per workgroup come in whole triples of
+// the hand-off words, so RC / RE cover ceil(words3(H) / CUs) triples in one
+// round of the four waves.
 const PEntry kPersistTable[] = {
     // Q4_K with Q6_K v/down/output (1.7B: H 2048, F 6144; test: H 256, F 768)
-    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 3, 4, 2, 6, 2, 8, 128),
-    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 1, 4, 2, 6, 2, 8, 64),
+    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 3, 5, 3, 6, 3, 8, 128),
+    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 1, 5, 3, 6, 3, 8, 64),
     // all Q8_0, tied FP16 lm_head (0.6B: H 1024, F 3072, qd 2048; test: H 512, F 1024, qd 512)
     BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 2, 4, 2, 6, 2, 4, 128),
     BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 1, 4, 2, 6, 2, 4, 64),
     // Q4_K everywhere with Q6_K output (8B: H 4096, F 12288)
-    BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 4, 4, 4, 2, 4, 128),
+    BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 6, 5, 4, 5, 4, 128),
 };
 
 struct PLayout {
-    size_t ctrl, hbuf, qkv, attn, act, part, cand, total;
+    size_t ctrl, hbuf, qw, kw, vw, attn, act, part, cand, total;
+    size_t part_stride;   // words per KV group
     size_t lds;
     int smax;
-    int ra;
+    int g_q, g_k;         // stage A workgroups of the q and k segments (v: the rest)
     PFn fn;
 };
 
+// Stage A split of the per-head q / k / v triples over G workgroups: every
+// segment gets at least the workgroups that keep each one within one task
+// round of its waves (cap words), spare workgroups go one by one to the
+// segment with the most bytes per workgroup.  Without room for one round,
+// proportional to bytes.
+static void split_stage_a(int G, const int (&words)[3], const double (&bpw)[3], int cap, int (&n)[3]) {
+    int sum = 0;
+    for (int i = 0; i < 3; ++i) {
+        n[i] = (words[i] + cap - 1) / cap;
+        sum += n[i];
+    }
+    if (sum > G) {
+        const double tot = words[0] * bpw[0] + words[1] * bpw[1] + words[2] * bpw[2];
+        sum = 0;
+        for (int i = 0; i < 3; ++i) {
+            n[i] = (int)(G * words[i] * bpw[i] / tot);
+            if (n[i] < 1) n[i] = 1;
+            sum += n[i];
+        }
+        while (sum > G) {
+            const int i = n[0] >= n[1] && n[0] >= n[2] ? 0 : (n[1] >= n[2] ? 1 : 2);
+            --n[i];
+            --sum;
+        }
+    }
+    while (sum < G) {
+        int best = 0;
+        double bb = -1.0;
+        for (int i = 0; i < 3; ++i) {
+            const double per = words[i] * bpw[i] / n[i];
+            if (per > bb) { bb = per; best = i; }
+        }
+        ++n[best];
+        ++sum;
+    }
+}
+
 int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
-    const int hd = d.head_dim, qd = d.n_q * hd, kvd = d.n_kv * hd;
+    const int hd = d.head_dim, qd = d.n_q * hd;
     if (d.n_kv <= 0 || d.n_q % d.n_kv) return fail(BX_EINVAL, "persist: bad head counts");
     const int Gq = d.n_q / d.n_kv;
     if (Gq > kMaxGq) return fail(BX_EUNSUPPORTED, "persist: more than 8 query heads per KV head");
@@ -1117,41 +1416,58 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
     if (d.hidden % 256 || d.intermediate % 256 || qd % 256) return fail(BX_EUNSUPPORTED, "persist: widths");
     const int smax = G / d.n_kv;
     if (smax < 1 || G < 3) return fail(BX_EUNSUPPORTED, "persist: too few CUs");
-    if ((d.hidden + G - 1) / G > kMaxOwn) return fail(BX_EUNSUPPORTED, "persist: hidden too wide for the grid");
-    // a combiner holds S * Gq * (dsl + 2) floats of the attention scratch, S <= smax, dsl <= hd / S + 2,
-    // and Gq * S split weights
-    const size_t att_bytes = att_scratch_bytes(hd, Gq);
-    const size_t rec_bytes = (size_t)Gq * (hd + 5 * smax) * 4;   // records + split weights
-    size_t lds = arena_bytes(d.hidden, d.intermediate, qd, hd, Gq);
-    if (rec_bytes > att_bytes) lds += rec_bytes - att_bytes;
-    if ((size_t)2 * G * 4 > att_bytes) return fail(BX_EUNSUPPORTED, "persist: candidate buffer");
-    if (lds > 160 * 1024) return fail(BX_EUNSUPPORTED, "persist: LDS budget exceeded");
     const PKey want{d.qkv_type_q, d.qkv_type_v, d.o_type, d.gate_type, d.down_type, d.lm_type,
                     upl_for(d.hidden), upl_for(qd), upl_for(d.intermediate), hd};
-    o.fn = nullptr;
+    const PEntry* ent = nullptr;
     for (const PEntry& e : kPersistTable) {
         if (e.k.fq == want.fq && e.k.fv == want.fv && e.k.fo == want.fo && e.k.fgu == want.fgu &&
             e.k.fd == want.fd && e.k.fh == want.fh && e.k.uh == want.uh && e.k.uo == want.uo && e.k.uf == want.uf &&
             e.k.hd == want.hd)
-        {
-            o.fn = e.fn;
-            o.ra = e.ra;
-        }
+            ent = &e;
     }
-    if (!o.fn) return fail(BX_EUNSUPPORTED, "persist: no instantiation for this format mix / width");
+    if (!ent) return fail(BX_EUNSUPPORTED, "persist: no instantiation for this format mix / width");
+    o.fn = ent->fn;
+    // rows per workgroup of the residual and SwiGLU triples (LDS holds kMaxOwn)
+    const int hw = head_words(hd);
+    if (3 * ((words3(d.hidden) + G - 1) / G) > kMaxOwn || 3 * ((words3(d.intermediate) + G - 1) / G) > kMaxOwn)
+        return fail(BX_EUNSUPPORTED, "persist: hidden / intermediate too wide for the grid");
+    // stage A split
+    auto row_bytes = [&](int t) {
+        return (double)type_block_bytes(t) * (double)(d.hidden / type_block_elems(t));
+    };
+    const int words[3] = {d.n_q * hw, d.n_kv * hw, d.n_kv * hw};
+    const double bpw[3] = {3 * row_bytes(d.qkv_type_q), 3 * row_bytes(d.qkv_type_k), 3 * row_bytes(d.qkv_type_v)};
+    int n[3];
+    split_stage_a(G, words, bpw, kPW * ent->ra / 3, n);
+    for (int i = 0; i < 3; ++i)
+        if (n[i] < 1 || 3 * ((words[i] + n[i] - 1) / n[i]) > kMaxOwn)
+            return fail(BX_EUNSUPPORTED, "persist: q / k / v too wide for the grid");
+    o.g_q = n[0];
+    o.g_k = n[1];
+    // LDS: the arena, with the attention scratch grown to a combiner's records
+    // or the head's 2G argmax candidates if either is larger
+    const size_t att_bytes = att_scratch_bytes(hd, Gq);
+    const size_t comb_bytes = comb_lds_floats(hd, Gq, smax) * 4;
+    size_t lds = arena_bytes(d.hidden, d.intermediate, qd, hd, Gq);
+    if (comb_bytes > att_bytes) lds += comb_bytes - att_bytes;
+    if ((size_t)2 * G * 4 > att_bytes) return fail(BX_EUNSUPPORTED, "persist: candidate buffer");
+    if (lds > 160 * 1024) return fail(BX_EUNSUPPORTED, "persist: LDS budget exceeded");
     size_t off = 0;
-    auto take = [&](size_t bytes) {
+    auto take = [&](size_t words_) {
         const size_t r = off;
-        off += (bytes + 255) / 256 * 256;
+        off += (words_ * 8 + 255) / 256 * 256;
         return r;
     };
-    o.ctrl = take(256);
-    o.hbuf = take((size_t)d.hidden * 8);
-    o.qkv = take((size_t)(qd + 2 * kvd) * 8);
-    o.attn = take((size_t)qd / 2 * 8);
-    o.act = take((size_t)d.intermediate / 2 * 8);
-    o.part = take((size_t)d.n_kv * part_words_per_group(hd, Gq, smax) * 8);
-    o.cand = take((size_t)2 * G * 8);
+    o.ctrl = take(32);
+    o.hbuf = take(words3(d.hidden));
+    o.qw = take((size_t)d.n_q * hw);
+    o.kw = take((size_t)d.n_kv * hw);
+    o.vw = take((size_t)d.n_kv * hw);
+    o.attn = take((size_t)d.n_q * hw);
+    o.act = take(words3(d.intermediate));
+    o.part_stride = (part_words_per_group(hd, Gq, smax) + 1) & ~(size_t)1;
+    o.part = take((size_t)d.n_kv * o.part_stride);
+    o.cand = take((size_t)2 * G);
     o.total = off;
     o.lds = lds;
     o.smax = smax;
@@ -1161,6 +1477,14 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
 int persist_grid() { return num_cus(); }
 
 uint64_t* g_trace = nullptr;   // set by bx_persist_trace
+
+// Workspace (re)initialization: control block zeroed (no abort), every
+// hand-off word all-ones (a tag no step writes).
+__global__ void persist_ws_init_kernel(uint32_t* ctrl, uint64_t* words, size_t nwords) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 64) ctrl[i] = 0u;
+    for (size_t j = i; j < nwords; j += (size_t)gridDim.x * blockDim.x) words[j] = ~0ull;
+}
 
 }  // namespace
 }  // namespace bx
@@ -1172,42 +1496,34 @@ extern "C" size_t bx_persist_ws_bytes(const bx_decode_dims* d) {
     return o.total;
 }
 
+extern "C" int bx_persist_ws_init(const bx_decode_dims* d, void* ws, void* stream) {
+    if (!d || !ws) return bx::fail(BX_EINVAL, "persist_ws_init: null pointer");
+    bx::PLayout o{};
+    if (int rc = bx::persist_layout(*d, bx::persist_grid(), o)) return rc;
+    unsigned char* base = static_cast<unsigned char*>(ws);
+    const size_t nwords = (o.total - o.hbuf) / 8;
+    hipLaunchKernelGGL(bx::persist_ws_init_kernel, dim3(256), dim3(256), 0, bx::as_stream(stream),
+                       reinterpret_cast<uint32_t*>(base + o.ctrl), reinterpret_cast<uint64_t*>(base + o.hbuf), nwords);
+    if (hipGetLastError() != hipSuccess) return bx::fail(BX_ELAUNCH, "persist_ws_init: launch failed");
+    return BX_OK;
+}
+
 extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev,
                                const uint16_t* embed, const uint16_t* final_norm, const void* lm_head,
                                const float* cos_tab, const float* sin_tab, int32_t* scal, uint16_t* logits,
                                void* ws, uint32_t epoch, void* stream) {
     if (!d || !layers_dev || !embed || !final_norm || !lm_head || !cos_tab || !sin_tab || !scal || !logits || !ws)
         return bx::fail(BX_EINVAL, "persist: null pointer");
-    if (n_layers <= 0 || n_layers > 127) return bx::fail(BX_EINVAL, "persist: layer count");
-    if (epoch == 0 || epoch >= (1u << 22)) return bx::fail(BX_EINVAL, "persist: epoch out of range");
+    if (n_layers <= 0 || n_layers > 126) return bx::fail(BX_EINVAL, "persist: layer count");
+    if (epoch == 0 || epoch >= 64) return bx::fail(BX_EINVAL, "persist: epoch out of range (1..63)");
     const int G = bx::persist_grid();
     bx::PLayout o{};
     if (int rc = bx::persist_layout(*d, G, o)) return rc;
-    const int hd = d->head_dim, qd = d->n_q * hd, kvd = d->n_kv * hd;
+    const int hd = d->head_dim;
     bx::PArgs a{};
     a.H = d->hidden; a.F = d->intermediate; a.n_q = d->n_q; a.n_kv = d->n_kv; a.hd = hd; a.V = d->vocab;
     a.cap = d->cap; a.L = n_layers; a.eps = d->eps;
-    // stage A: when the grid has room, give every q / k workgroup at most one
-    // round of rows (kPW waves x RA rows: all of them prefetched before the
-    // residual poll) and v the rest; otherwise split in proportion to bytes.
-    const int rnd = bx::kPW * o.ra;
-    const int nq = (qd + rnd - 1) / rnd, nk = (kvd + rnd - 1) / rnd;
-    auto row_bytes = [&](int t) {
-        return (double)bx::type_block_bytes(t) * (double)(d->hidden / bx::type_block_elems(t));
-    };
-    const double bq = row_bytes(d->qkv_type_q) * qd;
-    const double bk = row_bytes(d->qkv_type_k) * kvd;
-    const double bv = row_bytes(d->qkv_type_v) * kvd;
-    int gq = (int)(G * bq / (bq + bk + bv) + 0.5), gk = (int)(G * bk / (bq + bk + bv) + 0.5);
-    if (nq + 2 * nk <= G) {
-        gq = nq;
-        gk = nk;
-    }
-    if (gq < 1) gq = 1;
-    if (gk < 1) gk = 1;
-    if (gq + gk > G - 1) gk = G - 1 - gq;
-    if (gk < 1) return bx::fail(BX_EUNSUPPORTED, "persist: grid too small");
-    a.g_q = gq; a.g_k = gk;
+    a.g_q = o.g_q; a.g_k = o.g_k;
     a.epoch = epoch;
     a.layers = layers_dev;
     a.embed = embed; a.final_norm = final_norm; a.lm_head = lm_head; a.cos_t = cos_tab; a.sin_t = sin_tab;
@@ -1215,13 +1531,18 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     unsigned char* base = static_cast<unsigned char*>(ws);
     a.ctrl = reinterpret_cast<uint32_t*>(base + o.ctrl);
     a.hbuf = reinterpret_cast<uint64_t*>(base + o.hbuf);
-    a.qkv = reinterpret_cast<uint64_t*>(base + o.qkv);
+    a.qw = reinterpret_cast<uint64_t*>(base + o.qw);
+    a.kw = reinterpret_cast<uint64_t*>(base + o.kw);
+    a.vw = reinterpret_cast<uint64_t*>(base + o.vw);
     a.attn = reinterpret_cast<uint64_t*>(base + o.attn);
     a.act = reinterpret_cast<uint64_t*>(base + o.act);
     a.part = reinterpret_cast<uint64_t*>(base + o.part);
+    a.part_stride = (int64_t)o.part_stride;
     a.cand = reinterpret_cast<uint64_t*>(base + o.cand);
     a.trace = bx::g_trace;
     hipStream_t st = bx::as_stream(stream);
+    o.lds += bx::layer_table_bytes(n_layers);
+    if (o.lds > 160 * 1024) return bx::fail(BX_EUNSUPPORTED, "persist: LDS budget exceeded (layer table)");
     if (o.lds > 64 * 1024) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(o.fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)o.lds) != hipSuccess)

@@ -174,14 +174,17 @@ int bx_decode_advance(int32_t* tok_dev, int32_t* pos_dev, const int32_t* next_de
  * each other through tagged words in `ws` instead of kernel boundaries
  * (replaces the captured step of dense_decoder.cpp:335-524 as a whole).
  * bx_persist_ws_bytes returns 0 (with a message) for shapes/format mixes it
- * does not cover.  `ws` must be zeroed once before the first step; `epoch`
- * must grow by one per launch on that ws (1 <= epoch < 2^22; re-zero ws and
- * restart at 1 when it runs out).  `layers_dev` is a device array of
- * n_layers bx_decode_layer.  scal = {tok, pos, next, count, hist[...]} as for
- * bx_decode_advance.  bx_persist_status reads the abort flag after the
- * launches completed (caller synchronizes): 0 ok, 1 aborted (`site` names the
- * wait that timed out). */
+ * does not cover.  bx_persist_ws_init (stream-ordered, a fill kernel: no
+ * memset node) must run on `ws` before the first step, after an aborted step,
+ * and before each cycle of epochs: `epoch` grows by one per launch on that ws
+ * through 1..63, then the caller re-initializes ws and restarts at 1 (the
+ * hand-off words carry 16-bit tags).  `layers_dev` is a device array of
+ * n_layers (<= 126) bx_decode_layer.  scal = {tok, pos, next, count,
+ * hist[...]} as for bx_decode_advance.  bx_persist_status reads the abort
+ * flag after the launches completed (caller synchronizes): 0 ok, 1 aborted
+ * (`site` names the wait that timed out). */
 size_t bx_persist_ws_bytes(const bx_decode_dims* d);
+int bx_persist_ws_init(const bx_decode_dims* d, void* ws, void* stream);
 int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev,
                     const uint16_t* embed, const uint16_t* final_norm, const void* lm_head, const float* cos_tab,
                     const float* sin_tab, int32_t* scal, uint16_t* logits, void* ws, uint32_t epoch, void* stream);
@@ -191,8 +194,10 @@ int bx_persist_status(const void* ws, uint32_t* site);
  * constant-rate counter) at each stage boundary of each workgroup into
  * buf_dev[wg * 1024 + slot]: slot 0 start, 1 + 10 l + {0 A input, 1 A done,
  * 2 B done, 3 C input, 4 C done, 5 D input, 6 D done, 7 E input, 8 E done},
- * 1 + 10 L + {0 head input, 1 head rows done, 2 step done (workgroup 0)}.
- * slots_per_wg must be >= 1024.  NULL switches it off. */
+ * 1 + 10 L + {0 head input, 1 head rows done, 2 step done (workgroup 0)};
+ * for layer 14 also the attention sub-stages (900-907) and the gate/up
+ * sub-stages (910 activation cached, 911 gate dots, 912 up dots, 913 all
+ * waves done).  slots_per_wg must be >= 1024.  NULL switches it off. */
 int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg);
 
 /* Device greedy argmax over FP16 logits, lowest index wins ties

@@ -215,6 +215,29 @@ def test_persistent_step_many_splits_vs_oracle(ba, small_gguf):
         tok = int(b.argmax())
 
 
+def test_persistent_tag_cycles_are_invisible(ba, small_gguf):
+    """The hand-off words carry 16-bit tags, re-initialized every 63 launches:
+    150 steps cross two cycle boundaries, at different steps in two models
+    (one ran 37 extra steps first).  Greedy tokens are identical, and the
+    logits after the boundaries still match the oracle."""
+    a = _load(ba, small_gguf, cap=256)
+    b = _load(ba, small_gguf, cap=256)
+    assert a.decode_mode() == b.decode_mode() == "persistent"
+    prompt = [3, 1, 4, 1, 5]
+    a.forward(prompt)
+    b.forward(prompt)
+    b.decode_greedy(9, 37)
+    b.truncate_cache(len(prompt))
+    ta = a.decode_greedy(2, 150)
+    tb = b.decode_greedy(2, 150)
+    assert ta == tb
+    got = a.forward_last([ta[-1]])
+    om = oracle.Model(str(small_gguf))
+    om.allocate_cache(256)
+    want = om.forward(prompt + [2] + ta, last_only=True)[0]
+    assert np.abs(got - want).max() <= LOGIT_TOL
+
+
 def test_cache_errors_raise(ba, small_gguf):
     m = _load(ba, small_gguf, cap=8)
     with pytest.raises(Exception):
