@@ -553,6 +553,9 @@ __device__ __forceinline__ void load_xu_all(const uint32_t* xs, const float* xsu
         const int u = lane + 64 * i;
         if (u < U) xu[i] = load_xu<FMT>(xs, xsum, u);
     }
+    // keep the LDS reads issued together, ahead of their first use (the
+    // scheduler would otherwise pair each read with its use)
+    asm volatile("" ::: "memory");
 }
 
 }  // namespace bx

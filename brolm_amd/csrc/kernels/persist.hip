@@ -27,6 +27,7 @@
 //   E  rows of Wd owned by w + residual
 // Head: rms_norm(h) -> lm_head rows -> FP16 logits + per-WG argmax; WG 0
 // reduces the candidates (lowest index on ties) and advances tok/pos.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -83,6 +84,17 @@ __host__ __device__ constexpr int words3(int n) { return (n + 2) / 3; }
 // others.
 __host__ __device__ constexpr int head_words(int hd) { return (words3(hd) + 1) & ~1; }
 
+// x / d for 0 <= x < 2^16 and 1 <= d <= 2^16 by a multiply-high with
+// ceil(2^32 / d): the error x / 2^32 < 2^-16 never crosses an integer, since
+// fractional parts of x / d are multiples of 1 / d.  A runtime integer
+// division would cost tens of instructions inside a poll loop.
+struct FastDiv {
+    uint32_t d, m;
+    __device__ __forceinline__ explicit FastDiv(int d_)
+        : d((uint32_t)d_), m((uint32_t)(0xffffffffu / (uint32_t)d_) + 1u) {}
+    __device__ __forceinline__ int div(int x) const { return d == 1 ? x : (int)__umulhi((uint32_t)x, m); }
+};
+
 __device__ __forceinline__ uint64_t ld_word(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -123,6 +135,11 @@ __device__ __forceinline__ int opaque_zero() {
 // the weight loads to their first use (past the polls in between) and waits
 // for them there, so nothing is in flight ahead of time.  It emits no
 // instruction and does not wait for the loads.
+// Compiler barrier after a batch of LDS reads: keeps the reads issued
+// together, ahead of their uses (otherwise each read may be scheduled next to
+// its use, one LDS latency per read).
+__device__ __forceinline__ void lds_batch() { asm volatile("" ::: "memory"); }
+
 template <int ID>
 __device__ __forceinline__ void pin_loads() { asm volatile("; prefetch point %0" ::"i"(ID) : "memory"); }
 
@@ -502,16 +519,43 @@ __device__ __forceinline__ void split_plan(int n, int smax, int& kps, int& S) {
 __host__ __device__ inline int comb_words(int hd, int S) { return (head_words(hd) + S - 1) / S; }
 __host__ __device__ inline int rec_words(int wpc) { return (3 * wpc + 2 + 1) & ~1; }
 
-// Attention scratch inside the arena (host and device agree on this size).
+// Attention scratch inside the arena (host and device agree on this size):
+// the key and value tiles, the group's raw q / k / v rows, and per wave its
+// roped q heads (at most two), the current key and value rows, and the
+// scores and probabilities of its keys.
+__host__ __device__ inline size_t att_wave_floats(int hd) { return (size_t)2 * hd + hd + 2 * kTile; }
 __host__ __device__ inline size_t att_scratch_bytes(int hd, int Gq) {
-    return (size_t)Gq * hd * 6             // q16 pairs, qraw
-           + (size_t)hd * 12               // kraw, vraw, kcur, vcur
-           + (size_t)kTile * hd * 4        // kt, vt
-           + (size_t)Gq * kTile * 6        // sc, p16
-           + (size_t)Gq * 12               // mrun, lrun, alph
-           + (size_t)kPT * 8               // slice partials
-           + 256;
+    return (size_t)2 * kTile * hd * 2 + (size_t)(Gq + 2) * hd * 4 + (size_t)kPW * att_wave_floats(hd) * 4;
 }
+// Key parts per head and heads per wave of the attention stage: the waves
+// split the key range of a split (P parts) when there are fewer heads than
+// waves, else take HPW heads each.
+__host__ __device__ inline int att_parts(int Gq) { return Gq >= kPW ? 1 : kPW / Gq; }
+__host__ __device__ inline int att_heads_per_wave(int Gq) { return Gq > kPW ? Gq / kPW : 1; }
+
+template <int HD>
+struct AttScratch {
+    uint16_t* kt;   // kTile x HD, 16-byte chunks XOR-swizzled by the key
+    uint16_t* vt;   // kTile x HD
+    float* qraw;    // Gq x HD
+    float* kraw;    // HD
+    float* vraw;    // HD
+    float* wv;      // this wave's area
+    __device__ __forceinline__ AttScratch(const Arena& ar, int Gq) {
+        kt = reinterpret_cast<uint16_t*>(ar.att);
+        vt = kt + kTile * HD;
+        qraw = reinterpret_cast<float*>(vt + kTile * HD);
+        kraw = qraw + Gq * HD;
+        vraw = kraw + HD;
+        wv = vraw + HD + (tidx() >> 6) * att_wave_floats(HD);
+    }
+    // wave area: q16 [2 x HD/2 pairs] | kcur [HD/2] | vcur [HD/2] | sw [kTile] | pw [kTile]
+    __device__ __forceinline__ uint32_t* q16(int hh) const { return reinterpret_cast<uint32_t*>(wv) + hh * (HD / 2); }
+    __device__ __forceinline__ uint32_t* kcur() const { return reinterpret_cast<uint32_t*>(wv) + HD; }
+    __device__ __forceinline__ uint32_t* vcur() const { return kcur() + HD / 2; }
+    __device__ __forceinline__ float* sw() const { return wv + 2 * HD; }
+    __device__ __forceinline__ float* pw() const { return sw() + kTile; }
+};
 
 // HBM -> LDS copies (global_load_lds_dwordx4): lane L of a wave writes the 16
 // bytes at its own source address to lds_base + 16 L.
@@ -541,21 +585,23 @@ __device__ __forceinline__ void dma_tile(const uint16_t* Kc, const uint16_t* Vc,
 }
 
 // Words of the split records per KV group, for the largest of any S <= smax:
-// ncomb slices x S splits x Gq heads x (dsl partial sums + m + l).
+// ncomb slices x S P partials (P key parts per split) x Gq heads x (dsl
+// partial sums + m + l).
 inline size_t part_words_per_group(int hd, int Gq, int smax) {
     size_t best = 0;
     for (int S = 1; S <= smax; ++S) {
         const int wpc = comb_words(hd, S), ncomb = (head_words(hd) + wpc - 1) / wpc;
-        const size_t n = (size_t)ncomb * S * Gq * rec_words(wpc);
+        const size_t n = (size_t)ncomb * S * att_parts(Gq) * Gq * rec_words(wpc);
         if (n > best) best = n;
     }
     return best;
 }
-// LDS floats a combiner needs: S x Gq records of dsl + 2 and Gq x S weights.
+// LDS floats a combiner needs: S P x Gq records of dsl + 2 and Gq x S P weights.
 inline size_t comb_lds_floats(int hd, int Gq, int smax) {
     size_t best = 0;
     for (int S = 1; S <= smax; ++S) {
-        const size_t n = (size_t)S * Gq * rec_words(comb_words(hd, S)) + (size_t)Gq * S;
+        const size_t Sp = (size_t)S * att_parts(Gq);
+        const size_t n = Sp * Gq * rec_words(comb_words(hd, S)) + (size_t)Gq * Sp;
         if (n > best) best = n;
     }
     return best;
@@ -621,13 +667,6 @@ __device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t 
     }
 }
 
-// Key tile of the attention scratch: after q16 [Gq HD/2], qraw [Gq HD],
-// kraw, vraw [HD each], kcur, vcur [HD/2 each] (4-byte units).
-template <int HD>
-__device__ __forceinline__ uint16_t* att_key_tile(const Arena& ar, int Gq) {
-    return reinterpret_cast<uint16_t*>(ar.att + Gq * HD / 2 + Gq * HD + 3 * HD);
-}
-
 // The first tile of cached keys / values of this workgroup's attention split
 // (rows below pos, written by earlier steps) goes straight to LDS.  Issued
 // right after the previous stage's output stores, so the copy overlaps the
@@ -636,7 +675,7 @@ template <int HD>
 __device__ __forceinline__ void attn_tile_prefetch(const PArgs& a, const Arena& ar, const bx_decode_layer& Ly,
                                                    int pos, int zl) {
     const int G = gridDim.x, w = blockIdx.x;
-    const int Gq = a.n_q / a.n_kv, kvd = a.n_kv * HD;
+    const int kvd = a.n_kv * HD;
     const int smax = G / a.n_kv;
     const int g = w % a.n_kv, s = w / a.n_kv;
     if (s >= smax) return;
@@ -644,26 +683,28 @@ __device__ __forceinline__ void attn_tile_prefetch(const PArgs& a, const Arena& 
     split_plan(pos + 1, smax, kps, S);
     if (s >= S) return;
     const int kb = s * kps + zl, ke = min(pos + 1, kb + kps);
-    uint16_t* kt = att_key_tile<HD>(ar, Gq);
-    uint16_t* vt = kt + kTile * HD;
+    uint16_t* kt = reinterpret_cast<uint16_t*>(ar.att);
     dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), kvd, (int64_t)g * HD, kb,
-                 min(kTile, ke - kb), kt, vt);
+                 ke - kb, kt, kt + kTile * HD);
 }
 
-// Stage B for (KV group g, split s) = (w % n_kv, w / n_kv).  The first tile of
-// cached keys / values is already on its way (attn_tile_prefetch); the static
-// per-row vectors are requested before q is polled.  Scores: FP16 q . K via v_dot2 over all waves, scaled in FP32;
-// softmax per head with the running max / sum across tiles; P.V via v_dot2
-// over key pairs (V staged as (v_2j[d], v_2j+1[d]) pairs).  Each split writes
-// its record in ncomb slices of head dims; split c < ncomb merges slice c of
-// all splits and writes those dims of the group's FP16 attention output.
+// Stage B for (KV group g, split s) = (w % n_kv, w / n_kv), keys [kb, ke) of
+// the split in one LDS tile (the host keeps the cache within smax tiles).
+// Every wave works alone on P key parts x HPW heads: q-norm + RoPE of its
+// heads, the current key / value (the part holding pos), scores by v_dot2
+// with four lanes per key, its own softmax (running max and sum of its keys
+// only), P.V with two head dims per lane, and a partial record [o, m, l] per
+// (split, part, head).  One barrier (the polled q / k / v and the tile) for
+// the whole computation.  Split c < ncomb then merges slice c of all S P
+// partials of its group and writes those dims of the FP16 attention output.
 template <int HD>
 __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar, const bx_decode_layer& Ly,
                                                 int layer, int pos, int zl) {
-    constexpr int CPK = HD / 8;                     // 16-byte chunks per key row
-    constexpr int kMaxItems = 4;                    // Gq * HD / 2 <= kPT * kMaxItems
+    constexpr int CPK = HD / 8;     // 16-byte chunks per key row
+    constexpr int QC = CPK / 4;     // chunks per lane of a four-lane key dot
+    constexpr int hw = head_words(HD);
     const int G = gridDim.x, w = blockIdx.x;
-    const int Gq = a.n_q / a.n_kv, qd = a.n_q * HD, kvd = a.n_kv * HD;
+    const int Gq = a.n_q / a.n_kv, kvd = a.n_kv * HD;
     const int smax = G / a.n_kv;
     const int g = w % a.n_kv, s = w / a.n_kv;
     if (s >= smax) return true;
@@ -674,42 +715,27 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     const bool has_cur = ke == pos + 1;
     const int wave = tidx() >> 6, lane = tidx() & 63;
     const uint32_t tin = tag_of(a, layer, 0), tout = tag_of(a, layer, 1);
+    const int P = att_parts(Gq), HPW = att_heads_per_wave(Gq), Sp = S * P;
+    const int part = wave % P, h0 = (wave / P) * HPW;
+    const int nk = ke - kb, kpp = (nk + P - 1) / P;
+    const int jb = min(nk, part * kpp), je = min(nk, jb + kpp);   // this wave's tile rows
+    const int jcur = pos - kb;                                      // tile row of pos when has_cur
+    const bool mine_cur = has_cur && jcur >= jb && jcur < je;
+    const AttScratch<HD> sc(ar, Gq);
     if (layer == kTraceLayer) stamp(a, 900 + 0);
-
-    uint32_t* q16 = reinterpret_cast<uint32_t*>(ar.att);          // Gq * HD/2
-    float* qraw = ar.att + Gq * HD / 2;                            // Gq * HD
-    float* kraw = qraw + Gq * HD;                                  // HD
-    float* vraw = kraw + HD;                                       // HD
-    uint32_t* kcur = reinterpret_cast<uint32_t*>(vraw + HD);      // HD/2
-    uint32_t* vcur = kcur + HD / 2;                                // HD/2
-    uint16_t* kt = att_key_tile<HD>(ar, Gq);                        // kTile x HD, 16-byte chunks XOR-swizzled
-    uint16_t* vt = kt + kTile * HD;                                // kTile x HD
-    float* sc = reinterpret_cast<float*>(vt + kTile * HD);        // Gq x kTile
-    uint32_t* p16 = reinterpret_cast<uint32_t*>(sc + Gq * kTile); // Gq x kTile/2
-    float* mrun = reinterpret_cast<float*>(p16 + Gq * kTile / 2); // Gq
-    float* lrun = mrun + Gq;
-    float* alph = lrun + Gq;
-    float* osl = alph + Gq;                                        // 2 kPT
-
-    const uint16_t* Kc = static_cast<const uint16_t*>(Ly.Kc);
-    const uint16_t* Vc = static_cast<const uint16_t*>(Ly.Vc);
-    const int64_t krow0 = (int64_t)g * HD;
-    // the first tile of cached rows was requested by attn_tile_prefetch
     RopeRegs<HD> rr;
     rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2));
     if (layer == kTraceLayer) stamp(a, 900 + 1);
 
-    // q triples of the group's heads, then (split holding pos) k and v.  Each
-    // wave's polls complete after its own tile copies (in-order counters).
-    constexpr int hw = head_words(HD);
-    auto unpack = [](float* dst, int i, uint64_t w) {
+    // one poll over the group's q words and, for the split holding pos, its k
+    // and v words (pairs: hw is even); word offsets from a.qw.  Each wave's
+    // polls complete after its own tile copies (in-order counters).
+    auto unpack = [](float* dst, int i, uint64_t wd) {
         const int h = i / hw, d = 3 * (i - h * hw);
 #pragma unroll
         for (int j = 0; j < 3; ++j)
-            if (d + j < HD) dst[h * HD + d + j] = h2f(word_h(w, j));
+            if (d + j < HD) dst[h * HD + d + j] = h2f(word_h(wd, j));
     };
-    // one poll over the group's q words and, for the split holding pos, its k
-    // and v words (pairs: hw is even); word offsets from a.qw
     const int npq = Gq * hw / 2, npk = has_cur ? hw / 2 : 0;
     const int kofs = (int)(a.kw - a.qw) + g * hw, vofs = (int)(a.vw - a.qw) + g * hw;
     bool ok = poll_pairs<1>(
@@ -717,251 +743,195 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
         [&](int p) {
             return p < npq ? g * Gq * hw + 2 * p : (p < npq + npk ? kofs + 2 * (p - npq) : vofs + 2 * (p - npq - npk));
         },
-        [&](int p, int h, uint64_t w) {
-            if (p < npq) unpack(qraw, 2 * p + h, w);
-            else if (p < npq + npk) unpack(kraw, 2 * (p - npq) + h, w);
-            else unpack(vraw, 2 * (p - npq - npk) + h, w);
+        [&](int p, int h, uint64_t wd) {
+            if (p < npq) unpack(sc.qraw, 2 * p + h, wd);
+            else if (p < npq + npk) unpack(sc.kraw, 2 * (p - npq) + h, wd);
+            else unpack(sc.vraw, 2 * (p - npq - npk) + h, wd);
         });
     __builtin_amdgcn_s_waitcnt(0);   // tile copies of this wave landed (also without polls)
     if (!__syncthreads_and(ok)) return false;
     if (layer == kTraceLayer) stamp(a, 900 + 2);
 
-    for (int h = wave; h < Gq; h += kPW) norm_rope_head<HD>(qraw + h * HD, rr.qg, rr, a.eps, q16 + h * HD / 2);
-    if (has_cur && wave == kPW - 1) {
-        norm_rope_head<HD>(kraw, rr.kg, rr, a.eps, kcur);
-        for (int p = lane; p < HD / 2; p += 64) vcur[p] = pack16(vraw[2 * p], vraw[2 * p + 1]);
-    }
-    if (tidx() < Gq) {
-        mrun[tidx()] = -INFINITY;
-        lrun[tidx()] = 0.f;
-    }
-    __syncthreads();
-    if (has_cur) {
-        uint16_t* Kw = static_cast<uint16_t*>(Ly.Kc);
-        uint16_t* Vw = static_cast<uint16_t*>(Ly.Vc);
-        for (int p = tidx(); p < HD / 2; p += kPT) {
-            gptr_w<uint32_t>(Kw + (int64_t)pos * kvd + krow0)[p] = kcur[p];
-            gptr_w<uint32_t>(Vw + (int64_t)pos * kvd + krow0)[p] = vcur[p];
+    // ---- from here each wave works alone
+    for (int hh = 0; hh < HPW; ++hh) norm_rope_head<HD>(sc.qraw + (h0 + hh) * HD, rr.qg, rr, a.eps, sc.q16(hh));
+    if (mine_cur) {
+        uint32_t* kc = sc.kcur();
+        uint32_t* vc = sc.vcur();
+        norm_rope_head<HD>(sc.kraw, rr.kg, rr, a.eps, kc);
+        for (int p = lane; p < HD / 2; p += 64) vc[p] = pack16(sc.vraw[2 * p], sc.vraw[2 * p + 1]);
+        // the current row replaces the stale cache row pos in the tile (another
+        // wave of this part writes the same bytes)
+        for (int d8 = lane; d8 < CPK; d8 += 64) {
+            *reinterpret_cast<u4v*>(sc.kt + jcur * HD + 8 * (d8 ^ (jcur & (CPK - 1)))) =
+                *reinterpret_cast<const u4v*>(kc + 4 * d8);
+            *reinterpret_cast<u4v*>(sc.vt + jcur * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vc + 4 * d8);
+        }
+        // KV-cache row pos: once per group
+        if (h0 == 0) {
+            uint16_t* Kw = static_cast<uint16_t*>(Ly.Kc);
+            uint16_t* Vw = static_cast<uint16_t*>(Ly.Vc);
+            const int64_t krow0 = (int64_t)g * HD;
+            for (int p = lane; p < HD / 2; p += 64) {
+                gptr_w<uint32_t>(Kw + (int64_t)pos * kvd + krow0)[p] = kc[p];
+                gptr_w<uint32_t>(Vw + (int64_t)pos * kvd + krow0)[p] = vc[p];
+            }
         }
     }
+    if (layer == kTraceLayer) stamp(a, 900 + 3);
 
-    // P.V items (head, dim pair) x key-pair slices
-    const int items = Gq * HD / 2;
-    const int nsl = items < kPT ? kPT / items : 1;
-    const int sl = items < kPT ? tidx() / items : 0;
-    const bool pv_on = tidx() < (items < kPT ? items * nsl : kPT);
-    float o0[kMaxItems], o1[kMaxItems];
-#pragma unroll
-    for (int i = 0; i < kMaxItems; ++i) o0[i] = o1[i] = 0.f;
     const float scale = 1.0f / sqrtf((float)HD);
-
-    int ti = 0;
-    for (int c0 = kb; c0 < ke; c0 += kTile, ++ti) {
-        const int nk = min(kTile, ke - c0);
-        if (ti > 0) {   // later tiles (splits longer than one tile)
-            __syncthreads();
-            dma_tile<HD>(Kc, Vc, kvd, krow0, c0, nk, kt, vt);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-        }
-        // the current key / value replace the stale cache row pos in the tile
-        if (pos >= c0 && pos < c0 + nk) {
-            const int j = pos - c0;
-            for (int d8 = tidx(); d8 < CPK; d8 += kPT) {
-                *reinterpret_cast<u4v*>(kt + j * HD + 8 * (d8 ^ (j & (CPK - 1)))) =
-                    *reinterpret_cast<const u4v*>(kcur + 4 * d8);
-                *reinterpret_cast<u4v*>(vt + j * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vcur + 4 * d8);
-            }
-        }
-        __syncthreads();
-        if (layer == kTraceLayer && ti == 0) stamp(a, 900 + 3);
-        // scores of the (head, key < nk) items: a quad of lanes per item, each
-        // lane a quarter of the head dim with all its LDS reads issued at once,
-        // then a quad reduction
-        {
-            constexpr int QC = CPK / 4;   // 16-byte chunks per lane
-            const int qt = tidx() & 3;
-            for (int it = tidx() >> 2; it < Gq * nk; it += kPT / 4) {
-                const int h = it / nk, j = it - h * nk;
-                const uint32_t* q = q16 + h * HD / 2;
-                const uint16_t* kr = kt + j * HD;
-                u4v kk[QC], qq[QC];
-#pragma unroll
-                for (int c = 0; c < QC; ++c) {
-                    const int d8 = qt * QC + c;
-                    kk[c] = *reinterpret_cast<const u4v*>(kr + 8 * (d8 ^ (j & (CPK - 1))));
-                    qq[c] = *reinterpret_cast<const u4v*>(q + 4 * d8);
-                }
-                float acc = 0.f, acc2 = 0.f;
-#pragma unroll
-                for (int c = 0; c < QC; ++c) {
-                    acc = dot2(qq[c].x, kk[c].x, acc);
-                    acc2 = dot2(qq[c].y, kk[c].y, acc2);
-                    acc = dot2(qq[c].z, kk[c].z, acc);
-                    acc2 = dot2(qq[c].w, kk[c].w, acc2);
-                }
-                acc += acc2;
-                acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0xB1, 0xF, 0xF, false));
-                acc += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x4E, 0xF, 0xF, false));
-                if (qt == 0) sc[h * kTile + j] = acc * scale;
-            }
-        }
-        __syncthreads();
-        // softmax update per head: lane owns keys 2 lane, 2 lane + 1 (kTile = 128)
-        for (int h = wave; h < Gq; h += kPW) {
-            const float s0 = 2 * lane < nk ? sc[h * kTile + 2 * lane] : -INFINITY;
-            const float s1 = 2 * lane + 1 < nk ? sc[h * kTile + 2 * lane + 1] : -INFINITY;
-            const float mc = wave_max(fmaxf(s0, s1));
-            const float mo = mrun[h];
-            const float mn = fmaxf(mo, mc);
-            const float p0 = 2 * lane < nk ? r16(__expf(s0 - mn)) : 0.f;
-            const float p1 = 2 * lane + 1 < nk ? r16(__expf(s1 - mn)) : 0.f;
-            const float ps = wave_allsum(p0 + p1);
-            p16[h * kTile / 2 + lane] = pack16(p0, p1);
-            if (lane == 0) {
-                const float al = mo == -INFINITY ? 0.f : __expf(mo - mn);
-                alph[h] = al;
-                lrun[h] = lrun[h] * al + ps;
-                mrun[h] = mn;
-            }
-        }
-        __syncthreads();
-        // P.V: (p_2j, p_2j+1) . (v_2j[d], v_2j+1[d]) by v_dot2 on v_perm-paired rows.
-        // The trip count is padded to a multiple of 4 per slice so that each
-        // step issues four pairs' reads at once; rows at or past nk are read
-        // from row nk - 1 (finite) and meet p = 0 (every pair of the tile holds
-        // its p, zero past nk).  4 nsl divides kTile / 2, so pairs stay in the tile.
-        if (pv_on) {
-            const int npair = (nk + 1) / 2;
-            const int npad = (npair + 4 * nsl - 1) / (4 * nsl) * (4 * nsl);
-#pragma unroll
-            for (int i = 0; i < kMaxItems; ++i) {
-                const int idx = items < kPT ? tidx() % items : tidx() + i * kPT;
-                if ((items < kPT && i == 0) || (items >= kPT && idx < items)) {
-                    const int h = idx / (HD / 2), dp = idx % (HD / 2);
-                    const uint32_t* pp = p16 + h * kTile / 2;
-                    const float al = alph[h];
-                    float a0 = o0[i] * al, a1 = o1[i] * al;
-                    for (int jp = sl; jp < npad; jp += 4 * nsl) {
-                        uint32_t v0[4], v1[4], pv[4];
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const int j2 = jp + u * nsl;
-                            const int r0 = min(2 * j2, nk - 1), r1 = min(2 * j2 + 1, nk - 1);
-                            v0[u] = *reinterpret_cast<const uint32_t*>(vt + r0 * HD + 2 * dp);
-                            v1[u] = *reinterpret_cast<const uint32_t*>(vt + r1 * HD + 2 * dp);
-                            pv[u] = pp[j2];
-                        }
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            a0 = dot2(pv[u], __builtin_amdgcn_perm(v1[u], v0[u], 0x05040100u), a0);
-                            a1 = dot2(pv[u], __builtin_amdgcn_perm(v1[u], v0[u], 0x07060302u), a1);
-                        }
-                    }
-                    o0[i] = a0;
-                    o1[i] = a1;
-                }
-            }
-        }
-        __syncthreads();
-    }
-    if (layer == kTraceLayer) stamp(a, 900 + 4);
-    // fold the key slices
-    if (nsl > 1) {
-        if (pv_on) {
-            osl[2 * tidx()] = o0[0];
-            osl[2 * tidx() + 1] = o1[0];
-        }
-        __syncthreads();
-        if (tidx() < items) {
-            float a0 = 0.f, a1 = 0.f;
-            for (int t = 0; t < nsl; ++t) {
-                a0 += osl[2 * (t * items + tidx())];
-                a1 += osl[2 * (t * items + tidx()) + 1];
-            }
-            o0[0] = a0;
-            o1[0] = a1;
-        }
-    }
-    // split record, in ncomb slices of dsl head dims: [o[dsl], m, l] per (slice, split, head)
     const int wpc = comb_words(HD, S), dsl = 3 * wpc, ncomb = (hw + wpc - 1) / wpc, rec = rec_words(wpc);
     uint64_t* gbase = a.part + zl + (int64_t)g * a.part_stride;
-    auto rec_at = [&](int c, int sp, int h) { return gbase + ((int64_t)(c * S + sp) * Gq + h) * rec; };
+    auto rec_at = [&](int c, int t, int h) { return gbase + ((int64_t)(c * Sp + t) * Gq + h) * rec; };
+    const int nkw = je - jb;   // <= kTile: lane t owns keys jb + t and jb + 64 + t
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = h0 + hh;
+        // scores: one lane per key, the whole head dim (q broadcast from LDS,
+        // the key row swizzled so that lanes hit distinct banks)
+        const uint32_t* q = sc.q16(hh);
+        float sv[2];
 #pragma unroll
-    for (int i = 0; i < kMaxItems; ++i) {
-        const int idx = tidx() + i * kPT;
-        if (idx < items && (nsl == 1 || i == 0)) {
-            const int h = idx / (HD / 2), d = 2 * (idx % (HD / 2));
-            const int c0 = d / dsl, c1 = (d + 1) / dsl;
-            st_u32(rec_at(c0, s, h) + (d - c0 * dsl), tout, __float_as_uint(o0[i]));
-            st_u32(rec_at(c1, s, h) + (d + 1 - c1 * dsl), tout, __float_as_uint(o1[i]));
+        for (int hb = 0; hb < 2; ++hb) {
+            const int t = lane + 64 * hb;
+            sv[hb] = -INFINITY;
+            if (64 * hb < nkw) {   // uniform
+                const int jr = jb + (t < nkw ? t : nkw - 1);
+                const uint16_t* kr = sc.kt + jr * HD;
+                float acc = 0.f, acc2 = 0.f;
+                // batches of eight chunks: all sixteen LDS reads issued before
+                // the math (the barrier keeps the compiler from pairing each
+                // read with its use, which would expose every LDS latency)
+#pragma unroll
+                for (int d0 = 0; d0 < CPK; d0 += 8) {
+                    u4v kk[8], qv[8];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        kk[c] = *reinterpret_cast<const u4v*>(kr + 8 * ((d0 + c) ^ (jr & (CPK - 1))));
+                        qv[c] = *reinterpret_cast<const u4v*>(q + 4 * (d0 + c));
+                    }
+                    lds_batch();
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        acc = dot2(qv[c].x, kk[c].x, acc);
+                        acc2 = dot2(qv[c].y, kk[c].y, acc2);
+                        acc = dot2(qv[c].z, kk[c].z, acc);
+                        acc2 = dot2(qv[c].w, kk[c].w, acc2);
+                    }
+                }
+                if (t < nkw) sv[hb] = (acc + acc2) * scale;
+            }
         }
-    }
-    for (int it = tidx(); it < ncomb * Gq; it += kPT) {
-        const int c = it / Gq, h = it % Gq;
-        uint64_t* r = rec_at(c, s, h);
-        st_u32(r + dsl, tout, __float_as_uint(mrun[h]));
-        st_u32(r + dsl + 1, tout, __float_as_uint(lrun[h]));
-        if (rec > dsl + 2) st_u32(r + dsl + 2, tout, 0u);
-        // the last slice may hold fewer than dsl dims: its unused slots are still
-        // polled by the combiner, so they carry the tag too
-        for (int dd = max(0, HD - c * dsl); dd < dsl; ++dd) st_u32(r + dd, tout, 0u);
+        if (layer == kTraceLayer && hh == 0) stamp(a, 900 + 4);
+        // softmax over this wave's keys, in registers (its own max and sum: the
+        // combiner rescales the partials)
+        const float M = wave_max(fmaxf(sv[0], sv[1]));
+        float pv[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? r16(__expf(sv[hb] - M)) : 0.f;
+        const float L = wave_allsum(pv[0] + pv[1]);
+        // P.V: lane holds head dims 2 lane, 2 lane + 1; the probabilities come
+        // by readlane, the value rows in batches of eight LDS reads
+        float o0 = 0.f, o1 = 0.f;
+        const uint16_t* vcol = sc.vt + jb * HD + 2 * (2 * lane < HD ? lane : 0);
+        for (int t0 = 0; t0 < nkw; t0 += 8) {
+            uint32_t vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t = min(t0 + u, nkw - 1);
+                vv[u] = *reinterpret_cast<const uint32_t*>(vcol + t * HD);
+            }
+            lds_batch();
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int t = t0 + u;   // uniform
+                float p = 0.f;
+                if (t < nkw)
+                    p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                      __builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]), t & 63));
+                o0 += p * h2f(vv[u] & 0xffff);
+                o1 += p * h2f(vv[u] >> 16);
+            }
+        }
+        const int t = s * P + part;
+        if (layer == kTraceLayer && hh == 0) stamp(a, 908);
+        if (2 * lane < HD) {
+            // partial record of (split s, part, head h), in ncomb slices of dsl dims
+            const int d = 2 * lane, c0 = d / dsl, c1 = (d + 1) / dsl;
+            st_u32(rec_at(c0, t, h) + (d - c0 * dsl), tout, __float_as_uint(o0));
+            st_u32(rec_at(c1, t, h) + (d + 1 - c1 * dsl), tout, __float_as_uint(o1));
+        }
+        for (int c = lane; c < ncomb; c += 64) {
+            uint64_t* r = rec_at(c, t, h);
+            st_u32(r + dsl, tout, __float_as_uint(M));
+            st_u32(r + dsl + 1, tout, __float_as_uint(L));
+            if (rec > dsl + 2) st_u32(r + dsl + 2, tout, 0u);
+            // the last slice may hold fewer than dsl dims: its unused slots are still
+            // polled by the combiner, so they carry the tag too
+            for (int dd = max(0, HD - c * dsl); dd < dsl; ++dd) st_u32(r + dd, tout, 0u);
+        }
     }
     if (layer == kTraceLayer) stamp(a, 900 + 5);
     if (s >= ncomb) return true;
 
-    // combiner s: dims [s dsl, s dsl + dsl) of every head of the group
+    // combiner s: dims [s dsl, s dsl + dsl) of every head of the group, over
+    // the S P partials (<= 128).  Records transposed in LDS, recs[j N + t Gq +
+    // h] (N = S P Gq), so lanes that walk partials read consecutive words.
     __syncthreads();
-    float* recs = ar.att;   // S * Gq * rec floats (checked on the host)
-    const uint64_t* mine = gbase + (int64_t)s * S * Gq * rec;
-    ok = poll_words<2>(a, mine, S * Gq * rec, tout, 13, [&](int i, uint64_t v) { recs[i] = __uint_as_float(word_lo(v)); });
+    float* recs = ar.att;   // S P Gq rec floats (checked on the host)
+    const int N = Sp * Gq;
+    const uint64_t* mine = gbase + (int64_t)s * Sp * Gq * rec;
+    const FastDiv drec(rec);
+    ok = poll_words<2>(a, mine, N * rec, tout, 13, [&](int i, uint64_t v) {
+        const int r = drec.div(i);
+        recs[(i - r * rec) * N + r] = __uint_as_float(word_lo(v));
+    });
     if (layer == kTraceLayer) stamp(a, 900 + 6);
     if (!__syncthreads_and(ok)) return false;
-    // split weights exp(m_t - M) / L, one wavefront per head, splits over lanes
-    float* wgt = recs + S * Gq * rec;   // Gq * S floats
-    for (int h = wave; h < Gq; h += kPW) {
-        float M = -INFINITY;
-        for (int t = lane; t < S; t += 64) M = fmaxf(M, recs[(t * Gq + h) * rec + dsl]);
-        M = wave_max(M);
+    // one wave per (head, third of the slice's words): the partial weights
+    // exp(m_t - M) / L with partials over lanes, then one wave sum per dim
+    // output words [s wpc, s wpc + nws) of every head of the group
+    const int nws = min(wpc, hw - s * wpc);
+    for (int job = wave; job < Gq * 3; job += kPW) {
+        const int h = job % Gq, third = job / Gq;
+        const int kb3 = nws * third / 3, ke3 = nws * (third + 1) / 3;
+        if (kb3 >= ke3) continue;   // uniform
+        float mt[2], wt[2], lt[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const int t = lane + 64 * hb;
+            mt[hb] = t < Sp ? recs[dsl * N + t * Gq + h] : -INFINITY;
+            lt[hb] = t < Sp ? recs[(dsl + 1) * N + t * Gq + h] : 0.f;
+        }
+        lds_batch();
+        const float M = wave_max(fmaxf(mt[0], mt[1]));
         float lsum = 0.f;
-        for (int t = lane; t < S; t += 64) {
-            const float* r = recs + (t * Gq + h) * rec;
-            const float wt = r[dsl] == -INFINITY ? 0.f : __expf(r[dsl] - M);
-            wgt[h * S + t] = wt;
-            lsum += wt * r[dsl + 1];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const int t = lane + 64 * hb;
+            wt[hb] = mt[hb] == -INFINITY ? 0.f : __expf(mt[hb] - M);
+            if (t < Sp) lsum += wt[hb] * lt[hb];
         }
         lsum = wave_allsum(lsum);
         const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-        for (int t = lane; t < S; t += 64) wgt[h * S + t] *= inv;
-    }
-    __syncthreads();
-    // output words [s wpc, s wpc + nws) of every head of the group: Q lanes per
-    // word (the power of two >= S, at most 16) sum strided splits, then a
-    // shuffle tree (a fixed order: the result is deterministic)
-    const int nws = min(wpc, hw - s * wpc);
-    const int Q = S > 8 ? 16 : (S > 4 ? 8 : (S > 2 ? 4 : (S > 1 ? 2 : 1)));
-    const int qi = tidx() & (Q - 1);
-    for (int it0 = 0; it0 < Gq * nws; it0 += kPT / Q) {
-        const int it = it0 + tidx() / Q;
-        const bool on = it < Gq * nws;
-        const int h = on ? it / nws : 0, k = on ? it % nws : 0;
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f;
-        if (on) {
-            for (int t = qi; t < S; t += Q) {
-                const float* r = recs + (t * Gq + h) * rec + 3 * k;
-                const float wt = wgt[h * S + t];
-                acc0 += wt * r[0];
-                acc1 += wt * r[1];
-                acc2 += wt * r[2];
-            }
+        for (int k = kb3; k < ke3; ++k) {
+            float ov[3][2];
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const int t = lane + 64 * hb;
+                    ov[j][hb] = t < Sp ? recs[(3 * k + j) * N + t * Gq + h] : 0.f;
+                }
+            lds_batch();
+            float acc[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[j] = wt[0] * ov[j][0] + wt[1] * ov[j][1];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc[j] = wave_allsum(acc[j]) * inv;
+            if (lane == 0)
+                st_h3(a.attn + zl + (int64_t)(g * Gq + h) * hw + s * wpc + k, tout, f2h(acc[0]), f2h(acc[1]),
+                      f2h(acc[2]));
         }
-        for (int m = Q / 2; m >= 1; m >>= 1) {
-            acc0 += __shfl_xor(acc0, m, 64);
-            acc1 += __shfl_xor(acc1, m, 64);
-            acc2 += __shfl_xor(acc2, m, 64);
-        }
-        if (on && qi == 0)
-            st_h3(a.attn + (int64_t)(g * Gq + h) * hw + s * wpc + k, tout, f2h(acc0), f2h(acc1), f2h(acc2));
     }
     if (layer == kTraceLayer) stamp(a, 900 + 7);
     return true;
@@ -1042,6 +1012,7 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     const int wave = tidx() >> 6, lane = tidx() & 63;
     const int tok = a.scal[0], pos = a.scal[1];
     stamp(a, 0);
+    if (a.trace && tidx() == 0) a.trace[(size_t)blockIdx.x * kTraceSlots + 920] = clock64();
 
     constexpr int hw = head_words(HD);
     // residual rows owned by this WG (rows of Wo and Wd): whole triples
@@ -1148,10 +1119,6 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
         stamp(a, sl + 1);
         // ---- B: attention
         if (!__syncthreads_and(attention_stage<HD>(a, ar, Ly, l, pos, zl))) return;
-        // D's weights stream while the attention output travels to the o-proj
-        wg.load(Ly.Wg, F, H, d0 + zl);
-        wu.load(Ly.Wu, F, H, d0 + zl);
-        pin_loads<3>();
         stamp(a, sl + 2);
         // ---- C: o-proj + residual
         {
@@ -1175,9 +1142,10 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             }
             __syncthreads();
             emit_triples(ar.own, a.hbuf + zl, hwb, hwe, hb, t, flat_row, [&](int W) { return min(3, H - 3 * W); });
-            // E's weights stream while the residual travels to the norm
-            we.load(Ly.Wd, H, F, e0 + zl);
-            pin_loads<4>();
+            // D's weights stream while the residual travels to the norm
+            wg.load(Ly.Wg, F, H, d0 + zl);
+            wu.load(Ly.Wu, F, H, d0 + zl);
+            pin_loads<3>();
         }
         __syncthreads();
         stamp(a, sl + 4);
@@ -1212,6 +1180,9 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
             __syncthreads();
             if (l == kTraceLayer) stamp(a, 913);
             emit_triples(ar.rows, a.act + zl, fwb, fwe, fb, t, flat_row, [&](int W) { return min(3, F - 3 * W); });
+            // E's weights stream while the SwiGLU output travels to the down-proj
+            we.load(Ly.Wd, H, F, e0 + zl);
+            pin_loads<4>();
         }
         __syncthreads();
         stamp(a, sl + 6);
@@ -1273,6 +1244,10 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
         });
     }
     stamp(a, sh + 1);
+    if (a.trace && tidx() == 0) {
+        a.trace[(size_t)blockIdx.x * kTraceSlots + 921] = clock64();
+        a.trace[(size_t)blockIdx.x * kTraceSlots + 922] = wall_clock64();
+    }
     // WG argmax: lane 0 of each wave holds its best (lowest index among equal values).
     float* rv = ar.red;
     int* ri = reinterpret_cast<int*>(ar.red + 8);
@@ -1416,6 +1391,11 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
     if (d.hidden % 256 || d.intermediate % 256 || qd % 256) return fail(BX_EUNSUPPORTED, "persist: widths");
     const int smax = G / d.n_kv;
     if (smax < 1 || G < 3) return fail(BX_EUNSUPPORTED, "persist: too few CUs");
+    // every attention split holds its keys in one LDS tile
+    if ((int64_t)d.cap > (int64_t)smax * kTile) return fail(BX_EUNSUPPORTED, "persist: KV cache longer than the splits' tiles");
+    // a combiner's lanes hold at most two partials each (S P <= 128)
+    if ((int64_t)std::min(smax, (d.cap + kSplitQ - 1) / kSplitQ) * att_parts(Gq) > 128)
+        return fail(BX_EUNSUPPORTED, "persist: more than 128 attention partials per head");
     const PKey want{d.qkv_type_q, d.qkv_type_v, d.o_type, d.gate_type, d.down_type, d.lm_type,
                     upl_for(d.hidden), upl_for(qd), upl_for(d.intermediate), hd};
     const PEntry* ent = nullptr;
