@@ -38,7 +38,7 @@ STEP_DESC = {
 # (FETCH_SIZE x 1.99974 + WRITE_SIZE x 1.0, each scale from a 256 MiB copy in the
 # same run): profiles/persist_kernel_traffic_qwen3-1.7b-q4k.md.
 MEASURED_TRAFFIC = {
-    ("qwen3-1.7b-q4k", "persistent"): 1_372_105_357,
+    ("qwen3-1.7b-q4k", "persistent"): 1_602_927_096,
 }
 KERNEL_DESC = {
     "persistent": "persist_kernel: the whole decode step (all layers, lm_head, argmax) in one launch",
