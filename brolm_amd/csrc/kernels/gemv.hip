@@ -1,6 +1,8 @@
 // Quant-carrier / FP16 batched linear (brotensor linear_forward_batched_*_fp16,
 // dispatched at include/brolm/detail/compute.h:54-86): Y[M,N] = X[M,K] W[N,K]^T.
-// M <= 16: GEMV kernels (one wavefront per weight row, lanes across K).
+// M = 1: GEMV kernels (lanes across K, rows per wavefront).
+// 3 <= M <= 16 with K % 256 == 0: the matrix-core GEMV (gemv_mfma.hip), except
+// M = 2 and 4 (see gemv_f16) and other K, which take the per-row GEMV kernel.
 // M > 16: the prefill GEMM (gemm.hip).
 #include "gemv_core.h"
 
@@ -8,6 +10,8 @@ namespace bx {
 
 int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st);
+int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+              hipStream_t st);
 
 namespace {
 
@@ -163,6 +167,13 @@ int check_linear_shape(int wtype, int M, int N, int K) {
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st) {
     if (M == 1 && upl_for(K) <= 6) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
+    // measured crossover (GEMV sweep): the per-row kernel is one launch at
+    // M = 2 and 4 and faster there, except Q4_K at 4 with N >= 4096; Q8_0
+    // below 8 M weights keeps it up to M = 8
+    const bool small_q8 = wtype == BX_TYPE_Q8_0 && M < 16 && (int64_t)N * K < (8 << 20);
+    const bool mfma = K % 256 == 0 && M >= 3 && (M != 4 || (wtype == BX_TYPE_Q4_K && N >= 4096)) &&
+                      !(small_q8 && (M == 8 || M <= 4));
+    if (mfma) return gemv_mfma(wtype, W, bias, X, Y, M, N, K, st);
     switch (wtype) {
         case BX_TYPE_Q4_K: return gemv_dispatch<FMT_Q4_K>(M, W, X, bias, Y, N, K, st);
         case BX_TYPE_Q6_K: return gemv_dispatch<FMT_Q6_K>(M, W, X, bias, Y, N, K, st);

@@ -1,0 +1,465 @@
+// Batched quant-carrier linear on the matrix cores, 3 <= M <= 16 rows of
+// activations (brotensor linear_forward_batched_*_fp16 at the decode batch
+// sizes, dispatched at include/brolm/detail/compute.h:54-86):
+// Y[M,N] = X[M,K] W[N,K]^T.
+//
+// A wavefront owns a tile of 16 weight rows and streams it along K in chunks
+// of 256 elements.  Each v_mfma_f32_16x16x32_f16 (v_mfma_f32_16x16x16_f16 for
+// Q6_K) multiplies the activations (A: 16 rows of X, zero past M) by one
+// scale group of the tile's weights (B: the 16 rows' quantized values of one
+// sub-block), so the group's scale applies to the instruction's result,
+//     acc[m][n] += s[n] * D[m][n].
+// Q4_K folds its 6-bit sub-block scales into the values instead (sc * q <= 945
+// is an exact FP16 integer), so one accumulation chain covers a 256-element
+// block and d applies once; the min term sum_sb dmin m_sb X_sb takes one more
+// instruction on the 32-element sums of X, split into two FP16 halves.
+// The weight values enter the matrix core as small exact integers (the
+// magic-exponent FP16 pairs of gemv_core.h), so every product is exact and the
+// result has the GEMV path's numerics: FP32 accumulation, no FP16 rounding of
+// dequantized weights.
+//
+// Lane l of a wavefront feeds row (l mod 16) of both operands and k-group
+// l / 16 (8 consecutive k slots; 4 for 16x16x16); its four results are
+// D[4 (l / 16) + j][l mod 16].  The activations sit in LDS in the swizzled
+// pair order of gemv_core.h, which is the order the byte masks pull weight
+// values out of a dword, so a lane's A fragment is one aligned 16-byte read;
+// rows past M read a zeroed row.
+//
+// Loads are software-pipelined: the next slice of SB chunks is requested
+// before the current one is multiplied.  Wide matrices give each wavefront
+// whole tiles; narrow ones split K over the 8 wavefronts of a workgroup and
+// add the partial tiles in LDS.
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "gemv_core.h"
+
+namespace bx {
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int kThr = 512;
+constexpr int kWav = kThr / 64;
+
+__device__ __forceinline__ f4v mfma_k32(u4v a, u4v b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v, a), __builtin_bit_cast(h8v, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f4v mfma_k16(u2v a, u2v b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4v, a), __builtin_bit_cast(h4v, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t ldg_u32(const void* p) { return *gptr<uint32_t>(p); }
+// Weight loads are plain (cached): a load instruction covers 32 bytes of each
+// of 16 rows, and the next instructions finish the lines it touched, so L2
+// must keep them meanwhile (streaming loads measured 10-20 % slower here).
+__device__ __forceinline__ u2v ldw8(const void* p) { return *gptr<u2v>(p); }
+__device__ __forceinline__ u4v ldw16(const void* p) { return *gptr<u4v>(p); }
+
+// Staged activations: Mr rows of K elements (swizzled pairs, natural for FP16
+// weights) and a zero row Mr, row stride xstride dwords; a lane reads row
+// min(l mod 16, Mr) (xrow: its first dword).  Q4_K also keeps
+// xs2[j * 16 + m] = the sum of x[m][32 j .. 32 j + 31] as an FP16 pair
+// (high part, remainder), zero for m >= Mr.
+struct XStage {
+    const uint32_t* xs;
+    const uint32_t* xs2;
+    int xrow;
+    __device__ __forceinline__ u4v a8(int e) const { return *reinterpret_cast<const u4v*>(xs + xrow + (e >> 1)); }
+    __device__ __forceinline__ u2v a4(int e) const { return *reinterpret_cast<const u2v*>(xs + xrow + (e >> 1)); }
+};
+
+// ---- per-format chunk: 256 K elements of one 16-row tile, per lane ---------
+
+template <int FMT>
+struct Chunk;
+
+// Q4_K: block b of row n; lane group g takes the 32 qs bytes 32g .. 32g + 31
+// (low nibbles: sub-block 2g, high: 2g + 1), eight k-slot groups of 8.
+template <>
+struct Chunk<FMT_Q4_K> {
+    u4v hdr;
+    u4v q0, q1;
+    __device__ __forceinline__ void load(const void* W, int64_t N, int K, int64_t n, int b, int g) {
+        const CarrierQ4K c = carrier_q4k(W, N, K);
+        const int64_t s = n * (K / 256) + b;
+        hdr = ldg16(c.hdr + s * 16);
+        q0 = ldw16(c.qs + s * 128 + 32 * g);
+        q1 = ldw16(c.qs + s * 128 + 32 * g + 16);
+    }
+    __device__ __forceinline__ void mul(const XStage& x, int e0, int r, int g, f4v& acc) const {
+        u4v a[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] = x.a8(e0 + 64 * g + 32 * (k >> 2) + 8 * (k & 3));
+        const uint32_t xm = x.xs2[(e0 >> 5) * 16 + 2 * g * 16 + r];
+        const uint32_t xm1 = x.xs2[(e0 >> 5) * 16 + (2 * g + 1) * 16 + r];
+        const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+        int sc0, m0, sc1, m1;
+        q4k_scale_min_regs(hdr.y, hdr.z, hdr.w, 2 * g, sc0, m0);
+        q4k_scale_min_regs(hdr.y, hdr.z, hdr.w, 2 * g + 1, sc1, m1);
+        // (1024 + q) * sc - 1024 sc = sc q, one rounding of an exact integer
+        const h2 s_lo = {(_Float16)sc0, (_Float16)sc0}, c_lo = {(_Float16)(-1024 * sc0), (_Float16)(-1024 * sc0)};
+        const h2 s_hi = {(_Float16)sc1, (_Float16)sc1}, c_hi = {(_Float16)(-1024 * sc1), (_Float16)(-1024 * sc1)};
+        const uint32_t mg = magic_vgpr();
+        const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        f4v d1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int hi = k >> 2;
+            const uint32_t wa = hi ? w[2 * (k & 3)] >> 4 : w[2 * (k & 3)];
+            const uint32_t wb = hi ? w[2 * (k & 3) + 1] >> 4 : w[2 * (k & 3) + 1];
+            const h2 sv = hi ? s_hi : s_lo, cv = hi ? c_hi : c_lo;
+            const u4v bw = {as_u32(__builtin_elementwise_fma(as_h2(and_or(wa, 0x000F000Fu, mg)), sv, cv)),
+                            as_u32(__builtin_elementwise_fma(as_h2(and_or(wa >> 8, 0x000F000Fu, mg)), sv, cv)),
+                            as_u32(__builtin_elementwise_fma(as_h2(and_or(wb, 0x000F000Fu, mg)), sv, cv)),
+                            as_u32(__builtin_elementwise_fma(as_h2(and_or(wb >> 8, 0x000F000Fu, mg)), sv, cv))};
+            d1 = mfma_k32(a[k], bw, d1);
+        }
+        // min term: slots (X_hi, X_lo) of sub-blocks 2g and 2g + 1 against (m, m)
+        const h2 mp0 = {(_Float16)m0, (_Float16)m0}, mp1 = {(_Float16)m1, (_Float16)m1};
+        const u4v am = {xm, xm1, 0u, 0u};
+        const u4v bm = {as_u32(mp0), as_u32(mp1), 0u, 0u};
+        const f4v d2 = mfma_k32(am, bm, f4v{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += d * d1[j] - dmin * d2[j];
+    }
+};
+
+// Q6_K: block b of row n; sub-block (h, p, hl) = elements 128h + 32p + 16hl
+// + 0..15 (scale index 8h + 2p + hl); lane group g takes 16hl + 4g .. +3.
+template <>
+struct Chunk<FMT_Q6_K> {
+    u4v sc;
+    uint32_t d;
+    u4v ql[4];
+    uint32_t qh[4];
+    __device__ __forceinline__ void load(const void* W, int64_t N, int K, int64_t n, int b, int g) {
+        const CarrierQ6K c = carrier_q6k(W, N, K);
+        const int64_t s = n * (K / 256) + b;
+        sc = ldg16(c.sc + s * 16);
+        d = ldg_u16(c.d + s * 2);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int t = 4 * (k >> 1) + 2 * (k & 1) + (g >> 1);
+            ql[k] = ldw16(c.ql + s * 128 + 16 * t);
+            qh[k] = ldg_u32(c.qh + s * 64 + 8 * t + 4 * (g & 1));
+        }
+    }
+    __device__ __forceinline__ void mul(const XStage& x, int e0, int r, int g, f4v& acc) const {
+        const float dd = h2f(d & 0xffff);
+        const uint32_t mg = magic_vgpr();
+        const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+        const f4v z = {0.f, 0.f, 0.f, 0.f};
+        u2v av[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int p = 0; p < 4; ++p) av[k][p] = x.a4(e0 + 128 * (k >> 1) + 32 * p + 16 * (k & 1) + 4 * g);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int h = k >> 1, hl = k & 1;
+            const uint32_t a = (g & 1) ? ql[k].y : ql[k].x, bq = (g & 1) ? ql[k].w : ql[k].z, q = qh[k];
+            const uint32_t a8 = a >> 8, b8 = bq >> 8;
+            const uint32_t ql4 = q << 4, qr4 = q >> 4, ql2 = q << 2, qr6 = q >> 6;
+            // (low nibble | 2 high bits) -> 1024 + q; (high nibble in place | 2 bits at 8-9) -> 1024 + 16 q
+            const uint32_t v[4][2] = {
+                {and_or(ql4, 0x00300030u, and_or(a, 0x000F000Fu, mg)), and_or(qr4, 0x00300030u, and_or(a8, 0x000F000Fu, mg))},
+                {and_or(ql2, 0x00300030u, and_or(bq, 0x000F000Fu, mg)), and_or(qr6, 0x00300030u, and_or(b8, 0x000F000Fu, mg))},
+                {and_or(ql4, 0x03000300u, and_or(a, 0x00F000F0u, mg)), and_or(qr4, 0x03000300u, and_or(a8, 0x00F000F0u, mg))},
+                {and_or(ql2, 0x03000300u, and_or(bq, 0x00F000F0u, mg)), and_or(qr6, 0x03000300u, and_or(b8, 0x00F000F0u, mg))}};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float off = p < 2 ? 1056.f : 1536.f;   // centre: q - 32, or 16 (q - 32)
+                const u2v bw = {centre(v[p][0], off), centre(v[p][1], off)};
+                const f4v dv = mfma_k16(av[k][p], bw, z);
+                const int sb = 8 * h + 2 * p + hl;
+                const float s = dd * (float)(int8_t)((scw[sb >> 2] >> (8 * (sb & 3))) & 0xff) * (p < 2 ? 1.f : 0.0625f);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] += s * dv[j];
+            }
+        }
+    }
+};
+
+// Q8_0: the 8 blocks of 32 of a chunk; lane group g takes qs bytes 8g .. +7.
+template <>
+struct Chunk<FMT_Q8_0> {
+    u4v dv;
+    u2v q[8];
+    __device__ __forceinline__ void load(const void* W, int64_t N, int K, int64_t n, int b, int g) {
+        const CarrierQ8 c = carrier_q8(W, N, K);
+        const int64_t s = n * (K / 32) + 8 * b;
+        dv = ldg16(c.d + s * 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = ldw8(c.qs + (s + j) * 32 + 8 * g);
+    }
+    __device__ __forceinline__ void mul(const XStage& x, int e0, int r, int g, f4v& acc) const {
+        const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+        const f4v z = {0.f, 0.f, 0.f, 0.f};
+        u4v a[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = x.a8(e0 + 32 * j + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w0 = q[j].x, w1 = q[j].y;
+            const u4v bw = {centre(magic_pair((w0 & 0x00FF00FFu) ^ 0x00800080u), 1152.f),
+                            centre(magic_pair(((w0 >> 8) & 0x00FF00FFu) ^ 0x00800080u), 1152.f),
+                            centre(magic_pair((w1 & 0x00FF00FFu) ^ 0x00800080u), 1152.f),
+                            centre(magic_pair(((w1 >> 8) & 0x00FF00FFu) ^ 0x00800080u), 1152.f)};
+            const f4v dvv = mfma_k32(a[j], bw, z);
+            const float s = h2f((dw[j >> 1] >> (16 * (j & 1))) & 0xffff);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += s * dvv[i];
+        }
+    }
+};
+
+// FP16 weights (natural activation layout): 8 consecutive weights per lane.
+template <>
+struct Chunk<FMT_F16> {
+    u4v w[8];
+    __device__ __forceinline__ void load(const void* W, int64_t, int K, int64_t n, int b, int g) {
+        const uint8_t* p = static_cast<const uint8_t*>(W) + (n * K + 256 * (int64_t)b + 8 * g) * 2;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = ldw16(p + 64 * j);
+    }
+    __device__ __forceinline__ void mul(const XStage& x, int e0, int r, int g, f4v& acc) const {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = mfma_k32(x.a8(e0 + 32 * j + 8 * g), w[j], acc);
+    }
+};
+
+template <int FMT> struct SliceLen { static constexpr int SB = 2; };
+template <> struct SliceLen<FMT_Q4_K> { static constexpr int SB = 4; };
+template <> struct SliceLen<FMT_Q6_K> { static constexpr int SB = 1; };
+
+// A wavefront's walk over slices: tiles tile0, tile0 + tstride, ... below
+// tiles; in each tile the chunks [c0, c1) in slices of SB.
+struct Walk {
+    int64_t tile;
+    int cb;
+    int64_t tstride, tiles;
+    int c0, c1;
+    __device__ __forceinline__ bool valid() const { return tile < tiles && c0 < c1; }
+    __device__ __forceinline__ bool last_of_tile(int SB) const { return cb + SB >= c1; }
+    __device__ __forceinline__ Walk next(int SB) const {
+        Walk w = *this;
+        w.cb += SB;
+        if (w.cb >= c1) {
+            w.cb = c0;
+            w.tile += tstride;
+        }
+        return w;
+    }
+};
+
+template <int FMT>
+struct SliceBuf {
+    static constexpr int SB = SliceLen<FMT>::SB;
+    Chunk<FMT> c[SB];
+    uint32_t bias;   // bias of the lane's row, loaded with a tile's first slice
+    __device__ __forceinline__ void load(const void* W, const uint16_t* bias_p, int64_t N, int K, const Walk& w, int r,
+                                         int g) {
+        int64_t n = w.tile * 16 + r;
+        if (n >= N) n = N - 1;
+        bias = bias_p ? ldg_u16(bias_p + n) : 0u;
+#pragma unroll
+        for (int i = 0; i < SB; ++i) {
+            const int b = w.cb + i < w.c1 ? w.cb + i : w.c1 - 1;   // clamped: every load is issued
+            c[i].load(W, N, K, n, b, g);
+        }
+    }
+    __device__ __forceinline__ void mul(const XStage& x, const Walk& w, int r, int g, f4v& acc) const {
+#pragma unroll
+        for (int i = 0; i < SB; ++i)
+            if (w.cb + i < w.c1) c[i].mul(x, 256 * (w.cb + i), r, g, acc);
+    }
+};
+
+// kpart: waves per tile.  1: every wave walks whole tiles (grid-stride);
+// 2, 4, 8: the workgroup takes 8 / kpart tiles, each split along K over kpart
+// waves whose partial tiles are added in LDS.
+template <int FMT>
+__global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
+                                                        const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
+                                                        int Mr, int N, int K, int kpart) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    constexpr bool kSwz = FMT != FMT_F16;
+    const int xstride = K / 2 + 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    XStage xst;
+    xst.xs = smem;
+    xst.xrow = (r < Mr ? r : Mr) * xstride;
+    uint32_t* xs2 = smem + (Mr + 1) * xstride;
+    xst.xs2 = xs2;
+    float* red = reinterpret_cast<float*>(xs2 + (FMT == FMT_Q4_K ? (K / 32) * 16 : 0));
+    const int nch = K / 256;
+    const int64_t tiles = ((int64_t)N + 15) / 16;
+    Walk w;
+    w.tiles = tiles;
+    if (kpart == 1) {
+        w.tile = (int64_t)blockIdx.x * kWav + wave;
+        w.tstride = (int64_t)gridDim.x * kWav;
+        w.c0 = 0;
+        w.c1 = nch;
+    } else {
+        const int part = wave % kpart;
+        w.tile = (int64_t)blockIdx.x * (kWav / kpart) + wave / kpart;
+        w.tstride = tiles;   // one tile per wave
+        w.c0 = part * nch / kpart;
+        w.c1 = (part + 1) * nch / kpart;
+    }
+    w.cb = w.c0;
+    const int64_t w0tile = w.tile;
+
+    // the first slice's weights stream while the activations are staged
+    constexpr int SB = SliceLen<FMT>::SB;
+    SliceBuf<FMT> b0, b1;
+    if (w.valid()) b0.load(W, bias, N, K, w, r, g);
+    stage_x_f16<kSwz, false>(X, K, Mr, K, smem, xstride, nullptr, 0);
+    for (int i = threadIdx.x; i < xstride; i += kThr) smem[Mr * xstride + i] = 0u;
+    __syncthreads();
+    if constexpr (FMT == FMT_Q4_K) {
+        // 32-element sums from the staged rows (16 dwords hold a permutation
+        // of the group's elements), kept as FP16 high part + remainder
+        for (int i = threadIdx.x; i < (K / 32) * 16; i += kThr) {
+            const int j = i >> 4, m = i & 15;
+            float s = 0.f;
+            if (m < Mr) {
+                const u4v* p = reinterpret_cast<const u4v*>(smem + m * xstride + 16 * j);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const u4v v = p[q];
+                    s += (h2f(v.x & 0xffff) + h2f(v.x >> 16)) + (h2f(v.y & 0xffff) + h2f(v.y >> 16)) +
+                         (h2f(v.z & 0xffff) + h2f(v.z >> 16)) + (h2f(v.w & 0xffff) + h2f(v.w >> 16));
+                }
+            }
+            const _Float16 hi = (_Float16)s;
+            const _Float16 lo = (_Float16)(s - (float)hi);
+            xs2[i] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        }
+        __syncthreads();
+    }
+
+    f4v acc = {0.f, 0.f, 0.f, 0.f};
+    auto finish = [&](int64_t tile, float bv) {
+        const int64_t n = tile * 16 + r;
+        if (n < N) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = 4 * g + j;
+                if (m < Mr) Y[(int64_t)m * N + n] = f2h(acc[j] + bv);
+            }
+        }
+        acc = f4v{0.f, 0.f, 0.f, 0.f};
+    };
+    // The next slice's loads are issued before the current slice's math and
+    // unconditionally (past the end they repeat the current slice), so the
+    // compiler's in-order wait for a slice never covers its successor.
+    float bv = 0.f;
+    if (w.valid()) {
+        for (;;) {
+            Walk nx = w.next(SB);
+            b1.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
+            if (w.cb == w.c0) bv = h2f(b0.bias & 0xffff);
+            b0.mul(xst, w, r, g, acc);
+            if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
+            w = nx;
+            if (!w.valid()) break;
+            nx = w.next(SB);
+            b0.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
+            if (w.cb == w.c0) bv = h2f(b1.bias & 0xffff);
+            b1.mul(xst, w, r, g, acc);
+            if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
+            w = nx;
+            if (!w.valid()) break;
+        }
+    }
+    if (kpart > 1) {
+        // partial tiles -> LDS -> the first wave of each tile adds and writes
+        *reinterpret_cast<f4v*>(red + (wave * 64 + lane) * 4) = acc;
+        __syncthreads();
+        if (wave % kpart == 0 && w0tile < tiles) {
+            f4v s = {0.f, 0.f, 0.f, 0.f};
+            for (int v = wave; v < wave + kpart; ++v) s += *reinterpret_cast<const f4v*>(red + (v * 64 + lane) * 4);
+            acc = s;
+            const int64_t n = w0tile * 16 + r;
+            finish(w0tile, (bias && n < N) ? h2f(bias[n]) : 0.f);
+        }
+    }
+}
+
+size_t mfma_lds_bytes(int fmt, int Mr, int K) {
+    size_t b = (size_t)(Mr + 1) * (K / 2 + 4) * 4;
+    if (fmt == FMT_Q4_K) b += (size_t)(K / 32) * 16 * 4;
+    return b + (size_t)kWav * 64 * 4 * 4;
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+int resident_wgs(const void* fn, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(fn, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kThr, lds) != hipSuccess || occ < 1) occ = 1;
+    cache.emplace(key, occ);
+    return occ;
+}
+
+}  // namespace
+
+// 1 <= M <= 16, K % 256 == 0 (the linear entry point sends 3 <= M <= 16).
+// Activations in row chunks whose staging fits the workgroup's LDS.
+int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+              hipStream_t st) {
+    int fmt;
+    switch (wtype) {
+        case BX_TYPE_Q4_K: fmt = FMT_Q4_K; break;
+        case BX_TYPE_Q6_K: fmt = FMT_Q6_K; break;
+        case BX_TYPE_Q8_0: fmt = FMT_Q8_0; break;
+        case BX_TYPE_F16: fmt = FMT_F16; break;
+        default: return fail(BX_EUNSUPPORTED, "gemv mfma: unsupported type");
+    }
+    if (K % 256 != 0) return fail(BX_EUNSUPPORTED, "gemv mfma: K must be a multiple of 256");
+    int mc = M;
+    while (mc > 1 && mfma_lds_bytes(fmt, mc, K) > kMaxLds) mc = (mc + 1) / 2;
+    if (mfma_lds_bytes(fmt, mc, K) > kMaxLds) return fail(BX_EUNSUPPORTED, "gemv mfma: K too large for LDS staging");
+    const int64_t tiles = ((int64_t)N + 15) / 16;
+    const int nch = K / 256;
+    const int cus = num_cus();
+    for (int m0 = 0; m0 < M; m0 += mc) {
+        const int mr = M - m0 < mc ? M - m0 : mc;
+        const size_t lds = mfma_lds_bytes(fmt, mr, K);
+        const uint16_t* Xc = X + (int64_t)m0 * K;
+        uint16_t* Yc = Y + (int64_t)m0 * N;
+        BX_DISPATCH_FMT(wtype, {
+            const void* fn = reinterpret_cast<const void*>(&gemv_mfma_kernel<FMT_>);
+            if (lds > 64 * 1024) {
+                const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return hip_check(e, "gemv mfma: LDS attribute");
+            }
+            // resident workgroups per CU (registers and LDS), asked once per
+            // format and staging size
+            const int occ = resident_wgs(fn, lds);
+            const int64_t slots = (int64_t)cus * occ;
+            // the most waves per tile (K split) whose workgroups still fit in
+            // one round of resident slots; 1: whole tiles, grid-stride
+            int kpart = 1;
+            while (kpart * 2 <= kWav && kpart * 2 <= nch && (tiles * kpart * 2 + kWav - 1) / kWav <= slots) kpart *= 2;
+            int64_t grid = (tiles * kpart + kWav - 1) / kWav;
+            if (kpart == 1 && grid > slots) grid = slots;
+            gemv_mfma_kernel<FMT_><<<(unsigned)grid, kThr, lds, st>>>(W, Xc, bias, Yc, mr, N, K, kpart);
+        })
+        if (int rc = launch_check("gemv mfma")) return rc;
+    }
+    return BX_OK;
+}
+
+}  // namespace bx

@@ -107,6 +107,28 @@ def test_linear_quant_vs_oracle(t, N, K):
         assert np.all(err <= tol), (M, float((err / tol).max()))
 
 
+@pytest.mark.parametrize("t", QTYPES + [1])
+def test_linear_batched_many_tiles(t):
+    """Batched GEMV with more 16-row tiles than the workgroups hold at once
+    (each wavefront walks several tiles) and a last tile of one row."""
+    rng = np.random.default_rng(77 + t)
+    N, K = 70001, 256
+    if t == 1:
+        Wv = _f16(rng.standard_normal((N, K)) * 0.05)
+        car = f16_dev(Wv)
+    else:
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        car = carrier(t, raw, N, K)
+    bias = _f16(rng.standard_normal(N))
+    for M in (3, 5, 8, 16):
+        print(f"[linear many tiles] type={t} N={N} K={K} M={M}", flush=True)
+        X = _f16(rng.standard_normal((M, K)))
+        got = _run_linear(t, car, X, N, K, bias)
+        ref = oracle.linear(Wv, X) + bias
+        tol = _linear_tol(Wv, X, ref) + 2.0 ** -10 * np.abs(bias)
+        assert np.all(np.abs(got - ref) <= tol), M
+
+
 @pytest.mark.parametrize("t", [1, 12])
 def test_linear_bias_and_dense_f16(t):
     rng = np.random.default_rng(5)
