@@ -209,6 +209,25 @@ def main() -> int:
         tok = int(model.forward_last([tok]).argmax())
     ref_tok_s = n_ref / (time.perf_counter() - t0)
 
+    # text path: the checkpoint's own tokenizer (host), and generate_text
+    # (encode -> greedy generate -> decode) end to end
+    tk = ba.Tokenizer.from_gguf(str(path))
+    corpus = ("The decoder reads the tokens of the prompt, 128 at a time; the sampler picks the next one. " * 12000)
+    t0 = time.perf_counter()
+    n_ids = len(tk.encode(corpus))
+    enc_s = time.perf_counter() - t0
+    model.truncate_cache(0)
+    gen_opts = ba.GenerateOptions(max_new_tokens=64, sampling=ba.SamplingParams(temperature=0.0), stop_on_eos=False)
+    text_prompt = tk.decode(prompt)
+    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)   # warm-up
+    t0 = time.perf_counter()
+    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)
+    gen_text_s = time.perf_counter() - t0
+    tokenizer = {"encode_mb_s": round(len(corpus) / enc_s / 1e6, 2), "encode_ids_s": round(n_ids / enc_s),
+                 "sample": f"{len(corpus) / 1e6:.2f} MB English-like text, {n_ids} ids, 1 host thread",
+                 "generate_text_ms": round(gen_text_s * 1e3, 2),
+                 "generate_text_note": "decoded 2000-byte prompt re-encoded, 64 greedy tokens, decode"}
+
     wbytes = model.decode_weight_bytes()
     achieved = wbytes / (gpu_ms * 1e-3) / 1e9
     kvd = cfg.num_key_value_heads * cfg.head_dim
@@ -239,6 +258,7 @@ def main() -> int:
         "kv_bytes_per_token_avg": int(kv_bytes),
         "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
         "ref_loop_tok_s": round(ref_tok_s, 2),
+        "tokenizer": tokenizer,
     }
     # device state goes before the process exit path (a profiler wrapping this
     # run finalizes there)

@@ -200,6 +200,109 @@ def generate(model: Qwen3Model, prompt_ids: Sequence[int], eos_id: int, opts: Ge
     return out[:k].tolist()
 
 
+class Tokenizer:
+    """qwen::Tokenizer (include/brolm/qwen_tokenizer.h): byte-level BPE, the
+    reference's token ids (reference include/brolm/qwen_tokenizer.h:41-151)."""
+
+    def __init__(self, handle):
+        if not handle:
+            raise _native.NativeError(f"tokenizer: {_native.lib().brolm_last_error().decode()}")
+        self._h = handle
+
+    @staticmethod
+    def _extra(extra) -> bytes | None:
+        return "\n".join(extra).encode() if extra else None
+
+    @classmethod
+    def load(cls, vocab_json: str, merges_txt: str, extra_special_tokens=()) -> "Tokenizer":
+        return cls(_native.lib().brolm_tokenizer_load(str(vocab_json).encode(), str(merges_txt).encode(),
+                                                     cls._extra(extra_special_tokens)))
+
+    @classmethod
+    def from_gguf(cls, path: str, extra_special_tokens=()) -> "Tokenizer":
+        return cls(_native.lib().brolm_tokenizer_from_gguf(str(path).encode(), cls._extra(extra_special_tokens)))
+
+    @classmethod
+    def from_tokenizer_json(cls, path: str, extra_special_tokens=()) -> "Tokenizer":
+        return cls(_native.lib().brolm_tokenizer_from_json(str(path).encode(), cls._extra(extra_special_tokens)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and _native._lib is not None:
+            _native.lib().brolm_tokenizer_free(self._h)
+        self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, text: str, add_special: bool = False) -> list[int]:
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = check(_native.lib().brolm_tokenizer_encode(self._h, b, len(b), 1 if add_special else 0, None, 0),
+                  "tokenizer encode")
+        out = np.empty((max(n, 1),), np.int32)
+        check(_native.lib().brolm_tokenizer_encode(self._h, b, len(b), 1 if add_special else 0,
+                                                   out.ctypes.data_as(_native.P_i32), n), "tokenizer encode")
+        return out[:n].tolist()
+
+    def decode_bytes(self, ids: Sequence[int]) -> bytes:
+        arr, p = _i32(list(ids) if len(ids) else [0])
+        n = check(_native.lib().brolm_tokenizer_decode(self._h, p, len(ids), None, 0), "tokenizer decode")
+        buf = C.create_string_buffer(max(n, 1))
+        check(_native.lib().brolm_tokenizer_decode(self._h, p, len(ids), buf, n), "tokenizer decode")
+        return buf.raw[:n]
+
+    def decode(self, ids: Sequence[int]) -> str:
+        return self.decode_bytes(ids).decode("utf-8", errors="replace")
+
+    def apply_chat_template(self, messages, add_generation_prompt: bool = True) -> str:
+        roles = (C.c_char_p * max(len(messages), 1))(*[r.encode() for r, _ in messages])
+        conts = (C.c_char_p * max(len(messages), 1))(*[c.encode() for _, c in messages])
+        args = (self._h, roles, conts, len(messages), 1 if add_generation_prompt else 0)
+        n = check(_native.lib().brolm_tokenizer_chat(*args, None, 0), "chat template")
+        buf = C.create_string_buffer(max(n, 1))
+        check(_native.lib().brolm_tokenizer_chat(*args, buf, n), "chat template")
+        return buf.raw[:n].decode()
+
+    def register_special_token(self, token: str, id_: int) -> None:
+        check(_native.lib().brolm_tokenizer_register_special(self._h, token.encode(), int(id_)), "register special")
+
+    def _info(self) -> list[int]:
+        a = np.zeros(6, np.int64)
+        check(_native.lib().brolm_tokenizer_info(self._h, a.ctypes.data_as(_native.P_i64)), "tokenizer info")
+        return a.tolist()
+
+    def vocab_count(self) -> int:
+        return self._info()[0]
+
+    def merge_count(self) -> int:
+        return self._info()[1]
+
+    def eos_id(self) -> int:
+        return self._info()[2]
+
+    def im_start_id(self) -> int:
+        return self._info()[3]
+
+    def im_end_id(self) -> int:
+        return self._info()[4]
+
+    def endoftext_id(self) -> int:
+        return self._info()[5]
+
+
+def generate_text(model: Qwen3Model, tok: Tokenizer, prompt: str, opts: GenerateOptions) -> str:
+    """qwen::generate_text (reference src/qwen_generate.cpp:19-25)."""
+    s = opts.sampling
+    args = (model._h, tok._h, prompt.encode(), int(opts.max_new_tokens), 1 if opts.stop_on_eos else 0,
+            float(s.temperature), int(s.top_k), float(s.top_p), int(s.seed))
+    cap = 64 * max(int(opts.max_new_tokens), 1) + 4096   # one generation fills it; longer text re-runs
+    while True:
+        buf = C.create_string_buffer(cap)
+        n = check(_native.lib().brolm_qwen3_generate_text(*args, buf, cap), "generate_text")
+        if n <= cap:
+            return buf.raw[:n].decode("utf-8", errors="replace")
+        cap = n
+
+
 def sample_token(logits: np.ndarray, params: SamplingParams, seed: int) -> int:
     """sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142)."""
     a = np.ascontiguousarray(logits, dtype=np.float32)

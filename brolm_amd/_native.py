@@ -114,6 +114,16 @@ C_SYMBOLS = {
     "brolm_qwen3_decode_mode": (C.c_int, [vp]),
     "brolm_sample_token": (C.c_int, [P_f32, C.c_int, f32, C.c_int, f32, u64]),
     "brolm_prompt_ids": (C.c_int, [u64, C.c_int, C.c_int, P_i32]),
+    "brolm_tokenizer_load": (vp, [cp, cp, cp]),
+    "brolm_tokenizer_from_gguf": (vp, [cp, cp]),
+    "brolm_tokenizer_from_json": (vp, [cp, cp]),
+    "brolm_tokenizer_free": (None, [vp]),
+    "brolm_tokenizer_encode": (C.c_int, [vp, cp, i64, C.c_int, P_i32, C.c_int]),
+    "brolm_tokenizer_decode": (i64, [vp, P_i32, C.c_int, C.c_char_p, i64]),
+    "brolm_tokenizer_chat": (i64, [vp, C.POINTER(cp), C.POINTER(cp), C.c_int, C.c_int, C.c_char_p, i64]),
+    "brolm_tokenizer_register_special": (C.c_int, [vp, cp, i32]),
+    "brolm_tokenizer_info": (C.c_int, [vp, P_i64]),
+    "brolm_qwen3_generate_text": (i64, [vp, vp, cp, C.c_int, C.c_int, f32, C.c_int, f32, u64, C.c_char_p, i64]),
     "brolm_profile_reset": (None, []),
     "brolm_profile_report": (None, []),
     "brolm_profile_enabled": (C.c_int, []),

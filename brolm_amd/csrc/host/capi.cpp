@@ -1,6 +1,7 @@
 // C facade of the Qwen3 stack (include/brolm_c.h).
 #include "brolm_c.h"
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -11,12 +12,17 @@
 #include "brolm/detail/profile.h"
 #include "brolm/qwen.h"
 #include "brolm/qwen_generate.h"
+#include "brolm/qwen_tokenizer.h"
 #include "brolm/synth.h"
 #include "brotensor/gguf.h"
 #include "brotensor/runtime.h"
 
 struct brolm_qwen3 {
     std::unique_ptr<brolm::qwen::Qwen3Model> model;
+};
+
+struct brolm_tokenizer {
+    std::unique_ptr<brolm::qwen::Tokenizer> tok;
 };
 
 namespace {
@@ -74,6 +80,43 @@ void to_host_f32(const brotensor::Tensor& t, float* dst) {
 brolm::qwen::Qwen3Model& model_of(brolm_qwen3* m) {
     if (!m || !m->model) throw std::runtime_error("null model handle");
     return *m->model;
+}
+
+}  // namespace
+
+namespace {
+
+std::vector<std::string> split_lines(const char* s) {
+    std::vector<std::string> out;
+    if (!s) return out;
+    std::string cur;
+    for (const char* p = s; *p; ++p) {
+        if (*p == '\n') {
+            if (!cur.empty()) out.push_back(cur);
+            cur.clear();
+        } else {
+            cur += *p;
+        }
+    }
+    if (!cur.empty()) out.push_back(cur);
+    return out;
+}
+
+template <class Make>
+brolm_tokenizer* make_tokenizer(Make&& make) {
+    brolm_tokenizer* h = nullptr;
+    guard([&] { h = new brolm_tokenizer{std::make_unique<brolm::qwen::Tokenizer>(make())}; });
+    return h;
+}
+
+const brolm::qwen::Tokenizer& tok_of(const brolm_tokenizer* t) {
+    if (!t || !t->tok) throw std::runtime_error("null tokenizer");
+    return *t->tok;
+}
+
+int64_t put_string(const std::string& s, char* out, int64_t cap) {
+    if (out && cap > 0) std::memcpy(out, s.data(), static_cast<std::size_t>(std::min<int64_t>(cap, s.size())));
+    return static_cast<int64_t>(s.size());
 }
 
 }  // namespace
@@ -236,6 +279,99 @@ int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, in
         count = static_cast<int>(g.size());
     });
     return rc == 0 ? count : -1;
+}
+
+brolm_tokenizer* brolm_tokenizer_load(const char* vocab_json, const char* merges_txt, const char* extra_specials) {
+    return make_tokenizer([&] {
+        if (!vocab_json || !merges_txt) throw std::runtime_error("brolm_tokenizer_load: null path");
+        return brolm::qwen::Tokenizer::load(vocab_json, merges_txt, split_lines(extra_specials));
+    });
+}
+
+brolm_tokenizer* brolm_tokenizer_from_gguf(const char* gguf_path, const char* extra_specials) {
+    return make_tokenizer([&] {
+        if (!gguf_path) throw std::runtime_error("brolm_tokenizer_from_gguf: null path");
+        const brotensor::gguf::File f = brotensor::gguf::File::open(gguf_path);
+        return brolm::qwen::Tokenizer::from_gguf(f, split_lines(extra_specials));
+    });
+}
+
+brolm_tokenizer* brolm_tokenizer_from_json(const char* tokenizer_json, const char* extra_specials) {
+    return make_tokenizer([&] {
+        if (!tokenizer_json) throw std::runtime_error("brolm_tokenizer_from_json: null path");
+        return brolm::qwen::Tokenizer::from_tokenizer_json(tokenizer_json, split_lines(extra_specials));
+    });
+}
+
+void brolm_tokenizer_free(brolm_tokenizer* t) { delete t; }
+
+int brolm_tokenizer_encode(const brolm_tokenizer* t, const char* text, int64_t len, int add_special, int32_t* ids,
+                           int cap) {
+    int count = -1;
+    const int rc = guard([&] {
+        if (!text && len > 0) throw std::runtime_error("brolm_tokenizer_encode: null text");
+        const std::vector<int32_t> v =
+            tok_of(t).encode(std::string_view(text ? text : "", static_cast<std::size_t>(len)), add_special != 0);
+        if (ids && cap > 0) std::memcpy(ids, v.data(), std::min<std::size_t>(cap, v.size()) * sizeof(int32_t));
+        count = static_cast<int>(v.size());
+    });
+    return rc == 0 ? count : -1;
+}
+
+int64_t brolm_tokenizer_decode(const brolm_tokenizer* t, const int32_t* ids, int n, char* out, int64_t cap) {
+    int64_t len = -1;
+    const int rc = guard([&] {
+        const std::vector<int32_t> v(ids, ids + (n > 0 ? n : 0));
+        len = put_string(tok_of(t).decode(v), out, cap);
+    });
+    return rc == 0 ? len : -1;
+}
+
+int64_t brolm_tokenizer_chat(const brolm_tokenizer* t, const char* const* roles, const char* const* contents, int n,
+                             int add_generation_prompt, char* out, int64_t cap) {
+    int64_t len = -1;
+    const int rc = guard([&] {
+        std::vector<std::pair<std::string, std::string>> msgs;
+        for (int i = 0; i < n; ++i) msgs.emplace_back(roles[i] ? roles[i] : "", contents[i] ? contents[i] : "");
+        len = put_string(tok_of(t).apply_chat_template(msgs, add_generation_prompt != 0), out, cap);
+    });
+    return rc == 0 ? len : -1;
+}
+
+int brolm_tokenizer_register_special(brolm_tokenizer* t, const char* token, int32_t id) {
+    return guard([&] {
+        if (!t || !t->tok || !token) throw std::runtime_error("brolm_tokenizer_register_special: null argument");
+        t->tok->register_special_token(token, id);
+    });
+}
+
+int brolm_tokenizer_info(const brolm_tokenizer* t, int64_t* info) {
+    return guard([&] {
+        const brolm::qwen::Tokenizer& k = tok_of(t);
+        info[0] = static_cast<int64_t>(k.vocab_count());
+        info[1] = static_cast<int64_t>(k.merge_count());
+        info[2] = k.eos_id();
+        info[3] = k.im_start_id();
+        info[4] = k.im_end_id();
+        info[5] = k.endoftext_id();
+    });
+}
+
+int64_t brolm_qwen3_generate_text(brolm_qwen3* m, const brolm_tokenizer* t, const char* prompt, int max_new,
+                                  int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
+                                  char* out, int64_t cap) {
+    int64_t len = -1;
+    const int rc = guard([&] {
+        brolm::qwen::GenerateOptions o;
+        o.max_new_tokens = max_new;
+        o.stop_on_eos = stop_on_eos != 0;
+        o.sampling.temperature = temperature;
+        o.sampling.top_k = top_k;
+        o.sampling.top_p = top_p;
+        o.sampling.seed = seed;
+        len = put_string(brolm::qwen::generate_text(model_of(m), tok_of(t), prompt ? prompt : "", o), out, cap);
+    });
+    return rc == 0 ? len : -1;
 }
 
 int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id) {

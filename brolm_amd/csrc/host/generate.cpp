@@ -97,4 +97,10 @@ std::vector<int32_t> generate(Qwen3Model& model, const std::vector<int32_t>& pro
     return brolm::detail::generate(model, prompt_ids, eos_id, opts);
 }
 
+std::string generate_text(Qwen3Model& model, const Tokenizer& tok, std::string_view prompt,
+                          const GenerateOptions& opts) {
+    const std::vector<int32_t> ids = tok.encode(prompt);
+    return tok.decode(generate(model, ids, tok.eos_id(), opts));
+}
+
 }  // namespace brolm::qwen

@@ -258,6 +258,14 @@ void Writer::add_string_array(const std::string& key, const std::vector<std::str
     kvs_.push_back(std::move(kv));
 }
 
+void Writer::add_i32_array(const std::string& key, const std::vector<std::int32_t>& v) {
+    KV kv{key, ValueType::Array, {}};
+    put<std::uint32_t>(kv.payload, static_cast<std::uint32_t>(ValueType::I32));
+    put<std::uint64_t>(kv.payload, v.size());
+    for (std::int32_t x : v) put<std::int32_t>(kv.payload, x);
+    kvs_.push_back(std::move(kv));
+}
+
 void Writer::add_tensor(const std::string& name, Dtype dt, const std::vector<std::int64_t>& dims,
                         std::vector<std::uint8_t> bytes) {
     if (dims.empty() || dims.size() > 4) bad("writer: 1..4 dims required");

@@ -2,9 +2,11 @@
 #include "brolm/synth.h"
 
 #include <algorithm>
+#include <cctype>
 #include <cmath>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <stdexcept>
 #include <thread>
 
@@ -207,6 +209,108 @@ void quantize(bt::Dtype dt, const float* src, std::int64_t n, std::uint8_t* dst)
     }
 }
 
+namespace {
+
+// A byte-level BPE vocabulary for synthetic checkpoints: the 256 byte tokens
+// (GPT-2 byte alphabet, id = byte), up to 256 merges learned greedily from a
+// fixed English paragraph (most frequent adjacent pair first, ties to the
+// smaller pair), the three ChatML specials (token type 3), then reserved
+// fillers up to the model's vocab size.
+const char kCorpus[] =
+    "The quick brown fox jumps over the lazy dog while the model reads the tokens of the prompt. "
+    "A decoder turns the hidden state into logits, and the sampler picks the next token from them. "
+    "In the beginning there was the word, and the word was split into pieces, and the pieces were merged "
+    "again by the rules that were learned from the text. Numbers such as 2024, 128 and 4096 appear too. "
+    "She said that they're going to the station, but we'll see whether it's true. "
+    "Weights are stored in blocks; each block keeps its scale and its small integers. "
+    "The cache holds the keys and the values of every position, so that attention can look back.";
+
+struct SynthVocab {
+    std::vector<std::string> tokens, merges;
+    std::vector<std::int32_t> types;
+};
+
+std::string byte_symbol(unsigned char b) {
+    int next = 256;
+    auto self = [](int x) { return (x >= 33 && x <= 126) || (x >= 161 && x <= 172) || (x >= 174 && x <= 255); };
+    for (int i = 0; i < b; ++i)
+        if (!self(i)) ++next;
+    const unsigned cp = self(b) ? b : static_cast<unsigned>(next);
+    std::string out;
+    if (cp < 0x80) {
+        out += static_cast<char>(cp);
+    } else {
+        out += static_cast<char>(0xC0 | (cp >> 6));
+        out += static_cast<char>(0x80 | (cp & 0x3F));
+    }
+    return out;
+}
+
+SynthVocab synth_vocab(int vocab) {
+    SynthVocab v;
+    for (int b = 0; b < 256; ++b) {
+        v.tokens.push_back(byte_symbol(static_cast<unsigned char>(b)));
+        v.types.push_back(1);
+    }
+    // words: letter runs with one folded leading space, other bytes alone
+    std::vector<std::vector<std::string>> words;
+    const std::string text(kCorpus);
+    for (std::size_t i = 0; i < text.size();) {
+        std::size_t j = i;
+        if (text[j] == ' ' && j + 1 < text.size()) ++j;
+        const bool alpha = std::isalpha(static_cast<unsigned char>(text[j])) != 0;
+        if (alpha)
+            while (j < text.size() && std::isalpha(static_cast<unsigned char>(text[j]))) ++j;
+        else
+            ++j;
+        std::vector<std::string> w;
+        for (std::size_t k = i; k < j; ++k) w.push_back(byte_symbol(static_cast<unsigned char>(text[k])));
+        words.push_back(std::move(w));
+        i = j;
+    }
+    const int max_merges = std::min(256, vocab - 256 - 3);
+    for (int m = 0; m < max_merges; ++m) {
+        std::map<std::pair<std::string, std::string>, int> counts;
+        for (const auto& w : words)
+            for (std::size_t k = 0; k + 1 < w.size(); ++k) ++counts[{w[k], w[k + 1]}];
+        const std::pair<std::string, std::string>* best = nullptr;
+        int best_n = 1;
+        for (const auto& [pair, n] : counts)
+            if (n > best_n) {   // map order: ties keep the smaller pair
+                best_n = n;
+                best = &pair;
+            }
+        if (!best) break;
+        const std::string a = best->first, b = best->second;
+        v.merges.push_back(a + " " + b);
+        v.tokens.push_back(a + b);
+        v.types.push_back(1);
+        for (auto& w : words) {
+            std::vector<std::string> nw;
+            for (std::size_t k = 0; k < w.size();) {
+                if (k + 1 < w.size() && w[k] == a && w[k + 1] == b) {
+                    nw.push_back(a + b);
+                    k += 2;
+                } else {
+                    nw.push_back(w[k++]);
+                }
+            }
+            w = std::move(nw);
+        }
+    }
+    for (const char* sp : {"<|endoftext|>", "<|im_start|>", "<|im_end|>"}) {
+        v.tokens.push_back(sp);
+        v.types.push_back(3);
+    }
+    for (int i = 0; static_cast<int>(v.tokens.size()) < vocab; ++i) {
+        v.tokens.push_back("<|reserved_" + std::to_string(i) + "|>");
+        v.types.push_back(1);
+    }
+    return v;
+}
+
+}  // namespace
+
 std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
     if (s.hidden <= 0 || s.intermediate <= 0 || s.layers <= 0 || s.vocab <= 0 || s.n_q <= 0 || s.n_kv <= 0 ||
         s.head_dim <= 0)
@@ -225,6 +329,19 @@ std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
     w.add_f32("qwen3.rope.freq_base", s.theta);
     w.add_u32("qwen3.context_length", static_cast<std::uint32_t>(s.context));
     w.add_u32("qwen3.vocab_size", static_cast<std::uint32_t>(s.vocab));
+    if (s.vocab >= 256 + 3) {
+        const SynthVocab tv = synth_vocab(s.vocab);
+        w.add_string("tokenizer.ggml.model", "gpt2");
+        w.add_string("tokenizer.ggml.pre", "qwen2");
+        w.add_string_array("tokenizer.ggml.tokens", tv.tokens);
+        w.add_i32_array("tokenizer.ggml.token_type", tv.types);
+        w.add_string_array("tokenizer.ggml.merges", tv.merges);
+        const auto id_of = [&](const char* t) {
+            return static_cast<std::uint32_t>(std::find(tv.tokens.begin(), tv.tokens.end(), t) - tv.tokens.begin());
+        };
+        w.add_u32("tokenizer.ggml.eos_token_id", id_of("<|im_end|>"));
+        w.add_u32("tokenizer.ggml.padding_token_id", id_of("<|endoftext|>"));
+    }
 
     struct Item {
         std::string name;

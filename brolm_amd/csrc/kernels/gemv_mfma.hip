@@ -231,9 +231,8 @@ struct Chunk<FMT_F16> {
     }
 };
 
-template <int FMT> struct SliceLen { static constexpr int SB = 2; };
-template <> struct SliceLen<FMT_Q4_K> { static constexpr int SB = 4; };
-template <> struct SliceLen<FMT_Q6_K> { static constexpr int SB = 1; };
+// chunks per slice (per buffer): two, one for Q6_K (register budget)
+template <int FMT> struct SliceLen { static constexpr int SB = FMT == FMT_Q6_K ? 1 : 2; };
 
 // A wavefront's walk over slices: tiles tile0, tile0 + tstride, ... below
 // tiles; in each tile the chunks [c0, c1) in slices of SB.
@@ -264,7 +263,9 @@ struct SliceBuf {
                                          int g) {
         int64_t n = w.tile * 16 + r;
         if (n >= N) n = N - 1;
-        bias = bias_p ? ldg_u16(bias_p + n) : 0u;
+        // unconditional (a dummy in-bounds address without bias): a load under
+        // a branch would make the compiler wait for every load before it
+        bias = ldg_u16(bias_p ? bias_p + n : static_cast<const uint16_t*>(W));
 #pragma unroll
         for (int i = 0; i < SB; ++i) {
             const int b = w.cb + i < w.c1 ? w.cb + i : w.c1 - 1;   // clamped: every load is issued
@@ -364,14 +365,14 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
         for (;;) {
             Walk nx = w.next(SB);
             b1.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
-            if (w.cb == w.c0) bv = h2f(b0.bias & 0xffff);
+            if (w.cb == w.c0) bv = bias ? h2f(b0.bias & 0xffff) : 0.f;
             b0.mul(xst, w, r, g, acc);
             if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
             w = nx;
             if (!w.valid()) break;
             nx = w.next(SB);
             b0.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
-            if (w.cb == w.c0) bv = h2f(b1.bias & 0xffff);
+            if (w.cb == w.c0) bv = bias ? h2f(b1.bias & 0xffff) : 0.f;
             b1.mul(xst, w, r, g, acc);
             if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
             w = nx;

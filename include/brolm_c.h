@@ -98,6 +98,34 @@ void brolm_profile_reset(void);
 void brolm_profile_report(void);
 int brolm_profile_enabled(void);
 
+/* qwen::Tokenizer (include/brolm/qwen_tokenizer.h; reference
+ * include/brolm/qwen_tokenizer.h:41-151).  A handle from one of the three
+ * loaders; NULL on failure (brolm_last_error).  `extra_specials` is a
+ * '\n'-separated list of extra special-token names or NULL. */
+typedef struct brolm_tokenizer brolm_tokenizer;
+brolm_tokenizer* brolm_tokenizer_load(const char* vocab_json, const char* merges_txt, const char* extra_specials);
+brolm_tokenizer* brolm_tokenizer_from_gguf(const char* gguf_path, const char* extra_specials);
+brolm_tokenizer* brolm_tokenizer_from_json(const char* tokenizer_json, const char* extra_specials);
+void brolm_tokenizer_free(brolm_tokenizer* t);
+/* encode: writes up to cap ids, returns the total count (may exceed cap) or -1. */
+int brolm_tokenizer_encode(const brolm_tokenizer* t, const char* text, int64_t len, int add_special, int32_t* ids,
+                           int cap);
+/* decode: writes up to cap bytes (not NUL-terminated), returns the total byte
+ * count (may exceed cap) or -1. */
+int64_t brolm_tokenizer_decode(const brolm_tokenizer* t, const int32_t* ids, int n, char* out, int64_t cap);
+/* apply_chat_template over n (role, content) pairs; same return convention. */
+int64_t brolm_tokenizer_chat(const brolm_tokenizer* t, const char* const* roles, const char* const* contents, int n,
+                             int add_generation_prompt, char* out, int64_t cap);
+int brolm_tokenizer_register_special(brolm_tokenizer* t, const char* token, int32_t id);
+/* info[6] = {vocab_count, merge_count, eos_id, im_start_id, im_end_id, endoftext_id}. */
+int brolm_tokenizer_info(const brolm_tokenizer* t, int64_t* info);
+/* qwen::generate_text (reference src/qwen_generate.cpp:19-25): encode(prompt),
+ * generate with eos = tok.eos_id(), decode the new ids; same return
+ * convention as brolm_tokenizer_decode. */
+int64_t brolm_qwen3_generate_text(brolm_qwen3* m, const brolm_tokenizer* t, const char* prompt, int max_new,
+                                  int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
+                                  char* out, int64_t cap);
+
 #ifdef __cplusplus
 }
 #endif

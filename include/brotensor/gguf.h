@@ -90,6 +90,7 @@ public:
     void add_f32(const std::string& key, float v);
     void add_bool(const std::string& key, bool v);
     void add_string_array(const std::string& key, const std::vector<std::string>& v);
+    void add_i32_array(const std::string& key, const std::vector<std::int32_t>& v);
     // dims in ggml order (dims[0] = row length); bytes must match the type.
     void add_tensor(const std::string& name, Dtype dt, const std::vector<std::int64_t>& dims,
                     std::vector<std::uint8_t> bytes);

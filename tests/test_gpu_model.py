@@ -148,6 +148,41 @@ def test_generate_lengths_eos_and_sampling(ba, small_gguf):
     assert o1 == o2 and len(o1) == 10
 
 
+def test_generate_text_matches_oracle(ba, small_gguf):
+    """qwen::generate_text (src/qwen_generate.cpp:19-25) on the checkpoint's own
+    tokenizer: the prompt encodes to the oracle tokenizer's ids, the text is the
+    decode of the greedy ids (oracle tokenizer, same bytes), and each greedy id
+    is the oracle model's teacher-forced argmax wherever its top-2 gap is
+    resolvable at the logit tolerance."""
+    from gguf_meta import read_metadata
+    from oracle import tokenizer as otok
+    meta = read_metadata(str(small_gguf))
+    orc_tok = otok.Tokenizer.from_lists(meta["tokenizer.ggml.tokens"], meta["tokenizer.ggml.merges"],
+                                        meta["tokenizer.ggml.token_type"])
+    tok = ba.Tokenizer.from_gguf(str(small_gguf))
+    m = _load(ba, small_gguf)
+    om = oracle.Model(str(small_gguf))
+    for prompt in ("The model reads the tokens of the prompt.", "<|im_start|>user\nhi cat<|im_end|>\n"):
+        ids = tok.encode(prompt)
+        assert ids == orc_tok.encode(prompt)
+        opts = ba.GenerateOptions(max_new_tokens=16, sampling=ba.SamplingParams(temperature=0.0))
+        text = ba.generate_text(m, tok, prompt, opts)
+        gen = ba.generate(m, ids, tok.eos_id(), opts)
+        assert text == tok.decode(gen)
+        assert tok.decode_bytes(gen) == orc_tok.decode_bytes(gen)
+        om.reset_cache()
+        om.allocate_cache(len(ids) + len(gen) + 1)
+        rows = om.forward(ids + gen[:-1])[len(ids) - 1:]
+        checked = 0
+        for t, row in zip(gen, rows):
+            a, _ = oracle.argmax(row)
+            top2 = np.sort(row)[-2:]
+            if top2[1] - top2[0] > 2 * LOGIT_TOL:
+                assert t == a
+                checked += 1
+        assert checked >= 1
+
+
 def _session(m, env: dict) -> str:
     """Create the model's step session under `env` (the switches are read when
     the session is created) and return its mode."""
