@@ -1,7 +1,8 @@
 """brolm_amd — MI355X-native implementation of brolm's quantized Qwen3 decode path.
 
 Python mirror of the C++ API (reference include/brolm/qwen.h,
-include/brolm/qwen_generate.h, include/brolm/detail/generate.h) over the C ABI
+include/brolm/qwen_generate.h, include/brolm/detail/generate.h,
+include/brolm/mistral3_text.h, include/brolm/mistral3_config.h) over the C ABI
 of libbrolm.so.  All compute runs in the native libraries on a gfx950 device;
 there is no Python or CPU fallback.
 """
@@ -19,7 +20,8 @@ from ._native import check
 GGML = {"F32": 0, "F16": 1, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "BF16": 30}
 
 __all__ = ["Qwen3Config", "Qwen3Model", "SamplingParams", "GenerateOptions", "generate", "sample_token",
-           "qwen3_hf_to_ggml", "SynthSpec", "write_synth_qwen3", "init", "GGML"]
+           "qwen3_hf_to_ggml", "SynthSpec", "write_synth_qwen3", "init", "GGML", "Mistral3Config",
+           "Mistral3TextConfig", "Mistral3TextModel", "mistral3_hf_to_ggml", "write_synth_mistral3"]
 
 
 def init() -> None:
@@ -166,6 +168,96 @@ class Qwen3Model:
         """Which single-token step path runs: "persistent", "graph" or "eager"."""
         m = check(_native.lib().brolm_qwen3_decode_mode(self._h), "decode_mode")
         return ("eager", "graph", "persistent")[m]
+
+
+@dataclass
+class Mistral3TextConfig:
+    """Mistral3Config::Text (include/brolm/mistral3_config.h:38-58); defaults
+    are Mistral-Small-3.1-24B."""
+    vocab_size: int = 131072
+    hidden_size: int = 5120
+    intermediate_size: int = 32768
+    num_hidden_layers: int = 40
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 1.0e9
+    tie_word_embeddings: bool = False
+    max_position_embeddings: int = 131072
+    has_sliding_window: bool = False
+    sliding_window: int = 0
+
+    _INT = ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+            "num_key_value_heads", "head_dim", "max_position_embeddings", "sliding_window")
+
+    def _c(self) -> _native.Mistral3TextConfigC:
+        c = _native.Mistral3TextConfigC()
+        for f in self._INT:
+            setattr(c, f, int(getattr(self, f)))
+        c.rms_norm_eps = float(self.rms_norm_eps)
+        c.rope_theta = float(self.rope_theta)
+        c.tie_word_embeddings = 1 if self.tie_word_embeddings else 0
+        c.has_sliding_window = 1 if self.has_sliding_window else 0
+        return c
+
+    @classmethod
+    def _from_c(cls, c: _native.Mistral3TextConfigC) -> "Mistral3TextConfig":
+        out = cls(**{f: getattr(c, f) for f in cls._INT})
+        out.rms_norm_eps, out.rope_theta = c.rms_norm_eps, c.rope_theta
+        out.tie_word_embeddings = bool(c.tie_word_embeddings)
+        out.has_sliding_window = bool(c.has_sliding_window)
+        return out
+
+
+@dataclass
+class Mistral3Config:
+    """Mistral3Config (include/brolm/mistral3_config.h:30-143): the text
+    section and the multimodal glue (no Pixtral vision section here)."""
+    text: Mistral3TextConfig = field(default_factory=Mistral3TextConfig)
+    image_token_index: int = 10
+    spatial_merge_size: int = 2
+    multimodal_projector_bias: bool = False
+
+    @classmethod
+    def _from_c(cls, c: _native.Mistral3ConfigC) -> "Mistral3Config":
+        return cls(Mistral3TextConfig._from_c(c.text), c.image_token_index, c.spatial_merge_size,
+                   bool(c.multimodal_projector_bias))
+
+    @classmethod
+    def from_gguf(cls, path: str) -> "Mistral3Config":
+        c = _native.Mistral3ConfigC()
+        check(_native.lib().brolm_mistral3_config_from_gguf(str(path).encode(), C.byref(c)), "from_gguf")
+        return cls._from_c(c)
+
+    @classmethod
+    def from_json_text(cls, text: str) -> "Mistral3Config":
+        c = _native.Mistral3ConfigC()
+        check(_native.lib().brolm_mistral3_config_from_json(text.encode(), C.byref(c)), "from_json_text")
+        return cls._from_c(c)
+
+    @classmethod
+    def load(cls, path: str) -> "Mistral3Config":
+        with open(path, encoding="utf-8") as f:
+            return cls.from_json_text(f.read())
+
+
+def mistral3_hf_to_ggml(hf_name: str) -> str:
+    buf = C.create_string_buffer(256)
+    n = _native.lib().brolm_mistral3_hf_to_ggml(hf_name.encode(), buf, 256)
+    return buf.value.decode() if n > 0 else ""
+
+
+class Mistral3TextModel(Qwen3Model):
+    """mistral3::TextModel (include/brolm/mistral3_text.h:52-131): the dense
+    decoder without QK-norm, untied lm_head; same forward / cache / decode
+    surface as Qwen3Model (one shared decoder handle type)."""
+
+    def __init__(self, cfg: Mistral3TextConfig):
+        self.cfg = cfg
+        self._h = _native.lib().brolm_mistral3_text_create(C.byref(cfg._c()))
+        if not self._h:
+            raise _native.NativeError(_native.lib().brolm_last_error().decode())
 
 
 @dataclass
@@ -345,7 +437,7 @@ class SynthSpec:
     seed: int = 0
 
 
-def write_synth_qwen3(spec: SynthSpec, path: str) -> None:
+def _synth_c(spec: SynthSpec) -> _native.SynthSpecC:
     s = _native.SynthSpecC()
     for f in ("vocab", "hidden", "intermediate", "layers", "n_q", "n_kv", "head_dim", "context"):
         setattr(s, f, int(getattr(spec, f)))
@@ -354,4 +446,15 @@ def write_synth_qwen3(spec: SynthSpec, path: str) -> None:
     for f in ("embed", "q", "k", "v", "o", "gate", "up", "down", "output"):
         setattr(s, f + "_type", GGML[getattr(spec, f)])
     s.seed = int(spec.seed)
-    check(_native.lib().brolm_synth_qwen3_write(C.byref(s), str(path).encode()), "write_synth_qwen3")
+    return s
+
+
+def write_synth_qwen3(spec: SynthSpec, path: str) -> None:
+    check(_native.lib().brolm_synth_qwen3_write(C.byref(_synth_c(spec)), str(path).encode()), "write_synth_qwen3")
+
+
+def write_synth_mistral3(spec: SynthSpec, path: str) -> None:
+    """Mistral 3.1 text checkpoint: the same tensors under general.architecture
+    "llama", without per-head QK-norm gammas; untied when spec.tied is False."""
+    check(_native.lib().brolm_synth_mistral3_write(C.byref(_synth_c(spec)), str(path).encode()),
+          "write_synth_mistral3")

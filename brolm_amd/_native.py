@@ -28,6 +28,19 @@ class Qwen3ConfigC(C.Structure):
         ("tie_word_embeddings", C.c_int), ("max_position_embeddings", C.c_int)]
 
 
+class Mistral3TextConfigC(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers",
+                                        "num_attention_heads", "num_key_value_heads", "head_dim")] + [
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float)] + [
+        (n, C.c_int) for n in ("tie_word_embeddings", "max_position_embeddings", "has_sliding_window",
+                               "sliding_window")]
+
+
+class Mistral3ConfigC(C.Structure):
+    _fields_ = [("text", Mistral3TextConfigC)] + [
+        (n, C.c_int) for n in ("image_token_index", "spatial_merge_size", "multimodal_projector_bias")]
+
+
 class SynthSpecC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "hidden", "intermediate", "layers", "n_q", "n_kv", "head_dim")] + [
         ("eps", C.c_float), ("theta", C.c_float), ("context", C.c_int), ("tied", C.c_int)] + [
@@ -38,7 +51,8 @@ class SynthSpecC(C.Structure):
 class DecodeDimsC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("hidden", "intermediate", "n_q", "n_kv", "head_dim", "vocab", "cap")] + [
         ("eps", C.c_float)] + [(n, C.c_int) for n in ("qkv_type_q", "qkv_type_k", "qkv_type_v", "o_type",
-                                                      "gate_type", "up_type", "down_type", "lm_type")]
+                                                      "gate_type", "up_type", "down_type", "lm_type",
+                                                      "no_qk_norm")]
 
 
 # symbol -> (restype, argtypes); every symbol of include/brolm_hip.h
@@ -96,6 +110,11 @@ C_SYMBOLS = {
     "brolm_gguf_tensor_count": (C.c_int, [cp, P_i64]),
     "brolm_gguf_tensor_info": (C.c_int, [cp, cp, C.POINTER(C.c_int), P_i64, C.POINTER(C.c_int), P_i64]),
     "brolm_qwen3_create": (vp, [C.POINTER(Qwen3ConfigC)]),
+    "brolm_mistral3_config_from_gguf": (C.c_int, [cp, C.POINTER(Mistral3ConfigC)]),
+    "brolm_mistral3_config_from_json": (C.c_int, [cp, C.POINTER(Mistral3ConfigC)]),
+    "brolm_mistral3_hf_to_ggml": (C.c_int, [cp, C.c_char_p, C.c_int]),
+    "brolm_synth_mistral3_write": (C.c_int, [C.POINTER(SynthSpecC), cp]),
+    "brolm_mistral3_text_create": (vp, [C.POINTER(Mistral3TextConfigC)]),
     "brolm_qwen3_free": (None, [vp]),
     "brolm_qwen3_load_gguf": (C.c_int, [vp, cp]),
     "brolm_qwen3_allocate_cache": (C.c_int, [vp, C.c_int]),

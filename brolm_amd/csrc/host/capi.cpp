@@ -1,4 +1,4 @@
-// C facade of the Qwen3 stack (include/brolm_c.h).
+// C facade of the Qwen3 and Mistral 3.1 text stacks (include/brolm_c.h).
 #include "brolm_c.h"
 
 #include <algorithm>
@@ -10,6 +10,8 @@
 #include <vector>
 
 #include "brolm/detail/profile.h"
+#include "brolm/mistral3_generate.h"
+#include "brolm/mistral3_text.h"
 #include "brolm/qwen.h"
 #include "brolm/qwen_generate.h"
 #include "brolm/qwen_tokenizer.h"
@@ -17,8 +19,12 @@
 #include "brotensor/gguf.h"
 #include "brotensor/runtime.h"
 
+// A decoder handle: holds a Qwen3Model or a Mistral 3.1 TextModel; both
+// wrap one DenseDecoder.
 struct brolm_qwen3 {
     std::unique_ptr<brolm::qwen::Qwen3Model> model;
+    std::unique_ptr<brolm::mistral3::TextModel> mistral;
+    brolm::detail::DenseDecoder* core = nullptr;
 };
 
 struct brolm_tokenizer {
@@ -78,8 +84,14 @@ void to_host_f32(const brotensor::Tensor& t, float* dst) {
 }
 
 brolm::qwen::Qwen3Model& model_of(brolm_qwen3* m) {
-    if (!m || !m->model) throw std::runtime_error("null model handle");
+    if (!m || !m->core) throw std::runtime_error("null model handle");
+    if (!m->model) throw std::runtime_error("this call needs a Qwen3 model handle");
     return *m->model;
+}
+
+brolm::detail::DenseDecoder& core_of(brolm_qwen3* m) {
+    if (!m || !m->core) throw std::runtime_error("null model handle");
+    return *m->core;
 }
 
 }  // namespace
@@ -129,7 +141,9 @@ int brolm_init(void) {
     return guard([] { brotensor::init(); });
 }
 
-int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* s, const char* path) {
+namespace {
+
+int synth_write(const brolm_synth_qwen3_spec* s, const char* path, const char* arch) {
     return guard([&] {
         if (!s || !path) throw std::runtime_error("synth: null argument");
         brolm::synth::Qwen3Spec q;
@@ -147,8 +161,19 @@ int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* s, const char* path) {
         q.output = brotensor::dtype_from_ggml(s->output_type);
         q.stddev = s->stddev;
         q.seed = s->seed;
+        q.arch = arch;
         brolm::synth::write_qwen3_gguf(q, path);
     });
+}
+
+}  // namespace
+
+int brolm_synth_mistral3_write(const brolm_synth_qwen3_spec* s, const char* path) {
+    return synth_write(s, path, "llama");
+}
+
+int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* s, const char* path) {
+    return synth_write(s, path, "qwen3");
 }
 
 int brolm_synth_normal_bf16(uint64_t key, int64_t n, float stddev, float* out) {
@@ -204,6 +229,70 @@ brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg) {
         if (!cfg) throw std::runtime_error("null config");
         auto h = std::make_unique<brolm_qwen3>();
         h->model = std::make_unique<brolm::qwen::Qwen3Model>(to_cfg(*cfg));
+        h->core = &h->model->core();
+        out = h.release();
+    });
+    return rc == 0 ? out : nullptr;
+}
+
+namespace {
+
+void from_m3(const brolm::mistral3::Mistral3Config& m, brolm_mistral3_config* c) {
+    const auto& t = m.text;
+    brolm_mistral3_text_config& o = c->text;
+    o.vocab_size = t.vocab_size; o.hidden_size = t.hidden_size; o.intermediate_size = t.intermediate_size;
+    o.num_hidden_layers = t.num_hidden_layers; o.num_attention_heads = t.num_attention_heads;
+    o.num_key_value_heads = t.num_key_value_heads; o.head_dim = t.head_dim;
+    o.rms_norm_eps = t.rms_norm_eps; o.rope_theta = t.rope_theta;
+    o.tie_word_embeddings = t.tie_word_embeddings ? 1 : 0; o.max_position_embeddings = t.max_position_embeddings;
+    o.has_sliding_window = t.has_sliding_window ? 1 : 0; o.sliding_window = t.sliding_window;
+    c->image_token_index = m.image_token_index;
+    c->spatial_merge_size = m.spatial_merge_size;
+    c->multimodal_projector_bias = m.multimodal_projector_bias ? 1 : 0;
+}
+
+}  // namespace
+
+int brolm_mistral3_config_from_gguf(const char* path, brolm_mistral3_config* out) {
+    return guard([&] {
+        if (!path || !out) throw std::runtime_error("null argument");
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        from_m3(brolm::mistral3::Mistral3Config::from_gguf(f), out);
+    });
+}
+
+int brolm_mistral3_config_from_json(const char* text, brolm_mistral3_config* out) {
+    return guard([&] {
+        if (!text || !out) throw std::runtime_error("null argument");
+        from_m3(brolm::mistral3::Mistral3Config::from_json_text(text), out);
+    });
+}
+
+int brolm_mistral3_hf_to_ggml(const char* hf_name, char* out, int cap) {
+    const std::string s = brolm::mistral3::mistral3_hf_to_ggml(hf_name ? hf_name : "");
+    if (out && cap > 0) {
+        const std::size_t n = std::min<std::size_t>(s.size(), static_cast<std::size_t>(cap - 1));
+        std::memcpy(out, s.data(), n);
+        out[n] = 0;
+    }
+    return static_cast<int>(s.size());
+}
+
+brolm_qwen3* brolm_mistral3_text_create(const brolm_mistral3_text_config* cfg) {
+    brolm_qwen3* out = nullptr;
+    const int rc = guard([&] {
+        if (!cfg) throw std::runtime_error("null config");
+        brolm::mistral3::Mistral3Config::Text t;
+        t.vocab_size = cfg->vocab_size; t.hidden_size = cfg->hidden_size;
+        t.intermediate_size = cfg->intermediate_size; t.num_hidden_layers = cfg->num_hidden_layers;
+        t.num_attention_heads = cfg->num_attention_heads; t.num_key_value_heads = cfg->num_key_value_heads;
+        t.head_dim = cfg->head_dim; t.rms_norm_eps = cfg->rms_norm_eps; t.rope_theta = cfg->rope_theta;
+        t.tie_word_embeddings = cfg->tie_word_embeddings != 0;
+        t.max_position_embeddings = cfg->max_position_embeddings;
+        t.has_sliding_window = cfg->has_sliding_window != 0; t.sliding_window = cfg->sliding_window;
+        auto h = std::make_unique<brolm_qwen3>();
+        h->mistral = std::make_unique<brolm::mistral3::TextModel>(t);
+        h->core = &h->mistral->core();
         out = h.release();
     });
     return rc == 0 ? out : nullptr;
@@ -215,19 +304,21 @@ int brolm_qwen3_load_gguf(brolm_qwen3* m, const char* path) {
     return guard([&] {
         brotensor::init();
         const brotensor::gguf::File f = brotensor::gguf::File::open(path);
-        model_of(m).load_weights(f);
+        core_of(m);
+        if (m->model) m->model->load_weights(f);
+        else m->mistral->load_weights(f);
     });
 }
 
-int brolm_qwen3_allocate_cache(brolm_qwen3* m, int n) { return guard([&] { model_of(m).allocate_cache(n); }); }
-int brolm_qwen3_reset_cache(brolm_qwen3* m) { return guard([&] { model_of(m).reset_cache(); }); }
-int brolm_qwen3_truncate_cache(brolm_qwen3* m, int n) { return guard([&] { model_of(m).truncate_cache(n); }); }
-int brolm_qwen3_cache_len(const brolm_qwen3* m) { return (m && m->model) ? m->model->cache_len() : -1; }
+int brolm_qwen3_allocate_cache(brolm_qwen3* m, int n) { return guard([&] { core_of(m).allocate_cache(n); }); }
+int brolm_qwen3_reset_cache(brolm_qwen3* m) { return guard([&] { core_of(m).reset_cache(); }); }
+int brolm_qwen3_truncate_cache(brolm_qwen3* m, int n) { return guard([&] { core_of(m).truncate_cache(n); }); }
+int brolm_qwen3_cache_len(const brolm_qwen3* m) { return (m && m->core) ? m->core->cache_len() : -1; }
 
 int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits, float* hidden) {
     return guard([&] {
         brotensor::Tensor lg, hd;
-        model_of(m).forward(ids, L, lg, hidden ? &hd : nullptr);
+        core_of(m).forward(ids, L, lg, hidden ? &hd : nullptr);
         if (logits) to_host_f32(lg, logits);
         if (hidden) to_host_f32(hd, hidden);
     });
@@ -236,7 +327,7 @@ int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits
 int brolm_qwen3_forward_last(brolm_qwen3* m, const int32_t* ids, int L, float* logits) {
     return guard([&] {
         brotensor::Tensor lg;
-        model_of(m).forward_last(ids, L, lg);
+        core_of(m).forward_last(ids, L, lg);
         if (logits) to_host_f32(lg, logits);
     });
 }
@@ -244,14 +335,14 @@ int brolm_qwen3_forward_last(brolm_qwen3* m, const int32_t* ids, int L, float* l
 int brolm_qwen3_embed_tokens(brolm_qwen3* m, const int32_t* ids, int L, uint16_t* out) {
     return guard([&] {
         brotensor::Tensor e;
-        model_of(m).embed_tokens(ids, L, e);
+        core_of(m).embed_tokens(ids, L, e);
         e.copy_to_host_fp16(out);
     });
 }
 
 int brolm_qwen3_forward_embeds(brolm_qwen3* m, const uint16_t* embeds, int L, float* logits, float* hidden) {
     return guard([&] {
-        brolm::qwen::Qwen3Model& q = model_of(m);
+        brolm::detail::DenseDecoder& q = core_of(m);
         brotensor::Tensor e = brotensor::Tensor::from_host_fp16(embeds, L, q.config().hidden_size);
         brotensor::Tensor lg, hd;
         q.forward_embeds(e, L, lg, hidden ? &hd : nullptr);
@@ -274,7 +365,7 @@ int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, in
         o.sampling.seed = seed;
         o.device_greedy = device_greedy != 0;
         const std::vector<int32_t> p(prompt, prompt + (n_prompt > 0 ? n_prompt : 0));
-        const std::vector<int32_t> g = brolm::qwen::generate(model_of(m), p, eos_id, o);
+        const std::vector<int32_t> g = brolm::detail::generate(core_of(m), p, eos_id, o);
         std::memcpy(out, g.data(), g.size() * sizeof(int32_t));
         count = static_cast<int>(g.size());
     });
@@ -376,23 +467,23 @@ int64_t brolm_qwen3_generate_text(brolm_qwen3* m, const brolm_tokenizer* t, cons
 
 int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id) {
     int count = -1;
-    const int rc = guard([&] { count = model_of(m).core().decode_greedy(token, n, out, eos_id); });
+    const int rc = guard([&] { count = core_of(m).decode_greedy(token, n, out, eos_id); });
     return rc == 0 ? count : -1;
 }
 
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n) {
     double ms = -1.0;
-    const int rc = guard([&] { ms = model_of(m).core().time_decode_steps(token, n); });
+    const int rc = guard([&] { ms = core_of(m).time_decode_steps(token, n); });
     return rc == 0 ? ms : -1.0;
 }
 
 int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m) {
-    return (m && m->model) ? const_cast<brolm::qwen::Qwen3Model&>(*m->model).core().decode_weight_bytes() : -1;
+    return (m && m->core) ? m->core->decode_weight_bytes() : -1;
 }
 
 int brolm_qwen3_decode_mode(brolm_qwen3* m) {
     int mode = -1;
-    const int rc = guard([&] { mode = model_of(m).core().decode_mode(); });
+    const int rc = guard([&] { mode = core_of(m).decode_mode(); });
     return rc == 0 ? mode : -1;
 }
 

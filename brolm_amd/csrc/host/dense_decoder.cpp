@@ -228,7 +228,8 @@ void DenseDecoder::forward_last(const int32_t* ids, int L, bt::Tensor& logits_ou
         d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
         d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
         d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
-        if (cfg_.use_qk_norm && bx_decode_ws_bytes(&d) != 0) {
+        d.no_qk_norm = cfg_.use_qk_norm ? 0 : 1;
+        if (bx_decode_ws_bytes(&d) != 0) {
             decode_step_(ids[0], logits_out);
             return;
         }
@@ -360,6 +361,7 @@ DecodeGraphSession& DenseDecoder::session_() {
     d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
     d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
     d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
+    d.no_qk_norm = cfg_.use_qk_norm ? 0 : 1;
     for (const Layer& L : layers_) {
         if (ggml_of(L.Wq) != d.qkv_type_q || ggml_of(L.Wk) != d.qkv_type_k || ggml_of(L.Wv) != d.qkv_type_v ||
             ggml_of(L.Wo) != d.o_type || ggml_of(L.gate_W) != d.gate_type || ggml_of(L.up_W) != d.up_type ||

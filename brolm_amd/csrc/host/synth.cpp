@@ -315,20 +315,23 @@ std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
     if (s.hidden <= 0 || s.intermediate <= 0 || s.layers <= 0 || s.vocab <= 0 || s.n_q <= 0 || s.n_kv <= 0 ||
         s.head_dim <= 0)
         throw std::runtime_error("synth: non-positive dimension");
+    if (s.arch.empty()) throw std::runtime_error("synth: empty architecture name");
+    const bool qk_norm = s.arch == "qwen3";
+    const std::string a = s.arch + ".";
     bt::gguf::Writer w;
-    w.add_string("general.architecture", "qwen3");
-    w.add_string("general.name", "brolm-synthetic-qwen3");
-    w.add_u32("qwen3.embedding_length", static_cast<std::uint32_t>(s.hidden));
-    w.add_u32("qwen3.feed_forward_length", static_cast<std::uint32_t>(s.intermediate));
-    w.add_u32("qwen3.block_count", static_cast<std::uint32_t>(s.layers));
-    w.add_u32("qwen3.attention.head_count", static_cast<std::uint32_t>(s.n_q));
-    w.add_u32("qwen3.attention.head_count_kv", static_cast<std::uint32_t>(s.n_kv));
-    w.add_u32("qwen3.attention.key_length", static_cast<std::uint32_t>(s.head_dim));
-    w.add_u32("qwen3.attention.value_length", static_cast<std::uint32_t>(s.head_dim));
-    w.add_f32("qwen3.attention.layer_norm_rms_epsilon", s.eps);
-    w.add_f32("qwen3.rope.freq_base", s.theta);
-    w.add_u32("qwen3.context_length", static_cast<std::uint32_t>(s.context));
-    w.add_u32("qwen3.vocab_size", static_cast<std::uint32_t>(s.vocab));
+    w.add_string("general.architecture", s.arch);
+    w.add_string("general.name", "brolm-synthetic-" + s.arch);
+    w.add_u32(a + "embedding_length", static_cast<std::uint32_t>(s.hidden));
+    w.add_u32(a + "feed_forward_length", static_cast<std::uint32_t>(s.intermediate));
+    w.add_u32(a + "block_count", static_cast<std::uint32_t>(s.layers));
+    w.add_u32(a + "attention.head_count", static_cast<std::uint32_t>(s.n_q));
+    w.add_u32(a + "attention.head_count_kv", static_cast<std::uint32_t>(s.n_kv));
+    w.add_u32(a + "attention.key_length", static_cast<std::uint32_t>(s.head_dim));
+    w.add_u32(a + "attention.value_length", static_cast<std::uint32_t>(s.head_dim));
+    w.add_f32(a + "attention.layer_norm_rms_epsilon", s.eps);
+    w.add_f32(a + "rope.freq_base", s.theta);
+    w.add_u32(a + "context_length", static_cast<std::uint32_t>(s.context));
+    w.add_u32(a + "vocab_size", static_cast<std::uint32_t>(s.vocab));
     if (s.vocab >= 256 + 3) {
         const SynthVocab tv = synth_vocab(s.vocab);
         w.add_string("tokenizer.ggml.model", "gpt2");
@@ -359,8 +362,10 @@ std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
         items.push_back({p + "attn_k.weight", s.k, kvd, H, false});
         items.push_back({p + "attn_v.weight", s.v, kvd, H, false});
         items.push_back({p + "attn_output.weight", s.o, H, qd, false});
-        items.push_back({p + "attn_q_norm.weight", bt::Dtype::FP32, 1, s.head_dim, true});
-        items.push_back({p + "attn_k_norm.weight", bt::Dtype::FP32, 1, s.head_dim, true});
+        if (qk_norm) {
+            items.push_back({p + "attn_q_norm.weight", bt::Dtype::FP32, 1, s.head_dim, true});
+            items.push_back({p + "attn_k_norm.weight", bt::Dtype::FP32, 1, s.head_dim, true});
+        }
         items.push_back({p + "ffn_norm.weight", bt::Dtype::FP32, 1, H, true});
         items.push_back({p + "ffn_gate.weight", s.gate, F, H, false});
         items.push_back({p + "ffn_up.weight", s.up, F, H, false});
@@ -393,6 +398,11 @@ void write_qwen3_gguf(const Qwen3Spec& spec, const std::string& path) {
     if (!f) throw std::runtime_error("synth: cannot write '" + path + "'");
     f.write(reinterpret_cast<const char*>(b.data()), static_cast<std::streamsize>(b.size()));
     if (!f) throw std::runtime_error("synth: short write to '" + path + "'");
+}
+
+void write_mistral3_gguf(Qwen3Spec spec, const std::string& path) {
+    spec.arch = "llama";
+    write_qwen3_gguf(spec, path);
 }
 
 }  // namespace brolm::synth

@@ -223,16 +223,27 @@ __global__ BX_GEMV_BOUNDS void norm_head_kernel(const float* __restrict__ h, con
 
 // Per-head RMSNorm of an hd-long FP32 vector (one wavefront), RoPE at the
 // table row, optional FP16 rounding (the value the cache will hold), scale.
+// gamma == nullptr: no norm; the head is the projection output rounded to
+// FP16 (the op path stores q and k in FP16 before RoPE).
 __device__ void head_norm_rope(const float* src, const uint16_t* gamma, float eps, int hd, const float* cos_row,
                                const float* sin_row, float* dst, bool round16, float post_scale) {
     const int lane = threadIdx.x & 63;
-    float ss = 0.f;
-    for (int d = lane; d < hd; d += 64) ss += src[d] * src[d];
-    ss = wave_allsum(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    float inv = 1.0f;
+    if (gamma) {
+        float ss = 0.f;
+        for (int d = lane; d < hd; d += 64) ss += src[d] * src[d];
+        ss = wave_allsum(ss);
+        inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
     for (int p = lane; p < hd / 2; p += 64) {
-        float x0 = src[2 * p] * inv * h2f(gamma[2 * p]);
-        float x1 = src[2 * p + 1] * inv * h2f(gamma[2 * p + 1]);
+        float x0, x1;
+        if (gamma) {
+            x0 = src[2 * p] * inv * h2f(gamma[2 * p]);
+            x1 = src[2 * p + 1] * inv * h2f(gamma[2 * p + 1]);
+        } else {
+            x0 = h2f(f2h(src[2 * p]));
+            x1 = h2f(f2h(src[2 * p + 1]));
+        }
         if (round16) { x0 = h2f(f2h(x0)); x1 = h2f(f2h(x1)); }
         const float c = cos_row[p], s = sin_row[p];
         float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
@@ -562,8 +573,8 @@ int bx_decode_layer_run(const bx_decode_dims* d, const bx_decode_layer* L, const
     const int G = d->n_q / d->n_kv;
     const dim3 agrid(w.S, d->n_kv);
     const size_t alds = attn_lds(G, hd);
-    const auto* qn = static_cast<const uint16_t*>(L->q_norm);
-    const auto* kn = static_cast<const uint16_t*>(L->k_norm);
+    const auto* qn = d->no_qk_norm ? nullptr : static_cast<const uint16_t*>(L->q_norm);
+    const auto* kn = d->no_qk_norm ? nullptr : static_cast<const uint16_t*>(L->k_norm);
     auto* Kc = static_cast<uint16_t*>(L->Kc);
     auto* Vc = static_cast<uint16_t*>(L->Vc);
     if (hd == 64)

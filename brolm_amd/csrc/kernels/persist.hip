@@ -49,6 +49,7 @@ constexpr int kTraceLayer = 14;            // attention sub-stage stamps (slots 
 struct PArgs {
     int H, F, n_q, n_kv, hd, V, cap, L;
     float eps;
+    int qk_norm;                     // 0: no per-head q/k RMSNorm (q_norm / k_norm not read)
     int g_q, g_k;                    // WGs of the q and k segments of stage A (v gets the rest)
     uint32_t epoch;
     const bx_decode_layer* layers;   // device array of L layers
@@ -614,14 +615,18 @@ struct RopeRegs {
     static constexpr int kP = (HD / 2 + 63) / 64;
     uint32_t qg[kP], kg[kP];
     float c[kP], s[kP];
-    __device__ __forceinline__ void load(const bx_decode_layer& Ly, const float* cos_row, const float* sin_row) {
+    __device__ __forceinline__ void load(const bx_decode_layer& Ly, const float* cos_row, const float* sin_row,
+                                         bool qk_norm) {
         const int lane = tidx() & 63;
 #pragma unroll
         for (int i = 0; i < kP; ++i) {
             const int p = lane + 64 * i;
+            qg[i] = kg[i] = 0u;
             if (p < HD / 2) {
-                qg[i] = gptr<uint32_t>(Ly.q_norm)[p];
-                kg[i] = gptr<uint32_t>(Ly.k_norm)[p];
+                if (qk_norm) {
+                    qg[i] = gptr<uint32_t>(Ly.q_norm)[p];
+                    kg[i] = gptr<uint32_t>(Ly.k_norm)[p];
+                }
                 c[i] = gptr<float>(cos_row)[p];
                 s[i] = gptr<float>(sin_row)[p];
             }
@@ -637,9 +642,11 @@ __device__ __forceinline__ uint32_t pack16(float lo, float hi) {
 // RMSNorm of one HD-long FP32 head (one wave) with gamma pairs gm, RoPE with
 // the lane's cos/sin, FP16 rounding after each step as the op path stores
 // them (q/k-norm into FP16, RoPE in place on FP16) -> FP16 pairs at dst.
+// Without QK-norm (qk_norm false) the head is the projection output rounded
+// to FP16, then rotated.
 template <int HD>
 __device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t (&gm)[RopeRegs<HD>::kP],
-                                               const RopeRegs<HD>& rr, float eps, uint32_t* dst) {
+                                               const RopeRegs<HD>& rr, float eps, bool qk_norm, uint32_t* dst) {
     const int lane = tidx() & 63;
     constexpr int kP = RopeRegs<HD>::kP;
     float x0[kP], x1[kP];
@@ -654,14 +661,17 @@ __device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t 
             ss += x0[i] * x0[i] + x1[i] * x1[i];
         }
     }
-    ss = wave_allsum(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+    float inv = 1.0f;
+    if (qk_norm) {
+        ss = wave_allsum(ss);
+        inv = 1.0f / sqrtf(ss / (float)HD + eps);
+    }
 #pragma unroll
     for (int i = 0; i < kP; ++i) {
         const int p = lane + 64 * i;
         if (p < HD / 2) {
-            const float a0 = r16(x0[i] * inv * h2f(gm[i] & 0xffff));
-            const float a1 = r16(x1[i] * inv * h2f(gm[i] >> 16));
+            const float a0 = qk_norm ? r16(x0[i] * inv * h2f(gm[i] & 0xffff)) : r16(x0[i]);
+            const float a1 = qk_norm ? r16(x1[i] * inv * h2f(gm[i] >> 16)) : r16(x1[i]);
             dst[p] = pack16(a0 * rr.c[i] - a1 * rr.s[i], a0 * rr.s[i] + a1 * rr.c[i]);
         }
     }
@@ -724,7 +734,7 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     const AttScratch<HD> sc(ar, Gq);
     if (layer == kTraceLayer) stamp(a, 900 + 0);
     RopeRegs<HD> rr;
-    rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2));
+    rr.load(Ly, a.cos_t + (int64_t)pos * (HD / 2), a.sin_t + (int64_t)pos * (HD / 2), a.qk_norm != 0);
     if (layer == kTraceLayer) stamp(a, 900 + 1);
 
     // one poll over the group's q words and, for the split holding pos, its k
@@ -753,11 +763,11 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
     if (layer == kTraceLayer) stamp(a, 900 + 2);
 
     // ---- from here each wave works alone
-    for (int hh = 0; hh < HPW; ++hh) norm_rope_head<HD>(sc.qraw + (h0 + hh) * HD, rr.qg, rr, a.eps, sc.q16(hh));
+    for (int hh = 0; hh < HPW; ++hh) norm_rope_head<HD>(sc.qraw + (h0 + hh) * HD, rr.qg, rr, a.eps, a.qk_norm != 0, sc.q16(hh));
     if (mine_cur) {
         uint32_t* kc = sc.kcur();
         uint32_t* vc = sc.vcur();
-        norm_rope_head<HD>(sc.kraw, rr.kg, rr, a.eps, kc);
+        norm_rope_head<HD>(sc.kraw, rr.kg, rr, a.eps, a.qk_norm != 0, kc);
         for (int p = lane; p < HD / 2; p += 64) vc[p] = pack16(sc.vraw[2 * p], sc.vraw[2 * p + 1]);
         // the current row replaces the stale cache row pos in the tile (another
         // wave of this part writes the same bytes)
@@ -1502,7 +1512,7 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     const int hd = d->head_dim;
     bx::PArgs a{};
     a.H = d->hidden; a.F = d->intermediate; a.n_q = d->n_q; a.n_kv = d->n_kv; a.hd = hd; a.V = d->vocab;
-    a.cap = d->cap; a.L = n_layers; a.eps = d->eps;
+    a.cap = d->cap; a.L = n_layers; a.eps = d->eps; a.qk_norm = d->no_qk_norm ? 0 : 1;
     a.g_q = o.g_q; a.g_k = o.g_k;
     a.epoch = epoch;
     a.layers = layers_dev;

@@ -38,6 +38,10 @@ struct Qwen3Spec {
     brotensor::Dtype output = brotensor::Dtype::Q6_K;
     float stddev = 0.02f;
     std::uint64_t seed = 0;
+    // general.architecture and metadata-key prefix.  "qwen3" writes per-head
+    // attn_q_norm / attn_k_norm gammas; any other name ("llama", the arch
+    // llama.cpp gives Mistral text models) writes none (no QK-norm).
+    std::string arch = "qwen3";
 };
 
 // Key of a tensor's random stream: seed mixed with the FNV-1a hash of its name.
@@ -50,5 +54,8 @@ void quantize(brotensor::Dtype dt, const float* src, std::int64_t n, std::uint8_
 
 std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& spec);
 void write_qwen3_gguf(const Qwen3Spec& spec, const std::string& path);
+// Mistral 3.1 text checkpoint: the same tensors under arch "llama", no
+// QK-norm gammas; untied when spec.tied is false (output.weight present).
+void write_mistral3_gguf(Qwen3Spec spec, const std::string& path);
 
 }  // namespace brolm::synth

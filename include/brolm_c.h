@@ -59,6 +59,40 @@ int brolm_gguf_tensor_count(const char* path, int64_t* out);
 int brolm_gguf_tensor_info(const char* path, const char* name, int* ggml_type, int64_t* dims4, int* ndims,
                            int64_t* nbytes);
 
+/* Mistral3Config (include/brolm/mistral3_config.h:30-143): the text section
+ * and the top-level multimodal glue (the Pixtral vision section is not part
+ * of this build). */
+typedef struct {
+    int vocab_size, hidden_size, intermediate_size, num_hidden_layers;
+    int num_attention_heads, num_key_value_heads, head_dim;
+    float rms_norm_eps, rope_theta;
+    int tie_word_embeddings, max_position_embeddings;
+    int has_sliding_window, sliding_window;
+} brolm_mistral3_text_config;
+typedef struct {
+    brolm_mistral3_text_config text;
+    int image_token_index, spatial_merge_size, multimodal_projector_bias;
+} brolm_mistral3_config;
+
+/* Mistral3Config::from_gguf (src/mistral3_config.cpp:130-191) */
+int brolm_mistral3_config_from_gguf(const char* path, brolm_mistral3_config* out);
+/* Mistral3Config::from_json_text (src/mistral3_config.cpp:36-93); text is a
+ * NUL-terminated config.json document. */
+int brolm_mistral3_config_from_json(const char* text, brolm_mistral3_config* out);
+/* mistral3_hf_to_ggml (src/mistral3_text.cpp:70-108); same contract as
+ * brolm_qwen3_hf_to_ggml. */
+int brolm_mistral3_hf_to_ggml(const char* hf_name, char* out, int cap);
+/* synth::write_mistral3_gguf: arch "llama", no QK-norm gammas. */
+int brolm_synth_mistral3_write(const brolm_synth_qwen3_spec* spec, const char* path);
+/* mistral3::TextModel (include/brolm/mistral3_text.h:52-131).  Returns a
+ * decoder handle: brolm_qwen3_free, _load_gguf, _allocate_cache,
+ * _reset_cache, _truncate_cache, _cache_len, _forward, _forward_last,
+ * _embed_tokens, _forward_embeds, _generate (mistral3::generate,
+ * include/brolm/mistral3_generate.h:40-43), _decode_greedy,
+ * _time_decode_steps, _decode_weight_bytes and _decode_mode accept it;
+ * brolm_qwen3_generate_text (Qwen tokenizer) rejects it. */
+brolm_qwen3* brolm_mistral3_text_create(const brolm_mistral3_text_config* cfg);
+
 /* Qwen3Model (include/brolm/qwen.h:58-157). */
 brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg);
 void brolm_qwen3_free(brolm_qwen3* m);

@@ -144,6 +144,11 @@ typedef struct {
     int hidden, intermediate, n_q, n_kv, head_dim, vocab, cap;
     float eps;
     int qkv_type_q, qkv_type_k, qkv_type_v, o_type, gate_type, up_type, down_type, lm_type;
+    /* 1: no per-head q/k RMSNorm (Mistral / Llama, DenseDecoderConfig
+     * use_qk_norm = false): q and k are rounded to FP16 and rotated as they
+     * come from the projections; the layers' q_norm / k_norm are not read.
+     * 0 (a zero-initialized struct): Qwen3's QK-norm. */
+    int no_qk_norm;
 } bx_decode_dims;
 
 typedef struct {

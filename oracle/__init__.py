@@ -26,7 +26,7 @@ class Config(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers",
                                         "num_attention_heads", "num_key_value_heads", "head_dim")] + [
         ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("tie_word_embeddings", C.c_int),
-        ("max_position_embeddings", C.c_int)]
+        ("max_position_embeddings", C.c_int), ("use_qk_norm", C.c_int)]
 
 
 def build() -> Path:

@@ -603,7 +603,7 @@ void or_attention(const float* q, const float* Kc, const float* Vc, int L, int p
 float or_silu(float x) { return (float)((double)x / (1.0 + exp(-(double)x))); }
 
 /* ------------------------------------------------------------------------- */
-/* Qwen3 decoder                                                              */
+/* Dense decoder (Qwen3 / Mistral 3.1 text)                                   */
 /* ------------------------------------------------------------------------- */
 
 typedef struct {
@@ -622,11 +622,18 @@ struct or_model {
 
 static const or_kv* kvx(const or_gguf* g, const char* k) { return find_kv(g, k); }
 
-/* Qwen3Config::from_gguf (src/qwen.cpp:88-149) */
+/* Qwen3Config::from_gguf (src/qwen.cpp:88-149) for "qwen3";
+ * Mistral3Config::from_gguf (src/mistral3_config.cpp:130-191) for any other
+ * architecture name, whose keys carry that name as prefix ("llama.",
+ * "mistral."), with QK-norm off (src/mistral3_text.cpp:26-42) and tying
+ * inferred from the absence of output.weight. */
 static int load_config(const or_gguf* g, or_config* c) {
     const char* arch = NULL;
-    if (or_gguf_meta_str(g, "general.architecture", &arch) == 0 && strcmp(arch, "qwen3") != 0) {
-        snprintf(g_err, sizeof g_err, "general.architecture is '%s', expected 'qwen3'", arch);
+    char a[64] = "qwen3";
+    if (or_gguf_meta_str(g, "general.architecture", &arch) == 0) snprintf(a, sizeof a, "%s", arch);
+    const int qwen = strcmp(a, "qwen3") == 0;
+    if (!qwen && strcmp(a, "llama") != 0 && strcmp(a, "mistral") != 0) {
+        snprintf(g_err, sizeof g_err, "general.architecture is '%s', expected qwen3, llama or mistral", a);
         return -1;
     }
     int64_t v;
@@ -634,26 +641,34 @@ static int load_config(const or_gguf* g, or_config* c) {
     c->num_hidden_layers = 28; c->num_attention_heads = 16; c->num_key_value_heads = 8;
     c->head_dim = 128; c->rms_norm_eps = 1e-6f; c->rope_theta = 1000000.0f;
     c->tie_word_embeddings = 1; c->max_position_embeddings = 40960;
-#define NEED(key, field) \
-    if (or_gguf_meta_int(g, key, &v) != 0) { snprintf(g_err, sizeof g_err, "missing metadata '%s'", key); return -1; } \
+    if (!qwen) {  /* Mistral3Config::Text defaults (mistral3_config.h:38-58) */
+        c->vocab_size = 131072; c->rms_norm_eps = 1e-5f; c->rope_theta = 1.0e9f;
+        c->tie_word_embeddings = 0; c->max_position_embeddings = 131072;
+    }
+    c->use_qk_norm = qwen;
+    char key[128];
+#define KEY(suffix) (snprintf(key, sizeof key, "%s.%s", a, suffix), key)
+#define NEED(suffix, field) \
+    if (or_gguf_meta_int(g, KEY(suffix), &v) != 0) { snprintf(g_err, sizeof g_err, "missing metadata '%s'", key); return -1; } \
     c->field = (int)v;
-    NEED("qwen3.embedding_length", hidden_size);
-    NEED("qwen3.feed_forward_length", intermediate_size);
-    NEED("qwen3.block_count", num_hidden_layers);
-    NEED("qwen3.attention.head_count", num_attention_heads);
+    NEED("embedding_length", hidden_size);
+    NEED("feed_forward_length", intermediate_size);
+    NEED("block_count", num_hidden_layers);
+    NEED("attention.head_count", num_attention_heads);
 #undef NEED
-    c->num_key_value_heads = or_gguf_meta_int(g, "qwen3.attention.head_count_kv", &v) == 0 ? (int)v : c->num_attention_heads;
-    c->head_dim = or_gguf_meta_int(g, "qwen3.attention.key_length", &v) == 0 ? (int)v
-                                                                             : c->hidden_size / c->num_attention_heads;
+    c->num_key_value_heads = or_gguf_meta_int(g, KEY("attention.head_count_kv"), &v) == 0 ? (int)v : c->num_attention_heads;
+    c->head_dim = or_gguf_meta_int(g, KEY("attention.key_length"), &v) == 0 ? (int)v
+                                                                          : c->hidden_size / c->num_attention_heads;
     double f;
-    if (or_gguf_meta_f64(g, "qwen3.attention.layer_norm_rms_epsilon", &f) == 0) c->rms_norm_eps = (float)f;
-    if (or_gguf_meta_f64(g, "qwen3.rope.freq_base", &f) == 0) c->rope_theta = (float)f;
-    if (or_gguf_meta_int(g, "qwen3.context_length", &v) == 0) c->max_position_embeddings = (int)v;
+    if (or_gguf_meta_f64(g, KEY("attention.layer_norm_rms_epsilon"), &f) == 0) c->rms_norm_eps = (float)f;
+    if (or_gguf_meta_f64(g, KEY("rope.freq_base"), &f) == 0) c->rope_theta = (float)f;
+    if (or_gguf_meta_int(g, KEY("context_length"), &v) == 0) c->max_position_embeddings = (int)v;
     if (or_gguf_meta_array_len(g, "tokenizer.ggml.tokens", &v) == 0) c->vocab_size = (int)v;
-    else if (or_gguf_meta_int(g, "qwen3.vocab_size", &v) == 0) c->vocab_size = (int)v;
-    const or_kv* tie = kvx(g, "qwen3.tie_word_embeddings");
+    else if (or_gguf_meta_int(g, KEY("vocab_size"), &v) == 0) c->vocab_size = (int)v;
+    const or_kv* tie = qwen ? kvx(g, "qwen3.tie_word_embeddings") : NULL;
     if (tie && tie->type == GV_BOOL) c->tie_word_embeddings = (int)tie->i;
     else c->tie_word_embeddings = or_gguf_find_tensor(g, "output.weight") < 0;
+#undef KEY
     return 0;
 }
 
@@ -735,16 +750,20 @@ or_model* or_model_load(const or_gguf* g) {
         snprintf(name, sizeof name, "blk.%d.attn_k.weight", l); LOAD(L->Wk, name, kvd, H);
         snprintf(name, sizeof name, "blk.%d.attn_v.weight", l); LOAD(L->Wv, name, kvd, H);
         snprintf(name, sizeof name, "blk.%d.attn_output.weight", l); LOAD(L->Wo, name, H, qd);
-        snprintf(name, sizeof name, "blk.%d.attn_q_norm.weight", l); LOAD(L->q_norm, name, HD, 1);
-        snprintf(name, sizeof name, "blk.%d.attn_k_norm.weight", l); LOAD(L->k_norm, name, HD, 1);
+        if (c->use_qk_norm) {
+            snprintf(name, sizeof name, "blk.%d.attn_q_norm.weight", l); LOAD(L->q_norm, name, HD, 1);
+            snprintf(name, sizeof name, "blk.%d.attn_k_norm.weight", l); LOAD(L->k_norm, name, HD, 1);
+        }
         snprintf(name, sizeof name, "blk.%d.ffn_norm.weight", l); LOAD(L->post_ln, name, H, 1);
         snprintf(name, sizeof name, "blk.%d.ffn_gate.weight", l); LOAD(L->Wg, name, F, H);
         snprintf(name, sizeof name, "blk.%d.ffn_up.weight", l); LOAD(L->Wu, name, F, H);
         snprintf(name, sizeof name, "blk.%d.ffn_down.weight", l); LOAD(L->Wd, name, H, F);
         permute_rows(L->Wq, c->num_attention_heads, HD, H);
         permute_rows(L->Wk, c->num_key_value_heads, HD, H);
-        permute_rows(L->q_norm, 1, HD, 1);
-        permute_rows(L->k_norm, 1, HD, 1);
+        if (c->use_qk_norm) {
+            permute_rows(L->q_norm, 1, HD, 1);
+            permute_rows(L->k_norm, 1, HD, 1);
+        }
     }
     LOAD(m->final_norm, "output_norm.weight", H, 1);
     if (or_gguf_find_tensor(g, "output.weight") >= 0) {
@@ -817,8 +836,13 @@ int or_model_forward(or_model* m, const int32_t* ids, int L, int last_only, floa
         or_linear(Ly->Wq, nrm, q, L, qd, H);
         or_linear(Ly->Wk, nrm, k, L, kvd, H);
         or_linear(Ly->Wv, nrm, v, L, kvd, H);
-        or_rms_norm(q, Ly->q_norm, eps, qn, L * nq, HD);
-        or_rms_norm(k, Ly->k_norm, eps, kn, L * nkv, HD);
+        if (c->use_qk_norm) {
+            or_rms_norm(q, Ly->q_norm, eps, qn, L * nq, HD);
+            or_rms_norm(k, Ly->k_norm, eps, kn, L * nkv, HD);
+        } else {
+            memcpy(qn, q, sizeof(float) * (size_t)L * qd);
+            memcpy(kn, k, sizeof(float) * (size_t)L * kvd);
+        }
         or_rope(qn, L, HD, nq, pos0, c->rope_theta);
         or_rope(kn, L, HD, nkv, pos0, c->rope_theta);
         memcpy(Ly->Kc + (size_t)pos0 * kvd, kn, sizeof(float) * (size_t)L * kvd);

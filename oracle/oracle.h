@@ -85,13 +85,16 @@ void or_attention(const float* q, const float* Kc, const float* Vc, int L, int p
                   int n_q, int n_kv, int hd, float* out);
 float or_silu(float x);
 
-/* ---- FP32 Qwen3 dense decoder on dequantized weights ---- */
+/* ---- FP32 dense decoder on dequantized weights: Qwen3 (general.architecture
+ * "qwen3", per-head QK-norm) or Mistral 3.1 text ("llama" / "mistral", no
+ * QK-norm) ---- */
 typedef struct or_model or_model;
 typedef struct {
     int vocab_size, hidden_size, intermediate_size, num_hidden_layers;
     int num_attention_heads, num_key_value_heads, head_dim;
     float rms_norm_eps, rope_theta;
     int tie_word_embeddings, max_position_embeddings;
+    int use_qk_norm;
 } or_config;
 
 or_model* or_model_load(const or_gguf* g);          /* NULL on error (or_gguf_error) */

@@ -23,6 +23,14 @@ SMALL_Q8 = dict(vocab=768, hidden=512, intermediate=1024, layers=2, n_q=8, n_kv=
                 embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0", up="Q8_0", down="Q8_0",
                 output="Q8_0", seed=11)
 
+# Mistral 3.1 text shape in miniature: no QK-norm, untied, GQA 4:1, head_dim
+# (128) != hidden / heads (64), Mistral's eps and rope theta; the FFN width
+# is Qwen3-1.7B's, so single-token steps run the persistent-step
+# instantiation of that model's format mix.
+SMALL_M3 = dict(vocab=1000, hidden=256, intermediate=6144, layers=2, n_q=4, n_kv=1, head_dim=128, tied=False,
+                eps=1e-5, theta=1e9, context=131072, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K",
+                gate="Q4_K", up="Q4_K", down="Q6_K", output="Q6_K", seed=23)
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device; calls the HIP path")
@@ -43,12 +51,13 @@ def native():
     return _native
 
 
-def write_synth(tmpdir: Path, spec: dict, name: str) -> Path:
+def write_synth(tmpdir: Path, spec: dict, name: str, arch: str = "qwen3") -> Path:
     _ensure_built()
     import brolm_amd as ba
     path = tmpdir / f"{name}.gguf"
     if not path.exists():
-        ba.write_synth_qwen3(ba.SynthSpec(**spec), str(path))
+        write = ba.write_synth_qwen3 if arch == "qwen3" else ba.write_synth_mistral3
+        write(ba.SynthSpec(**spec), str(path))
     return path
 
 
@@ -60,3 +69,8 @@ def small_gguf(tmp_path_factory) -> Path:
 @pytest.fixture(scope="session")
 def small_q8_gguf(tmp_path_factory) -> Path:
     return write_synth(tmp_path_factory.mktemp("synth8"), SMALL_Q8, "small_q8")
+
+
+@pytest.fixture(scope="session")
+def small_m3_gguf(tmp_path_factory) -> Path:
+    return write_synth(tmp_path_factory.mktemp("synth_m3"), SMALL_M3, "small_m3", arch="mistral3")
