@@ -55,6 +55,12 @@ CONFIGS = {
     "qwen3-0.6b-q8_0": dict(vocab=151936, hidden=1024, intermediate=3072, layers=28, n_q=16, n_kv=8, head_dim=128,
                             tied=True, embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0",
                             up="Q8_0", down="Q8_0", output="Q8_0", prompt=512, decode=256, cap=2048),
+    # Mistral-Small-3.1-24B text decoder (no QK-norm, untied), Q4_K_M-style mix
+    "mistral-small-3.1-24b-q4k": dict(arch="mistral3", vocab=131072, hidden=5120, intermediate=32768, layers=40,
+                                      n_q=32, n_kv=8, head_dim=128, eps=1e-5, theta=1e9, context=131072,
+                                      tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K",
+                                      gate="Q4_K", up="Q4_K", down="Q6_K", output="Q6_K", prompt=1024,
+                                      decode=128, cap=2048),
     # BASELINE.json configs[4]
     "qwen3-8b-q4k": dict(vocab=151936, hidden=4096, intermediate=12288, layers=36, n_q=32, n_kv=8, head_dim=128,
                          tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K",
@@ -77,10 +83,11 @@ def make_model_file(name: str, seed: int) -> Path:
     c = CONFIGS[name]
     path = synth_path(name, seed)
     if not path.exists():
-        spec = ba.SynthSpec(**{k: v for k, v in c.items() if k not in ("prompt", "decode", "cap")}, seed=seed)
+        spec = ba.SynthSpec(**{k: v for k, v in c.items() if k not in ("arch", "prompt", "decode", "cap")}, seed=seed)
         t0 = time.time()
         tmp = path.with_suffix(".tmp")
-        ba.write_synth_qwen3(spec, str(tmp))
+        write = ba.write_synth_mistral3 if c.get("arch") == "mistral3" else ba.write_synth_qwen3
+        write(spec, str(tmp))
         os.replace(tmp, path)
         log(f"synthetic checkpoint {path.name}: {path.stat().st_size / 1e9:.3f} GB in {time.time() - t0:.1f} s")
     return path
@@ -129,6 +136,26 @@ def cpu_baseline(path: Path, vocab: int, prompt: list[int], seconds: float) -> d
     }
 
 
+def text_path(ba, path: Path, model, prompt: list[int]) -> dict:
+    tk = ba.Tokenizer.from_gguf(str(path))
+    corpus = ("The decoder reads the tokens of the prompt, 128 at a time; the sampler picks the next one. " * 12000)
+    t0 = time.perf_counter()
+    n_ids = len(tk.encode(corpus))
+    enc_s = time.perf_counter() - t0
+    model.truncate_cache(0)
+    gen_opts = ba.GenerateOptions(max_new_tokens=64, sampling=ba.SamplingParams(temperature=0.0), stop_on_eos=False)
+    text_prompt = tk.decode(prompt)
+    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)   # warm-up
+    t0 = time.perf_counter()
+    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)
+    gen_text_s = time.perf_counter() - t0
+    tokenizer = {"encode_mb_s": round(len(corpus) / enc_s / 1e6, 2), "encode_ids_s": round(n_ids / enc_s),
+                 "sample": f"{len(corpus) / 1e6:.2f} MB English-like text, {n_ids} ids, 1 host thread",
+                 "generate_text_ms": round(gen_text_s * 1e3, 2),
+                 "generate_text_note": "decoded 2000-byte prompt re-encoded, 64 greedy tokens, decode"}
+    return tokenizer
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,8 +193,13 @@ def main() -> int:
     steps = args.steps if args.steps is not None else c["decode"]
     path = make_model_file(args.config, args.seed)
     ba.init()
-    cfg = ba.Qwen3Config.from_gguf(str(path))
-    model = ba.Qwen3Model(cfg)
+    mistral = c.get("arch") == "mistral3"
+    if mistral:
+        cfg = ba.Mistral3Config.from_gguf(str(path)).text
+        model = ba.Mistral3TextModel(cfg)
+    else:
+        cfg = ba.Qwen3Config.from_gguf(str(path))
+        model = ba.Qwen3Model(cfg)
     t0 = time.time()
     model.load_weights(str(path))
     log(f"loaded in {time.time() - t0:.1f} s")
@@ -210,23 +242,11 @@ def main() -> int:
     ref_tok_s = n_ref / (time.perf_counter() - t0)
 
     # text path: the checkpoint's own tokenizer (host), and generate_text
-    # (encode -> greedy generate -> decode) end to end
-    tk = ba.Tokenizer.from_gguf(str(path))
-    corpus = ("The decoder reads the tokens of the prompt, 128 at a time; the sampler picks the next one. " * 12000)
-    t0 = time.perf_counter()
-    n_ids = len(tk.encode(corpus))
-    enc_s = time.perf_counter() - t0
-    model.truncate_cache(0)
-    gen_opts = ba.GenerateOptions(max_new_tokens=64, sampling=ba.SamplingParams(temperature=0.0), stop_on_eos=False)
-    text_prompt = tk.decode(prompt)
-    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)   # warm-up
-    t0 = time.perf_counter()
-    ba.generate_text(model, tk, text_prompt[:2000], gen_opts)
-    gen_text_s = time.perf_counter() - t0
-    tokenizer = {"encode_mb_s": round(len(corpus) / enc_s / 1e6, 2), "encode_ids_s": round(n_ids / enc_s),
-                 "sample": f"{len(corpus) / 1e6:.2f} MB English-like text, {n_ids} ids, 1 host thread",
-                 "generate_text_ms": round(gen_text_s * 1e3, 2),
-                 "generate_text_note": "decoded 2000-byte prompt re-encoded, 64 greedy tokens, decode"}
+    # (encode -> greedy generate -> decode) end to end; Qwen3 only (Mistral's
+    # tokenizer is Tekken, not part of this build)
+    tokenizer = None
+    if not mistral:
+        tokenizer = text_path(ba, path, model, prompt)
 
     wbytes = model.decode_weight_bytes()
     achieved = wbytes / (gpu_ms * 1e-3) / 1e9
@@ -234,7 +254,8 @@ def main() -> int:
     avg_ctx = len(prompt) + steps / 2
     kv_bytes = 2 * cfg.num_hidden_layers * avg_ctx * kvd * 2
     result = {
-        "metric": "decode tok/s bs=1 Qwen3-1.7B Q4_K; quant-GEMV HBM GB/s as % of peak",
+        "metric": ("decode tok/s bs=1 Qwen3-1.7B Q4_K; quant-GEMV HBM GB/s as % of peak"
+                   if args.config == "qwen3-1.7b-q4k" else f"decode tok/s bs=1 {args.config}"),
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -263,7 +284,9 @@ def main() -> int:
     # device state goes before the process exit path (a profiler wrapping this
     # run finalizes there)
     model.close()
-    if not args.no_cpu_baseline:
+    if mistral and not args.no_cpu_baseline:
+        log("cpu baseline skipped: the FP32 oracle of a 24B model needs ~96 GB of host memory")
+    elif not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
         result["cpu_baseline"] = cpu_baseline(path, cfg.vocab_size, prompt, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -164,9 +164,11 @@ __global__ BX_GEMV_BOUNDS void norm_qkv_kernel(const float* __restrict__ h, cons
     }
 }
 
-// 4 / 6: FP16 activation x, GEMV, residual add into h.
+// 4 / 6: FP16 activation x, GEMV, residual add into h.  The wide form (16
+// units per lane, K up to 32768) gets 256 registers: its 80 KB of staged
+// activations allow two workgroups per CU anyway.
 template <int FMT, int UPL>
-__global__ BX_GEMV_BOUNDS void gemv_resid_kernel(const uint16_t* __restrict__ x, int K, const void* W, int N,
+__global__ __launch_bounds__(kThreads, UPL > 6 ? 2 : 4) void gemv_resid_kernel(const uint16_t* __restrict__ x, int K, const void* W, int N,
                                                  float* __restrict__ h) {
     extern __shared__ __align__(16) uint32_t smem[];
     uint32_t* xs = smem;
@@ -458,8 +460,9 @@ int check_dims(const bx_decode_dims* d) {
     if (!d) return fail(BX_EINVAL, "decode: null dims");
     if (d->hidden <= 0 || d->hidden % 256 || d->intermediate <= 0 || d->intermediate % 256)
         return fail(BX_EUNSUPPORTED, "decode: hidden and intermediate must be multiples of 256");
-    if (d->hidden > 12288 || d->intermediate > 12288 || d->n_q * d->head_dim > 12288)
-        return fail(BX_EUNSUPPORTED, "decode: K above 12288");
+    // the intermediate width is K only of the down projection (wide dispatch)
+    if (d->hidden > 12288 || d->intermediate > 32768 || d->n_q * d->head_dim > 12288)
+        return fail(BX_EUNSUPPORTED, "decode: hidden or n_q*head_dim above 12288, or intermediate above 32768");
     if (d->n_q <= 0 || d->n_kv <= 0 || d->n_q % d->n_kv || d->n_q / d->n_kv > kMaxGroup)
         return fail(BX_EUNSUPPORTED, "decode: unsupported head counts");
     if (d->head_dim % 8 || d->head_dim > 256 || d->head_dim <= 0)
@@ -509,8 +512,15 @@ int launch_qkv(int ta, int tb, int upl, unsigned blocks, size_t lds, hipStream_t
 }
 int launch_resid(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const uint16_t* x, int K,
                  const void* W, int N, float* h) {
-    BX_DISPATCH_FMT(type, BX_DISPATCH_UPL(upl, (gemv_resid_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(
-                                                   x, K, W, N, h))));
+    BX_DISPATCH_FMT(type, BX_DISPATCH_UPL_WIDE(upl, {
+        if (lds > 65536) {   // the down projection of FFN widths above 26112
+            const void* fn = reinterpret_cast<const void*>(&gemv_resid_kernel<FMT_, UPL_>);
+            if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                                   "decode gemv_resid: LDS attribute"))
+                return rc;
+        }
+        gemv_resid_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(x, K, W, N, h);
+    }));
     return launch_check("decode gemv_resid");
 }
 int launch_mlp(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const float* h, const uint16_t* g,

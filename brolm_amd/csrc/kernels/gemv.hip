@@ -95,13 +95,19 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
 int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int N, int K,
                    hipStream_t st) {
     const int upl = upl_for(K);
-    if (upl > 6) return fail(BX_EUNSUPPORTED, "gemv: K above 12288 at M = 1");
+    if (upl > 16) return fail(BX_EUNSUPPORTED, "gemv: K above 32768 at M = 1");
     const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
     if (blocks > cap) blocks = cap;
     const size_t lds = (size_t)K * 2 + (size_t)(K / 8) * 4;
-    BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL(upl, {
+    BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL_WIDE(upl, {
+        if (lds > 65536) {   // K above 26214: more than the default 64 KB of dynamic LDS
+            const void* fn = reinterpret_cast<const void*>(&gemv_m1_kernel<FMT_, UPL_>);
+            if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                                   "gemv m1: LDS attribute"))
+                return rc;
+        }
         gemv_m1_kernel<FMT_, UPL_><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
     }))
     return launch_check("gemv m1");
@@ -166,7 +172,7 @@ int check_linear_shape(int wtype, int M, int N, int K) {
 
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st) {
-    if (M == 1 && upl_for(K) <= 6) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
+    if (M == 1 && upl_for(K) <= 16) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
     // measured crossover (GEMV sweep): the per-row kernel is one launch at
     // M = 2 and 4 and faster there, except Q4_K at 4 with N >= 4096; Q8_0
     // below 8 M weights keeps it up to M = 8
@@ -190,6 +196,8 @@ extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, con
     if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
     if (!W || !X || !Y) return bx::fail(BX_EINVAL, "linear: null pointer");
     hipStream_t st = bx::as_stream(stream);
-    if (M <= 16) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
+    // K beyond 12288 (an FFN width such as 32768) at 2..16 rows: the per-row
+    // kernels' staged activations outgrow LDS, the tiled GEMM does not
+    if (M == 1 || (M <= 16 && K <= 12288)) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
     return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
 }

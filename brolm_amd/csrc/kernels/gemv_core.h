@@ -504,31 +504,44 @@ struct RowsPer {
     static constexpr int R = UPL == 1 ? 4 : (UPL == 2 ? 2 : 1);
 };
 
+// A lane owning more than 8 units (K above 16384) loads them in batches of 4,
+// each batch's math before the next batch's loads, to bound its registers;
+// up to 8 units every load is issued before any math.
 template <int FMT, int UPL, int R>
 __device__ __forceinline__ void rows_dot_m1(const void* W, int64_t N, int K, int64_t row0,
                                             const XCache<FMT, UPL>& xu, float (&out)[R]) {
+    constexpr int kB = UPL > 8 ? 4 : UPL;
+    static_assert(UPL % kB == 0, "units per lane must be a whole number of batches");
     const int lane = threadIdx.x & 63;
     const int U = K / 32;
-    typename RawOf<FMT>::T raw[R][UPL];
+    float a[R];
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-        const int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+    for (int rr = 0; rr < R; ++rr) a[rr] = 0.f;
 #pragma unroll
-        for (int i = 0; i < UPL; ++i) {
-            const int u = lane + 64 * i;
-            if (u < U) raw[rr][i] = load_unit<FMT>(W, N, K, row, u);
+    for (int b0 = 0; b0 < UPL; b0 += kB) {
+        typename RawOf<FMT>::T raw[R][kB];
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            const int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int u = lane + 64 * (b0 + i);
+                if (u < U) raw[rr][i] = load_unit<FMT>(W, N, K, row, u);
+            }
         }
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int u = lane + 64 * (b0 + i);
+                if (u < U) a[rr] += dot_reg(raw[rr][i], u, xu.get(b0 + i, u));
+            }
+        }
+        // keep the next batch's loads behind this batch's math
+        if constexpr (kB < UPL) asm volatile("" ::: "memory");
     }
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < UPL; ++i) {
-            const int u = lane + 64 * i;
-            if (u < U) a += dot_reg(raw[rr][i], u, xu.get(i, u));
-        }
-        out[rr] = wave_allsum(a);
-    }
+    for (int rr = 0; rr < R; ++rr) out[rr] = wave_allsum(a[rr]);
 }
 
 template <int FMT, int UPL>
@@ -612,6 +625,18 @@ __host__ __device__ constexpr int upl_for(int K) { return (K / 32 + 63) / 64; }
         case 3: { constexpr int UPL_ = 3; __VA_ARGS__; } break;    \
         case 4: { constexpr int UPL_ = 4; __VA_ARGS__; } break;    \
         default: { constexpr int UPL_ = 6; __VA_ARGS__; } break;   \
+    }
+// As BX_DISPATCH_UPL, with 7..16 units per lane (K up to 32768) run as 16:
+// for the GEMVs whose K is an FFN width (down projection, M = 1 linear).
+#define BX_DISPATCH_UPL_WIDE(upl, ...)                             \
+    switch (upl) {                                                 \
+        case 1: { constexpr int UPL_ = 1; __VA_ARGS__; } break;    \
+        case 2: { constexpr int UPL_ = 2; __VA_ARGS__; } break;    \
+        case 3: { constexpr int UPL_ = 3; __VA_ARGS__; } break;    \
+        case 4: { constexpr int UPL_ = 4; __VA_ARGS__; } break;    \
+        case 5:                                                    \
+        case 6: { constexpr int UPL_ = 6; __VA_ARGS__; } break;    \
+        default: { constexpr int UPL_ = 16; __VA_ARGS__; } break;  \
     }
 #define BX_DISPATCH_FMT(type, ...)                                                 \
     switch (type) {                                                                \

@@ -107,6 +107,25 @@ def test_linear_quant_vs_oracle(t, N, K):
         assert np.all(err <= tol), (M, float((err / tol).max()))
 
 
+@pytest.mark.parametrize("t", QTYPES)
+def test_linear_ffn_width_k(t):
+    """K = 32768 (Mistral-Small-3.1's FFN width, the down projection): the
+    wide one-row GEMV (16 units per lane, 80 KB of staged activations) and
+    the GEMM for 2..16 rows, and a K between the instantiated widths."""
+    rng = np.random.default_rng(4242 + t)
+    for N, K in ((320, 32768), (130, 17408)):
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        car = carrier(t, raw, N, K)
+        for M in (1, 2, 5, 17):
+            print(f"[linear wide K] type={t} N={N} K={K} M={M}", flush=True)
+            # activations scaled so the 32768-term sums stay well inside FP16
+            X = _f16(rng.standard_normal((M, K)) * 0.05)
+            got = _run_linear(t, car, X, N, K)
+            ref = oracle.linear(Wv, X)
+            tol = _linear_tol(Wv, X, ref)
+            assert np.all(np.abs(got - ref) <= tol), (M, K)
+
+
 @pytest.mark.parametrize("t", QTYPES + [1])
 def test_linear_batched_many_tiles(t):
     """Batched GEMV with more 16-row tiles than the workgroups hold at once
