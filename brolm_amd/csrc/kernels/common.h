@@ -25,6 +25,17 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Number of compute units on the current device (cached per device).
 int num_cus();
+// Workgroups of `threads` threads and `lds` dynamic LDS bytes that one CU
+// holds at once for kernel `fn` (registers and LDS); asked of the runtime once
+// per (kernel, threads, LDS) and cached; at least 1.
+int resident_wgs(const void* fn, int threads, size_t lds);
+
+// Workgroups per CU launched for the wide-row GEMVs (K above 12288), one
+// round of residents: a lane's 128+ registers and up to 80 KB of staged
+// activations leave room for two.
+#ifndef BX_WIDE_WGS_PER_CU
+#define BX_WIDE_WGS_PER_CU 2
+#endif
 
 // ------------------------------------------------------------- device side
 

@@ -513,13 +513,18 @@ int launch_qkv(int ta, int tb, int upl, unsigned blocks, size_t lds, hipStream_t
 int launch_resid(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const uint16_t* x, int K,
                  const void* W, int N, float* h) {
     BX_DISPATCH_FMT(type, BX_DISPATCH_UPL_WIDE(upl, {
+        const void* fn = reinterpret_cast<const void*>(&gemv_resid_kernel<FMT_, UPL_>);
         if (lds > 65536) {   // the down projection of FFN widths above 26112
-            const void* fn = reinterpret_cast<const void*>(&gemv_resid_kernel<FMT_, UPL_>);
             if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                                    "decode gemv_resid: LDS attribute"))
                 return rc;
         }
-        gemv_resid_kernel<FMT_, UPL_><<<blocks, kThreads, lds, st>>>(x, K, W, N, h);
+        // wide rows: one round of resident workgroups, each staging its
+        // activations once for many rows (a fixed count: this launch is
+        // recorded into the step graph)
+        unsigned b = blocks;
+        if (UPL_ > 6) b = (unsigned)std::min<int64_t>(b, (int64_t)num_cus() * BX_WIDE_WGS_PER_CU);
+        gemv_resid_kernel<FMT_, UPL_><<<b, kThreads, lds, st>>>(x, K, W, N, h);
     }));
     return launch_check("decode gemv_resid");
 }

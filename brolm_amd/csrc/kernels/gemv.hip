@@ -102,12 +102,14 @@ int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* 
     if (blocks > cap) blocks = cap;
     const size_t lds = (size_t)K * 2 + (size_t)(K / 8) * 4;
     BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL_WIDE(upl, {
+        const void* fn = reinterpret_cast<const void*>(&gemv_m1_kernel<FMT_, UPL_>);
         if (lds > 65536) {   // K above 26214: more than the default 64 KB of dynamic LDS
-            const void* fn = reinterpret_cast<const void*>(&gemv_m1_kernel<FMT_, UPL_>);
             if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                                    "gemv m1: LDS attribute"))
                 return rc;
         }
+        // wide rows: one round of resident workgroups (activations staged once each)
+        if (UPL_ > 6) blocks = std::min<int64_t>(blocks, (int64_t)num_cus() * BX_WIDE_WGS_PER_CU);
         gemv_m1_kernel<FMT_, UPL_><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
     }))
     return launch_check("gemv m1");

@@ -401,19 +401,6 @@ size_t mfma_lds_bytes(int fmt, int Mr, int K) {
 
 constexpr size_t kMaxLds = 160 * 1024;
 
-int resident_wgs(const void* fn, size_t lds) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, int> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    const auto key = std::make_pair(fn, lds);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kThr, lds) != hipSuccess || occ < 1) occ = 1;
-    cache.emplace(key, occ);
-    return occ;
-}
-
 }  // namespace
 
 // 1 <= M <= 16, K % 256 == 0 (the linear entry point sends 3 <= M <= 16).
@@ -448,7 +435,7 @@ int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X,
             }
             // resident workgroups per CU (registers and LDS), asked once per
             // format and staging size
-            const int occ = resident_wgs(fn, lds);
+            const int occ = resident_wgs(fn, kThr, lds);
             const int64_t slots = (int64_t)cus * occ;
             // the most waves per tile (K split) whose workgroups still fit in
             // one round of resident slots; 1: whole tiles, grid-stride

@@ -1,7 +1,9 @@
 // Host-side plumbing shared by every bx_* entry point: error state, device info.
 #include "common.h"
 
+#include <map>
 #include <mutex>
+#include <tuple>
 #include <vector>
 
 namespace bx {
@@ -36,6 +38,19 @@ int num_cus() {
         cache[dev] = n;
     }
     return cache[dev];
+}
+
+int resident_wgs(const void* fn, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<const void*, int, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_tuple(fn, threads, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds) != hipSuccess || occ < 1) occ = 1;
+    cache.emplace(key, occ);
+    return occ;
 }
 
 }  // namespace bx
