@@ -61,6 +61,11 @@ CONFIGS = {
                                       tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K",
                                       gate="Q4_K", up="Q4_K", down="Q6_K", output="Q6_K", prompt=1024,
                                       decode=128, cap=2048),
+    # LLM2Vec's base, Meta-Llama-3-8B (no QK-norm), as a GGUF Q4_K_M-style mix
+    "llama3-8b-q4k": dict(arch="mistral3", vocab=128256, hidden=4096, intermediate=14336, layers=32, n_q=32,
+                          n_kv=8, head_dim=128, eps=1e-5, theta=5e5, context=8192, tied=False, embed="Q4_K",
+                          q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K", gate="Q4_K", up="Q4_K", down="Q6_K",
+                          output="Q6_K", prompt=1024, decode=256, cap=2048),
     # BASELINE.json configs[4]
     "qwen3-8b-q4k": dict(vocab=151936, hidden=4096, intermediate=12288, layers=36, n_q=32, n_kv=8, head_dim=128,
                          tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K",
@@ -217,6 +222,14 @@ def main() -> int:
     logits = model.forward_last(prompt)
     prefill_s = min(prefill_s, time.perf_counter() - t0)
     log(f"prefill {c['prompt']} tokens: {prefill_s * 1e3:.1f} ms")
+    # bidirectional encode (DenseDecoder::forward_encode, the LLM2Vec pass) of
+    # the first 512 prompt tokens; the KV cache is not touched
+    n_enc = min(512, len(prompt))
+    model.forward_encode(prompt[:n_enc])
+    t0 = time.perf_counter()
+    model.forward_encode(prompt[:n_enc])
+    encode_s = time.perf_counter() - t0
+    log(f"encode {n_enc} tokens: {encode_s * 1e3:.1f} ms")
 
     # warm-up steps, then roll back to the end of the prompt
     if args.warmup > 0:
@@ -278,6 +291,8 @@ def main() -> int:
         "weight_bytes_per_token": wbytes,
         "kv_bytes_per_token_avg": int(kv_bytes),
         "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
+        "encode_tok_s": round(n_enc / encode_s, 1),
+        "encode_note": f"forward_encode of {n_enc} tokens (bidirectional, cacheless, hidden states downloaded)",
         "ref_loop_tok_s": round(ref_tok_s, 2),
         "tokenizer": tokenizer,
     }

@@ -21,7 +21,8 @@ GGML = {"F32": 0, "F16": 1, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "BF16": 30}
 
 __all__ = ["Qwen3Config", "Qwen3Model", "SamplingParams", "GenerateOptions", "generate", "sample_token",
            "qwen3_hf_to_ggml", "SynthSpec", "write_synth_qwen3", "init", "GGML", "Mistral3Config",
-           "Mistral3TextConfig", "Mistral3TextModel", "mistral3_hf_to_ggml", "write_synth_mistral3"]
+           "Mistral3TextConfig", "Mistral3TextModel", "mistral3_hf_to_ggml", "write_synth_mistral3",
+           "Llm2VecConfig", "Llm2VecEncoder"]
 
 
 def init() -> None:
@@ -148,6 +149,15 @@ class Qwen3Model:
               "forward_embeds")
         return (logits, hidden) if want_hidden else logits
 
+    def forward_encode(self, ids: Sequence[int]) -> np.ndarray:
+        """DenseDecoder::forward_encode (dense_decoder.h:157-169): bidirectional,
+        cacheless; (L, hidden) post-final-norm hidden states."""
+        arr, p = _i32(ids)
+        out = np.empty((len(ids), self.cfg.hidden_size), np.float32)
+        check(_native.lib().brolm_decoder_forward_encode(self._h, p, len(ids), out.ctypes.data_as(_native.P_f32)),
+              "forward_encode")
+        return out
+
     def decode_greedy(self, token: int, n: int, eos_id: int = -1) -> list[int]:
         out = np.empty((max(n, 1),), np.int32)
         k = check(_native.lib().brolm_qwen3_decode_greedy(self._h, int(token), int(n),
@@ -258,6 +268,67 @@ class Mistral3TextModel(Qwen3Model):
         self._h = _native.lib().brolm_mistral3_text_create(C.byref(cfg._c()))
         if not self._h:
             raise _native.NativeError(_native.lib().brolm_last_error().decode())
+
+
+@dataclass
+class Llm2VecConfig:
+    """llm2vec::Config (include/brolm/llm2vec.h:41-63); defaults are
+    Meta-Llama-3-8B-Instruct."""
+    vocab_size: int = 128256
+    hidden_size: int = 4096
+    intermediate_size: int = 14336
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 5.0e5
+
+    def _c(self) -> _native.Llm2VecConfigC:
+        c = _native.Llm2VecConfigC()
+        for f in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+                  "num_key_value_heads", "head_dim"):
+            setattr(c, f, int(getattr(self, f)))
+        c.rms_norm_eps, c.rope_theta = float(self.rms_norm_eps), float(self.rope_theta)
+        return c
+
+    @classmethod
+    def from_json_text(cls, text: str) -> "Llm2VecConfig":
+        c = _native.Llm2VecConfigC()
+        check(_native.lib().brolm_llm2vec_config_from_json(text.encode(), C.byref(c)), "from_json_text")
+        return cls(c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
+                   c.num_key_value_heads, c.head_dim, c.rms_norm_eps, c.rope_theta)
+
+    @classmethod
+    def load(cls, path: str) -> "Llm2VecConfig":
+        with open(path, encoding="utf-8") as f:
+            return cls.from_json_text(f.read())
+
+
+class Llm2VecEncoder(Qwen3Model):
+    """llm2vec::Encoder (include/brolm/llm2vec.h:65-114) over GGUF weights."""
+
+    def __init__(self, cfg: Llm2VecConfig):
+        self.cfg = cfg
+        self._h = _native.lib().brolm_llm2vec_create(C.byref(cfg._c()))
+        if not self._h:
+            raise _native.NativeError(_native.lib().brolm_last_error().decode())
+
+    def encode(self, ids: Sequence[int]) -> np.ndarray:
+        return self.forward_encode(ids)
+
+    def encode_pooled(self, ids: Sequence[int], pool_mask=None) -> np.ndarray:
+        arr, p = _i32(ids)
+        out = np.empty((self.cfg.hidden_size,), np.float32)
+        m = None
+        if pool_mask is not None:
+            mk = np.ascontiguousarray(np.asarray(pool_mask, np.float32))
+            if mk.shape != (len(ids),):
+                raise ValueError("pool_mask must hold one value per token")
+            m = mk.ctypes.data_as(_native.P_f32)
+        check(_native.lib().brolm_llm2vec_encode_pooled(self._h, p, len(ids), m, out.ctypes.data_as(_native.P_f32)),
+              "encode_pooled")
+        return out
 
 
 @dataclass

@@ -41,6 +41,12 @@ class Mistral3ConfigC(C.Structure):
         (n, C.c_int) for n in ("image_token_index", "spatial_merge_size", "multimodal_projector_bias")]
 
 
+class Llm2VecConfigC(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab_size", "hidden_size", "intermediate_size", "num_hidden_layers",
+                                        "num_attention_heads", "num_key_value_heads", "head_dim")] + [
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
 class SynthSpecC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "hidden", "intermediate", "layers", "n_q", "n_kv", "head_dim")] + [
         ("eps", C.c_float), ("theta", C.c_float), ("context", C.c_int), ("tied", C.c_int)] + [
@@ -75,6 +81,9 @@ HIP_SYMBOLS = {
     "bx_attention_workspace_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "bx_attention_decode_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, f32, C.c_int,
                                           vp, vp, vp]),
+    "bx_attention_gqa_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp,
+                                       vp]),
+    "bx_masked_mean_pool_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
     "bx_attention_masked_f16": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp]),
     "bx_scatter_row": (C.c_int, [vp, vp, vp, i64, C.c_int, vp]),
     "bx_silu_mul_f16": (C.c_int, [vp, vp, i64, vp]),
@@ -115,6 +124,10 @@ C_SYMBOLS = {
     "brolm_mistral3_hf_to_ggml": (C.c_int, [cp, C.c_char_p, C.c_int]),
     "brolm_synth_mistral3_write": (C.c_int, [C.POINTER(SynthSpecC), cp]),
     "brolm_mistral3_text_create": (vp, [C.POINTER(Mistral3TextConfigC)]),
+    "brolm_llm2vec_config_from_json": (C.c_int, [cp, C.POINTER(Llm2VecConfigC)]),
+    "brolm_llm2vec_create": (vp, [C.POINTER(Llm2VecConfigC)]),
+    "brolm_decoder_forward_encode": (C.c_int, [vp, P_i32, C.c_int, P_f32]),
+    "brolm_llm2vec_encode_pooled": (C.c_int, [vp, P_i32, C.c_int, P_f32, P_f32]),
     "brolm_qwen3_free": (None, [vp]),
     "brolm_qwen3_load_gguf": (C.c_int, [vp, cp]),
     "brolm_qwen3_allocate_cache": (C.c_int, [vp, C.c_int]),

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "brolm/detail/profile.h"
+#include "brolm/llm2vec.h"
 #include "brolm/mistral3_generate.h"
 #include "brolm/mistral3_text.h"
 #include "brolm/qwen.h"
@@ -24,6 +25,7 @@
 struct brolm_qwen3 {
     std::unique_ptr<brolm::qwen::Qwen3Model> model;
     std::unique_ptr<brolm::mistral3::TextModel> mistral;
+    std::unique_ptr<brolm::llm2vec::Encoder> encoder;
     brolm::detail::DenseDecoder* core = nullptr;
 };
 
@@ -298,6 +300,53 @@ brolm_qwen3* brolm_mistral3_text_create(const brolm_mistral3_text_config* cfg) {
     return rc == 0 ? out : nullptr;
 }
 
+int brolm_llm2vec_config_from_json(const char* text, brolm_llm2vec_config* out) {
+    return guard([&] {
+        if (!text || !out) throw std::runtime_error("null argument");
+        const brolm::llm2vec::Config c = brolm::llm2vec::Config::from_json_text(text);
+        out->vocab_size = c.vocab_size; out->hidden_size = c.hidden_size;
+        out->intermediate_size = c.intermediate_size; out->num_hidden_layers = c.num_hidden_layers;
+        out->num_attention_heads = c.num_attention_heads; out->num_key_value_heads = c.num_key_value_heads;
+        out->head_dim = c.head_dim; out->rms_norm_eps = c.rms_norm_eps; out->rope_theta = c.rope_theta;
+    });
+}
+
+brolm_qwen3* brolm_llm2vec_create(const brolm_llm2vec_config* cfg) {
+    brolm_qwen3* out = nullptr;
+    const int rc = guard([&] {
+        if (!cfg) throw std::runtime_error("null config");
+        brolm::llm2vec::Config c;
+        c.vocab_size = cfg->vocab_size; c.hidden_size = cfg->hidden_size;
+        c.intermediate_size = cfg->intermediate_size; c.num_hidden_layers = cfg->num_hidden_layers;
+        c.num_attention_heads = cfg->num_attention_heads; c.num_key_value_heads = cfg->num_key_value_heads;
+        c.head_dim = cfg->head_dim; c.rms_norm_eps = cfg->rms_norm_eps; c.rope_theta = cfg->rope_theta;
+        c.validate();
+        auto h = std::make_unique<brolm_qwen3>();
+        h->encoder = std::make_unique<brolm::llm2vec::Encoder>(c);
+        h->core = &h->encoder->core();
+        out = h.release();
+    });
+    return rc == 0 ? out : nullptr;
+}
+
+int brolm_decoder_forward_encode(brolm_qwen3* m, const int32_t* ids, int L, float* hidden) {
+    return guard([&] {
+        brotensor::Tensor hd;
+        core_of(m).forward_encode(ids, L, hd);
+        if (hidden) to_host_f32(hd, hidden);
+    });
+}
+
+int brolm_llm2vec_encode_pooled(brolm_qwen3* m, const int32_t* ids, int L, const float* mask, float* emb) {
+    return guard([&] {
+        core_of(m);
+        if (!m->encoder) throw std::runtime_error("encode_pooled needs an llm2vec handle");
+        brotensor::Tensor e;
+        m->encoder->encode_pooled(ids, L, e, mask);
+        if (emb) to_host_f32(e, emb);
+    });
+}
+
 void brolm_qwen3_free(brolm_qwen3* m) { delete m; }
 
 int brolm_qwen3_load_gguf(brolm_qwen3* m, const char* path) {
@@ -306,7 +355,8 @@ int brolm_qwen3_load_gguf(brolm_qwen3* m, const char* path) {
         const brotensor::gguf::File f = brotensor::gguf::File::open(path);
         core_of(m);
         if (m->model) m->model->load_weights(f);
-        else m->mistral->load_weights(f);
+        else if (m->mistral) m->mistral->load_weights(f);
+        else m->encoder->load_weights(f);
     });
 }
 

@@ -264,6 +264,62 @@ void DenseDecoder::forward_embeds(const bt::Tensor& embeds, int L, bt::Tensor& l
     run_layers_(L, logits_out, hidden_out);
 }
 
+void DenseDecoder::forward_encode(const int32_t* ids, int L, bt::Tensor& hidden_out) {
+    if (!ids) fail("forward_encode: ids pointer is null");
+    if (L <= 0) fail("forward_encode: L must be positive");
+    if (embed_tokens_.size() == 0) fail("forward_encode: weights not loaded");
+    for (int i = 0; i < L; ++i)
+        if (ids[i] < 0 || ids[i] >= cfg_.vocab_size) fail("forward_encode: token id out of range");
+    ids_dev_ = make_idx_device(ids, L);
+    resize_like(h_, L, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+    hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                              embed_tokens_.cols, static_cast<const int32_t*>(ids_dev_.data), L,
+                              static_cast<float*>(h_.data), bt::stream()),
+             "embedding");
+    run_layers_encode_(L, hidden_out);
+}
+
+// The encoder's layer stack (dense_decoder.cpp:682-779): run_layers_ with
+// full attention over the L rows' own k / v instead of the causal cache.
+void DenseDecoder::run_layers_encode_(int L, bt::Tensor& hidden_out) {
+    const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
+    const float eps = cfg_.rms_norm_eps;
+    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst) {
+        bt::Tensor v = bt::Tensor::view(src.device, src.data, src.rows * num_heads, HD, src.dtype);
+        bt::rms_norm_forward(v, gain, eps, dst);
+        dst.rows = src.rows;
+        dst.cols = num_heads * HD;
+    };
+    for (Layer& layer : layers_) {
+        bt::rms_norm_forward(h_, layer.input_ln, eps, norm_);
+        linear_batched(layer.Wq, nullptr, norm_, q_);
+        linear_batched(layer.Wk, nullptr, norm_, k_);
+        linear_batched(layer.Wv, nullptr, norm_, v_);
+        bt::Tensor* q_attn = &q_;
+        bt::Tensor* k_attn = &k_;
+        if (cfg_.use_qk_norm) {
+            headnorm(q_, n_q, layer.q_norm, qn_);
+            headnorm(k_, n_kv, layer.k_norm, kn_);
+            q_attn = &qn_;
+            k_attn = &kn_;
+        }
+        bt::rope_forward(*q_attn, HD, n_q, 0, cfg_.rope_theta, *q_attn);
+        bt::rope_forward(*k_attn, HD, n_kv, 0, cfg_.rope_theta, *k_attn);
+        bt::flash_attention_gqa_forward(*q_attn, *k_attn, v_, n_q, n_kv, /*causal=*/false, attn_);
+        linear_batched(layer.Wo, nullptr, attn_, proj_);
+        bt::add_inplace(h_, proj_);
+        bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_);
+        linear_batched(layer.gate_W, nullptr, norm_, gate_);
+        linear_batched(layer.up_W, nullptr, norm_, up_);
+        bt::silu_forward(gate_, gate_);
+        bt::mul_inplace(gate_, up_);
+        linear_batched(layer.down_W, nullptr, gate_, proj_);
+        bt::add_inplace(h_, proj_);
+    }
+    bt::rms_norm_forward(h_, final_norm_, eps, norm_);
+    hidden_out = norm_.clone();
+}
+
 // ─── op-surface layer stack (dense_decoder.cpp:526-681) ─────────────────────
 
 void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden_out, bool logits_last_row_only) {

@@ -250,6 +250,35 @@ void flash_attention_decode(const Tensor& q, const Tensor& Kc, const Tensor& Vc,
              "flash_attention_decode");
 }
 
+void flash_attention_gqa_forward(const Tensor& q, const Tensor& k, const Tensor& v, int n_q, int n_kv, bool causal,
+                                 Tensor& out) {
+    for (const Tensor* t : {&q, &k, &v}) {
+        need_device(*t, "flash_attention_gqa_forward", "operand");
+        need_dtype(*t, Dtype::FP16, "flash_attention_gqa_forward", "operand");
+    }
+    if (n_q <= 0 || n_kv <= 0 || q.cols % n_q) contract("flash_attention_gqa_forward", "bad head counts");
+    const int hd = q.cols / n_q;
+    if (k.cols != n_kv * hd || v.cols != k.cols || v.rows != k.rows)
+        contract("flash_attention_gqa_forward", "k / v shape does not match n_kv * head_dim");
+    size_out(out, q.rows, q.cols, Dtype::FP16);
+    std::lock_guard<std::mutex> lk(scratch().mu);
+    Scratch& S = scratch();
+    void* ws = grow(S.attn_ws, S.attn_bytes, bx_attention_workspace_bytes(q.rows, n_q, hd, k.rows));
+    hipx::bx(bx_attention_gqa_f16(static_cast<const uint16_t*>(q.data), static_cast<const uint16_t*>(k.data),
+                                  static_cast<const uint16_t*>(v.data), q.rows, k.rows, n_q, n_kv, hd, causal ? 1 : 0,
+                                  static_cast<uint16_t*>(out.data), ws, hipx::stream()),
+             "flash_attention_gqa_forward");
+}
+
+void masked_mean_pool_forward(const Tensor& x, const float* mask, Tensor& out) {
+    need_device(x, "masked_mean_pool_forward", "x");
+    need_dtype(x, Dtype::FP16, "masked_mean_pool_forward", "x");
+    size_out(out, x.cols, 1, Dtype::FP16);
+    hipx::bx(bx_masked_mean_pool_f16(static_cast<const uint16_t*>(x.data), mask, x.rows, x.cols,
+                                     static_cast<uint16_t*>(out.data), hipx::stream()),
+             "masked_mean_pool_forward");
+}
+
 void flash_attention_decode_masked(const Tensor& q, const Tensor& Kc, const Tensor& Vc, const float* mask, int n_q,
                                    int n_kv, Tensor& out) {
     for (const Tensor* t : {&q, &Kc, &Vc}) {

@@ -17,7 +17,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float att_smem[];
     const int s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
     const int G = a.n_q / a.n_kv;
-    const int p = a.valid_len - a.L + r;  // last key this row may see
+    const int p = a.bidir ? a.valid_len - 1 : a.valid_len - a.L + r;  // last key this row may see
     const int lo = a.window > 0 ? max(0, p - a.window + 1) : 0;
     const int kb = max(lo, s * a.kps);
     const int ke = min(p + 1, (s + 1) * a.kps);
@@ -108,6 +108,31 @@ int bx_attention_decode_f16(const uint16_t* q, const uint16_t* Kc, const uint16_
     if (int rc = launch_check("attention partial")) return rc;
     attn_combine_kernel<<<dim3(n_q, L), 128, 0, st>>>(a.ws, n_q, hd, a.S, out);
     return launch_check("attention combine");
+}
+
+int bx_attention_gqa_f16(const uint16_t* q, const uint16_t* K, const uint16_t* V, int L, int n_keys, int n_q,
+                         int n_kv, int hd, int causal, uint16_t* out, void* workspace, void* stream) {
+    if (!q || !K || !V || !out || !workspace) return fail(BX_EINVAL, "attention_gqa: null pointer");
+    if (L <= 0 || n_keys <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv)
+        return fail(BX_EINVAL, "attention_gqa: bad shape");
+    if (n_q / n_kv > kAttnMaxGroup) return fail(BX_EUNSUPPORTED, "attention_gqa: GQA group larger than 8");
+    if (hd <= 0 || hd % 8 || hd > 256)
+        return fail(BX_EUNSUPPORTED, "attention_gqa: head_dim must be a multiple of 8, <= 256");
+    if (causal && n_keys < L) return fail(BX_EINVAL, "attention_gqa: causal with fewer keys than rows");
+    AttnArgs a{};
+    a.q = q; a.Kc = K; a.Vc = V; a.mask = nullptr;
+    a.L = L; a.valid_len = n_keys; a.n_q = n_q; a.n_kv = n_kv; a.hd = hd;
+    a.softcap = 0.f; a.window = 0; a.bidir = causal ? 0 : 1;
+    a.kps = attn_keys_per_split(L, n_kv, n_keys);
+    a.S = (n_keys + a.kps - 1) / a.kps;
+    a.ws = static_cast<float*>(workspace);
+    const int G = n_q / n_kv;
+    const size_t lds = (size_t)(G * hd + G * 256 + 64) * sizeof(float);
+    hipStream_t st = as_stream(stream);
+    attn_partial_kernel<<<dim3(a.S, n_kv, L), 256, lds, st>>>(a);
+    if (int rc = launch_check("attention_gqa partial")) return rc;
+    attn_combine_kernel<<<dim3(n_q, L), 128, 0, st>>>(a.ws, n_q, hd, a.S, out);
+    return launch_check("attention_gqa combine");
 }
 
 int bx_attention_masked_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, const float* mask, int n_keys,

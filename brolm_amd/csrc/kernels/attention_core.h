@@ -19,6 +19,7 @@ struct AttnArgs {
     int window;
     int kps, S;
     float* ws;  // partials [L][n_q][S][hd + 2]
+    int bidir;  // 1: every row attends all valid_len keys (no causal limit)
 };
 
 struct AttnState {

@@ -108,12 +108,34 @@ __global__ void f32_to_f16_kernel(const float* __restrict__ x, uint16_t* __restr
     if (i < n) y[i] = f2h(x[i]);
 }
 
+// One thread per column, rows in order: the sums are deterministic.
+__global__ void mean_pool_kernel(const uint16_t* __restrict__ x, const float* __restrict__ mask, int L, int cols,
+                                 uint16_t* __restrict__ out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.f, w = 0.f;
+    for (int r = 0; r < L; ++r) {
+        const float m = mask ? mask[r] : 1.0f;
+        if (m != 0.f) {
+            s += m * h2f(x[(int64_t)r * cols + c]);
+            w += m;
+        }
+    }
+    out[c] = f2h(w != 0.f ? s / w : 0.f);
+}
+
 }  // namespace
 }  // namespace bx
 
 using namespace bx;
 
 extern "C" {
+
+int bx_masked_mean_pool_f16(const uint16_t* x, const float* mask, int L, int cols, uint16_t* out, void* stream) {
+    if (!x || !out || L <= 0 || cols <= 0) return fail(BX_EINVAL, "masked_mean_pool: bad arguments");
+    mean_pool_kernel<<<(cols + 255) / 256, 256, 0, as_stream(stream)>>>(x, mask, L, cols, out);
+    return launch_check("masked_mean_pool");
+}
 
 int bx_embedding_f16(const uint16_t* W, int V, int H, const int32_t* ids, int L, uint16_t* out, void* stream) {
     if (!W || !ids || !out || V <= 0 || H <= 0 || L <= 0) return fail(BX_EINVAL, "embedding: bad arguments");

@@ -63,6 +63,11 @@ public:
     void embed_tokens(const int32_t* ids, int L, brotensor::Tensor& out);
     void forward_embeds(const brotensor::Tensor& embeds, int L, brotensor::Tensor& logits_out,
                         brotensor::Tensor* hidden_out = nullptr);
+    // Bidirectional, cacheless pass for encoder use (dense_decoder.h:157-169):
+    // every layer attends all L tokens (no causal mask, RoPE positions from
+    // 0), no lm_head; hidden_out := (L, hidden_size) post-final-norm FP16.
+    // Needs no cache allocation and leaves the KV cache untouched.
+    void forward_encode(const int32_t* ids, int L, brotensor::Tensor& hidden_out);
 
     // Greedy decode of up to n tokens starting from `token` at position
     // cache_len(), entirely on the device (argmax feeds the next step).
@@ -96,6 +101,7 @@ private:
         brotensor::Tensor K_cache, V_cache;
     };
 
+    void run_layers_encode_(int L, brotensor::Tensor& hidden_out);
     void run_layers_(int L, brotensor::Tensor& logits_out, brotensor::Tensor* hidden_out,
                      bool logits_last_row_only = false);
     void decode_step_(int32_t token, brotensor::Tensor& logits_out);

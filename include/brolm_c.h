@@ -93,6 +93,25 @@ int brolm_synth_mistral3_write(const brolm_synth_qwen3_spec* spec, const char* p
  * brolm_qwen3_generate_text (Qwen tokenizer) rejects it. */
 brolm_qwen3* brolm_mistral3_text_create(const brolm_mistral3_text_config* cfg);
 
+/* llm2vec::Config (include/brolm/llm2vec.h:41-63). */
+typedef struct {
+    int vocab_size, hidden_size, intermediate_size, num_hidden_layers;
+    int num_attention_heads, num_key_value_heads, head_dim;
+    float rms_norm_eps, rope_theta;
+} brolm_llm2vec_config;
+/* llm2vec::Config::from_json_text (src/llm2vec.cpp:70-96). */
+int brolm_llm2vec_config_from_json(const char* text, brolm_llm2vec_config* out);
+/* llm2vec::Encoder (include/brolm/llm2vec.h:65-114) over GGUF weights: a
+ * decoder handle for brolm_qwen3_free / _load_gguf / brolm_decoder_forward_encode. */
+brolm_qwen3* brolm_llm2vec_create(const brolm_llm2vec_config* cfg);
+/* DenseDecoder::forward_encode (dense_decoder.h:157-169) on any decoder
+ * handle: bidirectional, cacheless; hidden (L, hidden_size) FP32 values of the
+ * FP16 result.  Encoder::encode on an llm2vec handle. */
+int brolm_decoder_forward_encode(brolm_qwen3* m, const int32_t* ids, int L, float* hidden);
+/* Encoder::encode_pooled (src/llm2vec.cpp:137-153): emb (hidden_size); mask
+ * (host, L floats) or NULL for every token. */
+int brolm_llm2vec_encode_pooled(brolm_qwen3* m, const int32_t* ids, int L, const float* mask, float* emb);
+
 /* Qwen3Model (include/brolm/qwen.h:58-157). */
 brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg);
 void brolm_qwen3_free(brolm_qwen3* m);

@@ -112,6 +112,14 @@ int bx_attention_decode_f16(const uint16_t* q, const uint16_t* Kc, const uint16_
                             int n_q, int n_kv, int hd, float softcap, int window, uint16_t* out,
                             void* workspace, void* stream);
 
+/* K14b: flash_attention_gqa_forward(q, k, v, nullptr, n_q, n_kv, causal, out)
+ * (dense_decoder.cpp:737-745, the encoder's attention): q (L, n_q*hd), K / V
+ * (n_keys, n_kv*hd) FP16, out (L, n_q*hd) FP16.  causal = 0: every row
+ * attends all n_keys keys; causal = 1: row r attends keys [0, n_keys - L + r].
+ * workspace: bx_attention_workspace_bytes(L, n_q, hd, n_keys) bytes. */
+int bx_attention_gqa_f16(const uint16_t* q, const uint16_t* K, const uint16_t* V, int L, int n_keys, int n_q,
+                         int n_kv, int hd, int causal, uint16_t* out, void* workspace, void* stream);
+
 /* K15: flash_attention_decode_masked(q, Kc, Vc, mask, n_q, n_kv, out)
  * (dense_decoder.cpp:476-478): one query row attends the keys j < n_keys
  * whose FP32 mask[j] (device) is non-zero.  workspace as above with L = 1,
@@ -131,6 +139,11 @@ int bx_silu_f16(const uint16_t* x, uint16_t* y, int64_t n, void* stream);
 int bx_mul_f16(uint16_t* a, const uint16_t* b, int64_t n, void* stream);
 /* K17: add_inplace(h, proj) (dense_decoder.cpp:616, :645); h FP32 or FP16. */
 int bx_add_inplace(void* h, int h_is_f32, const uint16_t* x, int64_t n, void* stream);
+/* masked_mean_pool_forward(x, mask, out) (src/llm2vec.cpp:139-153): out[c] =
+ * sum_r mask[r] x[r, c] / sum_r mask[r] over the L rows of x (L, cols) FP16,
+ * FP32 sums, FP16 out (cols); mask (device FP32, L) or NULL for all rows; an
+ * all-zero mask gives zeros. */
+int bx_masked_mean_pool_f16(const uint16_t* x, const float* mask, int L, int cols, uint16_t* out, void* stream);
 /* FP32 -> FP16 copy (RNE). */
 int bx_f32_to_f16(const float* x, uint16_t* y, int64_t n, void* stream);
 

@@ -53,6 +53,13 @@ void scatter_rows(const Tensor& src, const Tensor& idx_row, Tensor& dst);
 // row to its last `window` keys (src/gemma2.cpp:365-367).
 void flash_attention_decode(const Tensor& q, const Tensor& Kc, const Tensor& Vc, int valid_len, int n_q, int n_kv,
                             Tensor& out, float softcap = 0.0f, int window = 0);
+// K16: GQA attention of the L rows of q over the n rows of k / v (no cache);
+// causal = false lets every row see every key (the encoder's form).
+void flash_attention_gqa_forward(const Tensor& q, const Tensor& k, const Tensor& v, int n_q, int n_kv, bool causal,
+                                 Tensor& out);
+// Mean of the rows of x (L, cols) FP16 weighted by the device FP32 mask (L,)
+// or all rows when mask is null -> out (cols, 1) FP16.
+void masked_mean_pool_forward(const Tensor& x, const float* mask, Tensor& out);
 // K15: single-row attention over the keys whose FP32 mask entry is non-zero
 // (mask has Kc.rows entries, device memory).
 void flash_attention_decode_masked(const Tensor& q, const Tensor& Kc, const Tensor& Vc, const float* mask, int n_q,

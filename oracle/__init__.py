@@ -82,6 +82,7 @@ def lib():
             "or_model_truncate_cache": (C.c_int, [C.c_void_p, C.c_int]),
             "or_model_cache_len": (C.c_int, [C.c_void_p]),
             "or_model_forward": (C.c_int, [C.c_void_p, P_i32, C.c_int, C.c_int, P_f32, P_f32]),
+            "or_model_forward_encode": (C.c_int, [C.c_void_p, P_i32, C.c_int, P_f32]),
             "or_model_weight": (P_f32, [C.c_void_p, C.c_int, C.c_char_p, C.POINTER(C.c_int64),
                                         C.POINTER(C.c_int64)]),
             "or_argmax": (C.c_int, [P_f32, C.c_int, P_f32]),
@@ -252,6 +253,14 @@ class Model:
         if rc != 0:
             raise ValueError(lib().or_gguf_error().decode())
         return (logits, hidden) if want_hidden else logits
+
+    def forward_encode(self, ids) -> np.ndarray:
+        """Bidirectional, cacheless (L, H) post-final-norm hidden states."""
+        a = np.ascontiguousarray(np.asarray(ids, np.int32))
+        out = np.empty((len(a), self.cfg.hidden_size), np.float32)
+        if lib().or_model_forward_encode(self._h, a.ctypes.data_as(P_i32), len(a), _f32p(out)) != 0:
+            raise RuntimeError(lib().or_gguf_error().decode())
+        return out
 
     def weight(self, layer: int, which: str) -> np.ndarray:
         r, c = C.c_int64(), C.c_int64()

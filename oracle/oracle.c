@@ -868,6 +868,63 @@ int or_model_forward(or_model* m, const int32_t* ids, int L, int last_only, floa
     return 0;
 }
 
+/* DenseDecoder::forward_encode / run_layers_encode_ (dense_decoder.cpp:296-309,
+ * :682-779) in FP32: the same layers with RoPE positions 0..L-1, every row
+ * attending all L keys (no causal limit, no KV cache), no lm_head.  hidden:
+ * (L, H) post-final-norm.  The cache is not touched. */
+int or_model_forward_encode(or_model* m, const int32_t* ids, int L, float* hidden) {
+    const or_config* c = &m->c;
+    if (!ids || L <= 0 || !hidden) { snprintf(g_err, sizeof g_err, "forward_encode: bad arguments"); return -1; }
+    for (int i = 0; i < L; ++i)
+        if (ids[i] < 0 || ids[i] >= c->vocab_size) { snprintf(g_err, sizeof g_err, "forward_encode: id out of range"); return -1; }
+    const int H = c->hidden_size, F = c->intermediate_size, HD = c->head_dim;
+    const int nq = c->num_attention_heads, nkv = c->num_key_value_heads;
+    const int qd = nq * HD, kvd = nkv * HD;
+    const float eps = c->rms_norm_eps;
+    float* h = (float*)malloc(sizeof(float) * (size_t)L * H);
+    float* nrm = (float*)malloc(sizeof(float) * (size_t)L * H);
+    float* q = (float*)malloc(sizeof(float) * (size_t)L * qd);
+    float* k = (float*)malloc(sizeof(float) * (size_t)L * kvd);
+    float* v = (float*)malloc(sizeof(float) * (size_t)L * kvd);
+    float* qn = (float*)malloc(sizeof(float) * (size_t)L * qd);
+    float* kn = (float*)malloc(sizeof(float) * (size_t)L * kvd);
+    float* att = (float*)malloc(sizeof(float) * (size_t)L * qd);
+    float* proj = (float*)malloc(sizeof(float) * (size_t)L * H);
+    float* gt = (float*)malloc(sizeof(float) * (size_t)L * F);
+    float* up = (float*)malloc(sizeof(float) * (size_t)L * F);
+    for (int i = 0; i < L; ++i) memcpy(h + (size_t)i * H, m->embed + (size_t)ids[i] * H, sizeof(float) * H);
+    for (int l = 0; l < c->num_hidden_layers; ++l) {
+        or_layer* Ly = &m->layers[l];
+        or_rms_norm(h, Ly->in_ln, eps, nrm, L, H);
+        or_linear(Ly->Wq, nrm, q, L, qd, H);
+        or_linear(Ly->Wk, nrm, k, L, kvd, H);
+        or_linear(Ly->Wv, nrm, v, L, kvd, H);
+        if (c->use_qk_norm) {
+            or_rms_norm(q, Ly->q_norm, eps, qn, L * nq, HD);
+            or_rms_norm(k, Ly->k_norm, eps, kn, L * nkv, HD);
+        } else {
+            memcpy(qn, q, sizeof(float) * (size_t)L * qd);
+            memcpy(kn, k, sizeof(float) * (size_t)L * kvd);
+        }
+        or_rope(qn, L, HD, nq, 0, c->rope_theta);
+        or_rope(kn, L, HD, nkv, 0, c->rope_theta);
+        /* one row at a time as the last of L positions: keys 0..L-1 */
+        for (int i = 0; i < L; ++i)
+            or_attention(qn + (size_t)i * qd, kn, v, 1, L - 1, nq, nkv, HD, att + (size_t)i * qd);
+        or_linear(Ly->Wo, att, proj, L, H, qd);
+        for (size_t i = 0; i < (size_t)L * H; ++i) h[i] += proj[i];
+        or_rms_norm(h, Ly->post_ln, eps, nrm, L, H);
+        or_linear(Ly->Wg, nrm, gt, L, F, H);
+        or_linear(Ly->Wu, nrm, up, L, F, H);
+        for (size_t i = 0; i < (size_t)L * F; ++i) gt[i] = or_silu(gt[i]) * up[i];
+        or_linear(Ly->Wd, gt, proj, L, H, F);
+        for (size_t i = 0; i < (size_t)L * H; ++i) h[i] += proj[i];
+    }
+    or_rms_norm(h, m->final_norm, eps, hidden, L, H);
+    free(h); free(nrm); free(q); free(k); free(v); free(qn); free(kn); free(att); free(proj); free(gt); free(up);
+    return 0;
+}
+
 const float* or_model_weight(const or_model* m, int layer, const char* which, int64_t* rows, int64_t* cols) {
     const or_config* c = &m->c;
     const int H = c->hidden_size, F = c->intermediate_size, HD = c->head_dim;

@@ -107,6 +107,8 @@ int       or_model_cache_len(const or_model* m);
 /* logits: (L, V) or (1, V) when last_only; hidden (optional): (L, H) post-final-norm */
 int       or_model_forward(or_model* m, const int32_t* ids, int L, int last_only,
                            float* logits, float* hidden);
+/* bidirectional, cacheless pass (forward_encode): hidden (L, H) post-final-norm */
+int       or_model_forward_encode(or_model* m, const int32_t* ids, int L, float* hidden);
 /* dequantized FP32 weights after load-time permutes (for tests). which: see oracle.c */
 const float* or_model_weight(const or_model* m, int layer, const char* which, int64_t* rows, int64_t* cols);
 
