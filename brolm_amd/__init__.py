@@ -347,6 +347,7 @@ class GenerateOptions:
     sampling: SamplingParams = field(default_factory=SamplingParams)
     stop_on_eos: bool = True
     device_greedy: bool = True
+    device_sampling: bool = True
 
 
 def generate(model: Qwen3Model, prompt_ids: Sequence[int], eos_id: int, opts: GenerateOptions) -> list[int]:
@@ -358,7 +359,7 @@ def generate(model: Qwen3Model, prompt_ids: Sequence[int], eos_id: int, opts: Ge
     k = check(_native.lib().brolm_qwen3_generate(model._h, p, n_prompt, int(opts.max_new_tokens), int(eos_id),
                                                  1 if opts.stop_on_eos else 0, float(s.temperature), int(s.top_k),
                                                  float(s.top_p), int(s.seed), 1 if opts.device_greedy else 0,
-                                                 out.ctypes.data_as(_native.P_i32)),
+                                                 1 if opts.device_sampling else 0, out.ctypes.data_as(_native.P_i32)),
               "generate")
     return out[:k].tolist()
 

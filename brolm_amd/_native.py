@@ -83,6 +83,8 @@ HIP_SYMBOLS = {
                                           vp, vp, vp]),
     "bx_attention_gqa_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp,
                                        vp]),
+    "bx_sample_workspace_bytes": (C.c_size_t, [C.c_int]),
+    "bx_sample_f16": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double, vp, vp, vp]),
     "bx_masked_mean_pool_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
     "bx_attention_masked_f16": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp]),
     "bx_scatter_row": (C.c_int, [vp, vp, vp, i64, C.c_int, vp]),
@@ -139,11 +141,12 @@ C_SYMBOLS = {
     "brolm_qwen3_embed_tokens": (C.c_int, [vp, P_i32, C.c_int, P_u16]),
     "brolm_qwen3_forward_embeds": (C.c_int, [vp, P_u16, C.c_int, P_f32, P_f32]),
     "brolm_qwen3_generate": (C.c_int, [vp, P_i32, C.c_int, C.c_int, C.c_int, C.c_int, f32, C.c_int, f32, u64,
-                                       C.c_int, P_i32]),
+                                       C.c_int, C.c_int, P_i32]),
     "brolm_qwen3_decode_greedy": (C.c_int, [vp, i32, C.c_int, P_i32, C.c_int]),
     "brolm_qwen3_time_decode_steps": (f64, [vp, i32, C.c_int]),
     "brolm_qwen3_decode_weight_bytes": (i64, [vp]),
     "brolm_qwen3_decode_mode": (C.c_int, [vp]),
+    "brolm_sample_token_device": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, u64]),
     "brolm_sample_token": (C.c_int, [P_f32, C.c_int, f32, C.c_int, f32, u64]),
     "brolm_prompt_ids": (C.c_int, [u64, C.c_int, C.c_int, P_i32]),
     "brolm_tokenizer_load": (vp, [cp, cp, cp]),

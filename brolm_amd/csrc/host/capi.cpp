@@ -403,7 +403,7 @@ int brolm_qwen3_forward_embeds(brolm_qwen3* m, const uint16_t* embeds, int L, fl
 
 int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, int max_new, int eos_id,
                          int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
-                         int device_greedy, int32_t* out) {
+                         int device_greedy, int device_sampling, int32_t* out) {
     int count = -1;
     const int rc = guard([&] {
         brolm::qwen::GenerateOptions o;
@@ -414,6 +414,7 @@ int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, in
         o.sampling.top_p = top_p;
         o.sampling.seed = seed;
         o.device_greedy = device_greedy != 0;
+        o.device_sampling = device_sampling != 0;
         const std::vector<int32_t> p(prompt, prompt + (n_prompt > 0 ? n_prompt : 0));
         const std::vector<int32_t> g = brolm::detail::generate(core_of(m), p, eos_id, o);
         std::memcpy(out, g.data(), g.size() * sizeof(int32_t));
@@ -535,6 +536,23 @@ int brolm_qwen3_decode_mode(brolm_qwen3* m) {
     int mode = -1;
     const int rc = guard([&] { mode = core_of(m).decode_mode(); });
     return rc == 0 ? mode : -1;
+}
+
+int brolm_sample_token_device(const uint16_t* logits_dev, int vocab, float temperature, int top_k, float top_p,
+                              uint64_t seed) {
+    int tok = -1;
+    const int rc = guard([&] {
+        if (!logits_dev || vocab <= 0) throw std::runtime_error("sample_token_device: bad arguments");
+        brolm::detail::SamplingParams p;
+        p.temperature = temperature;
+        p.top_k = top_k;
+        p.top_p = top_p;
+        std::mt19937_64 rng(seed);
+        const brotensor::Tensor row = brotensor::Tensor::view(brotensor::Device::ROCm, const_cast<uint16_t*>(logits_dev),
+                                                              1, vocab, brotensor::Dtype::FP16);
+        tok = brolm::detail::sample_token_device(row, p, rng);
+    });
+    return rc == 0 ? tok : -1;
 }
 
 int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed) {

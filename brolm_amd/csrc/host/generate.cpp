@@ -9,6 +9,8 @@
 #include "brolm/detail/profile.h"
 #include "brolm/qwen_generate.h"
 #include "brotensor/runtime.h"
+#include "brolm_hip.h"
+#include "hip_util.h"
 
 namespace brolm::detail {
 
@@ -40,6 +42,31 @@ std::vector<float> last_row_fp32(const brotensor::Tensor& logits) {
         static_cast<char*>(logits.data) + static_cast<std::size_t>(logits.rows - 1) * logits.cols * es, 1,
         logits.cols, logits.dtype);
     return download_fp32(last);
+}
+
+int sample_token_device(const brotensor::Tensor& logits, const SamplingParams& p, std::mt19937_64& rng) {
+    profile::ScopedStage ps(profile::Stage::sample);
+    if (is_greedy(p)) {
+        const std::vector<float> row = last_row_fp32(logits);
+        return argmax(row.data(), logits.cols);
+    }
+    if (logits.dtype != brotensor::Dtype::FP16 || logits.device != brotensor::Device::ROCm)
+        throw std::runtime_error("sample_token_device: logits must be FP16 on the ROCm device");
+    std::uniform_real_distribution<double> dist(0.0, 1.0);
+    const double u = dist(rng);
+    const int V = logits.cols;
+    const auto* row = static_cast<const uint16_t*>(logits.data) + static_cast<std::size_t>(logits.rows - 1) * V;
+    static thread_local brotensor::Tensor ws, tok;
+    const std::size_t wsb = bx_sample_workspace_bytes(V);
+    if (static_cast<std::size_t>(ws.rows) * 4 < wsb) ws = brotensor::Tensor::empty_on(
+        brotensor::Device::ROCm, static_cast<int>((wsb + 3) / 4), 1, brotensor::Dtype::FP32);
+    if (tok.rows == 0) tok = brotensor::Tensor::empty_on(brotensor::Device::ROCm, 1, 1, brotensor::Dtype::FP32);
+    hipx::bx(bx_sample_f16(row, V, p.temperature, p.top_k, p.top_p, u, static_cast<int32_t*>(tok.data), ws.data,
+                           hipx::stream()),
+             "sample_token_device");
+    int32_t out = 0;
+    hipx::d2h(&out, tok.data, sizeof(out));
+    return out;
 }
 
 int sample_token(const float* logits, int vocab, const SamplingParams& p, std::mt19937_64& rng) {

@@ -1,0 +1,213 @@
+// Device top-k / top-p sampling over FP16 logits (reference
+// src/detail/generate.cpp:68-142, sample_token).  The reference sorts all V
+// probabilities on the host; here one workgroup finds the same thresholds by
+// bisection on the probability value, so nothing is sorted and only the
+// chosen id leaves the device:
+//   p_i   = fp32(exp(l_i / T - max)) * fp32(1 / sum)  (sum in FP64), as the reference;
+//   M(v)  = sum of p_i >= v (FP64), C(v) = count of p_i >= v;
+//   top-k level  v_k = largest v with C(v) >= k   (k-th largest p);
+//   top-p level  v_p = largest v with M'(v) >= top_p, M' over p >= v_k
+//                (the nucleus ends at the token whose running sum crosses top_p);
+//   kept = p >= max(v_k, v_p); r = u * M(kept);
+//   token = the lowest index whose p is the largest level w with M'(w) > r.
+// The host draws u from the caller's std::mt19937_64 exactly as the reference
+// does (one uniform_real_distribution<double>(0, 1) per sampled token).
+// Ties: tokens of equal probability at a top-k boundary are all kept, and
+// within a level the lowest index is chosen, where the reference's std::sort
+// leaves the order of equal probabilities unspecified.
+#include <cmath>
+
+#include "common.h"
+
+namespace bx {
+namespace {
+
+constexpr int kST = 1024;
+
+__device__ double block_sum_d(double v, double* red) {
+    const int t = threadIdx.x;
+    red[t] = v;
+    __syncthreads();
+    for (int s = kST / 2; s > 0; s >>= 1) {
+        if (t < s) red[t] += red[t + s];
+        __syncthreads();
+    }
+    const double r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__device__ float block_max_f(float v, float* red) {
+    const int t = threadIdx.x;
+    red[t] = v;
+    __syncthreads();
+    for (int s = kST / 2; s > 0; s >>= 1) {
+        if (t < s) red[t] = fmaxf(red[t], red[t + s]);
+        __syncthreads();
+    }
+    const float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// Mass (FP64) and count of p_i >= v among p_i >= floor_v.
+__device__ void mass_at(const float* p, int V, float v, float floor_v, double* red, double& mass, double& cnt) {
+    double m = 0.0, c = 0.0;
+    const float lo = fmaxf(v, floor_v);
+    for (int i = threadIdx.x; i < V; i += kST) {
+        const float x = p[i];
+        if (x >= lo) {
+            m += x;
+            c += 1.0;
+        }
+    }
+    mass = block_sum_d(m, red);
+    cnt = block_sum_d(c, red);
+}
+
+__global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict__ logits, int V, float inv_t,
+                                                     int top_k, float top_p, double u, float* __restrict__ p,
+                                                     int32_t* __restrict__ out) {
+    __shared__ double red[kST];
+    float* redf = reinterpret_cast<float*>(red);
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < V; i += kST) mx = fmaxf(mx, h2f(logits[i]) * inv_t);
+    mx = block_max_f(mx, redf);
+    double s = 0.0;
+    for (int i = threadIdx.x; i < V; i += kST) {
+        const float e = expf(h2f(logits[i]) * inv_t - mx);
+        p[i] = e;
+        s += e;
+    }
+    s = block_sum_d(s, red);
+    const float norm = s > 0.0 ? (float)(1.0 / s) : 0.0f;
+    for (int i = threadIdx.x; i < V; i += kST) p[i] *= norm;
+    __syncthreads();
+
+    // bisection over the bit patterns of non-negative floats: lo satisfies the
+    // predicate, hi does not
+    auto search = [&](float floor_v, auto pred) {
+        uint32_t lo = 0, hi = 0x3f800001u;   // p <= 1
+        while (hi - lo > 1) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            double m, c;
+            mass_at(p, V, __uint_as_float(mid), floor_v, red, m, c);
+            if (pred(m, c)) lo = mid;
+            else hi = mid;
+        }
+        return __uint_as_float(lo);
+    };
+    auto above = [&](float v, double& m, double& c) {   // mass / count of p > v
+        mass_at(p, V, __uint_as_float(__float_as_uint(v) + 1u), 0.0f, red, m, c);
+    };
+    double m, c, mg, cg;
+    // top-k: the k-th largest probability; the reference keeps exactly k ids,
+    // so of the ids tied at that level only k - (ids above) count
+    float vk = 0.0f;
+    double take_k = -1.0;
+    if (top_k > 0 && top_k < V) {
+        vk = search(0.0f, [&](double, double cc) { return cc >= (double)top_k; });
+        above(vk, mg, cg);
+        take_k = (double)top_k - cg;
+    }
+    // kept mass before top-p: the ids above vk plus take_k of those at vk
+    mass_at(p, V, vk, vk, red, m, c);
+    above(vk, mg, cg);
+    const double kept_k = take_k < 0.0 ? m : mg + take_k * (double)vk;
+    float vf = vk;          // the lowest kept level
+    double take = take_k;   // ids kept at vf (-1: all of them)
+    if (top_p < 1.0f && kept_k >= (double)top_p) {
+        // the nucleus ends at the id whose running sum reaches top_p
+        const float vp = search(vk, [&](double mm, double) { return mm >= (double)top_p; });
+        above(vp, mg, cg);
+        double n = ceil(((double)top_p - mg) / (double)vp);
+        mass_at(p, V, vp, vp, red, m, c);
+        const double group = c - cg;
+        n = fmin(fmax(n, 1.0), group);
+        if (vp == vk && take_k >= 0.0) n = fmin(n, take_k);
+        vf = vp;
+        take = n;
+    }
+    above(vf, mg, cg);
+    mass_at(p, V, vf, vf, red, m, c);
+    const double nf = take < 0.0 ? c - cg : take;
+    const double kept = mg + nf * (double)vf;
+    int32_t chosen = -1;
+    if (kept > 0.0) {
+        const double r = u * kept;
+        // the level holding the id where the running kept mass passes r, and
+        // the position of that id among the level's ids (lowest index first)
+        const float w = search(vf, [&](double mm, double) { return mm > r; });
+        above(w, mg, cg);
+        mass_at(p, V, w, w, red, m, c);
+        const double gw = w == vf ? nf : c - cg;
+        double j = w > 0.0f ? floor((r - mg) / (double)w) : 0.0;
+        j = fmin(fmax(j, 0.0), gw - 1.0);
+        // j-th lowest index with p == w: per-thread counts over contiguous
+        // chunks, an exclusive scan, then one thread walks its chunk
+        __shared__ int cnt[kST];
+        const int chunk = (V + kST - 1) / kST;
+        const int b0 = threadIdx.x * chunk, b1 = min(V, b0 + chunk);
+        int mine = 0;
+        for (int q = b0; q < b1; ++q) mine += p[q] == w;
+        cnt[threadIdx.x] = mine;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int acc = 0;
+            for (int t = 0; t < kST; ++t) {
+                const int x = cnt[t];
+                cnt[t] = acc;
+                acc += x;
+            }
+        }
+        __syncthreads();
+        const int jj = (int)j;
+        __shared__ int pick;
+        if (threadIdx.x == 0) pick = -1;
+        __syncthreads();
+        if (jj >= cnt[threadIdx.x] && jj < cnt[threadIdx.x] + mine) {
+            int seen = cnt[threadIdx.x];
+            for (int q = b0; q < b1; ++q)
+                if (p[q] == w) {
+                    if (seen == jj) { pick = q; break; }
+                    ++seen;
+                }
+        }
+        __syncthreads();
+        chosen = pick;
+    }
+    if (chosen < 0) {   // no mass: the most probable id (lowest index on ties)
+        __shared__ int best2;
+        if (threadIdx.x == 0) best2 = 0x7fffffff;
+        __syncthreads();
+        float pm = -1.0f;
+        for (int q = threadIdx.x; q < V; q += kST) pm = fmaxf(pm, p[q]);
+        pm = block_max_f(pm, redf);
+        for (int q = threadIdx.x; q < V; q += kST)
+            if (p[q] == pm) atomicMin(&best2, q);
+        __syncthreads();
+        chosen = best2 == 0x7fffffff ? 0 : best2;
+    }
+    if (threadIdx.x == 0) out[0] = chosen;
+}
+
+}  // namespace
+}  // namespace bx
+
+using namespace bx;
+
+extern "C" {
+
+size_t bx_sample_workspace_bytes(int vocab) { return vocab > 0 ? (size_t)vocab * sizeof(float) : 0; }
+
+int bx_sample_f16(const uint16_t* logits, int vocab, float temperature, int top_k, float top_p, double u,
+                  int32_t* out, void* workspace, void* stream) {
+    if (!logits || !out || !workspace || vocab <= 0) return fail(BX_EINVAL, "sample: bad arguments");
+    if (!(temperature > 0.0f)) return fail(BX_EINVAL, "sample: temperature must be positive (greedy uses argmax)");
+    if (!(u >= 0.0 && u < 1.0)) return fail(BX_EINVAL, "sample: u must be in [0, 1)");
+    sample_kernel<<<1, kST, 0, as_stream(stream)>>>(logits, vocab, 1.0f / temperature, top_k, top_p, u,
+                                                    static_cast<float*>(workspace), out);
+    return launch_check("sample");
+}
+
+}  // extern "C"

@@ -23,6 +23,9 @@ struct SamplingParams {
 };
 
 int sample_token(const float* logits, int vocab, const SamplingParams& p, std::mt19937_64& rng);
+// sample_token on the device for the last row of FP16 device logits: the same
+// RNG draw, only the chosen id is downloaded (greedy: host argmax of the row).
+int sample_token_device(const brotensor::Tensor& logits, const SamplingParams& p, std::mt19937_64& rng);
 std::vector<float> last_row_fp32(const brotensor::Tensor& logits);
 
 struct GenerateOptions {
@@ -31,6 +34,9 @@ struct GenerateOptions {
     bool stop_on_eos = true;
     // Greedy only: keep argmax + token feedback on the device (default on).
     bool device_greedy = true;
+    // Sampling (temperature > 0, top_k != 1): softmax, top-k / top-p and the
+    // draw on the device (default on); off: download the row, sample on host.
+    bool device_sampling = true;
 };
 
 inline bool is_greedy(const SamplingParams& p) { return p.temperature <= 0.0f || p.top_k == 1; }
@@ -45,9 +51,14 @@ std::vector<int32_t> generate(Model& model, const std::vector<int32_t>& prompt_i
     std::mt19937_64 rng(opts.sampling.seed);
 
     brotensor::Tensor logits;
+    const bool on_device = opts.device_sampling && !is_greedy(opts.sampling);
+    auto pick = [&]() {
+        if (on_device) return sample_token_device(logits, opts.sampling, rng);
+        const std::vector<float> row = last_row_fp32(logits);
+        return sample_token(row.data(), vocab, opts.sampling, rng);
+    };
     model.forward_last(prompt_ids.data(), static_cast<int>(prompt_ids.size()), logits);
-    std::vector<float> row = last_row_fp32(logits);
-    int next = sample_token(row.data(), vocab, opts.sampling, rng);
+    int next = pick();
     const bool stop = opts.stop_on_eos && eos_id >= 0;
     if (stop && next == eos_id) return generated;
     generated.push_back(static_cast<int32_t>(next));
@@ -68,8 +79,7 @@ std::vector<int32_t> generate(Model& model, const std::vector<int32_t>& prompt_i
     while (static_cast<int>(generated.size()) < opts.max_new_tokens) {
         int32_t cur = generated.back();
         model.forward_last(&cur, 1, logits);
-        row = last_row_fp32(logits);
-        next = sample_token(row.data(), vocab, opts.sampling, rng);
+        next = pick();
         if (stop && next == eos_id) break;
         generated.push_back(static_cast<int32_t>(next));
     }

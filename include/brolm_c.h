@@ -131,7 +131,7 @@ int brolm_qwen3_forward_embeds(brolm_qwen3* m, const uint16_t* embeds, int L, fl
 /* qwen::generate (include/brolm/qwen_generate.h:45-47); returns the count. */
 int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, int max_new, int eos_id,
                          int stop_on_eos, float temperature, int top_k, float top_p, uint64_t seed,
-                         int device_greedy, int32_t* out);
+                         int device_greedy, int device_sampling, int32_t* out);
 /* DenseDecoder::decode_greedy / time_decode_steps / decode_weight_bytes. */
 int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id);
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n);
@@ -142,6 +142,12 @@ int brolm_qwen3_decode_mode(brolm_qwen3* m);
 
 /* sample_token with a fresh std::mt19937_64(seed) (src/detail/generate.cpp:68-142). */
 int brolm_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, uint64_t seed);
+/* The same draw on the device (sample_token_device, include/brolm/detail/generate.h):
+ * logits_dev is one FP16 row in device memory; u is the first
+ * uniform_real_distribution<double>(0, 1) draw of std::mt19937_64(seed).
+ * Returns the token id, or -1 with brolm_last_error(). */
+int brolm_sample_token_device(const uint16_t* logits_dev, int vocab, float temperature, int top_k, float top_p,
+                              uint64_t seed);
 
 /* Synthetic prompt of tools/bench_decode.cpp:208-213: std::mt19937_64(seed)() % vocab. */
 int brolm_prompt_ids(uint64_t seed, int n, int vocab, int32_t* out);

@@ -139,6 +139,16 @@ int bx_silu_f16(const uint16_t* x, uint16_t* y, int64_t n, void* stream);
 int bx_mul_f16(uint16_t* a, const uint16_t* b, int64_t n, void* stream);
 /* K17: add_inplace(h, proj) (dense_decoder.cpp:616, :645); h FP32 or FP16. */
 int bx_add_inplace(void* h, int h_is_f32, const uint16_t* x, int64_t n, void* stream);
+/* sample_token (src/detail/generate.cpp:68-142) for temperature > 0 on the
+ * device: softmax of logits / temperature, top-k then top-p truncation in
+ * descending probability, and the token where the running kept mass first
+ * exceeds u * kept (u: the host's uniform_real_distribution<double>(0, 1)
+ * draw).  One FP16 logits row (device); *out (device int32).  Equal
+ * probabilities resolve to the lowest index.  workspace:
+ * bx_sample_workspace_bytes(vocab). */
+size_t bx_sample_workspace_bytes(int vocab);
+int bx_sample_f16(const uint16_t* logits, int vocab, float temperature, int top_k, float top_p, double u,
+                  int32_t* out, void* workspace, void* stream);
 /* masked_mean_pool_forward(x, mask, out) (src/llm2vec.cpp:139-153): out[c] =
  * sum_r mask[r] x[r, c] / sum_r mask[r] over the L rows of x (L, cols) FP16,
  * FP32 sums, FP16 out (cols); mask (device FP32, L) or NULL for all rows; an
