@@ -254,6 +254,17 @@ def main() -> int:
         tok = int(model.forward_last([tok]).argmax())
     ref_tok_s = n_ref / (time.perf_counter() - t0)
 
+    # sampled generation (temperature 0.8, top-k 40, top-p 0.95): the draw on
+    # the device (default) against the host sampler (logits download + sort)
+    sampled = {}
+    for dev in (True, False):
+        sp = ba.SamplingParams(temperature=0.8, top_k=40, top_p=0.95, seed=1)
+        opts = ba.GenerateOptions(max_new_tokens=64, sampling=sp, stop_on_eos=False, device_sampling=dev)
+        ba.generate(model, prompt[:16], -1, opts)
+        t0 = time.perf_counter()
+        n = len(ba.generate(model, prompt[:16], -1, opts))
+        sampled["device" if dev else "host"] = round(n / (time.perf_counter() - t0), 2)
+
     # text path: the checkpoint's own tokenizer (host), and generate_text
     # (encode -> greedy generate -> decode) end to end; Qwen3 only (Mistral's
     # tokenizer is Tekken, not part of this build)
@@ -292,6 +303,8 @@ def main() -> int:
         "kv_bytes_per_token_avg": int(kv_bytes),
         "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
         "encode_tok_s": round(n_enc / encode_s, 1),
+        "sampled_tok_s": sampled,
+        "sampled_note": "generate, 64 tokens, T 0.8 / top-k 40 / top-p 0.95: device sampler vs host sampler",
         "encode_note": f"forward_encode of {n_enc} tokens (bidirectional, cacheless, hidden states downloaded)",
         "ref_loop_tok_s": round(ref_tok_s, 2),
         "tokenizer": tokenizer,
