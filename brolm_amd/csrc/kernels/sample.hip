@@ -50,6 +50,29 @@ __device__ float block_max_f(float v, float* red) {
     return r;
 }
 
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Both sums over the workgroup in a fixed order (lanes by butterfly, then
+// the 16 wave partials by every wave alike): one barrier per pass.
+__device__ void block_sum2(double& a, double& b, double* red) {
+    a = wave_sum_d(a);
+    b = wave_sum_d(b);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (l == 0) {
+        red[w] = a;
+        red[kST / 64 + w] = b;
+    }
+    __syncthreads();
+    double x = l < kST / 64 ? red[l] : 0.0, y = l < kST / 64 ? red[kST / 64 + l] : 0.0;
+    a = wave_sum_d(x);
+    b = wave_sum_d(y);
+    __syncthreads();
+}
+
 // Mass (FP64) and count of p_i >= v among p_i >= floor_v.
 __device__ void mass_at(const float* p, int V, float v, float floor_v, double* red, double& mass, double& cnt) {
     double m = 0.0, c = 0.0;
@@ -61,8 +84,9 @@ __device__ void mass_at(const float* p, int V, float v, float floor_v, double* r
             c += 1.0;
         }
     }
-    mass = block_sum_d(m, red);
-    cnt = block_sum_d(c, red);
+    block_sum2(m, c, red);
+    mass = m;
+    cnt = c;
 }
 
 __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict__ logits, int V, float inv_t,
