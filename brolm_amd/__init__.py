@@ -507,6 +507,9 @@ class SynthSpec:
     output: str = "Q6_K"
     stddev: float = 0.02
     seed: int = 0
+    # type of attn_v / ffn_down on llama.cpp's use_more_bits layers ("" none):
+    # "Q6_K" over a Q4_K base gives a Q4_K_M-style per-layer mix
+    more_bits: str = ""
 
 
 def _synth_c(spec: SynthSpec) -> _native.SynthSpecC:
@@ -518,6 +521,7 @@ def _synth_c(spec: SynthSpec) -> _native.SynthSpecC:
     for f in ("embed", "q", "k", "v", "o", "gate", "up", "down", "output"):
         setattr(s, f + "_type", GGML[getattr(spec, f)])
     s.seed = int(spec.seed)
+    s.more_bits_type = GGML[spec.more_bits] if spec.more_bits else -1
     return s
 
 

@@ -51,14 +51,15 @@ class SynthSpecC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "hidden", "intermediate", "layers", "n_q", "n_kv", "head_dim")] + [
         ("eps", C.c_float), ("theta", C.c_float), ("context", C.c_int), ("tied", C.c_int)] + [
         (n, C.c_int) for n in ("embed_type", "q_type", "k_type", "v_type", "o_type", "gate_type", "up_type",
-                               "down_type", "output_type")] + [("stddev", C.c_float), ("seed", C.c_uint64)]
+                               "down_type", "output_type")] + [("stddev", C.c_float), ("seed", C.c_uint64),
+                                                                ("more_bits_type", C.c_int)]
 
 
 class DecodeDimsC(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("hidden", "intermediate", "n_q", "n_kv", "head_dim", "vocab", "cap")] + [
         ("eps", C.c_float)] + [(n, C.c_int) for n in ("qkv_type_q", "qkv_type_k", "qkv_type_v", "o_type",
                                                       "gate_type", "up_type", "down_type", "lm_type",
-                                                      "no_qk_norm")]
+                                                      "no_qk_norm", "v_alt_type", "down_alt_type")]
 
 
 # symbol -> (restype, argtypes); every symbol of include/brolm_hip.h

@@ -163,6 +163,8 @@ int synth_write(const brolm_synth_qwen3_spec* s, const char* path, const char* a
         q.output = brotensor::dtype_from_ggml(s->output_type);
         q.stddev = s->stddev;
         q.seed = s->seed;
+        q.more_bits_type = s->more_bits_type;
+        if (q.more_bits_type >= 0) (void)brotensor::dtype_from_ggml(q.more_bits_type);  // throws if unknown
         q.arch = arch;
         brolm::synth::write_qwen3_gguf(q, path);
     });

@@ -219,20 +219,9 @@ void DenseDecoder::forward(const int32_t* ids, int L, bt::Tensor& logits_out, bt
 
 void DenseDecoder::forward_last(const int32_t* ids, int L, bt::Tensor& logits_out) {
     check_forward("forward_last", ids, L, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
-    if (L == 1 && !profile::enabled()) {
-        bx_decode_dims d{};
-        d.hidden = cfg_.hidden_size; d.intermediate = cfg_.intermediate_size;
-        d.n_q = cfg_.num_attention_heads; d.n_kv = cfg_.num_key_value_heads; d.head_dim = cfg_.head_dim;
-        d.vocab = cfg_.vocab_size; d.cap = max_seq_len_; d.eps = cfg_.rms_norm_eps;
-        d.qkv_type_q = ggml_of(layers_[0].Wq); d.qkv_type_k = ggml_of(layers_[0].Wk);
-        d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
-        d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
-        d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
-        d.no_qk_norm = cfg_.use_qk_norm ? 0 : 1;
-        if (bx_decode_ws_bytes(&d) != 0) {
-            decode_step_(ids[0], logits_out);
-            return;
-        }
+    if (L == 1 && !profile::enabled() && fused_step_ok_()) {
+        decode_step_(ids[0], logits_out);
+        return;
     }
     {
         profile::ScopedStage ps(profile::Stage::idx_upload);
@@ -404,31 +393,77 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
 
 void DenseDecoder::invalidate_graph_() { graph_.reset(); }
 
-DecodeGraphSession& DenseDecoder::session_() {
-    if (graph_ && graph_->cap == max_seq_len_) return *graph_;
-    graph_.reset();
-    auto s = std::make_unique<DecodeGraphSession>();
-    s->cap = max_seq_len_;
-    bx_decode_dims& d = s->dims;
+// The step's dims: shapes, layer 0's matrix types, and the second attn_v /
+// ffn_down type of a mixed (Q4_K_M-style) file when one exists.
+bx_decode_dims DenseDecoder::decode_dims_() const {
+    bx_decode_dims d{};
     d.hidden = cfg_.hidden_size; d.intermediate = cfg_.intermediate_size;
     d.n_q = cfg_.num_attention_heads; d.n_kv = cfg_.num_key_value_heads; d.head_dim = cfg_.head_dim;
     d.vocab = cfg_.vocab_size; d.cap = max_seq_len_; d.eps = cfg_.rms_norm_eps;
-    d.qkv_type_q = ggml_of(layers_[0].Wq); d.qkv_type_k = ggml_of(layers_[0].Wk);
-    d.qkv_type_v = ggml_of(layers_[0].Wv); d.o_type = ggml_of(layers_[0].Wo);
-    d.gate_type = ggml_of(layers_[0].gate_W); d.up_type = ggml_of(layers_[0].up_W);
-    d.down_type = ggml_of(layers_[0].down_W); d.lm_type = ggml_of(lm_head_);
+    const Layer& L0 = layers_[0];
+    d.qkv_type_q = ggml_of(L0.Wq); d.qkv_type_k = ggml_of(L0.Wk); d.qkv_type_v = ggml_of(L0.Wv);
+    d.o_type = ggml_of(L0.Wo); d.gate_type = ggml_of(L0.gate_W); d.up_type = ggml_of(L0.up_W);
+    d.down_type = ggml_of(L0.down_W); d.lm_type = ggml_of(lm_head_);
     d.no_qk_norm = cfg_.use_qk_norm ? 0 : 1;
     for (const Layer& L : layers_) {
-        if (ggml_of(L.Wq) != d.qkv_type_q || ggml_of(L.Wk) != d.qkv_type_k || ggml_of(L.Wv) != d.qkv_type_v ||
-            ggml_of(L.Wo) != d.o_type || ggml_of(L.gate_W) != d.gate_type || ggml_of(L.up_W) != d.up_type ||
-            ggml_of(L.down_W) != d.down_type)
-            fail("decode step: per-layer weight types must match across layers");
+        if (ggml_of(L.Wv) != d.qkv_type_v && d.v_alt_type == 0) d.v_alt_type = ggml_of(L.Wv);
+        if (ggml_of(L.down_W) != d.down_type && d.down_alt_type == 0) d.down_alt_type = ggml_of(L.down_W);
+    }
+    return d;
+}
+
+// Whether single-token steps can run fused (persistent kernel or the graph of
+// per-stage kernels): every layer's types are ones the step kernels read,
+// with q/k and gate/up sharing a type, and the shape fits the step's
+// workspace.  Otherwise forward_last and decode_greedy take the op path, as
+// the reference does for any weight dtype (compute.h:54-86).
+bool DenseDecoder::fused_step_ok_() const {
+    if (max_seq_len_ == 0 || layers_.empty() || embed_tokens_.size() == 0) return false;
+    auto known = [](int t) {
+        return t == BX_TYPE_Q4_K || t == BX_TYPE_Q6_K || t == BX_TYPE_Q8_0 || t == BX_TYPE_F16;
+    };
+    for (const Layer& L : layers_) {
+        const int t[7] = {ggml_of(L.Wq), ggml_of(L.Wk), ggml_of(L.Wv), ggml_of(L.Wo), ggml_of(L.gate_W),
+                          ggml_of(L.up_W), ggml_of(L.down_W)};
+        for (int x : t)
+            if (!known(x)) return false;
+        if (t[0] != t[1] || t[4] != t[5]) return false;
+    }
+    if (!known(ggml_of(lm_head_))) return false;
+    const bx_decode_dims d = decode_dims_();
+    return bx_decode_ws_bytes(&d) != 0;
+}
+
+// The persistent kernel serves one type per role except attn_v and ffn_down,
+// which may take a second type (decode_dims_) in some layers.
+static bool persist_types_ok(const bx_decode_dims& d, const std::vector<bx_decode_layer>& ls) {
+    for (const bx_decode_layer& L : ls) {
+        if (L.type_q != d.qkv_type_q || L.type_k != d.qkv_type_k || L.type_o != d.o_type ||
+            L.type_gate != d.gate_type || L.type_up != d.up_type)
+            return false;
+        if (L.type_v != d.qkv_type_v && L.type_v != d.v_alt_type) return false;
+        if (L.type_down != d.down_type && L.type_down != d.down_alt_type) return false;
+    }
+    return true;
+}
+
+DecodeGraphSession& DenseDecoder::session_() {
+    if (graph_ && graph_->cap == max_seq_len_) return *graph_;
+    graph_.reset();
+    if (!fused_step_ok_()) fail(std::string("decode step: unsupported shape or weight types: ") + bx_last_error());
+    auto s = std::make_unique<DecodeGraphSession>();
+    s->cap = max_seq_len_;
+    bx_decode_dims& d = s->dims;
+    d = decode_dims_();
+    for (const Layer& L : layers_) {
         bx_decode_layer bl{};
         bl.in_ln = L.input_ln.data; bl.q_norm = L.q_norm.data; bl.k_norm = L.k_norm.data;
         bl.post_ln = L.post_attn_ln.data;
         bl.Wq = L.Wq.data; bl.Wk = L.Wk.data; bl.Wv = L.Wv.data; bl.Wo = L.Wo.data;
         bl.Wg = L.gate_W.data; bl.Wu = L.up_W.data; bl.Wd = L.down_W.data;
         bl.Kc = L.K_cache.data; bl.Vc = L.V_cache.data;
+        bl.type_q = ggml_of(L.Wq); bl.type_k = ggml_of(L.Wk); bl.type_v = ggml_of(L.Wv); bl.type_o = ggml_of(L.Wo);
+        bl.type_gate = ggml_of(L.gate_W); bl.type_up = ggml_of(L.up_W); bl.type_down = ggml_of(L.down_W);
         s->layers.push_back(bl);
     }
     const std::size_t wsb = bx_decode_ws_bytes(&d);
@@ -445,7 +480,7 @@ DecodeGraphSession& DenseDecoder::session_() {
                 "hipHostMalloc");
     hipx::check(hipEventCreateWithFlags(&s->staged, hipEventDisableTiming), "hipEventCreate");
     s->use_graph = !env_flag("BROLM_NO_GRAPH");
-    if (s->use_graph && !env_flag("BROLM_NO_PERSIST")) {
+    if (s->use_graph && !env_flag("BROLM_NO_PERSIST") && persist_types_ok(d, s->layers)) {
         s->pws_bytes = bx_persist_ws_bytes(&d);
         if (s->pws_bytes != 0) {
             hipx::check(hipMalloc(&s->pws, s->pws_bytes), "hipMalloc persist ws");
@@ -566,6 +601,27 @@ int DenseDecoder::decode_greedy(int32_t token, int n, int32_t* out, int eos_id) 
     if (n <= 0) return 0;
     check_forward("decode_greedy", &token, 1, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
     if (cache_len_ + n > max_seq_len_) fail("decode_greedy: cache_len + n exceeds allocated cache capacity");
+    if (!fused_step_ok_()) {
+        // op path, one token at a time: logits to the host, lowest-index argmax
+        // (generate.cpp:38-48)
+        std::vector<uint16_t> row(static_cast<std::size_t>(cfg_.vocab_size));
+        bt::Tensor lg;
+        int32_t cur = token;
+        for (int i = 0; i < n; ++i) {
+            forward_last(&cur, 1, lg);
+            hipx::d2h(row.data(), lg.data, row.size() * sizeof(uint16_t));
+            int best = 0;
+            float bv = bt::fp16_bits_to_fp32(row[0]);
+            for (int j = 1; j < cfg_.vocab_size; ++j) {
+                const float v = bt::fp16_bits_to_fp32(row[static_cast<std::size_t>(j)]);
+                if (v > bv) { bv = v; best = j; }
+            }
+            out[i] = best;
+            cur = best;
+            if (eos_id >= 0 && best == eos_id) return i + 1;
+        }
+        return n;
+    }
     DecodeGraphSession& s = session_();
     int done = 0;
     int32_t cur = token;

@@ -311,6 +311,11 @@ SynthVocab synth_vocab(int vocab) {
 
 }  // namespace
 
+bool use_more_bits(int i_layer, int n_layers) {
+    const int e = n_layers / 8;
+    return i_layer < e || i_layer >= 7 * n_layers / 8 || (i_layer - e) % 3 == 2;
+}
+
 std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
     if (s.hidden <= 0 || s.intermediate <= 0 || s.layers <= 0 || s.vocab <= 0 || s.n_q <= 0 || s.n_kv <= 0 ||
         s.head_dim <= 0)
@@ -360,7 +365,10 @@ std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
         items.push_back({p + "attn_norm.weight", bt::Dtype::FP32, 1, H, true});
         items.push_back({p + "attn_q.weight", s.q, qd, H, false});
         items.push_back({p + "attn_k.weight", s.k, kvd, H, false});
-        items.push_back({p + "attn_v.weight", s.v, kvd, H, false});
+        const bool more = s.more_bits_type >= 0 && use_more_bits(l, s.layers);
+        const bt::Dtype vt = more ? bt::dtype_from_ggml(s.more_bits_type) : s.v;
+        const bt::Dtype dt = more ? bt::dtype_from_ggml(s.more_bits_type) : s.down;
+        items.push_back({p + "attn_v.weight", vt, kvd, H, false});
         items.push_back({p + "attn_output.weight", s.o, H, qd, false});
         if (qk_norm) {
             items.push_back({p + "attn_q_norm.weight", bt::Dtype::FP32, 1, s.head_dim, true});
@@ -369,7 +377,7 @@ std::vector<std::uint8_t> make_qwen3_gguf(const Qwen3Spec& s) {
         items.push_back({p + "ffn_norm.weight", bt::Dtype::FP32, 1, H, true});
         items.push_back({p + "ffn_gate.weight", s.gate, F, H, false});
         items.push_back({p + "ffn_up.weight", s.up, F, H, false});
-        items.push_back({p + "ffn_down.weight", s.down, H, F, false});
+        items.push_back({p + "ffn_down.weight", dt, H, F, false});
     }
     items.push_back({"output_norm.weight", bt::Dtype::FP32, 1, H, true});
     if (!s.tied) items.push_back({"output.weight", s.output, s.vocab, H, false});

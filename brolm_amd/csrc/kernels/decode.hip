@@ -577,11 +577,17 @@ int bx_decode_layer_run(const bx_decode_dims* d, const bx_decode_layer* L, const
     const int qd = d->n_q * hd, kvd = d->n_kv * hd;
     hipStream_t st = as_stream(stream);
 
+    // this layer's own matrix types (a mixed file differs per layer)
+    const int lts[7] = {L->type_q, L->type_k, L->type_v, L->type_o, L->type_gate, L->type_up, L->type_down};
+    for (int t : lts)
+        if (!known_type(t)) return fail(BX_EUNSUPPORTED, "decode_layer: unsupported weight type");
+    if (L->type_q != L->type_k || L->type_gate != L->type_up)
+        return fail(BX_EUNSUPPORTED, "decode_layer: q/k or gate/up types differ");
     Seg3 seg{};
-    seg.W[0] = L->Wq; seg.type[0] = d->qkv_type_q; seg.rows[0] = qd;
-    seg.W[1] = L->Wk; seg.type[1] = d->qkv_type_k; seg.rows[1] = kvd;
-    seg.W[2] = L->Wv; seg.type[2] = d->qkv_type_v; seg.rows[2] = kvd;
-    if (int rc = launch_qkv(d->qkv_type_q, d->qkv_type_v, upl_for(H), gemv_blocks(qd + 2 * kvd, H), norm_lds(H), st,
+    seg.W[0] = L->Wq; seg.type[0] = L->type_q; seg.rows[0] = qd;
+    seg.W[1] = L->Wk; seg.type[1] = L->type_k; seg.rows[1] = kvd;
+    seg.W[2] = L->Wv; seg.type[2] = L->type_v; seg.rows[2] = kvd;
+    if (int rc = launch_qkv(L->type_q, L->type_v, upl_for(H), gemv_blocks(qd + 2 * kvd, H), norm_lds(H), st,
                             h, static_cast<const uint16_t*>(L->in_ln), d->eps, H, seg, qkv))
         return rc;
 
@@ -605,12 +611,12 @@ int bx_decode_layer_run(const bx_decode_dims* d, const bx_decode_layer* L, const
     combine_kernel<<<d->n_q, 128, 0, st>>>(part, w.S, hd, attn);
     if (int rc = launch_check("decode combine")) return rc;
 
-    if (int rc = launch_resid(d->o_type, upl_for(qd), gemv_blocks(H, qd), norm_lds(qd), st, attn, qd, L->Wo, H, h))
+    if (int rc = launch_resid(L->type_o, upl_for(qd), gemv_blocks(H, qd), norm_lds(qd), st, attn, qd, L->Wo, H, h))
         return rc;
-    if (int rc = launch_mlp(d->gate_type, upl_for(H), gemv_blocks(2 * F, H), norm_lds(H), st, h,
+    if (int rc = launch_mlp(L->type_gate, upl_for(H), gemv_blocks(2 * F, H), norm_lds(H), st, h,
                             static_cast<const uint16_t*>(L->post_ln), d->eps, H, L->Wg, L->Wu, F, act))
         return rc;
-    return launch_resid(d->down_type, upl_for(F), gemv_blocks(H, F), norm_lds(F), st, act, F, L->Wd, H, h);
+    return launch_resid(L->type_down, upl_for(F), gemv_blocks(H, F), norm_lds(F), st, act, F, L->Wd, H, h);
 }
 
 int bx_decode_head(const bx_decode_dims* d, const uint16_t* final_norm, const void* lm_head, uint16_t* logits,

@@ -1398,6 +1398,11 @@ int persist_layout(const bx_decode_dims& d, int G, PLayout& o) {
     if (d.hidden > 4 * 4 * kPT) return fail(BX_EUNSUPPORTED, "persist: hidden above 4096");
     if (d.qkv_type_q != d.qkv_type_k || d.gate_type != d.up_type)
         return fail(BX_EUNSUPPORTED, "persist: q/k or gate/up formats differ");
+    // one format per role across layers (the step is instantiated per format
+    // mix); a file that mixes attn_v / ffn_down types by layer runs the
+    // per-stage step, which reads each layer's types
+    if ((d.v_alt_type && d.v_alt_type != d.qkv_type_v) || (d.down_alt_type && d.down_alt_type != d.down_type))
+        return fail(BX_EUNSUPPORTED, "persist: per-layer attn_v / ffn_down types differ");
     if (d.hidden % 256 || d.intermediate % 256 || qd % 256) return fail(BX_EUNSUPPORTED, "persist: widths");
     const int smax = G / d.n_kv;
     if (smax < 1 || G < 3) return fail(BX_EUNSUPPORTED, "persist: too few CUs");

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "brotensor/tensor.h"
+#include "brolm_hip.h"
 
 namespace brolm::detail::weights { class Source; }
 
@@ -106,6 +107,8 @@ private:
                      bool logits_last_row_only = false);
     void decode_step_(int32_t token, brotensor::Tensor& logits_out);
     DecodeGraphSession& session_();
+    bool fused_step_ok_() const;
+    ::bx_decode_dims decode_dims_() const;
     void invalidate_graph_();
     void ensure_rope_table_();
 

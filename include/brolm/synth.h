@@ -42,7 +42,16 @@ struct Qwen3Spec {
     // attn_q_norm / attn_k_norm gammas; any other name ("llama", the arch
     // llama.cpp gives Mistral text models) writes none (no QK-norm).
     std::string arch = "qwen3";
+    // ggml type id written for attn_v and ffn_down on the layers llama.cpp's
+    // Q4_K_M recipe gives more bits (use_more_bits: the first and last eighth
+    // of the layers and every third layer between), or -1 for none: the
+    // per-layer format mix of a real Q4_K_M file (base type from v / down).
+    int more_bits_type = -1;
 };
+
+// llama.cpp's layer rule for the larger attn_v / ffn_down type of its _M
+// mixes: i < n/8, i >= 7n/8, or (i - n/8) % 3 == 2.
+bool use_more_bits(int i_layer, int n_layers);
 
 // Key of a tensor's random stream: seed mixed with the FNV-1a hash of its name.
 std::uint64_t tensor_key(std::uint64_t seed, const std::string& name);

@@ -36,6 +36,7 @@ typedef struct {
     int embed_type, q_type, k_type, v_type, o_type, gate_type, up_type, down_type, output_type;
     float stddev;
     uint64_t seed;
+    int more_bits_type;  /* ggml id for attn_v / ffn_down on use_more_bits layers, -1: none */
 } brolm_synth_qwen3_spec;
 
 const char* brolm_last_error(void);

@@ -172,12 +172,22 @@ typedef struct {
      * come from the projections; the layers' q_norm / k_norm are not read.
      * 0 (a zero-initialized struct): Qwen3's QK-norm. */
     int no_qk_norm;
+    /* A second type that some layers use for attn_v / ffn_down (llama.cpp
+     * Q4_K_M raises them to Q6_K on some layers only), or 0 when every
+     * layer has qkv_type_v / down_type.  Each layer's own types travel in
+     * its bx_decode_layer. */
+    int v_alt_type, down_alt_type;
 } bx_decode_dims;
 
 typedef struct {
     const void *in_ln, *q_norm, *k_norm, *post_ln;  /* FP16 gammas (q/k norms permuted) */
     const void *Wq, *Wk, *Wv, *Wo, *Wg, *Wu, *Wd;   /* carriers or FP16 */
     void *Kc, *Vc;                                  /* FP16 (cap, n_kv*hd) */
+    /* BX_TYPE_* of this layer's matrices.  Layers may differ: a llama.cpp
+     * Q4_K_M file stores attn_v / ffn_down as Q6_K in some layers only (the
+     * reference dispatches per weight on its dtype, compute.h:54-86).  The
+     * bx_decode_dims types describe layer 0 and size the workspaces. */
+    int type_q, type_k, type_v, type_o, type_gate, type_up, type_down, type_pad;
 } bx_decode_layer;
 
 size_t bx_decode_ws_bytes(const bx_decode_dims* d);

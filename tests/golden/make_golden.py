@@ -13,6 +13,20 @@ model_small.npz
              (std::mt19937_64(42) % vocab, tools/bench_decode.cpp:208-213),
              plus a hash of the synthetic checkpoint bytes so a change in the
              generator is told apart from a change in the decoder.
+model_full.npz
+             full-depth greedy fixtures at BASELINE.json shapes, each with the
+             oracle's per-step top-2 logit margins and the checkpoint hash:
+             "q4k" Qwen3-1.7B (28 layers, Q4_K with Q6_K v / down / output,
+             untied; configs[2]'s format mix), 32-token prompt, 32 tokens;
+             "bf16" Qwen3-0.6B random-init BF16, tied, 32-token
+             prompt, 128 tokens.  Prompts: std::mt19937_64(42) % vocab.
+model_8b_width.npz
+             Qwen3-8B widths (hidden 4096, FFN 12288, 32 / 8 heads of 128,
+             vocab 151936; all-Q4_K layers, Q6_K output: configs[4]'s mix)
+             over 2 layers: the oracle's logits at every 37th vocabulary id,
+             argmax and top-2 margin after a 2048-token prefill and after
+             each of 8 greedy steps (the oracle's prefill takes about a minute
+             on 8 cores, too slow to rerun inside a GPU test).
 The reference has no numeric fixtures for this path (its quant tests check
 finiteness against downloaded checkpoints only), so these are the vectors.
 """
@@ -68,11 +82,81 @@ def make_model_fixture(tmp: Path) -> dict:
             "sha256": np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)}
 
 
+# Full-depth shapes of BASELINE.json (synthetic, seeded): name -> (spec, prompt, new tokens)
+FULL = {
+    "q4k": (dict(vocab=151936, hidden=2048, intermediate=6144, layers=28, n_q=16, n_kv=8, head_dim=128,
+                 tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K", gate="Q4_K", up="Q4_K",
+                 down="Q6_K", output="Q6_K", seed=0), 32, 32),
+    "bf16": (dict(vocab=151936, hidden=1024, intermediate=3072, layers=28, n_q=16, n_kv=8, head_dim=128,
+                  tied=True, embed="BF16", q="BF16", k="BF16", v="BF16", o="BF16", gate="BF16", up="BF16",
+                  down="BF16", output="BF16", seed=0), 32, 128),
+}
+
+
+def make_full_fixture(tmp: Path) -> dict:
+    import brolm_amd as ba
+    import oracle
+    from conftest import write_synth
+
+    out = {}
+    for name, (spec, n_prompt, n_new) in FULL.items():
+        path = write_synth(tmp, spec, f"full_{name}")
+        prompt = ba.prompt_ids(n_prompt, spec["vocab"], seed=42)
+        m = oracle.Model(str(path))
+        toks, margins = m.generate_greedy(prompt, n_new)
+        out[f"{name}_prompt"] = np.asarray(prompt, np.int32)
+        out[f"{name}_tokens"] = np.asarray(toks, np.int32)
+        out[f"{name}_margins"] = margins.astype(np.float32)
+        out[f"{name}_sha256"] = np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)
+        print(name, "margins min", float(margins.min()), "tokens", toks[:8], flush=True)
+        del m
+        path.unlink()
+    return out
+
+
+W8B = dict(vocab=151936, hidden=4096, intermediate=12288, layers=2, n_q=32, n_kv=8, head_dim=128, tied=False,
+           embed="Q4_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K", up="Q4_K", down="Q4_K",
+           output="Q6_K", seed=5)
+W8B_PROMPT, W8B_STEPS, W8B_STRIDE = 2048, 8, 37
+
+
+def make_8b_width_fixture(tmp: Path) -> dict:
+    import brolm_amd as ba
+    import oracle
+    from conftest import write_synth
+
+    path = write_synth(tmp, W8B, "w8b")
+    prompt = ba.prompt_ids(W8B_PROMPT, W8B["vocab"], seed=42)
+    m = oracle.Model(str(path))
+    m.allocate_cache(W8B_PROMPT + W8B_STEPS + 1)
+    rows, arg, marg, toks = [], [], [], []
+    lg = m.forward(prompt, last_only=True)[0]
+    for step in range(W8B_STEPS + 1):
+        top = np.argsort(lg)[::-1][:2]
+        rows.append(lg[::W8B_STRIDE].copy())
+        arg.append(int(top[0]))
+        marg.append(float(lg[top[0]] - lg[top[1]]))
+        if step == W8B_STEPS:
+            break
+        toks.append(int(top[0]))
+        lg = m.forward([toks[-1]], last_only=True)[0]
+    return {"logits": np.stack(rows).astype(np.float32), "argmax": np.asarray(arg, np.int32),
+            "margins": np.asarray(marg, np.float32), "tokens": np.asarray(toks, np.int32),
+            "sha256": np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)}
+
+
 def main() -> None:
-    np.savez_compressed(HERE / "blocks.npz", **make_blocks())
+    which = sys.argv[1:] or ["blocks", "small", "full", "w8b"]
+    if "blocks" in which:
+        np.savez_compressed(HERE / "blocks.npz", **make_blocks())
     with tempfile.TemporaryDirectory() as td:
-        np.savez_compressed(HERE / "model_small.npz", **make_model_fixture(Path(td)))
-    print("wrote", HERE / "blocks.npz", HERE / "model_small.npz")
+        if "small" in which:
+            np.savez_compressed(HERE / "model_small.npz", **make_model_fixture(Path(td)))
+        if "full" in which:
+            np.savez_compressed(HERE / "model_full.npz", **make_full_fixture(Path(td)))
+        if "w8b" in which:
+            np.savez_compressed(HERE / "model_8b_width.npz", **make_8b_width_fixture(Path(td)))
+    print("wrote", which)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,212 @@
+"""BASELINE.json configurations on the device, against the oracle or the
+committed fixtures of tests/golden/ (make_golden.py):
+
+- configs[2] at full depth: Qwen3-1.7B, 28 layers, Q4_K with Q6_K v / down /
+  output, greedy continuation of a 32-token prompt vs the oracle's;
+- configs[0] at full depth: Qwen3-0.6B random-init BF16 (tied), 128 greedy
+  tokens vs the oracle's;
+- configs[1] at its widths: Qwen3-0.6B all-Q8_0, tied (FP16 lm_head clone),
+  512-token prompt then single-token steps, vs the oracle;
+- configs[4] at its widths: Qwen3-8B shapes (H 4096, F 12288, 32/8 heads),
+  Q4_K with Q6_K output, 2048-token prefill then single-token steps, vs the
+  oracle's logits sampled at every 37th vocabulary id;
+- a llama.cpp Q4_K_M-style file (attn_v / ffn_down Q6_K on use_more_bits
+  layers only, Q4_K elsewhere) vs the oracle;
+- a KV cache longer than the fused step covers: single-token steps and
+  greedy decode fall back to the op path (the reference loops forward_last,
+  include/brolm/detail/generate.h:78-123).
+
+Greedy identity (tests/test_qwen_generate.cpp:282-323, "first 32 tokens
+identical"): free-running tokens equal the oracle's until the first step
+where they differ, and that step's oracle top-2 margin must be within twice
+the logit tolerance (a near tie FP16 compute may resolve either way);
+teacher-forced argmax equals the oracle token at every step whose margin
+exceeds twice the tolerance.  Logit tolerance: max-abs 2e-2."""
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SMALL, write_synth
+from golden.make_golden import FULL, W8B, W8B_PROMPT, W8B_STEPS, W8B_STRIDE
+
+pytestmark = pytest.mark.gpu
+LOGIT_TOL = 2e-2
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(scope="module")
+def ba():
+    import brolm_amd
+    brolm_amd.init()
+    return brolm_amd
+
+
+def _load(ba, path, cap):
+    m = ba.Qwen3Model(ba.Qwen3Config.from_gguf(str(path)))
+    m.load_weights(str(path))
+    m.allocate_cache(cap)
+    return m
+
+
+def _sha256(path: Path) -> str:
+    h = hashlib.sha256()
+    with open(path, "rb") as f:
+        for blk in iter(lambda: f.read(1 << 24), b""):
+            h.update(blk)
+    return h.hexdigest()
+
+
+def _tensor_type(path: Path, name: str) -> int:
+    from brolm_amd import _native
+    t, nd = C.c_int(), C.c_int()
+    dims = (C.c_int64 * 4)()
+    nb = C.c_int64()
+    rc = _native.lib().brolm_gguf_tensor_info(str(path).encode(), name.encode(), C.byref(t), dims, C.byref(nd),
+                                              C.byref(nb))
+    assert rc == 0, name
+    return t.value
+
+
+def _first_difference(got, want) -> int:
+    for i, (g, w) in enumerate(zip(got, want)):
+        if g != w:
+            return i
+    return min(len(got), len(want))
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["q4k", "bf16"])
+def test_full_depth_greedy_matches_oracle(ba, name, tmp_path_factory):
+    d = np.load(GOLD / "model_full.npz")
+    spec, n_prompt, n_new = FULL[name]
+    path = write_synth(tmp_path_factory.mktemp(f"full_{name}"), spec, f"full_{name}")
+    print(f"[configs] {name}: checkpoint written", flush=True)
+    assert _sha256(path) == d[f"{name}_sha256"].tobytes().hex(), "synthetic generator changed; rerun make_golden.py"
+    prompt = d[f"{name}_prompt"].tolist()
+    want = d[f"{name}_tokens"].tolist()
+    margins = d[f"{name}_margins"]
+    assert len(prompt) == n_prompt and len(want) == n_new
+    m = _load(ba, path, cap=n_prompt + n_new + 1)
+    assert m.decode_mode() == ("persistent" if name == "q4k" else "graph")
+    first = int(m.forward_last(prompt).argmax())
+    got = [first] + m.decode_greedy(first, n_new - 1)
+    k = _first_difference(got, want)
+    print(f"[configs] {name}: {k} of {n_new} greedy tokens identical; margins at the first 8 steps "
+          f"{np.round(margins[:8], 3).tolist()}", flush=True)
+    if k < n_new:
+        assert margins[k] <= 2 * LOGIT_TOL, f"step {k}: {got[k]} != {want[k]} with oracle margin {margins[k]:.4f}"
+    # teacher forced: one prefill over the oracle's sequence
+    m.reset_cache()
+    rows = m.forward(prompt + want[:-1])[n_prompt - 1:]
+    sure = margins > 2 * LOGIT_TOL
+    assert np.array_equal(rows.argmax(axis=1)[sure], np.asarray(want)[sure])
+    m.close()
+
+
+@pytest.mark.timeout(600)
+def test_q8_0_tied_0p6b_widths_prompt_512(ba, tmp_path_factory):
+    spec = dict(vocab=151936, hidden=1024, intermediate=3072, layers=2, n_q=16, n_kv=8, head_dim=128, tied=True,
+                embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0", up="Q8_0", down="Q8_0",
+                output="Q8_0", seed=9)
+    path = write_synth(tmp_path_factory.mktemp("w06"), spec, "w06")
+    m = _load(ba, path, cap=2048)
+    assert m.decode_mode() == "persistent"
+    om = oracle.Model(str(path))
+    om.allocate_cache(2048)
+    prompt = ba.prompt_ids(512, 151936, seed=42)
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    print(f"[configs] 0.6B Q8_0 prefill max diff {np.abs(a - b).max():.3e}", flush=True)
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    for _ in range(8):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
+    m.close()
+
+
+@pytest.mark.timeout(900)
+def test_q4k_8b_widths_prefill_2048(ba, tmp_path_factory):
+    d = np.load(GOLD / "model_8b_width.npz")
+    path = write_synth(tmp_path_factory.mktemp("w8b"), W8B, "w8b")
+    print("[configs] 8B-width checkpoint written", flush=True)
+    assert _sha256(path) == d["sha256"].tobytes().hex(), "synthetic generator changed; rerun make_golden.py"
+    m = _load(ba, path, cap=W8B_PROMPT + 256)
+    assert m.decode_mode() == "persistent"
+    lg = m.forward_last(ba.prompt_ids(W8B_PROMPT, W8B["vocab"], seed=42))
+    for step in range(W8B_STEPS + 1):
+        diff = np.abs(lg[::W8B_STRIDE] - d["logits"][step]).max()
+        print(f"[configs] 8B widths step {step}: sampled max diff {diff:.3e}", flush=True)
+        assert diff <= LOGIT_TOL
+        if d["margins"][step] > 2 * LOGIT_TOL:
+            assert int(lg.argmax()) == int(d["argmax"][step])
+        if step == W8B_STEPS:
+            break
+        lg = m.forward_last([int(d["tokens"][step])])
+    m.close()
+
+
+def test_q4k_m_layer_mix_vs_oracle(ba, tmp_path_factory):
+    """attn_v / ffn_down are Q6_K on llama.cpp's use_more_bits layers (0, 3,
+    6, 7 of 8) and Q4_K on the others; each layer's matrices dispatch on
+    their own type (compute.h:54-86)."""
+    spec = dict(SMALL, layers=8, v="Q4_K", down="Q4_K", more_bits="Q6_K", seed=13)
+    path = write_synth(tmp_path_factory.mktemp("q4km"), spec, "q4km")
+    q6 = [l for l in range(8) if _tensor_type(path, f"blk.{l}.attn_v.weight") == 14]
+    assert q6 == [0, 3, 6, 7]
+    assert [l for l in range(8) if _tensor_type(path, f"blk.{l}.ffn_down.weight") == 14] == q6
+    m = _load(ba, path, cap=128)
+    om = oracle.Model(str(path))
+    om.allocate_cache(128)
+    ids = [5, 17, 2, 31, 999, 0]
+    assert np.abs(m.forward(ids) - om.forward(ids)).max() <= LOGIT_TOL
+    assert m.decode_mode() in ("graph", "persistent")
+    tok = 7
+    for _ in range(6):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
+    want, margins = oracle.Model(str(path)).generate_greedy([3, 1, 4], 16)
+    m.reset_cache()
+    first = int(m.forward_last([3, 1, 4]).argmax())
+    got = [first] + m.decode_greedy(first, 15)
+    k = _first_difference(got, want)
+    if k < len(want):
+        assert margins[k] <= 2 * LOGIT_TOL
+    m.close()
+
+
+def test_cache_beyond_fused_step_uses_op_path(ba, small_gguf):
+    """The fused step's workspace covers caches up to 32768 positions; with a
+    longer cache forward_last(L = 1) and decode_greedy run the op path."""
+    m = _load(ba, small_gguf, cap=33000)
+    om = oracle.Model(str(small_gguf))
+    om.allocate_cache(64)
+    prompt = [3, 1, 4, 1, 5]
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    for _ in range(3):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
+    want, margins = oracle.Model(str(small_gguf)).generate_greedy(prompt, 8)
+    m.reset_cache()
+    first = int(m.forward_last(prompt).argmax())
+    got = [first] + m.decode_greedy(first, 7)
+    k = _first_difference(got, want)
+    if k < len(want):
+        assert margins[k] <= 2 * LOGIT_TOL
+    assert m.cache_len() == len(prompt) + 7
+    m.close()
