@@ -107,6 +107,7 @@ HIP_SYMBOLS = {
     "bx_persist_trace": (C.c_int, [vp, C.c_int]),
     "bx_argmax_workspace_bytes": (C.c_size_t, [i64]),
     "bx_argmax_f16": (C.c_int, [vp, i64, vp, vp, vp]),
+    "bx_argmax_f16_noalloc": (C.c_int, [vp, i64, vp, vp]),
 }
 
 # every symbol of include/brolm_c.h

@@ -1,8 +1,16 @@
 // Device greedy sampling: argmax over FP16 logits with the reference's tie
 // rule (strict '>' scan, so the lowest index wins; src/detail/generate.cpp:38-48).
 #include <cmath>
+#include <mutex>
 
 #include "common.h"
+
+// Partials of bx_argmax_f16_noalloc, the entry point that allocates nothing:
+// one float value and one int index per partial block.  Each GPU the library
+// runs on holds its own copy until the process ends.  Host code never uses
+// this name as an address: the per-device address comes from
+// hipGetSymbolAddress (scratch_device_ptr below).
+static __device__ __align__(256) unsigned char scratch[256 * (sizeof(float) + sizeof(int))];
 
 namespace bx {
 namespace {
@@ -67,6 +75,41 @@ __global__ __launch_bounds__(kArgThreads) void argmax_final(const float* __restr
     if (threadIdx.x == 0) *out = best.i < 0 ? 0 : best.i;
 }
 
+static_assert(sizeof(scratch) == (size_t)kArgBlocks * (sizeof(float) + sizeof(int)),
+              "scratch holds exactly one round of partials");
+
+// Launch the two argmax kernels with the partials at pv / pi.
+int argmax_launch(const uint16_t* logits, int64_t n, int32_t* out, float* pv, int* pi, hipStream_t st) {
+    int64_t nb = (n + kArgThreads - 1) / kArgThreads;
+    if (nb > kArgBlocks) nb = kArgBlocks;
+    argmax_partial<<<(unsigned)nb, kArgThreads, 0, st>>>(logits, n, pv, pi);
+    if (int rc = launch_check("argmax partial")) return rc;
+    argmax_final<<<1, kArgThreads, 0, st>>>(pv, pi, (int)nb, out);
+    return launch_check("argmax final");
+}
+
+// Device address of `scratch` on the current device: looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_device_ptr(void** out) {
+    int dev = 0;
+    if (int rc = hip_check(hipGetDevice(&dev), "argmax_noalloc: hipGetDevice")) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return fail(BX_EUNSUPPORTED, "argmax_noalloc: device index above 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "argmax_noalloc: hipGetSymbolAddress"))
+            return rc;
+        if (!p) return fail(BX_ELAUNCH, "argmax_noalloc: scratch has no device address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return BX_OK;
+}
+
 }  // namespace
 }  // namespace bx
 
@@ -83,13 +126,21 @@ int bx_argmax_f16(const uint16_t* logits, int64_t n, int32_t* out, void* workspa
     if (!logits || !out || !workspace || n <= 0 || n > 0x7fffffff) return fail(BX_EINVAL, "argmax: bad arguments");
     float* pv = static_cast<float*>(workspace);
     int* pi = reinterpret_cast<int*>(pv + kArgBlocks);
-    int64_t nb = (n + kArgThreads - 1) / kArgThreads;
-    if (nb > kArgBlocks) nb = kArgBlocks;
-    hipStream_t st = as_stream(stream);
-    argmax_partial<<<(unsigned)nb, kArgThreads, 0, st>>>(logits, n, pv, pi);
-    if (int rc = launch_check("argmax partial")) return rc;
-    argmax_final<<<1, kArgThreads, 0, st>>>(pv, pi, (int)nb, out);
-    return launch_check("argmax final");
+    return argmax_launch(logits, n, out, pv, pi, as_stream(stream));
+}
+
+int bx_argmax_f16_noalloc(const uint16_t* logits, int64_t n, int32_t* out, void* stream) {
+    if (!logits || !out || n <= 0) return fail(BX_EINVAL, "argmax_noalloc: bad arguments");
+    if (n > 0x7fffffff) return fail(BX_EUNSUPPORTED, "argmax_noalloc: n above 2^31 - 1 elements");
+    if (bx_argmax_workspace_bytes(n) > sizeof(scratch))
+        return fail(BX_EUNSUPPORTED, "argmax_noalloc: partials exceed the 2048-byte scratch");
+    void* p = nullptr;
+    if (int rc = scratch_device_ptr(&p)) return rc;
+    // every partial argmax_final reads is written by argmax_partial in the
+    // same call: nothing carries over from an earlier call
+    float* pv = static_cast<float*>(p);
+    int* pi = reinterpret_cast<int*>(pv + kArgBlocks);
+    return argmax_launch(logits, n, out, pv, pi, as_stream(stream));
 }
 
 }  // extern "C"

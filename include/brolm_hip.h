@@ -9,7 +9,8 @@
  *   - Pointers are device pointers (hipMalloc'd or torch-owned) unless stated.
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *   - Nothing here allocates device memory; scratch is passed in by the
- *     caller, sized by the matching *_workspace_bytes query.
+ *     caller, sized by the matching *_workspace_bytes query (except
+ *     bx_argmax_f16_noalloc, whose scratch is a fixed array of the library).
  *   - Return 0 on success or a negative BX_E* code; bx_last_error() gives a
  *     thread-local message.  Shapes are validated on the host before any
  *     launch, so an invalid shape is an error return, never a device fault.
@@ -243,6 +244,15 @@ int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg);
  * workspace: bx_argmax_workspace_bytes(n). */
 size_t bx_argmax_workspace_bytes(int64_t n);
 int bx_argmax_f16(const uint16_t* logits, int64_t n, int32_t* out, void* workspace, void* stream);
+/* bx_argmax_f16 without a workspace argument and without any allocation: the
+ * partials live in a fixed 2 KB device array of the library (one copy per
+ * GPU, held until the process ends).  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops with a fixed memory budget).  Same result and error
+ * behaviour as bx_argmax_f16; n up to 2^31 - 1.  Calls that overlap on one GPU
+ * (different streams, or different threads) share the array and race:
+ * serialize them. */
+int bx_argmax_f16_noalloc(const uint16_t* logits, int64_t n, int32_t* out, void* stream);
 
 #ifdef __cplusplus
 }
