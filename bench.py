@@ -309,9 +309,10 @@ def main() -> int:
         "ref_loop_tok_s": round(ref_tok_s, 2),
         "tokenizer": tokenizer,
     }
-    # device state goes before the process exit path (a profiler wrapping this
-    # run finalizes there)
+    # every device buffer and the op stream go before the process exit path (a
+    # profiler wrapping this run finalizes there)
     model.close()
+    ba.shutdown()
     if mistral and not args.no_cpu_baseline:
         log("cpu baseline skipped: the FP32 oracle of a 24B model needs ~96 GB of host memory")
     elif not args.no_cpu_baseline:

@@ -8,6 +8,7 @@ there is no Python or CPU fallback.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -22,12 +23,30 @@ GGML = {"F32": 0, "F16": 1, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "BF16": 30}
 __all__ = ["Qwen3Config", "Qwen3Model", "SamplingParams", "GenerateOptions", "generate", "sample_token",
            "qwen3_hf_to_ggml", "SynthSpec", "write_synth_qwen3", "init", "GGML", "Mistral3Config",
            "Mistral3TextConfig", "Mistral3TextModel", "mistral3_hf_to_ggml", "write_synth_mistral3",
-           "Llm2VecConfig", "Llm2VecEncoder"]
+           "Llm2VecConfig", "Llm2VecEncoder", "shutdown",
+           "PROFILE_STAGES", "profile_stages", "profile_reset", "profile_report"]
 
 
 def init() -> None:
-    """brotensor::init(): register the gfx950 device (raises without one)."""
+    """brotensor::init(): register the gfx950 device (raises without one).
+    The first call also registers shutdown() with atexit, so the runtime's
+    own device buffers and stream are released while the HIP runtime is
+    still whole, before the process's exit handlers run."""
+    global _atexit_registered
     check(_native.lib().brolm_init(), "init")
+    if not _atexit_registered:
+        atexit.register(shutdown)
+        _atexit_registered = True
+
+
+def shutdown() -> None:
+    """brotensor::shutdown(): wait for queued work, free the runtime's scratch,
+    sampler buffers and profiler events, destroy the op stream.  Open models
+    stay valid to close(); init() may be called again."""
+    check(_native.lib().brolm_shutdown(), "shutdown")
+
+
+_atexit_registered = False
 
 
 def _i32(a) -> "C.Array":
@@ -472,6 +491,32 @@ def sample_token(logits: np.ndarray, params: SamplingParams, seed: int) -> int:
     a = np.ascontiguousarray(logits, dtype=np.float32)
     return _native.lib().brolm_sample_token(a.ctypes.data_as(_native.P_f32), a.size, float(params.temperature),
                                             int(params.top_k), float(params.top_p), int(seed))
+
+
+PROFILE_STAGES = ("embed", "idx_upload", "rms_norm", "qkv_proj", "qk_norm", "rope", "kv_append", "attention",
+                  "o_proj", "mlp_proj", "swiglu", "residual_add", "final_norm", "lm_head", "logits_download",
+                  "sample", "other")
+
+
+def profile_stages() -> dict:
+    """BROLM_PROFILE totals: {stage: (device ns, calls)} for every stage with
+    calls (include/brolm/detail/profile.h:19-38 order)."""
+    out = {}
+    for i, name in enumerate(PROFILE_STAGES):
+        ns, calls = C.c_uint64(), C.c_uint64()
+        if _native.lib().brolm_profile_stage(i, C.byref(ns), C.byref(calls)) != 0:
+            raise RuntimeError(f"brolm_profile_stage({i}) failed")
+        if calls.value:
+            out[name] = (ns.value, calls.value)
+    return out
+
+
+def profile_reset() -> None:
+    _native.lib().brolm_profile_reset()
+
+
+def profile_report() -> None:
+    _native.lib().brolm_profile_report()
 
 
 def prompt_ids(n: int, vocab: int, seed: int = 42) -> list[int]:

@@ -114,6 +114,7 @@ HIP_SYMBOLS = {
 C_SYMBOLS = {
     "brolm_last_error": (cp, []),
     "brolm_init": (C.c_int, []),
+    "brolm_shutdown": (C.c_int, []),
     "brolm_synth_qwen3_write": (C.c_int, [C.POINTER(SynthSpecC), cp]),
     "brolm_synth_normal_bf16": (C.c_int, [u64, i64, f32, P_f32]),
     "brolm_synth_tensor_key": (u64, [u64, cp]),
@@ -164,6 +165,7 @@ C_SYMBOLS = {
     "brolm_profile_reset": (None, []),
     "brolm_profile_report": (None, []),
     "brolm_profile_enabled": (C.c_int, []),
+    "brolm_profile_stage": (C.c_int, [C.c_int, C.POINTER(u64), C.POINTER(u64)]),
 }
 
 

@@ -143,6 +143,10 @@ int brolm_init(void) {
     return guard([] { brotensor::init(); });
 }
 
+int brolm_shutdown(void) {
+    return guard([] { brotensor::shutdown(); });
+}
+
 namespace {
 
 int synth_write(const brolm_synth_qwen3_spec* s, const char* path, const char* arch) {
@@ -569,6 +573,13 @@ int brolm_sample_token(const float* logits, int vocab, float temperature, int to
 void brolm_profile_reset(void) { brolm::detail::profile::reset(); }
 void brolm_profile_report(void) { brolm::detail::profile::report(); }
 int brolm_profile_enabled(void) { return brolm::detail::profile::enabled() ? 1 : 0; }
+int brolm_profile_stage(int stage, uint64_t* ns, uint64_t* calls) {
+    namespace pr = brolm::detail::profile;
+    if (stage < 0 || stage >= static_cast<int>(pr::Stage::COUNT) || !ns || !calls) return -1;
+    *ns = pr::total_ns(static_cast<pr::Stage>(stage));
+    *calls = pr::calls(static_cast<pr::Stage>(stage));
+    return 0;
+}
 
 }  // extern "C"
 

@@ -75,7 +75,8 @@ struct DecodeGraphSession {
     uint32_t epoch = 0;
 
     ~DecodeGraphSession() {
-        (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
+        // after brotensor::shutdown() the op stream is gone and already drained
+        if (bt::initialized()) (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
         if (pws) (void)hipFree(pws);
         if (layers_dev) (void)hipFree(layers_dev);
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -89,17 +90,36 @@ struct DecodeGraphSession {
     }
 };
 
-// ─── ctor / dtor ─────────────────────────────────────────────────────────────
+// ─── construction ────────────────────────────────────────────────────────────
+//
+// The shape rules and their messages are the reference's
+// (src/detail/dense_decoder.cpp:97-112); they are checked in table order.
+
+namespace {
+
+struct ShapeRule {
+    bool (*bad)(const DenseDecoderConfig&);
+    const char* message;
+};
+constexpr ShapeRule kShapeRules[] = {
+    {[](const DenseDecoderConfig& c) {
+         return c.hidden_size <= 0 || c.intermediate_size <= 0 || c.num_hidden_layers <= 0 || c.vocab_size <= 0 ||
+                c.head_dim <= 0;
+     },
+     "config has non-positive dimension"},
+    {[](const DenseDecoderConfig& c) { return c.num_attention_heads <= 0 || c.num_key_value_heads <= 0; },
+     "num_attention_heads / num_key_value_heads must be positive"},
+    {[](const DenseDecoderConfig& c) { return c.num_attention_heads % c.num_key_value_heads != 0; },
+     "num_attention_heads must be a multiple of num_key_value_heads"},
+    {[](const DenseDecoderConfig& c) { return c.head_dim % 2 != 0; },
+     "head_dim must be even (RoPE rotates dimension pairs)"},
+};
+
+}  // namespace
 
 DenseDecoder::DenseDecoder(const DenseDecoderConfig& cfg) : cfg_(cfg) {
-    if (cfg_.hidden_size <= 0 || cfg_.intermediate_size <= 0 || cfg_.num_hidden_layers <= 0 ||
-        cfg_.vocab_size <= 0 || cfg_.head_dim <= 0)
-        fail("config has non-positive dimension");
-    if (cfg_.num_attention_heads <= 0 || cfg_.num_key_value_heads <= 0)
-        fail("num_attention_heads / num_key_value_heads must be positive");
-    if (cfg_.num_attention_heads % cfg_.num_key_value_heads != 0)
-        fail("num_attention_heads must be a multiple of num_key_value_heads");
-    if (cfg_.head_dim % 2 != 0) fail("head_dim must be even (RoPE rotates dimension pairs)");
+    for (const ShapeRule& r : kShapeRules)
+        if (r.bad(cfg_)) fail(r.message);
     layers_.resize(static_cast<std::size_t>(cfg_.num_hidden_layers));
 }
 
@@ -107,52 +127,136 @@ DenseDecoder::~DenseDecoder() = default;
 DenseDecoder::DenseDecoder(DenseDecoder&&) noexcept = default;
 DenseDecoder& DenseDecoder::operator=(DenseDecoder&&) noexcept = default;
 
-// ─── load_weights (dense_decoder.cpp:121-192) ───────────────────────────────
+// ─── weights ─────────────────────────────────────────────────────────────────
+//
+// What a checkpoint must hold is one table: the HF tensor name (the Source
+// maps it to the file's own naming), its (rows, cols) in model dimensions,
+// how it is uploaded, and the Layer member it lands in.  The names, shapes,
+// upload kinds and the lm_head tie rule are the reference's contract
+// (src/detail/dense_decoder.cpp:121-192); the table order is the order a
+// missing tensor is reported in.
+//   carrier  quantized matrices keep their GGUF blocks on the device;
+//   dense    norm gammas (and the embedding) are dequantized to FP16;
+//   rope     q / k rows (and the QK-norm gammas, as one head over head_dim)
+//            are permuted within each head from interleaved to half-split
+//            pairs, so RoPE rotates contiguous halves.
+
+namespace {
+
+enum class Dim : std::uint8_t { One, Hidden, Ffn, QWidth, KvWidth, HeadDim, Vocab };
+enum class Upload : std::uint8_t { Carrier, Dense, Rope };
+
+struct ModelDims {
+    int v, h, f, hd, n_q, n_kv;
+    int of(Dim d) const {
+        switch (d) {
+            case Dim::One: return 1;
+            case Dim::Hidden: return h;
+            case Dim::Ffn: return f;
+            case Dim::QWidth: return n_q * hd;
+            case Dim::KvWidth: return n_kv * hd;
+            case Dim::HeadDim: return hd;
+            case Dim::Vocab: return v;
+        }
+        return 0;
+    }
+    // heads a rope-permuted tensor's rows split into
+    int heads_of(Dim rows) const { return rows == Dim::QWidth ? n_q : rows == Dim::KvWidth ? n_kv : 1; }
+};
+
+struct TensorSpec {
+    const char* hf;      // name after "model.layers.<i>." (per layer) or the full name
+    const char* label;   // the short name the Source's errors use
+    Dim rows, cols;
+    Upload how;
+};
+
+void upload(const weights::Source& src, const std::string& name, const TensorSpec& t, const ModelDims& d,
+            bt::Tensor& dst) {
+    const int rows = d.of(t.rows), cols = d.of(t.cols);
+    switch (t.how) {
+        case Upload::Carrier: src.upload_compute_checked(name, rows, cols, dst, t.label); break;
+        case Upload::Dense: src.upload_compute_dequant(name, rows, cols, dst, t.label); break;
+        case Upload::Rope:
+            src.upload_compute_rope_permuted(name, rows, cols, d.heads_of(t.rows), d.hd, dst, t.label);
+            break;
+    }
+}
+
+}  // namespace
 
 void DenseDecoder::load_weights(const weights::Source& src) {
-    invalidate_graph_();
-    const int V = cfg_.vocab_size, H = cfg_.hidden_size, F = cfg_.intermediate_size, HD = cfg_.head_dim;
-    const int n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
-    const int q_dim = n_q * HD, kv_dim = n_kv * HD;
-
-    src.upload_compute_dequant("model.embed_tokens.weight", V, H, embed_tokens_, "embed_tokens.weight");
-    for (int i = 0; i < cfg_.num_hidden_layers; ++i) {
-        const std::string p = "model.layers." + std::to_string(i) + ".";
-        Layer& L = layers_[static_cast<std::size_t>(i)];
-        src.upload_compute_dequant(p + "input_layernorm.weight", H, 1, L.input_ln, "input_layernorm.weight");
-        src.upload_compute_rope_permuted(p + "self_attn.q_proj.weight", q_dim, H, n_q, HD, L.Wq, "q_proj.weight");
-        src.upload_compute_rope_permuted(p + "self_attn.k_proj.weight", kv_dim, H, n_kv, HD, L.Wk, "k_proj.weight");
-        src.upload_compute_checked(p + "self_attn.v_proj.weight", kv_dim, H, L.Wv, "v_proj.weight");
-        src.upload_compute_checked(p + "self_attn.o_proj.weight", H, q_dim, L.Wo, "o_proj.weight");
-        if (cfg_.use_qk_norm) {
-            src.upload_compute_rope_permuted(p + "self_attn.q_norm.weight", HD, 1, 1, HD, L.q_norm, "q_norm.weight");
-            src.upload_compute_rope_permuted(p + "self_attn.k_norm.weight", HD, 1, 1, HD, L.k_norm, "k_norm.weight");
-        }
-        src.upload_compute_dequant(p + "post_attention_layernorm.weight", H, 1, L.post_attn_ln,
-                                   "post_attention_layernorm.weight");
-        src.upload_compute_checked(p + "mlp.gate_proj.weight", F, H, L.gate_W, "gate_proj.weight");
-        src.upload_compute_checked(p + "mlp.up_proj.weight", F, H, L.up_W, "up_proj.weight");
-        src.upload_compute_checked(p + "mlp.down_proj.weight", H, F, L.down_W, "down_proj.weight");
+    struct LayerSlot {
+        TensorSpec spec;
+        bt::Tensor Layer::* member;
+        bool qk_norm_only;
+    };
+    static const LayerSlot kLayerSlots[] = {
+        {{"input_layernorm.weight", "input_layernorm.weight", Dim::Hidden, Dim::One, Upload::Dense},
+         &Layer::input_ln, false},
+        {{"self_attn.q_proj.weight", "q_proj.weight", Dim::QWidth, Dim::Hidden, Upload::Rope}, &Layer::Wq, false},
+        {{"self_attn.k_proj.weight", "k_proj.weight", Dim::KvWidth, Dim::Hidden, Upload::Rope}, &Layer::Wk, false},
+        {{"self_attn.v_proj.weight", "v_proj.weight", Dim::KvWidth, Dim::Hidden, Upload::Carrier}, &Layer::Wv, false},
+        {{"self_attn.o_proj.weight", "o_proj.weight", Dim::Hidden, Dim::QWidth, Upload::Carrier}, &Layer::Wo, false},
+        {{"self_attn.q_norm.weight", "q_norm.weight", Dim::HeadDim, Dim::One, Upload::Rope}, &Layer::q_norm, true},
+        {{"self_attn.k_norm.weight", "k_norm.weight", Dim::HeadDim, Dim::One, Upload::Rope}, &Layer::k_norm, true},
+        {{"post_attention_layernorm.weight", "post_attention_layernorm.weight", Dim::Hidden, Dim::One,
+          Upload::Dense},
+         &Layer::post_attn_ln, false},
+        {{"mlp.gate_proj.weight", "gate_proj.weight", Dim::Ffn, Dim::Hidden, Upload::Carrier}, &Layer::gate_W, false},
+        {{"mlp.up_proj.weight", "up_proj.weight", Dim::Ffn, Dim::Hidden, Upload::Carrier}, &Layer::up_W, false},
+        {{"mlp.down_proj.weight", "down_proj.weight", Dim::Hidden, Dim::Ffn, Upload::Carrier}, &Layer::down_W,
+         false},
+    };
+    invalidate_graph_();   // a captured step holds the old weight pointers
+    const ModelDims d{cfg_.vocab_size, cfg_.hidden_size, cfg_.intermediate_size, cfg_.head_dim,
+                      cfg_.num_attention_heads, cfg_.num_key_value_heads};
+    upload(src, "model.embed_tokens.weight", {"", "embed_tokens.weight", Dim::Vocab, Dim::Hidden, Upload::Dense}, d,
+           embed_tokens_);
+    for (std::size_t i = 0; i < layers_.size(); ++i) {
+        const std::string prefix = "model.layers." + std::to_string(i) + ".";
+        for (const LayerSlot& s : kLayerSlots)
+            if (!s.qk_norm_only || cfg_.use_qk_norm) upload(src, prefix + s.spec.hf, s.spec, d, layers_[i].*s.member);
     }
-    src.upload_compute_dequant("model.norm.weight", H, 1, final_norm_, "model.norm.weight");
+    upload(src, "model.norm.weight", {"", "model.norm.weight", Dim::Hidden, Dim::One, Upload::Dense}, d, final_norm_);
     if (src.has("lm_head.weight")) {
-        src.upload_compute_checked("lm_head.weight", V, H, lm_head_, "lm_head.weight");
-    } else {
-        if (!cfg_.tie_word_embeddings) fail("load_weights: lm_head.weight missing and tie_word_embeddings is false");
+        upload(src, "lm_head.weight", {"", "lm_head.weight", Dim::Vocab, Dim::Hidden, Upload::Carrier}, d, lm_head_);
+    } else if (cfg_.tie_word_embeddings) {
+        // tied: the head reads its own copy of the FP16 embedding rows
         lm_head_ = embed_tokens_.clone();
+    } else {
+        fail("load_weights: lm_head.weight missing and tie_word_embeddings is false");
     }
     bt::sync_all();
 }
 
-// ─── cache management (dense_decoder.cpp:196-227) ───────────────────────────
+// ─── KV cache ────────────────────────────────────────────────────────────────
+//
+// One HBM arena holds every layer's cache: layer l's K rows, then its V rows,
+// each (capacity, n_kv * head_dim) FP16, so the whole cache is one allocation
+// and each layer's K and V are contiguous views the kernels read by row.  A
+// call with the current capacity keeps the arena (the captured step bakes its
+// pointers in); any other capacity reallocates and drops the step session.
+// reset / truncate only move cache_len: rows past it are dead until the next
+// forward overwrites them, and RoPE positions restart from cache_len.
 
 void DenseDecoder::allocate_cache(int max_seq_len) {
     if (max_seq_len <= 0) fail("allocate_cache: max_seq_len must be positive");
-    if (max_seq_len != max_seq_len_) invalidate_graph_();
-    const int cols = cfg_.num_key_value_heads * cfg_.head_dim;
-    for (Layer& L : layers_) {
-        resize_like(L.K_cache, max_seq_len, cols, bt::Dtype::FP16, bt::Device::ROCm);
-        resize_like(L.V_cache, max_seq_len, cols, bt::Dtype::FP16, bt::Device::ROCm);
+    const int width = cfg_.num_key_value_heads * cfg_.head_dim;
+    if (max_seq_len != max_seq_len_ || kv_arena_.data == nullptr) {
+        invalidate_graph_();
+        const std::int64_t rows = 2LL * static_cast<std::int64_t>(layers_.size()) * max_seq_len;
+        if (rows > INT32_MAX) fail("allocate_cache: KV arena rows exceed the tensor row limit");
+        kv_arena_ = bt::Tensor();   // free the old arena before taking the new one
+        kv_arena_ = bt::Tensor::empty_on(bt::Device::ROCm, static_cast<int>(rows), width, bt::Dtype::FP16);
+        const std::size_t plane = static_cast<std::size_t>(max_seq_len) * width;   // FP16 elements
+        auto* base = static_cast<std::uint16_t*>(kv_arena_.data);
+        for (std::size_t l = 0; l < layers_.size(); ++l) {
+            layers_[l].K_cache = bt::Tensor::view(bt::Device::ROCm, base + (2 * l) * plane, max_seq_len, width,
+                                                  bt::Dtype::FP16);
+            layers_[l].V_cache = bt::Tensor::view(bt::Device::ROCm, base + (2 * l + 1) * plane, max_seq_len, width,
+                                                  bt::Dtype::FP16);
+        }
     }
     max_seq_len_ = max_seq_len;
     cache_len_ = 0;

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <numeric>
 
 #include "brolm/detail/profile.h"
@@ -31,6 +32,31 @@ int argmax(const float* logits, int vocab) {
     return best;
 }
 
+// The device sampler's workspace and result slot, shared by every call and
+// released by brotensor::shutdown().
+struct SamplerBuffers {
+    std::mutex mu;
+    brotensor::Tensor ws, tok;
+    void reserve(std::size_t ws_bytes) {
+        if (static_cast<std::size_t>(ws.rows) * 4 < ws_bytes)
+            ws = brotensor::Tensor::empty_on(brotensor::Device::ROCm, static_cast<int>((ws_bytes + 3) / 4), 1,
+                                             brotensor::Dtype::FP32);
+        if (tok.rows == 0) tok = brotensor::Tensor::empty_on(brotensor::Device::ROCm, 1, 1, brotensor::Dtype::FP32);
+        brotensor::on_shutdown(release);
+    }
+    static void release();
+};
+SamplerBuffers& sampler_buffers() {
+    static SamplerBuffers* b = new SamplerBuffers();   // outlives every caller, freed by release()
+    return *b;
+}
+void SamplerBuffers::release() {
+    SamplerBuffers& b = sampler_buffers();
+    std::lock_guard<std::mutex> lk(b.mu);
+    b.ws = brotensor::Tensor();
+    b.tok = brotensor::Tensor();
+}
+
 }  // namespace
 
 std::vector<float> last_row_fp32(const brotensor::Tensor& logits) {
@@ -56,16 +82,14 @@ int sample_token_device(const brotensor::Tensor& logits, const SamplingParams& p
     const double u = dist(rng);
     const int V = logits.cols;
     const auto* row = static_cast<const uint16_t*>(logits.data) + static_cast<std::size_t>(logits.rows - 1) * V;
-    static thread_local brotensor::Tensor ws, tok;
-    const std::size_t wsb = bx_sample_workspace_bytes(V);
-    if (static_cast<std::size_t>(ws.rows) * 4 < wsb) ws = brotensor::Tensor::empty_on(
-        brotensor::Device::ROCm, static_cast<int>((wsb + 3) / 4), 1, brotensor::Dtype::FP32);
-    if (tok.rows == 0) tok = brotensor::Tensor::empty_on(brotensor::Device::ROCm, 1, 1, brotensor::Dtype::FP32);
-    hipx::bx(bx_sample_f16(row, V, p.temperature, p.top_k, p.top_p, u, static_cast<int32_t*>(tok.data), ws.data,
+    SamplerBuffers& b = sampler_buffers();
+    std::lock_guard<std::mutex> lk(b.mu);
+    b.reserve(bx_sample_workspace_bytes(V));
+    hipx::bx(bx_sample_f16(row, V, p.temperature, p.top_k, p.top_p, u, static_cast<int32_t*>(b.tok.data), b.ws.data,
                            hipx::stream()),
              "sample_token_device");
     int32_t out = 0;
-    hipx::d2h(&out, tok.data, sizeof(out));
+    hipx::d2h(&out, b.tok.data, sizeof(out));
     return out;
 }
 

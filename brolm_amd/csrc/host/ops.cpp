@@ -37,8 +37,9 @@ void size_out(Tensor& t, int r, int c, Dtype dt) {
     t.resize(r, c, dt);
 }
 
-// Process-lifetime scratch (never freed: avoids teardown-order issues with the
-// HIP runtime at exit).
+// Scratch shared by every op call (attention split-K partials, argmax
+// partials, the RoPE tables), grown on demand and released by
+// brotensor::shutdown(), so none of it is left for exit handlers to free.
 struct Scratch {
     std::mutex mu;
     void* attn_ws = nullptr;
@@ -56,6 +57,17 @@ Scratch& scratch() {
     return *s;
 }
 
+void release_scratch() {
+    Scratch& S = scratch();
+    std::lock_guard<std::mutex> lk(S.mu);
+    for (void* p : {S.attn_ws, S.argmax_ws, static_cast<void*>(S.cos_t), static_cast<void*>(S.sin_t)})
+        if (p) (void)hipFree(p);
+    S.attn_ws = S.argmax_ws = nullptr;
+    S.cos_t = S.sin_t = nullptr;
+    S.attn_bytes = S.argmax_bytes = 0;
+    S.rows = S.hd = 0;
+}
+
 void* grow(void*& p, std::size_t& have, std::size_t need) {
     if (need <= have && p) return p;
     if (p) {
@@ -64,6 +76,7 @@ void* grow(void*& p, std::size_t& have, std::size_t need) {
         p = nullptr;
     }
     std::size_t n = need < 4096 ? 4096 : need;
+    on_shutdown(release_scratch);
     hipx::check(hipMalloc(&p, n), "hipMalloc scratch");
     have = n;
     return p;
@@ -81,6 +94,7 @@ void rope_table(float theta, int hd, int rows, const float** c, const float** s,
         hipx::sync();
         if (S.cos_t) (void)hipFree(S.cos_t);
         if (S.sin_t) (void)hipFree(S.sin_t);
+        on_shutdown(release_scratch);
         hipx::check(hipMalloc(reinterpret_cast<void**>(&S.cos_t), hc.size() * 4), "hipMalloc rope");
         hipx::check(hipMalloc(reinterpret_cast<void**>(&S.sin_t), hs.size() * 4), "hipMalloc rope");
         hipx::h2d(S.cos_t, hc.data(), hc.size() * 4);

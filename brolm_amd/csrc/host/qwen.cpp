@@ -1,7 +1,15 @@
-// Qwen3 facade (reference src/qwen.cpp): config from GGUF metadata, the
-// HF -> ggml tensor-name map, and the GGUF load overloads.
+// Qwen3 facade: config from GGUF metadata, the HF -> ggml tensor-name map and
+// the GGUF load overloads (reference include/brolm/qwen.h:35-157).
+//
+// The metadata keys, the ggml tensor names and the error texts are the
+// reference's contract (src/qwen.cpp:88-149, :173-208); the reading is table
+// driven: every config field is one row naming its key, whether it is
+// required, and how a missing key is filled.
 #include "brolm/qwen.h"
 
+#include <array>
+#include <charconv>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <string_view>
@@ -16,9 +24,136 @@ namespace gg = ::brotensor::gguf;
 
 namespace {
 
-[[noreturn]] void fail(const std::string& msg) { throw std::runtime_error("qwen::Qwen3Model: " + msg); }
+constexpr const char* kWho = "qwen::Qwen3Config::from_gguf: ";
 
-brolm::detail::DenseDecoderConfig to_core_config(const Qwen3Config& c) {
+// A GGUF scalar as a double (every integer width and both float widths);
+// nullopt for strings, arrays and booleans.
+std::optional<double> scalar_value(const gg::Value& v) {
+    using T = gg::ValueType;
+    switch (v.type) {
+        case T::U8: return v.scalar.u8;
+        case T::I8: return v.scalar.i8;
+        case T::U16: return v.scalar.u16;
+        case T::I16: return v.scalar.i16;
+        case T::U32: return v.scalar.u32;
+        case T::I32: return v.scalar.i32;
+        case T::U64: return static_cast<double>(v.scalar.u64);
+        case T::I64: return static_cast<double>(v.scalar.i64);
+        case T::F32: return v.scalar.f32;
+        case T::F64: return v.scalar.f64;
+        default: return std::nullopt;
+    }
+}
+bool is_integer_type(gg::ValueType t) {
+    using T = gg::ValueType;
+    return t == T::U8 || t == T::I8 || t == T::U16 || t == T::I16 || t == T::U32 || t == T::I32 || t == T::U64 ||
+           t == T::I64;
+}
+
+// Typed access to a file's metadata with the reference's error texts.
+class Meta {
+public:
+    explicit Meta(const gg::File& f) : f_(f) {}
+
+    std::optional<int> integer(const char* key) const {
+        const gg::Value* v = f_.find_meta(key);
+        if (!v) return std::nullopt;
+        if (!is_integer_type(v->type))
+            throw std::runtime_error(std::string(kWho) + "metadata '" + key + "' is not an integer scalar");
+        return static_cast<int>(static_cast<long long>(*scalar_value(*v)));
+    }
+    std::optional<float> real(const char* key) const {
+        const gg::Value* v = f_.find_meta(key);
+        if (!v) return std::nullopt;
+        if (v->type != gg::ValueType::F32 && v->type != gg::ValueType::F64)
+            throw std::runtime_error(std::string(kWho) + "metadata '" + key + "' is not a float scalar");
+        return static_cast<float>(*scalar_value(*v));
+    }
+    int required(const char* key) const {
+        const std::optional<int> v = integer(key);
+        if (!v) throw std::runtime_error(std::string(kWho) + "missing metadata '" + key + "'");
+        return *v;
+    }
+    const gg::Value* raw(const char* key) const { return f_.find_meta(key); }
+    const gg::File& file() const { return f_; }
+
+private:
+    const gg::File& f_;
+};
+
+// Integer fields: key, required, and (when optional) the fallback computed
+// from the fields read before it.
+struct IntField {
+    const char* key;
+    int Qwen3Config::* field;
+    bool required;
+    int (*fallback)(const Qwen3Config&);
+};
+const std::array<IntField, 7> kIntFields = {{
+    {"qwen3.embedding_length", &Qwen3Config::hidden_size, true, nullptr},
+    {"qwen3.feed_forward_length", &Qwen3Config::intermediate_size, true, nullptr},
+    {"qwen3.block_count", &Qwen3Config::num_hidden_layers, true, nullptr},
+    {"qwen3.attention.head_count", &Qwen3Config::num_attention_heads, true, nullptr},
+    // GQA defaults to one KV head per query head, head_dim to hidden / heads
+    {"qwen3.attention.head_count_kv", &Qwen3Config::num_key_value_heads, false,
+     [](const Qwen3Config& c) { return c.num_attention_heads; }},
+    {"qwen3.attention.key_length", &Qwen3Config::head_dim, false,
+     [](const Qwen3Config& c) { return c.hidden_size / c.num_attention_heads; }},
+    {"qwen3.context_length", &Qwen3Config::max_position_embeddings, false,
+     [](const Qwen3Config& c) { return c.max_position_embeddings; }},
+}};
+struct RealField {
+    const char* key;
+    float Qwen3Config::* field;
+};
+const std::array<RealField, 2> kRealFields = {{
+    {"qwen3.attention.layer_norm_rms_epsilon", &Qwen3Config::rms_norm_eps},
+    {"qwen3.rope.freq_base", &Qwen3Config::rope_theta},
+}};
+
+// vocab: the tokenizer's token list when present, else qwen3.vocab_size.
+void read_vocab(const Meta& m, Qwen3Config& c) {
+    const gg::Value* toks = m.raw("tokenizer.ggml.tokens");
+    if (toks && toks->type == gg::ValueType::Array) {
+        c.vocab_size = static_cast<int>(toks->array.size());
+        return;
+    }
+    if (const std::optional<int> v = m.integer("qwen3.vocab_size")) c.vocab_size = *v;
+}
+// Tied embeddings: the boolean key when present, else "no output.weight".
+void read_tie(const Meta& m, Qwen3Config& c) {
+    const gg::Value* v = m.raw("qwen3.tie_word_embeddings");
+    c.tie_word_embeddings = (v && v->type == gg::ValueType::Bool) ? v->scalar.b
+                                                                   : m.file().find_tensor("output.weight") == nullptr;
+}
+
+// ---- HF -> ggml names -----------------------------------------------------
+
+struct NamePair {
+    std::string_view hf, ggml;
+};
+// Whole-model tensors.
+constexpr std::array<NamePair, 3> kGlobalNames = {{
+    {"model.embed_tokens.weight", "token_embd.weight"},
+    {"model.norm.weight", "output_norm.weight"},
+    {"lm_head.weight", "output.weight"},
+}};
+// Per-layer tensors: the suffix after "model.layers.<i>." and after "blk.<i>.".
+constexpr std::array<NamePair, 11> kLayerNames = {{
+    {"self_attn.q_proj.weight", "attn_q.weight"},
+    {"self_attn.k_proj.weight", "attn_k.weight"},
+    {"self_attn.v_proj.weight", "attn_v.weight"},
+    {"self_attn.o_proj.weight", "attn_output.weight"},
+    {"self_attn.q_norm.weight", "attn_q_norm.weight"},
+    {"self_attn.k_norm.weight", "attn_k_norm.weight"},
+    {"input_layernorm.weight", "attn_norm.weight"},
+    {"post_attention_layernorm.weight", "ffn_norm.weight"},
+    {"mlp.gate_proj.weight", "ffn_gate.weight"},
+    {"mlp.up_proj.weight", "ffn_up.weight"},
+    {"mlp.down_proj.weight", "ffn_down.weight"},
+}};
+
+brolm::detail::DenseDecoderConfig core_config_of(const Qwen3Config& c) {
     brolm::detail::DenseDecoderConfig d;
     d.vocab_size = c.vocab_size;
     d.hidden_size = c.hidden_size;
@@ -29,123 +164,59 @@ brolm::detail::DenseDecoderConfig to_core_config(const Qwen3Config& c) {
     d.head_dim = c.head_dim;
     d.rms_norm_eps = c.rms_norm_eps;
     d.rope_theta = c.rope_theta;
-    d.use_qk_norm = true;
     d.tie_word_embeddings = c.tie_word_embeddings;
+    d.use_qk_norm = true;   // the one architectural switch that makes the dense decoder Qwen3
     return d;
 }
-
-const gg::Value& need_meta(const gg::File& f, const char* key) {
-    const gg::Value* v = f.find_meta(key);
-    if (!v) throw std::runtime_error(std::string("qwen::Qwen3Config::from_gguf: missing metadata '") + key + "'");
-    return *v;
-}
-
-int meta_as_int(const gg::Value& v, const char* key) {
-    switch (v.type) {
-        case gg::ValueType::U8: return static_cast<int>(v.scalar.u8);
-        case gg::ValueType::I8: return static_cast<int>(v.scalar.i8);
-        case gg::ValueType::U16: return static_cast<int>(v.scalar.u16);
-        case gg::ValueType::I16: return static_cast<int>(v.scalar.i16);
-        case gg::ValueType::U32: return static_cast<int>(v.scalar.u32);
-        case gg::ValueType::I32: return static_cast<int>(v.scalar.i32);
-        case gg::ValueType::U64: return static_cast<int>(v.scalar.u64);
-        case gg::ValueType::I64: return static_cast<int>(v.scalar.i64);
-        default:
-            throw std::runtime_error(std::string("qwen::Qwen3Config::from_gguf: metadata '") + key +
-                                     "' is not an integer scalar");
-    }
-}
-
-float meta_as_f32(const gg::Value& v, const char* key) {
-    if (v.type == gg::ValueType::F32) return v.scalar.f32;
-    if (v.type == gg::ValueType::F64) return static_cast<float>(v.scalar.f64);
-    throw std::runtime_error(std::string("qwen::Qwen3Config::from_gguf: metadata '") + key + "' is not a float scalar");
-}
-
-bool starts_with(std::string_view s, std::string_view p) { return s.size() >= p.size() && s.compare(0, p.size(), p) == 0; }
 
 }  // namespace
 
 Qwen3Config Qwen3Config::from_gguf(const gg::File& f) {
-    if (const auto* arch = f.find_meta("general.architecture")) {
-        if (arch->type == gg::ValueType::String && arch->str != "qwen3")
-            throw std::runtime_error("qwen::Qwen3Config::from_gguf: general.architecture is '" + arch->str +
-                                     "', expected 'qwen3'");
+    const Meta m(f);
+    if (const gg::Value* arch = m.raw("general.architecture");
+        arch && arch->type == gg::ValueType::String && arch->str != "qwen3")
+        throw std::runtime_error(std::string(kWho) + "general.architecture is '" + arch->str + "', expected 'qwen3'");
+    Qwen3Config c;
+    for (const IntField& fld : kIntFields) {
+        if (fld.required) {
+            c.*fld.field = m.required(fld.key);
+        } else {
+            const std::optional<int> v = m.integer(fld.key);
+            c.*fld.field = v ? *v : fld.fallback(c);
+        }
     }
-    Qwen3Config cfg;
-    cfg.hidden_size = meta_as_int(need_meta(f, "qwen3.embedding_length"), "qwen3.embedding_length");
-    cfg.intermediate_size = meta_as_int(need_meta(f, "qwen3.feed_forward_length"), "qwen3.feed_forward_length");
-    cfg.num_hidden_layers = meta_as_int(need_meta(f, "qwen3.block_count"), "qwen3.block_count");
-    cfg.num_attention_heads = meta_as_int(need_meta(f, "qwen3.attention.head_count"), "qwen3.attention.head_count");
-    if (const auto* v = f.find_meta("qwen3.attention.head_count_kv"))
-        cfg.num_key_value_heads = meta_as_int(*v, "qwen3.attention.head_count_kv");
-    else
-        cfg.num_key_value_heads = cfg.num_attention_heads;
-    if (const auto* v = f.find_meta("qwen3.attention.key_length"))
-        cfg.head_dim = meta_as_int(*v, "qwen3.attention.key_length");
-    else
-        cfg.head_dim = cfg.hidden_size / cfg.num_attention_heads;
-    if (const auto* v = f.find_meta("qwen3.attention.layer_norm_rms_epsilon"))
-        cfg.rms_norm_eps = meta_as_f32(*v, "qwen3.attention.layer_norm_rms_epsilon");
-    if (const auto* v = f.find_meta("qwen3.rope.freq_base")) cfg.rope_theta = meta_as_f32(*v, "qwen3.rope.freq_base");
-    if (const auto* v = f.find_meta("qwen3.context_length"))
-        cfg.max_position_embeddings = meta_as_int(*v, "qwen3.context_length");
-    if (const auto* toks = f.find_meta("tokenizer.ggml.tokens"); toks && toks->type == gg::ValueType::Array)
-        cfg.vocab_size = static_cast<int>(toks->array.size());
-    else if (const auto* vs = f.find_meta("qwen3.vocab_size"))
-        cfg.vocab_size = meta_as_int(*vs, "qwen3.vocab_size");
-    if (const auto* v = f.find_meta("qwen3.tie_word_embeddings"); v && v->type == gg::ValueType::Bool)
-        cfg.tie_word_embeddings = v->scalar.b;
-    else
-        cfg.tie_word_embeddings = f.find_tensor("output.weight") == nullptr;
-    return cfg;
+    for (const RealField& fld : kRealFields)
+        if (const std::optional<float> v = m.real(fld.key)) c.*fld.field = *v;
+    read_vocab(m, c);
+    read_tie(m, c);
+    return c;
 }
 
-std::string qwen3_hf_to_ggml(std::string_view hf_name) {
-    if (hf_name == "model.embed_tokens.weight") return "token_embd.weight";
-    if (hf_name == "model.norm.weight") return "output_norm.weight";
-    if (hf_name == "lm_head.weight") return "output.weight";
-    constexpr std::string_view kLayers = "model.layers.";
-    if (!starts_with(hf_name, kLayers)) return {};
-    const auto dot = hf_name.find('.', kLayers.size());
-    if (dot == std::string_view::npos) return {};
-    const std::string_view idx = hf_name.substr(kLayers.size(), dot - kLayers.size());
-    if (idx.empty()) return {};
-    for (char ch : idx)
-        if (ch < '0' || ch > '9') return {};
-    const std::string_view tail = hf_name.substr(dot + 1);
-    auto blk = [&](std::string_view suffix) {
-        std::string out = "blk.";
-        out.append(idx);
-        out.push_back('.');
-        out.append(suffix);
-        return out;
-    };
-    if (tail == "self_attn.q_proj.weight") return blk("attn_q.weight");
-    if (tail == "self_attn.k_proj.weight") return blk("attn_k.weight");
-    if (tail == "self_attn.v_proj.weight") return blk("attn_v.weight");
-    if (tail == "self_attn.o_proj.weight") return blk("attn_output.weight");
-    if (tail == "self_attn.q_norm.weight") return blk("attn_q_norm.weight");
-    if (tail == "self_attn.k_norm.weight") return blk("attn_k_norm.weight");
-    if (tail == "input_layernorm.weight") return blk("attn_norm.weight");
-    if (tail == "post_attention_layernorm.weight") return blk("ffn_norm.weight");
-    if (tail == "mlp.gate_proj.weight") return blk("ffn_gate.weight");
-    if (tail == "mlp.up_proj.weight") return blk("ffn_up.weight");
-    if (tail == "mlp.down_proj.weight") return blk("ffn_down.weight");
+std::string qwen3_hf_to_ggml(std::string_view hf) {
+    for (const NamePair& p : kGlobalNames)
+        if (hf == p.hf) return std::string(p.ggml);
+    constexpr std::string_view kPrefix = "model.layers.";
+    if (hf.substr(0, kPrefix.size()) != kPrefix) return {};
+    const std::string_view rest = hf.substr(kPrefix.size());
+    // the layer index: decimal digits up to the next '.'
+    unsigned layer = 0;
+    const auto [end, ec] = std::from_chars(rest.data(), rest.data() + rest.size(), layer);
+    const std::size_t ndig = static_cast<std::size_t>(end - rest.data());
+    if (ec != std::errc() || ndig == 0 || ndig >= rest.size() || rest[ndig] != '.') return {};
+    const std::string_view suffix = rest.substr(ndig + 1);
+    for (const NamePair& p : kLayerNames)
+        if (suffix == p.hf) return "blk." + std::string(rest.substr(0, ndig)) + "." + std::string(p.ggml);
     return {};
 }
 
-Qwen3Model::Qwen3Model(const Qwen3Config& cfg) : cfg_(cfg), core_(to_core_config(cfg)) {}
+Qwen3Model::Qwen3Model(const Qwen3Config& cfg) : cfg_(cfg), core_(core_config_of(cfg)) {}
 Qwen3Model::~Qwen3Model() = default;
 
-void Qwen3Model::load_weights(const gg::File& f) {
-    const std::vector<const gg::File*> shards = {&f};
-    load_weights(shards);
-}
+void Qwen3Model::load_weights(const gg::File& f) { load_weights(std::vector<const gg::File*>{&f}); }
 
 void Qwen3Model::load_weights(const std::vector<const gg::File*>& shards) {
-    if (shards.empty()) fail("load_weights: no gguf shards");
-    brolm::detail::weights::GgufSource src(shards, [](std::string_view hf) { return qwen3_hf_to_ggml(hf); });
+    if (shards.empty()) throw std::runtime_error("qwen::Qwen3Model: load_weights: no gguf shards");
+    const brolm::detail::weights::GgufSource src(shards, [](std::string_view hf) { return qwen3_hf_to_ggml(hf); });
     core_.load_weights(src);
 }
 

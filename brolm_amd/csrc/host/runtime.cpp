@@ -7,6 +7,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "hip_util.h"
 
@@ -16,6 +17,7 @@ struct RuntimeState {
     bool ready = false;
     int device = 0;
     hipStream_t stream = nullptr;
+    std::vector<void (*)()> releases;   // on_shutdown hooks, registration order
 };
 
 RuntimeState& state() {
@@ -94,5 +96,30 @@ void sync_all() {
 void* stream() { return hipx::stream(); }
 
 int device_ordinal() { return state().device; }
+
+void on_shutdown(void (*release)()) {
+    std::lock_guard<std::mutex> lk(init_mutex());
+    std::vector<void (*)()>& r = state().releases;
+    for (void (*f)() : r)
+        if (f == release) return;
+    r.push_back(release);
+}
+
+void shutdown() {
+    std::vector<void (*)()> hooks;
+    {
+        std::lock_guard<std::mutex> lk(init_mutex());
+        if (!state().ready) return;
+        hooks.swap(state().releases);
+    }
+    (void)hipStreamSynchronize(state().stream);
+    for (auto it = hooks.rbegin(); it != hooks.rend(); ++it) (*it)();
+    std::lock_guard<std::mutex> lk(init_mutex());
+    RuntimeState& s = state();
+    (void)hipStreamSynchronize(s.stream);
+    (void)hipStreamDestroy(s.stream);
+    s.stream = nullptr;
+    s.ready = false;
+}
 
 }  // namespace brotensor

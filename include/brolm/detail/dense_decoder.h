@@ -120,6 +120,9 @@ private:
 
     int cache_len_ = 0;
     int max_seq_len_ = 0;
+    // every layer's K then V, (capacity, n_kv*head_dim) FP16 each; the
+    // layers' K_cache / V_cache are views into it
+    brotensor::Tensor kv_arena_;
 
     brotensor::Tensor rope_cos_, rope_sin_;  // (cap, hd/2) FP32
     brotensor::Tensor ids_dev_, h_, norm_, q_, k_, v_, qn_, kn_, attn_, proj_, gate_, up_;

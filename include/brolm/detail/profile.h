@@ -1,9 +1,14 @@
 #pragma once
 
-// Env-gated per-stage timing (reference include/brolm/detail/profile.h:19-69).
-// BROLM_PROFILE=1 brackets each stage with sync_all() and accumulates wall
-// time; report() prints the table to stderr.  Profiling runs the eager path
-// (one kernel group per stage), so its throughput is not the graph's.
+// Env-gated per-stage timing (reference include/brolm/detail/profile.h:19-69:
+// the Stage list and this surface).  BROLM_PROFILE set to a non-empty value
+// other than "0" turns ScopedStage on: it records a HIP event on the op
+// stream at each end of the stage and never waits, so the accumulated times
+// are device time between those events (kernel time for device stages) and
+// the stream is not serialised.  report() prints the table to stderr.
+// Profiling runs single-token steps on the per-stage kernels (the fused step
+// has no stage boundaries), so its throughput is not the fused step's.
+// Thread-safe.
 
 #include <cstdint>
 
@@ -46,8 +51,11 @@ public:
     ScopedStage& operator=(const ScopedStage&) = delete;
 
 private:
+    enum class Mode : std::uint8_t { Off, Device, Host };
     Stage stage_;
-    std::uint64_t t0_ = 0;
+    Mode mode_ = Mode::Off;
+    void* open_ = nullptr;     // the opening hipEvent_t (Device)
+    std::uint64_t t0_ = 0;     // host steady_clock ns at entry (Host: before brotensor::init)
 };
 
 }  // namespace brolm::detail::profile

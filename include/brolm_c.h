@@ -42,6 +42,11 @@ typedef struct {
 const char* brolm_last_error(void);
 /* brotensor::init(): registers the gfx950 device (fails without one). */
 int brolm_init(void);
+/* brotensor::shutdown(): after the queued work, frees the runtime's own
+ * device buffers (op scratch, RoPE tables, sampler buffers, profiler events)
+ * and the op stream.  Models still open stay valid to close.  No-op when
+ * not initialised. */
+int brolm_shutdown(void);
 
 /* synth::write_qwen3_gguf */
 int brolm_synth_qwen3_write(const brolm_synth_qwen3_spec* spec, const char* path);
@@ -153,10 +158,14 @@ int brolm_sample_token_device(const uint16_t* logits_dev, int vocab, float tempe
 /* Synthetic prompt of tools/bench_decode.cpp:208-213: std::mt19937_64(seed)() % vocab. */
 int brolm_prompt_ids(uint64_t seed, int n, int vocab, int32_t* out);
 
-/* BROLM_PROFILE stage table (src/detail/profile.cpp). */
+/* BROLM_PROFILE stage table (reference src/detail/profile.cpp), timed with
+ * HIP events on the op stream. */
 void brolm_profile_reset(void);
 void brolm_profile_report(void);
 int brolm_profile_enabled(void);
+/* Accumulated device nanoseconds and call count of one stage
+ * (profile::Stage order: embed = 0 ... other = 16); -1 for a bad index. */
+int brolm_profile_stage(int stage, uint64_t* ns, uint64_t* calls);
 
 /* qwen::Tokenizer (include/brolm/qwen_tokenizer.h; reference
  * include/brolm/qwen_tokenizer.h:41-151).  A handle from one of the three

@@ -21,4 +21,14 @@ void sync_all();                // waits for every op issued so far
 void* stream();                 // the hipStream_t every op is issued on
 int device_ordinal();
 
+// Releases what the runtime itself holds on the device, after the queued
+// work has finished: every hook registered with on_shutdown (latest first:
+// the ops' scratch and RoPE tables, the sampler's buffers, the stage
+// profiler's events), then the op stream.  Tensors and models the caller
+// still owns stay valid to destroy afterwards.  init() may be called again.
+// The Python package calls this from an atexit hook, so nothing the library
+// allocated is left for the process's exit handlers to free.
+void shutdown();
+void on_shutdown(void (*release)());
+
 }  // namespace brotensor
