@@ -165,6 +165,12 @@ C_SYMBOLS = {
     "brolm_profile_reset": (None, []),
     "brolm_profile_report": (None, []),
     "brolm_profile_enabled": (C.c_int, []),
+    "brolm_gguf_tensor_data": (i64, [cp, cp, P_u8, i64]),
+    "brolm_gguf_meta_int": (C.c_int, [cp, cp, C.POINTER(i64)]),
+    "brolm_gguf_meta_f64": (C.c_int, [cp, cp, C.POINTER(f64)]),
+    "brolm_gguf_meta_str": (i64, [cp, cp, C.c_char_p, i64]),
+    "brolm_gguf_meta_array": (C.c_int, [cp, cp, C.POINTER(C.c_int), C.POINTER(i64)]),
+    "brolm_gguf_parse_memory": (C.c_int, [P_u8, i64, C.POINTER(i64)]),
     "brolm_profile_stage": (C.c_int, [C.c_int, C.POINTER(u64), C.POINTER(u64)]),
 }
 

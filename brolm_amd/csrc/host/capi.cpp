@@ -231,6 +231,94 @@ int brolm_gguf_tensor_info(const char* path, const char* name, int* ggml_type, i
     });
 }
 
+namespace {
+
+const brotensor::gguf::Value& need_meta(const brotensor::gguf::File& f, const char* key) {
+    const brotensor::gguf::Value* v = f.find_meta(key);
+    if (!v) throw std::runtime_error(std::string("gguf: no metadata '") + key + "'");
+    return *v;
+}
+
+}  // namespace
+
+int64_t brolm_gguf_tensor_data(const char* path, const char* name, uint8_t* out, int64_t cap) {
+    int64_t n = -1;
+    const int rc = guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto* t = f.find_tensor(name);
+        if (!t) throw std::runtime_error(std::string("gguf: no tensor '") + name + "'");
+        if (static_cast<int64_t>(t->nbytes) > cap) throw std::runtime_error("gguf: output buffer too small");
+        std::memcpy(out, t->data, t->nbytes);
+        n = static_cast<int64_t>(t->nbytes);
+    });
+    return rc == 0 ? n : -1;
+}
+
+int brolm_gguf_meta_int(const char* path, const char* key, int64_t* out) {
+    return guard([&] {
+        using T = brotensor::gguf::ValueType;
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto& v = need_meta(f, key);
+        switch (v.type) {
+            case T::U8: *out = v.scalar.u8; break;
+            case T::I8: *out = v.scalar.i8; break;
+            case T::U16: *out = v.scalar.u16; break;
+            case T::I16: *out = v.scalar.i16; break;
+            case T::U32: *out = v.scalar.u32; break;
+            case T::I32: *out = v.scalar.i32; break;
+            case T::U64: *out = static_cast<int64_t>(v.scalar.u64); break;
+            case T::I64: *out = v.scalar.i64; break;
+            case T::Bool: *out = v.scalar.b ? 1 : 0; break;
+            default: throw std::runtime_error(std::string("gguf: metadata '") + key + "' is not an integer");
+        }
+    });
+}
+
+int brolm_gguf_meta_f64(const char* path, const char* key, double* out) {
+    return guard([&] {
+        using T = brotensor::gguf::ValueType;
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto& v = need_meta(f, key);
+        if (v.type == T::F32) *out = v.scalar.f32;
+        else if (v.type == T::F64) *out = v.scalar.f64;
+        else throw std::runtime_error(std::string("gguf: metadata '") + key + "' is not a float");
+    });
+}
+
+int64_t brolm_gguf_meta_str(const char* path, const char* key, char* out, int64_t cap) {
+    int64_t n = -1;
+    const int rc = guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto& v = need_meta(f, key);
+        if (v.type != brotensor::gguf::ValueType::String)
+            throw std::runtime_error(std::string("gguf: metadata '") + key + "' is not a string");
+        if (static_cast<int64_t>(v.str.size()) > cap) throw std::runtime_error("gguf: output buffer too small");
+        std::memcpy(out, v.str.data(), v.str.size());
+        n = static_cast<int64_t>(v.str.size());
+    });
+    return rc == 0 ? n : -1;
+}
+
+int brolm_gguf_meta_array(const char* path, const char* key, int* elem_type, int64_t* count) {
+    return guard([&] {
+        const brotensor::gguf::File f = brotensor::gguf::File::open(path);
+        const auto& v = need_meta(f, key);
+        if (v.type != brotensor::gguf::ValueType::Array)
+            throw std::runtime_error(std::string("gguf: metadata '") + key + "' is not an array");
+        *elem_type = static_cast<int>(v.array_type);
+        *count = static_cast<int64_t>(v.array.size());
+    });
+}
+
+int brolm_gguf_parse_memory(const uint8_t* data, int64_t size, int64_t* n_tensors) {
+    return guard([&] {
+        if (size < 0 || (!data && size > 0)) throw std::runtime_error("gguf: bad buffer");
+        std::vector<std::uint8_t> bytes(data, data + size);
+        const brotensor::gguf::File f = brotensor::gguf::File::from_memory(std::move(bytes));
+        *n_tensors = static_cast<int64_t>(f.tensor_count());
+    });
+}
+
 brolm_qwen3* brolm_qwen3_create(const brolm_qwen3_config* cfg) {
     brolm_qwen3* out = nullptr;
     const int rc = guard([&] {

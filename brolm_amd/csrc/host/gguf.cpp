@@ -65,6 +65,19 @@ struct Reader {
     }
 };
 
+// Smallest encoding of one value of type t (strings: the u64 length; arrays:
+// element type + count).
+std::uint64_t min_encoded_bytes(ValueType t) {
+    switch (t) {
+        case ValueType::U8: case ValueType::I8: case ValueType::Bool: return 1;
+        case ValueType::U16: case ValueType::I16: return 2;
+        case ValueType::U32: case ValueType::I32: case ValueType::F32: return 4;
+        case ValueType::U64: case ValueType::I64: case ValueType::F64: case ValueType::String: return 8;
+        case ValueType::Array: return 12;
+        default: bad("unknown metadata value type " + std::to_string(static_cast<unsigned>(t)));
+    }
+}
+
 Value read_value(Reader& r, ValueType t, int depth) {
     Value v;
     v.type = t;
@@ -85,7 +98,11 @@ Value read_value(Reader& r, ValueType t, int depth) {
             if (depth > 4) bad("nested arrays too deep");
             v.array_type = static_cast<ValueType>(r.get<std::uint32_t>());
             const std::uint64_t n = r.get<std::uint64_t>();
-            if (n > (std::uint64_t(1) << 32)) bad("array too long");
+            // every element takes at least min_encoded_bytes of the file: a
+            // count the remaining bytes cannot hold is malformed (and is
+            // refused before anything is reserved for it)
+            const std::uint64_t room = static_cast<std::uint64_t>(r.end - r.p);
+            if (n > room / min_encoded_bytes(v.array_type)) bad("array count exceeds the file");
             v.array.reserve(static_cast<std::size_t>(n));
             for (std::uint64_t i = 0; i < n; ++i) v.array.push_back(read_value(r, v.array_type, depth + 1));
             break;
@@ -112,9 +129,15 @@ void File::parse_() {
         const auto t = static_cast<ValueType>(r.get<std::uint32_t>());
         Value v = read_value(r, t, 0);
         if (key == "general.alignment") {
-            if (t == ValueType::U32) alignment_ = v.scalar.u32;
-            else if (t == ValueType::U64) alignment_ = static_cast<std::uint32_t>(v.scalar.u64);
-            if (alignment_ == 0) bad("zero alignment");
+            // a u32 in the spec; a power of two here, since data offsets are
+            // rounded to it
+            std::uint64_t a = 0;
+            if (t == ValueType::U32) a = v.scalar.u32;
+            else if (t == ValueType::U64) a = v.scalar.u64;
+            else bad("general.alignment is not an unsigned integer");
+            if (a == 0 || (a & (a - 1)) != 0 || a > (1u << 20)) bad("general.alignment " + std::to_string(a) +
+                                                                   " is not a power of two up to 1 MiB");
+            alignment_ = static_cast<std::uint32_t>(a);
         }
         meta_.emplace_back(std::move(key), std::move(v));
     }
@@ -126,25 +149,34 @@ void File::parse_() {
         if (nd < 1 || nd > 4) bad("tensor '" + ti.name + "' has " + std::to_string(nd) + " dims");
         ti.numel = 1;
         for (std::uint32_t d = 0; d < nd; ++d) {
-            const std::int64_t x = static_cast<std::int64_t>(r.get<std::uint64_t>());
-            if (x <= 0) bad("tensor '" + ti.name + "' has a non-positive dim");
-            ti.dims.push_back(x);
-            ti.numel *= x;
+            const std::uint64_t x = r.get<std::uint64_t>();
+            if (x == 0 || x > static_cast<std::uint64_t>(INT64_MAX) ||
+                __builtin_mul_overflow(ti.numel, static_cast<std::int64_t>(x), &ti.numel))
+                bad("tensor '" + ti.name + "' has a zero or overflowing dim");
+            ti.dims.push_back(static_cast<std::int64_t>(x));
         }
         ti.dtype = dtype_from_ggml(static_cast<int>(r.get<std::uint32_t>()));
         ti.offset = r.get<std::uint64_t>();
         if (ti.dims[0] % dtype_block_size(ti.dtype) != 0)
             bad("tensor '" + ti.name + "' row length is not a multiple of the block size");
-        ti.nbytes = static_cast<std::size_t>(dtype_storage_bytes(ti.dtype, ti.dims[0]) * (ti.numel / ti.dims[0]));
+        std::uint64_t nbytes = 0;
+        if (__builtin_mul_overflow(static_cast<std::uint64_t>(dtype_storage_bytes(ti.dtype, ti.dims[0])),
+                                   static_cast<std::uint64_t>(ti.numel / ti.dims[0]), &nbytes))
+            bad("tensor '" + ti.name + "' byte size overflows");
+        ti.nbytes = static_cast<std::size_t>(nbytes);
         tensors_.push_back(std::move(ti));
     }
     const std::size_t hdr = static_cast<std::size_t>(r.p - storage_->base);
     const std::size_t data0 = (hdr + alignment_ - 1) / alignment_ * alignment_;
+    if (data0 > storage_->size && !tensors_.empty()) bad("data section starts past the end of the file");
+    const std::uint64_t room = storage_->size > data0 ? storage_->size - data0 : 0;
     for (std::size_t i = 0; i < tensors_.size(); ++i) {
         TensorInfo& ti = tensors_[i];
-        if (data0 + ti.offset + ti.nbytes > storage_->size) bad("tensor '" + ti.name + "' data out of range");
+        if (ti.offset % alignment_ != 0) bad("tensor '" + ti.name + "' offset is not a multiple of the alignment");
+        // offset and size each checked against what is left, so no sum can wrap
+        if (ti.offset > room || ti.nbytes > room - ti.offset) bad("tensor '" + ti.name + "' data out of range");
         ti.data = storage_->base + data0 + ti.offset;
-        tensor_index_[ti.name] = i;
+        if (!tensor_index_.emplace(ti.name, i).second) bad("duplicate tensor '" + ti.name + "'");
     }
 }
 

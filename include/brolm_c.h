@@ -64,6 +64,20 @@ int brolm_qwen3_config_from_gguf(const char* path, brolm_qwen3_config* out);
 int brolm_gguf_tensor_count(const char* path, int64_t* out);
 int brolm_gguf_tensor_info(const char* path, const char* name, int* ggml_type, int64_t* dims4, int* ndims,
                            int64_t* nbytes);
+/* Tensor bytes as stored (nbytes of brolm_gguf_tensor_info); returns nbytes,
+ * or -1 on error or when cap is too small. */
+int64_t brolm_gguf_tensor_data(const char* path, const char* name, uint8_t* out, int64_t cap);
+/* Metadata of the product reader: integer scalars of any width (and bool),
+ * float scalars (F32 / F64), strings (returns the byte length, -1 when absent,
+ * not a string or cap too small; no terminator written), arrays (element
+ * value type and count). */
+int brolm_gguf_meta_int(const char* path, const char* key, int64_t* out);
+int brolm_gguf_meta_f64(const char* path, const char* key, double* out);
+int64_t brolm_gguf_meta_str(const char* path, const char* key, char* out, int64_t cap);
+int brolm_gguf_meta_array(const char* path, const char* key, int* elem_type, int64_t* count);
+/* gguf::File::from_memory over a byte buffer: 0 and the tensor count when it
+ * parses, nonzero with brolm_last_error() when it is malformed. */
+int brolm_gguf_parse_memory(const uint8_t* data, int64_t size, int64_t* n_tensors);
 
 /* Mistral3Config (include/brolm/mistral3_config.h:30-143): the text section
  * and the top-level multimodal glue (the Pixtral vision section is not part

@@ -311,6 +311,23 @@ static int gv_size(int t) {
         default: return 0;
     }
 }
+/* Steps over one encoded value of type t (gguf.md: strings are a u64 length
+ * and bytes, arrays a u32 element type, a u64 count and the elements). */
+static void rd_skip(rd* r, int t, int depth) {
+    if (t == GV_STR) {
+        uint64_t len = rd_u(r, 8);
+        if (rd_need(r, len)) r->p += len;
+    } else if (t == GV_ARR) {
+        int et = (int)rd_u(r, 4);
+        uint64_t n = rd_u(r, 8);
+        if (depth > 8 || n > (uint64_t)(r->end - r->p)) { r->bad = 1; return; }
+        for (uint64_t k = 0; k < n && !r->bad; ++k) rd_skip(r, et, depth + 1);
+    } else if (gv_size(t) > 0) {
+        if (rd_need(r, (size_t)gv_size(t))) r->p += gv_size(t);
+    } else {
+        r->bad = 1;
+    }
+}
 static void rd_scalar(rd* r, int t, int64_t* iv, double* fv) {
     uint64_t raw = rd_u(r, gv_size(t));
     switch (t) {
@@ -373,27 +390,19 @@ static or_gguf* parse(or_gguf* g) {
             kv->s = rd_str(&r);
         } else if (kv->type == GV_ARR) {
             kv->arr_type = (int)rd_u(&r, 4);
-            kv->arr_len = (int64_t)rd_u(&r, 8);
-            for (int64_t k = 0; k < kv->arr_len && !r.bad; ++k) {
-                if (kv->arr_type == GV_STR) {
-                    uint64_t len = rd_u(&r, 8);
-                    if (!rd_need(&r, len)) break;
-                    r.p += len;
-                } else if (gv_size(kv->arr_type) > 0) {
-                    if (!rd_need(&r, (size_t)gv_size(kv->arr_type))) break;
-                    r.p += gv_size(kv->arr_type);
-                } else {
-                    r.bad = 1;
-                }
-            }
+            uint64_t n = rd_u(&r, 8);
+            if (n > (uint64_t)(r.end - r.p)) r.bad = 1; /* every element is at least one byte */
+            kv->arr_len = (int64_t)n;
+            for (uint64_t k = 0; k < n && !r.bad; ++k) rd_skip(&r, kv->arr_type, 1);
         } else if (gv_size(kv->type) > 0) {
             rd_scalar(&r, kv->type, &kv->i, &kv->f);
         } else {
             r.bad = 1;
         }
-        if (!r.bad && kv->key && strcmp(kv->key, "general.alignment") == 0 && kv->type != GV_STR &&
-            kv->type != GV_ARR)
+        if (!r.bad && kv->key && strcmp(kv->key, "general.alignment") == 0) {
+            if (kv->type != GV_U32 && kv->type != GV_U64) r.bad = 1;
             alignment = (uint64_t)kv->i;
+        }
     }
     for (int64_t i = 0; i < g->n_t && !r.bad; ++i) {
         or_tinfo* t = &g->t[i];
@@ -401,11 +410,15 @@ static or_gguf* parse(or_gguf* g) {
         t->ndims = (int)rd_u(&r, 4);
         if (t->ndims < 1 || t->ndims > 4) { r.bad = 1; break; }
         for (int d = 0; d < 4; ++d) t->dims[d] = 1;
-        for (int d = 0; d < t->ndims; ++d) t->dims[d] = (int64_t)rd_u(&r, 8);
+        for (int d = 0; d < t->ndims; ++d) {
+            uint64_t x = rd_u(&r, 8);
+            if (x == 0 || x > ((uint64_t)1 << 40)) r.bad = 1; /* zero or implausible: no product can wrap */
+            t->dims[d] = (int64_t)x;
+        }
         t->type = (int)rd_u(&r, 4);
         t->offset = rd_u(&r, 8);
     }
-    if (r.bad || alignment == 0) {
+    if (r.bad || alignment == 0 || (alignment & (alignment - 1)) != 0) {
         snprintf(g_err, sizeof g_err, "gguf: truncated or malformed header");
         or_gguf_close(g);
         return NULL;
@@ -414,15 +427,25 @@ static or_gguf* parse(or_gguf* g) {
     size_t data0 = (hdr + alignment - 1) / alignment * alignment;
     for (int64_t i = 0; i < g->n_t; ++i) {
         or_tinfo* t = &g->t[i];
-        int64_t n = t->dims[0] * t->dims[1] * t->dims[2] * t->dims[3];
+        int64_t n = 1;
+        int wrap = 0;
+        for (int d = 0; d < 4; ++d) wrap |= __builtin_mul_overflow(n, t->dims[d], &n);
         int64_t rb = or_row_bytes(t->type, t->dims[0]);
         if (rb < 0) {
             snprintf(g_err, sizeof g_err, "gguf: tensor %s has unsupported type %d or ragged row", t->name, t->type);
             or_gguf_close(g);
             return NULL;
         }
-        t->nbytes = rb * (n / t->dims[0]);
-        if (data0 + t->offset + (uint64_t)t->nbytes > g->size) {
+        uint64_t rows = (uint64_t)(n / t->dims[0]);
+        uint64_t room = g->size > data0 ? g->size - data0 : 0;
+        if (wrap || n <= 0 ||
+            (rows != 0 && (uint64_t)rb > UINT64_MAX / rows)) {
+            snprintf(g_err, sizeof g_err, "gguf: tensor %s size overflows", t->name);
+            or_gguf_close(g);
+            return NULL;
+        }
+        t->nbytes = (int64_t)((uint64_t)rb * rows);
+        if (t->offset % alignment != 0 || t->offset > room || (uint64_t)t->nbytes > room - t->offset) {
             snprintf(g_err, sizeof g_err, "gguf: tensor %s data out of range", t->name);
             or_gguf_close(g);
             return NULL;
