@@ -1,10 +1,20 @@
 // Prefill contraction (M > 16) on MFMA: Y[M,N] = X[M,K] deq(W)[N,K]^T + bias.
 // Weight tiles are dequantized to FP16 in LDS with the exact GGUF formula
 // (same values as bx_dequant_to_f16), activations are FP16, products
-// accumulate in FP32 on v_mfma_f32_16x16x16_f16.
+// accumulate in FP32.
 //
-// Block tile 64 (M) x 64 (N), K step 32; 4 wavefronts each own a 32x32
-// quadrant as 2x2 MFMA tiles of 16x16.
+// Two kernels:
+//  - gemm_tile_kernel<FMT, BM, BN> (M >= 128, K a multiple of 64): a BM x BN
+//    block tile (256x128 or 128x128), 4 wavefronts as 2x2, each owning a
+//    (BM/2) x (BN/2) tile of 32x32 v_mfma_f32_32x32x16_f16 fragments.  K
+//    advances 64 per stage through two LDS buffers: the global loads of
+//    stage k+1 (activation rows, raw quant bytes) are issued before the
+//    MFMAs of stage k, the weights are dequantized after them and written to
+//    the other buffer, one barrier per stage.  Blocks map to tiles so that
+//    each XCD (blocks are dispatched round-robin over the 8) works a
+//    contiguous run of tiles that share weight columns in its own L2.
+//  - gemm_kernel<FMT> (other shapes): 64x64 block tile, K step 32, 4
+//    wavefronts each a 32x32 quadrant of 16x16x16 MFMAs.
 #include "carrier_layout.h"
 #include "common.h"
 
@@ -152,10 +162,278 @@ __global__ __launch_bounds__(256) void gemm_kernel(const void* __restrict__ W, c
         }
 }
 
+
+// ---------------------------------------------------------------- big tiles
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int TK = 64;         // K per LDS stage
+constexpr int TROW = TK + 8;   // halves per LDS row: 144 bytes, rows start 4 banks apart
+
+// The raw bytes behind 8 consecutive weights [k0, k0+8) of one row, loaded
+// ahead of the MFMAs that hide their latency, and their FP16 values.
+template <int FMT>
+struct RawW;
+template <>
+struct RawW<BX_TYPE_F16> {
+    u4v v;
+};
+template <>
+struct RawW<BX_TYPE_Q8_0> {
+    u2v q;
+    uint32_t d;
+};
+template <>
+struct RawW<BX_TYPE_Q4_K> {
+    u4v hdr;
+    u2v q;
+};
+template <>
+struct RawW<BX_TYPE_Q6_K> {
+    u2v ql, qh;
+    uint32_t sc, d;
+};
+
+template <int FMT>
+__device__ __forceinline__ RawW<FMT> load_w(const void* W, int64_t N, int64_t K, int64_t n, int64_t k0);
+template <>
+__device__ __forceinline__ RawW<BX_TYPE_F16> load_w<BX_TYPE_F16>(const void* W, int64_t, int64_t K, int64_t n,
+                                                                  int64_t k0) {
+    return {ldg16(static_cast<const uint16_t*>(W) + n * K + k0)};
+}
+template <>
+__device__ __forceinline__ RawW<BX_TYPE_Q8_0> load_w<BX_TYPE_Q8_0>(const void* W, int64_t N, int64_t K, int64_t n,
+                                                                    int64_t k0) {
+    const CarrierQ8 c = carrier_q8(W, N, K);
+    RawW<BX_TYPE_Q8_0> r;
+    r.q = *gptr<u2v>(c.qs + n * K + k0);
+    r.d = ldg_u16(c.d + (n * (K / 32) + k0 / 32) * 2);
+    return r;
+}
+template <>
+__device__ __forceinline__ RawW<BX_TYPE_Q4_K> load_w<BX_TYPE_Q4_K>(const void* W, int64_t N, int64_t K, int64_t n,
+                                                                    int64_t k0) {
+    const CarrierQ4K c = carrier_q4k(W, N, K);
+    const int64_t s = n * (K / 256) + k0 / 256;
+    const int o = (int)(k0 % 256);
+    RawW<BX_TYPE_Q4_K> r;
+    r.hdr = ldg16(c.hdr + s * 16);
+    r.q = *gptr<u2v>(c.qs + s * 128 + 32 * (o / 64) + (o % 32));
+    return r;
+}
+template <>
+__device__ __forceinline__ RawW<BX_TYPE_Q6_K> load_w<BX_TYPE_Q6_K>(const void* W, int64_t N, int64_t K, int64_t n,
+                                                                    int64_t k0) {
+    const CarrierQ6K c = carrier_q6k(W, N, K);
+    const int64_t s = n * (K / 256) + k0 / 256;
+    const int o = (int)(k0 % 256);
+    const int h = o / 128, j = (o % 128) / 32, l0 = o % 32;
+    const int t = 4 * h + l0 / 8;
+    RawW<BX_TYPE_Q6_K> r;
+    r.ql = *gptr<u2v>(c.ql + s * 128 + 16 * t + ((j & 1) ? 8 : 0));
+    r.qh = *gptr<u2v>(c.qh + s * 64 + 8 * t);
+    r.sc = *gptr<uint8_t>(c.sc + s * 16 + 8 * h + 2 * j + (l0 >= 16 ? 1 : 0));
+    r.d = ldg_u16(c.d + s * 2);
+    return r;
+}
+
+__device__ __forceinline__ u4v pack8(const uint16_t (&v)[8]) {
+    u4v p;
+    p.x = v[0] | ((uint32_t)v[1] << 16);
+    p.y = v[2] | ((uint32_t)v[3] << 16);
+    p.z = v[4] | ((uint32_t)v[5] << 16);
+    p.w = v[6] | ((uint32_t)v[7] << 16);
+    return p;
+}
+
+#pragma clang fp contract(off)
+// FP16 values of the 8 weights, the same formulas as deq8 / bx_dequant_to_f16.
+template <int FMT>
+__device__ __forceinline__ u4v decode_w(const RawW<FMT>& r, int k0);
+template <>
+__device__ __forceinline__ u4v decode_w<BX_TYPE_F16>(const RawW<BX_TYPE_F16>& r, int) {
+    return r.v;
+}
+template <>
+__device__ __forceinline__ u4v decode_w<BX_TYPE_Q8_0>(const RawW<BX_TYPE_Q8_0>& r, int) {
+    const float d = h2f((uint16_t)r.d);
+    const uint32_t a[2] = {r.q.x, r.q.y};
+    uint16_t out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = f2h(d * (float)(int8_t)((a[i >> 2] >> (8 * (i & 3))) & 0xff));
+    return pack8(out);
+}
+template <>
+__device__ __forceinline__ u4v decode_w<BX_TYPE_Q4_K>(const RawW<BX_TYPE_Q4_K>& r, int k0) {
+    const int j = (k0 % 256) / 32, shift = (j & 1) * 4;
+    const float d = h2f(r.hdr.x & 0xffff), dmin = h2f(r.hdr.x >> 16);
+    int sc, m;
+    q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, j, sc, m);
+    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+    const uint32_t a[2] = {r.q.x, r.q.y};
+    uint16_t out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = f2h(d1 * (float)((a[i >> 2] >> (8 * (i & 3) + shift)) & 0x0f) - m1);
+    return pack8(out);
+}
+template <>
+__device__ __forceinline__ u4v decode_w<BX_TYPE_Q6_K>(const RawW<BX_TYPE_Q6_K>& r, int k0) {
+    const int j = ((k0 % 256) % 128) / 32;
+    const float d1 = h2f((uint16_t)r.d) * (float)(int8_t)r.sc;
+    const uint32_t a[2] = {r.ql.x, r.ql.y}, hb[2] = {r.qh.x, r.qh.y};
+    const int nshift = (j >> 1) * 4;
+    uint16_t out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t lo = (a[i >> 2] >> (8 * (i & 3) + nshift)) & 0x0f;
+        const uint32_t hi = (hb[i >> 2] >> (8 * (i & 3) + 2 * j)) & 0x03;
+        out[i] = f2h(d1 * (float)((int)(lo | (hi << 4)) - 32));
+    }
+    return pack8(out);
+}
+#pragma clang fp contract(on)
+
+// Tile t of T (tiles of M fastest within a weight column) for block b: the
+// dispatcher deals blocks to the 8 XCDs round-robin, so XCD x receives
+// blocks x, x+8, ...; those are given the x-th contiguous run of tiles.
+__device__ __forceinline__ int xcd_tile(int b, int T) {
+    const int x = b & 7, i = b >> 3, per = T >> 3, rem = T & 7;
+    return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i;
+}
+
+template <int FMT, int TBM, int TBN>
+__global__ __launch_bounds__(256) void gemm_tile_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
+                                                       const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
+                                                       int M, int N, int K, int tiles_m) {
+    constexpr int WM = TBM / 2, WN = TBN / 2;   // wave tile
+    constexpr int FM = WM / 32, FN = WN / 32;   // 32x32 fragments per wave
+    constexpr int RA = TBM / 32, RB = TBN / 32; // loader rows per thread
+    __shared__ __align__(16) uint16_t As[2][TBM * TROW];
+    __shared__ __align__(16) uint16_t Bs[2][TBN * TROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tiles = tiles_m * (int)((N + TBN - 1) / TBN);
+    const int t = xcd_tile((int)blockIdx.x, tiles);
+    const int64_t m0 = (int64_t)(t % tiles_m) * TBM, n0 = (int64_t)(t / tiles_m) * TBN;
+
+    // loaders: 8 lanes per row, 8 halves each; rows past M / N read the last
+    // row (their results are not stored)
+    const int lrow = tid >> 3, lcol = (tid & 7) * 8;
+    const uint16_t* xrow[RA];
+#pragma unroll
+    for (int i = 0; i < RA; ++i) {
+        const int64_t m = m0 + lrow + 32 * i;
+        xrow[i] = X + (m < M ? m : M - 1) * (int64_t)K;
+    }
+    int64_t wrow[RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+        const int64_t n = n0 + lrow + 32 * i;
+        wrow[i] = n < N ? n : N - 1;
+    }
+    u4v ra[RA];
+    RawW<FMT> rb[RB];
+    auto gload = [&](int kt) {
+        const int64_t k0 = (int64_t)kt * TK + lcol;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) ra[i] = ldg16(xrow[i] + k0);
+#pragma unroll
+        for (int i = 0; i < RB; ++i) rb[i] = load_w<FMT>(W, N, K, wrow[i], k0);
+    };
+    auto lstore = [&](int buf, int kt) {
+        const int k0 = (int)(((int64_t)kt * TK + lcol) % 256);
+#pragma unroll
+        for (int i = 0; i < RA; ++i) *reinterpret_cast<u4v*>(&As[buf][(lrow + 32 * i) * TROW + lcol]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+            *reinterpret_cast<u4v*>(&Bs[buf][(lrow + 32 * i) * TROW + lcol]) = decode_w<FMT>(rb[i], k0);
+    };
+
+    f16v acc[FM][FN];
+#pragma unroll
+    for (int f = 0; f < FM; ++f)
+#pragma unroll
+        for (int g = 0; g < FN; ++g)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[f][g][r] = 0.f;
+
+    const int nk = K / TK;
+    gload(0);
+    lstore(0, 0);
+    __syncthreads();
+    // fragment reads: lane l holds row l%32, k [8*(l/32), +8) of a 32x16 slice
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int kk = 0; kk < TK; kk += 16) {
+            h8 a[FM], b[FN];
+#pragma unroll
+            for (int f = 0; f < FM; ++f)
+                a[f] = *reinterpret_cast<const h8*>(&As[cur][(wm0 + 32 * f + fr) * TROW + kk + fk]);
+#pragma unroll
+            for (int g = 0; g < FN; ++g)
+                b[g] = *reinterpret_cast<const h8*>(&Bs[cur][(wn0 + 32 * g + fr) * TROW + kk + fk]);
+#pragma unroll
+            for (int f = 0; f < FM; ++f)
+#pragma unroll
+                for (int g = 0; g < FN; ++g)
+                    acc[f][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[f], b[g], acc[f][g], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1, kt + 1);
+        __syncthreads();
+    }
+
+    // D layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
+#pragma unroll
+    for (int g = 0; g < FN; ++g) {
+        const int64_t n = n0 + wn0 + 32 * g + (lane & 31);
+        if (n >= N) continue;
+        const float bv = bias ? h2f(bias[n]) : 0.f;
+#pragma unroll
+        for (int f = 0; f < FM; ++f)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t m = m0 + wm0 + 32 * f + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M) Y[m * N + n] = f2h(acc[f][g][r] + bv);
+            }
+    }
+}
+
+template <int FMT, int TBM, int TBN>
+int launch_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                 hipStream_t st) {
+    const int tm = (M + TBM - 1) / TBM, tn = (N + TBN - 1) / TBN;
+    if ((int64_t)tm * tn > (1 << 30)) return fail(BX_EINVAL, "gemm: too many tiles");
+    gemm_tile_kernel<FMT, TBM, TBN><<<dim3((unsigned)(tm * tn)), 256, 0, st>>>(W, X, bias, Y, M, N, K, tm);
+    return launch_check("gemm_tile");
+}
+
+template <int FMT>
+int gemm_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+               hipStream_t st) {
+    // 256x128 tiles when they still give every CU a block, else 128x128
+    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
+    if (big >= num_cus()) return launch_tiles<FMT, 256, 128>(W, bias, X, Y, M, N, K, st);
+    return launch_tiles<FMT, 128, 128>(W, bias, X, Y, M, N, K, st);
+}
+
 }  // namespace
 
 int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st) {
+    if (M >= 128 && K % TK == 0) {
+        switch (wtype) {
+            case BX_TYPE_Q4_K: return gemm_tiles<BX_TYPE_Q4_K>(W, bias, X, Y, M, N, K, st);
+            case BX_TYPE_Q6_K: return gemm_tiles<BX_TYPE_Q6_K>(W, bias, X, Y, M, N, K, st);
+            case BX_TYPE_Q8_0: return gemm_tiles<BX_TYPE_Q8_0>(W, bias, X, Y, M, N, K, st);
+            case BX_TYPE_F16: return gemm_tiles<BX_TYPE_F16>(W, bias, X, Y, M, N, K, st);
+            default: return fail(BX_EUNSUPPORTED, "gemm: unsupported type");
+        }
+    }
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
     if (grid.y > 65535) return fail(BX_EINVAL, "gemm: M too large");
     switch (wtype) {

@@ -107,6 +107,29 @@ def test_linear_quant_vs_oracle(t, N, K):
         assert np.all(err <= tol), (M, float((err / tol).max()))
 
 
+@pytest.mark.parametrize("t", QTYPES + [1])
+@pytest.mark.parametrize("N,K", [(128, 256), (300, 1024), (1024, 512), (4100, 256)])
+def test_linear_big_tiles_vs_oracle(t, N, K):
+    """The 256x128 / 128x128 MFMA tiles (M >= 128, K a multiple of 64):
+    partial tiles in M and N, a grid above and below the CU count (both tile
+    shapes), bias."""
+    rng = np.random.default_rng(N * 7 + K + t)
+    if t == 1:
+        Wv = _f16(rng.standard_normal((N, K)) * 0.05)
+        car = f16_dev(Wv)
+    else:
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        car = carrier(t, raw, N, K)
+    bias = _f16(rng.standard_normal(N))
+    for M in (128, 129, 255, 256, 600):
+        print(f"[linear tiles] type={t} N={N} K={K} M={M}", flush=True)
+        X = _f16(rng.standard_normal((M, K)))
+        got = _run_linear(t, car, X, N, K, bias)
+        ref = oracle.linear(Wv, X) + bias
+        tol = _linear_tol(Wv, X, ref)
+        assert np.all(np.abs(got - ref) <= tol), (M, float((np.abs(got - ref) / tol).max()))
+
+
 @pytest.mark.parametrize("t", QTYPES)
 def test_linear_ffn_width_k(t):
     """K = 32768 (Mistral-Small-3.1's FFN width, the down projection): the
