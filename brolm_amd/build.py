@@ -54,12 +54,20 @@ def _jobs() -> int:
     return max(1, min(n, 16))
 
 
+# Per-file additions.  gemm.hip: LLVM's iterative ILP scheduler keeps the
+# next k16 step's LDS fragment reads in flight under the current step's MFMAs
+# (the default occupancy-driven schedule reuses one fragment register and
+# waits on every read): 806-866 vs 703-787 TFLOP/s on FP16 8B shapes.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
+
+
 def build_kernels() -> Path:
     srcs = sorted((CSRC / "kernels").glob("*.hip"))
     OBJDIR.mkdir(parents=True, exist_ok=True)
     objs = [OBJDIR / (s.stem + ".hip.o") for s in srcs]
     with cf.ThreadPoolExecutor(_jobs()) as ex:
-        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", str(so[0]), "-o", str(so[1])]), zip(srcs, objs)))
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(so[0].name, []), "-c", str(so[0]),
+                                     "-o", str(so[1])]), zip(srcs, objs)))
     LIBDIR.mkdir(parents=True, exist_ok=True)
     out = LIBDIR / "libbrolm_hip.so"
     tmp = out.with_suffix(".so.tmp")

@@ -2,7 +2,9 @@
 // called at src/detail/dense_decoder.cpp:606-607; Gemma form with softcap and
 // window at src/gemma2.cpp:365-367; masked form at dense_decoder.cpp:476-478).
 //
-// Split-K ("flash decoding"): block (split s, kv head g, query row r) streams
+// L >= 16 rows with head_dim 64 / 128 and no softcap, window or mask run the
+// MFMA flash-attention kernel (attention_mfma.hip); everything else runs
+// split-K ("flash decoding"): block (split s, kv head g, query row r) streams
 // its key range in chunks of 256 with an online softmax and writes an
 // unnormalised partial (o[hd], m, l) per query head of the group; a combine
 // kernel merges the splits.  Query head h reads KV head h / (n_q / n_kv).
@@ -94,6 +96,8 @@ int bx_attention_decode_f16(const uint16_t* q, const uint16_t* Kc, const uint16_
     if (n_q / n_kv > kAttnMaxGroup) return fail(BX_EUNSUPPORTED, "attention: GQA group larger than 8");
     if (hd <= 0 || hd % 8 || hd > 256) return fail(BX_EUNSUPPORTED, "attention: head_dim must be a multiple of 8, <= 256");
     if (valid_len < L) return fail(BX_EINVAL, "attention: valid_len < L");
+    if (attn_mfma_supported(L, hd, softcap, window, nullptr))
+        return attn_mfma(q, Kc, Vc, L, valid_len, n_q, n_kv, hd, 0, out, as_stream(stream));
     AttnArgs a{};
     a.q = q; a.Kc = Kc; a.Vc = Vc; a.mask = nullptr;
     a.L = L; a.valid_len = valid_len; a.n_q = n_q; a.n_kv = n_kv; a.hd = hd;
@@ -119,6 +123,8 @@ int bx_attention_gqa_f16(const uint16_t* q, const uint16_t* K, const uint16_t* V
     if (hd <= 0 || hd % 8 || hd > 256)
         return fail(BX_EUNSUPPORTED, "attention_gqa: head_dim must be a multiple of 8, <= 256");
     if (causal && n_keys < L) return fail(BX_EINVAL, "attention_gqa: causal with fewer keys than rows");
+    if (attn_mfma_supported(L, hd, 0.f, 0, nullptr))
+        return attn_mfma(q, K, V, L, n_keys, n_q, n_kv, hd, causal ? 0 : 1, out, as_stream(stream));
     AttnArgs a{};
     a.q = q; a.Kc = K; a.Vc = V; a.mask = nullptr;
     a.L = L; a.valid_len = n_keys; a.n_q = n_q; a.n_kv = n_kv; a.hd = hd;

@@ -22,6 +22,12 @@ struct AttnArgs {
     int bidir;  // 1: every row attends all valid_len keys (no causal limit)
 };
 
+// Flash attention on MFMA for L >= 16 query rows (attention_mfma.hip): head
+// dims 64 and 128, no softcap / window / key mask.
+bool attn_mfma_supported(int L, int hd, float softcap, int window, const float* mask);
+int attn_mfma(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, int L, int valid_len, int n_q, int n_kv,
+              int hd, int bidir, uint16_t* out, hipStream_t st);
+
 struct AttnState {
     float o[kAttnPairsPerThread];
 };

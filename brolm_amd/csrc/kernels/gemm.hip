@@ -4,9 +4,10 @@
 // accumulate in FP32.
 //
 // Two kernels:
-//  - gemm_tile_kernel<FMT, BM, BN> (M >= 128, K a multiple of 64): a BM x BN
-//    block tile (256x128 or 128x128), 4 wavefronts as 2x2, each owning a
-//    (BM/2) x (BN/2) tile of 32x32 v_mfma_f32_32x32x16_f16 fragments.  K
+//  - gemm_tile_kernel<FMT, BM, BN, NW> (M >= 128, K a multiple of 64): a
+//    BM x BN block tile (256x128 with 8 wavefronts as 4x2, or 128x128 with 4
+//    as 2x2), each wavefront owning a 64x64 tile of 32x32
+//    v_mfma_f32_32x32x16_f16 fragments.  K
 //    advances 64 per stage through two LDS buffers: the global loads of
 //    stage k+1 (activation rows, raw quant bytes) are issued before the
 //    MFMAs of stage k, the weights are dequantized after them and written to
@@ -302,13 +303,15 @@ __device__ __forceinline__ int xcd_tile(int b, int T) {
     return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i;
 }
 
-template <int FMT, int TBM, int TBN>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
-                                                       const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
-                                                       int M, int N, int K, int tiles_m) {
-    constexpr int WM = TBM / 2, WN = TBN / 2;   // wave tile
-    constexpr int FM = WM / 32, FN = WN / 32;   // 32x32 fragments per wave
-    constexpr int RA = TBM / 32, RB = TBN / 32; // loader rows per thread
+// NW wavefronts (4 or 8) as (NW/2) x 2 over the block tile.
+template <int FMT, int TBM, int TBN, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
+                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
+                                                           int M, int N, int K, int tiles_m) {
+    constexpr int NT = 64 * NW, ROWS = NT / 8;  // threads; rows one loader pass covers
+    constexpr int WM = TBM / (NW / 2), WN = TBN / 2;  // wave tile
+    constexpr int FM = WM / 32, FN = WN / 32;         // 32x32 fragments per wave
+    constexpr int RA = TBM / ROWS, RB = TBN / ROWS;   // loader rows per thread
     __shared__ __align__(16) uint16_t As[2][TBM * TROW];
     __shared__ __align__(16) uint16_t Bs[2][TBN * TROW];
 
@@ -323,13 +326,13 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const void* __restrict__
     const uint16_t* xrow[RA];
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
-        const int64_t m = m0 + lrow + 32 * i;
+        const int64_t m = m0 + lrow + ROWS * i;
         xrow[i] = X + (m < M ? m : M - 1) * (int64_t)K;
     }
     int64_t wrow[RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-        const int64_t n = n0 + lrow + 32 * i;
+        const int64_t n = n0 + lrow + ROWS * i;
         wrow[i] = n < N ? n : N - 1;
     }
     u4v ra[RA];
@@ -344,10 +347,10 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const void* __restrict__
     auto lstore = [&](int buf, int kt) {
         const int k0 = (int)(((int64_t)kt * TK + lcol) % 256);
 #pragma unroll
-        for (int i = 0; i < RA; ++i) *reinterpret_cast<u4v*>(&As[buf][(lrow + 32 * i) * TROW + lcol]) = ra[i];
+        for (int i = 0; i < RA; ++i) *reinterpret_cast<u4v*>(&As[buf][(lrow + ROWS * i) * TROW + lcol]) = ra[i];
 #pragma unroll
         for (int i = 0; i < RB; ++i)
-            *reinterpret_cast<u4v*>(&Bs[buf][(lrow + 32 * i) * TROW + lcol]) = decode_w<FMT>(rb[i], k0);
+            *reinterpret_cast<u4v*>(&Bs[buf][(lrow + ROWS * i) * TROW + lcol]) = decode_w<FMT>(rb[i], k0);
     };
 
     f16v acc[FM][FN];
@@ -403,12 +406,12 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const void* __restrict__
     }
 }
 
-template <int FMT, int TBM, int TBN>
+template <int FMT, int TBM, int TBN, int NW>
 int launch_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
                  hipStream_t st) {
     const int tm = (M + TBM - 1) / TBM, tn = (N + TBN - 1) / TBN;
     if ((int64_t)tm * tn > (1 << 30)) return fail(BX_EINVAL, "gemm: too many tiles");
-    gemm_tile_kernel<FMT, TBM, TBN><<<dim3((unsigned)(tm * tn)), 256, 0, st>>>(W, X, bias, Y, M, N, K, tm);
+    gemm_tile_kernel<FMT, TBM, TBN, NW><<<dim3((unsigned)(tm * tn)), 64 * NW, 0, st>>>(W, X, bias, Y, M, N, K, tm);
     return launch_check("gemm_tile");
 }
 
@@ -417,8 +420,10 @@ int gemm_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t*
                hipStream_t st) {
     // 256x128 tiles when they still give every CU a block, else 128x128
     const int64_t big = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
-    if (big >= num_cus()) return launch_tiles<FMT, 256, 128>(W, bias, X, Y, M, N, K, st);
-    return launch_tiles<FMT, 128, 128>(W, bias, X, Y, M, N, K, st);
+    // eight wavefronts (two per SIMD): one wave's dequantization overlaps
+    // the other's MFMAs (Q4_K 8B shapes 631-698 vs 480-555 TFLOP/s)
+    if (big >= num_cus()) return launch_tiles<FMT, 256, 128, 8>(W, bias, X, Y, M, N, K, st);
+    return launch_tiles<FMT, 128, 128, 4>(W, bias, X, Y, M, N, K, st);
 }
 
 }  // namespace

@@ -278,7 +278,11 @@ def _attn_ref(q, K, V, L, valid, n_q, n_kv, hd, softcap=0.0, window=0, mask=None
 
 @pytest.mark.parametrize("L,valid,n_q,n_kv,hd", [
     (1, 1, 4, 2, 64), (1, 5, 16, 8, 128), (1, 64, 16, 8, 128), (1, 65, 16, 8, 128), (1, 300, 8, 8, 64),
-    (1, 2049, 16, 8, 128), (1, 4096, 32, 8, 128), (4, 70, 4, 2, 64), (16, 600, 16, 8, 128)])
+    (1, 2049, 16, 8, 128), (1, 4096, 32, 8, 128), (4, 70, 4, 2, 64), (16, 600, 16, 8, 128),
+    # L >= 16 rows: the MFMA flash-attention kernel (partial query and key
+    # tiles, GQA groups 1..4, prompt-only and after a cached prefix)
+    (17, 17, 4, 2, 64), (64, 64, 16, 8, 128), (65, 200, 32, 8, 128), (130, 130, 8, 8, 64),
+    (300, 1000, 8, 2, 128)])
 def test_attention_decode(L, valid, n_q, n_kv, hd):
     print(f"[attention] L={L} valid={valid} n_q={n_q} n_kv={n_kv} hd={hd}", flush=True)
     rng = np.random.default_rng(valid + 7 * L)
@@ -291,6 +295,28 @@ def test_attention_decode(L, valid, n_q, n_kv, hd):
     call("bx_attention_decode_f16", ptr(f16_dev(q)), ptr(f16_dev(K)), ptr(f16_dev(V)), L, valid, n_q, n_kv, hd,
          C.c_float(0.0), 0, ptr(out), ptr(ws), stream())
     ref = _attn_ref(q, K, V, L, valid, n_q, n_kv, hd)
+    np.testing.assert_allclose(f16_host(out).reshape(L, -1), ref, atol=3e-3)
+
+
+@pytest.mark.parametrize("L,n_keys,causal,hd", [(16, 16, 0, 128), (100, 100, 0, 64), (77, 77, 1, 128),
+                                                 (40, 90, 1, 128), (200, 200, 0, 128)])
+def test_attention_gqa_encode(L, n_keys, causal, hd):
+    """flash_attention_gqa_forward (dense_decoder.cpp:737-745): bidirectional
+    rows see every key, causal rows the keys up to their position."""
+    print(f"[attention gqa] L={L} keys={n_keys} causal={causal} hd={hd}", flush=True)
+    rng = np.random.default_rng(L * 3 + n_keys + causal)
+    n_q, n_kv = 8, 4
+    q = _f16(rng.standard_normal((L, n_q * hd)))
+    K = _f16(rng.standard_normal((n_keys, n_kv * hd)))
+    V = _f16(rng.standard_normal((n_keys, n_kv * hd)))
+    ws = empty(max(1, hip().bx_attention_workspace_bytes(L, n_q, hd, n_keys)))
+    out = torch().empty(L * n_q * hd, dtype=torch().int16, device="cuda")
+    call("bx_attention_gqa_f16", ptr(f16_dev(q)), ptr(f16_dev(K)), ptr(f16_dev(V)), L, n_keys, n_q, n_kv, hd, causal,
+         ptr(out), ptr(ws), stream())
+    if causal:
+        ref = _attn_ref(q, K, V, L, n_keys, n_q, n_kv, hd)
+    else:
+        ref = np.concatenate([_attn_ref(q[r:r + 1], K, V, 1, n_keys, n_q, n_kv, hd) for r in range(L)])
     np.testing.assert_allclose(f16_host(out).reshape(L, -1), ref, atol=3e-3)
 
 
