@@ -108,6 +108,11 @@ HIP_SYMBOLS = {
     "bx_argmax_workspace_bytes": (C.c_size_t, [i64]),
     "bx_argmax_f16": (C.c_int, [vp, i64, vp, vp, vp]),
     "bx_argmax_f16_noalloc": (C.c_int, [vp, i64, vp, vp]),
+    "bx_linear_tiles_ok": (C.c_int, [C.c_int, C.c_int]),
+    "bx_linear_group_f16": (C.c_int, [C.c_int, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), vp, C.c_int,
+                                      C.c_int, vp]),
+    "bx_linear_residual_f16": (C.c_int, [C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "bx_linear_swiglu_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
 }
 
 # every symbol of include/brolm_c.h

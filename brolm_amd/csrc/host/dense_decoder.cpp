@@ -433,10 +433,15 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
     for (Layer& layer : layers_) {
         { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.input_ln, eps, norm_); }
         {
+            // one launch for the projections that share a weight dtype
+            // (q / k always, v too unless a Q4_K_M layer raised it)
             prof::ScopedStage ps(PS::qkv_proj);
-            linear_batched(layer.Wq, nullptr, norm_, q_);
-            linear_batched(layer.Wk, nullptr, norm_, k_);
-            linear_batched(layer.Wv, nullptr, norm_, v_);
+            const bt::Tensor* w[3] = {&layer.Wq, &layer.Wk, &layer.Wv};
+            bt::Tensor* y[3] = {&q_, &k_, &v_};
+            const int same = layer.Wv.dtype == layer.Wq.dtype ? 3 : 2;
+            int done = 0;
+            if (layer.Wk.dtype == layer.Wq.dtype && bt::linear_group_forward_batched(w, y, same, norm_)) done = same;
+            for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, norm_, *y[i]);
         }
         bt::Tensor* q_attn = &q_;
         bt::Tensor* k_attn = &k_;
@@ -457,21 +462,41 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
             prof::ScopedStage ps(PS::attention);
             bt::flash_attention_decode(*q_attn, layer.K_cache, layer.V_cache, cache_len_ + L, n_q, n_kv, attn_);
         }
-        { prof::ScopedStage ps(PS::o_proj); linear_batched(layer.Wo, nullptr, attn_, proj_); }
-        { prof::ScopedStage ps(PS::residual_add); bt::add_inplace(h_, proj_); }
-        { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_); }
+        bool fused_o;
         {
-            prof::ScopedStage ps(PS::mlp_proj);
-            linear_batched(layer.gate_W, nullptr, norm_, gate_);
-            linear_batched(layer.up_W, nullptr, norm_, up_);
+            prof::ScopedStage ps(PS::o_proj);  // o_proj and the residual add in one launch
+            fused_o = bt::linear_residual_forward_batched(layer.Wo, attn_, h_);
+            if (!fused_o) linear_batched(layer.Wo, nullptr, attn_, proj_);
         }
+        if (!fused_o) {
+            prof::ScopedStage ps(PS::residual_add);
+            bt::add_inplace(h_, proj_);
+        }
+        { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_); }
+        bool fused_mlp;
         {
+            prof::ScopedStage ps(PS::mlp_proj);  // gate / up projections with the SwiGLU in one launch
+            fused_mlp = bt::linear_swiglu_forward_batched(layer.gate_W, layer.up_W, norm_, gate_);
+            if (!fused_mlp) {
+                linear_batched(layer.gate_W, nullptr, norm_, gate_);
+                linear_batched(layer.up_W, nullptr, norm_, up_);
+            }
+        }
+        if (!fused_mlp) {
             prof::ScopedStage ps(PS::swiglu);
             bt::silu_forward(gate_, gate_);
             bt::mul_inplace(gate_, up_);
         }
-        { prof::ScopedStage ps(PS::mlp_proj); linear_batched(layer.down_W, nullptr, gate_, proj_); }
-        { prof::ScopedStage ps(PS::residual_add); bt::add_inplace(h_, proj_); }
+        bool fused_down;
+        {
+            prof::ScopedStage ps(PS::mlp_proj);  // down and the residual add in one launch
+            fused_down = bt::linear_residual_forward_batched(layer.down_W, gate_, h_);
+            if (!fused_down) linear_batched(layer.down_W, nullptr, gate_, proj_);
+        }
+        if (!fused_down) {
+            prof::ScopedStage ps(PS::residual_add);
+            bt::add_inplace(h_, proj_);
+        }
     }
     {
         prof::ScopedStage ps(PS::final_norm);
@@ -633,17 +658,26 @@ static void stage_step(DecodeGraphSession& s, int32_t token, int32_t pos) {
     hipx::check(hipEventRecord(s.staged, hipx::stream()), "hipEventRecord");
 }
 
-static void launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
+// False when the runtime refused the cooperative launch (nothing was
+// enqueued): it does so, for one, while another process holds a context on
+// the device, since it cannot then promise that the grid is co-resident.
+static bool launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
                            const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
     if (++s.epoch >= 64) {  // a cycle of 16-bit tags is used up: re-initialize the words
         hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
         s.epoch = 1;
     }
-    hipx::bx(bx_persist_step(&s.dims, static_cast<int>(s.layers.size()), s.layers_dev,
-                             static_cast<const uint16_t*>(embed.data), static_cast<const uint16_t*>(final_norm.data),
-                             lm_head.data, static_cast<const float*>(cos.data), static_cast<const float*>(sin.data),
-                             s.scal, s.logits, s.pws, s.epoch, bt::stream()),
-             "persist step");
+    const int rc = bx_persist_step(&s.dims, static_cast<int>(s.layers.size()), s.layers_dev,
+                                   static_cast<const uint16_t*>(embed.data),
+                                   static_cast<const uint16_t*>(final_norm.data), lm_head.data,
+                                   static_cast<const float*>(cos.data), static_cast<const float*>(sin.data), s.scal,
+                                   s.logits, s.pws, s.epoch, bt::stream());
+    if (rc == BX_ELAUNCH) {
+        (void)hipGetLastError();  // the refused launch's status is not the stream's
+        return false;
+    }
+    hipx::bx(rc, "persist step");
+    return true;
 }
 
 // After the launches completed: a persistent step that gave up on a wait
@@ -666,8 +700,13 @@ static void check_persist(DecodeGraphSession& s) {
 static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, const bt::Tensor& final_norm,
                          const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
     if (s.use_persist) {
-        for (int i = 0; i < n; ++i) launch_persist(s, embed, final_norm, lm_head, cos, sin);
-        return;
+        int i = 0;
+        while (i < n && launch_persist(s, embed, final_norm, lm_head, cos, sin)) ++i;
+        if (i == n) return;
+        // refused: this session runs the per-stage graph from here on (same
+        // step, same results to the decode tolerance; decode_mode() says so)
+        s.use_persist = false;
+        n -= i;
     }
     if (s.use_graph && !s.exec) {
         hipStream_t st = hipx::stream();

@@ -153,6 +153,56 @@ void linear_forward_batched_q8_0_fp16(const Tensor& W, const Tensor* bias, const
     linear_impl("linear_forward_batched_q8_0_fp16", Dtype::Q8_0, W, bias, X, Y);
 }
 
+namespace {
+
+bool fused_ok(const Tensor& X, const Tensor& W) {
+    const bool quant_kernel = W.dtype == Dtype::FP16 || W.dtype == Dtype::Q4_K || W.dtype == Dtype::Q6_K ||
+                              W.dtype == Dtype::Q8_0;
+    return quant_kernel && W.device == Device::ROCm && X.device == Device::ROCm && X.dtype == Dtype::FP16 &&
+           X.cols == W.cols && bx_linear_tiles_ok(X.rows, X.cols) == 1;
+}
+
+}  // namespace
+
+bool linear_group_forward_batched(const Tensor* const* W, Tensor* const* Y, int n, const Tensor& X) {
+    if (n < 1 || n > 3) return false;
+    for (int i = 0; i < n; ++i)
+        if (!fused_ok(X, *W[i]) || W[i]->dtype != W[0]->dtype || Y[i]->data == X.data) return false;
+    const void* w[3];
+    uint16_t* y[3];
+    int N[3];
+    for (int i = 0; i < n; ++i) {
+        size_out(*Y[i], X.rows, W[i]->rows, Dtype::FP16);
+        w[i] = W[i]->data;
+        y[i] = static_cast<uint16_t*>(Y[i]->data);
+        N[i] = W[i]->rows;
+    }
+    hipx::bx(bx_linear_group_f16(dtype_to_ggml(W[0]->dtype), n, w, y, N, static_cast<const uint16_t*>(X.data), X.rows,
+                                 X.cols, hipx::stream()),
+             "linear_group_forward_batched");
+    return true;
+}
+
+bool linear_residual_forward_batched(const Tensor& W, const Tensor& X, Tensor& H) {
+    if (!fused_ok(X, W) || H.dtype != Dtype::FP32 || H.device != Device::ROCm || H.rows != X.rows ||
+        H.cols != W.rows)
+        return false;
+    hipx::bx(bx_linear_residual_f16(dtype_to_ggml(W.dtype), W.data, static_cast<const uint16_t*>(X.data),
+                                    static_cast<float*>(H.data), X.rows, W.rows, W.cols, hipx::stream()),
+             "linear_residual_forward_batched");
+    return true;
+}
+
+bool linear_swiglu_forward_batched(const Tensor& Wg, const Tensor& Wu, const Tensor& X, Tensor& Y) {
+    if (!fused_ok(X, Wg) || !fused_ok(X, Wu) || Wg.dtype != Wu.dtype || Wg.rows != Wu.rows || Y.data == X.data)
+        return false;
+    size_out(Y, X.rows, Wg.rows, Dtype::FP16);
+    hipx::bx(bx_linear_swiglu_f16(dtype_to_ggml(Wg.dtype), Wg.data, Wu.data, static_cast<const uint16_t*>(X.data),
+                                  static_cast<uint16_t*>(Y.data), X.rows, Wg.rows, Wg.cols, hipx::stream()),
+             "linear_swiglu_forward_batched");
+    return true;
+}
+
 void dequant_q8_0_to_fp16(const Tensor& raw, Tensor& dst) { dequant_impl("dequant_q8_0_to_fp16", Dtype::Q8_0, raw, dst); }
 void dequant_q4k_to_fp16(const Tensor& raw, Tensor& dst) { dequant_impl("dequant_q4k_to_fp16", Dtype::Q4_K, raw, dst); }
 void dequant_q6k_to_fp16(const Tensor& raw, Tensor& dst) { dequant_impl("dequant_q6k_to_fp16", Dtype::Q6_K, raw, dst); }

@@ -49,6 +49,9 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_c
 // mode; FP16 denormals are kept by the default gfx950 float mode).
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// SiLU as the elementwise kernels compute it (x / (1 + e^-x), fast exp).
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 

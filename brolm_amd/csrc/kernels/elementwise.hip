@@ -75,15 +75,14 @@ __global__ void kv_append_kernel(const uint16_t* __restrict__ k, const uint16_t*
     Vc[dst] = v[i];
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 __global__ void silu_mul_kernel(uint16_t* __restrict__ g, const uint16_t* __restrict__ u, int64_t n) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (i < n) g[i] = f2h(silu(h2f(g[i])) * h2f(u[i]));
+    if (i < n) g[i] = f2h(silu_f32(h2f(g[i])) * h2f(u[i]));
 }
 __global__ void silu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (i < n) y[i] = f2h(silu(h2f(x[i])));
+    if (i < n) y[i] = f2h(silu_f32(h2f(x[i])));
 }
 __global__ void mul_kernel(uint16_t* __restrict__ a, const uint16_t* __restrict__ b, int64_t n) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;

@@ -303,22 +303,46 @@ __device__ __forceinline__ int xcd_tile(int b, int T) {
     return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + i;
 }
 
+// What a tile launch computes.  Up to three weights share the activation
+// rows X (q / k / v): member i has N[i] output columns in Y[i], tiles_n[i]
+// column tiles; a block's tile index runs over the members' column tiles in
+// order.  EPI_STORE writes Y = f16(acc + bias); EPI_RESID adds f16(acc) to
+// the FP32 residual H[M, N[0]]; EPI_SWIGLU computes gate (W[0]) and up (W[1])
+// columns of the same tile and writes Y[0] = f16(f16(silu(f16(gate))) *
+// f16(up)), the values the separate linear, silu and mul kernels give.
+enum : int { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+struct TileJob {
+    const void* W[3];
+    uint16_t* Y[3];
+    int N[3];
+    int tiles_n[3];
+    int members;
+    int tiles_m;
+    float* H;
+};
+
 // NW wavefronts (4 or 8) as (NW/2) x 2 over the block tile.
-template <int FMT, int TBM, int TBN, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
-                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
-                                                           int M, int N, int K, int tiles_m) {
+template <int FMT, int TBM, int TBN, int NW, int EPI>
+__global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(TileJob job, const uint16_t* __restrict__ X,
+                                                           const uint16_t* __restrict__ bias, int M, int K) {
     constexpr int NT = 64 * NW, ROWS = NT / 8;  // threads; rows one loader pass covers
     constexpr int WM = TBM / (NW / 2), WN = TBN / 2;  // wave tile
     constexpr int FM = WM / 32, FN = WN / 32;         // 32x32 fragments per wave
     constexpr int RA = TBM / ROWS, RB = TBN / ROWS;   // loader rows per thread
+    // SwiGLU: B rows [0, TBN/2) are gate rows, [TBN/2, TBN) the same up rows
+    constexpr int CN = EPI == EPI_SWIGLU ? TBN / 2 : TBN;  // output columns per tile
+    static_assert(EPI != EPI_SWIGLU || RB == 2, "SwiGLU tiles take one gate and one up row per loader thread");
     __shared__ __align__(16) uint16_t As[2][TBM * TROW];
     __shared__ __align__(16) uint16_t Bs[2][TBN * TROW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tiles = tiles_m * (int)((N + TBN - 1) / TBN);
-    const int t = xcd_tile((int)blockIdx.x, tiles);
-    const int64_t m0 = (int64_t)(t % tiles_m) * TBM, n0 = (int64_t)(t / tiles_m) * TBN;
+    int tiles = 0;
+    for (int i = 0; i < job.members; ++i) tiles += job.tiles_n[i];
+    const int t = xcd_tile((int)blockIdx.x, job.tiles_m * tiles);
+    int tn = t / job.tiles_m, mem = 0;
+    while (tn >= job.tiles_n[mem]) tn -= job.tiles_n[mem++];
+    const int N = job.N[mem];
+    const int64_t m0 = (int64_t)(t % job.tiles_m) * TBM, n0 = (int64_t)tn * CN;
 
     // loaders: 8 lanes per row, 8 halves each; rows past M / N read the last
     // row (their results are not stored)
@@ -330,10 +354,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(const void* __restri
         xrow[i] = X + (m < M ? m : M - 1) * (int64_t)K;
     }
     int64_t wrow[RB];
+    const void* wsrc[RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-        const int64_t n = n0 + lrow + ROWS * i;
+        const int r = lrow + ROWS * i;
+        const int64_t n = n0 + (EPI == EPI_SWIGLU ? r % CN : r);
         wrow[i] = n < N ? n : N - 1;
+        wsrc[i] = EPI == EPI_SWIGLU ? job.W[i] : job.W[mem];
     }
     u4v ra[RA];
     RawW<FMT> rb[RB];
@@ -342,7 +369,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(const void* __restri
 #pragma unroll
         for (int i = 0; i < RA; ++i) ra[i] = ldg16(xrow[i] + k0);
 #pragma unroll
-        for (int i = 0; i < RB; ++i) rb[i] = load_w<FMT>(W, N, K, wrow[i], k0);
+        for (int i = 0; i < RB; ++i) rb[i] = load_w<FMT>(wsrc[i], N, K, wrow[i], k0);
     };
     auto lstore = [&](int buf, int kt) {
         const int k0 = (int)(((int64_t)kt * TK + lcol) % 256);
@@ -391,53 +418,115 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(const void* __restri
     }
 
     // D layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
+    if constexpr (EPI == EPI_SWIGLU) {
+        // the up wavefront (right half of the tile) hands its accumulators to
+        // the gate wavefront of the same rows through LDS (the loop's buffers
+        // are free after its last barrier)
+        float* xs = reinterpret_cast<float*>(&As[0][0]);
+        const int wm = wave >> 1;
+        if (wave & 1) {
 #pragma unroll
-    for (int g = 0; g < FN; ++g) {
-        const int64_t n = n0 + wn0 + 32 * g + (lane & 31);
-        if (n >= N) continue;
-        const float bv = bias ? h2f(bias[n]) : 0.f;
+            for (int f = 0; f < FM; ++f)
 #pragma unroll
-        for (int f = 0; f < FM; ++f)
+                for (int g = 0; g < FN; ++g)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t m = m0 + wm0 + 32 * f + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M) Y[m * N + n] = f2h(acc[f][g][r] + bv);
+                    for (int r = 0; r < 16; ++r) xs[(((wm * FM + f) * FN + g) * 16 + r) * 64 + lane] = acc[f][g][r];
+        }
+        __syncthreads();
+        if (!(wave & 1)) {
+            uint16_t* Y = job.Y[0];
+#pragma unroll
+            for (int g = 0; g < FN; ++g) {
+                const int64_t n = n0 + 32 * g + (lane & 31);
+                if (n >= N) continue;
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t m = m0 + wm0 + 32 * f + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (m >= M) continue;
+                        const float up = h2f(f2h(xs[(((wm * FM + f) * FN + g) * 16 + r) * 64 + lane]));
+                        const float act = h2f(f2h(silu_f32(h2f(f2h(acc[f][g][r])))));
+                        Y[m * N + n] = f2h(act * up);
+                    }
             }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < FN; ++g) {
+            const int64_t n = n0 + wn0 + 32 * g + (lane & 31);
+            if (n >= N) continue;
+            const float bv = (EPI == EPI_STORE && bias) ? h2f(bias[n]) : 0.f;
+#pragma unroll
+            for (int f = 0; f < FM; ++f)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t m = m0 + wm0 + 32 * f + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m >= M) continue;
+                    if constexpr (EPI == EPI_RESID) job.H[m * N + n] += h2f(f2h(acc[f][g][r]));
+                    else job.Y[mem][m * N + n] = f2h(acc[f][g][r] + bv);
+                }
+        }
     }
 }
 
-template <int FMT, int TBM, int TBN, int NW>
-int launch_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-                 hipStream_t st) {
-    const int tm = (M + TBM - 1) / TBM, tn = (N + TBN - 1) / TBN;
-    if ((int64_t)tm * tn > (1 << 30)) return fail(BX_EINVAL, "gemm: too many tiles");
-    gemm_tile_kernel<FMT, TBM, TBN, NW><<<dim3((unsigned)(tm * tn)), 64 * NW, 0, st>>>(W, X, bias, Y, M, N, K, tm);
+template <int FMT, int TBM, int TBN, int NW, int EPI>
+int launch_tiles(TileJob job, const uint16_t* bias, const uint16_t* X, int M, int K, hipStream_t st) {
+    constexpr int CN = EPI == EPI_SWIGLU ? TBN / 2 : TBN;
+    job.tiles_m = (M + TBM - 1) / TBM;
+    int64_t tiles = 0;
+    for (int i = 0; i < job.members; ++i) {
+        job.tiles_n[i] = (job.N[i] + CN - 1) / CN;
+        tiles += job.tiles_n[i];
+    }
+    tiles *= job.tiles_m;
+    if (tiles > (1 << 30)) return fail(BX_EINVAL, "gemm: too many tiles");
+    gemm_tile_kernel<FMT, TBM, TBN, NW, EPI><<<dim3((unsigned)tiles), 64 * NW, 0, st>>>(job, X, bias, M, K);
     return launch_check("gemm_tile");
 }
 
-template <int FMT>
-int gemm_tiles(const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-               hipStream_t st) {
-    // 256x128 tiles when they still give every CU a block, else 128x128
-    const int64_t big = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
-    // eight wavefronts (two per SIMD): one wave's dequantization overlaps
-    // the other's MFMAs (Q4_K 8B shapes 631-698 vs 480-555 TFLOP/s)
-    if (big >= num_cus()) return launch_tiles<FMT, 256, 128, 8>(W, bias, X, Y, M, N, K, st);
-    return launch_tiles<FMT, 128, 128, 4>(W, bias, X, Y, M, N, K, st);
+template <int FMT, int EPI>
+int gemm_tiles(const TileJob& job, const uint16_t* bias, const uint16_t* X, int M, int K, hipStream_t st) {
+    // 256x128 tiles (eight wavefronts, two per SIMD: one wave's
+    // dequantization overlaps the other's MFMAs) when they still give every
+    // CU a block, else 128x128; SwiGLU tiles always take 256 rows x 64 gate
+    // and 64 up columns
+    int64_t cols = 0;
+    for (int i = 0; i < job.members; ++i) cols += (job.N[i] + 127) / 128;
+    const int64_t big = (int64_t)((M + 255) / 256) * cols;
+    if constexpr (EPI == EPI_SWIGLU) {
+        return launch_tiles<FMT, 256, 128, 8, EPI>(job, bias, X, M, K, st);
+    } else {
+        if (big >= num_cus()) return launch_tiles<FMT, 256, 128, 8, EPI>(job, bias, X, M, K, st);
+        return launch_tiles<FMT, 128, 128, 4, EPI>(job, bias, X, M, K, st);
+    }
+}
+
+template <int EPI>
+int gemm_tiles_typed(int wtype, const TileJob& job, const uint16_t* bias, const uint16_t* X, int M, int K,
+                     hipStream_t st) {
+    switch (wtype) {
+        case BX_TYPE_Q4_K: return gemm_tiles<BX_TYPE_Q4_K, EPI>(job, bias, X, M, K, st);
+        case BX_TYPE_Q6_K: return gemm_tiles<BX_TYPE_Q6_K, EPI>(job, bias, X, M, K, st);
+        case BX_TYPE_Q8_0: return gemm_tiles<BX_TYPE_Q8_0, EPI>(job, bias, X, M, K, st);
+        case BX_TYPE_F16: return gemm_tiles<BX_TYPE_F16, EPI>(job, bias, X, M, K, st);
+        default: return fail(BX_EUNSUPPORTED, "gemm: unsupported type");
+    }
 }
 
 }  // namespace
 
+bool gemm_tiles_ok(int M, int K);
+
 int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st) {
-    if (M >= 128 && K % TK == 0) {
-        switch (wtype) {
-            case BX_TYPE_Q4_K: return gemm_tiles<BX_TYPE_Q4_K>(W, bias, X, Y, M, N, K, st);
-            case BX_TYPE_Q6_K: return gemm_tiles<BX_TYPE_Q6_K>(W, bias, X, Y, M, N, K, st);
-            case BX_TYPE_Q8_0: return gemm_tiles<BX_TYPE_Q8_0>(W, bias, X, Y, M, N, K, st);
-            case BX_TYPE_F16: return gemm_tiles<BX_TYPE_F16>(W, bias, X, Y, M, N, K, st);
-            default: return fail(BX_EUNSUPPORTED, "gemm: unsupported type");
-        }
+    if (gemm_tiles_ok(M, K)) {
+        TileJob job{};
+        job.W[0] = W;
+        job.Y[0] = Y;
+        job.N[0] = N;
+        job.members = 1;
+        return gemm_tiles_typed<EPI_STORE>(wtype, job, bias, X, M, K, st);
     }
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
     if (grid.y > 65535) return fail(BX_EINVAL, "gemm: M too large");
@@ -449,6 +538,40 @@ int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
         default: return fail(BX_EUNSUPPORTED, "gemm: unsupported type");
     }
     return launch_check("gemm");
+}
+
+bool gemm_tiles_ok(int M, int K) { return M >= 128 && K % TK == 0; }
+
+int gemm_group_f16(int wtype, int members, const void* const* W, uint16_t* const* Y, const int* N,
+                   const uint16_t* X, int M, int K, hipStream_t st) {
+    TileJob job{};
+    job.members = members;
+    for (int i = 0; i < members; ++i) {
+        job.W[i] = W[i];
+        job.Y[i] = Y[i];
+        job.N[i] = N[i];
+    }
+    return gemm_tiles_typed<EPI_STORE>(wtype, job, nullptr, X, M, K, st);
+}
+
+int gemm_resid_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st) {
+    TileJob job{};
+    job.W[0] = W;
+    job.N[0] = N;
+    job.members = 1;
+    job.H = H;
+    return gemm_tiles_typed<EPI_RESID>(wtype, job, nullptr, X, M, K, st);
+}
+
+int gemm_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
+                    hipStream_t st) {
+    TileJob job{};
+    job.W[0] = Wg;
+    job.W[1] = Wu;
+    job.Y[0] = Y;
+    job.N[0] = F;
+    job.members = 1;
+    return gemm_tiles_typed<EPI_SWIGLU>(wtype, job, nullptr, X, M, K, st);
 }
 
 }  // namespace bx

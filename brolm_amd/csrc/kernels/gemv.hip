@@ -8,6 +8,12 @@
 
 namespace bx {
 
+bool gemm_tiles_ok(int M, int K);
+int gemm_group_f16(int wtype, int members, const void* const* W, uint16_t* const* Y, const int* N,
+                   const uint16_t* X, int M, int K, hipStream_t st);
+int gemm_resid_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st);
+int gemm_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
+                    hipStream_t st);
 int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st);
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
@@ -202,4 +208,33 @@ extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, con
     // kernels' staged activations outgrow LDS, the tiled GEMM does not
     if (M == 1 || (M <= 16 && K <= 12288)) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
     return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
+}
+
+extern "C" int bx_linear_tiles_ok(int M, int K) { return bx::gemm_tiles_ok(M, K) ? 1 : 0; }
+
+extern "C" int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N,
+                                   const uint16_t* X, int M, int K, void* stream) {
+    if (n < 1 || n > 3 || !W || !Y || !N || !X) return bx::fail(BX_EINVAL, "linear_group: bad arguments");
+    for (int i = 0; i < n; ++i) {
+        if (int rc = bx::check_linear_shape(wtype, M, N[i], K)) return rc;
+        if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group: null pointer");
+    }
+    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_group: needs M >= 128, K % 64 == 0");
+    return bx::gemm_group_f16(wtype, n, W, Y, N, X, M, K, bx::as_stream(stream));
+}
+
+extern "C" int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K,
+                                      void* stream) {
+    if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
+    if (!W || !X || !H) return bx::fail(BX_EINVAL, "linear_residual: null pointer");
+    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_residual: needs M >= 128, K % 64 == 0");
+    return bx::gemm_resid_f16(wtype, W, X, H, M, N, K, bx::as_stream(stream));
+}
+
+extern "C" int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M,
+                                    int F, int K, void* stream) {
+    if (int rc = bx::check_linear_shape(wtype, M, F, K)) return rc;
+    if (!Wg || !Wu || !X || !Y) return bx::fail(BX_EINVAL, "linear_swiglu: null pointer");
+    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_swiglu: needs M >= 128, K % 64 == 0");
+    return bx::gemm_swiglu_f16(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
 }

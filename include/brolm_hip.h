@@ -78,6 +78,23 @@ int bx_dequant_to_f32(int type, const void* carrier, float* dst, int64_t rows, i
 int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y,
                   int M, int N, int K, void* stream);
 
+/* Fused prefill forms of the linears of src/detail/dense_decoder.cpp:526-681
+ * (the op sequence linear / silu / mul / add_inplace, with the same
+ * roundings).  They take the MFMA tile path only: 1 when (M, K) qualify
+ * (M >= 128, K a multiple of 64), else 0 and the caller runs the unfused ops.
+ * bx_linear_group_f16: n (1..3) weights of one type sharing X (q / k / v
+ *   projections), Y[i] (M, N[i]) FP16, one launch.
+ * bx_linear_residual_f16: H (M, N) FP32 += f16(X W^T) (o / down projection
+ *   and the residual add).
+ * bx_linear_swiglu_f16: Y (M, F) = f16(f16(silu(f16(X Wg^T))) * f16(X Wu^T))
+ *   (gate / up projections, silu, mul). */
+int bx_linear_tiles_ok(int M, int K);
+int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
+                        int M, int K, void* stream);
+int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* stream);
+int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F,
+                         int K, void* stream);
+
 /* ------------------------------------------------------------- elementwise */
 
 /* K7: embedding_lookup_forward(W, idx_dev, L, out) (dense_decoder.cpp:259-261).

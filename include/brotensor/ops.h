@@ -23,6 +23,17 @@ void linear_forward_batched_q4k_fp16(const Tensor& W, const Tensor* bias, const 
 void linear_forward_batched_q6k_fp16(const Tensor& W, const Tensor* bias, const Tensor& X, Tensor& Y);
 void linear_forward_batched_q8_0_fp16(const Tensor& W, const Tensor* bias, const Tensor& X, Tensor& Y);
 
+// Fused prefill linears (MFMA tile path only).  Each returns false, having
+// done nothing, when the shapes or dtypes do not qualify (fewer than 128 rows,
+// K not a multiple of 64, mixed weight dtypes, a dtype without a quant
+// kernel): the caller then runs the unfused ops, which give the same values.
+//   linear_group_forward_batched:    Y[i] = X . W[i]^T, 1..3 weights of one dtype
+//   linear_residual_forward_batched: H (FP32) += fp16(X . W^T)
+//   linear_swiglu_forward_batched:   Y = fp16(fp16(silu(fp16(X . Wg^T))) * fp16(X . Wu^T))
+bool linear_group_forward_batched(const Tensor* const* W, Tensor* const* Y, int n, const Tensor& X);
+bool linear_residual_forward_batched(const Tensor& W, const Tensor& X, Tensor& H);
+bool linear_swiglu_forward_batched(const Tensor& Wg, const Tensor& Wu, const Tensor& X, Tensor& Y);
+
 // K6: quant carrier -> FP16 tensor of the same (rows, cols).
 void dequant_q8_0_to_fp16(const Tensor& raw, Tensor& dst);
 void dequant_q4k_to_fp16(const Tensor& raw, Tensor& dst);

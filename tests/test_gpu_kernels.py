@@ -130,6 +130,60 @@ def test_linear_big_tiles_vs_oracle(t, N, K):
         assert np.all(np.abs(got - ref) <= tol), (M, float((np.abs(got - ref) / tol).max()))
 
 
+def _weights(rng, t, N, K):
+    if t == 1:
+        Wv = _f16(rng.standard_normal((N, K)) * 0.05)
+        return f16_dev(Wv), Wv
+    raw, Wv = sb.random_matrix(rng, t, N, K)
+    return carrier(t, raw, N, K), Wv
+
+
+@pytest.mark.parametrize("t", QTYPES + [1])
+def test_fused_prefill_linears_equal_unfused_ops(t):
+    """bx_linear_group / _residual / _swiglu give bit-identical results to the
+    separate linear, add_inplace, silu and mul launches they replace (same
+    MFMA tile arithmetic, same FP16 roundings); below 128 rows they decline."""
+    rng = np.random.default_rng(900 + t)
+    M, K = 300, 512
+    Ns = (384, 128, 128)
+    ws = [_weights(rng, t, n, K)[0] for n in Ns]
+    X = _f16(rng.standard_normal((M, K)))
+    x = f16_dev(X)
+    h = hip()
+    # q / k / v group vs three linears
+    ys = [torch().empty(M * n, dtype=torch().int16, device="cuda") for n in Ns]
+    W_arr = (C.c_void_p * 3)(*[ptr(w) for w in ws])
+    Y_arr = (C.c_void_p * 3)(*[ptr(y) for y in ys])
+    N_arr = (C.c_int * 3)(*Ns)
+    call("bx_linear_group_f16", t, 3, W_arr, Y_arr, N_arr, ptr(x), M, K, stream())
+    for w, y, n in zip(ws, ys, Ns):
+        ref = torch().empty(M * n, dtype=torch().int16, device="cuda")
+        call("bx_linear_f16", t, ptr(w), None, ptr(x), ptr(ref), M, n, K, stream())
+        assert np.array_equal(host(y), host(ref))
+    # residual: H (FP32) += f16(X W^T)
+    H0 = rng.standard_normal((M, Ns[0])).astype(np.float32)
+    Hf = dev(H0)
+    call("bx_linear_residual_f16", t, ptr(ws[0]), ptr(x), ptr(Hf), M, Ns[0], K, stream())
+    Hr = dev(H0)
+    proj = torch().empty(M * Ns[0], dtype=torch().int16, device="cuda")
+    call("bx_linear_f16", t, ptr(ws[0]), None, ptr(x), ptr(proj), M, Ns[0], K, stream())
+    call("bx_add_inplace", ptr(Hr), 1, ptr(proj), M * Ns[0], stream())
+    assert np.array_equal(host(Hf).view(np.uint32), host(Hr).view(np.uint32))
+    # SwiGLU: gate = ws[1], up = ws[2] (same shape)
+    act = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
+    call("bx_linear_swiglu_f16", t, ptr(ws[1]), ptr(ws[2]), ptr(x), ptr(act), M, Ns[1], K, stream())
+    g = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
+    u = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
+    call("bx_linear_f16", t, ptr(ws[1]), None, ptr(x), ptr(g), M, Ns[1], K, stream())
+    call("bx_linear_f16", t, ptr(ws[2]), None, ptr(x), ptr(u), M, Ns[1], K, stream())
+    call("bx_silu_f16", ptr(g), ptr(g), M * Ns[1], stream())
+    call("bx_mul_f16", ptr(g), ptr(u), M * Ns[1], stream())
+    assert np.array_equal(host(act), host(g))
+    # below the tile path: declined, nothing written
+    assert h.bx_linear_tiles_ok(100, K) == 0 and h.bx_linear_tiles_ok(M, K) == 1
+    assert h.bx_linear_residual_f16(t, ptr(ws[0]), ptr(x), ptr(Hf), 100, Ns[0], K, stream()) == -3  # BX_EUNSUPPORTED
+
+
 @pytest.mark.parametrize("t", QTYPES)
 def test_linear_ffn_width_k(t):
     """K = 32768 (Mistral-Small-3.1's FFN width, the down projection): the
