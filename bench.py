@@ -170,6 +170,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time the prompt prefill only and print its throughput (for hardware-counter runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a reference dispatch of known bytes for "
                          "hardware-counter runs)")
@@ -222,6 +224,13 @@ def main() -> int:
     logits = model.forward_last(prompt)
     prefill_s = min(prefill_s, time.perf_counter() - t0)
     log(f"prefill {c['prompt']} tokens: {prefill_s * 1e3:.1f} ms")
+    if args.prefill_only:
+        model.close()
+        ba.shutdown()
+        print(json.dumps({"metric": f"prefill tok/s {args.config}", "value": round(c["prompt"] / prefill_s, 1),
+                          "unit": "tok/s", "prompt_tokens": c["prompt"], "ms": round(prefill_s * 1e3, 3),
+                          "data": "synthetic"}), flush=True)
+        return 0
     # bidirectional encode (DenseDecoder::forward_encode, the LLM2Vec pass) of
     # the first 512 prompt tokens; the KV cache is not touched
     n_enc = min(512, len(prompt))
