@@ -86,6 +86,8 @@ def lib():
             "or_model_weight": (P_f32, [C.c_void_p, C.c_int, C.c_char_p, C.POINTER(C.c_int64),
                                         C.POINTER(C.c_int64)]),
             "or_argmax": (C.c_int, [P_f32, C.c_int, P_f32]),
+            "or_sample_token": (C.c_int, [P_f32, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double,
+                                          C.POINTER(C.c_double)]),
             "or_generate_greedy": (C.c_int, [C.c_void_p, P_i32, C.c_int, C.c_int, C.c_int, P_i32, P_f32]),
             "or_num_threads": (C.c_int, []),
         }
@@ -167,6 +169,15 @@ def argmax(logits: np.ndarray) -> tuple[int, float]:
     m = C.c_float()
     i = lib().or_argmax(_f32p(a), a.size, C.byref(m))
     return i, m.value
+
+
+def sample_token(logits: np.ndarray, temperature: float, top_k: int, top_p: float, u: float) -> tuple[int, float]:
+    """sample_token (src/detail/generate.cpp:68-142) with the uniform draw u;
+    returns (token, margin of u to the chosen interval's ends / kept mass)."""
+    a = np.ascontiguousarray(logits, np.float32)
+    m = C.c_double()
+    t = lib().or_sample_token(_f32p(a), a.size, temperature, top_k, top_p, u, C.byref(m))
+    return t, m.value
 
 
 class Gguf:

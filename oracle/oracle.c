@@ -983,6 +983,91 @@ int or_argmax(const float* logits, int vocab, float* margin) {
     return best;
 }
 
+/* sample_token (src/detail/generate.cpp:68-142) with the uniform draw u in
+ * [0, 1) supplied by the caller (the reference draws it from
+ * uniform_real_distribution<double>(0, 1) over its std::mt19937_64):
+ *   greedy (T <= 0 or top_k == 1): the strict-'>' argmax;
+ *   p_i = float(exp(float(l_i * (1/T)) - max)) * float(1 / sum), sum in double;
+ *   order = indices by descending p; equal p keep ascending index (the
+ *     reference's std::sort leaves that order unspecified);
+ *   keep = top_k, then the shortest prefix whose running double sum reaches
+ *     top_p (at least 1); r = u * (double sum of the kept p);
+ *   the first kept index whose running sum exceeds r, else the last kept.
+ * margin (optional): distance of r to the nearer end of the chosen token's
+ * interval, as a fraction of the kept mass (0 for greedy). */
+static const float* g_sort_p;
+static int cmp_desc_p(const void* a, const void* b) {
+    const int i = *(const int*)a, j = *(const int*)b;
+    const float pi = g_sort_p[i], pj = g_sort_p[j];
+    if (pi > pj) return -1;
+    if (pi < pj) return 1;
+    return (i > j) - (i < j);
+}
+int or_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, double u,
+                    double* margin) {
+    if (margin) *margin = 0.0;
+    if (vocab <= 0) return 0;
+    if (temperature <= 0.0f || top_k == 1) return or_argmax(logits, vocab, NULL);
+    const float inv_t = 1.0f / temperature;
+    float mx = logits[0] * inv_t;
+    for (int i = 1; i < vocab; ++i) {
+        const float x = logits[i] * inv_t;
+        if (x > mx) mx = x;
+    }
+    float* p = (float*)malloc(sizeof(float) * (size_t)vocab);
+    int* order = (int*)malloc(sizeof(int) * (size_t)vocab);
+    double sum = 0.0;
+    for (int i = 0; i < vocab; ++i) {
+        p[i] = expf(logits[i] * inv_t - mx);
+        sum += p[i];
+    }
+    const float norm = sum > 0.0 ? (float)(1.0 / sum) : 0.0f;
+    for (int i = 0; i < vocab; ++i) {
+        p[i] *= norm;
+        order[i] = i;
+    }
+    g_sort_p = p;
+    qsort(order, (size_t)vocab, sizeof(int), cmp_desc_p);
+    int keep = vocab;
+    if (top_k > 0 && top_k < keep) keep = top_k;
+    if (top_p < 1.0f) {
+        double cum = 0.0;
+        int nucleus = 0;
+        for (int i = 0; i < keep; ++i) {
+            cum += p[order[i]];
+            ++nucleus;
+            if (cum >= (double)top_p) break;
+        }
+        keep = nucleus > 1 ? nucleus : 1;
+    }
+    double kept = 0.0;
+    for (int i = 0; i < keep; ++i) kept += p[order[i]];
+    int tok = order[0];
+    if (kept > 0.0) {
+        const double r = u * kept;
+        double acc = 0.0, lo = 0.0;
+        tok = order[keep - 1];
+        int found = 0;
+        for (int i = 0; i < keep; ++i) {
+            lo = acc;
+            acc += p[order[i]];
+            if (r < acc) {
+                tok = order[i];
+                found = 1;
+                break;
+            }
+        }
+        if (margin) {
+            const double a = found ? r - lo : r - (acc - p[order[keep - 1]]);
+            const double b = found ? acc - r : 0.0;
+            *margin = (a < b ? a : b) / kept;
+        }
+    }
+    free(p);
+    free(order);
+    return tok;
+}
+
 /* generate (include/brolm/detail/generate.h:78-123), greedy sampling. */
 int or_generate_greedy(or_model* m, const int32_t* prompt, int n_prompt, int max_new, int eos_id, int32_t* out,
                        float* margins) {

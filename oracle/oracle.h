@@ -19,6 +19,10 @@
  *     :196-227, forward/forward_last :242-294.
  *   - Greedy argmax with lowest-index ties (src/detail/generate.cpp:38-48)
  *     and the generate loop (include/brolm/detail/generate.h:78-123).
+ *   - Temperature / top-k / top-p sampling (src/detail/generate.cpp:68-142)
+ *     given the uniform draw; pinned by exhaustive draws over tiny
+ *     vocabularies against the kept set and renormalised probabilities the
+ *     definition fixes (tests/test_sampling.py).
  *
  * Parity status per function (how each is pinned) is stated beside it.
  */
@@ -114,6 +118,11 @@ const float* or_model_weight(const or_model* m, int layer, const char* which, in
 
 /* greedy argmax, lowest index wins ties; margin = top1 - top2 (optional) */
 int or_argmax(const float* logits, int vocab, float* margin);
+/* sample_token (src/detail/generate.cpp:68-142) given the uniform draw u in
+ * [0, 1); equal probabilities in ascending index order; margin (optional):
+ * the draw's distance to the chosen interval's nearer end / kept mass */
+int or_sample_token(const float* logits, int vocab, float temperature, int top_k, float top_p, double u,
+                    double* margin);
 /* generate: prefill prompt, then decode; writes <= max_new ids; returns count.
  * margins (optional, max_new floats) receives the top-2 gap at each step. */
 int or_generate_greedy(or_model* m, const int32_t* prompt, int n_prompt, int max_new,

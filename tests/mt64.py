@@ -1,7 +1,7 @@
 """std::mt19937_64 and libstdc++'s uniform_real_distribution<double>(0, 1)
 first draw, written from the published MT19937-64 parameters (Matsumoto &
 Nishimura) for the sampling tests.  Pinned by the C++ standard's required
-10000th output of a default-seeded engine (tests/test_sampling.py)."""
+10000th output of a default-seeded engine (tests/test_mt64.py)."""
 from __future__ import annotations
 
 _M = (1 << 64) - 1

@@ -1,7 +1,14 @@
 """Device top-k / top-p sampling (bx_sample_f16 through
-brolm_sample_token_device) against the host sampler brolm_sample_token, the
-reference's algorithm (src/detail/generate.cpp:68-142), on the same FP16
-logits and the same std::mt19937_64 draw."""
+brolm_sample_token_device) against the oracle's sampler (the reference's
+sample_token, src/detail/generate.cpp:68-142) on the same FP16 logits and the
+same std::mt19937_64 draw.
+
+Criterion: the device id equals the oracle's, except (a) an id of equal
+logit (the reference's std::sort leaves the order of equal probabilities
+unspecified) or (b) a draw within 1e-5 of the kept mass from the boundary of
+the oracle's interval (FP32 / FP64 summation order moves boundaries by ~1e-7);
+(b) is counted and printed.  Logits are distinct where the top-k / top-p cut
+falls, so the device's keep-all-ties rule at the cut never applies."""
 from __future__ import annotations
 
 import ctypes as C
@@ -9,6 +16,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+import oracle
 from mt64 import first_uniform
 
 pytestmark = pytest.mark.gpu
@@ -23,53 +31,48 @@ def env():
     return torch, _native
 
 
-def _boundary_ok(lg32, T, k, p, u, a, b):
-    """True when the host and device ids differ only because the draw lies
-    within rounding distance of the cumulative boundary between them."""
-    x = lg32.astype(np.float64) / T
-    e = np.exp(x - x.max())
-    pr = e / e.sum()
-    order = np.argsort(-pr, kind="stable")
-    keep = len(pr) if k <= 0 or k >= len(pr) else k
-    if p < 1.0:
-        c = np.cumsum(pr[order[:keep]])
-        keep = max(1, int(np.searchsorted(c, p) + 1))
-    cum = np.cumsum(pr[order[:keep]])
-    r = u * cum[-1]
-    ia, ib = np.where(order == a)[0], np.where(order == b)[0]
-    if not len(ia) or not len(ib):
-        return bool(pr[a] == pr[b])
-    lo = min(ia[0], ib[0])
-    return abs(cum[lo] - r) < 1e-5 * cum[-1] or pr[a] == pr[b]
+def _distinct_fp16(rng, n, lo, hi):
+    """n distinct FP16 values in [lo, hi), shuffled."""
+    cand = np.unique(rng.uniform(lo, hi, 8 * n).astype(np.float16))
+    assert cand.size >= n
+    return rng.permutation(cand)[:n]
 
 
 @pytest.mark.parametrize("V", [1000, 151936])
-def test_device_sampler_matches_host(env, V):
+def test_device_sampler_matches_oracle(env, V):
     torch, nat = env
     lib = nat.lib()
     rng = np.random.default_rng(V)
     cases = [(1.0, 0, 1.0), (0.7, 50, 1.0), (1.0, 0, 0.9), (1.3, 40, 0.8), (0.5, 5, 0.5), (1.0, 0, 0.01),
              (2.0, 1000, 0.95)]
-    mism = 0
-    total = 0
+    near = total = 0
     for scale in (0.5, 3.0, 8.0):
-        lg16 = (rng.standard_normal(V) * scale).astype(np.float16)
+        if V <= 2000:
+            lg16 = _distinct_fp16(rng, V, -scale * 3, scale * 3)
+        else:
+            # the top 4000 distinct (every cut above falls among them), the
+            # rest below them, FP16 ties allowed there
+            lg16 = np.empty(V, np.float16)
+            top = rng.choice(V, 4000, replace=False)
+            rest = np.setdiff1d(np.arange(V), top)
+            bits = rng.choice(np.arange(0x3C00, 0x4C40, dtype=np.uint16), 4000, replace=False)  # [1, 17)
+            lg16[top] = bits.view(np.float16)
+            lg16[rest] = np.minimum(rng.uniform(-scale * 3, 0.99, rest.size), 0.99).astype(np.float16)
         lg32 = lg16.astype(np.float32)
         dev = torch.from_numpy(lg16.view(np.uint16).astype(np.int16)).cuda()
         for T, k, p in cases:
             for seed in range(6):
                 print(f"[sample] V={V} scale={scale} T={T} k={k} p={p} seed={seed}", flush=True)
-                host = lib.brolm_sample_token(lg32.ctypes.data_as(nat.P_f32), V, T, k, p, seed)
+                want, margin = oracle.sample_token(lg32, T, k, p, first_uniform(seed))
                 got = lib.brolm_sample_token_device(C.c_void_p(dev.data_ptr()), V, T, k, p, seed)
                 assert got >= 0, nat.lib().brolm_last_error()
                 total += 1
-                # equal logits are equal probabilities: the reference's
-                # std::sort leaves their order unspecified, so either id is
-                # its answer; any other difference must sit on a boundary
-                if got != host and lg32[got] != lg32[host]:
-                    mism += 1
-                    assert _boundary_ok(lg32, T, k, p, first_uniform(seed), host, got), (T, k, p, seed, host, got)
-    assert mism <= total // 20
+                if got == want or lg32[got] == lg32[want]:
+                    continue
+                assert margin < 1e-5, (T, k, p, seed, want, got, margin)
+                near += 1
+    print(f"[sample] V={V}: {total} draws, {near} within 1e-5 of an interval boundary", flush=True)
+    assert near <= 2
 
 
 def test_sampled_generation_on_device_matches_host(env, small_gguf):
