@@ -2,10 +2,19 @@
 
 Weight matrices [N, K] in {(3072,1024), (1024,3072), (6144,2048), (2048,6144),
 (151936,2048)} x {Q8_0, Q4_K, Q6_K}, FP16 activations N(0,1), batch
-M in {1,2,4,8,16}.  Each timed batch rotates over enough distinct weight
-copies (> 2 GB) that the 256 MB Infinity Cache cannot serve repeats; the
-launch time is the median over >= 100 launches (HIP events on the launch
-stream).  GB/s counts the carrier bytes + M*(K+N)*2 activation bytes.
+M in {1,2,4,8,16}.  Each timed batch rotates over distinct weight copies
+totalling about --rotate-gb (2.5 GB: ten times the 256 MB Infinity Cache, so
+repeats come from HBM; a row whose rotation stays under 512 MB says
+"cache_resident").  Two timings per case:
+  us        median of 100 launches, HIP events around each launch (includes
+            the GPU-side dispatch gap, so small matrices read launch-bound);
+  us_batch  100 back-to-back launches between two events / 100 (dispatch
+            overlapped, the kernels' own throughput).
+GB/s counts the carrier bytes + M*(K+N)*2 activation bytes.  The comparison
+leg "ref_fp32_us" is the reference's FP32 route for a quantized weight
+(include/brolm/detail/compute.h:77-85: dequantize to FP32, then an FP32
+GEMM; here bx_dequant_to_f32 then torch.matmul in FP32) on the same case.
+The first line printed is the measured device-copy bandwidth.
 
 Device memory comes from torch (plumbing only); every GEMV runs through the
 C ABI bx_linear_f16 of libbrolm_hip.so.
@@ -79,9 +88,41 @@ def time_case(torch, t: str, n: int, k: int, m: int, weights, reps: int = 100) -
     torch.cuda.synchronize()
     times = [a.elapsed_time(b) * 1e3 for a, b in evs]  # us
     med = statistics.median(times)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(reps):
+        launch(weights[i % len(weights)])
+    e1.record(st)
+    torch.cuda.synchronize()
+    batch = e0.elapsed_time(e1) * 1e3 / reps
     byts = carrier_bytes(t, n, k) + m * (k + n) * 2
     return {"type": t, "N": n, "K": k, "M": m, "us": round(med, 3), "GBps": round(byts / (med * 1e-6) / 1e9, 1),
-            "frac": round(byts / (med * 1e-6) / 1e9 / HBM_PEAK, 4), "bytes": byts}
+            "frac": round(byts / (med * 1e-6) / 1e9 / HBM_PEAK, 4), "us_batch": round(batch, 3),
+            "GBps_batch": round(byts / (batch * 1e-6) / 1e9, 1), "bytes": byts}
+
+
+def time_ref_fp32(torch, t: str, n: int, k: int, m: int, w, reps: int = 20) -> float:
+    """Dequantize the carrier to FP32, then X (M, K) @ W^T in FP32: the route
+    the reference takes for a weight dtype without a quant kernel."""
+    hip = _native.hip()
+    st = torch.cuda.current_stream()
+    x = torch.randn(m, k, device="cuda", dtype=torch.float32)
+    wf = torch.empty(n, k, device="cuda", dtype=torch.float32)
+
+    def run():
+        _native.bx_check(hip.bx_dequant_to_f32(GGML[t], C.c_void_p(w.data_ptr()), C.c_void_p(wf.data_ptr()), n, k,
+                                               C.c_void_p(st.cuda_stream)), "dequant")
+        return x @ wf.t()
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        run()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
 
 
 def main(argv=None) -> int:
@@ -91,19 +132,38 @@ def main(argv=None) -> int:
     ap.add_argument("--ms", default=",".join(map(str, MS)))
     ap.add_argument("--rotate-gb", type=float, default=2.5)
     ap.add_argument("--json", default=None)
+    ap.add_argument("--no-ref", action="store_true", help="skip the dequant + FP32 GEMM comparison leg")
     a = ap.parse_args(argv)
     import torch
+
+    src = torch.empty(2 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"stream_copy_GBps": round(2.0 * src.numel() * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)}),
+          flush=True)
+    del src, dst
+    torch.cuda.empty_cache()
 
     shapes = [tuple(int(v) for v in s.split("x")) for s in a.shapes.split(",")]
     rows = []
     for t in a.types.split(","):
         for n, k in shapes:
             nb = carrier_bytes(t, n, k)
-            copies = max(2, min(64, int(a.rotate_gb * 1e9 // nb) + 1))
+            copies = max(2, min(4096, int(a.rotate_gb * 1e9 // nb) + 1))
             ws = make_weights(torch, t, n, k, copies, seed=n * 7 + k)
             for m in [int(v) for v in a.ms.split(",")]:
                 r = time_case(torch, t, n, k, m, ws)
                 r["copies"] = copies
+                r["cache_resident"] = copies * nb < 512e6
+                if not a.no_ref:
+                    r["ref_fp32_us"] = round(time_ref_fp32(torch, t, n, k, m, ws[0]), 3)
                 rows.append(r)
                 print(json.dumps(r), flush=True)
             del ws

@@ -81,6 +81,7 @@ def lib():
             "or_model_reset_cache": (None, [C.c_void_p]),
             "or_model_truncate_cache": (C.c_int, [C.c_void_p, C.c_int]),
             "or_model_cache_len": (C.c_int, [C.c_void_p]),
+            "or_model_fill_cache": (C.c_int, [C.c_void_p, C.c_int, C.c_uint64]),
             "or_model_forward": (C.c_int, [C.c_void_p, P_i32, C.c_int, C.c_int, P_f32, P_f32]),
             "or_model_forward_encode": (C.c_int, [C.c_void_p, P_i32, C.c_int, P_f32]),
             "or_model_weight": (P_f32, [C.c_void_p, C.c_int, C.c_char_p, C.POINTER(C.c_int64),
@@ -250,6 +251,11 @@ class Model:
     def truncate_cache(self, n: int) -> None:
         if lib().or_model_truncate_cache(self._h, n) != 0:
             raise ValueError("truncate_cache")
+
+    def fill_cache(self, n: int, seed: int = 1) -> None:
+        """Benchmark helper: deterministic K / V rows [0, n), cache_len = n."""
+        if lib().or_model_fill_cache(self._h, n, seed) != 0:
+            raise ValueError("fill_cache")
 
     def cache_len(self) -> int:
         return lib().or_model_cache_len(self._h)

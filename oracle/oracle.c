@@ -821,6 +821,25 @@ int or_model_allocate_cache(or_model* m, int max_seq_len) {
     return 0;
 }
 void or_model_reset_cache(or_model* m) { m->cache_len = 0; }
+/* Benchmark helper: K / V rows [0, len) of every layer get deterministic
+ * values in [-1, 1) (an xorshift stream from seed) and cache_len = len, so a
+ * decode timing runs at the context of a long prompt without its prefill. */
+int or_model_fill_cache(or_model* m, int len, uint64_t seed) {
+    if (len < 0 || len > m->max_seq) return -1;
+    const size_t kvd = (size_t)m->c.num_key_value_heads * m->c.head_dim;
+    uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (int l = 0; l < m->c.num_hidden_layers; ++l) {
+        or_layer* L = &m->layers[l];
+        for (size_t i = 0; i < (size_t)len * kvd; ++i) {
+            x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+            L->Kc[i] = (float)((int64_t)(x >> 40) - (1 << 23)) / (float)(1 << 23);
+            x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+            L->Vc[i] = (float)((int64_t)(x >> 40) - (1 << 23)) / (float)(1 << 23);
+        }
+    }
+    m->cache_len = len;
+    return 0;
+}
 int or_model_truncate_cache(or_model* m, int len) {
     if (len < 0 || len > m->cache_len) return -1;
     m->cache_len = len;

@@ -107,6 +107,8 @@ void      or_model_config(const or_model* m, or_config* out);
 int       or_model_allocate_cache(or_model* m, int max_seq_len);
 void      or_model_reset_cache(or_model* m);
 int       or_model_truncate_cache(or_model* m, int len);
+/* bench helper: K / V rows [0, len) filled with deterministic values, cache_len = len */
+int       or_model_fill_cache(or_model* m, int len, uint64_t seed);
 int       or_model_cache_len(const or_model* m);
 /* logits: (L, V) or (1, V) when last_only; hidden (optional): (L, H) post-final-norm */
 int       or_model_forward(or_model* m, const int32_t* ids, int L, int last_only,
