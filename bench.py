@@ -309,6 +309,25 @@ def main() -> int:
     if not mistral:
         tokenizer = text_path(ba, path, model, prompt)
 
+    # multi-sequence batched decode: M sequences, each holding the prompt in
+    # its own KV slot, stepped together (one weight pass per M tokens)
+    batched = {}
+    n_b = 32
+    model.allocate_batch(16, len(prompt) + n_b + 8)
+    for s in range(16):
+        model.prefill_slot(s, prompt)
+    for M in (4, 16):
+        slots = list(range(M))
+        ids = [first] * M
+        model.time_forward_batch(ids, slots, 4)
+        for s in slots:
+            model.truncate_slot(s, len(prompt))
+        ms = model.time_forward_batch(ids, slots, n_b)
+        batched[str(M)] = round(M * 1e3 / ms, 1)
+        for s in slots:
+            model.truncate_slot(s, len(prompt))
+    log(f"batched decode tok/s: {batched}")
+
     import torch
 
     copy_gbs = stream_copy_gbs(torch)
@@ -350,6 +369,9 @@ def main() -> int:
         "sampled_note": "generate, 64 tokens, T 0.8 / top-k 40 / top-p 0.95: device sampler vs host sampler",
         "encode_note": f"forward_encode of {n_enc} tokens (bidirectional, cacheless, hidden states downloaded)",
         "ref_loop_tok_s": round(ref_tok_s, 2),
+        "batched_decode_tok_s": batched,
+        "batched_decode_note": (f"forward_batch over M sequences of {len(prompt)}-token context each, {n_b} "
+                                "steps, wall clock, logits left on the device; key = M"),
         "tokenizer": tokenizer,
     }
     # every device buffer and the op stream go before the process exit path (a

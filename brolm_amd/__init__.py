@@ -190,6 +190,48 @@ class Qwen3Model:
             raise _native.NativeError(_native.lib().brolm_last_error().decode())
         return ms
 
+    # -- multi-sequence batched decode (beyond the reference's one-sequence model)
+    def allocate_batch(self, n_slots: int, max_seq_len: int) -> None:
+        """n_slots independent sequences, each with its own KV rows."""
+        check(_native.lib().brolm_qwen3_allocate_batch(self._h, int(n_slots), int(max_seq_len)), "allocate_batch")
+
+    def slot_len(self, slot: int) -> int:
+        return check(_native.lib().brolm_qwen3_slot_len(self._h, int(slot)), "slot_len")
+
+    def truncate_slot(self, slot: int, length: int) -> None:
+        check(_native.lib().brolm_qwen3_truncate_slot(self._h, int(slot), int(length)), "truncate_slot")
+
+    def prefill_slot(self, slot: int, ids: Sequence[int]) -> np.ndarray:
+        """Appends a prompt to one slot; logits of its last token."""
+        arr, p = _i32(ids)
+        logits = np.empty((self.cfg.vocab_size,), np.float32)
+        check(_native.lib().brolm_qwen3_prefill_slot(self._h, int(slot), p, arr.size,
+                                                     logits.ctypes.data_as(_native.P_f32)), "prefill_slot")
+        return logits
+
+    def forward_batch(self, ids: Sequence[int], slots: Sequence[int]) -> np.ndarray:
+        """One decode step of len(ids) sequences: ids[r] joins slot slots[r];
+        (M, vocab) logits."""
+        a, pa = _i32(ids)
+        b, pb = _i32(slots)
+        if a.size != b.size:
+            raise ValueError("forward_batch: ids and slots differ in length")
+        logits = np.empty((a.size, self.cfg.vocab_size), np.float32)
+        check(_native.lib().brolm_qwen3_forward_batch(self._h, pa, pb, a.size, logits.ctypes.data_as(_native.P_f32)),
+              "forward_batch")
+        return logits
+
+    def time_forward_batch(self, ids: Sequence[int], slots: Sequence[int], n: int) -> float:
+        """Wall-clock ms per batched step over n steps (logits stay on the device)."""
+        a, pa = _i32(ids)
+        b, pb = _i32(slots)
+        if a.size != b.size:
+            raise ValueError("time_forward_batch: ids and slots differ in length")
+        ms = _native.lib().brolm_qwen3_time_forward_batch(self._h, pa, pb, a.size, int(n))
+        if ms < 0:
+            raise _native.NativeError(_native.lib().brolm_last_error().decode())
+        return ms
+
     def decode_weight_bytes(self) -> int:
         return int(_native.lib().brolm_qwen3_decode_weight_bytes(self._h))
 

@@ -109,6 +109,10 @@ HIP_SYMBOLS = {
     "bx_argmax_f16": (C.c_int, [vp, i64, vp, vp, vp]),
     "bx_argmax_f16_noalloc": (C.c_int, [vp, i64, vp, vp]),
     "bx_linear_tiles_ok": (C.c_int, [C.c_int, C.c_int]),
+    "bx_attention_varlen_f16": (C.c_int, [vp, vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp,
+                                          vp]),
+    "bx_rope_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp]),
+    "bx_kv_append_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp, vp, i64, vp]),
     "bx_linear_group_f16": (C.c_int, [C.c_int, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), vp, C.c_int,
                                       C.c_int, vp]),
     "bx_linear_residual_f16": (C.c_int, [C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
@@ -146,6 +150,12 @@ C_SYMBOLS = {
     "brolm_qwen3_cache_len": (C.c_int, [vp]),
     "brolm_qwen3_forward": (C.c_int, [vp, P_i32, C.c_int, P_f32, P_f32]),
     "brolm_qwen3_forward_last": (C.c_int, [vp, P_i32, C.c_int, P_f32]),
+    "brolm_qwen3_allocate_batch": (C.c_int, [vp, C.c_int, C.c_int]),
+    "brolm_qwen3_slot_len": (C.c_int, [vp, C.c_int]),
+    "brolm_qwen3_truncate_slot": (C.c_int, [vp, C.c_int, C.c_int]),
+    "brolm_qwen3_prefill_slot": (C.c_int, [vp, C.c_int, P_i32, C.c_int, P_f32]),
+    "brolm_qwen3_forward_batch": (C.c_int, [vp, P_i32, P_i32, C.c_int, P_f32]),
+    "brolm_qwen3_time_forward_batch": (C.c_double, [vp, P_i32, P_i32, C.c_int, C.c_int]),
     "brolm_qwen3_embed_tokens": (C.c_int, [vp, P_i32, C.c_int, P_u16]),
     "brolm_qwen3_forward_embeds": (C.c_int, [vp, P_u16, C.c_int, P_f32, P_f32]),
     "brolm_qwen3_generate": (C.c_int, [vp, P_i32, C.c_int, C.c_int, C.c_int, C.c_int, f32, C.c_int, f32, u64,

@@ -2,6 +2,7 @@
 #include "brolm_c.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -458,6 +459,49 @@ int brolm_qwen3_allocate_cache(brolm_qwen3* m, int n) { return guard([&] { core_
 int brolm_qwen3_reset_cache(brolm_qwen3* m) { return guard([&] { core_of(m).reset_cache(); }); }
 int brolm_qwen3_truncate_cache(brolm_qwen3* m, int n) { return guard([&] { core_of(m).truncate_cache(n); }); }
 int brolm_qwen3_cache_len(const brolm_qwen3* m) { return (m && m->core) ? m->core->cache_len() : -1; }
+
+int brolm_qwen3_allocate_batch(brolm_qwen3* m, int n_slots, int max_seq_len) {
+    return guard([&] { core_of(m).allocate_batch(n_slots, max_seq_len); });
+}
+int brolm_qwen3_slot_len(const brolm_qwen3* m, int slot) {
+    int n = -1;
+    const int rc = guard([&] {
+        if (!m || !m->core) throw std::invalid_argument("null model handle");
+        n = m->core->slot_len(slot);
+    });
+    return rc == 0 ? n : rc;
+}
+int brolm_qwen3_truncate_slot(brolm_qwen3* m, int slot, int len) {
+    return guard([&] { core_of(m).truncate_slot(slot, len); });
+}
+int brolm_qwen3_prefill_slot(brolm_qwen3* m, int slot, const int32_t* ids, int L, float* logits) {
+    return guard([&] {
+        brotensor::Tensor lg;
+        core_of(m).prefill_slot(slot, ids, L, lg);
+        if (logits) to_host_f32(lg, logits);
+    });
+}
+int brolm_qwen3_forward_batch(brolm_qwen3* m, const int32_t* ids, const int32_t* slots, int M, float* logits) {
+    return guard([&] {
+        brotensor::Tensor lg;
+        core_of(m).forward_batch(ids, slots, M, lg);
+        if (logits) to_host_f32(lg, logits);
+    });
+}
+double brolm_qwen3_time_forward_batch(brolm_qwen3* m, const int32_t* ids, const int32_t* slots, int M, int n) {
+    double ms = -1.0;
+    const int rc = guard([&] {
+        if (n <= 0) throw std::invalid_argument("time_forward_batch: n must be positive");
+        brolm::detail::DenseDecoder& d = core_of(m);
+        brotensor::Tensor lg;
+        brotensor::sync_all();
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < n; ++i) d.forward_batch(ids, slots, M, lg);
+        brotensor::sync_all();
+        ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() / n;
+    });
+    return rc == 0 ? ms : -1.0;
+}
 
 int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits, float* hidden) {
     return guard([&] {

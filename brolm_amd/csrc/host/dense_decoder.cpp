@@ -830,4 +830,191 @@ std::int64_t DenseDecoder::decode_weight_bytes() const {
     return b;
 }
 
+// ─── multi-sequence batched decode ──────────────────────────────────────────
+//
+// The reference decodes one sequence per model (one cache, one position).
+// Here n_slots sequences keep their own KV rows in one slot-major arena and a
+// step takes one token from each of M of them: every projection streams its
+// weights once for M rows (the 3..16-row MFMA GEMV), RoPE and the KV append
+// take a position per row, and attention runs each row over its own slot's
+// keys (split-K, per-row length).  Prompts enter a slot through the op-path
+// prefill with the layer caches pointed at the slot's rows.
+
+namespace {
+constexpr int kMetaI64PerRow = 4;  // dst row, base row (int64); pos, len, id (int32) fit in two more
+}
+
+void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
+    if (n_slots <= 0 || max_seq_len <= 0) fail("allocate_batch: n_slots and max_seq_len must be positive");
+    if (embed_tokens_.size() == 0) fail("allocate_batch: weights not loaded");
+    const int width = cfg_.num_key_value_heads * cfg_.head_dim;
+    const std::int64_t rows = 2LL * static_cast<std::int64_t>(layers_.size()) * n_slots * max_seq_len;
+    if (rows > INT32_MAX) fail("allocate_batch: KV arena rows exceed the tensor row limit");
+    batch_kv_ = bt::Tensor();
+    batch_kv_ = bt::Tensor::empty_on(bt::Device::ROCm, static_cast<int>(rows), width, bt::Dtype::FP16);
+    batch_slots_ = n_slots;
+    batch_cap_ = max_seq_len;
+    slot_len_.assign(static_cast<std::size_t>(n_slots), 0);
+    const int half = cfg_.head_dim / 2;
+    std::vector<float> c(static_cast<std::size_t>(max_seq_len) * half), sn(c.size());
+    bx_rope_table_host(c.data(), sn.data(), max_seq_len, cfg_.head_dim, cfg_.rope_theta);
+    batch_cos_ = bt::Tensor::from_host_on(bt::Device::ROCm, c.data(), max_seq_len, half);
+    batch_sin_ = bt::Tensor::from_host_on(bt::Device::ROCm, sn.data(), max_seq_len, half);
+    batch_meta_ = bt::Tensor::empty_on(bt::Device::ROCm, n_slots, 2 * kMetaI64PerRow, bt::Dtype::FP32);
+}
+
+int DenseDecoder::slot_len(int slot) const {
+    if (slot < 0 || slot >= batch_slots_) fail("slot_len: slot out of range");
+    return slot_len_[static_cast<std::size_t>(slot)];
+}
+
+void DenseDecoder::truncate_slot(int slot, int len) {
+    if (slot < 0 || slot >= batch_slots_) fail("truncate_slot: slot out of range");
+    if (len < 0 || len > slot_len_[static_cast<std::size_t>(slot)])
+        fail("truncate_slot: len must be in [0, slot_len]");
+    slot_len_[static_cast<std::size_t>(slot)] = len;
+}
+
+void DenseDecoder::prefill_slot(int slot, const int32_t* ids, int L, bt::Tensor& logits_out) {
+    if (batch_slots_ == 0) fail("prefill_slot: batch not allocated");
+    if (slot < 0 || slot >= batch_slots_) fail("prefill_slot: slot out of range");
+    const int len = slot_len_[static_cast<std::size_t>(slot)];
+    check_forward("prefill_slot", ids, L, true, batch_cap_, len, cfg_.vocab_size);
+    const int width = cfg_.num_key_value_heads * cfg_.head_dim;
+    const std::size_t plane = static_cast<std::size_t>(batch_slots_) * batch_cap_ * width;  // FP16 elements
+    const std::size_t at = static_cast<std::size_t>(slot) * batch_cap_ * width;
+    auto* base = static_cast<std::uint16_t*>(batch_kv_.data);
+    // point every layer's cache at the slot's rows for the op-path prefill,
+    // then put the single-sequence views (and cache_len) back
+    std::vector<bt::Tensor> saved;
+    saved.reserve(2 * layers_.size());
+    for (std::size_t l = 0; l < layers_.size(); ++l) {
+        saved.push_back(std::move(layers_[l].K_cache));
+        saved.push_back(std::move(layers_[l].V_cache));
+        layers_[l].K_cache = bt::Tensor::view(bt::Device::ROCm, base + 2 * l * plane + at, batch_cap_, width,
+                                              bt::Dtype::FP16);
+        layers_[l].V_cache = bt::Tensor::view(bt::Device::ROCm, base + (2 * l + 1) * plane + at, batch_cap_, width,
+                                              bt::Dtype::FP16);
+    }
+    const int saved_len = cache_len_;
+    auto restore = [&] {
+        for (std::size_t l = 0; l < layers_.size(); ++l) {
+            layers_[l].K_cache = std::move(saved[2 * l]);
+            layers_[l].V_cache = std::move(saved[2 * l + 1]);
+        }
+        cache_len_ = saved_len;
+    };
+    try {
+        cache_len_ = len;
+        ids_dev_ = make_idx_device(ids, L);
+        resize_like(h_, L, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+        hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                                  embed_tokens_.cols, static_cast<const int32_t*>(ids_dev_.data), L,
+                                  static_cast<float*>(h_.data), bt::stream()),
+                 "embedding");
+        run_layers_(L, logits_out, nullptr, /*logits_last_row_only=*/true);
+    } catch (...) {
+        restore();
+        throw;
+    }
+    slot_len_[static_cast<std::size_t>(slot)] = len + L;
+    restore();
+}
+
+void DenseDecoder::forward_batch(const int32_t* ids, const int32_t* slots, int M, bt::Tensor& logits_out) {
+    if (batch_slots_ == 0) fail("forward_batch: batch not allocated");
+    if (!ids || !slots) fail("forward_batch: null ids or slots");
+    if (M <= 0 || M > batch_slots_) fail("forward_batch: M must be in [1, batch_slots]");
+    std::vector<char> seen(static_cast<std::size_t>(batch_slots_), 0);
+    batch_meta_host_.assign(static_cast<std::size_t>(kMetaI64PerRow) * M, 0);
+    std::int64_t* dst = batch_meta_host_.data();
+    std::int64_t* base = dst + M;
+    auto* pos = reinterpret_cast<int32_t*>(dst + 2 * M);
+    int32_t* lens = pos + M;
+    int32_t* idv = lens + M;
+    int max_len = 0;
+    for (int r = 0; r < M; ++r) {
+        const int s = slots[r];
+        if (s < 0 || s >= batch_slots_) fail("forward_batch: slot out of range");
+        if (seen[static_cast<std::size_t>(s)]) fail("forward_batch: a slot appears twice");
+        seen[static_cast<std::size_t>(s)] = 1;
+        const int len = slot_len_[static_cast<std::size_t>(s)];
+        if (len >= batch_cap_) fail("forward_batch: slot is full");
+        if (ids[r] < 0 || ids[r] >= cfg_.vocab_size) fail("forward_batch: token id out of range");
+        base[r] = static_cast<std::int64_t>(s) * batch_cap_;
+        dst[r] = base[r] + len;
+        pos[r] = len;
+        lens[r] = len + 1;
+        idv[r] = ids[r];
+        max_len = std::max(max_len, len + 1);
+    }
+    hipx::h2d(batch_meta_.data, batch_meta_host_.data(), batch_meta_host_.size() * sizeof(std::int64_t));
+    const auto* dst_d = static_cast<const std::int64_t*>(batch_meta_.data);
+    const std::int64_t* base_d = dst_d + M;
+    const auto* pos_d = reinterpret_cast<const int32_t*>(dst_d + 2 * M);
+    const int32_t* lens_d = pos_d + M;
+    const int32_t* ids_d = lens_d + M;
+
+    const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
+    const int width = n_kv * HD;
+    const float eps = cfg_.rms_norm_eps;
+    void* st = bt::stream();
+    resize_like(h_, M, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
+    hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                              embed_tokens_.cols, ids_d, M, static_cast<float*>(h_.data), st),
+             "forward_batch embedding");
+    const std::size_t wsb = bx_attention_workspace_bytes(M, n_q, HD, max_len);
+    resize_like(attn_ws_, 1, static_cast<int>((wsb + 3) / 4), bt::Dtype::FP32, bt::Device::ROCm);
+    resize_like(attn_, M, n_q * HD, bt::Dtype::FP16, bt::Device::ROCm);
+    const std::int64_t plane_rows = static_cast<std::int64_t>(batch_slots_) * batch_cap_;
+    auto* arena = static_cast<std::uint16_t*>(batch_kv_.data);
+    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst_t) {
+        bt::Tensor v = bt::Tensor::view(src.device, src.data, src.rows * num_heads, HD, src.dtype);
+        bt::rms_norm_forward(v, gain, eps, dst_t);
+        dst_t.rows = src.rows;
+        dst_t.cols = num_heads * HD;
+    };
+    for (std::size_t l = 0; l < layers_.size(); ++l) {
+        Layer& layer = layers_[l];
+        bt::rms_norm_forward(h_, layer.input_ln, eps, norm_);
+        linear_batched(layer.Wq, nullptr, norm_, q_);
+        linear_batched(layer.Wk, nullptr, norm_, k_);
+        linear_batched(layer.Wv, nullptr, norm_, v_);
+        bt::Tensor* q_attn = &q_;
+        bt::Tensor* k_attn = &k_;
+        if (cfg_.use_qk_norm) {
+            headnorm(q_, n_q, layer.q_norm, qn_);
+            headnorm(k_, n_kv, layer.k_norm, kn_);
+            q_attn = &qn_;
+            k_attn = &kn_;
+        }
+        auto* qd = static_cast<uint16_t*>(q_attn->data);
+        auto* kd = static_cast<uint16_t*>(k_attn->data);
+        const auto* cs = static_cast<const float*>(batch_cos_.data);
+        const auto* sn = static_cast<const float*>(batch_sin_.data);
+        hipx::bx(bx_rope_rows_f16(qd, qd, M, HD, n_q, pos_d, cs, sn, batch_cap_, st), "forward_batch rope q");
+        hipx::bx(bx_rope_rows_f16(kd, kd, M, HD, n_kv, pos_d, cs, sn, batch_cap_, st), "forward_batch rope k");
+        std::uint16_t* Kp = arena + static_cast<std::size_t>(2 * l) * plane_rows * width;
+        std::uint16_t* Vp = Kp + static_cast<std::size_t>(plane_rows) * width;
+        hipx::bx(bx_kv_append_rows_f16(kd, static_cast<const uint16_t*>(v_.data), M, width, dst_d, Kp, Vp,
+                                       plane_rows, st),
+                 "forward_batch kv append");
+        hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, max_len, n_q, n_kv, HD,
+                                         static_cast<uint16_t*>(attn_.data), attn_ws_.data, st),
+                 "forward_batch attention");
+        linear_batched(layer.Wo, nullptr, attn_, proj_);
+        bt::add_inplace(h_, proj_);
+        bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_);
+        linear_batched(layer.gate_W, nullptr, norm_, gate_);
+        linear_batched(layer.up_W, nullptr, norm_, up_);
+        bt::silu_forward(gate_, gate_);
+        bt::mul_inplace(gate_, up_);
+        linear_batched(layer.down_W, nullptr, gate_, proj_);
+        bt::add_inplace(h_, proj_);
+    }
+    bt::rms_norm_forward(h_, final_norm_, eps, norm_);
+    linear_batched(lm_head_, nullptr, norm_, logits_out);
+    for (int r = 0; r < M; ++r) ++slot_len_[static_cast<std::size_t>(slots[r])];
+}
+
 }  // namespace brolm::detail

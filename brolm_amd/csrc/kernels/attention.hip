@@ -19,7 +19,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float att_smem[];
     const int s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
     const int G = a.n_q / a.n_kv;
-    const int p = a.bidir ? a.valid_len - 1 : a.valid_len - a.L + r;  // last key this row may see
+    if (a.rlen) {  // this row's own sequence: its keys start at cache row rbase[r]
+        const int64_t shift = a.rbase[r] * (int64_t)a.n_kv * a.hd;
+        a.Kc += shift;
+        a.Vc += shift;
+    }
+    const int p = a.rlen ? a.rlen[r] - 1 : a.bidir ? a.valid_len - 1 : a.valid_len - a.L + r;  // last key
     const int lo = a.window > 0 ? max(0, p - a.window + 1) : 0;
     const int kb = max(lo, s * a.kps);
     const int ke = min(p + 1, (s + 1) * a.kps);
@@ -139,6 +144,32 @@ int bx_attention_gqa_f16(const uint16_t* q, const uint16_t* K, const uint16_t* V
     if (int rc = launch_check("attention_gqa partial")) return rc;
     attn_combine_kernel<<<dim3(n_q, L), 128, 0, st>>>(a.ws, n_q, hd, a.S, out);
     return launch_check("attention_gqa combine");
+}
+
+int bx_attention_varlen_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, int rows,
+                            const int32_t* lens_dev, const int64_t* base_rows_dev, int max_len, int n_q, int n_kv,
+                            int hd, uint16_t* out, void* workspace, void* stream) {
+    if (!q || !Kc || !Vc || !lens_dev || !base_rows_dev || !out || !workspace)
+        return fail(BX_EINVAL, "attention_varlen: null pointer");
+    if (rows <= 0 || max_len <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv)
+        return fail(BX_EINVAL, "attention_varlen: bad shape");
+    if (n_q / n_kv > kAttnMaxGroup) return fail(BX_EUNSUPPORTED, "attention_varlen: GQA group larger than 8");
+    if (hd <= 0 || hd % 8 || hd > 256) return fail(BX_EUNSUPPORTED, "attention_varlen: bad head_dim");
+    AttnArgs a{};
+    a.q = q; a.Kc = Kc; a.Vc = Vc; a.mask = nullptr;
+    a.L = rows; a.valid_len = max_len; a.n_q = n_q; a.n_kv = n_kv; a.hd = hd;
+    a.softcap = 0.f; a.window = 0;
+    a.rlen = lens_dev; a.rbase = base_rows_dev;
+    a.kps = attn_keys_per_split(rows, n_kv, max_len);
+    a.S = (max_len + a.kps - 1) / a.kps;
+    a.ws = static_cast<float*>(workspace);
+    const int G = n_q / n_kv;
+    const size_t lds = (size_t)(G * hd + G * 256 + 64) * sizeof(float);
+    hipStream_t st = as_stream(stream);
+    attn_partial_kernel<<<dim3(a.S, n_kv, rows), 256, lds, st>>>(a);
+    if (int rc = launch_check("attention_varlen partial")) return rc;
+    attn_combine_kernel<<<dim3(n_q, rows), 128, 0, st>>>(a.ws, n_q, hd, a.S, out);
+    return launch_check("attention_varlen combine");
 }
 
 int bx_attention_masked_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, const float* mask, int n_keys,

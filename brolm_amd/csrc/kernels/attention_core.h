@@ -20,6 +20,10 @@ struct AttnArgs {
     int kps, S;
     float* ws;  // partials [L][n_q][S][hd + 2]
     int bidir;  // 1: every row attends all valid_len keys (no causal limit)
+    // per-row key ranges (batched decode of independent sequences): row r
+    // attends cache rows rbase[r] .. rbase[r] + rlen[r] - 1; null otherwise
+    const int32_t* rlen;
+    const int64_t* rbase;
 };
 
 // Flash attention on MFMA for L >= 16 query rows (attention_mfma.hip): head

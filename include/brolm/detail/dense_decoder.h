@@ -90,6 +90,24 @@ public:
     // Needs loaded weights and an allocated cache (creates the step session).
     int decode_mode();
 
+    // ── Multi-sequence batched decode ──────────────────────────────────────
+    // An extension beyond the reference's single cache: n_slots independent
+    // sequences, each with its own KV rows (slot-major arena, capacity
+    // max_seq_len per slot), stepped together so one pass over the weights
+    // serves M tokens.  The single-sequence cache above is untouched.
+    void allocate_batch(int n_slots, int max_seq_len);
+    int batch_slots() const { return batch_slots_; }
+    int batch_capacity() const { return batch_cap_; }
+    int slot_len(int slot) const;
+    void truncate_slot(int slot, int len);
+    // Appends L prompt tokens to `slot` (op path, causal over the slot's own
+    // rows); logits_out := logits of the last row (1, vocab).
+    void prefill_slot(int slot, const int32_t* ids, int L, brotensor::Tensor& logits_out);
+    // One decode step of M sequences: row r is token ids[r] of slot slots[r]
+    // (distinct slots) at position slot_len(slots[r]); logits_out := (M,
+    // vocab) FP16 on the device.  Every listed slot's length advances by one.
+    void forward_batch(const int32_t* ids, const int32_t* slots, int M, brotensor::Tensor& logits_out);
+
     const DenseDecoderConfig& config() const { return cfg_; }
 
 private:
@@ -129,6 +147,17 @@ private:
     brotensor::Tensor attn_ws_;
 
     std::unique_ptr<DecodeGraphSession> graph_;
+
+    // batched decode: per layer a K plane then a V plane, each
+    // (n_slots * capacity, n_kv * head_dim) FP16; slot s, position p is row
+    // s * capacity + p of both
+    int batch_slots_ = 0;
+    int batch_cap_ = 0;
+    std::vector<int> slot_len_;
+    brotensor::Tensor batch_kv_;
+    brotensor::Tensor batch_cos_, batch_sin_;  // (capacity, hd/2) FP32
+    brotensor::Tensor batch_meta_;             // per-step row metadata (device)
+    std::vector<std::int64_t> batch_meta_host_;
 };
 
 }  // namespace brolm::detail

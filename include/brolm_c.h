@@ -141,6 +141,21 @@ int brolm_qwen3_reset_cache(brolm_qwen3* m);
 int brolm_qwen3_truncate_cache(brolm_qwen3* m, int len);
 int brolm_qwen3_cache_len(const brolm_qwen3* m);
 /* forward: logits (L, vocab); hidden (L, hidden) or NULL. */
+/* Multi-sequence batched decode (no counterpart in the reference, whose
+ * model holds one sequence; dense_decoder.h:84-239 is the one-sequence
+ * surface these extend): n_slots sequences with their own KV rows. */
+int brolm_qwen3_allocate_batch(brolm_qwen3* m, int n_slots, int max_seq_len);
+/* Tokens held by `slot` (>= 0), or a negative error code. */
+int brolm_qwen3_slot_len(const brolm_qwen3* m, int slot);
+int brolm_qwen3_truncate_slot(brolm_qwen3* m, int slot, int len);
+/* Appends L prompt tokens to `slot`; logits (vocab) of the last one. */
+int brolm_qwen3_prefill_slot(brolm_qwen3* m, int slot, const int32_t* ids, int L, float* logits);
+/* One step of M sequences: ids[r] joins slot slots[r] (distinct slots);
+ * logits (M, vocab) row-major. */
+int brolm_qwen3_forward_batch(brolm_qwen3* m, const int32_t* ids, const int32_t* slots, int M, float* logits);
+/* n calls of forward_batch without reading logits back; wall-clock ms per
+ * call (every slot advances by n), or -1 on error. */
+double brolm_qwen3_time_forward_batch(brolm_qwen3* m, const int32_t* ids, const int32_t* slots, int M, int n);
 int brolm_qwen3_forward(brolm_qwen3* m, const int32_t* ids, int L, float* logits, float* hidden);
 /* forward_last: logits (1, vocab). */
 int brolm_qwen3_forward_last(brolm_qwen3* m, const int32_t* ids, int L, float* logits);

@@ -138,6 +138,22 @@ int bx_attention_decode_f16(const uint16_t* q, const uint16_t* Kc, const uint16_
 int bx_attention_gqa_f16(const uint16_t* q, const uint16_t* K, const uint16_t* V, int L, int n_keys, int n_q,
                          int n_kv, int hd, int causal, uint16_t* out, void* workspace, void* stream);
 
+/* Batched decode of independent sequences (an extension of the one-sequence
+ * cache of dense_decoder.cpp:196-227, 585-607): row r of q (rows, n_q*hd) is
+ * the newest token of its own sequence, whose rlen = lens_dev[r] keys sit in
+ * cache rows base_rows_dev[r] .. + rlen - 1 (the last one its own); max_len >=
+ * every rlen sizes the split.  workspace: bx_attention_workspace_bytes(rows,
+ * n_q, hd, max_len) bytes. */
+int bx_attention_varlen_f16(const uint16_t* q, const uint16_t* Kc, const uint16_t* Vc, int rows,
+                            const int32_t* lens_dev, const int64_t* base_rows_dev, int max_len, int n_q, int n_kv,
+                            int hd, uint16_t* out, void* workspace, void* stream);
+/* rope_forward with a position per row (pos_dev, device int32 < tab_rows). */
+int bx_rope_rows_f16(const uint16_t* X, uint16_t* Y, int rows, int hd, int n_heads, const int32_t* pos_dev,
+                     const float* cos_tab, const float* sin_tab, int tab_rows, void* stream);
+/* kv_cache_append of row r to cache row dst_rows_dev[r] (< cache_rows). */
+int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int cols, const int64_t* dst_rows_dev,
+                          uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, void* stream);
+
 /* K15: flash_attention_decode_masked(q, Kc, Vc, mask, n_q, n_kv, out)
  * (dense_decoder.cpp:476-478): one query row attends the keys j < n_keys
  * whose FP32 mask[j] (device) is non-zero.  workspace as above with L = 1,

@@ -1,0 +1,152 @@
+"""Multi-sequence batched decode on the device (brolm_qwen3_allocate_batch /
+_prefill_slot / _forward_batch): every row of a batched step must give the
+logits that sequence gets alone.  The checker is one CPU oracle model per
+sequence (the reference's one-sequence DenseDecoder semantics,
+src/detail/dense_decoder.cpp:231-329, 526-681), fed the same tokens.
+Logit tolerance: max-abs 2e-2 against the oracle's FP32 logits, as for the
+one-sequence model tests."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+LOGIT_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def ba():
+    import brolm_amd
+    brolm_amd.init()
+    return brolm_amd
+
+
+def _model(ba, path, arch):
+    if arch == "mistral3":
+        m = ba.Mistral3TextModel(ba.Mistral3Config.from_gguf(str(path)).text)
+    else:
+        m = ba.Qwen3Model(ba.Qwen3Config.from_gguf(str(path)))
+    m.load_weights(str(path))
+    return m
+
+
+def _oracles(path, n, cap):
+    out = []
+    for _ in range(n):
+        om = oracle.Model(str(path))
+        om.allocate_cache(cap)
+        out.append(om)
+    return out
+
+
+@pytest.mark.parametrize("which,arch", [("small_gguf", "qwen3"), ("small_q8_gguf", "qwen3"),
+                                        ("small_m3_gguf", "mistral3")])
+def test_batched_steps_match_each_sequence_alone(ba, which, arch, request):
+    """Ragged prompts in non-contiguous slots, then steps over changing
+    subsets of the slots in shuffled row order (M from 1 to 5)."""
+    path = request.getfixturevalue(which)
+    print(f"[batch] {which}", flush=True)
+    cap = 64
+    m = _model(ba, path, arch)
+    m.allocate_batch(8, cap)
+    V = m.cfg.vocab_size
+    rng = np.random.default_rng(5)
+    slots = [0, 2, 3, 5, 7]
+    lens = [1, 7, 3, 19, 12]
+    om = dict(zip(slots, _oracles(path, len(slots), cap)))
+    for s, n in zip(slots, lens):
+        prompt = rng.integers(0, V, n).tolist()
+        got = m.prefill_slot(s, prompt)
+        want = om[s].forward(prompt, last_only=True)[0]
+        assert np.abs(got - want).max() <= LOGIT_TOL, f"prefill slot {s}"
+        assert m.slot_len(s) == n
+    steps = [[0, 2, 3, 5, 7], [7, 0, 3], [5], [2, 7, 5, 0], [3, 2, 0, 7, 5], [0, 5]]
+    for step in steps:
+        ids = rng.integers(0, V, len(step)).tolist()
+        got = m.forward_batch(ids, step)
+        assert got.shape == (len(step), V) and np.isfinite(got).all()
+        for r, (s, t) in enumerate(zip(step, ids)):
+            want = om[s].forward([t], last_only=True)[0]
+            err = np.abs(got[r] - want).max()
+            assert err <= LOGIT_TOL, f"step {step} row {r} slot {s}: {err}"
+    for s, n in zip(slots, lens):
+        assert m.slot_len(s) == n + sum(s in st for st in steps)
+    m.close()
+
+
+def test_sixteen_rows_and_long_slots(ba, small_gguf):
+    """M = 16 (the widest MFMA-GEMV row count) with slots past several
+    attention splits; then a truncated slot replays bit-for-bit."""
+    print("[batch] 16 rows", flush=True)
+    cap = 640
+    m = _model(ba, small_gguf, "qwen3")
+    m.allocate_batch(16, cap)
+    V = m.cfg.vocab_size
+    rng = np.random.default_rng(9)
+    lens = [int(x) for x in rng.integers(1, 600, 16)]
+    oms = _oracles(small_gguf, 16, cap)
+    for s in range(16):
+        prompt = rng.integers(0, V, lens[s]).tolist()
+        m.prefill_slot(s, prompt)
+        oms[s].forward(prompt, last_only=True)
+    order = rng.permutation(16).tolist()
+    ids = rng.integers(0, V, 16).tolist()
+    got = m.forward_batch(ids, order)
+    for r, s in enumerate(order):
+        want = oms[s].forward([ids[r]], last_only=True)[0]
+        assert np.abs(got[r] - want).max() <= LOGIT_TOL, f"row {r} slot {s}"
+    # drop the step from every slot and repeat it: identical logits
+    for s in range(16):
+        m.truncate_slot(s, lens[s])
+    again = m.forward_batch(ids, order)
+    assert np.array_equal(got, again)
+    m.close()
+
+
+def test_batch_leaves_the_single_sequence_cache_alone(ba, small_gguf):
+    print("[batch] isolation", flush=True)
+    m = _model(ba, small_gguf, "qwen3")
+    m.allocate_cache(64)
+    m.allocate_batch(4, 64)
+    V = m.cfg.vocab_size
+    a = m.forward([3, 4, 5, 6])
+    m.prefill_slot(1, [9, 8, 7])
+    m.forward_batch([1, 2], [1, 3])
+    assert m.cache_len() == 4
+    b = m.forward_last([10])
+    om = oracle.Model(str(small_gguf))
+    om.allocate_cache(64)
+    om.forward([3, 4, 5, 6])
+    assert np.abs(b - om.forward([10], last_only=True)[0]).max() <= LOGIT_TOL
+    assert a.shape == (4, V)
+    m.close()
+
+
+def test_batch_errors_raise(ba, small_gguf):
+    print("[batch] errors", flush=True)
+    m = _model(ba, small_gguf, "qwen3")
+    with pytest.raises(ba._native.NativeError, match="not allocated"):
+        m.forward_batch([1], [0])
+    m.allocate_batch(3, 8)
+    with pytest.raises(ba._native.NativeError, match="appears twice"):
+        m.forward_batch([1, 2], [1, 1])
+    with pytest.raises(ba._native.NativeError, match="out of range"):
+        m.forward_batch([1], [3])
+    with pytest.raises(ba._native.NativeError, match="token id out of range"):
+        m.forward_batch([m.cfg.vocab_size], [0])
+    with pytest.raises(ba._native.NativeError, match="M must be"):
+        m.forward_batch([1, 2, 3, 4], [0, 1, 2, 0])
+    with pytest.raises(ba._native.NativeError, match="exceeds"):
+        m.prefill_slot(0, list(range(9)))
+    m.prefill_slot(0, list(range(8)))
+    with pytest.raises(ba._native.NativeError, match="slot is full"):
+        m.forward_batch([1], [0])
+    with pytest.raises(ba._native.NativeError, match="truncate_slot"):
+        m.truncate_slot(1, 1)
+    m.truncate_slot(0, 7)
+    assert m.slot_len(0) == 7
+    m.forward_batch([1], [0])
+    assert m.slot_len(0) == 8
+    m.close()
