@@ -844,6 +844,25 @@ namespace {
 constexpr int kMetaI64PerRow = 4;  // dst row, base row (int64); pos, len, id (int32) fit in two more
 }
 
+// One replayable step per row count M: the first step of a given M runs
+// eagerly (it also settles every buffer), the second is captured and every
+// later one replays the graph.  The kernels read positions, lengths, slots
+// and token ids from batch_meta_, so a replay needs only that upload.
+struct DenseDecoder::BatchGraphs {
+    std::vector<hipGraphExec_t> exec;
+    std::vector<char> warmed;
+    bool use_graph = true;
+
+    explicit BatchGraphs(int n) : exec(static_cast<std::size_t>(n) + 1, nullptr), warmed(exec.size(), 0) {
+        use_graph = !env_flag("BROLM_NO_GRAPH");
+    }
+    ~BatchGraphs() {
+        if (bt::initialized()) (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
+        for (hipGraphExec_t e : exec)
+            if (e) (void)hipGraphExecDestroy(e);
+    }
+};
+
 void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
     if (n_slots <= 0 || max_seq_len <= 0) fail("allocate_batch: n_slots and max_seq_len must be positive");
     if (embed_tokens_.size() == 0) fail("allocate_batch: weights not loaded");
@@ -861,6 +880,24 @@ void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
     batch_cos_ = bt::Tensor::from_host_on(bt::Device::ROCm, c.data(), max_seq_len, half);
     batch_sin_ = bt::Tensor::from_host_on(bt::Device::ROCm, sn.data(), max_seq_len, half);
     batch_meta_ = bt::Tensor::empty_on(bt::Device::ROCm, n_slots, 2 * kMetaI64PerRow, bt::Dtype::FP32);
+    batch_graphs_.reset();
+    const int H = cfg_.hidden_size, F = cfg_.intermediate_size, qd = cfg_.num_attention_heads * cfg_.head_dim;
+    const auto dev = bt::Device::ROCm;
+    bh_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP32);
+    bnorm_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP16);
+    bq_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
+    bqn_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
+    bk_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
+    bkn_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
+    bv_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
+    battn_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
+    bproj_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP16);
+    bgate_ = bt::Tensor::empty_on(dev, n_slots, F, bt::Dtype::FP16);
+    bup_ = bt::Tensor::empty_on(dev, n_slots, F, bt::Dtype::FP16);
+    blogits_ = bt::Tensor::empty_on(dev, n_slots, cfg_.vocab_size, bt::Dtype::FP16);
+    const std::size_t wsb = bx_attention_workspace_bytes(n_slots, cfg_.num_attention_heads, cfg_.head_dim, max_seq_len);
+    bws_ = bt::Tensor::empty_on(dev, 1, static_cast<int>((wsb + 3) / 4), bt::Dtype::FP32);
+    batch_graphs_ = std::make_unique<BatchGraphs>(n_slots);
 }
 
 int DenseDecoder::slot_len(int slot) const {
@@ -921,6 +958,74 @@ void DenseDecoder::prefill_slot(int slot, const int32_t* ids, int L, bt::Tensor&
     restore();
 }
 
+// The batched step for M rows on the op stream (eager, or recorded into a
+// graph): every pointer it uses is fixed between allocate_batch calls, and the
+// attention split plan is sized by the slot capacity, not the current lengths.
+void DenseDecoder::enqueue_batch_(int M) {
+    const auto* dst_d = static_cast<const std::int64_t*>(batch_meta_.data);
+    const std::int64_t* base_d = dst_d + M;
+    const auto* pos_d = reinterpret_cast<const int32_t*>(dst_d + 2 * M);
+    const int32_t* lens_d = pos_d + M;
+    const int32_t* ids_d = lens_d + M;
+    const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
+    const int width = n_kv * HD;
+    const float eps = cfg_.rms_norm_eps;
+    void* st = bt::stream();
+    bh_.resize(M, cfg_.hidden_size, bt::Dtype::FP32);
+    battn_.resize(M, n_q * HD, bt::Dtype::FP16);
+    hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
+                              embed_tokens_.cols, ids_d, M, static_cast<float*>(bh_.data), st),
+             "forward_batch embedding");
+    const std::int64_t plane_rows = static_cast<std::int64_t>(batch_slots_) * batch_cap_;
+    auto* arena = static_cast<std::uint16_t*>(batch_kv_.data);
+    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst_t) {
+        bt::Tensor v = bt::Tensor::view(src.device, src.data, src.rows * num_heads, HD, src.dtype);
+        bt::rms_norm_forward(v, gain, eps, dst_t);
+        dst_t.rows = src.rows;
+        dst_t.cols = num_heads * HD;
+    };
+    const auto* cs = static_cast<const float*>(batch_cos_.data);
+    const auto* sn = static_cast<const float*>(batch_sin_.data);
+    for (std::size_t l = 0; l < layers_.size(); ++l) {
+        Layer& layer = layers_[l];
+        bt::rms_norm_forward(bh_, layer.input_ln, eps, bnorm_);
+        linear_batched(layer.Wq, nullptr, bnorm_, bq_);
+        linear_batched(layer.Wk, nullptr, bnorm_, bk_);
+        linear_batched(layer.Wv, nullptr, bnorm_, bv_);
+        bt::Tensor* q_attn = &bq_;
+        bt::Tensor* k_attn = &bk_;
+        if (cfg_.use_qk_norm) {
+            headnorm(bq_, n_q, layer.q_norm, bqn_);
+            headnorm(bk_, n_kv, layer.k_norm, bkn_);
+            q_attn = &bqn_;
+            k_attn = &bkn_;
+        }
+        auto* qd = static_cast<uint16_t*>(q_attn->data);
+        auto* kd = static_cast<uint16_t*>(k_attn->data);
+        hipx::bx(bx_rope_rows_f16(qd, qd, M, HD, n_q, pos_d, cs, sn, batch_cap_, st), "forward_batch rope q");
+        hipx::bx(bx_rope_rows_f16(kd, kd, M, HD, n_kv, pos_d, cs, sn, batch_cap_, st), "forward_batch rope k");
+        std::uint16_t* Kp = arena + static_cast<std::size_t>(2 * l) * plane_rows * width;
+        std::uint16_t* Vp = Kp + static_cast<std::size_t>(plane_rows) * width;
+        hipx::bx(bx_kv_append_rows_f16(kd, static_cast<const uint16_t*>(bv_.data), M, width, dst_d, Kp, Vp,
+                                       plane_rows, st),
+                 "forward_batch kv append");
+        hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, batch_cap_, n_q, n_kv, HD,
+                                         static_cast<uint16_t*>(battn_.data), bws_.data, st),
+                 "forward_batch attention");
+        linear_batched(layer.Wo, nullptr, battn_, bproj_);
+        bt::add_inplace(bh_, bproj_);
+        bt::rms_norm_forward(bh_, layer.post_attn_ln, eps, bnorm_);
+        linear_batched(layer.gate_W, nullptr, bnorm_, bgate_);
+        linear_batched(layer.up_W, nullptr, bnorm_, bup_);
+        bt::silu_forward(bgate_, bgate_);
+        bt::mul_inplace(bgate_, bup_);
+        linear_batched(layer.down_W, nullptr, bgate_, bproj_);
+        bt::add_inplace(bh_, bproj_);
+    }
+    bt::rms_norm_forward(bh_, final_norm_, eps, bnorm_);
+    linear_batched(lm_head_, nullptr, bnorm_, blogits_);
+}
+
 void DenseDecoder::forward_batch(const int32_t* ids, const int32_t* slots, int M, bt::Tensor& logits_out) {
     if (batch_slots_ == 0) fail("forward_batch: batch not allocated");
     if (!ids || !slots) fail("forward_batch: null ids or slots");
@@ -932,7 +1037,6 @@ void DenseDecoder::forward_batch(const int32_t* ids, const int32_t* slots, int M
     auto* pos = reinterpret_cast<int32_t*>(dst + 2 * M);
     int32_t* lens = pos + M;
     int32_t* idv = lens + M;
-    int max_len = 0;
     for (int r = 0; r < M; ++r) {
         const int s = slots[r];
         if (s < 0 || s >= batch_slots_) fail("forward_batch: slot out of range");
@@ -946,74 +1050,33 @@ void DenseDecoder::forward_batch(const int32_t* ids, const int32_t* slots, int M
         pos[r] = len;
         lens[r] = len + 1;
         idv[r] = ids[r];
-        max_len = std::max(max_len, len + 1);
     }
     hipx::h2d(batch_meta_.data, batch_meta_host_.data(), batch_meta_host_.size() * sizeof(std::int64_t));
-    const auto* dst_d = static_cast<const std::int64_t*>(batch_meta_.data);
-    const std::int64_t* base_d = dst_d + M;
-    const auto* pos_d = reinterpret_cast<const int32_t*>(dst_d + 2 * M);
-    const int32_t* lens_d = pos_d + M;
-    const int32_t* ids_d = lens_d + M;
-
-    const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
-    const int width = n_kv * HD;
-    const float eps = cfg_.rms_norm_eps;
-    void* st = bt::stream();
-    resize_like(h_, M, cfg_.hidden_size, bt::Dtype::FP32, bt::Device::ROCm);
-    hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
-                              embed_tokens_.cols, ids_d, M, static_cast<float*>(h_.data), st),
-             "forward_batch embedding");
-    const std::size_t wsb = bx_attention_workspace_bytes(M, n_q, HD, max_len);
-    resize_like(attn_ws_, 1, static_cast<int>((wsb + 3) / 4), bt::Dtype::FP32, bt::Device::ROCm);
-    resize_like(attn_, M, n_q * HD, bt::Dtype::FP16, bt::Device::ROCm);
-    const std::int64_t plane_rows = static_cast<std::int64_t>(batch_slots_) * batch_cap_;
-    auto* arena = static_cast<std::uint16_t*>(batch_kv_.data);
-    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst_t) {
-        bt::Tensor v = bt::Tensor::view(src.device, src.data, src.rows * num_heads, HD, src.dtype);
-        bt::rms_norm_forward(v, gain, eps, dst_t);
-        dst_t.rows = src.rows;
-        dst_t.cols = num_heads * HD;
-    };
-    for (std::size_t l = 0; l < layers_.size(); ++l) {
-        Layer& layer = layers_[l];
-        bt::rms_norm_forward(h_, layer.input_ln, eps, norm_);
-        linear_batched(layer.Wq, nullptr, norm_, q_);
-        linear_batched(layer.Wk, nullptr, norm_, k_);
-        linear_batched(layer.Wv, nullptr, norm_, v_);
-        bt::Tensor* q_attn = &q_;
-        bt::Tensor* k_attn = &k_;
-        if (cfg_.use_qk_norm) {
-            headnorm(q_, n_q, layer.q_norm, qn_);
-            headnorm(k_, n_kv, layer.k_norm, kn_);
-            q_attn = &qn_;
-            k_attn = &kn_;
+    BatchGraphs& g = *batch_graphs_;
+    const std::size_t mi = static_cast<std::size_t>(M);
+    if (!g.use_graph || !g.warmed[mi]) {
+        enqueue_batch_(M);
+        g.warmed[mi] = 1;
+    } else {
+        hipStream_t st = static_cast<hipStream_t>(bt::stream());
+        if (!g.exec[mi]) {
+            hipx::check(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+            hipGraph_t graph = nullptr;
+            try {
+                enqueue_batch_(M);
+            } catch (...) {
+                (void)hipStreamEndCapture(st, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            hipx::check(hipStreamEndCapture(st, &graph), "hipStreamEndCapture");
+            const hipError_t e = hipGraphInstantiate(&g.exec[mi], graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            hipx::check(e, "hipGraphInstantiate");
         }
-        auto* qd = static_cast<uint16_t*>(q_attn->data);
-        auto* kd = static_cast<uint16_t*>(k_attn->data);
-        const auto* cs = static_cast<const float*>(batch_cos_.data);
-        const auto* sn = static_cast<const float*>(batch_sin_.data);
-        hipx::bx(bx_rope_rows_f16(qd, qd, M, HD, n_q, pos_d, cs, sn, batch_cap_, st), "forward_batch rope q");
-        hipx::bx(bx_rope_rows_f16(kd, kd, M, HD, n_kv, pos_d, cs, sn, batch_cap_, st), "forward_batch rope k");
-        std::uint16_t* Kp = arena + static_cast<std::size_t>(2 * l) * plane_rows * width;
-        std::uint16_t* Vp = Kp + static_cast<std::size_t>(plane_rows) * width;
-        hipx::bx(bx_kv_append_rows_f16(kd, static_cast<const uint16_t*>(v_.data), M, width, dst_d, Kp, Vp,
-                                       plane_rows, st),
-                 "forward_batch kv append");
-        hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, max_len, n_q, n_kv, HD,
-                                         static_cast<uint16_t*>(attn_.data), attn_ws_.data, st),
-                 "forward_batch attention");
-        linear_batched(layer.Wo, nullptr, attn_, proj_);
-        bt::add_inplace(h_, proj_);
-        bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_);
-        linear_batched(layer.gate_W, nullptr, norm_, gate_);
-        linear_batched(layer.up_W, nullptr, norm_, up_);
-        bt::silu_forward(gate_, gate_);
-        bt::mul_inplace(gate_, up_);
-        linear_batched(layer.down_W, nullptr, gate_, proj_);
-        bt::add_inplace(h_, proj_);
+        hipx::check(hipGraphLaunch(g.exec[mi], st), "hipGraphLaunch");
     }
-    bt::rms_norm_forward(h_, final_norm_, eps, norm_);
-    linear_batched(lm_head_, nullptr, norm_, logits_out);
+    logits_out = bt::Tensor::view(bt::Device::ROCm, blogits_.data, M, cfg_.vocab_size, bt::Dtype::FP16);
     for (int r = 0; r < M; ++r) ++slot_len_[static_cast<std::size_t>(slots[r])];
 }
 

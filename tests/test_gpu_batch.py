@@ -150,3 +150,37 @@ def test_batch_errors_raise(ba, small_gguf):
     m.forward_batch([1], [0])
     assert m.slot_len(0) == 8
     m.close()
+
+
+def test_batched_graph_replays_equal_eager(ba, small_gguf, monkeypatch):
+    """The second step of a given M is captured into a hipGraph and later steps
+    replay it; every replay must equal the eager step bit for bit, also with
+    other device work (a prefill into another slot, single-sequence steps) and
+    host synchronisation between the replays."""
+    print("[batch] graph vs eager", flush=True)
+    models = {}
+    for mode in ("graph", "eager"):
+        if mode == "eager":
+            monkeypatch.setenv("BROLM_NO_GRAPH", "1")
+        m = _model(ba, small_gguf, "qwen3")
+        m.allocate_cache(32)
+        m.allocate_batch(6, 48)
+        monkeypatch.delenv("BROLM_NO_GRAPH", raising=False)
+        models[mode] = m
+    V = models["graph"].cfg.vocab_size
+    rng = np.random.default_rng(3)
+    for s, n in zip(range(4), (3, 9, 1, 5)):
+        prompt = rng.integers(0, V, n).tolist()
+        for m in models.values():
+            m.prefill_slot(s, prompt)
+    for step in range(6):
+        ids = rng.integers(0, V, 4).tolist()
+        order = rng.permutation(4).tolist()
+        out = {k: m.forward_batch(ids, order) for k, m in models.items()}
+        assert np.array_equal(out["graph"], out["eager"]), f"step {step}"
+        # unrelated device work between replays
+        for m in models.values():
+            m.prefill_slot(5, [int(step) + 1])
+            m.forward_last([7])
+    for m in models.values():
+        m.close()
