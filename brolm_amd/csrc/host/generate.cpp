@@ -93,50 +93,76 @@ int sample_token_device(const brotensor::Tensor& logits, const SamplingParams& p
     return out;
 }
 
+namespace {
+
+// softmax(logits / T) with the reference's arithmetic (generate.cpp:68-142):
+// FP32 exponentials against the FP32 maximum, their sum in FP64, and one FP32
+// reciprocal of that sum applied to every term.
+std::vector<float> tempered_probs(const float* logits, int vocab, float temperature) {
+    const float inv_t = 1.0f / temperature;
+    const float top = inv_t * *std::max_element(logits, logits + vocab, [inv_t](float a, float b) {
+        return a * inv_t < b * inv_t;
+    });
+    std::vector<float> pr(logits, logits + vocab);
+    double total = 0.0;
+    for (float& v : pr) {
+        v = std::exp(v * inv_t - top);
+        total += v;
+    }
+    const float scale = total > 0.0 ? static_cast<float>(1.0 / total) : 0.0f;
+    for (float& v : pr) v *= scale;
+    return pr;
+}
+
+// The candidate ids, most probable first, cut to top_k (0: no cut) and then
+// to the shortest prefix whose FP64 running sum reaches top_p (at least one
+// id).  Equal probabilities are ordered by id: the reference's std::sort
+// leaves their order open, and this is the order its restatement in the test
+// oracle uses.
+std::vector<int> candidates(const std::vector<float>& pr, int top_k, float top_p) {
+    const int V = static_cast<int>(pr.size());
+    std::vector<int> ids(pr.size());
+    std::iota(ids.begin(), ids.end(), 0);
+    auto before = [&pr](int a, int b) {
+        const float pa = pr[static_cast<std::size_t>(a)], pb = pr[static_cast<std::size_t>(b)];
+        return pa > pb || (pa == pb && a < b);
+    };
+    const int limit = top_k > 0 && top_k < V ? top_k : V;
+    std::partial_sort(ids.begin(), ids.begin() + limit, ids.end(), before);
+    ids.resize(static_cast<std::size_t>(limit));
+    if (top_p < 1.0f) {
+        double run = 0.0;
+        std::size_t n = 0;
+        while (n < ids.size()) {
+            run += pr[static_cast<std::size_t>(ids[n++])];
+            if (run >= static_cast<double>(top_p)) break;
+        }
+        ids.resize(std::max<std::size_t>(n, 1));
+    }
+    return ids;
+}
+
+}  // namespace
+
 int sample_token(const float* logits, int vocab, const SamplingParams& p, std::mt19937_64& rng) {
     profile::ScopedStage ps(profile::Stage::sample);
     if (vocab <= 0) return 0;
     if (p.temperature <= 0.0f || p.top_k == 1) return argmax(logits, vocab);
-    const float inv_t = 1.0f / p.temperature;
-    float max_logit = logits[0] * inv_t;
-    for (int i = 1; i < vocab; ++i) max_logit = std::max(max_logit, logits[i] * inv_t);
-    std::vector<float> probs(static_cast<std::size_t>(vocab));
-    double sum = 0.0;
-    for (int i = 0; i < vocab; ++i) {
-        const float e = std::exp(logits[i] * inv_t - max_logit);
-        probs[static_cast<std::size_t>(i)] = e;
-        sum += e;
+    const std::vector<float> pr = tempered_probs(logits, vocab, p.temperature);
+    const std::vector<int> ids = candidates(pr, p.top_k, p.top_p);
+    double mass = 0.0;
+    for (int i : ids) mass += pr[static_cast<std::size_t>(i)];
+    // a distribution with no mass left takes the first candidate without a draw
+    if (mass <= 0.0) return ids.front();
+    // one uniform draw in [0, 1) scaled by the kept mass, located against the
+    // running sum of the candidates in order
+    const double target = std::uniform_real_distribution<double>(0.0, 1.0)(rng) * mass;
+    double run = 0.0;
+    for (int i : ids) {
+        run += pr[static_cast<std::size_t>(i)];
+        if (target < run) return i;
     }
-    const float norm = sum > 0.0 ? static_cast<float>(1.0 / sum) : 0.0f;
-    for (float& v : probs) v *= norm;
-    std::vector<int> order(static_cast<std::size_t>(vocab));
-    std::iota(order.begin(), order.end(), 0);
-    std::sort(order.begin(), order.end(), [&](int a, int b) {
-        return probs[static_cast<std::size_t>(a)] > probs[static_cast<std::size_t>(b)];
-    });
-    std::size_t keep = static_cast<std::size_t>(vocab);
-    if (p.top_k > 0 && static_cast<std::size_t>(p.top_k) < keep) keep = static_cast<std::size_t>(p.top_k);
-    if (p.top_p < 1.0f) {
-        double cum = 0.0;
-        std::size_t nucleus = 0;
-        for (std::size_t i = 0; i < keep; ++i) {
-            cum += probs[static_cast<std::size_t>(order[i])];
-            ++nucleus;
-            if (cum >= static_cast<double>(p.top_p)) break;
-        }
-        keep = std::max<std::size_t>(nucleus, 1);
-    }
-    double kept = 0.0;
-    for (std::size_t i = 0; i < keep; ++i) kept += probs[static_cast<std::size_t>(order[i])];
-    if (kept <= 0.0) return order[0];
-    std::uniform_real_distribution<double> dist(0.0, 1.0);
-    const double r = dist(rng) * kept;
-    double acc = 0.0;
-    for (std::size_t i = 0; i < keep; ++i) {
-        acc += probs[static_cast<std::size_t>(order[i])];
-        if (r < acc) return order[i];
-    }
-    return order[keep - 1];
+    return ids.back();
 }
 
 }  // namespace brolm::detail
