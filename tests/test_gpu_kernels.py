@@ -333,6 +333,9 @@ def _attn_ref(q, K, V, L, valid, n_q, n_kv, hd, softcap=0.0, window=0, mask=None
 @pytest.mark.parametrize("L,valid,n_q,n_kv,hd", [
     (1, 1, 4, 2, 64), (1, 5, 16, 8, 128), (1, 64, 16, 8, 128), (1, 65, 16, 8, 128), (1, 300, 8, 8, 64),
     (1, 2049, 16, 8, 128), (1, 4096, 32, 8, 128), (4, 70, 4, 2, 64), (16, 600, 16, 8, 128),
+    # split-K head dims other than 64 / 128 (a partial last chunk per lane
+    # quad, two dims pairs per lane) and a GQA group of 8
+    (1, 300, 8, 2, 96), (2, 130, 8, 8, 256), (1, 77, 4, 1, 72), (3, 1000, 32, 4, 128), (1, 20000, 16, 8, 128),
     # L >= 16 rows: the MFMA flash-attention kernel (partial query and key
     # tiles, GQA groups 1..4, prompt-only and after a cached prefix)
     (17, 17, 4, 2, 64), (64, 64, 16, 8, 128), (65, 200, 32, 8, 128), (130, 130, 8, 8, 64),
