@@ -989,9 +989,16 @@ void DenseDecoder::enqueue_batch_(int M) {
     for (std::size_t l = 0; l < layers_.size(); ++l) {
         Layer& layer = layers_[l];
         bt::rms_norm_forward(bh_, layer.input_ln, eps, bnorm_);
-        linear_batched(layer.Wq, nullptr, bnorm_, bq_);
-        linear_batched(layer.Wk, nullptr, bnorm_, bk_);
-        linear_batched(layer.Wv, nullptr, bnorm_, bv_);
+        {
+            // one launch for the projections that share a weight type (the
+            // fused forms cover 3 <= M <= 16 on the matrix cores)
+            const bt::Tensor* w[3] = {&layer.Wq, &layer.Wk, &layer.Wv};
+            bt::Tensor* y[3] = {&bq_, &bk_, &bv_};
+            const int same = layer.Wv.dtype == layer.Wq.dtype ? 3 : 2;
+            int done = 0;
+            if (layer.Wk.dtype == layer.Wq.dtype && bt::linear_group_forward_batched(w, y, same, bnorm_)) done = same;
+            for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, bnorm_, *y[i]);
+        }
         bt::Tensor* q_attn = &bq_;
         bt::Tensor* k_attn = &bk_;
         if (cfg_.use_qk_norm) {
@@ -1012,15 +1019,21 @@ void DenseDecoder::enqueue_batch_(int M) {
         hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, batch_cap_, n_q, n_kv, HD,
                                          static_cast<uint16_t*>(battn_.data), bws_.data, st),
                  "forward_batch attention");
-        linear_batched(layer.Wo, nullptr, battn_, bproj_);
-        bt::add_inplace(bh_, bproj_);
+        if (!bt::linear_residual_forward_batched(layer.Wo, battn_, bh_)) {
+            linear_batched(layer.Wo, nullptr, battn_, bproj_);
+            bt::add_inplace(bh_, bproj_);
+        }
         bt::rms_norm_forward(bh_, layer.post_attn_ln, eps, bnorm_);
-        linear_batched(layer.gate_W, nullptr, bnorm_, bgate_);
-        linear_batched(layer.up_W, nullptr, bnorm_, bup_);
-        bt::silu_forward(bgate_, bgate_);
-        bt::mul_inplace(bgate_, bup_);
-        linear_batched(layer.down_W, nullptr, bgate_, bproj_);
-        bt::add_inplace(bh_, bproj_);
+        if (!bt::linear_swiglu_forward_batched(layer.gate_W, layer.up_W, bnorm_, bgate_)) {
+            linear_batched(layer.gate_W, nullptr, bnorm_, bgate_);
+            linear_batched(layer.up_W, nullptr, bnorm_, bup_);
+            bt::silu_forward(bgate_, bgate_);
+            bt::mul_inplace(bgate_, bup_);
+        }
+        if (!bt::linear_residual_forward_batched(layer.down_W, bgate_, bh_)) {
+            linear_batched(layer.down_W, nullptr, bgate_, bproj_);
+            bt::add_inplace(bh_, bproj_);
+        }
     }
     bt::rms_norm_forward(bh_, final_norm_, eps, bnorm_);
     linear_batched(lm_head_, nullptr, bnorm_, blogits_);

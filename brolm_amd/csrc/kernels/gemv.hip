@@ -18,6 +18,15 @@ int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
              hipStream_t st);
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
               hipStream_t st);
+int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
+                    int M, int K, hipStream_t st);
+int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st);
+int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
+                     hipStream_t st);
+
+// The fused linear forms run on the MFMA tile GEMM (M >= 128, K % 64 == 0)
+// and, for decode batches, on the MFMA GEMV (3 <= M <= 16, K % 256 == 0).
+inline bool fused_gemv_ok(int M, int K) { return M >= 3 && M <= 16 && K % 256 == 0; }
 
 namespace {
 
@@ -210,7 +219,7 @@ extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, con
     return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
 }
 
-extern "C" int bx_linear_tiles_ok(int M, int K) { return bx::gemm_tiles_ok(M, K) ? 1 : 0; }
+extern "C" int bx_linear_tiles_ok(int M, int K) { return (bx::gemm_tiles_ok(M, K) || bx::fused_gemv_ok(M, K)) ? 1 : 0; }
 
 extern "C" int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N,
                                    const uint16_t* X, int M, int K, void* stream) {
@@ -219,7 +228,9 @@ extern "C" int bx_linear_group_f16(int wtype, int n, const void* const* W, uint1
         if (int rc = bx::check_linear_shape(wtype, M, N[i], K)) return rc;
         if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group: null pointer");
     }
-    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_group: needs M >= 128, K % 64 == 0");
+    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_group(wtype, n, W, Y, N, X, M, K, bx::as_stream(stream));
+    if (!bx::gemm_tiles_ok(M, K))
+        return bx::fail(BX_EUNSUPPORTED, "linear_group: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_group_f16(wtype, n, W, Y, N, X, M, K, bx::as_stream(stream));
 }
 
@@ -227,7 +238,9 @@ extern "C" int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* 
                                       void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
     if (!W || !X || !H) return bx::fail(BX_EINVAL, "linear_residual: null pointer");
-    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_residual: needs M >= 128, K % 64 == 0");
+    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_resid(wtype, W, X, H, M, N, K, bx::as_stream(stream));
+    if (!bx::gemm_tiles_ok(M, K))
+        return bx::fail(BX_EUNSUPPORTED, "linear_residual: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_resid_f16(wtype, W, X, H, M, N, K, bx::as_stream(stream));
 }
 
@@ -235,6 +248,8 @@ extern "C" int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, c
                                     int F, int K, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, F, K)) return rc;
     if (!Wg || !Wu || !X || !Y) return bx::fail(BX_EINVAL, "linear_swiglu: null pointer");
-    if (!bx::gemm_tiles_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_swiglu: needs M >= 128, K % 64 == 0");
+    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_swiglu(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
+    if (!bx::gemm_tiles_ok(M, K))
+        return bx::fail(BX_EUNSUPPORTED, "linear_swiglu: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_swiglu_f16(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
 }

@@ -279,15 +279,40 @@ struct SliceBuf {
     }
 };
 
+// What one launch computes.  STORE: Y[0] = f16(X W[0]^T + bias) (one weight)
+// or up to three weights sharing X, each into its own Y[i] (q / k / v): the
+// tile index runs over the members' row tiles in order.  RESID: the FP32
+// residual H (Mr, N[0]) += f16(X W[0]^T).  SWIGLU: gate W[0] and up W[1] rows
+// of the same tile, Y[0] = f16(f16(silu(f16(gate))) * f16(up)), the values the
+// separate linear, silu and mul kernels give.
+enum : int { MEPI_STORE = 0, MEPI_RESID = 1, MEPI_SWIGLU = 2 };
+struct MfmaJob {
+    const void* W[3];
+    uint16_t* Y[3];
+    float* H;
+    const uint16_t* bias;   // STORE with one member only
+    int N[3];
+    int64_t tiles_n[3];
+    int members;
+    int64_t tiles;          // total tiles of the launch
+};
+
+// Tile t of the launch -> (member, row tile within the member).
+__device__ __forceinline__ void member_of(const MfmaJob& job, int64_t t, int& mem, int64_t& lt) {
+    mem = 0;
+    lt = t;
+    while (mem + 1 < job.members && lt >= job.tiles_n[mem]) lt -= job.tiles_n[mem++];
+}
+
 // kpart: waves per tile.  1: every wave walks whole tiles (grid-stride);
 // 2, 4, 8: the workgroup takes 8 / kpart tiles, each split along K over kpart
 // waves whose partial tiles are added in LDS.
-template <int FMT>
-__global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict__ W, const uint16_t* __restrict__ X,
-                                                        const uint16_t* __restrict__ bias, uint16_t* __restrict__ Y,
-                                                        int Mr, int N, int K, int kpart) {
+template <int FMT, int EPI>
+__global__ __launch_bounds__(kThr) void gemv_mfma_kernel(MfmaJob job, const uint16_t* __restrict__ X, int Mr, int K,
+                                                        int kpart) {
     extern __shared__ __align__(16) uint32_t smem[];
     constexpr bool kSwz = FMT != FMT_F16;
+    constexpr bool kTwo = EPI == MEPI_SWIGLU;   // gate and up rows per tile
     const int xstride = K / 2 + 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -298,7 +323,7 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
     xst.xs2 = xs2;
     float* red = reinterpret_cast<float*>(xs2 + (FMT == FMT_Q4_K ? (K / 32) * 16 : 0));
     const int nch = K / 256;
-    const int64_t tiles = ((int64_t)N + 15) / 16;
+    const int64_t tiles = job.tiles;
     Walk w;
     w.tiles = tiles;
     if (kpart == 1) {
@@ -315,11 +340,20 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
     }
     w.cb = w.c0;
     const int64_t w0tile = w.tile;
+    // the slice loads of a walk position: its member's weight (and the up
+    // weight for SwiGLU) at the member's own row tile
+    auto load = [&](SliceBuf<FMT>& bg, SliceBuf<FMT>& bu, const Walk& at) {
+        int mem;
+        Walk lw = at;
+        member_of(job, at.tile, mem, lw.tile);
+        const int N = job.N[mem];
+        bg.load(job.W[mem], EPI == MEPI_STORE ? job.bias : nullptr, N, K, lw, r, g);
+        if constexpr (kTwo) bu.load(job.W[1], nullptr, N, K, lw, r, g);
+    };
 
     // the first slice's weights stream while the activations are staged
-    constexpr int SB = SliceLen<FMT>::SB;
-    SliceBuf<FMT> b0, b1;
-    if (w.valid()) b0.load(W, bias, N, K, w, r, g);
+    SliceBuf<FMT> b0, b1, u0, u1;
+    if (w.valid()) load(b0, u0, w);
     stage_x_f16<kSwz, false>(X, K, Mr, K, smem, xstride, nullptr, 0);
     for (int i = threadIdx.x; i < xstride; i += kThr) smem[Mr * xstride + i] = 0u;
     __syncthreads();
@@ -345,17 +379,33 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
         __syncthreads();
     }
 
-    f4v acc = {0.f, 0.f, 0.f, 0.f};
-    auto finish = [&](int64_t tile, float bv) {
-        const int64_t n = tile * 16 + r;
-        if (n < N) {
+    f4v acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    // the epilogue of tile `tile` from lane values a (and u for SwiGLU)
+    auto store = [&](int64_t tile, const f4v& a, const f4v& u, float bv) {
+        int mem;
+        int64_t lt;
+        member_of(job, tile, mem, lt);
+        const int N = job.N[mem];
+        const int64_t n = lt * 16 + r;
+        if (n >= N) return;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int m = 4 * g + j;
-                if (m < Mr) Y[(int64_t)m * N + n] = f2h(acc[j] + bv);
+        for (int j = 0; j < 4; ++j) {
+            const int m = 4 * g + j;
+            if (m >= Mr) continue;
+            if constexpr (EPI == MEPI_RESID) {
+                job.H[(int64_t)m * N + n] += h2f(f2h(a[j]));
+            } else if constexpr (EPI == MEPI_SWIGLU) {
+                const float act = h2f(f2h(silu_f32(h2f(f2h(a[j])))));
+                job.Y[0][(int64_t)m * N + n] = f2h(act * h2f(f2h(u[j])));
+            } else {
+                job.Y[mem][(int64_t)m * N + n] = f2h(a[j] + bv);
             }
         }
+    };
+    auto finish = [&](int64_t tile, float bv) {
+        store(tile, acc, accu, bv);
         acc = f4v{0.f, 0.f, 0.f, 0.f};
+        accu = f4v{0.f, 0.f, 0.f, 0.f};
     };
     // The next slice's loads are issued before the current slice's math and
     // unconditionally (past the end they repeat the current slice), so the
@@ -363,18 +413,20 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
     float bv = 0.f;
     if (w.valid()) {
         for (;;) {
-            Walk nx = w.next(SB);
-            b1.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
-            if (w.cb == w.c0) bv = bias ? h2f(b0.bias & 0xffff) : 0.f;
+            Walk nx = w.next(SliceLen<FMT>::SB);
+            load(b1, u1, nx.valid() ? nx : w);
+            if (w.cb == w.c0) bv = (EPI == MEPI_STORE && job.bias) ? h2f(b0.bias & 0xffff) : 0.f;
             b0.mul(xst, w, r, g, acc);
-            if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
+            if constexpr (kTwo) u0.mul(xst, w, r, g, accu);
+            if (kpart == 1 && w.last_of_tile(SliceLen<FMT>::SB)) finish(w.tile, bv);
             w = nx;
             if (!w.valid()) break;
-            nx = w.next(SB);
-            b0.load(W, bias, N, K, nx.valid() ? nx : w, r, g);
-            if (w.cb == w.c0) bv = bias ? h2f(b1.bias & 0xffff) : 0.f;
+            nx = w.next(SliceLen<FMT>::SB);
+            load(b0, u0, nx.valid() ? nx : w);
+            if (w.cb == w.c0) bv = (EPI == MEPI_STORE && job.bias) ? h2f(b1.bias & 0xffff) : 0.f;
             b1.mul(xst, w, r, g, acc);
-            if (kpart == 1 && w.last_of_tile(SB)) finish(w.tile, bv);
+            if constexpr (kTwo) u1.mul(xst, w, r, g, accu);
+            if (kpart == 1 && w.last_of_tile(SliceLen<FMT>::SB)) finish(w.tile, bv);
             w = nx;
             if (!w.valid()) break;
         }
@@ -382,31 +434,34 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(const void* __restrict_
     if (kpart > 1) {
         // partial tiles -> LDS -> the first wave of each tile adds and writes
         *reinterpret_cast<f4v*>(red + (wave * 64 + lane) * 4) = acc;
+        if constexpr (kTwo) *reinterpret_cast<f4v*>(red + ((kWav + wave) * 64 + lane) * 4) = accu;
         __syncthreads();
         if (wave % kpart == 0 && w0tile < tiles) {
-            f4v s = {0.f, 0.f, 0.f, 0.f};
-            for (int v = wave; v < wave + kpart; ++v) s += *reinterpret_cast<const f4v*>(red + (v * 64 + lane) * 4);
-            acc = s;
-            const int64_t n = w0tile * 16 + r;
-            finish(w0tile, (bias && n < N) ? h2f(bias[n]) : 0.f);
+            f4v s = {0.f, 0.f, 0.f, 0.f}, su = {0.f, 0.f, 0.f, 0.f};
+            for (int v = wave; v < wave + kpart; ++v) {
+                s += *reinterpret_cast<const f4v*>(red + (v * 64 + lane) * 4);
+                if constexpr (kTwo) su += *reinterpret_cast<const f4v*>(red + ((kWav + v) * 64 + lane) * 4);
+            }
+            int mem;
+            int64_t lt;
+            member_of(job, w0tile, mem, lt);
+            const int64_t n = lt * 16 + r;
+            store(w0tile, s, su, (EPI == MEPI_STORE && job.bias && n < job.N[mem]) ? h2f(job.bias[n]) : 0.f);
         }
     }
 }
 
-size_t mfma_lds_bytes(int fmt, int Mr, int K) {
+size_t mfma_lds_bytes(int fmt, int Mr, int K, bool two = false) {
     size_t b = (size_t)(Mr + 1) * (K / 2 + 4) * 4;
     if (fmt == FMT_Q4_K) b += (size_t)(K / 32) * 16 * 4;
-    return b + (size_t)kWav * 64 * 4 * 4;
+    return b + (size_t)(two ? 2 : 1) * kWav * 64 * 4 * 4;
 }
 
 constexpr size_t kMaxLds = 160 * 1024;
 
-}  // namespace
-
-// 1 <= M <= 16, K % 256 == 0 (the linear entry point sends 3 <= M <= 16).
-// Activations in row chunks whose staging fits the workgroup's LDS.
-int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-              hipStream_t st) {
+// Launch a job for M rows of X, in row chunks whose staging fits the LDS.
+template <int EPI>
+int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStream_t st) {
     int fmt;
     switch (wtype) {
         case BX_TYPE_Q4_K: fmt = FMT_Q4_K; break;
@@ -416,19 +471,28 @@ int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X,
         default: return fail(BX_EUNSUPPORTED, "gemv mfma: unsupported type");
     }
     if (K % 256 != 0) return fail(BX_EUNSUPPORTED, "gemv mfma: K must be a multiple of 256");
+    const bool two = EPI == MEPI_SWIGLU;
     int mc = M;
-    while (mc > 1 && mfma_lds_bytes(fmt, mc, K) > kMaxLds) mc = (mc + 1) / 2;
-    if (mfma_lds_bytes(fmt, mc, K) > kMaxLds) return fail(BX_EUNSUPPORTED, "gemv mfma: K too large for LDS staging");
-    const int64_t tiles = ((int64_t)N + 15) / 16;
+    while (mc > 1 && mfma_lds_bytes(fmt, mc, K, two) > kMaxLds) mc = (mc + 1) / 2;
+    if (mfma_lds_bytes(fmt, mc, K, two) > kMaxLds) return fail(BX_EUNSUPPORTED, "gemv mfma: K too large for LDS staging");
+    job.tiles = 0;
+    for (int i = 0; i < job.members; ++i) {
+        job.tiles_n[i] = ((int64_t)job.N[i] + 15) / 16;
+        job.tiles += job.tiles_n[i];
+    }
+    const int64_t tiles = job.tiles;
     const int nch = K / 256;
     const int cus = num_cus();
     for (int m0 = 0; m0 < M; m0 += mc) {
         const int mr = M - m0 < mc ? M - m0 : mc;
-        const size_t lds = mfma_lds_bytes(fmt, mr, K);
+        const size_t lds = mfma_lds_bytes(fmt, mr, K, two);
+        MfmaJob jc = job;
+        for (int i = 0; i < job.members; ++i)
+            if (jc.Y[i]) jc.Y[i] += (int64_t)m0 * job.N[i];
+        if (jc.H) jc.H += (int64_t)m0 * job.N[0];
         const uint16_t* Xc = X + (int64_t)m0 * K;
-        uint16_t* Yc = Y + (int64_t)m0 * N;
         BX_DISPATCH_FMT(wtype, {
-            const void* fn = reinterpret_cast<const void*>(&gemv_mfma_kernel<FMT_>);
+            const void* fn = reinterpret_cast<const void*>(&gemv_mfma_kernel<FMT_, EPI>);
             if (lds > 64 * 1024) {
                 const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
                 if (e != hipSuccess) return hip_check(e, "gemv mfma: LDS attribute");
@@ -443,11 +507,57 @@ int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X,
             while (kpart * 2 <= kWav && kpart * 2 <= nch && (tiles * kpart * 2 + kWav - 1) / kWav <= slots) kpart *= 2;
             int64_t grid = (tiles * kpart + kWav - 1) / kWav;
             if (kpart == 1 && grid > slots) grid = slots;
-            gemv_mfma_kernel<FMT_><<<(unsigned)grid, kThr, lds, st>>>(W, Xc, bias, Yc, mr, N, K, kpart);
+            gemv_mfma_kernel<FMT_, EPI><<<(unsigned)grid, kThr, lds, st>>>(jc, Xc, mr, K, kpart);
         })
         if (int rc = launch_check("gemv mfma")) return rc;
     }
     return BX_OK;
+}
+
+}  // namespace
+
+// 1 <= M <= 16, K % 256 == 0 (the linear entry point sends 3 <= M <= 16).
+int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+              hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = W;
+    job.Y[0] = Y;
+    job.N[0] = N;
+    job.bias = bias;
+    job.members = 1;
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st);
+}
+
+int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
+                    int M, int K, hipStream_t st) {
+    MfmaJob job{};
+    for (int i = 0; i < n; ++i) {
+        job.W[i] = W[i];
+        job.Y[i] = Y[i];
+        job.N[i] = N[i];
+    }
+    job.members = n;
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st);
+}
+
+int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = W;
+    job.N[0] = N;
+    job.H = H;
+    job.members = 1;
+    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, st);
+}
+
+int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
+                     hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = Wg;
+    job.W[1] = Wu;
+    job.Y[0] = Y;
+    job.N[0] = F;
+    job.members = 1;   // one tile space; each tile takes the same rows of both
+    return mfma_launch<MEPI_SWIGLU>(wtype, job, X, M, K, st);
 }
 
 }  // namespace bx

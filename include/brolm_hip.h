@@ -80,8 +80,10 @@ int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t
 
 /* Fused prefill forms of the linears of src/detail/dense_decoder.cpp:526-681
  * (the op sequence linear / silu / mul / add_inplace, with the same
- * roundings).  They take the MFMA tile path only: 1 when (M, K) qualify
- * (M >= 128, K a multiple of 64), else 0 and the caller runs the unfused ops.
+ * roundings).  bx_linear_tiles_ok is 1 when (M, K) qualify: M >= 128 with K a
+ * multiple of 64 (the MFMA tile GEMM) or 3 <= M <= 16 with K a multiple of
+ * 256 (the MFMA GEMV of decode batches); else 0 and the caller runs the
+ * unfused ops.
  * bx_linear_group_f16: n (1..3) weights of one type sharing X (q / k / v
  *   projections), Y[i] (M, N[i]) FP16, one launch.
  * bx_linear_residual_f16: H (M, N) FP32 += f16(X W^T) (o / down projection

@@ -138,14 +138,17 @@ def _weights(rng, t, N, K):
     return carrier(t, raw, N, K), Wv
 
 
+@pytest.mark.parametrize("M,K,Ns", [(300, 512, (384, 128, 128)), (5, 512, (384, 136, 136)),
+                                    (16, 512, (256, 120, 120)), (16, 6144, (64, 48, 48))])
 @pytest.mark.parametrize("t", QTYPES + [1])
-def test_fused_prefill_linears_equal_unfused_ops(t):
+def test_fused_prefill_linears_equal_unfused_ops(t, M, K, Ns):
     """bx_linear_group / _residual / _swiglu give bit-identical results to the
     separate linear, add_inplace, silu and mul launches they replace (same
-    MFMA tile arithmetic, same FP16 roundings); below 128 rows they decline."""
-    rng = np.random.default_rng(900 + t)
-    M, K = 300, 512
-    Ns = (384, 128, 128)
+    MFMA arithmetic, same FP16 roundings): the tile GEMM at M >= 128, the MFMA
+    GEMV of decode batches at 3 <= M <= 16 (partial row tiles; K = 6144 in two
+    row chunks of staged activations); other M decline."""
+    print(f"[fused] t={t} M={M} K={K} N={Ns}", flush=True)
+    rng = np.random.default_rng(900 + t + M)
     ws = [_weights(rng, t, n, K)[0] for n in Ns]
     X = _f16(rng.standard_normal((M, K)))
     x = f16_dev(X)
@@ -179,8 +182,8 @@ def test_fused_prefill_linears_equal_unfused_ops(t):
     call("bx_silu_f16", ptr(g), ptr(g), M * Ns[1], stream())
     call("bx_mul_f16", ptr(g), ptr(u), M * Ns[1], stream())
     assert np.array_equal(host(act), host(g))
-    # below the tile path: declined, nothing written
-    assert h.bx_linear_tiles_ok(100, K) == 0 and h.bx_linear_tiles_ok(M, K) == 1
+    # between the two paths: declined, nothing written
+    assert h.bx_linear_tiles_ok(100, K) == 0 and h.bx_linear_tiles_ok(2, K) == 0 and h.bx_linear_tiles_ok(M, K) == 1
     assert h.bx_linear_residual_f16(t, ptr(ws[0]), ptr(x), ptr(Hf), 100, Ns[0], K, stream()) == -3  # BX_EUNSUPPORTED
 
 
