@@ -383,11 +383,28 @@ void DenseDecoder::run_layers_encode_(int L, bt::Tensor& hidden_out) {
         dst.rows = src.rows;
         dst.cols = num_heads * HD;
     };
+    const bool f16 = prefill_f16_(L);
+    auto pick = [f16](const bt::Tensor& q, const bt::Tensor& c) -> const bt::Tensor& {
+        return f16 && c.data ? c : q;
+    };
     for (Layer& layer : layers_) {
+        const bt::Tensor& Wq = pick(layer.Wq, layer.q16);
+        const bt::Tensor& Wk = pick(layer.Wk, layer.k16);
+        const bt::Tensor& Wv = pick(layer.Wv, layer.v16);
+        const bt::Tensor& Wo = pick(layer.Wo, layer.o16);
+        const bt::Tensor& Wg = pick(layer.gate_W, layer.gate16);
+        const bt::Tensor& Wu = pick(layer.up_W, layer.up16);
+        const bt::Tensor& Wd = pick(layer.down_W, layer.down16);
         bt::rms_norm_forward(h_, layer.input_ln, eps, norm_);
-        linear_batched(layer.Wq, nullptr, norm_, q_);
-        linear_batched(layer.Wk, nullptr, norm_, k_);
-        linear_batched(layer.Wv, nullptr, norm_, v_);
+        {
+            // the fused forms where the shape allows (same results as the ops)
+            const bt::Tensor* w[3] = {&Wq, &Wk, &Wv};
+            bt::Tensor* y[3] = {&q_, &k_, &v_};
+            const int same = Wv.dtype == Wq.dtype ? 3 : 2;
+            int done = 0;
+            if (Wk.dtype == Wq.dtype && bt::linear_group_forward_batched(w, y, same, norm_)) done = same;
+            for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, norm_, *y[i]);
+        }
         bt::Tensor* q_attn = &q_;
         bt::Tensor* k_attn = &k_;
         if (cfg_.use_qk_norm) {
@@ -399,18 +416,74 @@ void DenseDecoder::run_layers_encode_(int L, bt::Tensor& hidden_out) {
         bt::rope_forward(*q_attn, HD, n_q, 0, cfg_.rope_theta, *q_attn);
         bt::rope_forward(*k_attn, HD, n_kv, 0, cfg_.rope_theta, *k_attn);
         bt::flash_attention_gqa_forward(*q_attn, *k_attn, v_, n_q, n_kv, /*causal=*/false, attn_);
-        linear_batched(layer.Wo, nullptr, attn_, proj_);
-        bt::add_inplace(h_, proj_);
+        if (!bt::linear_residual_forward_batched(Wo, attn_, h_)) {
+            linear_batched(Wo, nullptr, attn_, proj_);
+            bt::add_inplace(h_, proj_);
+        }
         bt::rms_norm_forward(h_, layer.post_attn_ln, eps, norm_);
-        linear_batched(layer.gate_W, nullptr, norm_, gate_);
-        linear_batched(layer.up_W, nullptr, norm_, up_);
-        bt::silu_forward(gate_, gate_);
-        bt::mul_inplace(gate_, up_);
-        linear_batched(layer.down_W, nullptr, gate_, proj_);
-        bt::add_inplace(h_, proj_);
+        if (!(Wg.dtype == Wu.dtype && bt::linear_swiglu_forward_batched(Wg, Wu, norm_, gate_))) {
+            linear_batched(Wg, nullptr, norm_, gate_);
+            linear_batched(Wu, nullptr, norm_, up_);
+            bt::silu_forward(gate_, gate_);
+            bt::mul_inplace(gate_, up_);
+        }
+        if (!bt::linear_residual_forward_batched(Wd, gate_, h_)) {
+            linear_batched(Wd, nullptr, gate_, proj_);
+            bt::add_inplace(h_, proj_);
+        }
     }
     bt::rms_norm_forward(h_, final_norm_, eps, norm_);
     hidden_out = norm_.clone();
+}
+
+// ─── FP16 layer copies for long prompts ─────────────────────────────────────
+//
+// A pass over L >= 512 rows is bound by the matrix cores, and the FP16 tiles
+// run about a fifth faster than the quantized ones, which dequantize inside
+// their K loop.  With HBM to spare (288 GB on this part), the first such pass
+// dequantizes every quantized layer matrix once into an FP16 copy held by the
+// layer, and every long pass after it multiplies those.  The copies are made
+// only if the device keeps at least max(8 GB, 10 %) free afterwards, and never
+// for single-token or batched decode, which stay on the quantized weights
+// (there the step is bound by weight bytes).  BROLM_PREFILL_F16=0 turns them off.
+// The weights multiplied are the FP16 roundings the quantized tiles form, so
+// results are those of the op path's tile GEMM to its stated tolerance.
+
+bool DenseDecoder::prefill_f16_(int L) {
+    constexpr int kRows = 512;
+    if (L < kRows) return false;
+    if (f16_state_ != 0) return f16_state_ > 0;
+    f16_state_ = -1;
+    if (const char* e = std::getenv("BROLM_PREFILL_F16"); e && e[0] == '0') return false;
+    auto quant = [](const bt::Tensor& t) { return t.dtype == bt::Dtype::Q4_K || t.dtype == bt::Dtype::Q6_K ||
+                                                  t.dtype == bt::Dtype::Q8_0; };
+    std::size_t need = 0;
+    for (const Layer& ly : layers_)
+        for (const bt::Tensor* t : {&ly.Wq, &ly.Wk, &ly.Wv, &ly.Wo, &ly.gate_W, &ly.up_W, &ly.down_W})
+            if (quant(*t)) need += static_cast<std::size_t>(t->rows) * t->cols * 2;
+    if (need == 0) return false;
+    std::size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
+    const std::size_t keep = std::max<std::size_t>(std::size_t(8) << 30, total_b / 10);
+    if (free_b < need + keep) return false;
+    for (Layer& ly : layers_) {
+        auto copy = [&](const bt::Tensor& w, bt::Tensor& out) {
+            if (!quant(w)) return;
+            out = bt::Tensor::empty_on(bt::Device::ROCm, w.rows, w.cols, bt::Dtype::FP16);
+            hipx::bx(bx_dequant_to_f16(bt::dtype_to_ggml(w.dtype), w.data, static_cast<uint16_t*>(out.data), w.rows,
+                                       w.cols, bt::stream()),
+                     "FP16 layer copy");
+        };
+        copy(ly.Wq, ly.q16);
+        copy(ly.Wk, ly.k16);
+        copy(ly.Wv, ly.v16);
+        copy(ly.Wo, ly.o16);
+        copy(ly.gate_W, ly.gate16);
+        copy(ly.up_W, ly.up16);
+        copy(ly.down_W, ly.down16);
+    }
+    f16_state_ = 1;
+    return true;
 }
 
 // ─── op-surface layer stack (dense_decoder.cpp:526-681) ─────────────────────
@@ -430,17 +503,29 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
 
     namespace prof = profile;
     using PS = profile::Stage;
+    const bool f16 = prefill_f16_(L);
+    // the FP16 copy of a quantized matrix when long passes use them
+    auto pick = [f16](const bt::Tensor& q, const bt::Tensor& c) -> const bt::Tensor& {
+        return f16 && c.data ? c : q;
+    };
     for (Layer& layer : layers_) {
+        const bt::Tensor& Wq = pick(layer.Wq, layer.q16);
+        const bt::Tensor& Wk = pick(layer.Wk, layer.k16);
+        const bt::Tensor& Wv = pick(layer.Wv, layer.v16);
+        const bt::Tensor& Wo = pick(layer.Wo, layer.o16);
+        const bt::Tensor& Wg = pick(layer.gate_W, layer.gate16);
+        const bt::Tensor& Wu = pick(layer.up_W, layer.up16);
+        const bt::Tensor& Wd = pick(layer.down_W, layer.down16);
         { prof::ScopedStage ps(PS::rms_norm); bt::rms_norm_forward(h_, layer.input_ln, eps, norm_); }
         {
             // one launch for the projections that share a weight dtype
             // (q / k always, v too unless a Q4_K_M layer raised it)
             prof::ScopedStage ps(PS::qkv_proj);
-            const bt::Tensor* w[3] = {&layer.Wq, &layer.Wk, &layer.Wv};
+            const bt::Tensor* w[3] = {&Wq, &Wk, &Wv};
             bt::Tensor* y[3] = {&q_, &k_, &v_};
-            const int same = layer.Wv.dtype == layer.Wq.dtype ? 3 : 2;
+            const int same = Wv.dtype == Wq.dtype ? 3 : 2;
             int done = 0;
-            if (layer.Wk.dtype == layer.Wq.dtype && bt::linear_group_forward_batched(w, y, same, norm_)) done = same;
+            if (Wk.dtype == Wq.dtype && bt::linear_group_forward_batched(w, y, same, norm_)) done = same;
             for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, norm_, *y[i]);
         }
         bt::Tensor* q_attn = &q_;
@@ -465,8 +550,8 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
         bool fused_o;
         {
             prof::ScopedStage ps(PS::o_proj);  // o_proj and the residual add in one launch
-            fused_o = bt::linear_residual_forward_batched(layer.Wo, attn_, h_);
-            if (!fused_o) linear_batched(layer.Wo, nullptr, attn_, proj_);
+            fused_o = bt::linear_residual_forward_batched(Wo, attn_, h_);
+            if (!fused_o) linear_batched(Wo, nullptr, attn_, proj_);
         }
         if (!fused_o) {
             prof::ScopedStage ps(PS::residual_add);
@@ -476,10 +561,10 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
         bool fused_mlp;
         {
             prof::ScopedStage ps(PS::mlp_proj);  // gate / up projections with the SwiGLU in one launch
-            fused_mlp = bt::linear_swiglu_forward_batched(layer.gate_W, layer.up_W, norm_, gate_);
+            fused_mlp = Wg.dtype == Wu.dtype && bt::linear_swiglu_forward_batched(Wg, Wu, norm_, gate_);
             if (!fused_mlp) {
-                linear_batched(layer.gate_W, nullptr, norm_, gate_);
-                linear_batched(layer.up_W, nullptr, norm_, up_);
+                linear_batched(Wg, nullptr, norm_, gate_);
+                linear_batched(Wu, nullptr, norm_, up_);
             }
         }
         if (!fused_mlp) {
@@ -490,8 +575,8 @@ void DenseDecoder::run_layers_(int L, bt::Tensor& logits_out, bt::Tensor* hidden
         bool fused_down;
         {
             prof::ScopedStage ps(PS::mlp_proj);  // down and the residual add in one launch
-            fused_down = bt::linear_residual_forward_batched(layer.down_W, gate_, h_);
-            if (!fused_down) linear_batched(layer.down_W, nullptr, gate_, proj_);
+            fused_down = bt::linear_residual_forward_batched(Wd, gate_, h_);
+            if (!fused_down) linear_batched(Wd, nullptr, gate_, proj_);
         }
         if (!fused_down) {
             prof::ScopedStage ps(PS::residual_add);

@@ -46,6 +46,8 @@ struct Scratch {
     std::size_t attn_bytes = 0;
     void* argmax_ws = nullptr;
     std::size_t argmax_bytes = 0;
+    void* wdeq = nullptr;          // FP16 copies of quantized weights for long prompts
+    std::size_t wdeq_bytes = 0;
     float theta = 0.f;
     int hd = 0, rows = 0;
     float* cos_t = nullptr;
@@ -60,11 +62,11 @@ Scratch& scratch() {
 void release_scratch() {
     Scratch& S = scratch();
     std::lock_guard<std::mutex> lk(S.mu);
-    for (void* p : {S.attn_ws, S.argmax_ws, static_cast<void*>(S.cos_t), static_cast<void*>(S.sin_t)})
+    for (void* p : {S.attn_ws, S.argmax_ws, S.wdeq, static_cast<void*>(S.cos_t), static_cast<void*>(S.sin_t)})
         if (p) (void)hipFree(p);
-    S.attn_ws = S.argmax_ws = nullptr;
+    S.attn_ws = S.argmax_ws = S.wdeq = nullptr;
     S.cos_t = S.sin_t = nullptr;
-    S.attn_bytes = S.argmax_bytes = 0;
+    S.attn_bytes = S.argmax_bytes = S.wdeq_bytes = 0;
     S.rows = S.hd = 0;
 }
 
@@ -108,6 +110,38 @@ void rope_table(float theta, int hd, int rows, const float** c, const float** s,
     *have_rows = S.rows;
 }
 
+// Long prompts (M >= kDequantRows rows on the tile GEMM) run the FP16 tiles on
+// an FP16 copy of each quantized weight, dequantized once per call into the
+// op scratch: at these M the GEMM is bound by the matrix cores, where the
+// in-loop dequantization of the quantized tiles costs about a fifth of the
+// rate, while the copy costs one pass over the weight.  Either way the matrix
+// cores multiply each weight rounded once to FP16, the tile path's stated
+// difference from the GEMV path.
+constexpr int kDequantRows = 512;
+
+bool dequant_first(const Tensor& W, int M, int K) {
+    const bool quant = W.dtype == Dtype::Q4_K || W.dtype == Dtype::Q6_K || W.dtype == Dtype::Q8_0;
+    return quant && M >= kDequantRows && bx_linear_tiles_ok(M, K) == 1;
+}
+
+// FP16 copies of W[0..n) in the scratch (the caller holds scratch().mu);
+// out[i] points at W[i]'s copy.
+void dequant_weights(const Tensor* const* W, int n, const void** out) {
+    std::size_t total = 0;
+    for (int i = 0; i < n; ++i) total += ((std::size_t)W[i]->rows * W[i]->cols * 2 + 255) / 256 * 256;
+    Scratch& S = scratch();
+    auto* base = static_cast<uint8_t*>(grow(S.wdeq, S.wdeq_bytes, total));
+    std::size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(base + off);
+        hipx::bx(bx_dequant_to_f16(dtype_to_ggml(W[i]->dtype), W[i]->data, dst, W[i]->rows, W[i]->cols,
+                                   hipx::stream()),
+                 "dequantize weights for the FP16 tiles");
+        out[i] = dst;
+        off += ((std::size_t)W[i]->rows * W[i]->cols * 2 + 255) / 256 * 256;
+    }
+}
+
 void linear_impl(const char* op, Dtype expect, const Tensor& W, const Tensor* bias, const Tensor& X, Tensor& Y) {
     need_device(W, op, "W");
     need_device(X, op, "X");
@@ -124,6 +158,16 @@ void linear_impl(const char* op, Dtype expect, const Tensor& W, const Tensor* bi
     }
     if (Y.data == X.data) contract(op, "Y must not alias X");
     size_out(Y, X.rows, W.rows, Dtype::FP16);
+    if (dequant_first(W, X.rows, X.cols)) {
+        std::lock_guard<std::mutex> lk(scratch().mu);
+        const Tensor* w[1] = {&W};
+        const void* wf[1];
+        dequant_weights(w, 1, wf);
+        hipx::bx(bx_linear_f16(BX_TYPE_F16, wf[0], b, static_cast<const uint16_t*>(X.data),
+                               static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::stream()),
+                 op);
+        return;
+    }
     hipx::bx(bx_linear_f16(dtype_to_ggml(W.dtype), W.data, b, static_cast<const uint16_t*>(X.data),
                            static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::stream()),
              op);
@@ -177,8 +221,15 @@ bool linear_group_forward_batched(const Tensor* const* W, Tensor* const* Y, int 
         y[i] = static_cast<uint16_t*>(Y[i]->data);
         N[i] = W[i]->rows;
     }
-    hipx::bx(bx_linear_group_f16(dtype_to_ggml(W[0]->dtype), n, w, y, N, static_cast<const uint16_t*>(X.data), X.rows,
-                                 X.cols, hipx::stream()),
+    int wtype = dtype_to_ggml(W[0]->dtype);
+    std::unique_lock<std::mutex> lk(scratch().mu, std::defer_lock);
+    if (dequant_first(*W[0], X.rows, X.cols)) {
+        lk.lock();
+        dequant_weights(W, n, w);
+        wtype = BX_TYPE_F16;
+    }
+    hipx::bx(bx_linear_group_f16(wtype, n, w, y, N, static_cast<const uint16_t*>(X.data), X.rows, X.cols,
+                                 hipx::stream()),
              "linear_group_forward_batched");
     return true;
 }
@@ -187,8 +238,17 @@ bool linear_residual_forward_batched(const Tensor& W, const Tensor& X, Tensor& H
     if (!fused_ok(X, W) || H.dtype != Dtype::FP32 || H.device != Device::ROCm || H.rows != X.rows ||
         H.cols != W.rows)
         return false;
-    hipx::bx(bx_linear_residual_f16(dtype_to_ggml(W.dtype), W.data, static_cast<const uint16_t*>(X.data),
-                                    static_cast<float*>(H.data), X.rows, W.rows, W.cols, hipx::stream()),
+    const void* w = W.data;
+    int wtype = dtype_to_ggml(W.dtype);
+    std::unique_lock<std::mutex> lk(scratch().mu, std::defer_lock);
+    if (dequant_first(W, X.rows, X.cols)) {
+        lk.lock();
+        const Tensor* ws[1] = {&W};
+        dequant_weights(ws, 1, &w);
+        wtype = BX_TYPE_F16;
+    }
+    hipx::bx(bx_linear_residual_f16(wtype, w, static_cast<const uint16_t*>(X.data), static_cast<float*>(H.data), X.rows,
+                                    W.rows, W.cols, hipx::stream()),
              "linear_residual_forward_batched");
     return true;
 }
@@ -197,7 +257,16 @@ bool linear_swiglu_forward_batched(const Tensor& Wg, const Tensor& Wu, const Ten
     if (!fused_ok(X, Wg) || !fused_ok(X, Wu) || Wg.dtype != Wu.dtype || Wg.rows != Wu.rows || Y.data == X.data)
         return false;
     size_out(Y, X.rows, Wg.rows, Dtype::FP16);
-    hipx::bx(bx_linear_swiglu_f16(dtype_to_ggml(Wg.dtype), Wg.data, Wu.data, static_cast<const uint16_t*>(X.data),
+    const void* w[2] = {Wg.data, Wu.data};
+    int wtype = dtype_to_ggml(Wg.dtype);
+    std::unique_lock<std::mutex> lk(scratch().mu, std::defer_lock);
+    if (dequant_first(Wg, X.rows, X.cols)) {
+        lk.lock();
+        const Tensor* ws[2] = {&Wg, &Wu};
+        dequant_weights(ws, 2, w);
+        wtype = BX_TYPE_F16;
+    }
+    hipx::bx(bx_linear_swiglu_f16(wtype, w[0], w[1], static_cast<const uint16_t*>(X.data),
                                   static_cast<uint16_t*>(Y.data), X.rows, Wg.rows, Wg.cols, hipx::stream()),
              "linear_swiglu_forward_batched");
     return true;

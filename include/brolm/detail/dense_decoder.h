@@ -118,6 +118,9 @@ private:
         brotensor::Tensor post_attn_ln;
         brotensor::Tensor gate_W, up_W, down_W;
         brotensor::Tensor K_cache, V_cache;
+        // FP16 copies of the quantized matrices for long prompts (empty until
+        // the first one, and when they would not fit)
+        brotensor::Tensor q16, k16, v16, o16, gate16, up16, down16;
     };
 
     void run_layers_encode_(int L, brotensor::Tensor& hidden_out);
@@ -129,6 +132,7 @@ private:
     ::bx_decode_dims decode_dims_() const;
     void invalidate_graph_();
     void ensure_rope_table_();
+    bool prefill_f16_(int L);   // FP16 layer copies in use for an L-row pass
 
     DenseDecoderConfig cfg_;
     brotensor::Tensor embed_tokens_;
@@ -147,6 +151,7 @@ private:
     brotensor::Tensor attn_ws_;
 
     std::unique_ptr<DecodeGraphSession> graph_;
+    int f16_state_ = 0;   // FP16 layer copies: 0 not tried, 1 built, -1 declined
 
     // batched decode: per layer a K plane then a V plane, each
     // (n_slots * capacity, n_kv * head_dim) FP16; slot s, position p is row

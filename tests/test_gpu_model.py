@@ -306,3 +306,30 @@ def test_real_width_layers_long_context(ba, tmp_path_factory):
         a = m.forward_last([t])
         b = om.forward([t], last_only=True)[0]
         assert np.abs(a - b).max() <= LOGIT_TOL
+
+
+def test_long_prompt_fp16_layer_copies_match_oracle(ba, small_gguf, monkeypatch):
+    """A pass over >= 512 rows multiplies FP16 copies of the quantized layer
+    matrices (made once, when HBM allows); with BROLM_PREFILL_F16=0 it runs
+    the quantized tiles.  Both match the oracle to the logit tolerance, and the
+    decode steps after them stay on the quantized weights."""
+    print("[model] FP16 layer copies", flush=True)
+    om = oracle.Model(str(small_gguf))
+    om.allocate_cache(700)
+    V = 1000
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, V, 600).tolist()
+    want = om.forward(prompt, last_only=True)[0]
+    nxt = om.forward([7], last_only=True)[0]
+    got = {}
+    for mode in ("copies", "quantized"):
+        if mode == "quantized":
+            monkeypatch.setenv("BROLM_PREFILL_F16", "0")
+        m = _load(ba, small_gguf, cap=700)
+        got[mode] = m.forward_last(prompt)
+        step = m.forward_last([7])
+        monkeypatch.delenv("BROLM_PREFILL_F16", raising=False)
+        assert np.abs(got[mode] - want).max() <= LOGIT_TOL, mode
+        assert np.abs(step - nxt).max() <= LOGIT_TOL, mode
+        assert m.decode_mode() == "persistent"
+        m.close()
