@@ -245,18 +245,21 @@ def main() -> int:
     # prefill (timed separately, reported as an extra field)
     t0 = time.perf_counter()
     logits = model.forward_last(prompt)
-    prefill_s = time.perf_counter() - t0
+    prefill_first_s = time.perf_counter() - t0
     first = int(logits.argmax())
     t0 = time.perf_counter()
     model.truncate_cache(0)
     logits = model.forward_last(prompt)
-    prefill_s = min(prefill_s, time.perf_counter() - t0)
-    log(f"prefill {c['prompt']} tokens: {prefill_s * 1e3:.1f} ms")
+    prefill_s = min(prefill_first_s, time.perf_counter() - t0)
+    log(f"prefill {c['prompt']} tokens: {prefill_s * 1e3:.1f} ms (first pass {prefill_first_s * 1e3:.1f} ms)")
+    prefill_note = ("best of two prefills of the prompt; the first pass of 512+ rows also makes the model's FP16 "
+                    "copies of its layer matrices (once per model; included in prefill_first_ms)")
     if args.prefill_only:
         model.close()
         ba.shutdown()
         print(json.dumps({"metric": f"prefill tok/s {args.config}", "value": round(c["prompt"] / prefill_s, 1),
                           "unit": "tok/s", "prompt_tokens": c["prompt"], "ms": round(prefill_s * 1e3, 3),
+                          "prefill_first_ms": round(prefill_first_s * 1e3, 3), "note": prefill_note,
                           "data": "synthetic"}), flush=True)
         return 0
     # bidirectional encode (DenseDecoder::forward_encode, the LLM2Vec pass) of
@@ -364,6 +367,8 @@ def main() -> int:
         "weight_bytes_per_token": wbytes,
         "kv_bytes_per_token_avg": int(kv_bytes),
         "prefill_tok_s": round(c["prompt"] / prefill_s, 1),
+        "prefill_first_ms": round(prefill_first_s * 1e3, 3),
+        "prefill_note": prefill_note,
         "encode_tok_s": round(n_enc / encode_s, 1),
         "sampled_tok_s": sampled,
         "sampled_note": "generate, 64 tokens, T 0.8 / top-k 40 / top-p 0.95: device sampler vs host sampler",
