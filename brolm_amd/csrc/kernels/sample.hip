@@ -2,7 +2,8 @@
 // src/detail/generate.cpp:68-142, sample_token).  The reference sorts all V
 // probabilities on the host; here one workgroup finds the same thresholds by
 // bisection on the probability value, so nothing is sorted and only the
-// chosen id leaves the device:
+// chosen id leaves the device (the bisection runs over the few candidates a
+// histogram pass leaves when top-k or top-p cut the set, see below):
 //   p_i   = fp32(exp(l_i / T - max)) * fp32(1 / sum)  (sum in FP64), as the reference;
 //   M(v)  = sum of p_i >= v (FP64), C(v) = count of p_i >= v;
 //   top-k level  v_k = largest v with C(v) >= k   (k-th largest p);
@@ -73,11 +74,11 @@ __device__ void block_sum2(double& a, double& b, double* red) {
     __syncthreads();
 }
 
-// Mass (FP64) and count of p_i >= v among p_i >= floor_v.
-__device__ void mass_at(const float* p, int V, float v, float floor_v, double* red, double& mass, double& cnt) {
+// Mass (FP64) and count of p_i >= v among p_i >= floor_v, over n values.
+__device__ void mass_at(const float* p, int n, float v, float floor_v, double* red, double& mass, double& cnt) {
     double m = 0.0, c = 0.0;
     const float lo = fmaxf(v, floor_v);
-    for (int i = threadIdx.x; i < V; i += kST) {
+    for (int i = threadIdx.x; i < n; i += kST) {
         const float x = p[i];
         if (x >= lo) {
             m += x;
@@ -89,10 +90,30 @@ __device__ void mass_at(const float* p, int V, float v, float floor_v, double* r
     cnt = c;
 }
 
+// Candidate compaction.  A histogram of the probabilities by the top 13 bits
+// of their pattern (16 buckets per octave of (0, 1]) gives counts (integer) and
+// masses (fixed point, 2^-44 units, integer adds: the same totals in any
+// order) per bucket.  Walking down from the top bucket, the first bucket where
+// the running count reaches top_k (or, without top_k, the bucket below the one
+// where the running mass reaches top_p) bounds the final kept level from below,
+// so every id the selection can keep or draw has p at or above that bucket's
+// floor.  When at most kCand ids do, they are copied with their indices, in
+// index order, and the selection runs over them alone.
+constexpr int kBuckets = 2048;
+constexpr int kCand = 4096;
+constexpr double kFix = 17592186044416.0;   // 2^44
+
+// p in [0, 1] maps to buckets 0 .. 2032; anything else (a NaN from bad logits)
+// to the last bucket, so the histogram stays in bounds
+__device__ __forceinline__ int bucket_of(float x) { return min((int)(__float_as_uint(x) >> 19), kBuckets - 1); }
+
 __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict__ logits, int V, float inv_t,
                                                      int top_k, float top_p, double u, float* __restrict__ p,
                                                      int32_t* __restrict__ out) {
     __shared__ double red[kST];
+    __shared__ int cnt[kST];
+    __shared__ __align__(16) unsigned char pool[kCand * 8];   // histogram, then candidates
+    __shared__ int sh_floor, sh_n;
     float* redf = reinterpret_cast<float*>(red);
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < V; i += kST) mx = fmaxf(mx, h2f(logits[i]) * inv_t);
@@ -106,7 +127,75 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
     s = block_sum_d(s, red);
     const float norm = s > 0.0 ? (float)(1.0 / s) : 0.0f;
     for (int i = threadIdx.x; i < V; i += kST) p[i] *= norm;
+
+    // ---- candidate floor from the histogram
+    uint32_t* hcount = reinterpret_cast<uint32_t*>(pool);
+    unsigned long long* hmass = reinterpret_cast<unsigned long long*>(pool + kBuckets * 4);
+    for (int b = threadIdx.x; b < kBuckets; b += kST) {
+        hcount[b] = 0u;
+        hmass[b] = 0ull;
+    }
     __syncthreads();
+    if (top_k > 0 || top_p < 1.0f) {
+        for (int i = threadIdx.x; i < V; i += kST) {
+            const float x = p[i];
+            const int b = bucket_of(x);
+            atomicAdd(&hcount[b], 1u);
+            atomicAdd(&hmass[b], (unsigned long long)((double)x * kFix));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int fb = -1;   // the floor bucket; -1: no useful floor
+        if (top_k > 0 || top_p < 1.0f) {
+            uint32_t c = 0;
+            unsigned long long m = 0;
+            const unsigned long long target = top_p < 1.0f ? (unsigned long long)((double)top_p * kFix) : ~0ull;
+            for (int b = kBuckets - 1; b >= 0; --b) {
+                c += hcount[b];
+                m += hmass[b];
+                if (top_k > 0 && c >= (uint32_t)top_k) { fb = b; break; }
+                if (top_k <= 0 && m >= target) { fb = b > 0 ? b - 1 : 0; break; }
+            }
+        }
+        sh_floor = fb;
+    }
+    __syncthreads();
+    const int fb = sh_floor;
+    // ids at or above the floor bucket, counted per contiguous chunk (index order)
+    const int chunk = (V + kST - 1) / kST;
+    const int b0 = threadIdx.x * chunk, b1 = min(V, b0 + chunk);
+    int mine = 0;
+    if (fb >= 0)
+        for (int q = b0; q < b1; ++q) mine += bucket_of(p[q]) >= fb;
+    cnt[threadIdx.x] = mine;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int t = 0; t < kST; ++t) {
+            const int x = cnt[t];
+            cnt[t] = acc;
+            acc += x;
+        }
+        sh_n = acc;
+    }
+    __syncthreads();
+    const bool compact = fb >= 0 && sh_n <= kCand;
+    float* pc = reinterpret_cast<float*>(pool);
+    int* ic = reinterpret_cast<int*>(pool + kCand * 4);
+    if (compact && mine > 0) {
+        int o = cnt[threadIdx.x];
+        for (int q = b0; q < b1; ++q)
+            if (bucket_of(p[q]) >= fb) {
+                pc[o] = p[q];
+                ic[o] = q;
+                ++o;
+            }
+    }
+    __syncthreads();
+    const float* pp = compact ? pc : p;
+    const int n = compact ? sh_n : V;
+    auto index_of = [&](int q) { return compact ? ic[q] : q; };
 
     // bisection over the bit patterns of non-negative floats: lo satisfies the
     // predicate, hi does not
@@ -115,14 +204,14 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         while (hi - lo > 1) {
             const uint32_t mid = lo + (hi - lo) / 2;
             double m, c;
-            mass_at(p, V, __uint_as_float(mid), floor_v, red, m, c);
+            mass_at(pp, n, __uint_as_float(mid), floor_v, red, m, c);
             if (pred(m, c)) lo = mid;
             else hi = mid;
         }
         return __uint_as_float(lo);
     };
     auto above = [&](float v, double& m, double& c) {   // mass / count of p > v
-        mass_at(p, V, __uint_as_float(__float_as_uint(v) + 1u), 0.0f, red, m, c);
+        mass_at(pp, n, __uint_as_float(__float_as_uint(v) + 1u), 0.0f, red, m, c);
     };
     double m, c, mg, cg;
     // top-k: the k-th largest probability; the reference keeps exactly k ids,
@@ -135,7 +224,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         take_k = (double)top_k - cg;
     }
     // kept mass before top-p: the ids above vk plus take_k of those at vk
-    mass_at(p, V, vk, vk, red, m, c);
+    mass_at(pp, n, vk, vk, red, m, c);
     above(vk, mg, cg);
     const double kept_k = take_k < 0.0 ? m : mg + take_k * (double)vk;
     float vf = vk;          // the lowest kept level
@@ -144,16 +233,16 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         // the nucleus ends at the id whose running sum reaches top_p
         const float vp = search(vk, [&](double mm, double) { return mm >= (double)top_p; });
         above(vp, mg, cg);
-        double n = ceil(((double)top_p - mg) / (double)vp);
-        mass_at(p, V, vp, vp, red, m, c);
+        double nn = ceil(((double)top_p - mg) / (double)vp);
+        mass_at(pp, n, vp, vp, red, m, c);
         const double group = c - cg;
-        n = fmin(fmax(n, 1.0), group);
-        if (vp == vk && take_k >= 0.0) n = fmin(n, take_k);
+        nn = fmin(fmax(nn, 1.0), group);
+        if (vp == vk && take_k >= 0.0) nn = fmin(nn, take_k);
         vf = vp;
-        take = n;
+        take = nn;
     }
     above(vf, mg, cg);
-    mass_at(p, V, vf, vf, red, m, c);
+    mass_at(pp, n, vf, vf, red, m, c);
     const double nf = take < 0.0 ? c - cg : take;
     const double kept = mg + nf * (double)vf;
     int32_t chosen = -1;
@@ -163,18 +252,19 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         // the position of that id among the level's ids (lowest index first)
         const float w = search(vf, [&](double mm, double) { return mm > r; });
         above(w, mg, cg);
-        mass_at(p, V, w, w, red, m, c);
+        mass_at(pp, n, w, w, red, m, c);
         const double gw = w == vf ? nf : c - cg;
         double j = w > 0.0f ? floor((r - mg) / (double)w) : 0.0;
         j = fmin(fmax(j, 0.0), gw - 1.0);
         // j-th lowest index with p == w: per-thread counts over contiguous
-        // chunks, an exclusive scan, then one thread walks its chunk
-        __shared__ int cnt[kST];
-        const int chunk = (V + kST - 1) / kST;
-        const int b0 = threadIdx.x * chunk, b1 = min(V, b0 + chunk);
-        int mine = 0;
-        for (int q = b0; q < b1; ++q) mine += p[q] == w;
-        cnt[threadIdx.x] = mine;
+        // chunks (the candidates are in index order), an exclusive scan, then
+        // one thread walks its chunk
+        const int ch2 = (n + kST - 1) / kST;
+        const int q0 = threadIdx.x * ch2, q1 = min(n, q0 + ch2);
+        int own = 0;
+        for (int q = q0; q < q1; ++q) own += pp[q] == w;
+        __syncthreads();
+        cnt[threadIdx.x] = own;
         __syncthreads();
         if (threadIdx.x == 0) {
             int acc = 0;
@@ -189,11 +279,11 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         __shared__ int pick;
         if (threadIdx.x == 0) pick = -1;
         __syncthreads();
-        if (jj >= cnt[threadIdx.x] && jj < cnt[threadIdx.x] + mine) {
+        if (jj >= cnt[threadIdx.x] && jj < cnt[threadIdx.x] + own) {
             int seen = cnt[threadIdx.x];
-            for (int q = b0; q < b1; ++q)
-                if (p[q] == w) {
-                    if (seen == jj) { pick = q; break; }
+            for (int q = q0; q < q1; ++q)
+                if (pp[q] == w) {
+                    if (seen == jj) { pick = index_of(q); break; }
                     ++seen;
                 }
         }
