@@ -74,20 +74,155 @@ __device__ void block_sum2(double& a, double& b, double* red) {
     __syncthreads();
 }
 
+// The FP64 sums of a pass: NT = kST, the whole workgroup (block_sum2); NT =
+// 64, wavefront 0 alone (butterfly shuffles, no barrier).
+template <int NT>
+__device__ __forceinline__ void sum2(double& a, double& b, double* red) {
+    if constexpr (NT == kST) {
+        block_sum2(a, b, red);
+    } else {
+        a = wave_sum_d(a);
+        b = wave_sum_d(b);
+    }
+}
+
 // Mass (FP64) and count of p_i >= v among p_i >= floor_v, over n values.
+template <int NT>
 __device__ void mass_at(const float* p, int n, float v, float floor_v, double* red, double& mass, double& cnt) {
     double m = 0.0, c = 0.0;
     const float lo = fmaxf(v, floor_v);
-    for (int i = threadIdx.x; i < n; i += kST) {
+    for (int i = threadIdx.x; i < n; i += NT) {
         const float x = p[i];
         if (x >= lo) {
             m += x;
             c += 1.0;
         }
     }
-    block_sum2(m, c, red);
+    sum2<NT>(m, c, red);
     mass = m;
     cnt = c;
+}
+
+// The id drawn from n probabilities pp (ic maps a position to its id, or null
+// for the identity), NT threads taking part; -1 when no mass is kept.
+template <int NT>
+__device__ int select_token(const float* pp, const int* ic, int n, int V, int top_k, float top_p, double u,
+                            double* red, int* cnt) {
+    // bisection over the bit patterns of non-negative floats: lo satisfies the
+    // predicate, hi does not
+    auto search = [&](float floor_v, auto pred) {
+        uint32_t lo = 0, hi = 0x3f800001u;   // p <= 1
+        while (hi - lo > 1) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            double m, c;
+            mass_at<NT>(pp, n, __uint_as_float(mid), floor_v, red, m, c);
+            if (pred(m, c)) lo = mid;
+            else hi = mid;
+        }
+        return __uint_as_float(lo);
+    };
+    auto above = [&](float v, double& m, double& c) {   // mass / count of p > v
+        mass_at<NT>(pp, n, __uint_as_float(__float_as_uint(v) + 1u), 0.0f, red, m, c);
+    };
+    double m, c, mg, cg;
+    // top-k: the k-th largest probability; the reference keeps exactly k ids,
+    // so of the ids tied at that level only k - (ids above) count
+    float vk = 0.0f;
+    double take_k = -1.0;
+    if (top_k > 0 && top_k < V) {
+        vk = search(0.0f, [&](double, double cc) { return cc >= (double)top_k; });
+        above(vk, mg, cg);
+        take_k = (double)top_k - cg;
+    }
+    // kept mass before top-p: the ids above vk plus take_k of those at vk
+    mass_at<NT>(pp, n, vk, vk, red, m, c);
+    above(vk, mg, cg);
+    const double kept_k = take_k < 0.0 ? m : mg + take_k * (double)vk;
+    float vf = vk;          // the lowest kept level
+    double take = take_k;   // ids kept at vf (-1: all of them)
+    if (top_p < 1.0f && kept_k >= (double)top_p) {
+        // the nucleus ends at the id whose running sum reaches top_p
+        const float vp = search(vk, [&](double mm, double) { return mm >= (double)top_p; });
+        above(vp, mg, cg);
+        double nn = ceil(((double)top_p - mg) / (double)vp);
+        mass_at<NT>(pp, n, vp, vp, red, m, c);
+        const double group = c - cg;
+        nn = fmin(fmax(nn, 1.0), group);
+        if (vp == vk && take_k >= 0.0) nn = fmin(nn, take_k);
+        vf = vp;
+        take = nn;
+    }
+    above(vf, mg, cg);
+    mass_at<NT>(pp, n, vf, vf, red, m, c);
+    const double nf = take < 0.0 ? c - cg : take;
+    const double kept = mg + nf * (double)vf;
+    if (!(kept > 0.0)) return -1;
+    const double r = u * kept;
+    // the level holding the id where the running kept mass passes r, and the
+    // position of that id among the level's ids (lowest index first)
+    const float w = search(vf, [&](double mm, double) { return mm > r; });
+    above(w, mg, cg);
+    mass_at<NT>(pp, n, w, w, red, m, c);
+    const double gw = w == vf ? nf : c - cg;
+    double j = w > 0.0f ? floor((r - mg) / (double)w) : 0.0;
+    j = fmin(fmax(j, 0.0), gw - 1.0);
+    const int jj = (int)j;
+    // j-th lowest index with p == w: per-thread counts over contiguous chunks
+    // (positions are in index order), an exclusive scan, then the thread whose
+    // chunk holds it walks the chunk
+    const int t = threadIdx.x;
+    const int ch = (n + NT - 1) / NT;
+    const int q0 = t * ch, q1 = min(n, q0 + ch);
+    int own = 0;
+    for (int q = q0; q < q1; ++q) own += pp[q] == w;
+    int before;
+    if constexpr (NT == kST) {
+        __syncthreads();
+        cnt[t] = own;
+        __syncthreads();
+        if (t == 0) {
+            int acc = 0;
+            for (int i = 0; i < kST; ++i) {
+                const int x = cnt[i];
+                cnt[i] = acc;
+                acc += x;
+            }
+        }
+        __syncthreads();
+        before = cnt[t];
+    } else {
+        int inc = own;   // inclusive scan over the wavefront
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(inc, o);
+            if (t >= o) inc += y;
+        }
+        before = inc - own;
+    }
+    int pick = -1;
+    if (jj >= before && jj < before + own) {
+        int seen = before;
+        for (int q = q0; q < q1; ++q)
+            if (pp[q] == w) {
+                if (seen == jj) {
+                    pick = ic ? ic[q] : q;
+                    break;
+                }
+                ++seen;
+            }
+    }
+    if constexpr (NT == kST) {
+        __shared__ int pick_sh;
+        if (t == 0) pick_sh = -1;
+        __syncthreads();
+        if (pick >= 0) pick_sh = pick;
+        __syncthreads();
+        return pick_sh;
+    } else {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) pick = max(pick, __shfl_xor(pick, o));
+        return pick;
+    }
 }
 
 // Candidate compaction.  A histogram of the probabilities by the top 13 bits
@@ -115,18 +250,44 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
     __shared__ __align__(16) unsigned char pool[kCand * 8];   // histogram, then candidates
     __shared__ int sh_floor, sh_n;
     float* redf = reinterpret_cast<float*>(red);
+    // passes over the vocabulary take eight elements per thread per step
+    // (stride kST, so each of the eight loads is coalesced), all loads first
+    constexpr int kU = 8;
+    const int tid = threadIdx.x;
     float mx = -INFINITY;
-    for (int i = threadIdx.x; i < V; i += kST) mx = fmaxf(mx, h2f(logits[i]) * inv_t);
+    for (int i0 = 0; i0 < V; i0 += kU * kST) {
+        float x[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kST + tid;
+            x[k] = i < V ? h2f(logits[i]) * inv_t : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < kU; ++k) mx = fmaxf(mx, x[k]);
+    }
     mx = block_max_f(mx, redf);
+    // exponentials and their FP64 sum, in the same per-thread order as one
+    // element per step (i = tid, tid + kST, ...)
     double s = 0.0;
-    for (int i = threadIdx.x; i < V; i += kST) {
-        const float e = expf(h2f(logits[i]) * inv_t - mx);
-        p[i] = e;
-        s += e;
+    for (int i0 = 0; i0 < V; i0 += kU * kST) {
+        float x[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kST + tid;
+            x[k] = i < V ? h2f(logits[i]) : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kST + tid;
+            if (i < V) {
+                const float e = expf(x[k] * inv_t - mx);
+                p[i] = e;
+                s += e;
+            }
+        }
     }
     s = block_sum_d(s, red);
     const float norm = s > 0.0 ? (float)(1.0 / s) : 0.0f;
-    for (int i = threadIdx.x; i < V; i += kST) p[i] *= norm;
 
     // ---- candidate floor from the histogram
     uint32_t* hcount = reinterpret_cast<uint32_t*>(pool);
@@ -136,12 +297,28 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         hmass[b] = 0ull;
     }
     __syncthreads();
-    if (top_k > 0 || top_p < 1.0f) {
-        for (int i = threadIdx.x; i < V; i += kST) {
-            const float x = p[i];
-            const int b = bucket_of(x);
-            atomicAdd(&hcount[b], 1u);
-            atomicAdd(&hmass[b], (unsigned long long)((double)x * kFix));
+    // normalise (each thread its own elements) and, when top-k or top-p cut
+    // the set, the histogram
+    const bool hist = top_k > 0 || top_p < 1.0f;
+    for (int i0 = 0; i0 < V; i0 += kU * kST) {
+        float x[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kST + tid;
+            x[k] = i < V ? p[i] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int i = i0 + k * kST + tid;
+            if (i < V) {
+                const float v = x[k] * norm;
+                p[i] = v;
+                if (hist) {
+                    const int b = bucket_of(v);
+                    atomicAdd(&hcount[b], 1u);
+                    atomicAdd(&hmass[b], (unsigned long long)((double)v * kFix));
+                }
+            }
         }
     }
     __syncthreads();
@@ -167,7 +344,13 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
     const int b0 = threadIdx.x * chunk, b1 = min(V, b0 + chunk);
     int mine = 0;
     if (fb >= 0)
-        for (int q = b0; q < b1; ++q) mine += bucket_of(p[q]) >= fb;
+        for (int q0 = b0; q0 < b1; q0 += kU) {
+            float x[kU];
+#pragma unroll
+            for (int k = 0; k < kU; ++k) x[k] = q0 + k < b1 ? p[q0 + k] : 0.f;
+#pragma unroll
+            for (int k = 0; k < kU; ++k) mine += (q0 + k < b1 && bucket_of(x[k]) >= fb) ? 1 : 0;
+        }
     cnt[threadIdx.x] = mine;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -193,102 +376,18 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
             }
     }
     __syncthreads();
-    const float* pp = compact ? pc : p;
-    const int n = compact ? sh_n : V;
-    auto index_of = [&](int q) { return compact ? ic[q] : q; };
-
-    // bisection over the bit patterns of non-negative floats: lo satisfies the
-    // predicate, hi does not
-    auto search = [&](float floor_v, auto pred) {
-        uint32_t lo = 0, hi = 0x3f800001u;   // p <= 1
-        while (hi - lo > 1) {
-            const uint32_t mid = lo + (hi - lo) / 2;
-            double m, c;
-            mass_at(pp, n, __uint_as_float(mid), floor_v, red, m, c);
-            if (pred(m, c)) lo = mid;
-            else hi = mid;
-        }
-        return __uint_as_float(lo);
-    };
-    auto above = [&](float v, double& m, double& c) {   // mass / count of p > v
-        mass_at(pp, n, __uint_as_float(__float_as_uint(v) + 1u), 0.0f, red, m, c);
-    };
-    double m, c, mg, cg;
-    // top-k: the k-th largest probability; the reference keeps exactly k ids,
-    // so of the ids tied at that level only k - (ids above) count
-    float vk = 0.0f;
-    double take_k = -1.0;
-    if (top_k > 0 && top_k < V) {
-        vk = search(0.0f, [&](double, double cc) { return cc >= (double)top_k; });
-        above(vk, mg, cg);
-        take_k = (double)top_k - cg;
-    }
-    // kept mass before top-p: the ids above vk plus take_k of those at vk
-    mass_at(pp, n, vk, vk, red, m, c);
-    above(vk, mg, cg);
-    const double kept_k = take_k < 0.0 ? m : mg + take_k * (double)vk;
-    float vf = vk;          // the lowest kept level
-    double take = take_k;   // ids kept at vf (-1: all of them)
-    if (top_p < 1.0f && kept_k >= (double)top_p) {
-        // the nucleus ends at the id whose running sum reaches top_p
-        const float vp = search(vk, [&](double mm, double) { return mm >= (double)top_p; });
-        above(vp, mg, cg);
-        double nn = ceil(((double)top_p - mg) / (double)vp);
-        mass_at(pp, n, vp, vp, red, m, c);
-        const double group = c - cg;
-        nn = fmin(fmax(nn, 1.0), group);
-        if (vp == vk && take_k >= 0.0) nn = fmin(nn, take_k);
-        vf = vp;
-        take = nn;
-    }
-    above(vf, mg, cg);
-    mass_at(pp, n, vf, vf, red, m, c);
-    const double nf = take < 0.0 ? c - cg : take;
-    const double kept = mg + nf * (double)vf;
-    int32_t chosen = -1;
-    if (kept > 0.0) {
-        const double r = u * kept;
-        // the level holding the id where the running kept mass passes r, and
-        // the position of that id among the level's ids (lowest index first)
-        const float w = search(vf, [&](double mm, double) { return mm > r; });
-        above(w, mg, cg);
-        mass_at(pp, n, w, w, red, m, c);
-        const double gw = w == vf ? nf : c - cg;
-        double j = w > 0.0f ? floor((r - mg) / (double)w) : 0.0;
-        j = fmin(fmax(j, 0.0), gw - 1.0);
-        // j-th lowest index with p == w: per-thread counts over contiguous
-        // chunks (the candidates are in index order), an exclusive scan, then
-        // one thread walks its chunk
-        const int ch2 = (n + kST - 1) / kST;
-        const int q0 = threadIdx.x * ch2, q1 = min(n, q0 + ch2);
-        int own = 0;
-        for (int q = q0; q < q1; ++q) own += pp[q] == w;
-        __syncthreads();
-        cnt[threadIdx.x] = own;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int acc = 0;
-            for (int t = 0; t < kST; ++t) {
-                const int x = cnt[t];
-                cnt[t] = acc;
-                acc += x;
-            }
+    int32_t chosen;
+    if (compact) {
+        // at most kCand candidates: wavefront 0 alone, no barriers
+        __shared__ int chosen_sh;
+        if (threadIdx.x < 64) {
+            const int pk = select_token<64>(pc, ic, sh_n, V, top_k, top_p, u, red, cnt);
+            if (threadIdx.x == 0) chosen_sh = pk;
         }
         __syncthreads();
-        const int jj = (int)j;
-        __shared__ int pick;
-        if (threadIdx.x == 0) pick = -1;
-        __syncthreads();
-        if (jj >= cnt[threadIdx.x] && jj < cnt[threadIdx.x] + own) {
-            int seen = cnt[threadIdx.x];
-            for (int q = q0; q < q1; ++q)
-                if (pp[q] == w) {
-                    if (seen == jj) { pick = index_of(q); break; }
-                    ++seen;
-                }
-        }
-        __syncthreads();
-        chosen = pick;
+        chosen = chosen_sh;
+    } else {
+        chosen = select_token<kST>(p, nullptr, V, V, top_k, top_p, u, red, cnt);
     }
     if (chosen < 0) {   // no mass: the most probable id (lowest index on ties)
         __shared__ int best2;
