@@ -184,6 +184,17 @@ class Qwen3Model:
                   "decode_greedy")
         return out[:k].tolist()
 
+    def decode_sampled(self, token: int, u: Sequence[float], temperature: float, top_k: int = 0,
+                       top_p: float = 1.0, eos_id: int = -1) -> list[int]:
+        """Top-k / top-p continuation on the device, step i drawing with u[i]."""
+        uu = np.ascontiguousarray(np.asarray(u, dtype=np.float64))
+        out = np.empty((max(uu.size, 1),), np.int32)
+        k = check(_native.lib().brolm_qwen3_decode_sampled(self._h, int(token), uu.size, uu.ctypes.data_as(C.c_void_p),
+                                                           float(temperature), int(top_k), float(top_p),
+                                                           out.ctypes.data_as(_native.P_i32), int(eos_id)),
+                  "decode_sampled")
+        return out[:k].tolist()
+
     def time_decode_steps(self, token: int, n: int) -> float:
         ms = _native.lib().brolm_qwen3_time_decode_steps(self._h, int(token), int(n))
         if ms < 0:

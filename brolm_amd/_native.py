@@ -111,6 +111,7 @@ HIP_SYMBOLS = {
     "bx_linear_tiles_ok": (C.c_int, [C.c_int, C.c_int]),
     "bx_attention_varlen_f16": (C.c_int, [vp, vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp,
                                           vp]),
+    "bx_sample_feed_f16": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, vp, vp, vp, vp, vp, vp]),
     "bx_rope_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp]),
     "bx_kv_append_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp, vp, i64, vp]),
     "bx_linear_group_f16": (C.c_int, [C.c_int, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), vp, C.c_int,
@@ -150,6 +151,8 @@ C_SYMBOLS = {
     "brolm_qwen3_cache_len": (C.c_int, [vp]),
     "brolm_qwen3_forward": (C.c_int, [vp, P_i32, C.c_int, P_f32, P_f32]),
     "brolm_qwen3_forward_last": (C.c_int, [vp, P_i32, C.c_int, P_f32]),
+    "brolm_qwen3_decode_sampled": (C.c_int, [vp, C.c_int32, C.c_int, vp, C.c_float, C.c_int, C.c_float, P_i32,
+                                             C.c_int]),
     "brolm_qwen3_allocate_batch": (C.c_int, [vp, C.c_int, C.c_int]),
     "brolm_qwen3_slot_len": (C.c_int, [vp, C.c_int]),
     "brolm_qwen3_truncate_slot": (C.c_int, [vp, C.c_int, C.c_int]),

@@ -660,6 +660,15 @@ int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out
     return rc == 0 ? count : -1;
 }
 
+int brolm_qwen3_decode_sampled(brolm_qwen3* m, int32_t token, int n, const double* u, float temperature, int top_k,
+                               float top_p, int32_t* out, int eos_id) {
+    int count = 0;
+    const int rc = guard([&] {
+        count = core_of(m).decode_sampled(token, n, u, temperature, top_k, top_p, out, eos_id);
+    });
+    return rc == 0 ? count : rc;
+}
+
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n) {
     double ms = -1.0;
     const int rc = guard([&] { ms = core_of(m).time_decode_steps(token, n); });

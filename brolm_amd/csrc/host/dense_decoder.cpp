@@ -73,11 +73,16 @@ struct DecodeGraphSession {
     std::size_t pws_bytes = 0;
     bx_decode_layer* layers_dev = nullptr;
     uint32_t epoch = 0;
+    // device-side sampled decoding: the sampler's workspace and the draws
+    void* sample_ws = nullptr;
+    double* draws = nullptr;
 
     ~DecodeGraphSession() {
         // after brotensor::shutdown() the op stream is gone and already drained
         if (bt::initialized()) (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
         if (pws) (void)hipFree(pws);
+        if (sample_ws) (void)hipFree(sample_ws);
+        if (draws) (void)hipFree(draws);
         if (layers_dev) (void)hipFree(layers_dev);
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
@@ -857,6 +862,71 @@ int DenseDecoder::decode_greedy(int32_t token, int n, int32_t* out, int eos_id) 
         const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
         stage_step(s, cur, cache_len_);
         launch_steps(s, chunk, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+        check_persist(s);
+        hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
+        for (int i = 0; i < chunk; ++i) {
+            if (eos_id >= 0 && out[done + i] == eos_id) {
+                cache_len_ += i + 1;
+                return done + i + 1;
+            }
+        }
+        cache_len_ += chunk;
+        done += chunk;
+        cur = out[done - 1];
+    }
+    return done;
+}
+
+int DenseDecoder::decode_sampled(int32_t token, int n, const double* u, float temperature, int top_k, float top_p,
+                                 int32_t* out, int eos_id) {
+    if (n <= 0) return 0;
+    if (!u || !out) fail("decode_sampled: null draws or output");
+    if (!(temperature > 0.0f)) fail("decode_sampled: temperature must be positive (greedy: decode_greedy)");
+    for (int i = 0; i < n; ++i)
+        if (!(u[i] >= 0.0 && u[i] < 1.0)) fail("decode_sampled: draws must lie in [0, 1)");
+    check_forward("decode_sampled", &token, 1, embed_tokens_.size() != 0, max_seq_len_, cache_len_, cfg_.vocab_size);
+    if (cache_len_ + n > max_seq_len_) fail("decode_sampled: cache_len + n exceeds allocated cache capacity");
+    const int V = cfg_.vocab_size;
+    if (!fused_step_ok_()) {
+        // op path, one token at a time, the same device sampler on its logits
+        bt::Tensor lg, ws, tok;
+        ws = bt::Tensor::empty_on(bt::Device::ROCm, static_cast<int>(bx_sample_workspace_bytes(V) / 4), 1,
+                                  bt::Dtype::FP32);
+        tok = bt::Tensor::empty_on(bt::Device::ROCm, 1, 1, bt::Dtype::FP32);
+        int32_t cur = token;
+        for (int i = 0; i < n; ++i) {
+            forward_last(&cur, 1, lg);
+            hipx::bx(bx_sample_f16(static_cast<const uint16_t*>(lg.data), V, temperature, top_k, top_p, u[i],
+                                   static_cast<int32_t*>(tok.data), ws.data, bt::stream()),
+                     "decode_sampled");
+            hipx::d2h(&cur, tok.data, sizeof(cur));
+            out[i] = cur;
+            if (eos_id >= 0 && cur == eos_id) return i + 1;
+        }
+        return n;
+    }
+    DecodeGraphSession& s = session_();
+    if (!s.sample_ws) {
+        hipx::check(hipMalloc(&s.sample_ws, bx_sample_workspace_bytes(V)), "hipMalloc sampler workspace");
+        hipx::check(hipMalloc(reinterpret_cast<void**>(&s.draws), DecodeGraphSession::kHist * sizeof(double)),
+                    "hipMalloc draws");
+    }
+    int done = 0;
+    int32_t cur = token;
+    while (done < n) {
+        const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
+        stage_step(s, cur, cache_len_);
+        hipx::check(hipMemcpyAsync(s.draws, u + done, static_cast<std::size_t>(chunk) * sizeof(double),
+                                   hipMemcpyHostToDevice, hipx::stream()),
+                    "upload draws");
+        for (int i = 0; i < chunk; ++i) {
+            // the fused step (its argmax advances token and history), then the
+            // draw replaces that token
+            launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+            hipx::bx(bx_sample_feed_f16(s.logits, V, temperature, top_k, top_p, s.draws, s.scal + 0, s.scal + 4,
+                                        s.scal + 3, s.sample_ws, bt::stream()),
+                     "decode_sampled");
+        }
         check_persist(s);
         hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
         for (int i = 0; i < chunk; ++i) {

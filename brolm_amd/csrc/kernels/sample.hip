@@ -242,9 +242,15 @@ constexpr double kFix = 17592186044416.0;   // 2^44
 // to the last bucket, so the histogram stays in bounds
 __device__ __forceinline__ int bucket_of(float x) { return min((int)(__float_as_uint(x) >> 19), kBuckets - 1); }
 
+// FEED: u is u_dev[count[0] - 1] and the id replaces the token and the last
+// history entry of a fused decode step (out = its token slot), so sampled
+// decoding continues on the device without a host round trip per token.
+template <bool FEED>
 __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict__ logits, int V, float inv_t,
                                                      int top_k, float top_p, double u, float* __restrict__ p,
-                                                     int32_t* __restrict__ out) {
+                                                     int32_t* __restrict__ out, const double* __restrict__ u_dev,
+                                                     const int32_t* __restrict__ count, int32_t* __restrict__ hist) {
+    if constexpr (FEED) u = u_dev[count[0] - 1];
     __shared__ double red[kST];
     __shared__ int cnt[kST];
     __shared__ __align__(16) unsigned char pool[kCand * 8];   // histogram, then candidates
@@ -299,7 +305,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
     __syncthreads();
     // normalise (each thread its own elements) and, when top-k or top-p cut
     // the set, the histogram
-    const bool hist = top_k > 0 || top_p < 1.0f;
+    const bool want_hist = top_k > 0 || top_p < 1.0f;
     for (int i0 = 0; i0 < V; i0 += kU * kST) {
         float x[kU];
 #pragma unroll
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
             if (i < V) {
                 const float v = x[k] * norm;
                 p[i] = v;
-                if (hist) {
+                if (want_hist) {
                     const int b = bucket_of(v);
                     atomicAdd(&hcount[b], 1u);
                     atomicAdd(&hmass[b], (unsigned long long)((double)v * kFix));
@@ -401,7 +407,10 @@ __global__ __launch_bounds__(kST) void sample_kernel(const uint16_t* __restrict_
         __syncthreads();
         chosen = best2 == 0x7fffffff ? 0 : best2;
     }
-    if (threadIdx.x == 0) out[0] = chosen;
+    if (threadIdx.x == 0) {
+        out[0] = chosen;
+        if constexpr (FEED) hist[count[0] - 1] = chosen;
+    }
 }
 
 }  // namespace
@@ -418,9 +427,21 @@ int bx_sample_f16(const uint16_t* logits, int vocab, float temperature, int top_
     if (!logits || !out || !workspace || vocab <= 0) return fail(BX_EINVAL, "sample: bad arguments");
     if (!(temperature > 0.0f)) return fail(BX_EINVAL, "sample: temperature must be positive (greedy uses argmax)");
     if (!(u >= 0.0 && u < 1.0)) return fail(BX_EINVAL, "sample: u must be in [0, 1)");
-    sample_kernel<<<1, kST, 0, as_stream(stream)>>>(logits, vocab, 1.0f / temperature, top_k, top_p, u,
-                                                    static_cast<float*>(workspace), out);
+    sample_kernel<false><<<1, kST, 0, as_stream(stream)>>>(logits, vocab, 1.0f / temperature, top_k, top_p, u,
+                                                           static_cast<float*>(workspace), out, nullptr, nullptr,
+                                                           nullptr);
     return launch_check("sample");
+}
+
+int bx_sample_feed_f16(const uint16_t* logits, int vocab, float temperature, int top_k, float top_p,
+                       const double* u_dev, int32_t* tok, int32_t* hist, const int32_t* count, void* workspace,
+                       void* stream) {
+    if (!logits || !u_dev || !tok || !hist || !count || !workspace || vocab <= 0)
+        return fail(BX_EINVAL, "sample_feed: bad arguments");
+    if (!(temperature > 0.0f)) return fail(BX_EINVAL, "sample_feed: temperature must be positive");
+    sample_kernel<true><<<1, kST, 0, as_stream(stream)>>>(logits, vocab, 1.0f / temperature, top_k, top_p, 0.0,
+                                                          static_cast<float*>(workspace), tok, u_dev, count, hist);
+    return launch_check("sample_feed");
 }
 
 }  // extern "C"

@@ -75,6 +75,11 @@ public:
     // Writes the n sampled ids to out; stops after eos_id when eos_id >= 0.
     // Returns the number of ids written; cache_len advances by that count.
     int decode_greedy(int32_t token, int n, int32_t* out, int eos_id);
+    // The same loop with top-k / top-p sampling on the device (temperature >
+    // 0): step i draws with u[i] (host values in [0, 1), one per token, taken
+    // from the caller's generator in order, as generate.cpp:68-142 draws them).
+    int decode_sampled(int32_t token, int n, const double* u, float temperature, int top_k, float top_p,
+                       int32_t* out, int eos_id);
 
     // Replays the captured step n times from `token` at cache_len() and
     // returns the GPU time per step in milliseconds (hipEvents around the

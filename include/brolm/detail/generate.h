@@ -76,6 +76,26 @@ std::vector<int32_t> generate(Model& model, const std::vector<int32_t>& prompt_i
         return generated;
     }
 
+    if (on_device) {
+        // the rest on the device: the draws are taken now, in the order the
+        // per-token loop below would take them (one per token)
+        const int want = opts.max_new_tokens - 1;
+        if (want > 0) {
+            std::uniform_real_distribution<double> dist(0.0, 1.0);
+            std::vector<double> u(static_cast<std::size_t>(want));
+            for (double& x : u) x = dist(rng);
+            std::vector<int32_t> tail(static_cast<std::size_t>(want));
+            const int got = model.decode_sampled(generated.back(), want, u.data(), opts.sampling.temperature,
+                                                 opts.sampling.top_k, opts.sampling.top_p, tail.data(),
+                                                 stop ? eos_id : -1);
+            for (int i = 0; i < got; ++i) {
+                if (stop && tail[static_cast<std::size_t>(i)] == eos_id) break;
+                generated.push_back(tail[static_cast<std::size_t>(i)]);
+            }
+        }
+        return generated;
+    }
+
     while (static_cast<int>(generated.size()) < opts.max_new_tokens) {
         int32_t cur = generated.back();
         model.forward_last(&cur, 1, logits);

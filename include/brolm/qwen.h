@@ -72,6 +72,11 @@ public:
     int decode_greedy(int32_t token, int n, int32_t* out, int eos_id) {
         return core_.decode_greedy(token, n, out, eos_id);
     }
+    // Device-side sampled continuation (DenseDecoder::decode_sampled).
+    int decode_sampled(int32_t token, int n, const double* u, float temperature, int top_k, float top_p,
+                       int32_t* out, int eos_id) {
+        return core_.decode_sampled(token, n, u, temperature, top_k, top_p, out, eos_id);
+    }
 
     const Qwen3Config& config() const { return cfg_; }
     brolm::detail::DenseDecoder& core() { return core_; }

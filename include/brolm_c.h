@@ -169,6 +169,11 @@ int brolm_qwen3_generate(brolm_qwen3* m, const int32_t* prompt, int n_prompt, in
                          int device_greedy, int device_sampling, int32_t* out);
 /* DenseDecoder::decode_greedy / time_decode_steps / decode_weight_bytes. */
 int brolm_qwen3_decode_greedy(brolm_qwen3* m, int32_t token, int n, int32_t* out, int eos_id);
+/* Device-side top-k / top-p continuation (DenseDecoder::decode_sampled): n
+ * tokens from `token`, step i drawing with u[i] in [0, 1); returns the ids
+ * written (stops after eos_id when eos_id >= 0), or a negative error code. */
+int brolm_qwen3_decode_sampled(brolm_qwen3* m, int32_t token, int n, const double* u, float temperature, int top_k,
+                               float top_p, int32_t* out, int eos_id);
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n);
 int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m);
 /* DenseDecoder::decode_mode: 2 persistent single launch, 1 captured graph, 0 eager; -1 on error

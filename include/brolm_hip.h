@@ -183,6 +183,14 @@ int bx_add_inplace(void* h, int h_is_f32, const uint16_t* x, int64_t n, void* st
  * probabilities resolve to the lowest index.  workspace:
  * bx_sample_workspace_bytes(vocab). */
 size_t bx_sample_workspace_bytes(int vocab);
+/* bx_sample_f16 inside a device-side decode loop (no reference counterpart:
+ * the reference samples on the host, generate.cpp:68-142): the draw is
+ * u_dev[*count - 1] (device, each in [0, 1)), and the id is written to *tok and
+ * hist[*count - 1], the token and history slots the fused decode step
+ * (bx_decode_advance / bx_persist_step) has just filled with its argmax. */
+int bx_sample_feed_f16(const uint16_t* logits, int vocab, float temperature, int top_k, float top_p,
+                       const double* u_dev, int32_t* tok, int32_t* hist, const int32_t* count, void* workspace,
+                       void* stream);
 int bx_sample_f16(const uint16_t* logits, int vocab, float temperature, int top_k, float top_p, double u,
                   int32_t* out, void* workspace, void* stream);
 /* masked_mean_pool_forward(x, mask, out) (src/llm2vec.cpp:139-153): out[c] =

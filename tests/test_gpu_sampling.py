@@ -98,3 +98,58 @@ def test_sampled_generation_on_device_matches_host(env, small_gguf):
     sp = ba.SamplingParams(temperature=0.8, top_k=40, top_p=0.9, seed=7)
     assert len(ba.generate(m, prompt, -1, ba.GenerateOptions(max_new_tokens=24, sampling=sp,
                                                              stop_on_eos=False))) == 24
+
+
+def _tie_at_cut(lg, T, k, p):
+    """Whether the logit where the top-k / top-p kept set ends is shared with
+    the first logit left out (float64 probabilities, enough to find the cut)."""
+    srt = np.sort(lg.astype(np.float64))[::-1]
+    n = srt.size if k <= 0 else min(k, srt.size)
+    if n < srt.size and srt[n - 1] == srt[n]:
+        return True
+    pr = np.exp((srt[:n] - srt[0]) / T)
+    c = np.cumsum(pr / pr.sum())
+    m = min(int(np.searchsorted(c, p)) + 1, n)
+    return m < srt.size and srt[m - 1] == srt[m]
+
+
+@pytest.mark.parametrize("cap", [64, 33000])
+def test_device_sampled_decode_matches_per_token_sampling(env, small_gguf, cap):
+    """decode_sampled (the fused step and the device sampler back to back, no
+    host round trip; with a cache beyond the fused step's, the op path) picks,
+    at every step, the oracle sampler's id for that step's own logits and draw
+    (a second model fed the same tokens gives the logits), up to the first
+    draw within 1e-5 of an interval boundary or an FP16 tie at the top-k cut
+    (criteria as above)."""
+    import brolm_amd as ba
+    print(f"[sample] decode_sampled cap={cap}", flush=True)
+    mods = []
+    for _ in range(2):
+        m = ba.Qwen3Model(ba.Qwen3Config.from_gguf(str(small_gguf)))
+        m.load_weights(str(small_gguf))
+        m.allocate_cache(cap)
+        mods.append(m)
+    a, b = mods
+    prompt = [5, 9, 2, 7]
+    rng = np.random.default_rng(cap)
+    T, k, p = 0.7, 50, 0.9
+    for m in mods:
+        m.forward_last(prompt)
+    first = 11
+    n = 32
+    u = rng.random(n)
+    got = a.decode_sampled(first, u, T, k, p)
+    assert len(got) == n
+    checked = 0
+    for i in range(n):
+        lg = np.asarray(b.forward_last([first if i == 0 else got[i - 1]]), dtype=np.float32).reshape(-1)
+        want, margin = oracle.sample_token(lg, T, k, p, float(u[i]))
+        if margin < 1e-5 or _tie_at_cut(lg, T, k, p):
+            continue  # boundary draw, or an FP16 tie where the kept set ends (the device keeps every tie)
+        assert got[i] == want or lg[got[i]] == lg[want], (i, got[i], want)
+        checked += 1
+    print(f"[sample] {checked} of {n} steps checked", flush=True)
+    assert checked >= n // 3
+    assert a.cache_len() == len(prompt) + n
+    for m in mods:
+        m.close()
