@@ -71,6 +71,28 @@ struct XStage {
     __device__ __forceinline__ u2v a4(int e) const { return *reinterpret_cast<const u2v*>(xs + xrow + (e >> 1)); }
 };
 
+// Q4_K: 32-element sums of the Mr staged rows of K elements (16 dwords hold a
+// permutation of a group's elements), kept as FP16 high part + remainder in
+// xs2[j * 16 + m]; zero for m >= Mr.
+__device__ __forceinline__ void q4k_xsums(const uint32_t* smem, int xstride, uint32_t* xs2, int Mr, int K) {
+    for (int i = threadIdx.x; i < (K / 32) * 16; i += blockDim.x) {
+        const int j = i >> 4, m = i & 15;
+        float s = 0.f;
+        if (m < Mr) {
+            const u4v* p = reinterpret_cast<const u4v*>(smem + m * xstride + 16 * j);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u4v v = p[q];
+                s += (h2f(v.x & 0xffff) + h2f(v.x >> 16)) + (h2f(v.y & 0xffff) + h2f(v.y >> 16)) +
+                     (h2f(v.z & 0xffff) + h2f(v.z >> 16)) + (h2f(v.w & 0xffff) + h2f(v.w >> 16));
+            }
+        }
+        const _Float16 hi = (_Float16)s;
+        const _Float16 lo = (_Float16)(s - (float)hi);
+        xs2[i] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    }
+}
+
 // ---- per-format chunk: 256 K elements of one 16-row tile, per lane ---------
 
 template <int FMT>
@@ -358,24 +380,7 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(MfmaJob job, const uint
     for (int i = threadIdx.x; i < xstride; i += kThr) smem[Mr * xstride + i] = 0u;
     __syncthreads();
     if constexpr (FMT == FMT_Q4_K) {
-        // 32-element sums from the staged rows (16 dwords hold a permutation
-        // of the group's elements), kept as FP16 high part + remainder
-        for (int i = threadIdx.x; i < (K / 32) * 16; i += kThr) {
-            const int j = i >> 4, m = i & 15;
-            float s = 0.f;
-            if (m < Mr) {
-                const u4v* p = reinterpret_cast<const u4v*>(smem + m * xstride + 16 * j);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const u4v v = p[q];
-                    s += (h2f(v.x & 0xffff) + h2f(v.x >> 16)) + (h2f(v.y & 0xffff) + h2f(v.y >> 16)) +
-                         (h2f(v.z & 0xffff) + h2f(v.z >> 16)) + (h2f(v.w & 0xffff) + h2f(v.w >> 16));
-                }
-            }
-            const _Float16 hi = (_Float16)s;
-            const _Float16 lo = (_Float16)(s - (float)hi);
-            xs2[i] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
-        }
+        q4k_xsums(smem, xstride, xs2, Mr, K);
         __syncthreads();
     }
 
@@ -388,13 +393,21 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(MfmaJob job, const uint
         const int N = job.N[mem];
         const int64_t n = lt * 16 + r;
         if (n >= N) return;
+        if constexpr (EPI == MEPI_RESID) {
+            float hv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * g + j < Mr) hv[j] = job.H[(int64_t)(4 * g + j) * N + n];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * g + j < Mr) job.H[(int64_t)(4 * g + j) * N + n] = hv[j] + h2f(f2h(a[j]));
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = 4 * g + j;
             if (m >= Mr) continue;
-            if constexpr (EPI == MEPI_RESID) {
-                job.H[(int64_t)m * N + n] += h2f(f2h(a[j]));
-            } else if constexpr (EPI == MEPI_SWIGLU) {
+            if constexpr (EPI == MEPI_SWIGLU) {
                 const float act = h2f(f2h(silu_f32(h2f(f2h(a[j])))));
                 job.Y[0][(int64_t)m * N + n] = f2h(act * h2f(f2h(u[j])));
             } else {
@@ -451,6 +464,210 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(MfmaJob job, const uint
     }
 }
 
+// ---- split-K launches for matrices of decoder-layer size --------------------
+//
+// Grid (tile groups, S): workgroup (x, s) runs the 16-row tiles 4x .. 4x + 3,
+// one per wavefront, over K slice s (chunks [s nch / S, (s + 1) nch / S) of
+// 256 elements) and stages only that slice of X, so a layer's matrix spreads
+// over the whole chip at any M and the LDS holds 16 rows at any K.  With
+// S > 1 every wavefront writes its partial tile (FP32, rows below Mr) to the
+// split workspace; the workgroup that completes a tile group last (a counter
+// per group) adds the S partials in slice order, so the sum does not depend on
+// which workgroup arrives when, applies the epilogue, and sets the counter back
+// to zero for the next launch.  The slice plan depends on K alone, so a member
+// of a q / k / v group gets the same sums as alone, and the fused epilogues the
+// same as the separate ops.
+constexpr int kSplThr = 256;
+constexpr int kSplWav = kSplThr / 64;
+constexpr int kSplMaxCps = 3;                    // chunks per slice
+constexpr int64_t kSplFloats = 8ll << 20;        // partials: 32 MB
+constexpr int kSplGroups = 4096;                 // tile groups of one launch
+
+}  // namespace
+}  // namespace bx
+
+// The split workspace, one copy per GPU, used by every split launch on it in
+// stream order: launches of 3 <= M <= 16 rows on one GPU must not overlap in
+// time (the library issues them on one stream).  Host code never takes these
+// names as addresses; only the kernels below touch them.
+static __device__ __align__(256) float split_part[bx::kSplFloats];
+static __device__ __align__(256) uint32_t split_cnt[bx::kSplGroups];
+
+namespace bx {
+namespace {
+
+// Cache policy of the partials' buffer stores and loads: sc1, device scope.
+constexpr int kSc1 = 16;
+
+__global__ void split_clear_kernel() {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kSplGroups; i += gridDim.x * blockDim.x) split_cnt[i] = 0u;
+}
+
+// The epilogue of one tile from lane values a (and u for SwiGLU).
+template <int EPI>
+__device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, int r, int g, int Mr, const f4v& a,
+                                              const f4v& u) {
+    int mem;
+    int64_t lt;
+    member_of(job, tile, mem, lt);
+    const int N = job.N[mem];
+    const int64_t n = lt * 16 + r;
+    if (n >= N) return;
+    const float bv = (EPI == MEPI_STORE && job.bias) ? h2f(job.bias[n]) : 0.f;
+    if constexpr (EPI == MEPI_RESID) {
+        // the rows' residuals read together, then written
+        float hv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * g + j < Mr) hv[j] = job.H[(int64_t)(4 * g + j) * N + n];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * g + j < Mr) job.H[(int64_t)(4 * g + j) * N + n] = hv[j] + h2f(f2h(a[j]));
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = 4 * g + j;
+        if (m >= Mr) continue;
+        if constexpr (EPI == MEPI_SWIGLU) {
+            const float act = h2f(f2h(silu_f32(h2f(f2h(a[j])))));
+            job.Y[0][(int64_t)m * N + n] = f2h(act * h2f(f2h(u[j])));
+        } else {
+            job.Y[mem][(int64_t)m * N + n] = f2h(a[j] + bv);
+        }
+    }
+}
+
+template <int FMT, int EPI, int CPS>
+__global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const uint16_t* __restrict__ X, int Mr,
+                                                            int K, int S) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ uint32_t last;
+    constexpr bool kSwz = FMT != FMT_F16;
+    constexpr bool kTwo = EPI == MEPI_SWIGLU;
+    constexpr int kParts = kTwo ? 2 : 1;
+    const int nch = K / 256;
+    const int s = blockIdx.y;
+    const int c0 = s * nch / S, nc = (s + 1) * nch / S - c0;   // 1 <= nc <= CPS
+    const int Ks = 256 * nc;
+    const int xstride = Ks / 2 + 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t tile = (int64_t)blockIdx.x * kSplWav + wave;
+    const bool live = tile < job.tiles;
+    // this wavefront's weights first, every load issued: a wavefront past the
+    // last tile re-reads it, chunk slots past the slice repeat its last chunk
+    int mem;
+    int64_t lt;
+    member_of(job, live ? tile : job.tiles - 1, mem, lt);
+    const int N = job.N[mem];
+    const int64_t n = lt * 16 + r < N ? lt * 16 + r : N - 1;
+    Chunk<FMT> cw[CPS];
+    Chunk<FMT> cu[kTwo ? CPS : 1];
+#pragma unroll
+    for (int i = 0; i < CPS; ++i) {
+        const int b = c0 + (i < nc ? i : nc - 1);
+        cw[i].load(job.W[mem], N, K, n, b, g);
+        if constexpr (kTwo) cu[i].load(job.W[1], N, K, n, b, g);
+    }
+    XStage xst;
+    xst.xs = smem;
+    xst.xrow = (r < Mr ? r : Mr) * xstride;
+    uint32_t* xs2 = smem + (Mr + 1) * xstride;
+    xst.xs2 = xs2;
+    stage_x_f16<kSwz, false>(X + 256 * c0, K, Mr, Ks, smem, xstride, nullptr, 0);
+    for (int i = threadIdx.x; i < xstride; i += kSplThr) smem[Mr * xstride + i] = 0u;
+    __syncthreads();
+    if constexpr (FMT == FMT_Q4_K) {
+        q4k_xsums(smem, xstride, xs2, Mr, Ks);
+        __syncthreads();
+    }
+    f4v acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CPS; ++i) {
+        if (i < nc) {
+            cw[i].mul(xst, 256 * i, r, g, acc);
+            if constexpr (kTwo) cu[i].mul(xst, 256 * i, r, g, accu);
+        }
+    }
+    if (S == 1) {
+        if (live) tile_epilogue<EPI>(job, tile, r, g, Mr, acc, accu);
+        return;
+    }
+    // Partial tile (tile, s): kParts blocks of the lane values of the lanes
+    // holding rows below Mr (4 floats a lane, lanes 0 .. 4 Mr4 - 1 with Mr4 =
+    // Mr rounded up to 4).  The partials travel by device-scope (sc1) buffer
+    // stores and loads, which write through and read past the per-XCD L2s,
+    // and every wavefront waits for its stores to complete before the
+    // workgroup counts itself in: the counter never runs ahead of the data it
+    // announces, without the L2 write-back a device-scope fence would cost.
+    const int Mr4 = (Mr + 3) & ~3;
+    const int pl = 4 * Mr4;                             // lanes with partials
+    const int64_t pstride = (int64_t)kParts * pl * 4;   // floats per (tile, slice)
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(split_part, 0, 0x7fffffff, 0x00020000);
+    const int64_t tbase = live ? tile * S * pstride : 0;
+    if (live && lane < pl) {
+        const int o = (int)((tbase + s * pstride) * 4) + lane * 16;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, acc), rs, o, 0, kSc1);
+        if constexpr (kTwo) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, accu), rs, o + pl * 16, 0, kSc1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(&split_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       (uint32_t)(S - 1)
+                   ? 1u
+                   : 0u;
+    __syncthreads();
+    if (!last) return;
+    if (live && lane < pl) {
+        // all S partials requested before any is added; added in slice order
+        f4v a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+        for (int q0 = 0; q0 < S; q0 += 4) {
+            u4v va[4], vu[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = q0 + i < S ? q0 + i : S - 1;
+                const int o = (int)((tbase + q * pstride) * 4) + lane * 16;
+                va[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kSc1);
+                if constexpr (kTwo) vu[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + pl * 16, 0, kSc1);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (q0 + i < S) {
+                    a += __builtin_bit_cast(f4v, va[i]);
+                    if constexpr (kTwo) u += __builtin_bit_cast(f4v, vu[i]);
+                }
+            }
+        }
+        tile_epilogue<EPI>(job, tile, r, g, Mr, a, u);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&split_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Slices of K for the split launch: at most 16, of at most kSplMaxCps chunks
+// each (cps returned); 0 when K needs more.
+int split_plan(int K, int& cps) {
+    const int nch = K / 256;
+    cps = (nch + 15) / 16;
+    return cps <= kSplMaxCps ? (nch + cps - 1) / cps : 0;
+}
+
+// The split counters start at zero: cleared once per GPU before its first
+// split launch (stream-ordered ahead of it).
+int split_ready(hipStream_t st) {
+    static std::mutex mu;
+    static std::map<int, bool> done;
+    int dev = 0;
+    if (int rc = hip_check(hipGetDevice(&dev), "gemv split: hipGetDevice")) return rc;
+    std::lock_guard<std::mutex> lk(mu);
+    if (done[dev]) return BX_OK;
+    split_clear_kernel<<<16, 256, 0, st>>>();
+    if (int rc = launch_check("gemv split clear")) return rc;
+    done[dev] = true;
+    return BX_OK;
+}
+
 size_t mfma_lds_bytes(int fmt, int Mr, int K, bool two = false) {
     size_t b = (size_t)(Mr + 1) * (K / 2 + 4) * 4;
     if (fmt == FMT_Q4_K) b += (size_t)(K / 32) * 16 * 4;
@@ -458,6 +675,9 @@ size_t mfma_lds_bytes(int fmt, int Mr, int K, bool two = false) {
 }
 
 constexpr size_t kMaxLds = 160 * 1024;
+// Above this many row tiles (the lm_head) the whole-tile launch streams at
+// full rate and the split partials would only add traffic.
+constexpr int64_t kSplitTiles = 2048;
 
 // Launch a job for M rows of X, in row chunks whose staging fits the LDS.
 template <int EPI>
@@ -483,6 +703,22 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
     const int64_t tiles = job.tiles;
     const int nch = K / 256;
     const int cus = num_cus();
+    // layer-sized matrices: the split launch (one launch for all M rows)
+    int cps = 0;
+    const int S = split_plan(K, cps);
+    const int64_t groups = (tiles + kSplWav - 1) / kSplWav;
+    if (S > 0 && M <= 16 && tiles <= kSplitTiles && groups <= kSplGroups &&
+        groups * kSplWav * S * (two ? 2 : 1) * M * 16 <= kSplFloats) {
+        if (int rc = split_ready(st)) return rc;
+        const size_t lds = (size_t)(M + 1) * (128 * cps + 4) * 4 + (fmt == FMT_Q4_K ? (size_t)8 * cps * 16 * 4 : 0);
+        const dim3 grid((unsigned)groups, (unsigned)S);
+        BX_DISPATCH_FMT(wtype, {
+            if (cps == 1) gemv_split_kernel<FMT_, EPI, 1><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+            else if (cps == 2) gemv_split_kernel<FMT_, EPI, 2><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+            else gemv_split_kernel<FMT_, EPI, 3><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+        })
+        return launch_check("gemv split");
+    }
     for (int m0 = 0; m0 < M; m0 += mc) {
         const int mr = M - m0 < mc ? M - m0 : mc;
         const size_t lds = mfma_lds_bytes(fmt, mr, K, two);

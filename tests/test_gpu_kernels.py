@@ -207,6 +207,32 @@ def test_linear_ffn_width_k(t):
 
 
 @pytest.mark.parametrize("t", QTYPES + [1])
+@pytest.mark.parametrize("N,K", [(1000, 6144), (4100, 2048), (77, 12288), (40, 768)])
+def test_linear_split_k_repeats_bitwise(t, N, K):
+    """Batched GEMV of decoder-layer size: K split over workgroups, partial
+    tiles added by the last workgroup of each tile group.  Row tiles not a
+    multiple of the group, slices of one to three chunks (K 768 .. 12288),
+    bias; three launches in a row give the same bits (the per-group counters
+    are back at zero after every launch) and match the oracle."""
+    rng = np.random.default_rng(5150 + N + t)
+    if t == 1:
+        Wv = _f16(rng.standard_normal((N, K)) * 0.05)
+        car = f16_dev(Wv)
+    else:
+        raw, Wv = sb.random_matrix(rng, t, N, K)
+        car = carrier(t, raw, N, K)
+    bias = _f16(rng.standard_normal(N))
+    for M in (3, 8, 13, 16):
+        print(f"[linear split] type={t} N={N} K={K} M={M}", flush=True)
+        X = _f16(rng.standard_normal((M, K)) * (0.25 if K > 4096 else 1.0))
+        outs = [_run_linear(t, car, X, N, K, bias) for _ in range(3)]
+        assert all(np.array_equal(o, outs[0]) for o in outs[1:]), M
+        ref = oracle.linear(Wv, X) + bias
+        tol = _linear_tol(Wv, X, ref) + 2.0 ** -10 * np.abs(bias)
+        assert np.all(np.abs(outs[0] - ref) <= tol), (M, float((np.abs(outs[0] - ref) / tol).max()))
+
+
+@pytest.mark.parametrize("t", QTYPES + [1])
 def test_linear_batched_many_tiles(t):
     """Batched GEMV with more 16-row tiles than the workgroups hold at once
     (each wavefront walks several tiles) and a last tile of one row."""
