@@ -1041,9 +1041,7 @@ void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
     bh_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP32);
     bnorm_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP16);
     bq_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
-    bqn_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
     bk_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
-    bkn_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
     bv_ = bt::Tensor::empty_on(dev, n_slots, width, bt::Dtype::FP16);
     battn_ = bt::Tensor::empty_on(dev, n_slots, qd, bt::Dtype::FP16);
     bproj_ = bt::Tensor::empty_on(dev, n_slots, H, bt::Dtype::FP16);
@@ -1133,12 +1131,6 @@ void DenseDecoder::enqueue_batch_(int M) {
              "forward_batch embedding");
     const std::int64_t plane_rows = static_cast<std::int64_t>(batch_slots_) * batch_cap_;
     auto* arena = static_cast<std::uint16_t*>(batch_kv_.data);
-    auto headnorm = [&](const bt::Tensor& src, int num_heads, const bt::Tensor& gain, bt::Tensor& dst_t) {
-        bt::Tensor v = bt::Tensor::view(src.device, src.data, src.rows * num_heads, HD, src.dtype);
-        bt::rms_norm_forward(v, gain, eps, dst_t);
-        dst_t.rows = src.rows;
-        dst_t.cols = num_heads * HD;
-    };
     const auto* cs = static_cast<const float*>(batch_cos_.data);
     const auto* sn = static_cast<const float*>(batch_sin_.data);
     for (std::size_t l = 0; l < layers_.size(); ++l) {
@@ -1154,23 +1146,18 @@ void DenseDecoder::enqueue_batch_(int M) {
             if (layer.Wk.dtype == layer.Wq.dtype && bt::linear_group_forward_batched(w, y, same, bnorm_)) done = same;
             for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, bnorm_, *y[i]);
         }
-        bt::Tensor* q_attn = &bq_;
-        bt::Tensor* k_attn = &bk_;
-        if (cfg_.use_qk_norm) {
-            headnorm(bq_, n_q, layer.q_norm, bqn_);
-            headnorm(bk_, n_kv, layer.k_norm, bkn_);
-            q_attn = &bqn_;
-            k_attn = &bkn_;
-        }
-        auto* qd = static_cast<uint16_t*>(q_attn->data);
-        auto* kd = static_cast<uint16_t*>(k_attn->data);
-        hipx::bx(bx_rope_rows_f16(qd, qd, M, HD, n_q, pos_d, cs, sn, batch_cap_, st), "forward_batch rope q");
-        hipx::bx(bx_rope_rows_f16(kd, kd, M, HD, n_kv, pos_d, cs, sn, batch_cap_, st), "forward_batch rope k");
+        // q / k head norms, RoPE and the cache write of k / v in one launch
+        // (the roped q in place)
         std::uint16_t* Kp = arena + static_cast<std::size_t>(2 * l) * plane_rows * width;
         std::uint16_t* Vp = Kp + static_cast<std::size_t>(plane_rows) * width;
-        hipx::bx(bx_kv_append_rows_f16(kd, static_cast<const uint16_t*>(bv_.data), M, width, dst_d, Kp, Vp,
-                                       plane_rows, st),
-                 "forward_batch kv append");
+        auto* qd = static_cast<uint16_t*>(bq_.data);
+        const bool qkn = cfg_.use_qk_norm;
+        hipx::bx(bx_qk_rope_kv_rows_f16(qd, static_cast<const uint16_t*>(bk_.data),
+                                        static_cast<const uint16_t*>(bv_.data), M, HD, n_q, n_kv,
+                                        qkn ? static_cast<const uint16_t*>(layer.q_norm.data) : nullptr,
+                                        qkn ? static_cast<const uint16_t*>(layer.k_norm.data) : nullptr, eps, pos_d,
+                                        cs, sn, batch_cap_, dst_d, Kp, Vp, plane_rows, qd, st),
+                 "forward_batch q / k norm, rope, kv write");
         hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, batch_cap_, n_q, n_kv, HD,
                                          static_cast<uint16_t*>(battn_.data), bws_.data, st),
                  "forward_batch attention");

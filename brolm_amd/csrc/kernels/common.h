@@ -52,6 +52,23 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 // SiLU as the elementwise kernels compute it (x / (1 + e^-x), fast exp).
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
 
+// An FP32 value the compiler cannot fuse into the instruction that consumes
+// it.  The backend otherwise turns an FP32 multiply followed by an FP16
+// conversion into one mixed-precision multiply (v_fma_mixlo_f16, a single
+// rounding straight to FP16) in some kernels and not in others, so the same
+// expression could round differently from one kernel to the next.
+__device__ __forceinline__ float f32_fence(float x) {
+    float y;
+    asm("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+    return y;
+}
+
+// An RMSNorm output element: x * inv * gain rounded to FP32, then to FP16,
+// the same bits in every kernel that applies a norm this way.
+__device__ __forceinline__ uint16_t norm_f16(float x, float inv, float gain) {
+    return f2h(f32_fence(x * inv * gain));
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 

@@ -44,7 +44,7 @@ __global__ __launch_bounds__(NT) void rms_norm_kernel(const InT* __restrict__ X,
     for (int c = threadIdx.x; c < cols; c += NT) {
         float v;
         if constexpr (sizeof(InT) == 4) v = x[c]; else v = h2f(x[c]);
-        Y[r * cols + c] = f2h(v * inv * h2f(gamma[c]));
+        Y[r * cols + c] = norm_f16(v, inv, h2f(gamma[c]));
     }
 }
 

@@ -155,6 +155,15 @@ int bx_rope_rows_f16(const uint16_t* X, uint16_t* Y, int rows, int hd, int n_hea
 /* kv_cache_append of row r to cache row dst_rows_dev[r] (< cache_rows). */
 int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int cols, const int64_t* dst_rows_dev,
                           uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, void* stream);
+/* The per-head ops of one batched step in one launch (dense_decoder.cpp:
+ * 575-607 per row): q / k head RMSNorm with q_gain / k_gain (both null: none),
+ * RoPE at pos_dev[r], roped q heads to q_out (may be q), roped k rows and the
+ * v rows to cache row dst_rows_dev[r]; bit-identical to rms_norm, rope_rows and
+ * kv_append_rows in sequence.  hd: 64, 128 or 256. */
+int bx_qk_rope_kv_rows_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int rows, int hd, int n_q,
+                           int n_kv, const uint16_t* q_gain, const uint16_t* k_gain, float eps, const int32_t* pos_dev,
+                           const float* cos_tab, const float* sin_tab, int tab_rows, const int64_t* dst_rows_dev,
+                           uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, uint16_t* q_out, void* stream);
 
 /* K15: flash_attention_decode_masked(q, Kc, Vc, mask, n_q, n_kv, out)
  * (dense_decoder.cpp:476-478): one query row attends the keys j < n_keys

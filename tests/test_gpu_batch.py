@@ -184,3 +184,54 @@ def test_batched_graph_replays_equal_eager(ba, small_gguf, monkeypatch):
             m.forward_last([7])
     for m in models.values():
         m.close()
+
+
+@pytest.mark.parametrize("hd,norm", [(128, True), (64, True), (256, True), (128, False)])
+def test_qk_rope_kv_rows_equals_separate_ops(hd, norm):
+    """bx_qk_rope_kv_rows_f16 (the per-head stage of a batched step in one
+    launch) gives exactly the bits of its three separate launches: head
+    rms_norm of q and k (when gains are given), rope_rows at each row's own
+    position, kv_append_rows into scattered cache rows; cache rows not written
+    stay as they were."""
+    from gpu_util import call, dev, f16_dev, host, ptr, stream, torch
+    import ctypes as C
+    print(f"[batch] qk_rope_kv hd={hd} norm={norm}", flush=True)
+    rng = np.random.default_rng(hd + norm)
+    M, n_q, n_kv, cap, tab = 7, 8, 2, 50, 64
+    width = n_kv * hd
+    q = rng.standard_normal((M, n_q * hd)) * 3
+    k = rng.standard_normal((M, width)) * 3
+    v = rng.standard_normal((M, width))
+    qg = rng.uniform(0.5, 1.5, hd) if norm else None
+    kg = rng.uniform(0.5, 1.5, hd) if norm else None
+    pos = np.array([0, 5, 63, 17, 1, 40, 33], np.int32)
+    dst = np.array([3, 49, 0, 20, 7, 31, 12], np.int64)
+    cos_t = np.empty((tab, hd // 2), np.float32)
+    sin_t = np.empty((tab, hd // 2), np.float32)
+    import brolm_amd._native as nat
+    nat.hip().bx_rope_table_host(cos_t.ctypes.data_as(nat.P_f32), sin_t.ctypes.data_as(nat.P_f32), tab, hd, 1e6)
+    cs, sn = dev(cos_t), dev(sin_t)
+    pos_d, dst_d = dev(pos), dev(dst)
+    fill = rng.integers(0, 2 ** 15, (cap, width)).astype(np.uint16)
+    eps = 1e-6
+    # fused
+    qf = f16_dev(q)
+    Kf, Vf = dev(fill), dev(fill)
+    gq = f16_dev(qg) if norm else None
+    gk = f16_dev(kg) if norm else None
+    kd, vd = f16_dev(k), f16_dev(v)
+    call("bx_qk_rope_kv_rows_f16", ptr(qf), ptr(kd), ptr(vd), M, hd, n_q, n_kv, ptr(gq), ptr(gk), C.c_float(eps),
+         ptr(pos_d), ptr(cs), ptr(sn), tab, ptr(dst_d), ptr(Kf), ptr(Vf), cap, ptr(qf), stream())
+    # separate
+    qs, ks = f16_dev(q), f16_dev(k)
+    if norm:
+        call("bx_rms_norm", ptr(qs), 0, ptr(gq), C.c_float(eps), ptr(qs), M * n_q, hd, stream())
+        call("bx_rms_norm", ptr(ks), 0, ptr(gk), C.c_float(eps), ptr(ks), M * n_kv, hd, stream())
+    call("bx_rope_rows_f16", ptr(qs), ptr(qs), M, hd, n_q, ptr(pos_d), ptr(cs), ptr(sn), tab, stream())
+    call("bx_rope_rows_f16", ptr(ks), ptr(ks), M, hd, n_kv, ptr(pos_d), ptr(cs), ptr(sn), tab, stream())
+    Ks, Vs = dev(fill), dev(fill)
+    call("bx_kv_append_rows_f16", ptr(ks), ptr(vd), M, width, ptr(dst_d), ptr(Ks), ptr(Vs), cap, stream())
+    assert np.array_equal(host(qf), host(qs))
+    assert np.array_equal(host(Kf), host(Ks)) and np.array_equal(host(Vf), host(Vs))
+    untouched = np.setdiff1d(np.arange(cap), dst)
+    assert np.array_equal(host(Kf).reshape(cap, width)[untouched], fill[untouched])
