@@ -27,12 +27,39 @@ __global__ void embedding_kernel(const uint16_t* __restrict__ W, int H, const in
 }
 
 // One block per row.  y = x * (mean(x^2) + eps)^-1/2 * gamma  (FP32 math).
-template <typename InT, int NT>
+// EPT > 0: every thread holds at most EPT elements (cols <= NT * EPT), all
+// its x and gamma loads issued before any use (one memory round trip instead
+// of one per element); EPT = 0: any width, element by element.  Thread t adds
+// the squares of elements t, t + NT, ... in that order either way, so both
+// forms give the same bits.
+template <typename InT, int NT, int EPT>
 __global__ __launch_bounds__(NT) void rms_norm_kernel(const InT* __restrict__ X, const uint16_t* __restrict__ gamma,
                                                       float eps, uint16_t* __restrict__ Y, int cols) {
     __shared__ float red[NT / 64];
     const int64_t r = blockIdx.x;
     const InT* x = X + r * cols;
+    if constexpr (EPT > 0) {
+        float v[EPT], g[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int c = threadIdx.x + NT * i;
+            const int cc = c < cols ? c : cols - 1;   // clamped: every load issued
+            if constexpr (sizeof(InT) == 4) v[i] = x[cc]; else v[i] = h2f(x[cc]);
+            g[i] = h2f(gamma[cc]);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            if (threadIdx.x + NT * i < cols) ss += v[i] * v[i];
+        ss = block_sum<NT>(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+            const int c = threadIdx.x + NT * i;
+            if (c < cols) Y[r * cols + c] = norm_f16(v[i], inv, g[i]);
+        }
+        return;
+    }
     float ss = 0.f;
     for (int c = threadIdx.x; c < cols; c += NT) {
         float v;
@@ -46,6 +73,18 @@ __global__ __launch_bounds__(NT) void rms_norm_kernel(const InT* __restrict__ X,
         if constexpr (sizeof(InT) == 4) v = x[c]; else v = h2f(x[c]);
         Y[r * cols + c] = norm_f16(v, inv, h2f(gamma[c]));
     }
+}
+
+template <typename InT, int NT>
+void rms_norm_launch(const InT* X, const uint16_t* gamma, float eps, uint16_t* Y, int rows, int cols,
+                     hipStream_t st) {
+    const int ept = (cols + NT - 1) / NT;
+    if (ept <= 1) rms_norm_kernel<InT, NT, 1><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
+    else if (ept <= 2) rms_norm_kernel<InT, NT, 2><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
+    else if (ept <= 4) rms_norm_kernel<InT, NT, 4><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
+    else if (ept <= 8) rms_norm_kernel<InT, NT, 8><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
+    else if (ept <= 16) rms_norm_kernel<InT, NT, 16><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
+    else rms_norm_kernel<InT, NT, 0><<<rows, NT, 0, st>>>(X, gamma, eps, Y, cols);
 }
 
 // Pairs (2i, 2i+1) of every head rotate by the table angle of row pos.
@@ -153,11 +192,11 @@ int bx_rms_norm(const void* X, int x_is_f32, const uint16_t* gamma, float eps, u
     if (!X || !gamma || !Y || rows <= 0 || cols <= 0) return fail(BX_EINVAL, "rms_norm: bad arguments");
     hipStream_t st = as_stream(stream);
     if (cols <= 512) {
-        if (x_is_f32) rms_norm_kernel<float, 64><<<rows, 64, 0, st>>>((const float*)X, gamma, eps, Y, cols);
-        else rms_norm_kernel<uint16_t, 64><<<rows, 64, 0, st>>>((const uint16_t*)X, gamma, eps, Y, cols);
+        if (x_is_f32) rms_norm_launch<float, 64>((const float*)X, gamma, eps, Y, rows, cols, st);
+        else rms_norm_launch<uint16_t, 64>((const uint16_t*)X, gamma, eps, Y, rows, cols, st);
     } else {
-        if (x_is_f32) rms_norm_kernel<float, 256><<<rows, 256, 0, st>>>((const float*)X, gamma, eps, Y, cols);
-        else rms_norm_kernel<uint16_t, 256><<<rows, 256, 0, st>>>((const uint16_t*)X, gamma, eps, Y, cols);
+        if (x_is_f32) rms_norm_launch<float, 256>((const float*)X, gamma, eps, Y, rows, cols, st);
+        else rms_norm_launch<uint16_t, 256>((const uint16_t*)X, gamma, eps, Y, rows, cols, st);
     }
     return launch_check("rms_norm");
 }
