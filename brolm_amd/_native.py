@@ -114,6 +114,9 @@ HIP_SYMBOLS = {
     "bx_sample_feed_f16": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, vp, vp, vp, vp, vp, vp]),
     "bx_rope_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp]),
     "bx_kv_append_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp, vp, i64, vp]),
+    "bx_batch_attention_workspace_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "bx_batch_attention_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
+                                         C.c_int, vp, vp, C.c_int, vp, vp, i64, vp, vp, vp]),
     "bx_qk_rope_kv_rows_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
                                          vp, C.c_int, vp, vp, vp, i64, vp, vp]),
     "bx_linear_group_f16": (C.c_int, [C.c_int, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), vp, C.c_int,

@@ -1048,8 +1048,14 @@ void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
     bgate_ = bt::Tensor::empty_on(dev, n_slots, F, bt::Dtype::FP16);
     bup_ = bt::Tensor::empty_on(dev, n_slots, F, bt::Dtype::FP16);
     blogits_ = bt::Tensor::empty_on(dev, n_slots, cfg_.vocab_size, bt::Dtype::FP16);
-    const std::size_t wsb = bx_attention_workspace_bytes(n_slots, cfg_.num_attention_heads, cfg_.head_dim, max_seq_len);
+    // the batched attention's records and counters, for any M <= n_slots;
+    // zeroed once (each launch leaves its counters at zero)
+    std::size_t wsb = 0;
+    for (int m = 1; m <= n_slots; ++m)
+        wsb = std::max(wsb, bx_batch_attention_workspace_bytes(m, cfg_.num_attention_heads,
+                                                               cfg_.num_key_value_heads, cfg_.head_dim, max_seq_len));
     bws_ = bt::Tensor::empty_on(dev, 1, static_cast<int>((wsb + 3) / 4), bt::Dtype::FP32);
+    hipx::check(hipMemset(bws_.data, 0, bws_.bytes()), "hipMemset batch attention workspace");
     batch_graphs_ = std::make_unique<BatchGraphs>(n_slots);
 }
 
@@ -1115,10 +1121,9 @@ void DenseDecoder::prefill_slot(int slot, const int32_t* ids, int L, bt::Tensor&
 // graph): every pointer it uses is fixed between allocate_batch calls, and the
 // attention split plan is sized by the slot capacity, not the current lengths.
 void DenseDecoder::enqueue_batch_(int M) {
-    const auto* dst_d = static_cast<const std::int64_t*>(batch_meta_.data);
-    const std::int64_t* base_d = dst_d + M;
-    const auto* pos_d = reinterpret_cast<const int32_t*>(dst_d + 2 * M);
-    const int32_t* lens_d = pos_d + M;
+    const auto* meta = static_cast<const std::int64_t*>(batch_meta_.data);
+    const std::int64_t* base_d = meta + M;
+    const int32_t* lens_d = reinterpret_cast<const int32_t*>(meta + 2 * M) + M;
     const int32_t* ids_d = lens_d + M;
     const int HD = cfg_.head_dim, n_q = cfg_.num_attention_heads, n_kv = cfg_.num_key_value_heads;
     const int width = n_kv * HD;
@@ -1146,20 +1151,17 @@ void DenseDecoder::enqueue_batch_(int M) {
             if (layer.Wk.dtype == layer.Wq.dtype && bt::linear_group_forward_batched(w, y, same, bnorm_)) done = same;
             for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, bnorm_, *y[i]);
         }
-        // q / k head norms, RoPE and the cache write of k / v in one launch
-        // (the roped q in place)
+        // q / k head norms, RoPE, the cache write of k / v and the attention
+        // over each row's own keys in one launch
         std::uint16_t* Kp = arena + static_cast<std::size_t>(2 * l) * plane_rows * width;
         std::uint16_t* Vp = Kp + static_cast<std::size_t>(plane_rows) * width;
-        auto* qd = static_cast<uint16_t*>(bq_.data);
         const bool qkn = cfg_.use_qk_norm;
-        hipx::bx(bx_qk_rope_kv_rows_f16(qd, static_cast<const uint16_t*>(bk_.data),
+        hipx::bx(bx_batch_attention_f16(static_cast<const uint16_t*>(bq_.data), static_cast<const uint16_t*>(bk_.data),
                                         static_cast<const uint16_t*>(bv_.data), M, HD, n_q, n_kv,
                                         qkn ? static_cast<const uint16_t*>(layer.q_norm.data) : nullptr,
-                                        qkn ? static_cast<const uint16_t*>(layer.k_norm.data) : nullptr, eps, pos_d,
-                                        cs, sn, batch_cap_, dst_d, Kp, Vp, plane_rows, qd, st),
-                 "forward_batch q / k norm, rope, kv write");
-        hipx::bx(bx_attention_varlen_f16(qd, Kp, Vp, M, lens_d, base_d, batch_cap_, n_q, n_kv, HD,
-                                         static_cast<uint16_t*>(battn_.data), bws_.data, st),
+                                        qkn ? static_cast<const uint16_t*>(layer.k_norm.data) : nullptr, eps, lens_d,
+                                        base_d, batch_cap_, cs, sn, batch_cap_, Kp, Vp, plane_rows,
+                                        static_cast<uint16_t*>(battn_.data), bws_.data, st),
                  "forward_batch attention");
         if (!bt::linear_residual_forward_batched(layer.Wo, battn_, bh_)) {
             linear_batched(layer.Wo, nullptr, battn_, bproj_);

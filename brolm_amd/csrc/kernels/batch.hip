@@ -64,22 +64,15 @@ __global__ void kv_rows_kernel(const uint16_t* __restrict__ k, const uint16_t* _
 // normed values and the rotation round exactly as the separate launches of
 // rms_norm, rope_rows and kv_append_rows.  A pair's partner element is in the
 // neighbouring lane.
+// One head (64 EPL elements, lane l holding elements l, l + 64, ...) of a raw
+// projection row: RMSNorm with gain (when given), FP16, RoPE by the table row
+// ps (identity when rot is false), FP16.  y[i] is element lane + 64 i.
 template <int EPL>
-__global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(
-    const uint16_t* q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int rows, int n_q, int n_kv, const uint16_t* __restrict__ q_gain, const uint16_t* __restrict__ k_gain, float eps,
-    const int32_t* __restrict__ pos, int tab_rows, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    const int64_t* __restrict__ dst, int64_t cache_rows, uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
-    uint16_t* q_out) {
+__device__ __forceinline__ void norm_rope_lane(const uint16_t* src, const uint16_t* gain, float eps, int ps, bool rot,
+                                               const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                               uint16_t (&y)[EPL]) {
     constexpr int HD = 64 * EPL, half = HD / 2;
-    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int heads = n_q + n_kv;
-    if (item >= rows * heads) return;
     const int lane = threadIdx.x & 63;
-    const int r = item / heads, h = item - r * heads;
-    const bool is_q = h < n_q;
-    const int hk = h - n_q;
-    const uint16_t* src = is_q ? q + ((int64_t)r * n_q + h) * HD : k + ((int64_t)r * n_kv + hk) * HD;
-    const uint16_t* gain = is_q ? q_gain : k_gain;
     float x[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) x[i] = h2f(src[lane + 64 * i]);
@@ -92,9 +85,6 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(
 #pragma unroll
         for (int i = 0; i < EPL; ++i) x[i] = h2f(norm_f16(x[i], inv, h2f(gain[lane + 64 * i])));
     }
-    const int ps = pos[r];
-    const bool rot = ps >= 0 && ps < tab_rows;
-    uint16_t y[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
         const int e = lane + 64 * i;
@@ -106,6 +96,27 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(
         else rope_pair(x[i], other, c, sn, y0, y1);
         y[i] = (e & 1) ? y1 : y0;
     }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(
+    const uint16_t* q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int rows, int n_q, int n_kv, const uint16_t* __restrict__ q_gain, const uint16_t* __restrict__ k_gain, float eps,
+    const int32_t* __restrict__ pos, int tab_rows, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const int64_t* __restrict__ dst, int64_t cache_rows, uint16_t* __restrict__ Kc, uint16_t* __restrict__ Vc,
+    uint16_t* q_out) {
+    constexpr int HD = 64 * EPL;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int heads = n_q + n_kv;
+    if (item >= rows * heads) return;
+    const int lane = threadIdx.x & 63;
+    const int r = item / heads, h = item - r * heads;
+    const bool is_q = h < n_q;
+    const int hk = h - n_q;
+    const uint16_t* src = is_q ? q + ((int64_t)r * n_q + h) * HD : k + ((int64_t)r * n_kv + hk) * HD;
+    const int ps = pos[r];
+    const bool rot = ps >= 0 && ps < tab_rows;
+    uint16_t y[EPL];
+    norm_rope_lane<EPL>(src, is_q ? q_gain : k_gain, eps, ps, rot, cos_t, sin_t, y);
     if (is_q) {
         if (!rot) return;
         uint16_t* o = q_out + ((int64_t)r * n_q + h) * HD;
@@ -124,6 +135,374 @@ __global__ __launch_bounds__(256) void qk_rope_kv_rows_kernel(
         Vc[d * width + (int64_t)hk * HD + e] = vs[e];
     }
 }
+
+// ---- batched attention with the per-head stage fused ------------------------
+//
+// One launch per layer of a batched step: workgroup (split s, KV group g, row
+// r) takes keys [s kps, s kps + kps) of row r's own sequence (cache rows
+// base[r] + j, its new key at j = lens[r] - 1).  Its prologue normalises and
+// rotates the group's q heads (norm_rope_lane, the arithmetic of the separate
+// q / k stage), and the split that holds the new key does the same for the new
+// k row and writes k and v to the cache (and into its LDS tile in place of the
+// stale row).  Key tiles are copied to LDS (K in 16-byte chunks XOR-swizzled
+// by the key, so lanes reading consecutive keys hit distinct banks); each
+// wavefront then works alone on a key part x head: one lane per key for the
+// scores (v_dot2 on FP16 q and k), an online softmax in registers, P.V with
+// the probabilities broadcast by readlane and EPL head dims per lane.  The key
+// parts of a head are merged in LDS; the (o, m, l) record of each (split,
+// head) goes out by device-scope stores, and the workgroup of a (row, group)
+// that finishes last merges its S records in split order (the result does not
+// depend on arrival order), writes the FP16 output and returns the counter to
+// zero.
+template <int HD>
+struct BaShape {
+    static constexpr int TK = 8192 / HD;   // keys per LDS tile (two tiles of K and V: 64 KB)
+    static constexpr int CPK = HD / 8;     // 16-byte chunks per key row
+    static constexpr int EPL = HD / 64;    // head elements (and output dims) per lane
+};
+
+struct BatchAttnArgs {
+    const uint16_t* q;     // rows x n_q HD, raw projections
+    const uint16_t* k;     // rows x n_kv HD
+    const uint16_t* v;
+    const uint16_t* q_gain;   // null: no head norm
+    const uint16_t* k_gain;
+    float eps;
+    const int32_t* lens;   // keys of row r with its new one (position lens[r] - 1)
+    const int64_t* base;   // cache row of key 0 of row r
+    const float* cos_t;
+    const float* sin_t;
+    int tab_rows;
+    uint16_t* Kc;
+    uint16_t* Vc;
+    int64_t cache_rows;
+    int n_q, n_kv, S, kps, P, HPW;
+    float* recs;       // (row, group) x S x G records of HD + 2 floats
+    uint32_t* cnt;     // rows x n_kv counters, zero between launches
+    uint16_t* out;     // rows x n_q HD
+};
+
+constexpr int kBaSc1 = 16;   // cache policy of the record stores and loads: sc1, device scope
+
+template <int HD>
+__device__ __forceinline__ void ba_dma(const void* src, uint16_t* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
+    using SH = BaShape<HD>;
+    constexpr int TK = SH::TK, CPK = SH::CPK, EPL = SH::EPL;
+    extern __shared__ __align__(16) uint16_t ba_lds[];
+    __shared__ uint32_t last;
+    uint16_t* tiles = ba_lds;          // two buffers of K (TK x HD, swizzled chunks) then V (TK x HD)
+    uint16_t* qs = tiles + 4 * TK * HD;   // 8 x HD roped q heads
+    uint16_t* kn = qs + 8 * HD;        // the new key row
+    uint16_t* vn = kn + HD;            // the new value row
+    const int s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+    const int G = a.n_q / a.n_kv, P = a.P, HPW = a.HPW, T = a.S;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int len = a.lens[r], pnew = len - 1;
+    const int kb = s * a.kps, ke = min(len, kb + a.kps);
+    const bool has_cur = kb <= pnew && pnew < ke;
+    const int64_t kvd = (int64_t)a.n_kv * HD;
+    const int64_t row0 = a.base[r];
+    const bool rot = pnew >= 0 && pnew < a.tab_rows;
+    const uint16_t* Kg = a.Kc + row0 * kvd + (int64_t)g * HD;
+    const uint16_t* Vg = a.Vc + row0 * kvd + (int64_t)g * HD;
+    // tile copy of keys [c0, c0 + nk) into buffer b; slots past nk repeat key
+    // nk - 1 (in bounds)
+    auto copy_tile = [&](int b, int c0, int nk) {
+        uint16_t* kt = tiles + 2 * b * TK * HD;
+        uint16_t* vt = kt + TK * HD;
+        const int ninst = (nk * CPK + 63) / 64;
+        for (int i = wave; i < ninst; i += 4) {
+            const int slot = 64 * i + lane;
+            int j = slot / CPK;
+            const int pc = slot % CPK;
+            if (j >= nk) j = nk - 1;
+            const int64_t rowo = (int64_t)(c0 + j) * kvd;
+            ba_dma<HD>(Kg + rowo + 8 * (pc ^ (j & (CPK - 1))), kt + 512 * i);
+            ba_dma<HD>(Vg + rowo + 8 * pc, vt + 512 * i);
+        }
+    };
+    if (kb < ke) copy_tile(0, kb, min(TK, ke - kb));   // lands while the prologue runs
+
+    // ---- prologue: roped q heads; the new k / v rows in the split holding them
+    for (int hh = wave; hh < G; hh += 4) {
+        uint16_t y[EPL];
+        norm_rope_lane<EPL>(a.q + ((int64_t)r * a.n_q + g * G + hh) * HD, a.q_gain, a.eps, pnew, rot, a.cos_t,
+                            a.sin_t, y);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) qs[hh * HD + lane + 64 * i] = y[i];
+    }
+    if (has_cur && wave == 3) {
+        uint16_t y[EPL];
+        norm_rope_lane<EPL>(a.k + (int64_t)r * kvd + (int64_t)g * HD, a.k_gain, a.eps, pnew, rot, a.cos_t, a.sin_t,
+                            y);
+        const uint16_t* vs = a.v + (int64_t)r * kvd + (int64_t)g * HD;
+        const int64_t d = row0 + pnew;
+        const bool write = rot && d >= 0 && d < a.cache_rows;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = lane + 64 * i;
+            const uint16_t vv = vs[e];
+            kn[e] = y[i];
+            vn[e] = vv;
+            if (write) {
+                a.Kc[d * kvd + (int64_t)g * HD + e] = y[i];
+                a.Vc[d * kvd + (int64_t)g * HD + e] = vv;
+            }
+        }
+    }
+
+    // ---- key tiles: each wavefront a key part x HPW heads, its own softmax
+    const int part = wave % P, h0 = (wave / P) * HPW;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float m_run[2], l_run[2], o[2][EPL];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        m_run[hh] = -INFINITY;
+        l_run[hh] = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) o[hh][i] = 0.f;
+    }
+    for (int c0 = kb, it = 0; c0 < ke; c0 += TK, ++it) {
+        const int nk = min(TK, ke - c0);
+        uint16_t* kt = tiles + 2 * (it & 1) * TK * HD;
+        uint16_t* vt = kt + TK * HD;
+        // this tile landed, and every wave is done with the other buffer:
+        // the next tile's copy goes there and overlaps this tile's math
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c0 + TK < ke) copy_tile((it & 1) ^ 1, c0 + TK, min(TK, ke - c0 - TK));
+        if (has_cur && pnew >= c0 && pnew < c0 + nk) {
+            const int jc = pnew - c0;
+            for (int d8 = threadIdx.x; d8 < CPK; d8 += 256) {
+                *reinterpret_cast<u4v*>(kt + jc * HD + 8 * (d8 ^ (jc & (CPK - 1)))) =
+                    *reinterpret_cast<const u4v*>(kn + 8 * d8);
+                *reinterpret_cast<u4v*>(vt + jc * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vn + 8 * d8);
+            }
+            __syncthreads();
+        }
+        const int kpp = (nk + P - 1) / P;
+        const int jb = min(nk, part * kpp), nkw = min(nk, jb + kpp) - jb;   // <= 128 keys: two per lane at most
+        if (nkw > 0) {
+            for (int hh = 0; hh < HPW; ++hh) {
+                const int h = h0 + hh;
+                if (h >= G) break;
+                const uint16_t* qh = qs + h * HD;
+                float sv[2];
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const int t = lane + 64 * hb;
+                    sv[hb] = -INFINITY;
+                    if (64 * hb < nkw) {   // uniform
+                        const int jr = jb + (t < nkw ? t : nkw - 1);
+                        const uint16_t* kr = kt + jr * HD;
+                        float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+                        for (int d0 = 0; d0 < CPK; d0 += 8) {
+                            u4v kk[8], qv[8];
+#pragma unroll
+                            for (int c = 0; c < 8; ++c) {
+                                kk[c] = *reinterpret_cast<const u4v*>(kr + 8 * ((d0 + c) ^ (jr & (CPK - 1))));
+                                qv[c] = *reinterpret_cast<const u4v*>(qh + 8 * (d0 + c));
+                            }
+                            asm volatile("" ::: "memory");
+#pragma unroll
+                            for (int c = 0; c < 8; ++c) {
+                                acc = dot2(qv[c].x, kk[c].x, acc);
+                                acc2 = dot2(qv[c].y, kk[c].y, acc2);
+                                acc = dot2(qv[c].z, kk[c].z, acc);
+                                acc2 = dot2(qv[c].w, kk[c].w, acc2);
+                            }
+                        }
+                        if (t < nkw) sv[hb] = (acc + acc2) * scale;
+                    }
+                }
+                const float mt = wave_max(fmaxf(sv[0], sv[1]));
+                const float mn = fmaxf(m_run[hh], mt);
+                const float al = m_run[hh] == -INFINITY ? 0.f : __expf(m_run[hh] - mn);
+                float pv[2];
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? __expf(sv[hb] - mn) : 0.f;
+                l_run[hh] = l_run[hh] * al + wave_sum(pv[0] + pv[1]);
+                m_run[hh] = mn;
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) o[hh][i] *= al;
+                // P.V: lane holds dims EPL lane .. EPL lane + EPL - 1
+                const uint16_t* vcol = vt + jb * HD + EPL * lane;
+                for (int t0 = 0; t0 < nkw; t0 += 8) {
+                    uint16_t vv[8][EPL];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int t = min(t0 + u, nkw - 1);
+#pragma unroll
+                        for (int i = 0; i < EPL; ++i) vv[u][i] = vcol[t * HD + i];
+                    }
+                    asm volatile("" ::: "memory");
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int t = t0 + u;   // uniform
+                        if (t < nkw) {
+                            const float pt = __builtin_bit_cast(
+                                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]),
+                                                                 t & 63));
+#pragma unroll
+                            for (int i = 0; i < EPL; ++i) o[hh][i] += pt * h2f(vv[u][i]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();   // all waves are done with the tiles (the merge area reuses them)
+
+    // ---- the P key parts of each head merged in LDS (the tile area is free
+    // after the last barrier), then one record (o, m, l) per (split, head)
+    const int rec = HD + 2;
+    float* pl = reinterpret_cast<float*>(ba_lds);   // P x G records
+    if (P > 1) {
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = h0 + hh;
+            if (h >= G) break;
+            float* pr = pl + (part * G + h) * rec;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) pr[EPL * lane + i] = o[hh][i];
+            if (lane == 0) {
+                pr[HD] = m_run[hh];
+                pr[HD + 1] = l_run[hh];
+            }
+        }
+        __syncthreads();
+        if (part == 0) {
+            for (int hh = 0; hh < HPW; ++hh) {
+                const int h = h0 + hh;
+                if (h >= G) break;
+                float mm = -INFINITY;
+                for (int q = 0; q < P; ++q) mm = fmaxf(mm, pl[(q * G + h) * rec + HD]);
+                float ll = 0.f, oo[EPL];
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) oo[i] = 0.f;
+                for (int q = 0; q < P; ++q) {
+                    const float* pr = pl + (q * G + h) * rec;
+                    const float w = pr[HD] == -INFINITY ? 0.f : __expf(pr[HD] - mm);
+                    ll += w * pr[HD + 1];
+#pragma unroll
+                    for (int i = 0; i < EPL; ++i) oo[i] += w * pr[EPL * lane + i];
+                }
+                m_run[hh] = mm;
+                l_run[hh] = ll;
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) o[hh][i] = oo[i];
+            }
+        }
+    }
+    float* grp = a.recs + ((int64_t)r * a.n_kv + g) * (int64_t)T * G * rec;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(grp, 0, 0x7fffffff, 0x00020000);
+    if (part == 0) {
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = h0 + hh;
+            if (h >= G) break;
+            const int ro = (s * G + h) * rec;   // record offset, floats
+#pragma unroll
+            for (int i = 0; i < EPL; ++i)
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, o[hh][i]), rs,
+                                                      4 * (ro + EPL * lane + i), 0, kBaSc1);
+            if (lane == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m_run[hh]), rs, 4 * (ro + HD), 0,
+                                                      kBaSc1);
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l_run[hh]), rs, 4 * (ro + HD + 1),
+                                                      0, kBaSc1);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* cn = a.cnt + (int64_t)r * a.n_kv + g;
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1) ? 1u
+                                                                                                               : 0u;
+    __syncthreads();
+    if (!last) return;
+
+    // ---- merge of the group's S records per head, in split order: m and l of
+    // every record in one pass (lane t <-> record t), the weights broadcast by
+    // readlane, the o rows requested sixteen records at a time
+    for (int h = wave; h < G; h += 4) {
+        float mt[4], lt[4], wt[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int t = min(lane + 64 * k, T - 1);
+            mt[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * ((t * G + h) * rec + HD), 0,
+                                                                                     kBaSc1));
+            lt[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  rs, 4 * ((t * G + h) * rec + HD + 1), 0, kBaSc1));
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (lane + 64 * k < T) mloc = fmaxf(mloc, mt[k]);
+        const float M = wave_max(mloc);
+        float lloc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const bool in = lane + 64 * k < T && mt[k] != -INFINITY;
+            wt[k] = in ? __expf(mt[k] - M) : 0.f;
+            lloc += wt[k] * (in ? lt[k] : 0.f);
+        }
+        const float L = wave_sum(lloc);
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        float acc[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) acc[i] = 0.f;
+        for (int t0 = 0; t0 < T; t0 += 16) {
+            float ov[16][EPL];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int t = min(t0 + u, T - 1);
+#pragma unroll
+                for (int i = 0; i < EPL; ++i)
+                    ov[u][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                             rs, 4 * ((t * G + h) * rec + EPL * lane + i), 0, kBaSc1));
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int t = t0 + u;   // uniform
+                if (t < T) {
+                    const float w = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt[t >> 6]), t & 63));
+#pragma unroll
+                    for (int i = 0; i < EPL; ++i) acc[i] += w * ov[u][i];
+                }
+            }
+        }
+        uint16_t* op = a.out + ((int64_t)r * a.n_q + g * G + h) * HD + EPL * lane;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) op[i] = f2h(acc[i] * inv);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split plan of the batched attention: about two workgroups per CU over all
+// (row, group) pairs, at least 64 keys a split; P key parts per tile and HPW
+// heads per wavefront from the group size G (four wavefronts).
+struct BaPlan {
+    int S, kps, P, HPW;
+};
+inline BaPlan ba_plan(int rows, int n_q, int n_kv, int max_len) {
+    BaPlan p;
+    const int G = n_q / n_kv;
+    p.P = G >= 4 ? 1 : 4 / G;
+    p.HPW = G > 4 ? (G + 3) / 4 : 1;
+    int S = (2 * num_cus()) / max(1, rows * n_kv);
+    S = max(1, min(min(S, (max_len + 63) / 64), 256));   // the merge takes at most 256 records
+    p.kps = ((max_len + S - 1) / S + 15) / 16 * 16;
+    p.S = (max_len + p.kps - 1) / p.kps;
+    return p;
+}
+inline size_t ba_lds_bytes(int hd) { return (size_t)4 * 8192 * 2 + (size_t)10 * hd * 2; }
 
 inline unsigned blocks_of(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
@@ -153,6 +532,60 @@ int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int co
                                                                                           dst_rows_dev, cache_rows,
                                                                                           Kc, Vc);
     return launch_check("kv_append_rows");
+}
+
+size_t bx_batch_attention_workspace_bytes(int rows, int n_q, int n_kv, int hd, int max_len) {
+    if (rows <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv || hd <= 0 || max_len <= 0) return 0;
+    const BaPlan p = ba_plan(rows, n_q, n_kv, max_len);
+    const size_t cnt = ((size_t)rows * n_kv * 4 + 255) / 256 * 256;
+    return cnt + (size_t)rows * n_q * p.S * (hd + 2) * sizeof(float);
+}
+
+int bx_batch_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int rows, int hd, int n_q,
+                           int n_kv, const uint16_t* q_gain, const uint16_t* k_gain, float eps, const int32_t* lens_dev,
+                           const int64_t* base_rows_dev, int max_len, const float* cos_tab, const float* sin_tab,
+                           int tab_rows, uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, uint16_t* out,
+                           void* workspace, void* stream) {
+    if (!q || !k || !v || !lens_dev || !base_rows_dev || !cos_tab || !sin_tab || !Kc || !Vc || !out || !workspace ||
+        rows <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv || max_len <= 0 || tab_rows <= 0 || cache_rows <= 0 ||
+        (q_gain == nullptr) != (k_gain == nullptr))
+        return fail(BX_EINVAL, "batch_attention: bad arguments");
+    if (n_q / n_kv > 8) return fail(BX_EUNSUPPORTED, "batch_attention: at most 8 query heads per KV head");
+    const BaPlan p = ba_plan(rows, n_q, n_kv, max_len);
+    const size_t cnt = ((size_t)rows * n_kv * 4 + 255) / 256 * 256;
+    if ((size_t)rows * n_q * p.S * (hd + 2) * sizeof(float) >= (size_t)1 << 31)
+        return fail(BX_EUNSUPPORTED, "batch_attention: records beyond 2 GiB");
+    BatchAttnArgs a{};
+    a.q = q; a.k = k; a.v = v;
+    a.q_gain = q_gain; a.k_gain = k_gain; a.eps = eps;
+    a.lens = lens_dev; a.base = base_rows_dev;
+    a.cos_t = cos_tab; a.sin_t = sin_tab; a.tab_rows = tab_rows;
+    a.Kc = Kc; a.Vc = Vc; a.cache_rows = cache_rows;
+    a.n_q = n_q; a.n_kv = n_kv; a.S = p.S; a.kps = p.kps; a.P = p.P; a.HPW = p.HPW;
+    a.cnt = static_cast<uint32_t*>(workspace);
+    a.recs = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + cnt);
+    a.out = out;
+    const dim3 grid((unsigned)p.S, (unsigned)n_kv, (unsigned)rows);
+    const size_t lds = ba_lds_bytes(hd);
+    hipStream_t st = as_stream(stream);
+    auto launch = [&](const void* fn, auto kern) -> int {
+        static bool attr_done[3] = {false, false, false};
+        const int slot = hd == 64 ? 0 : hd == 128 ? 1 : 2;
+        if (!attr_done[slot] && lds > 64 * 1024) {
+            if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                                   "batch_attention: LDS attribute"))
+                return rc;
+            attr_done[slot] = true;
+        }
+        kern<<<grid, 256, lds, st>>>(a);
+        return launch_check("batch_attention");
+    };
+    switch (hd) {
+        case 64: return launch(reinterpret_cast<const void*>(&batch_attn_kernel<64>), batch_attn_kernel<64>);
+        case 128: return launch(reinterpret_cast<const void*>(&batch_attn_kernel<128>), batch_attn_kernel<128>);
+        case 256: return launch(reinterpret_cast<const void*>(&batch_attn_kernel<256>), batch_attn_kernel<256>);
+        default: return fail(BX_EUNSUPPORTED, "batch_attention: head_dim must be 64, 128 or 256");
+    }
 }
 
 int bx_qk_rope_kv_rows_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int rows, int hd, int n_q,

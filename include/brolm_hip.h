@@ -155,6 +155,21 @@ int bx_rope_rows_f16(const uint16_t* X, uint16_t* Y, int rows, int hd, int n_hea
 /* kv_cache_append of row r to cache row dst_rows_dev[r] (< cache_rows). */
 int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int cols, const int64_t* dst_rows_dev,
                           uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, void* stream);
+/* Attention of one batched step with its per-head stage in one launch: for row
+ * r (its sequence's newest token at position lens_dev[r] - 1, keys in cache
+ * rows base_rows_dev[r] .. + lens_dev[r] - 1): the q / k head RMSNorm and RoPE
+ * of bx_qk_rope_kv_rows_f16 (same bits), the new k / v rows written to the
+ * cache, split attention over the row's keys and the merge of the splits ->
+ * out (rows, n_q*hd) FP16.  q, k, v: the raw projections.  workspace:
+ * bx_batch_attention_workspace_bytes(rows, ...) bytes, zeroed once before its
+ * first use (the kernel leaves its counters at zero); calls sharing one
+ * workspace must not overlap.  hd: 64, 128 or 256; n_q / n_kv <= 8. */
+size_t bx_batch_attention_workspace_bytes(int rows, int n_q, int n_kv, int hd, int max_len);
+int bx_batch_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int rows, int hd, int n_q,
+                           int n_kv, const uint16_t* q_gain, const uint16_t* k_gain, float eps, const int32_t* lens_dev,
+                           const int64_t* base_rows_dev, int max_len, const float* cos_tab, const float* sin_tab,
+                           int tab_rows, uint16_t* Kc, uint16_t* Vc, int64_t cache_rows, uint16_t* out,
+                           void* workspace, void* stream);
 /* The per-head ops of one batched step in one launch (dense_decoder.cpp:
  * 575-607 per row): q / k head RMSNorm with q_gain / k_gain (both null: none),
  * RoPE at pos_dev[r], roped q heads to q_out (may be q), roped k rows and the

@@ -235,3 +235,74 @@ def test_qk_rope_kv_rows_equals_separate_ops(hd, norm):
     assert np.array_equal(host(Kf), host(Ks)) and np.array_equal(host(Vf), host(Vs))
     untouched = np.setdiff1d(np.arange(cap), dst)
     assert np.array_equal(host(Kf).reshape(cap, width)[untouched], fill[untouched])
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv,norm,cap", [(128, 8, 4, True, 300), (64, 8, 2, False, 200),
+                                                  (256, 2, 2, True, 150), (128, 16, 2, True, 700)])
+def test_batch_attention_fused(hd, n_q, n_kv, norm, cap):
+    """bx_batch_attention_f16 (q / k norm + RoPE + k / v cache write + split
+    attention + merge in one launch): the cache rows it writes have exactly the
+    bits of bx_qk_rope_kv_rows_f16, the output matches a float64 softmax over
+    each row's own keys (atol 3e-3, as the single-sequence kernel), for ragged
+    rows in scattered slots across several key tiles and splits (one row with a
+    single key); a second launch gives the same bits (its counters are back at
+    zero)."""
+    from gpu_util import call, dev, f16_dev, f16_host, host, ptr, stream, torch
+    import ctypes as C
+    import brolm_amd._native as nat
+    print(f"[batch] fused attention hd={hd} n_q={n_q} n_kv={n_kv} norm={norm} cap={cap}", flush=True)
+    rng = np.random.default_rng(hd * 7 + n_q + cap)
+    slots = [3, 0, 5, 1, 4]
+    lens = [cap, 1, cap // 2 + 7, 129, 64]
+    M, n_slots, width = len(slots), 6, n_kv * hd
+    rows_total = n_slots * cap
+    q = rng.standard_normal((M, n_q * hd))
+    k = rng.standard_normal((M, width))
+    v = rng.standard_normal((M, width))
+    qg = rng.uniform(0.5, 1.5, hd) if norm else None
+    kg = rng.uniform(0.5, 1.5, hd) if norm else None
+    cache_k = (rng.standard_normal((rows_total, width)) * 0.5).astype(np.float16)
+    cache_v = rng.standard_normal((rows_total, width)).astype(np.float16)
+    cos_t = np.empty((cap, hd // 2), np.float32)
+    sin_t = np.empty((cap, hd // 2), np.float32)
+    nat.hip().bx_rope_table_host(cos_t.ctypes.data_as(nat.P_f32), sin_t.ctypes.data_as(nat.P_f32), cap, hd, 1e6)
+    cs, sn = dev(cos_t), dev(sin_t)
+    base = np.array([s * cap for s in slots], np.int64)
+    lens_a = np.array(lens, np.int32)
+    pos = lens_a - 1
+    dst = base + pos
+    gq = f16_dev(qg) if norm else None
+    gk = f16_dev(kg) if norm else None
+    qd, kd, vd = f16_dev(q), f16_dev(k), f16_dev(v)
+    # the separate q / k stage (reference for the cache rows and the roped q)
+    qs = f16_dev(q)
+    Ks, Vs = dev(cache_k.view(np.uint16)), dev(cache_v.view(np.uint16))
+    call("bx_qk_rope_kv_rows_f16", ptr(qs), ptr(kd), ptr(vd), M, hd, n_q, n_kv, ptr(gq), ptr(gk), C.c_float(1e-6),
+         ptr(dev(pos)), ptr(cs), ptr(sn), cap, ptr(dev(dst)), ptr(Ks), ptr(Vs), rows_total, ptr(qs), stream())
+    # fused
+    Kf, Vf = dev(cache_k.view(np.uint16)), dev(cache_v.view(np.uint16))
+    wsb = nat.hip().bx_batch_attention_workspace_bytes(M, n_q, n_kv, hd, cap)
+    ws = torch().zeros(wsb, dtype=torch().uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        out = torch().empty(M * n_q * hd, dtype=torch().int16, device="cuda")
+        call("bx_batch_attention_f16", ptr(qd), ptr(kd), ptr(vd), M, hd, n_q, n_kv, ptr(gq), ptr(gk),
+             C.c_float(1e-6), ptr(dev(lens_a)), ptr(dev(base)), cap, ptr(cs), ptr(sn), cap, ptr(Kf), ptr(Vf),
+             rows_total, ptr(out), ptr(ws), stream())
+        outs.append(host(out))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(host(Kf), host(Ks)) and np.array_equal(host(Vf), host(Vs))
+    Kh = host(Ks).view(np.float16).reshape(rows_total, width)
+    Vh = host(Vs).view(np.float16).reshape(rows_total, width)
+    qr = f16_host(qs).reshape(M, n_q * hd)
+    got = outs[0].view(np.float16).astype(np.float32).reshape(M, n_q * hd)
+    G = n_q // n_kv
+    for r in range(M):
+        keys = np.arange(base[r], base[r] + lens[r])
+        for h in range(n_q):
+            g = h // G
+            sc = Kh[keys, g * hd:(g + 1) * hd].astype(np.float64) @ qr[r, h * hd:(h + 1) * hd].astype(np.float64)
+            w = np.exp(sc / np.sqrt(hd) - (sc / np.sqrt(hd)).max())
+            ref = (w / w.sum()) @ Vh[keys, g * hd:(g + 1) * hd].astype(np.float64)
+            np.testing.assert_allclose(got[r, h * hd:(h + 1) * hd], ref, atol=3e-3, err_msg=f"row {r} head {h}")
+    assert not host(ws)[:256].any()   # counters back at zero
