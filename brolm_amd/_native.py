@@ -114,6 +114,12 @@ HIP_SYMBOLS = {
     "bx_sample_feed_f16": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, vp, vp, vp, vp, vp, vp]),
     "bx_rope_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp]),
     "bx_kv_append_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp, vp, i64, vp]),
+    "bx_linear_ss_floats": (C.c_size_t, [C.c_int]),
+    "bx_linear_residual_ss_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "bx_linear_group_norm_f16": (C.c_int, [C.c_int, C.c_int, vp, vp, vp, vp, vp, C.c_float, vp, C.c_int, C.c_int,
+                                           vp]),
+    "bx_linear_swiglu_norm_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_float, vp, vp, C.c_int, C.c_int, C.c_int,
+                                            vp]),
     "bx_batch_attention_workspace_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "bx_batch_attention_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
                                          C.c_int, vp, vp, C.c_int, vp, vp, i64, vp, vp, vp]),

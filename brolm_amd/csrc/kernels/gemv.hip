@@ -23,6 +23,12 @@ int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, 
 int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st);
 int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
                      hipStream_t st);
+int gemv_mfma_resid_ss(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N, int K,
+                       hipStream_t st);
+int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
+                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, hipStream_t st);
+int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,
+                          const float* ss_in, uint16_t* Y, int M, int F, int K, hipStream_t st);
 
 // The fused linear forms run on the MFMA tile GEMM (M >= 128, K % 64 == 0)
 // and, for decode batches, on the MFMA GEMV (3 <= M <= 16, K % 256 == 0).
@@ -252,4 +258,39 @@ extern "C" int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, c
     if (!bx::gemm_tiles_ok(M, K))
         return bx::fail(BX_EUNSUPPORTED, "linear_swiglu: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_swiglu_f16(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
+}
+
+// Decode-batch forms with the residual RMSNorm carried between launches (3 <=
+// M <= 16, K % 256 == 0, matrices the split batched GEMV takes; otherwise
+// BX_EUNSUPPORTED and nothing launched, and the caller runs the separate norm).
+extern "C" size_t bx_linear_ss_floats(int N) { return N > 0 ? (size_t)(N + 63) / 64 * 16 : 0; }
+
+extern "C" int bx_linear_residual_ss_f16(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M,
+                                         int N, int K, void* stream) {
+    if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
+    if (!W || !X || !H || !ss_out) return bx::fail(BX_EINVAL, "linear_residual_ss: null pointer");
+    if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_residual_ss: needs 3 <= M <= 16, K % 256 == 0");
+    return bx::gemv_mfma_resid_ss(wtype, W, X, H, ss_out, M, N, K, bx::as_stream(stream));
+}
+
+extern "C" int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N,
+                                        const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
+                                        int K, void* stream) {
+    if (n < 1 || n > 3 || !W || !Y || !N || !H || !gamma || !ss_in)
+        return bx::fail(BX_EINVAL, "linear_group_norm: bad arguments");
+    for (int i = 0; i < n; ++i) {
+        if (int rc = bx::check_linear_shape(wtype, M, N[i], K)) return rc;
+        if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group_norm: null pointer");
+    }
+    if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_group_norm: needs 3 <= M <= 16, K % 256 == 0");
+    return bx::gemv_mfma_group_norm(wtype, n, W, Y, N, H, gamma, eps, ss_in, M, K, bx::as_stream(stream));
+}
+
+extern "C" int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const float* H,
+                                         const uint16_t* gamma, float eps, const float* ss_in, uint16_t* Y, int M,
+                                         int F, int K, void* stream) {
+    if (int rc = bx::check_linear_shape(wtype, M, F, K)) return rc;
+    if (!Wg || !Wu || !H || !gamma || !ss_in || !Y) return bx::fail(BX_EINVAL, "linear_swiglu_norm: null pointer");
+    if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_swiglu_norm: needs 3 <= M <= 16, K % 256 == 0");
+    return bx::gemv_mfma_swiglu_norm(wtype, Wg, Wu, H, gamma, eps, ss_in, Y, M, F, K, bx::as_stream(stream));
 }

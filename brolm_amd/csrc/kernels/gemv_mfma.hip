@@ -317,6 +317,16 @@ struct MfmaJob {
     int64_t tiles_n[3];
     int members;
     int64_t tiles;          // total tiles of the launch
+    // norm-input split launches: X is the RMSNorm (gamma, eps) of the FP32
+    // rows Hn, row m's sum of squares the sum of ss_in[q * 16 + m], q < ss_groups
+    const float* Hn;
+    const uint16_t* gamma;
+    const float* ss_in;
+    int ss_groups;
+    float eps;
+    // residual split launches: row sums of squares of the updated residual,
+    // ss_out[group * 16 + m] for the 64 columns of each tile group (or null)
+    float* ss_out;
 };
 
 // Tile t of the launch -> (member, row tile within the member).
@@ -503,10 +513,13 @@ __global__ void split_clear_kernel() {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kSplGroups; i += gridDim.x * blockDim.x) split_cnt[i] = 0u;
 }
 
-// The epilogue of one tile from lane values a (and u for SwiGLU).
+// The epilogue of one tile from lane values a (and u for SwiGLU); for the
+// residual, sq[j] is the square of the lane's updated value of row 4 g + j
+// (0 where there is none).
 template <int EPI>
 __device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, int r, int g, int Mr, const f4v& a,
-                                              const f4v& u) {
+                                              const f4v& u, f4v& sq) {
+    sq = f4v{0.f, 0.f, 0.f, 0.f};
     int mem;
     int64_t lt;
     member_of(job, tile, mem, lt);
@@ -522,7 +535,11 @@ __device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, 
             if (4 * g + j < Mr) hv[j] = job.H[(int64_t)(4 * g + j) * N + n];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (4 * g + j < Mr) job.H[(int64_t)(4 * g + j) * N + n] = hv[j] + h2f(f2h(a[j]));
+            if (4 * g + j < Mr) {
+                const float y = hv[j] + h2f(f2h(a[j]));
+                job.H[(int64_t)(4 * g + j) * N + n] = y;
+                sq[j] = y * y;
+            }
         return;
     }
 #pragma unroll
@@ -538,11 +555,33 @@ __device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, 
     }
 }
 
-template <int FMT, int EPI, int CPS>
+// Row sums of squares of a residual tile group (its 4 tiles x 16 columns):
+// over the 16 lanes of a row group by DPP, then the 4 wavefronts in order, to
+// ss_out[blockIdx.x * 16 + m].  Every thread of the workgroup calls it.
+__device__ __forceinline__ void group_row_ss(const MfmaJob& job, int Mr, int wave, int r, int g, const f4v& sq,
+                                             float (*wss)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float v = sq[j];
+        v += dpp_f<0xB1>(v, 0.f);
+        v += dpp_f<0x4E>(v, 0.f);
+        v += dpp_f<0x141>(v, 0.f);
+        v += dpp_f<0x140>(v, 0.f);
+        if (r == 0) wss[wave][4 * g + j] = v;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < Mr) {
+        const int m = threadIdx.x;
+        job.ss_out[blockIdx.x * 16 + m] = ((wss[0][m] + wss[1][m]) + wss[2][m]) + wss[3][m];
+    }
+}
+
+template <int FMT, int EPI, int CPS, bool NIN>
 __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const uint16_t* __restrict__ X, int Mr,
                                                             int K, int S) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint32_t last;
+    __shared__ float wss[kSplWav][16];   // per-row partials: residual sums of squares, norm-input row sums
     constexpr bool kSwz = FMT != FMT_F16;
     constexpr bool kTwo = EPI == MEPI_SWIGLU;
     constexpr int kParts = kTwo ? 2 : 1;
@@ -575,7 +614,62 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     xst.xrow = (r < Mr ? r : Mr) * xstride;
     uint32_t* xs2 = smem + (Mr + 1) * xstride;
     xst.xs2 = xs2;
-    stage_x_f16<kSwz, false>(X + 256 * c0, K, Mr, Ks, smem, xstride, nullptr, 0);
+    if constexpr (NIN) {
+        // the thread's first four 4-element groups of the slice (h and gamma)
+        // are requested before the row sums are added, so both round trips
+        // overlap; groups past the slice repeat its last one (in bounds)
+        const int G4 = Ks / 4, total = Mr * G4;
+        f4v hv[4];
+        u2v gv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = min((int)threadIdx.x + kSplThr * j, total - 1);
+            const int m = i / G4, k = 256 * c0 + 4 * (i - m * G4);
+            hv[j] = *reinterpret_cast<const f4v*>(job.Hn + (int64_t)m * K + k);
+            gv[j] = *reinterpret_cast<const u2v*>(job.gamma + k);
+        }
+        // each row's 1 / rms from the producer's per-group sums of squares:
+        // thread (q0, m) adds groups q0, q0 + 16, ..., then row m adds the 16
+        // part sums in order
+        __shared__ float qsum[16][16];
+        __shared__ float row_inv[16];
+        {
+            const int m = threadIdx.x & 15, q0 = threadIdx.x >> 4;
+            float v = 0.f;
+            if (m < Mr)
+                for (int q = q0; q < job.ss_groups; q += 16) v += job.ss_in[q * 16 + m];
+            qsum[q0][m] = v;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < Mr) {
+            const int m = threadIdx.x;
+            float ssum = 0.f;
+#pragma unroll
+            for (int q0 = 0; q0 < 16; ++q0) ssum += qsum[q0][m];
+            row_inv[m] = 1.0f / sqrtf(ssum / (float)K + job.eps);
+        }
+        __syncthreads();
+        // the slice of the normalised rows, FP16, into LDS
+        auto put = [&](int i, const f4v& h4, const u2v& g4) {
+            const int m = i / G4, gg = i - m * G4;
+            const float inv = row_inv[m];
+            store_group<kSwz>(smem + m * xstride, gg, norm_f16(h4.x, inv, h2f(g4.x & 0xffff)),
+                              norm_f16(h4.y, inv, h2f(g4.x >> 16)), norm_f16(h4.z, inv, h2f(g4.y & 0xffff)),
+                              norm_f16(h4.w, inv, h2f(g4.y >> 16)));
+        };
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = threadIdx.x + kSplThr * j;
+            if (i < total) put(i, hv[j], gv[j]);
+        }
+        for (int i = threadIdx.x + 4 * kSplThr; i < total; i += kSplThr) {
+            const int m = i / G4, k = 256 * c0 + 4 * (i - m * G4);
+            put(i, *reinterpret_cast<const f4v*>(job.Hn + (int64_t)m * K + k),
+                *reinterpret_cast<const u2v*>(job.gamma + k));
+        }
+    } else {
+        stage_x_f16<kSwz, false>(X + 256 * c0, K, Mr, Ks, smem, xstride, nullptr, 0);
+    }
     for (int i = threadIdx.x; i < xstride; i += kSplThr) smem[Mr * xstride + i] = 0u;
     __syncthreads();
     if constexpr (FMT == FMT_Q4_K) {
@@ -590,8 +684,11 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
             if constexpr (kTwo) cu[i].mul(xst, 256 * i, r, g, accu);
         }
     }
+    f4v sq;
     if (S == 1) {
-        if (live) tile_epilogue<EPI>(job, tile, r, g, Mr, acc, accu);
+        if (live) tile_epilogue<EPI>(job, tile, r, g, Mr, acc, accu, sq);
+        else sq = f4v{0.f, 0.f, 0.f, 0.f};
+        if (EPI == MEPI_RESID && job.ss_out) group_row_ss(job, Mr, wave, r, g, sq, wss);
         return;
     }
     // Partial tile (tile, s): kParts blocks of the lane values of the lanes
@@ -640,8 +737,11 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
                 }
             }
         }
-        tile_epilogue<EPI>(job, tile, r, g, Mr, a, u);
+        tile_epilogue<EPI>(job, tile, r, g, Mr, a, u, sq);
+    } else {
+        sq = f4v{0.f, 0.f, 0.f, 0.f};
     }
+    if (EPI == MEPI_RESID && job.ss_out) group_row_ss(job, Mr, wave, r, g, sq, wss);
     if (threadIdx.x == 0) __hip_atomic_store(&split_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -680,8 +780,12 @@ constexpr size_t kMaxLds = 160 * 1024;
 constexpr int64_t kSplitTiles = 2048;
 
 // Launch a job for M rows of X, in row chunks whose staging fits the LDS.
+// nin: X is the RMSNorm of job.Hn (the split form only); split_only: fail
+// with BX_EUNSUPPORTED, launching nothing, when the split form does not apply
+// (norm-input launches, and residual launches that must report row sums).
 template <int EPI>
-int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStream_t st) {
+int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStream_t st, bool nin = false,
+                bool split_only = false) {
     int fmt;
     switch (wtype) {
         case BX_TYPE_Q4_K: fmt = FMT_Q4_K; break;
@@ -707,18 +811,30 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
     int cps = 0;
     const int S = split_plan(K, cps);
     const int64_t groups = (tiles + kSplWav - 1) / kSplWav;
-    if (S > 0 && M <= 16 && tiles <= kSplitTiles && groups <= kSplGroups &&
-        groups * kSplWav * S * (two ? 2 : 1) * M * 16 <= kSplFloats) {
+    const bool split = S > 0 && M <= 16 && tiles <= kSplitTiles && groups <= kSplGroups &&
+                       groups * kSplWav * S * (two ? 2 : 1) * M * 16 <= kSplFloats;
+    if (split) {
         if (int rc = split_ready(st)) return rc;
         const size_t lds = (size_t)(M + 1) * (128 * cps + 4) * 4 + (fmt == FMT_Q4_K ? (size_t)8 * cps * 16 * 4 : 0);
         const dim3 grid((unsigned)groups, (unsigned)S);
-        BX_DISPATCH_FMT(wtype, {
-            if (cps == 1) gemv_split_kernel<FMT_, EPI, 1><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
-            else if (cps == 2) gemv_split_kernel<FMT_, EPI, 2><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
-            else gemv_split_kernel<FMT_, EPI, 3><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
-        })
+        if (nin) {
+            if constexpr (EPI != MEPI_RESID) {
+                BX_DISPATCH_FMT(wtype, {
+                    if (cps == 1) gemv_split_kernel<FMT_, EPI, 1, true><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                    else if (cps == 2) gemv_split_kernel<FMT_, EPI, 2, true><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                    else gemv_split_kernel<FMT_, EPI, 3, true><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                })
+            }
+        } else {
+            BX_DISPATCH_FMT(wtype, {
+                if (cps == 1) gemv_split_kernel<FMT_, EPI, 1, false><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                else if (cps == 2) gemv_split_kernel<FMT_, EPI, 2, false><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                else gemv_split_kernel<FMT_, EPI, 3, false><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+            })
+        }
         return launch_check("gemv split");
     }
+    if (split_only || nin) return fail(BX_EUNSUPPORTED, "gemv: the fused-norm forms need the split launch");
     for (int m0 = 0; m0 < M; m0 += mc) {
         const int mr = M - m0 < mc ? M - m0 : mc;
         const size_t lds = mfma_lds_bytes(fmt, mr, K, two);
@@ -783,6 +899,50 @@ int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M
     job.H = H;
     job.members = 1;
     return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, st);
+}
+
+int gemv_mfma_resid_ss(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N, int K,
+                       hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = W;
+    job.N[0] = N;
+    job.H = H;
+    job.ss_out = ss_out;
+    job.members = 1;
+    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, st, false, true);
+}
+
+int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
+                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, hipStream_t st) {
+    MfmaJob job{};
+    for (int i = 0; i < n; ++i) {
+        job.W[i] = W[i];
+        job.Y[i] = Y[i];
+        job.N[i] = N[i];
+    }
+    job.members = n;
+    job.Hn = H;
+    job.gamma = gamma;
+    job.eps = eps;
+    job.ss_in = ss_in;
+    job.ss_groups = (K + 63) / 64;
+    return mfma_launch<MEPI_STORE>(wtype, job, nullptr, M, K, st, true);
+}
+
+int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,
+                          const float* ss_in, uint16_t* Y, int M, int F, int K, hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = Wg;
+    job.W[1] = Wu;
+    job.Y[0] = Y;
+    job.N[0] = F;
+    job.members = 1;
+    job.Hn = H;
+    job.gamma = gamma;
+    job.eps = eps;
+    job.ss_in = ss_in;
+    job.ss_groups = (K + 63) / 64;
+    return mfma_launch<MEPI_SWIGLU>(wtype, job, nullptr, M, K, st, true);
 }
 
 int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,

@@ -171,7 +171,7 @@ private:
     // the batched step's own activations, sized for n_slots rows at
     // allocate_batch so that a step of any M <= n_slots keeps their addresses
     // (each M's step is captured once into a hipGraph and replayed)
-    brotensor::Tensor bh_, bnorm_, bq_, bk_, bv_, battn_, bproj_, bgate_, bup_, blogits_, bws_;
+    brotensor::Tensor bh_, bnorm_, bq_, bk_, bv_, battn_, bproj_, bgate_, bup_, blogits_, bws_, bss_;
     struct BatchGraphs;
     std::unique_ptr<BatchGraphs> batch_graphs_;
     void enqueue_batch_(int M);

@@ -96,6 +96,24 @@ int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const*
 int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* stream);
 int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F,
                          int K, void* stream);
+/* Decode batches (3 <= M <= 16, K % 256 == 0) with the residual RMSNorm
+ * (rms_norm_forward, dense_decoder.cpp:559, :540-550) carried between
+ * launches instead of run on its own: bx_linear_residual_ss_f16 is
+ * bx_linear_residual_f16 that also writes, per 64 columns of the updated H,
+ * each row's sum of squares (ss_out: bx_linear_ss_floats(N) floats); the
+ * group / SwiGLU forms then take X = RMSNorm(H; gamma, eps) with the row sums
+ * of those partials (ss_in from the launch that last updated H, K = its N).
+ * The norm's sum of squares is added in another order than bx_rms_norm's.
+ * All three return BX_EUNSUPPORTED, launching nothing, for matrices outside
+ * the split batched GEMV (the caller then runs bx_rms_norm and the plain
+ * forms). */
+size_t bx_linear_ss_floats(int N);
+int bx_linear_residual_ss_f16(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N,
+                              int K, void* stream);
+int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
+                             const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* stream);
+int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma,
+                              float eps, const float* ss_in, uint16_t* Y, int M, int F, int K, void* stream);
 
 /* ------------------------------------------------------------- elementwise */
 

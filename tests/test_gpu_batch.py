@@ -45,7 +45,7 @@ def _oracles(path, n, cap):
                                         ("small_m3_gguf", "mistral3")])
 def test_batched_steps_match_each_sequence_alone(ba, which, arch, request):
     """Ragged prompts in non-contiguous slots, then steps over changing
-    subsets of the slots in shuffled row order (M from 1 to 5)."""
+    subsets of the slots in shuffled row order (M from 1 to 5), then all 8."""
     path = request.getfixturevalue(which)
     print(f"[batch] {which}", flush=True)
     cap = 64
@@ -63,6 +63,15 @@ def test_batched_steps_match_each_sequence_alone(ba, which, arch, request):
         assert np.abs(got - want).max() <= LOGIT_TOL, f"prefill slot {s}"
         assert m.slot_len(s) == n
     steps = [[0, 2, 3, 5, 7], [7, 0, 3], [5], [2, 7, 5, 0], [3, 2, 0, 7, 5], [0, 5]]
+    # then every slot: 8 rows (the residual norms carried by the GEMV launches)
+    for s in (1, 4, 6):
+        prompt = rng.integers(0, V, 4 + s).tolist()
+        m.prefill_slot(s, prompt)
+        om[s] = _oracles(path, 1, cap)[0]
+        om[s].forward(prompt, last_only=True)
+        lens.append(4 + s)
+        slots.append(s)
+    steps += [[6, 1, 0, 3, 5, 2, 7, 4], [0, 1, 2, 3, 4, 5, 6, 7]]
     for step in steps:
         ids = rng.integers(0, V, len(step)).tolist()
         got = m.forward_batch(ids, step)
@@ -72,7 +81,7 @@ def test_batched_steps_match_each_sequence_alone(ba, which, arch, request):
             err = np.abs(got[r] - want).max()
             assert err <= LOGIT_TOL, f"step {step} row {r} slot {s}: {err}"
     for s, n in zip(slots, lens):
-        assert m.slot_len(s) == n + sum(s in st for st in steps)
+        assert m.slot_len(s) == n + sum(s in st for st in steps[6 if s in (1, 4, 6) else 0:])
     m.close()
 
 
@@ -164,23 +173,25 @@ def test_batched_graph_replays_equal_eager(ba, small_gguf, monkeypatch):
             monkeypatch.setenv("BROLM_NO_GRAPH", "1")
         m = _model(ba, small_gguf, "qwen3")
         m.allocate_cache(32)
-        m.allocate_batch(6, 48)
+        m.allocate_batch(10, 48)
         monkeypatch.delenv("BROLM_NO_GRAPH", raising=False)
         models[mode] = m
     V = models["graph"].cfg.vocab_size
     rng = np.random.default_rng(3)
-    for s, n in zip(range(4), (3, 9, 1, 5)):
+    for s, n in zip(range(8), (3, 9, 1, 5, 2, 7, 4, 6)):
         prompt = rng.integers(0, V, n).tolist()
         for m in models.values():
             m.prefill_slot(s, prompt)
+    # 4 rows (norms on their own) and 8 rows (norms carried by the GEMVs)
     for step in range(6):
-        ids = rng.integers(0, V, 4).tolist()
-        order = rng.permutation(4).tolist()
+        M = 4 if step % 2 == 0 else 8
+        ids = rng.integers(0, V, M).tolist()
+        order = rng.permutation(M).tolist()
         out = {k: m.forward_batch(ids, order) for k, m in models.items()}
         assert np.array_equal(out["graph"], out["eager"]), f"step {step}"
         # unrelated device work between replays
         for m in models.values():
-            m.prefill_slot(5, [int(step) + 1])
+            m.prefill_slot(9, [int(step) + 1])
             m.forward_last([7])
     for m in models.values():
         m.close()

@@ -495,3 +495,69 @@ def test_linear_rejects_bad_shapes_and_types():
     assert h.bx_linear_f16(2, ptr(x), None, ptr(x), ptr(y), 1, 1, 256, stream()) == -3    # unsupported type
     assert h.bx_linear_f16(12, None, None, ptr(x), ptr(y), 1, 1, 256, stream()) == -1     # null weight
     assert b"linear" in h.bx_last_error()
+
+
+@pytest.mark.parametrize("t", [12, 14, 8])
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_linear_norm_carried_between_launches(t, M):
+    """Decode-batch forms with the residual RMSNorm carried between launches:
+    bx_linear_residual_ss_f16 updates H exactly as bx_linear_residual_f16 and
+    writes partial row sums of squares adding up to each row's sum (rel 1e-5);
+    bx_linear_group_norm_f16 / bx_linear_swiglu_norm_f16 on H match
+    bx_rms_norm + the plain forms up to the FP16 rounding of the normalised
+    input (their sum of squares is added in another order); outside the split
+    GEMV (M = 2, or N beyond 32768 rows) they refuse with BX_EUNSUPPORTED and
+    write nothing."""
+    print(f"[linear norm] type={t} M={M}", flush=True)
+    rng = np.random.default_rng(700 + t + M)
+    K, Ka, F = 2048, 1024, 768
+    Ns = (512, 256, 256)
+    Wo, Wov = _weights(rng, t, K, Ka)
+    ws = [_weights(rng, t, n, K) for n in Ns]
+    wg, wu = _weights(rng, t, F, K), _weights(rng, t, F, K)
+    gamma = _f16(rng.uniform(0.5, 1.5, K))
+    gd = f16_dev(gamma)
+    X = _f16(rng.standard_normal((M, Ka)))
+    H0 = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    h = hip()
+    nss = h.bx_linear_ss_floats(K)
+    ss = torch().zeros(nss, dtype=torch().float32, device="cuda")
+    # residual with row sums vs the plain residual
+    Hs, Hp = dev(H0), dev(H0)
+    call("bx_linear_residual_ss_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hs), ptr(ss), M, K, Ka, stream())
+    call("bx_linear_residual_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hp), M, K, Ka, stream())
+    Hn = host(Hs).reshape(M, K)
+    assert np.array_equal(Hn.view(np.uint32), host(Hp).reshape(M, K).view(np.uint32))
+    rows = host(ss).reshape(-1, 16)[:, :M].sum(axis=0, dtype=np.float64)
+    np.testing.assert_allclose(rows, (Hn.astype(np.float64) ** 2).sum(axis=1), rtol=1e-5)
+    # separate norm -> FP16 X for the plain forms
+    xn = torch().empty(M * K, dtype=torch().int16, device="cuda")
+    call("bx_rms_norm", ptr(Hs), 1, ptr(gd), C.c_float(1e-6), ptr(xn), M, K, stream())
+    Xn = f16_host(xn).reshape(M, K)
+    ys = [torch().empty(M * n, dtype=torch().int16, device="cuda") for n in Ns]
+    yr = [torch().empty(M * n, dtype=torch().int16, device="cuda") for n in Ns]
+    W_arr = (C.c_void_p * 3)(*[ptr(w[0]) for w in ws])
+    N_arr = (C.c_int * 3)(*Ns)
+    call("bx_linear_group_norm_f16", t, 3, W_arr, (C.c_void_p * 3)(*[ptr(y) for y in ys]), N_arr, ptr(Hs), ptr(gd),
+         C.c_float(1e-6), ptr(ss), M, K, stream())
+    call("bx_linear_group_f16", t, 3, W_arr, (C.c_void_p * 3)(*[ptr(y) for y in yr]), N_arr, ptr(xn), M, K, stream())
+    for (w, Wv), n, y, r in zip(ws, Ns, ys, yr):
+        got, ref = f16_host(y).reshape(M, n), f16_host(r).reshape(M, n)
+        # one FP16 ulp of the normalised input per element, on top of the output rounding
+        tol = 2.0 ** -10 * np.abs(ref) + 2.0 ** -10 * (np.abs(Xn) @ np.abs(Wv).T) + 1e-6
+        assert np.all(np.abs(got - ref) <= tol), (n, float((np.abs(got - ref) / tol).max()))
+    act = torch().empty(M * F, dtype=torch().int16, device="cuda")
+    act_r = torch().empty(M * F, dtype=torch().int16, device="cuda")
+    call("bx_linear_swiglu_norm_f16", t, ptr(wg[0]), ptr(wu[0]), ptr(Hs), ptr(gd), C.c_float(1e-6), ptr(ss), ptr(act),
+         M, F, K, stream())
+    call("bx_linear_swiglu_f16", t, ptr(wg[0]), ptr(wu[0]), ptr(xn), ptr(act_r), M, F, K, stream())
+    got, ref = f16_host(act).reshape(M, F), f16_host(act_r).reshape(M, F)
+    scale = (np.abs(Xn) @ np.abs(wg[1]).T) * (np.abs(Xn) @ np.abs(wu[1]).T)
+    fin = np.isfinite(ref)   # products beyond FP16 overflow the same way in both
+    assert np.array_equal(np.isfinite(got), fin)
+    assert np.all((np.abs(got[fin] - ref[fin]) <= (2.0 ** -9 * np.abs(ref) + 2.0 ** -9 * scale + 1e-5)[fin]))
+    # refused, nothing written
+    sentinel = torch().full((M * Ns[0],), 0x1234, dtype=torch().int16, device="cuda")
+    rc = h.bx_linear_group_norm_f16(t, 1, W_arr, (C.c_void_p * 3)(ptr(sentinel), None, None), N_arr, ptr(Hs), ptr(gd),
+                                    C.c_float(1e-6), ptr(ss), 2, K, stream())
+    assert rc == -3 and np.all(host(sentinel) == 0x1234)
