@@ -288,9 +288,12 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
         const int kpp = (nk + P - 1) / P;
         const int jb = min(nk, part * kpp), nkw = min(nk, jb + kpp) - jb;   // <= 128 keys: two per lane at most
         if (nkw > 0) {
-            for (int hh = 0; hh < HPW; ++hh) {
+            // unrolled over the (at most two) heads of the wave: the running
+            // state stays in registers with fixed indices
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
                 const int h = h0 + hh;
-                if (h >= G) break;
+                if (hh >= HPW || h >= G) continue;   // uniform
                 const uint16_t* qh = qs + h * HD;
                 float sv[2];
 #pragma unroll
@@ -342,16 +345,15 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
                         for (int i = 0; i < EPL; ++i) vv[u][i] = vcol[t * HD + i];
                     }
                     asm volatile("" ::: "memory");
+                    // keys past nkw (up to the next multiple of 8, below 128)
+                    // have p = 0 and a clamped, finite value row
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
                         const int t = t0 + u;   // uniform
-                        if (t < nkw) {
-                            const float pt = __builtin_bit_cast(
-                                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]),
-                                                                 t & 63));
+                        const float pt = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]), t & 63));
 #pragma unroll
-                            for (int i = 0; i < EPL; ++i) o[hh][i] += pt * h2f(vv[u][i]);
-                        }
+                        for (int i = 0; i < EPL; ++i) o[hh][i] += pt * h2f(vv[u][i]);
                     }
                 }
             }
@@ -364,9 +366,10 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     const int rec = HD + 2;
     float* pl = reinterpret_cast<float*>(ba_lds);   // P x G records
     if (P > 1) {
-        for (int hh = 0; hh < HPW; ++hh) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
             const int h = h0 + hh;
-            if (h >= G) break;
+            if (hh >= HPW || h >= G) continue;
             float* pr = pl + (part * G + h) * rec;
 #pragma unroll
             for (int i = 0; i < EPL; ++i) pr[EPL * lane + i] = o[hh][i];
@@ -377,9 +380,10 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
         }
         __syncthreads();
         if (part == 0) {
-            for (int hh = 0; hh < HPW; ++hh) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
                 const int h = h0 + hh;
-                if (h >= G) break;
+                if (hh >= HPW || h >= G) continue;
                 float mm = -INFINITY;
                 for (int q = 0; q < P; ++q) mm = fmaxf(mm, pl[(q * G + h) * rec + HD]);
                 float ll = 0.f, oo[EPL];
@@ -402,9 +406,10 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     float* grp = a.recs + ((int64_t)r * a.n_kv + g) * (int64_t)T * G * rec;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(grp, 0, 0x7fffffff, 0x00020000);
     if (part == 0) {
-        for (int hh = 0; hh < HPW; ++hh) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
             const int h = h0 + hh;
-            if (h >= G) break;
+            if (hh >= HPW || h >= G) continue;
             const int ro = (s * G + h) * rec;   // record offset, floats
 #pragma unroll
             for (int i = 0; i < EPL; ++i)
