@@ -198,6 +198,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=18.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batched-only", type=int, default=0, metavar="M",
+                    help="time only the batched decode of M sequences (prompt context each) and print its "
+                         "throughput (for profiler runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prompt prefill only and print its throughput (for hardware-counter runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -241,6 +244,26 @@ def main() -> int:
     prompt = ba.prompt_ids(c["prompt"], cfg.vocab_size, seed=42)
     cap = max(c["cap"], c["prompt"] + args.warmup + steps + 1)
     model.allocate_cache(cap)
+
+    if args.batched_only > 0:
+        M, n_b = args.batched_only, 32
+        if not 1 <= M <= 16:
+            print("bench.py: --batched-only takes 1..16 sequences", file=sys.stderr)
+            return 2
+        model.allocate_batch(M, len(prompt) + n_b + 8)
+        for s in range(M):
+            model.prefill_slot(s, prompt)
+        ids, slots = [1] * M, list(range(M))
+        model.time_forward_batch(ids, slots, 4)
+        for s in slots:
+            model.truncate_slot(s, len(prompt))
+        ms = model.time_forward_batch(ids, slots, n_b)
+        model.close()
+        ba.shutdown()
+        print(json.dumps({"metric": f"batched decode tok/s {args.config}", "value": round(M * 1e3 / ms, 1),
+                          "unit": "tok/s", "rows": M, "context": len(prompt), "steps": n_b,
+                          "ms_per_step": round(ms, 4), "data": "synthetic"}), flush=True)
+        return 0
 
     # prefill (timed separately, reported as an extra field)
     t0 = time.perf_counter()
