@@ -120,6 +120,9 @@ HIP_SYMBOLS = {
                                            vp]),
     "bx_linear_swiglu_norm_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_float, vp, vp, C.c_int, C.c_int, C.c_int,
                                             vp]),
+    "bx_linear_group2_f16": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
+    "bx_linear_group2_norm_f16": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, C.c_float, vp,
+                                            C.c_int, C.c_int, vp]),
     "bx_batch_attention_workspace_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "bx_batch_attention_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
                                          C.c_int, vp, vp, C.c_int, vp, vp, i64, vp, vp, vp]),

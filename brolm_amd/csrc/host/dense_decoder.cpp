@@ -1175,6 +1175,29 @@ void DenseDecoder::enqueue_batch_(int M) {
                                                      cfg_.hidden_size, st),
                             "forward_batch q / k / v with the norm");
     };
+    // q and k of one weight type and v of another (Q4_K and Q6_K) in one
+    // launch, normalising h (with_norm: needs the row sums) or from bnorm_
+    auto group2 = [&](const bt::Tensor* const* w, bt::Tensor* const* y, const bt::Tensor& gain,
+                      bool with_norm = true) {
+        if (with_norm && !have_ss) return false;
+        const void* W[3];
+        uint16_t* Y[3];
+        int N[3];
+        for (int i = 0; i < 3; ++i) {
+            y[i]->resize(M, w[i]->rows, bt::Dtype::FP16);
+            W[i] = w[i]->data;
+            Y[i] = static_cast<uint16_t*>(y[i]->data);
+            N[i] = w[i]->rows;
+        }
+        const int t1 = bt::dtype_to_ggml(w[0]->dtype), t2 = bt::dtype_to_ggml(w[2]->dtype);
+        const int rc = with_norm ? bx_linear_group2_norm_f16(t1, t2, 3, 2, W, Y, N, hf,
+                                                             static_cast<const uint16_t*>(gain.data), eps, ss, M,
+                                                             cfg_.hidden_size, st)
+                                 : bx_linear_group2_f16(t1, t2, 3, 2, W, Y, N,
+                                                        static_cast<const uint16_t*>(bnorm_.data), M,
+                                                        cfg_.hidden_size, st);
+        return !unsupported(rc, "forward_batch q / k / v");
+    };
     auto residual = [&](const bt::Tensor& W, const bt::Tensor& X) {
         int rc = BX_EUNSUPPORTED;
         if (carry_norm)
@@ -1197,12 +1220,15 @@ void DenseDecoder::enqueue_batch_(int M) {
             bt::Tensor* y[3] = {&bq_, &bk_, &bv_};
             const int same = layer.Wk.dtype != layer.Wq.dtype ? 1 : layer.Wv.dtype == layer.Wq.dtype ? 3 : 2;
             int done = 0;
-            if (group_norm(w, y, same, layer.input_ln)) {
+            if (same == 2 && group2(w, y, layer.input_ln)) {
+                done = 3;
+            } else if (group_norm(w, y, same, layer.input_ln)) {
                 done = same;
                 while (done < 3 && group_norm(w + done, y + done, 1, layer.input_ln)) ++done;
             }
             if (done < 3) {
                 bt::rms_norm_forward(bh_, layer.input_ln, eps, bnorm_);
+                if (done == 0 && same == 2 && group2(w, y, layer.input_ln, false)) done = 3;
                 if (done == 0 && same > 1 && bt::linear_group_forward_batched(w, y, same, bnorm_)) done = same;
                 for (int i = done; i < 3; ++i) linear_batched(*w[i], nullptr, bnorm_, *y[i]);
             }

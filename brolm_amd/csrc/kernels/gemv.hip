@@ -29,6 +29,9 @@ int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const
                          const uint16_t* gamma, float eps, const float* ss_in, int M, int K, hipStream_t st);
 int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,
                           const float* ss_in, uint16_t* Y, int M, int F, int K, hipStream_t st);
+int gemv_mfma_group2(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
+                     const uint16_t* X, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
+                     int K, hipStream_t st);
 
 // The fused linear forms run on the MFMA tile GEMM (M >= 128, K % 64 == 0)
 // and, for decode batches, on the MFMA GEMV (3 <= M <= 16, K % 256 == 0).
@@ -293,4 +296,35 @@ extern "C" int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* 
     if (!Wg || !Wu || !H || !gamma || !ss_in || !Y) return bx::fail(BX_EINVAL, "linear_swiglu_norm: null pointer");
     if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_swiglu_norm: needs 3 <= M <= 16, K % 256 == 0");
     return bx::gemv_mfma_swiglu_norm(wtype, Wg, Wu, H, gamma, eps, ss_in, Y, M, F, K, bx::as_stream(stream));
+}
+
+// q / k / v in one launch when v's weight type differs (members [0, n1) of
+// type wtype, [n1, n) of type wtype2; Q4_K then Q6_K), from FP16 X or, with
+// H non-null, from RMSNorm(H) with the residual launch's row sums.
+static int group2_checks(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
+                         int M, int K) {
+    if (n < 2 || n > 3 || n1 < 1 || n1 >= n || !W || !Y || !N) return bx::fail(BX_EINVAL, "linear_group2: bad arguments");
+    for (int i = 0; i < n; ++i) {
+        if (int rc = bx::check_linear_shape(i < n1 ? wtype : wtype2, M, N[i], K)) return rc;
+        if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group2: null pointer");
+    }
+    if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_group2: needs 3 <= M <= 16, K % 256 == 0");
+    return BX_OK;
+}
+
+extern "C" int bx_linear_group2_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
+                                    const int* N, const uint16_t* X, int M, int K, void* stream) {
+    if (int rc = group2_checks(wtype, wtype2, n, n1, W, Y, N, M, K)) return rc;
+    if (!X) return bx::fail(BX_EINVAL, "linear_group2: null X");
+    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, X, nullptr, nullptr, 0.f, nullptr, M, K,
+                                bx::as_stream(stream));
+}
+
+extern "C" int bx_linear_group2_norm_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
+                                         const int* N, const float* H, const uint16_t* gamma, float eps,
+                                         const float* ss_in, int M, int K, void* stream) {
+    if (int rc = group2_checks(wtype, wtype2, n, n1, W, Y, N, M, K)) return rc;
+    if (!H || !gamma || !ss_in) return bx::fail(BX_EINVAL, "linear_group2_norm: null pointer");
+    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, nullptr, H, gamma, eps, ss_in, M, K,
+                                bx::as_stream(stream));
 }

@@ -30,6 +30,7 @@
 // whole tiles; narrow ones split K over the 8 wavefronts of a workgroup and
 // add the partial tiles in LDS.
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <utility>
 
@@ -327,6 +328,8 @@ struct MfmaJob {
     // residual split launches: row sums of squares of the updated residual,
     // ss_out[group * 16 + m] for the 64 columns of each tile group (or null)
     float* ss_out;
+    // two-format groups: members from mem2 on have the second weight type
+    int mem2;
 };
 
 // Tile t of the launch -> (member, row tile within the member).
@@ -576,7 +579,10 @@ __device__ __forceinline__ void group_row_ss(const MfmaJob& job, int Mr, int wav
     }
 }
 
-template <int FMT, int EPI, int CPS, bool NIN>
+// FMT2 >= 0: a group whose members from job.mem2 on have weight type FMT2
+// (q and k in FMT, v in FMT2); a wavefront's tile belongs to one member, so
+// it takes that member's load and multiply path (a wave-uniform branch).
+template <int FMT, int EPI, int CPS, bool NIN, int FMT2 = -1>
 __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const uint16_t* __restrict__ X, int Mr,
                                                             int K, int S) {
     extern __shared__ __align__(16) uint32_t smem[];
@@ -601,13 +607,21 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     member_of(job, live ? tile : job.tiles - 1, mem, lt);
     const int N = job.N[mem];
     const int64_t n = lt * 16 + r < N ? lt * 16 + r : N - 1;
+    constexpr bool kMix = FMT2 >= 0;
+    const bool second = kMix && mem >= job.mem2;
     Chunk<FMT> cw[CPS];
     Chunk<FMT> cu[kTwo ? CPS : 1];
+    Chunk<kMix ? FMT2 : FMT> c2[kMix ? CPS : 1];
+    if (!second) {
 #pragma unroll
-    for (int i = 0; i < CPS; ++i) {
-        const int b = c0 + (i < nc ? i : nc - 1);
-        cw[i].load(job.W[mem], N, K, n, b, g);
-        if constexpr (kTwo) cu[i].load(job.W[1], N, K, n, b, g);
+        for (int i = 0; i < CPS; ++i) {
+            const int b = c0 + (i < nc ? i : nc - 1);
+            cw[i].load(job.W[mem], N, K, n, b, g);
+            if constexpr (kTwo) cu[i].load(job.W[1], N, K, n, b, g);
+        }
+    } else if constexpr (kMix) {
+#pragma unroll
+        for (int i = 0; i < CPS; ++i) c2[i].load(job.W[mem], N, K, n, c0 + (i < nc ? i : nc - 1), g);
     }
     XStage xst;
     xst.xs = smem;
@@ -672,17 +686,23 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     }
     for (int i = threadIdx.x; i < xstride; i += kSplThr) smem[Mr * xstride + i] = 0u;
     __syncthreads();
-    if constexpr (FMT == FMT_Q4_K) {
+    if constexpr (FMT == FMT_Q4_K || FMT2 == FMT_Q4_K) {
         q4k_xsums(smem, xstride, xs2, Mr, Ks);
         __syncthreads();
     }
     f4v acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    if (!second) {
 #pragma unroll
-    for (int i = 0; i < CPS; ++i) {
-        if (i < nc) {
-            cw[i].mul(xst, 256 * i, r, g, acc);
-            if constexpr (kTwo) cu[i].mul(xst, 256 * i, r, g, accu);
+        for (int i = 0; i < CPS; ++i) {
+            if (i < nc) {
+                cw[i].mul(xst, 256 * i, r, g, acc);
+                if constexpr (kTwo) cu[i].mul(xst, 256 * i, r, g, accu);
+            }
         }
+    } else if constexpr (kMix) {
+#pragma unroll
+        for (int i = 0; i < CPS; ++i)
+            if (i < nc) c2[i].mul(xst, 256 * i, r, g, acc);
     }
     f4v sq;
     if (S == 1) {
@@ -783,9 +803,14 @@ constexpr int64_t kSplitTiles = 2048;
 // nin: X is the RMSNorm of job.Hn (the split form only); split_only: fail
 // with BX_EUNSUPPORTED, launching nothing, when the split form does not apply
 // (norm-input launches, and residual launches that must report row sums).
+// wtype2 >= 0: a two-format group (members from job.mem2 on), Q4_K then
+// Q6_K only, split form only.
 template <int EPI>
 int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStream_t st, bool nin = false,
-                bool split_only = false) {
+                bool split_only = false, int wtype2 = -1) {
+    if (wtype2 >= 0 && (EPI != MEPI_STORE || wtype != BX_TYPE_Q4_K || wtype2 != BX_TYPE_Q6_K))
+        return fail(BX_EUNSUPPORTED, "gemv: two-format groups are Q4_K then Q6_K");
+    if (wtype2 < 0) job.mem2 = job.members;
     int fmt;
     switch (wtype) {
         case BX_TYPE_Q4_K: fmt = FMT_Q4_K; break;
@@ -817,7 +842,21 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
         if (int rc = split_ready(st)) return rc;
         const size_t lds = (size_t)(M + 1) * (128 * cps + 4) * 4 + (fmt == FMT_Q4_K ? (size_t)8 * cps * 16 * 4 : 0);
         const dim3 grid((unsigned)groups, (unsigned)S);
-        if (nin) {
+        if (wtype2 >= 0) {
+            if constexpr (EPI == MEPI_STORE) {
+                auto go = [&](auto nin_c) {
+                    constexpr bool kN = decltype(nin_c)::value;
+                    if (cps == 1)
+                        gemv_split_kernel<FMT_Q4_K, EPI, 1, kN, FMT_Q6_K><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                    else if (cps == 2)
+                        gemv_split_kernel<FMT_Q4_K, EPI, 2, kN, FMT_Q6_K><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                    else
+                        gemv_split_kernel<FMT_Q4_K, EPI, 3, kN, FMT_Q6_K><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
+                };
+                if (nin) go(std::true_type{});
+                else go(std::false_type{});
+            }
+        } else if (nin) {
             if constexpr (EPI != MEPI_RESID) {
                 BX_DISPATCH_FMT(wtype, {
                     if (cps == 1) gemv_split_kernel<FMT_, EPI, 1, true><<<grid, kSplThr, lds, st>>>(job, X, M, K, S);
@@ -834,7 +873,8 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
         }
         return launch_check("gemv split");
     }
-    if (split_only || nin) return fail(BX_EUNSUPPORTED, "gemv: the fused-norm forms need the split launch");
+    if (split_only || nin || wtype2 >= 0)
+        return fail(BX_EUNSUPPORTED, "gemv: the fused-norm and two-format forms need the split launch");
     for (int m0 = 0; m0 < M; m0 += mc) {
         const int mr = M - m0 < mc ? M - m0 : mc;
         const size_t lds = mfma_lds_bytes(fmt, mr, K, two);
@@ -927,6 +967,28 @@ int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const
     job.ss_in = ss_in;
     job.ss_groups = (K + 63) / 64;
     return mfma_launch<MEPI_STORE>(wtype, job, nullptr, M, K, st, true);
+}
+
+int gemv_mfma_group2(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
+                     const uint16_t* X, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
+                     int K, hipStream_t st) {
+    MfmaJob job{};
+    for (int i = 0; i < n; ++i) {
+        job.W[i] = W[i];
+        job.Y[i] = Y[i];
+        job.N[i] = N[i];
+    }
+    job.members = n;
+    job.mem2 = n1;
+    const bool nin = H != nullptr;
+    if (nin) {
+        job.Hn = H;
+        job.gamma = gamma;
+        job.eps = eps;
+        job.ss_in = ss_in;
+        job.ss_groups = (K + 63) / 64;
+    }
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st, nin, true, wtype2);
 }
 
 int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,

@@ -114,6 +114,18 @@ int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, uint16_t* c
                              const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* stream);
 int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma,
                               float eps, const float* ss_in, uint16_t* Y, int M, int F, int K, void* stream);
+/* The q / k / v projections in one decode-batch launch when v's weight type
+ * differs from q / k's (the per-weight dispatch of compute.h:54-86 over
+ * llama.cpp's Q4_K_M mix): members [0, n1) of type wtype, [n1, n) of type
+ * wtype2, Q4_K then Q6_K only; each member's output has exactly the bits of
+ * its own launch.  The _norm form takes X = RMSNorm(H) with the row sums of
+ * bx_linear_residual_ss_f16, as bx_linear_group_norm_f16.  BX_EUNSUPPORTED,
+ * nothing launched, for other types or shapes outside the split GEMV. */
+int bx_linear_group2_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
+                         const uint16_t* X, int M, int K, void* stream);
+int bx_linear_group2_norm_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
+                              const int* N, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
+                              int K, void* stream);
 
 /* ------------------------------------------------------------- elementwise */
 

@@ -561,3 +561,52 @@ def test_linear_norm_carried_between_launches(t, M):
     rc = h.bx_linear_group_norm_f16(t, 1, W_arr, (C.c_void_p * 3)(ptr(sentinel), None, None), N_arr, ptr(Hs), ptr(gd),
                                     C.c_float(1e-6), ptr(ss), 2, K, stream())
     assert rc == -3 and np.all(host(sentinel) == 0x1234)
+
+
+@pytest.mark.parametrize("M", [3, 4, 9, 16])
+def test_linear_group_two_formats_equals_own_launches(M):
+    """bx_linear_group2_f16 / _norm_f16: q and k (Q4_K) with v (Q6_K) in one
+    launch give each member exactly the bits of its own group launch (the K
+    split depends on K alone), from FP16 X and from RMSNorm(H) with carried
+    row sums; other type pairs are refused with nothing launched."""
+    print(f"[linear group2] M={M}", flush=True)
+    rng = np.random.default_rng(4400 + M)
+    K, Ns = 2048, (512, 256, 256)
+    ws = [_weights(rng, 12, Ns[0], K)[0], _weights(rng, 12, Ns[1], K)[0], _weights(rng, 14, Ns[2], K)[0]]
+    X = _f16(rng.standard_normal((M, K)))
+    x = f16_dev(X)
+    W_arr = (C.c_void_p * 3)(*[ptr(w) for w in ws])
+    N_arr = (C.c_int * 3)(*Ns)
+
+    def outs():
+        return [torch().empty(M * n, dtype=torch().int16, device="cuda") for n in Ns]
+
+    def arr(ys):
+        return (C.c_void_p * 3)(*[ptr(y) for y in ys])
+
+    ya, yb = outs(), outs()
+    call("bx_linear_group2_f16", 12, 14, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, stream())
+    call("bx_linear_group_f16", 12, 2, W_arr, arr(yb), N_arr, ptr(x), M, K, stream())
+    call("bx_linear_group_f16", 14, 1, (C.c_void_p * 3)(ptr(ws[2]), None, None), (C.c_void_p * 3)(ptr(yb[2]), None, None),
+         (C.c_int * 3)(Ns[2], 0, 0), ptr(x), M, K, stream())
+    for a, b in zip(ya, yb):
+        assert np.array_equal(host(a), host(b))
+    # from RMSNorm(H), the row sums from a residual launch
+    Wo, _ = _weights(rng, 12, K, 512)
+    H = dev((rng.standard_normal((M, K)) * 2).astype(np.float32))
+    h = hip()
+    ss = torch().zeros(h.bx_linear_ss_floats(K), dtype=torch().float32, device="cuda")
+    call("bx_linear_residual_ss_f16", 12, ptr(Wo), ptr(f16_dev(rng.standard_normal((M, 512)))), ptr(H), ptr(ss), M, K,
+         512, stream())
+    gd = f16_dev(rng.uniform(0.5, 1.5, K))
+    ya, yb = outs(), outs()
+    call("bx_linear_group2_norm_f16", 12, 14, 3, 2, W_arr, arr(ya), N_arr, ptr(H), ptr(gd), C.c_float(1e-6), ptr(ss),
+         M, K, stream())
+    call("bx_linear_group_norm_f16", 12, 2, W_arr, arr(yb), N_arr, ptr(H), ptr(gd), C.c_float(1e-6), ptr(ss), M, K,
+         stream())
+    call("bx_linear_group_norm_f16", 14, 1, (C.c_void_p * 3)(ptr(ws[2]), None, None),
+         (C.c_void_p * 3)(ptr(yb[2]), None, None), (C.c_int * 3)(Ns[2], 0, 0), ptr(H), ptr(gd), C.c_float(1e-6),
+         ptr(ss), M, K, stream())
+    for a, b in zip(ya, yb):
+        assert np.array_equal(host(a), host(b))
+    assert h.bx_linear_group2_f16(14, 12, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, stream()) == -3
