@@ -1139,16 +1139,13 @@ void DenseDecoder::enqueue_batch_(int M) {
     auto* arena = static_cast<std::uint16_t*>(batch_kv_.data);
     const auto* cs = static_cast<const float*>(batch_cos_.data);
     const auto* sn = static_cast<const float*>(batch_sin_.data);
-    // From 8 rows on, the residual RMSNorms ride on the GEMV launches: a
-    // residual launch also writes each row's sum of squares of the updated h
-    // (per 64 columns, into bss_), and the next q / k / v or gate / up launch
-    // normalises h itself while staging it.  (Measured against the separate
-    // norm launches: +3.3 % tok/s at 8 rows, +2.8 % at 12, +3.1 % at 16, but
-    // -2.2 % at 4 rows, where the plain path keeps a per-row kernel for the
-    // Q6_K v projection.)  A launch outside those forms returns
-    // BX_EUNSUPPORTED without running; then the norm runs on its own and the
-    // plain forms take its FP16 output.
-    const bool carry_norm = M >= 8;
+    // The residual RMSNorms ride on the GEMV launches: a residual launch also
+    // writes each row's sum of squares of the updated h (per 64 columns, into
+    // bss_), and the next q / k / v or gate / up launch normalises h itself
+    // while staging it.  A launch outside those forms (fewer than 3 rows, or
+    // shapes the split GEMV does not take) returns BX_EUNSUPPORTED without
+    // running; then the norm runs on its own and the plain forms take its
+    // FP16 output.
     float* ss = static_cast<float*>(bss_.data);
     const float* hf = static_cast<const float*>(bh_.data);
     bool have_ss = false;   // ss holds the row sums of the current h
@@ -1199,10 +1196,9 @@ void DenseDecoder::enqueue_batch_(int M) {
         return !unsupported(rc, "forward_batch q / k / v");
     };
     auto residual = [&](const bt::Tensor& W, const bt::Tensor& X) {
-        int rc = BX_EUNSUPPORTED;
-        if (carry_norm)
-            rc = bx_linear_residual_ss_f16(bt::dtype_to_ggml(W.dtype), W.data, static_cast<const uint16_t*>(X.data),
-                                           static_cast<float*>(bh_.data), ss, M, W.rows, W.cols, st);
+        const int rc = bx_linear_residual_ss_f16(bt::dtype_to_ggml(W.dtype), W.data,
+                                                 static_cast<const uint16_t*>(X.data), static_cast<float*>(bh_.data),
+                                                 ss, M, W.rows, W.cols, st);
         have_ss = rc == BX_OK;
         if (have_ss || !unsupported(rc, "forward_batch residual projection")) return;
         if (!bt::linear_residual_forward_batched(W, X, bh_)) {
