@@ -493,7 +493,8 @@ __global__ __launch_bounds__(kThr) void gemv_mfma_kernel(MfmaJob job, const uint
 constexpr int kSplThr = 256;
 constexpr int kSplWav = kSplThr / 64;
 constexpr int kSplMaxCps = 3;                    // chunks per slice
-constexpr int64_t kSplFloats = 8ll << 20;        // partials: 32 MB
+constexpr int kSplMaxSlices = 64;                // K up to 49152
+constexpr int64_t kSplFloats = 16ll << 20;       // partials: 64 MB
 constexpr int kSplGroups = 4096;                 // tile groups of one launch
 
 }  // namespace
@@ -740,17 +741,17 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     if (live && lane < pl) {
         // all S partials requested before any is added; added in slice order
         f4v a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-        for (int q0 = 0; q0 < S; q0 += 4) {
-            u4v va[4], vu[4];
+        for (int q0 = 0; q0 < S; q0 += 8) {
+            u4v va[8], vu[kTwo ? 8 : 1];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 8; ++i) {
                 const int q = q0 + i < S ? q0 + i : S - 1;
                 const int o = (int)((tbase + q * pstride) * 4) + lane * 16;
                 va[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kSc1);
                 if constexpr (kTwo) vu[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o + pl * 16, 0, kSc1);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 8; ++i) {
                 if (q0 + i < S) {
                     a += __builtin_bit_cast(f4v, va[i]);
                     if constexpr (kTwo) u += __builtin_bit_cast(f4v, vu[i]);
@@ -765,12 +766,14 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     if (threadIdx.x == 0) __hip_atomic_store(&split_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Slices of K for the split launch: at most 16, of at most kSplMaxCps chunks
-// each (cps returned); 0 when K needs more.
+// Slices of K for the split launch: up to 16 slices of as few chunks as that
+// allows, then slices of kSplMaxCps chunks, at most kSplMaxSlices (cps
+// returned); 0 when K needs more.  A function of K alone.
 int split_plan(int K, int& cps) {
     const int nch = K / 256;
-    cps = (nch + 15) / 16;
-    return cps <= kSplMaxCps ? (nch + cps - 1) / cps : 0;
+    cps = min(kSplMaxCps, (nch + 15) / 16);
+    const int S = (nch + cps - 1) / cps;
+    return S <= kSplMaxSlices ? S : 0;
 }
 
 // The split counters start at zero: cleared once per GPU before its first

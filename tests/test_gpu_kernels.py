@@ -207,11 +207,12 @@ def test_linear_ffn_width_k(t):
 
 
 @pytest.mark.parametrize("t", QTYPES + [1])
-@pytest.mark.parametrize("N,K", [(1000, 6144), (4100, 2048), (77, 12288), (40, 768)])
+@pytest.mark.parametrize("N,K", [(1000, 6144), (4100, 2048), (77, 12288), (40, 768), (96, 14336), (40, 32768)])
 def test_linear_split_k_repeats_bitwise(t, N, K):
     """Batched GEMV of decoder-layer size: K split over workgroups, partial
     tiles added by the last workgroup of each tile group.  Row tiles not a
-    multiple of the group, slices of one to three chunks (K 768 .. 12288),
+    multiple of the group, slices of one to three chunks (K 768 .. 32768, up to
+    43 slices),
     bias; three launches in a row give the same bits (the per-group counters
     are back at zero after every launch) and match the oracle."""
     rng = np.random.default_rng(5150 + N + t)
@@ -224,7 +225,7 @@ def test_linear_split_k_repeats_bitwise(t, N, K):
     bias = _f16(rng.standard_normal(N))
     for M in (3, 8, 13, 16):
         print(f"[linear split] type={t} N={N} K={K} M={M}", flush=True)
-        X = _f16(rng.standard_normal((M, K)) * (0.25 if K > 4096 else 1.0))
+        X = _f16(rng.standard_normal((M, K)) * (0.05 if K > 12288 else 0.25 if K > 4096 else 1.0))
         outs = [_run_linear(t, car, X, N, K, bias) for _ in range(3)]
         assert all(np.array_equal(o, outs[0]) for o in outs[1:]), M
         ref = oracle.linear(Wv, X) + bias
