@@ -18,6 +18,8 @@ int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
              hipStream_t st);
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
               hipStream_t st);
+int gemv_mfma_split(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                    hipStream_t st);
 int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
                     int M, int K, hipStream_t st);
 int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st);
@@ -223,8 +225,13 @@ extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, con
     if (!W || !X || !Y) return bx::fail(BX_EINVAL, "linear: null pointer");
     hipStream_t st = bx::as_stream(stream);
     // K beyond 12288 (an FFN width such as 32768) at 2..16 rows: the per-row
-    // kernels' staged activations outgrow LDS, the tiled GEMM does not
+    // kernels' staged activations outgrow LDS; the split MFMA GEMV stages only
+    // a K slice (3..16 rows, shapes it takes), else the tiled GEMM
     if (M == 1 || (M <= 16 && K <= 12288)) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
+    if (bx::fused_gemv_ok(M, K)) {
+        const int rc = bx::gemv_mfma_split(wtype, W, bias, X, Y, M, N, K, st);
+        if (rc != BX_EUNSUPPORTED) return rc;
+    }
     return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
 }
 

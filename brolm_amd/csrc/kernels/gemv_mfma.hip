@@ -923,6 +923,19 @@ int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X,
     return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st);
 }
 
+// The split launch only (BX_EUNSUPPORTED, nothing launched, when it does not
+// take the shape): rows beyond the whole-K kernel's LDS staging.
+int gemv_mfma_split(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
+                    hipStream_t st) {
+    MfmaJob job{};
+    job.W[0] = W;
+    job.Y[0] = Y;
+    job.N[0] = N;
+    job.bias = bias;
+    job.members = 1;
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st, false, true);
+}
+
 int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
                     int M, int K, hipStream_t st) {
     MfmaJob job{};
