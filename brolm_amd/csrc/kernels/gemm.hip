@@ -491,14 +491,25 @@ int gemm_tiles(const TileJob& job, const uint16_t* bias, const uint16_t* X, int 
     // dequantization overlaps the other's MFMAs) when they still give every
     // CU a block, else 128x128; SwiGLU tiles always take 256 rows x 64 gate
     // and 64 up columns
-    int64_t cols = 0;
-    for (int i = 0; i < job.members; ++i) cols += (job.N[i] + 127) / 128;
+    // ... and 64x64 tiles (four wavefronts of one 32x32 fragment) where
+    // 128x128 would leave CUs without a block.  Every tile shape runs the same
+    // 32x32x16 MFMA over the same K order, so an output element gets the same
+    // bits whichever tile computes it.
+    int64_t cols = 0, cols64 = 0;
+    for (int i = 0; i < job.members; ++i) {
+        cols += (job.N[i] + 127) / 128;
+        cols64 += (job.N[i] + (EPI == EPI_SWIGLU ? 31 : 63)) / (EPI == EPI_SWIGLU ? 32 : 64);
+    }
     const int64_t big = (int64_t)((M + 255) / 256) * cols;
+    const int64_t mid = (int64_t)((M + 127) / 128) * cols;
     if constexpr (EPI == EPI_SWIGLU) {
-        return launch_tiles<FMT, 256, 128, 8, EPI>(job, bias, X, M, K, st);
+        if (big >= num_cus() || (int64_t)((M + 63) / 64) * cols64 <= big)
+            return launch_tiles<FMT, 256, 128, 8, EPI>(job, bias, X, M, K, st);
+        return launch_tiles<FMT, 64, 64, 4, EPI>(job, bias, X, M, K, st);
     } else {
         if (big >= num_cus()) return launch_tiles<FMT, 256, 128, 8, EPI>(job, bias, X, M, K, st);
-        return launch_tiles<FMT, 128, 128, 4, EPI>(job, bias, X, M, K, st);
+        if (mid >= num_cus()) return launch_tiles<FMT, 128, 128, 4, EPI>(job, bias, X, M, K, st);
+        return launch_tiles<FMT, 64, 64, 4, EPI>(job, bias, X, M, K, st);
     }
 }
 
