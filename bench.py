@@ -189,6 +189,17 @@ def text_path(ba, path: Path, model, prompt: list[int]) -> dict:
     return tokenizer
 
 
+def sampled_rate(ba, model, prompt, device: bool) -> float:
+    """tok/s of generate() with T 0.8 / top-k 40 / top-p 0.95, 64 tokens from a
+    16-token prompt (one untimed run first), the draw on the device or on the host."""
+    sp = ba.SamplingParams(temperature=0.8, top_k=40, top_p=0.95, seed=1)
+    opts = ba.GenerateOptions(max_new_tokens=64, sampling=sp, stop_on_eos=False, device_sampling=device)
+    ba.generate(model, prompt[:16], -1, opts)
+    t0 = time.perf_counter()
+    n = len(ba.generate(model, prompt[:16], -1, opts))
+    return round(n / (time.perf_counter() - t0), 2)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,6 +212,9 @@ def main() -> int:
     ap.add_argument("--batched-only", type=int, default=0, metavar="M",
                     help="time only the batched decode of M sequences (prompt context each) and print its "
                          "throughput (for profiler runs)")
+    ap.add_argument("--sampled-only", action="store_true",
+                    help="time only sampled generation with the device sampler and print its throughput "
+                         "(for profiler runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prompt prefill only and print its throughput (for hardware-counter runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -244,6 +258,15 @@ def main() -> int:
     prompt = ba.prompt_ids(c["prompt"], cfg.vocab_size, seed=42)
     cap = max(c["cap"], c["prompt"] + args.warmup + steps + 1)
     model.allocate_cache(cap)
+
+    if args.sampled_only:
+        rate = sampled_rate(ba, model, prompt, True)
+        model.close()
+        ba.shutdown()
+        print(json.dumps({"metric": f"sampled generate tok/s {args.config}", "value": rate, "unit": "tok/s",
+                          "sampling": "T 0.8, top-k 40, top-p 0.95, device sampler", "new_tokens": 64,
+                          "data": "synthetic"}), flush=True)
+        return 0
 
     if args.batched_only > 0:
         M, n_b = args.batched_only, 32
@@ -319,14 +342,7 @@ def main() -> int:
 
     # sampled generation (temperature 0.8, top-k 40, top-p 0.95): the draw on
     # the device (default) against the host sampler (logits download + sort)
-    sampled = {}
-    for dev in (True, False):
-        sp = ba.SamplingParams(temperature=0.8, top_k=40, top_p=0.95, seed=1)
-        opts = ba.GenerateOptions(max_new_tokens=64, sampling=sp, stop_on_eos=False, device_sampling=dev)
-        ba.generate(model, prompt[:16], -1, opts)
-        t0 = time.perf_counter()
-        n = len(ba.generate(model, prompt[:16], -1, opts))
-        sampled["device" if dev else "host"] = round(n / (time.perf_counter() - t0), 2)
+    sampled = {("device" if dev else "host"): sampled_rate(ba, model, prompt, dev) for dev in (True, False)}
 
     # text path: the checkpoint's own tokenizer (host), and generate_text
     # (encode -> greedy generate -> decode) end to end; Qwen3 only (Mistral's

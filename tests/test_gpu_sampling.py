@@ -75,6 +75,37 @@ def test_device_sampler_matches_oracle(env, V):
     assert near <= 2
 
 
+def test_device_sampler_ties_at_the_cut(env):
+    """Logits from 40 FP16 values over 151936 ids, so every top-k / top-p cut
+    and most draws fall inside groups of equal probability.  The oracle orders
+    equal probabilities by ascending id, as the device does, so the id must be
+    the oracle's exactly (draws within 1e-5 of an interval boundary aside).
+    k = 6000 leaves more candidates above the histogram floor than the gathered
+    path takes, so the draw over all ids runs there."""
+    torch, nat = env
+    lib = nat.lib()
+    V = 151936
+    rng = np.random.default_rng(11)
+    levels = _distinct_fp16(rng, 40, -4.0, 6.0)
+    lg16 = levels[rng.integers(0, levels.size, V)]
+    lg32 = lg16.astype(np.float32)
+    dev = torch.from_numpy(lg16.view(np.uint16).astype(np.int16)).cuda()
+    near = total = 0
+    for T, k, p in [(1.0, 40, 1.0), (0.8, 100, 0.9), (1.0, 0, 0.3), (1.0, 6000, 1.0), (1.5, 6000, 0.5),
+                    (0.6, 2500, 0.95)]:
+        for seed in range(5):
+            print(f"[sample] ties T={T} k={k} p={p} seed={seed}", flush=True)
+            want, margin = oracle.sample_token(lg32, T, k, p, first_uniform(seed))
+            got = lib.brolm_sample_token_device(C.c_void_p(dev.data_ptr()), V, T, k, p, seed)
+            assert got >= 0, nat.lib().brolm_last_error()
+            total += 1
+            if got != want:
+                assert margin < 1e-5, (T, k, p, seed, want, got, margin)
+                near += 1
+    print(f"[sample] ties: {total} draws, {near} within 1e-5 of an interval boundary", flush=True)
+    assert near <= 2
+
+
 def test_sampled_generation_on_device_matches_host(env, small_gguf):
     """generate() with temperature sampling: the device sampler (default) and
     the host path draw, from the same seed, ids of equal probability (this
