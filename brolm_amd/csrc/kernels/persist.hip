@@ -1063,8 +1063,15 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     // A blocks are requested during E of the layer before (the first layer's
     // here), so that they have landed before A's residual poll: loads complete
     // in issue order, and a poll issued behind fresh weight loads waits for them.
+    // A workgroup loads the rows of one segment only, so when q / k and v share
+    // a format one block serves all three: two blocks live across the layer
+    // loop would not fit the registers of the widest shapes.
     RowBlock<FQ, UH, RA> wa_qk;
-    RowBlock<FV, UH, RA> wa_v;
+    std::conditional_t<FQ == FV, char, RowBlock<FV, UH, RA>> wa_v_own;
+    RowBlock<FV, UH, RA>& wa_v = [&]() -> RowBlock<FV, UH, RA>& {
+        if constexpr (FQ == FV) return wa_qk;
+        else return wa_v_own;
+    }();
     auto issue_a = [&](const bx_decode_layer& L, int z) {
         if (a0 < ae) {
             if (seg == 2) wa_v.load(L.Wv, kvd, H, a0 + z);
@@ -1326,11 +1333,12 @@ struct PEntry {
     int ra, rc, rd, re;
 };
 
-// Instantiated shapes: the BASELINE format mixes at their widths and the small
-// test models of the same mixes.  RA..RH: rows per wave task of stages A, C, D
-// (per matrix), E and the head.  Rows per workgroup come in whole triples of
-// the hand-off words, so RC / RE cover ceil(words3(H) / CUs) triples in one
-// round of the four waves.
+// Instantiated shapes: the common quantization mixes at their widths and the
+// small test models of the same mixes.  RA..RH: rows per wave task of stages
+// A, C, D (per matrix), E and the head.  Rows per workgroup come in whole
+// triples of the hand-off words; RC / RE cover ceil(words3(H) / CUs) triples in
+// one round of the four waves where the blocks fit the registers, and in
+// several rounds of smaller tasks where they do not.
 const PEntry kPersistTable[] = {
     // Q4_K with Q6_K v/down/output (1.7B: H 2048, F 6144; test: H 256, F 768)
     BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 1, 1, 3, 5, 3, 6, 3, 8, 128),
@@ -1338,8 +1346,11 @@ const PEntry kPersistTable[] = {
     // all Q8_0, tied FP16 lm_head (0.6B: H 1024, F 3072, qd 2048; test: H 512, F 1024, qd 512)
     BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 2, 4, 2, 6, 2, 4, 128),
     BX_PK(FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_Q8_0, FMT_F16, 1, 1, 1, 4, 2, 6, 2, 4, 64),
-    // Q4_K everywhere with Q6_K output (8B: H 4096, F 12288)
-    BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 6, 5, 4, 5, 4, 128),
+    // Q4_K everywhere with Q6_K output (8B: H 4096, F 12288); A and E in tasks
+    // of 2 rows: larger blocks held across the stage boundaries spill registers
+    // to scratch at these widths (measured 250 tok/s at RA 6 / RE 5 against
+    // 389 tok/s here)
+    BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 2, 5, 4, 2, 4, 128),
 };
 
 struct PLayout {
