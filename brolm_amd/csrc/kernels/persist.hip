@@ -432,6 +432,33 @@ __device__ __forceinline__ void peeled_tasks(int first, int end, int stride, Loa
     }
 }
 
+// The same tasks with two blocks in turn: b0 holds the first task (loaded by
+// the caller), and every task but the last requests the next task's block into
+// the other one before its own math, so a wave with several tasks waits for
+// memory once.  Each path issues its loads unconditionally, so the compiler's
+// wait before a task's math covers that task's loads and not the ones requested
+// after them; a single task takes the path with no loads, as peeled_tasks.
+template <class Blk, class Load, class Comp>
+__device__ __forceinline__ void piped_tasks(Blk& b0, Blk& b1, int first, int end, int stride, Load&& load,
+                                            Comp&& comp) {
+    for (int t = first; t < end;) {
+        if (t + stride >= end) {
+            comp(b0, t);
+            break;
+        }
+        load(b1, t + stride);
+        comp(b0, t);
+        t += stride;
+        if (t + stride >= end) {
+            comp(b1, t);
+            break;
+        }
+        load(b0, t + stride);
+        comp(b1, t);
+        t += stride;
+    }
+}
+
 // Rows [r0, r1) of W (N x K): wave w takes tasks of R rows starting at
 // r0 + w R with stride kPW R.  prefetch() loads the first task before the
 // caller waits for the activation; finish() computes every task (later tasks
