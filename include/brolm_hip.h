@@ -234,8 +234,10 @@ int bx_add_inplace(void* h, int h_is_f32, const uint16_t* x, int64_t n, void* st
  * descending probability, and the token where the running kept mass first
  * exceeds u * kept (u: the host's uniform_real_distribution<double>(0, 1)
  * draw).  One FP16 logits row (device); *out (device int32).  Equal
- * probabilities resolve to the lowest index.  workspace:
- * bx_sample_workspace_bytes(vocab). */
+ * probabilities resolve to the lowest index.  workspace (device, 256-byte
+ * aligned, about 12 bytes per id): bx_sample_workspace_bytes(vocab); vocab up
+ * to 4,194,304.  Four stream-ordered launches; calls that share a workspace
+ * must be ordered on one stream. */
 size_t bx_sample_workspace_bytes(int vocab);
 /* bx_sample_f16 inside a device-side decode loop (no reference counterpart:
  * the reference samples on the host, generate.cpp:68-142): the draw is
