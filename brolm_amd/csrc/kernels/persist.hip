@@ -1378,6 +1378,10 @@ const PEntry kPersistTable[] = {
     // to scratch at these widths (measured 250 tok/s at RA 6 / RE 5 against
     // 389 tok/s here)
     BX_PK(FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, 2, 2, 6, 2, 5, 4, 2, 4, 128),
+    // Q4_K with Q6_K v/down/output at Llama-3-8B widths (H 4096, F 14336, no
+    // QK-norm): 1-row A and E tasks keep the Q6_K E blocks (7 units a lane) and
+    // the two A blocks in registers (397 tok/s against 368 for the graph step)
+    BX_PK(FMT_Q4_K, FMT_Q6_K, FMT_Q4_K, FMT_Q4_K, FMT_Q6_K, FMT_Q6_K, 2, 2, 7, 1, 3, 3, 1, 4, 128),
 };
 
 struct PLayout {

@@ -22,6 +22,37 @@ def ba():
     return brolm_amd
 
 
+@pytest.mark.timeout(600)
+def test_llama3_8b_widths_persistent_vs_oracle(ba, tmp_path_factory):
+    """Two layers at Llama-3-8B widths (H 4096, F 14336, 32 / 8 heads of 128,
+    no QK-norm, vocab 128256; Q4_K with Q6_K v / down / output): the persistent
+    step's instantiation for these widths, a 256-token prefill and 8 greedy
+    steps against the oracle."""
+    from conftest import write_synth
+    spec = dict(vocab=128256, hidden=4096, intermediate=14336, layers=2, n_q=32, n_kv=8, head_dim=128,
+                tied=False, eps=1e-5, theta=5e5, context=8192, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K",
+                o="Q4_K", gate="Q4_K", up="Q4_K", down="Q6_K", output="Q6_K", seed=31)
+    path = write_synth(tmp_path_factory.mktemp("wl8"), spec, "wl8", arch="mistral3")
+    print("[mistral3] Llama-3-8B-width checkpoint written", flush=True)
+    m = _load(ba, path, cap=1024)
+    assert m.decode_mode() == "persistent"
+    om = oracle.Model(str(path))
+    om.allocate_cache(1024)
+    prompt = ba.prompt_ids(256, spec["vocab"], seed=42)
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    print(f"[mistral3] Llama-3-8B widths prefill max diff {np.abs(a - b).max():.3e}", flush=True)
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    for step in range(8):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        print(f"[mistral3] Llama-3-8B widths step {step} max diff {np.abs(a - b).max():.3e}", flush=True)
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
+    m.close()
+
+
 def _load(ba, path, cap=128, env=None):
     m = ba.Mistral3TextModel(ba.Mistral3Config.from_gguf(str(path)).text)
     m.load_weights(str(path))
