@@ -25,6 +25,12 @@
 #include "gemv_core.h"
 
 namespace bx {
+
+// One-row GEMV with K split over a workgroup's wavefronts (gemv.hip), here
+// adding into the FP32 residual h.
+int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, float* h, int N,
+                   int K, hipStream_t st);
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -512,6 +518,8 @@ int launch_qkv(int ta, int tb, int upl, unsigned blocks, size_t lds, hipStream_t
 }
 int launch_resid(int type, int upl, unsigned blocks, size_t lds, hipStream_t st, const uint16_t* x, int K,
                  const void* W, int N, float* h) {
+    // FFN widths of 24576 / 32768: K split over each workgroup's wavefronts
+    if (K % 8192 == 0 && K > 16384) return gemv_m1_ksplit(type, W, x, nullptr, nullptr, h, N, K, st);
     BX_DISPATCH_FMT(type, BX_DISPATCH_UPL_WIDE(upl, {
         const void* fn = reinterpret_cast<const void*>(&gemv_resid_kernel<FMT_, UPL_>);
         if (lds > 65536) {   // the down projection of FFN widths above 26112

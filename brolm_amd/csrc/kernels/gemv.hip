@@ -4,6 +4,8 @@
 // 3 <= M <= 16 with K % 256 == 0: the matrix-core GEMV (gemv_mfma.hip), except
 // M = 2 and 4 (see gemv_f16) and other K, which take the per-row GEMV kernel.
 // M > 16: the prefill GEMM (gemm.hip).
+#include <type_traits>
+
 #include "gemv_core.h"
 
 namespace bx {
@@ -18,6 +20,10 @@ int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
              hipStream_t st);
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
               hipStream_t st);
+// One-row GEMV with K split over a workgroup's wavefronts (K 24576 or 32768):
+// FP16 out (+ bias), or with h non-null added into the FP32 residual h.
+int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, float* h, int N,
+                   int K, hipStream_t st);
 int gemv_mfma_split(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
                     hipStream_t st);
 int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
@@ -118,10 +124,76 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
     }
 }
 
+// M = 1 at K of 24576 or 32768 (U = K / 32 a multiple of 256): the four
+// wavefronts of a workgroup split K in quarters, so a lane owns UPW = U / 256
+// units of each row (a Q6_K row at K 32768: 4 units, where one wavefront per
+// row holds 16 and streams them in four dependent batches).  Each wavefront
+// keeps its quarter of the activation in registers for all its rows, requests
+// the next row's units before the current row's math (two blocks in turn; the
+// request past a chunk's last row repeats that row, so every path issues the
+// same loads and the waits stay exact), and parks its quarter sums in LDS; the
+// workgroup then adds the four quarters of each row in quarter order and
+// stores FP16 (+ bias), or with RESID adds the sum into the FP32 residual h.
+constexpr int kKsMaxRows = 64;   // rows of one workgroup chunk (LDS quarter sums)
+
+template <int FMT, int UPW, bool RESID>
+__global__ __launch_bounds__(kThreads) void gemv_m1_ksplit_kernel(const void* __restrict__ W,
+                                                                 const uint16_t* __restrict__ X,
+                                                                 const uint16_t* __restrict__ bias,
+                                                                 uint16_t* __restrict__ Y, float* __restrict__ h,
+                                                                 int N, int K, int rows) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    uint32_t* xs = smem;
+    float* xsum = reinterpret_cast<float*>(smem + K / 2);
+    float* part = xsum + K / 8;
+    stage_x_f16<true, false>(X, K, 1, K, xs, K / 2, xsum, K / 16);
+    __syncthreads();
+    sums8_from_lds(xs, K, xsum);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ub = wave * 64 * UPW + lane;   // this lane's first unit
+    XU xu[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) xu[i] = load_xu<FMT>(xs, xsum, ub + 64 * i);
+    using Raw = typename RawOf<FMT>::T;
+    auto load = [&](Raw(&b)[UPW], int64_t row) {
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) b[i] = load_unit<FMT>(W, N, K, row, ub + 64 * i);
+    };
+    auto dot = [&](const Raw(&b)[UPW]) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) a += dot_reg(b[i], ub + 64 * i, xu[i]);
+        return wave_allsum(a);
+    };
+    for (int64_t c0 = (int64_t)blockIdx.x * rows; c0 < N; c0 += (int64_t)gridDim.x * rows) {
+        const int nr = (int)(N - c0 < rows ? N - c0 : rows);
+        Raw b0[UPW], b1[UPW];
+        load(b0, c0);
+        for (int j = 0; j < nr; j += 2) {
+            load(b1, c0 + min(j + 1, nr - 1));
+            const float s0 = dot(b0);
+            if (lane == 0) part[4 * j + wave] = s0;
+            if (j + 1 >= nr) break;
+            load(b0, c0 + min(j + 2, nr - 1));
+            const float s1 = dot(b1);
+            if (lane == 0) part[4 * (j + 1) + wave] = s1;
+        }
+        __syncthreads();
+        for (int r = threadIdx.x; r < nr; r += kThreads) {
+            const float v = ((part[4 * r] + part[4 * r + 1]) + part[4 * r + 2]) + part[4 * r + 3];
+            if constexpr (RESID) h[c0 + r] += v;
+            else Y[c0 + r] = f2h(v + (bias ? h2f(bias[c0 + r]) : 0.f));
+        }
+        __syncthreads();
+    }
+}
+
 int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int N, int K,
                    hipStream_t st) {
     const int upl = upl_for(K);
     if (upl > 16) return fail(BX_EUNSUPPORTED, "gemv: K above 32768 at M = 1");
+    if (K % 8192 == 0 && K > 16384) return gemv_m1_ksplit(wtype, W, X, bias, Y, nullptr, N, K, st);
     const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
@@ -196,6 +268,39 @@ int check_linear_shape(int wtype, int M, int N, int K) {
     if (K % 32 != 0 || K % be != 0)
         return fail(BX_EINVAL, "linear: K=" + std::to_string(K) + " must be a multiple of 32 and of the block size");
     return BX_OK;
+}
+
+int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, float* h, int N,
+                   int K, hipStream_t st) {
+    if (K % 8192 != 0 || K <= 16384 || K > 32768) return fail(BX_EUNSUPPORTED, "gemv ksplit: K must be 24576 or 32768");
+    // one chunk of rows per CU where N allows, at most kKsMaxRows rows a chunk
+    const int cus = num_cus();
+    int rows = (int)std::min<int64_t>(kKsMaxRows, ((int64_t)N + cus - 1) / cus);
+    if (rows < 1) rows = 1;
+    const int64_t blocks = std::min<int64_t>(((int64_t)N + rows - 1) / rows, cus);
+    const size_t lds = (size_t)K * 2 + (size_t)(K / 8) * 4 + (size_t)kKsMaxRows * 4 * sizeof(float);
+    auto go = [&](auto fmt_c, auto upw_c, auto resid_c) -> int {
+        constexpr int F = decltype(fmt_c)::value, P = decltype(upw_c)::value;
+        constexpr bool R = decltype(resid_c)::value;
+        const void* fn = reinterpret_cast<const void*>(&gemv_m1_ksplit_kernel<F, P, R>);
+        if (int rc = hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                               "gemv ksplit: LDS attribute"))
+            return rc;
+        gemv_m1_ksplit_kernel<F, P, R><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, h, N, K, rows);
+        return 0;
+    };
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using RT = std::true_type;
+    using RF = std::false_type;
+    int rc = 0;
+    BX_DISPATCH_FMT(wtype, {
+        const std::integral_constant<int, FMT_> f{};
+        if (K == 24576) rc = h ? go(f, I3{}, RT{}) : go(f, I3{}, RF{});
+        else rc = h ? go(f, I4{}, RT{}) : go(f, I4{}, RF{});
+    })
+    if (rc) return rc;
+    return launch_check("gemv ksplit");
 }
 
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,

@@ -189,11 +189,13 @@ def test_fused_prefill_linears_equal_unfused_ops(t, M, K, Ns):
 
 @pytest.mark.parametrize("t", QTYPES)
 def test_linear_ffn_width_k(t):
-    """K = 32768 (Mistral-Small-3.1's FFN width, the down projection): the
-    wide one-row GEMV (16 units per lane, 80 KB of staged activations) and
-    the GEMM for 2..16 rows, and a K between the instantiated widths."""
+    """K = 32768 (Mistral-Small-3.1's FFN width, the down projection) and
+    24576: the one-row GEMV with K split over the workgroup's four wavefronts
+    (odd row counts end a chunk on the repeated-row request), and the GEMM for
+    2..16 rows; K 17408, between the split widths, takes the one-wavefront-
+    per-row kernel (16 units per lane, 80 KB of staged activations)."""
     rng = np.random.default_rng(4242 + t)
-    for N, K in ((320, 32768), (130, 17408)):
+    for N, K in ((320, 32768), (331, 24576), (130, 17408)):
         raw, Wv = sb.random_matrix(rng, t, N, K)
         car = carrier(t, raw, N, K)
         for M in (1, 2, 5, 17):

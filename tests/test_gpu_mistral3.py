@@ -53,6 +53,37 @@ def test_llama3_8b_widths_persistent_vs_oracle(ba, tmp_path_factory):
     m.close()
 
 
+@pytest.mark.timeout(600)
+def test_mistral_24b_widths_graph_step_vs_oracle(ba, tmp_path_factory):
+    """Two layers at Mistral-Small-3.1-24B widths (H 5120 > the persistent
+    step's 4096, so the graph step; F 32768: the down projection takes the
+    one-row GEMV with K split over each workgroup's wavefronts, adding into the
+    FP32 residual), vocab cut to 8192: a 64-token prefill and 6 single-token
+    steps against the oracle."""
+    from conftest import write_synth
+    spec = dict(vocab=8192, hidden=5120, intermediate=32768, layers=2, n_q=32, n_kv=8, head_dim=128,
+                tied=False, eps=1e-5, theta=1e9, context=131072, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K",
+                o="Q4_K", gate="Q4_K", up="Q4_K", down="Q6_K", output="Q6_K", seed=37)
+    path = write_synth(tmp_path_factory.mktemp("wm24"), spec, "wm24", arch="mistral3")
+    print("[mistral3] 24B-width checkpoint written", flush=True)
+    m = _load(ba, path, cap=256)
+    assert m.decode_mode() == "graph"
+    om = oracle.Model(str(path))
+    om.allocate_cache(256)
+    prompt = ba.prompt_ids(64, spec["vocab"], seed=42)
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    for step in range(6):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        print(f"[mistral3] 24B widths step {step} max diff {np.abs(a - b).max():.3e}", flush=True)
+        assert np.abs(a - b).max() <= LOGIT_TOL
+        tok = int(b.argmax())
+    m.close()
+
+
 def _load(ba, path, cap=128, env=None):
     m = ba.Mistral3TextModel(ba.Mistral3Config.from_gguf(str(path)).text)
     m.load_weights(str(path))
