@@ -217,6 +217,9 @@ def main() -> int:
                          "(for profiler runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the prompt prefill only and print its throughput (for hardware-counter runs)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="prefill, then time only the greedy decode steps and print their throughput (for "
+                         "profiler and hardware-counter runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a reference dispatch of known bytes for "
                          "hardware-counter runs)")
@@ -307,6 +310,23 @@ def main() -> int:
                           "unit": "tok/s", "prompt_tokens": c["prompt"], "ms": round(prefill_s * 1e3, 3),
                           "prefill_first_ms": round(prefill_first_s * 1e3, 3), "note": prefill_note,
                           "data": "synthetic"}), flush=True)
+        return 0
+    if args.decode_only:
+        if args.warmup > 0:
+            model.time_decode_steps(first, args.warmup)
+        model.truncate_cache(len(prompt))
+        mode = model.decode_mode()
+        t0 = time.perf_counter()
+        gpu_ms = model.time_decode_steps(first, steps)
+        wall = time.perf_counter() - t0
+        wbytes = model.decode_weight_bytes()
+        model.close()
+        ba.shutdown()
+        print(json.dumps({"metric": f"decode tok/s bs=1 {args.config}", "value": round(steps / wall, 2),
+                          "unit": "tok/s", "steps": steps, "decode_step": mode,
+                          "gpu_ms_per_step_events": round(gpu_ms, 5),
+                          "achieved_gbs": round(wbytes / (gpu_ms * 1e-3) / 1e9, 1), "data": "synthetic"}),
+              flush=True)
         return 0
     # bidirectional encode (DenseDecoder::forward_encode, the LLM2Vec pass) of
     # the first 512 prompt tokens; the KV cache is not touched

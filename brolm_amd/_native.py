@@ -67,6 +67,7 @@ HIP_SYMBOLS = {
     "bx_last_error": (cp, []),
     "bx_abi_version": (C.c_int, []),
     "bx_device_ok": (C.c_int, []),
+    "bx_profiler_attached": (C.c_int, []),
     "bx_repack_gguf_rows": (C.c_int, [C.c_int, vp, vp, i64, i64, vp]),
     "bx_unpack_carrier_rows": (C.c_int, [C.c_int, vp, vp, i64, i64, vp]),
     "bx_carrier_bytes": (i64, [C.c_int, i64, i64]),

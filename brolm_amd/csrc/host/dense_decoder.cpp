@@ -97,6 +97,27 @@ struct DecodeGraphSession {
 
 // ─── construction ────────────────────────────────────────────────────────────
 //
+// One replayable step per row count M: the first step of a given M runs
+// eagerly (it also settles every buffer), the second is captured and every
+// later one replays the graph.  The kernels read positions, lengths, slots
+// and token ids from batch_meta_, so a replay needs only that upload.
+struct DenseDecoder::BatchGraphs {
+    std::vector<hipGraphExec_t> exec;
+    std::vector<char> warmed;
+    bool use_graph = true;
+
+    explicit BatchGraphs(int n) : exec(static_cast<std::size_t>(n) + 1, nullptr), warmed(exec.size(), 0) {
+        // eager steps under a profiler tool (a graph launch under rocprofv3
+        // has ended the process in the profiler's exit path)
+        use_graph = !env_flag("BROLM_NO_GRAPH") && !bx_profiler_attached();
+    }
+    ~BatchGraphs() {
+        if (bt::initialized()) (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
+        for (hipGraphExec_t e : exec)
+            if (e) (void)hipGraphExecDestroy(e);
+    }
+};
+
 // The shape rules and their messages are the reference's
 // (src/detail/dense_decoder.cpp:97-112); they are checked in table order.
 
@@ -213,7 +234,15 @@ void DenseDecoder::load_weights(const weights::Source& src) {
         {{"mlp.down_proj.weight", "down_proj.weight", Dim::Hidden, Dim::Ffn, Upload::Carrier}, &Layer::down_W,
          false},
     };
-    invalidate_graph_();   // a captured step holds the old weight pointers
+    // Everything derived from the old weights goes: the captured single-token
+    // step and the batched steps' graphs hold their pointers, and the FP16
+    // layer copies of long passes hold their values (rebuilt by the next pass
+    // of 512+ rows).
+    invalidate_graph_();
+    if (batch_graphs_) batch_graphs_ = std::make_unique<BatchGraphs>(batch_slots_);
+    for (Layer& ly : layers_)
+        for (bt::Tensor* t : {&ly.q16, &ly.k16, &ly.v16, &ly.o16, &ly.gate16, &ly.up16, &ly.down16}) *t = bt::Tensor();
+    f16_state_ = 0;
     const ModelDims d{cfg_.vocab_size, cfg_.hidden_size, cfg_.intermediate_size, cfg_.head_dim,
                       cfg_.num_attention_heads, cfg_.num_key_value_heads};
     upload(src, "model.embed_tokens.weight", {"", "embed_tokens.weight", Dim::Vocab, Dim::Hidden, Upload::Dense}, d,
@@ -698,8 +727,11 @@ DecodeGraphSession& DenseDecoder::session_() {
     hipx::check(hipHostMalloc(reinterpret_cast<void**>(&s->pinned), 4 * sizeof(int32_t), hipHostMallocDefault),
                 "hipHostMalloc");
     hipx::check(hipEventCreateWithFlags(&s->staged, hipEventDisableTiming), "hipEventCreate");
-    s->use_graph = !env_flag("BROLM_NO_GRAPH");
-    if (s->use_graph && !env_flag("BROLM_NO_PERSIST") && persist_types_ok(d, s->layers)) {
+    // no captured graph under a profiler tool: a graph launch under
+    // rocprofv3 has ended the process in the profiler's exit path
+    const bool no_fused = env_flag("BROLM_NO_GRAPH");
+    s->use_graph = !no_fused && !bx_profiler_attached();
+    if (!no_fused && !env_flag("BROLM_NO_PERSIST") && persist_types_ok(d, s->layers)) {
         s->pws_bytes = bx_persist_ws_bytes(&d);
         if (s->pws_bytes != 0) {
             hipx::check(hipMalloc(&s->pws, s->pws_bytes), "hipMalloc persist ws");
@@ -999,24 +1031,6 @@ namespace {
 constexpr int kMetaI64PerRow = 4;  // dst row, base row (int64); pos, len, id (int32) fit in two more
 }
 
-// One replayable step per row count M: the first step of a given M runs
-// eagerly (it also settles every buffer), the second is captured and every
-// later one replays the graph.  The kernels read positions, lengths, slots
-// and token ids from batch_meta_, so a replay needs only that upload.
-struct DenseDecoder::BatchGraphs {
-    std::vector<hipGraphExec_t> exec;
-    std::vector<char> warmed;
-    bool use_graph = true;
-
-    explicit BatchGraphs(int n) : exec(static_cast<std::size_t>(n) + 1, nullptr), warmed(exec.size(), 0) {
-        use_graph = !env_flag("BROLM_NO_GRAPH");
-    }
-    ~BatchGraphs() {
-        if (bt::initialized()) (void)hipStreamSynchronize(static_cast<hipStream_t>(bt::stream()));
-        for (hipGraphExec_t e : exec)
-            if (e) (void)hipGraphExecDestroy(e);
-    }
-};
 
 void DenseDecoder::allocate_batch(int n_slots, int max_seq_len) {
     if (n_slots <= 0 || max_seq_len <= 0) fail("allocate_batch: n_slots and max_seq_len must be positive");

@@ -25,6 +25,8 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Number of compute units on the current device (cached per device).
 int num_cus();
+// true when a rocprofiler-sdk tool (rocprofv3) is loaded into the process
+bool profiler_attached();
 // Workgroups of `threads` threads and `lds` dynamic LDS bytes that one CU
 // holds at once for kernel `fn` (registers and LDS); asked of the runtime once
 // per (kernel, threads, LDS) and cached; at least 1.

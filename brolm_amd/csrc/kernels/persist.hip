@@ -1524,16 +1524,17 @@ __global__ void persist_ws_init_kernel(uint32_t* ctrl, uint64_t* words, size_t n
 }
 
 }  // namespace
-}  // namespace bx
 
-extern "C" size_t bx_persist_ws_bytes(const bx_decode_dims* d) {
+// The first persistent step, kept for the shapes persist2.hip has no
+// instantiation for; the bx_persist_* entry points (persist2.hip) call these.
+size_t p1_ws_bytes(const bx_decode_dims* d) {
     if (!d) return 0;
     bx::PLayout o{};
     if (bx::persist_layout(*d, bx::persist_grid(), o) != BX_OK) return 0;
     return o.total;
 }
 
-extern "C" int bx_persist_ws_init(const bx_decode_dims* d, void* ws, void* stream) {
+int p1_ws_init(const bx_decode_dims* d, void* ws, void* stream) {
     if (!d || !ws) return bx::fail(BX_EINVAL, "persist_ws_init: null pointer");
     bx::PLayout o{};
     if (int rc = bx::persist_layout(*d, bx::persist_grid(), o)) return rc;
@@ -1545,10 +1546,9 @@ extern "C" int bx_persist_ws_init(const bx_decode_dims* d, void* ws, void* strea
     return BX_OK;
 }
 
-extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev,
-                               const uint16_t* embed, const uint16_t* final_norm, const void* lm_head,
-                               const float* cos_tab, const float* sin_tab, int32_t* scal, uint16_t* logits,
-                               void* ws, uint32_t epoch, void* stream) {
+int p1_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers_dev, const uint16_t* embed,
+            const uint16_t* final_norm, const void* lm_head, const float* cos_tab, const float* sin_tab, int32_t* scal,
+            uint16_t* logits, void* ws, uint32_t epoch, void* stream) {
     if (!d || !layers_dev || !embed || !final_norm || !lm_head || !cos_tab || !sin_tab || !scal || !logits || !ws)
         return bx::fail(BX_EINVAL, "persist: null pointer");
     if (n_layers <= 0 || n_layers > 126) return bx::fail(BX_EINVAL, "persist: layer count");
@@ -1586,13 +1586,15 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
             return bx::fail(BX_ELAUNCH, "persist: cannot raise the LDS limit");
     }
     void* args[] = {&a};
-    // BROLM_PERSIST_PLAIN_LAUNCH: launch the same grid without the cooperative
-    // API, for profilers that cannot finish a process whose kernels were
-    // launched cooperatively.  The occupancy check below is the one the
-    // cooperative launch makes (one workgroup per CU, grid = CU count), so
-    // the grid is co-resident on an otherwise idle device; every wait is also
-    // bounded and raises the abort flag, so the kernel ends either way.
-    static const bool plain = std::getenv("BROLM_PERSIST_PLAIN_LAUNCH") != nullptr;
+    // Plain launch of the same grid, without the cooperative API, whenever a
+    // profiler tool is loaded (rocprofv3 has ended processes whose kernels
+    // were launched cooperatively with a segmentation fault in its exit
+    // path), or when BROLM_PERSIST_PLAIN_LAUNCH is set.  The occupancy check
+    // below is the one the cooperative launch makes (one workgroup per CU,
+    // grid = CU count), so the grid is co-resident on an otherwise idle
+    // device; every wait is also bounded and raises the abort flag, so the
+    // kernel ends either way.
+    static const bool plain = std::getenv("BROLM_PERSIST_PLAIN_LAUNCH") != nullptr || bx::profiler_attached();
     hipError_t e;
     if (plain) {
         int per_cu = 0;
@@ -1609,17 +1611,6 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     return BX_OK;
 }
 
-extern "C" int bx_persist_status(const void* ws, uint32_t* site) {
-    if (!ws) return bx::fail(BX_EINVAL, "persist_status: null workspace");
-    uint32_t c[2] = {0, 0};
-    if (hipMemcpy(c, ws, sizeof(c), hipMemcpyDeviceToHost) != hipSuccess)
-        return bx::fail(BX_ELAUNCH, "persist_status: copy failed");
-    if (site) *site = c[1];
-    return c[0] ? 1 : 0;
-}
+void p1_set_trace(uint64_t* buf) { g_trace = buf; }
 
-extern "C" int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg) {
-    if (buf_dev && slots_per_wg < bx::kTraceSlots) return bx::fail(BX_EINVAL, "persist_trace: need 1024 slots per workgroup");
-    bx::g_trace = buf_dev;
-    return BX_OK;
-}
+}  // namespace bx

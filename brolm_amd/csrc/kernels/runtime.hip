@@ -1,6 +1,10 @@
 // Host-side plumbing shared by every bx_* entry point: error state, device info.
 #include "common.h"
 
+#include <link.h>
+
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -53,9 +57,35 @@ int resident_wgs(const void* fn, int threads, size_t lds) {
     return occ;
 }
 
+// rocprofv3 injects its tool by LD_PRELOAD of librocprofiler-sdk-tool.so and
+// names it in ROCP_TOOL_LIBRARIES.  Under that tool, a process whose kernels
+// were launched cooperatively, or through a hipGraph, has ended in a host
+// segmentation fault in the profiler's exit path; the launch paths consult
+// this to take the plain launch and the eager step instead.
+static int find_profiler_tool(struct dl_phdr_info* info, size_t, void* hit) {
+    if (info->dlpi_name && std::strstr(info->dlpi_name, "librocprofiler-sdk-tool")) {
+        *static_cast<int*>(hit) = 1;
+        return 1;
+    }
+    return 0;
+}
+
+bool profiler_attached() {
+    static const bool attached = [] {
+        const char* t = std::getenv("ROCP_TOOL_LIBRARIES");
+        if (t && t[0]) return true;
+        int hit = 0;
+        dl_iterate_phdr(find_profiler_tool, &hit);
+        return hit != 0;
+    }();
+    return attached;
+}
+
 }  // namespace bx
 
 extern "C" {
+
+int bx_profiler_attached(void) { return bx::profiler_attached() ? 1 : 0; }
 
 const char* bx_last_error(void) { return bx::g_last_error.c_str(); }
 

@@ -48,6 +48,12 @@ const char* bx_last_error(void);
 int bx_abi_version(void);
 /* 1 if a gfx950 device is present and the code objects load. */
 int bx_device_ok(void);
+/* 1 if a rocprofiler-sdk tool (rocprofv3) is loaded into this process.  No
+ * counterpart in the reference.  Under such a tool, bx_persist_step launches
+ * its grid without the cooperative API and the host decode session steps
+ * eagerly instead of through a hipGraph: with those two launch forms, the
+ * profiler's exit path has ended the process with a segmentation fault. */
+int bx_profiler_attached(void);
 
 /* ---------------------------------------------------------------- carriers */
 
