@@ -53,6 +53,13 @@ CONFIGS = {
     "qwen3-1.7b-q4k": dict(vocab=151936, hidden=2048, intermediate=6144, layers=28, n_q=16, n_kv=8, head_dim=128,
                            tied=False, embed="Q4_K", q="Q4_K", k="Q4_K", v="Q6_K", o="Q4_K", gate="Q4_K",
                            up="Q4_K", down="Q6_K", output="Q6_K", prompt=1024, decode=512, cap=4096),
+    # the layout of a real Qwen3-1.7B-Q4_K_M file: tied Q6_K embedding (FP16
+    # lm_head clone), attn_v / ffn_down Q6_K on llama.cpp's use_more_bits
+    # layers and Q4_K elsewhere
+    "qwen3-1.7b-q4k_m": dict(vocab=151936, hidden=2048, intermediate=6144, layers=28, n_q=16, n_kv=8, head_dim=128,
+                             tied=True, embed="Q6_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K",
+                             up="Q4_K", down="Q4_K", output="Q6_K", more_bits="Q6_K", prompt=1024, decode=512,
+                             cap=4096),
     # BASELINE.json configs[1]
     "qwen3-0.6b-q8_0": dict(vocab=151936, hidden=1024, intermediate=3072, layers=28, n_q=16, n_kv=8, head_dim=128,
                             tied=True, embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0",

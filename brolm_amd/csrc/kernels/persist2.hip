@@ -99,7 +99,7 @@ struct Args {
     int rec;                // words per attention record (even)
     int fblk;               // FFN slice granularity (elements)
     int wact;               // SwiGLU words per workgroup (even)
-    int wpart;              // partial words per workgroup (even), ceil(H / 32 / 3) rounded up
+    int wpart;              // h-update words per workgroup (even), ceil(H / 32 / 3) rounded up
     const bx_decode_layer* layers;
     const uint16_t* embed;
     const uint16_t* final_norm;
@@ -112,10 +112,12 @@ struct Args {
     uint64_t* qkv;          // local, [kX][qkv_stride]
     uint64_t* recw;         // local, [kX][rec_stride]
     uint64_t* act;          // local, [kX][act_stride]
-    uint64_t* pwo;          // cross, [kX][part_stride]
-    uint64_t* pdn;          // cross, [kX][part_stride]
+    uint64_t* pwo;          // cross, [kX][part_stride]: Wo partials, one FP32 row per word
+    uint64_t* pdn;          // cross, [kX][part_stride]: Wd partials
+    uint64_t* hupo;         // local, [kX][hup_stride]: summed Wo update of h (FP16 triples)
+    uint64_t* hupd;         // local, [kX][hup_stride]: summed Wd update of h
     uint64_t* cand;         // cross, [2 kG]
-    int qkv_stride, rec_stride, act_stride, part_stride;
+    int qkv_stride, rec_stride, act_stride, part_stride, hup_stride;
     uint64_t* trace;
 };
 
@@ -172,6 +174,11 @@ struct FastDivP {
 
 __device__ __forceinline__ void stamp(const Args& a, int slot) {
     if (a.trace && tidx() == 0) a.trace[(size_t)blockIdx.x * kTraceSlots + slot] = wall_clock64();
+}
+
+// Sub-stage stamps of layer 14 (slots 600 + k).
+__device__ __forceinline__ void sub(const Args& a, int l, int k) {
+    if (l == 14) stamp(a, 600 + k);
 }
 
 __device__ __forceinline__ bool aborted(const Args& a) {
@@ -371,45 +378,79 @@ struct Task {
     static constexpr int RPP = 64 / LPR;   // rows per pass
     Raw raw[NP][UPL];
 
+    // Pass p's units (rows r0 + p (64 / LPR) + lane / LPR, clamped).
     template <int FMT>
-    __device__ __forceinline__ void load(const void* W, int64_t N, int64_t K, int uc0, int U, int r0) {
+    __device__ __forceinline__ void load_pass(const void* W, int64_t N, int64_t K, int uc0, int U, int r0, int p) {
         const int lane = tidx() & 63;
         const int slot = lane & (LPR - 1), rip = lane / LPR;
+        int64_t row = r0 + p * RPP + rip;
+        row = row < N ? row : N - 1;
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            int64_t row = r0 + p * RPP + rip;
-            row = row < N ? row : N - 1;
-#pragma unroll
-            for (int i = 0; i < UPL; ++i) {
-                const int u = slot + LPR * i;
-                const int uu = uc0 + (u < U ? u : U - 1);
-                if constexpr (std::is_same_v<Raw, RawAny>) load_any<FMT>(raw[p][i], W, N, K, row, uu);
-                else raw[p][i] = load_unit<FMT>(W, N, K, row, uu);
-            }
+        for (int i = 0; i < UPL; ++i) {
+            const int u = slot + LPR * i;
+            const int uu = uc0 + (u < U ? u : U - 1);
+            if constexpr (std::is_same_v<Raw, RawAny>) load_any<FMT>(raw[p][i], W, N, K, row, uu);
+            else raw[p][i] = load_unit<FMT>(W, N, K, row, uu);
         }
+    }
+    template <int FMT>
+    __device__ __forceinline__ void load(const void* W, int64_t N, int64_t K, int uc0, int U, int r0) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) load_pass<FMT>(W, N, K, uc0, U, r0, p);
+    }
+
+    template <int FMT>
+    __device__ __forceinline__ float dot_pass(const XRegs<FMT, LPR, UPL>& xr, int U, int p) const {
+        const int slot = (tidx() & 63) & (LPR - 1);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = slot + LPR * i;
+            const int uc = u < U ? u : U - 1;
+            float c;
+            if constexpr (std::is_same_v<Raw, RawAny>) c = dot_any<FMT>(raw[p][i], uc, xr.x[i]);
+            else c = dot_reg(raw[p][i], uc, xr.x[i]);
+            acc += u < U ? c : 0.f;
+        }
+        return acc;
     }
 
     // out[p]: the row sum of pass p, valid in lane sum_lane<LPR>(lane / LPR).
-    template <int FMT>
-    __device__ __forceinline__ void dot(const XRegs<FMT, LPR, UPL>& xr, int U, float (&out)[NP]) const {
-        const int slot = (tidx() & 63) & (LPR - 1);
+    // side(p) runs after pass p's products (the next stage's loads issued
+    // between passes, so the texture unit works while the SIMD computes).
+    template <int FMT, class Side>
+    __device__ __forceinline__ void dot(const XRegs<FMT, LPR, UPL>& xr, int U, float (&out)[NP], Side side) const {
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < UPL; ++i) {
-                const int u = slot + LPR * i;
-                const int uc = u < U ? u : U - 1;
-                float c;
-                if constexpr (std::is_same_v<Raw, RawAny>) c = dot_any<FMT>(raw[p][i], uc, xr.x[i]);
-                else c = dot_reg(raw[p][i], uc, xr.x[i]);
-                acc += u < U ? c : 0.f;
-            }
-            out[p] = acc;
+            out[p] = dot_pass<FMT>(xr, U, p);
+            side(p);
+            pin();
         }
         group_sum<LPR, NP>(out);
     }
+    template <int FMT>
+    __device__ __forceinline__ void dot(const XRegs<FMT, LPR, UPL>& xr, int U, float (&out)[NP]) const {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) out[p] = dot_pass<FMT>(xr, U, p);
+        group_sum<LPR, NP>(out);
+    }
 };
+
+// Two tasks of one format and shape (gate / up) pass by pass, side(p) after each.
+template <int FMT, class Raw, int LPR, int UPL, int NP, class Side>
+__device__ __forceinline__ void dot_pair(const Task<Raw, LPR, UPL, NP>& ta, const Task<Raw, LPR, UPL, NP>& tb,
+                                         const XRegs<FMT, LPR, UPL>& xr, int U, float (&oa)[NP], float (&ob)[NP],
+                                         Side side) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        oa[p] = ta.template dot_pass<FMT>(xr, U, p);
+        ob[p] = tb.template dot_pass<FMT>(xr, U, p);
+        side(p);
+        pin();
+    }
+    group_sum<LPR, NP>(oa);
+    group_sum<LPR, NP>(ob);
+}
 
 // Calls emit(row, value) from the lane holding each row's sum, for rows below
 // r_end.
@@ -503,75 +544,74 @@ __device__ __forceinline__ void norm_to_xs(const Arena& ar, int H, float ss, con
     __syncthreads();
 }
 
-// Residual update from the partial vectors of the XCDs set in xmask (each
-// [kR][wpart] words: workgroup r's rows r Hr + 3k + j in word k, slot j):
-// h += p_0 + p_1 + ... in XCD order.  A thread polls the same word pair of
-// every XCD, so it adds each of its rows' terms in that fixed order.  Returns
-// this thread's share of sum(h^2) in ss.
-template <int EP>
-__device__ __forceinline__ bool gather_partials(const Args& a, const Arena& ar, const uint64_t* buf, uint32_t xmask,
-                                                uint32_t tag, uint32_t site, float& ss) {
+// The residual update of a layer half is the sum of the XCDs' partials (Wo
+// over each attention unit's heads, Wd over each FFN slice).  It reaches every
+// workgroup in two hops: workgroup (x, r) sums the partials of its own rows
+// [r Hr, r Hr + Hr) over the XCDs in xmask, in XCD order, and publishes the
+// sum rounded to FP16 (the op path's projection output) through its XCD's L2;
+// then every workgroup of XCD x adds the 32 blocks to its copy of h.  The
+// first hop crosses XCDs with Hr words per XCD, the second stays in the L2.
+__device__ __forceinline__ bool reduce_block(const Args& a, const Arena& ar, const uint64_t* part, uint32_t xmask,
+                                             int x, int r, uint32_t tin, uint32_t site, uint64_t* hup,
+                                             uint32_t tout) {
     const int Hr = a.H / kR;
-    const int np = kR * a.wpart / 2;   // pairs per XCD vector
-    const __amdgpu_buffer_rsrc_t rs = rsrc(buf);
-    int nx = 0, xs_[kX];
+    const __amdgpu_buffer_rsrc_t rs = rsrc(part);
+    bool ok = true;
+    __syncthreads();   // ar.rows may still be read by the previous stage's emit
+    const int q0 = __builtin_ctz(xmask);   // XCDs outside xmask poll a copy of the first one's words
+    for (int p = tidx(); p < Hr / 2; p += kT) {
+        int off[kX];
 #pragma unroll
-    for (int x = 0; x < kX; ++x)
-        if (xmask & (1u << x)) xs_[nx++] = x;
-    ss = 0.f;
-    constexpr int kPP = EP / kX;   // pairs per thread per round
-    for (int base = 0; base < np; base += kPP * kT) {
-        int off[EP];
-        int n = 0;
+        for (int q = 0; q < kX; ++q) off[q] = (((xmask >> q) & 1u ? q : q0) * a.part_stride + r * Hr + 2 * p) * 8;
+        u4v v[kX];
+        ok = ok && poll_slots<kX, kCross>(a, rs, off, kX, tin, site, v);
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int q = 0; q < kPP; ++q) {
-            const int p = base + tidx() + q * kT;
-#pragma unroll
-            for (int x = 0; x < kX; ++x) {
-                const int e = q * kX + x;
-                const bool ok = p < np && x < nx;
-                off[e] = ok ? (xs_[x] * a.part_stride + 2 * p) * 8 : 0;
-                if (ok) n = e + 1;
-            }
+        for (int q = 0; q < kX; ++q) {
+            if (!((xmask >> q) & 1u)) continue;
+            s0 += __uint_as_float(v[q][0]);
+            s1 += __uint_as_float(v[q][2]);
         }
-        // slots past n are pairs of XCDs beyond nx or past the vector: polled as
-        // copies of slot 0 (always live) so that every slot below n is meaningful
+        ar.rows[2 * p] = s0;
+        ar.rows[2 * p + 1] = s1;
+    }
+    if (!__syncthreads_and(ok)) return false;
+    uint64_t* out = hup + (int64_t)x * a.hup_stride + r * a.wpart;
+    for (int k = tidx(); k < a.wpart; k += kT) {
+        uint32_t v[3];
 #pragma unroll
-        for (int e = 0; e < EP; ++e) {
-            const int q = e / kX, x = e % kX;
-            const int p = base + tidx() + q * kT;
-            if (!(p < np && x < nx)) off[e] = off[0];
-        }
-        u4v v[EP];
-        if (!poll_slots<EP, kCross>(a, rs, off, n, tag, site, v)) return false;
-        const FastDivP dw(a.wpart);
-#pragma unroll
-        for (int q = 0; q < kPP; ++q) {
-            const int p = base + tidx() + q * kT;
-            if (p >= np) continue;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int W = 2 * p + h;
-                const int r = dw.div(W), k = W - r * a.wpart;
-#pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const int idx = 3 * k + j;
-                    if (idx >= Hr) continue;
-                    const int row = r * Hr + idx;
-                    float s = ar.hv[row];
-#pragma unroll
-                    for (int x = 0; x < kX; ++x) {
-                        if (x >= nx) break;
-                        const u4v w = v[q * kX + x];
-                        s += h2f((uint16_t)fld(h ? w[2] : w[0], h ? w[3] : w[1], j));
-                    }
-                    ar.hv[row] = s;
-                    ss += s * s;
-                }
-            }
-        }
+        for (int j = 0; j < 3; ++j) v[j] = 3 * k + j < Hr ? f2h(ar.rows[3 * k + j]) : 0u;
+        st_local(out + k, word3(tout, v[0], v[1], v[2]));
     }
     return true;
+}
+
+// h += the 32 FP16 update blocks of XCD x; ss = this thread's share of sum(h^2).
+__device__ __forceinline__ bool apply_update(const Args& a, const Arena& ar, const uint64_t* hup, int x, uint32_t tag,
+                                             uint32_t site, float& ss) {
+    const int Hr = a.H / kR;
+    const FastDivP dw(a.wpart);
+    ss = 0.f;
+    return poll_vec<2, kLocal>(a, hup + (int64_t)x * a.hup_stride, kR * a.wpart, tag, site,
+                               [&](int W, uint32_t lo, uint32_t hi) {
+                                   const int rr = dw.div(W), k = W - rr * a.wpart;
+#pragma unroll
+                                   for (int j = 0; j < 3; ++j) {
+                                       if (3 * k + j >= Hr) continue;
+                                       const int row = rr * Hr + 3 * k + j;
+                                       const float hvv = ar.hv[row] + h2f((uint16_t)fld(lo, hi, j));
+                                       ar.hv[row] = hvv;
+                                       ss += hvv * hvv;
+                                   }
+                               });
+}
+
+// This workgroup's partial rows [hb, hb + Hr) (ar.rows) as FP32 words.
+__device__ __forceinline__ void emit_partial(const Args& a, const Arena& ar, uint64_t* part, int x, int r,
+                                             uint32_t tag) {
+    const int Hr = a.H / kR;
+    uint64_t* out = part + (int64_t)x * a.part_stride + r * Hr;
+    for (int i = tidx(); i < Hr; i += kT) st_cross(out + i, word1(tag, __float_as_uint(ar.rows[i])));
 }
 
 // ---- attention --------------------------------------------------------------------
@@ -784,8 +824,10 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
                                           dst[row] = h2f((uint16_t)fld(lo, hi, j));
                                       }
                                   });
+    sub(a, layer, 1);
     __builtin_amdgcn_s_waitcnt(0);   // this wave's tile copies have landed
     if (!__syncthreads_and(ok)) return false;
+    sub(a, layer, 2);
 
     // q head of this wave, and the current key / value for the part holding pos
     const int h = sp.gl * Gq + hh;   // head within the unit
@@ -812,6 +854,7 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
         }
     }
 
+    sub(a, layer, 3);
     // scores of this wave's keys (lane t: keys jb + t, jb + 64 + t)
     const float scale = 1.0f / sqrtf((float)HD);
     const int nkw = je - jb;
@@ -869,6 +912,7 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
             o1 += p * h2f(vv[u] >> 16);
         }
     }
+    sub(a, layer, 4);
     // this wave's part: o (unnormalized), m, l (an empty part has l = 0)
     float* pr = sc.parts + wave * (HD + 2);
     if (2 * lane < HD) {
@@ -880,6 +924,7 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
         pr[HD + 1] = nkw > 0 ? Lw : 0.f;
     }
     __syncthreads();
+    sub(a, layer, 5);
     // records of the group's heads: o / l over the merged parts (FP16), m, l
     const uint32_t tout = tag_of(a, layer, 1);
     uint64_t* rbase = a.recw + (int64_t)sp.x * a.rec_stride + (int64_t)((sp.gl * a.smax + sp.s) * Gq) * a.rec;
@@ -920,6 +965,7 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
         }
         st_local(rbase + t, wd);
     }
+    sub(a, layer, 6);
     return true;
 }
 
@@ -953,34 +999,38 @@ __device__ __forceinline__ bool combine(const Args& a, int x, const Arena& ar, f
         });
         if (!__syncthreads_and(ok)) return false;
     }
-    // weights per (head, split): exp(m_s - M) l_s / sum
+    sub(a, layer, 15);
+    // weights per (head, split), exp(m_s - M) l_s / sum: one wave per head, one lane per split
     float* wts = ar.att;   // heads x S
-    for (int h = tidx(); h < heads; h += kT) {
-        float M = -INFINITY;
-        for (int s = 0; s < S; ++s) M = fmaxf(M, recs[(h * S + s) * (HD + 2) + HD]);
-        float tot = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float* r = recs + (h * S + s) * (HD + 2);
-            const float wgt = r[HD + 1] > 0.f ? __expf(r[HD] - M) * r[HD + 1] : 0.f;
-            wts[h * S + s] = wgt;
-            tot += wgt;
+    {
+        const int lane = tidx() & 63;
+        for (int h = tidx() >> 6; h < heads; h += kW) {
+            float m = -INFINITY, l = 0.f;
+            if (lane < S) {
+                m = recs[(h * S + lane) * (HD + 2) + HD];
+                l = recs[(h * S + lane) * (HD + 2) + HD + 1];
+            }
+            const float M = wave_max(m);
+            const float wgt = lane < S && l > 0.f ? __expf(m - M) * l : 0.f;
+            const float tot = wave_sum(wgt);
+            if (lane < S) wts[h * S + lane] = wgt / tot;
         }
-        const float inv = 1.0f / tot;
-        for (int s = 0; s < S; ++s) wts[h * S + s] *= inv;
     }
     __syncthreads();
-    // output pairs (head h, dims 2p, 2p + 1) -> FP16 -> swizzled activation
-    for (int t = tidx(); t < heads * HD / 2; t += kT) {
-        const int h = t / (HD / 2), d = 2 * (t - h * (HD / 2));
-        float o0 = 0.f, o1 = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float wgt = wts[h * S + s];
-            const float* r = recs + (h * S + s) * (HD + 2);
-            o0 += wgt * r[d];
-            o1 += wgt * r[d + 1];
+    sub(a, layer, 16);
+    // output element (head h, dim d) -> FP16 -> swizzled activation
+    for (int t = tidx(); t < heads * HD; t += kT) {
+        const int h = t / HD, d = t - h * HD;
+        const float* r0 = recs + h * S * (HD + 2) + d;
+        const float* w0 = wts + h * S;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        int s = 0;
+        for (; s + 4 <= S; s += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o[u] += w0[s + u] * r0[(s + u) * (HD + 2)];
         }
-        put_swz(ar.xs, h * HD + d, f2h(o0));
-        put_swz(ar.xs, h * HD + d + 1, f2h(o1));
+        for (; s < S; ++s) o[0] += w0[s] * r0[s * (HD + 2)];
+        put_swz(ar.xs, h * HD + d, f2h((o[0] + o[1]) + (o[2] + o[3])));
     }
     __syncthreads();
     sums8_from_lds(ar.xs, heads * HD, ar.xsum);
@@ -1114,33 +1164,49 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
     Task<typename RawOf<FGU>::T, LD, UD, ND> tg, tu;
     Task<RawFor<FD, FD2>, LE, UE, NE> te;
     auto a_fmt = [&](const bx_decode_layer& Ly) { return seg == 2 ? Ly.type_v : FQ; };
-    auto load_a = [&](const bx_decode_layer& Ly, int row) {
-        if (!unit || awb >= awe) return;
-        const void* W = seg == 0 ? Ly.Wq : (seg == 1 ? Ly.Wk : Ly.Wv);
-        const int f = a_fmt(Ly);
-        if (f == FQ || seg != 2) ta.template load<FQ>(W, aN, H, 0, UAn, srow0 + row);
-        else if (f == FV) ta.template load<FV>(W, aN, H, 0, UAn, srow0 + row);
-        else if constexpr (FV2 >= 0) ta.template load<FV2>(W, aN, H, 0, UAn, srow0 + row);
+    const void* const* a_mat = seg == 0 ? &lt[0].Wq : (seg == 1 ? &lt[0].Wk : &lt[0].Wv);
+    const size_t a_mat_off = (const char*)a_mat - (const char*)&lt[0];
+    auto a_w = [&](const bx_decode_layer& Ly) {
+        return *reinterpret_cast<const void* const*>(reinterpret_cast<const char*>(&Ly) + a_mat_off);
     };
-    auto load_e = [&](const bx_decode_layer& Ly, int row) {
-        if (Fx == 0) return;
-        if (Ly.type_down == FD) te.template load<FD>(Ly.Wd, H, a.F, fb / 32, UEn, row);
-        else if constexpr (FD2 >= 0) te.template load<FD2>(Ly.Wd, H, a.F, fb / 32, UEn, row);
+    // pass p of the q / k / v block of layer Ly (rows clamped: a workgroup
+    // without rows loads harmless copies, so the loads stay unconditional)
+    auto load_a_pass = [&](const bx_decode_layer& Ly, int p, int zl) {
+        const int f = a_fmt(Ly);
+        if (seg != 2 || f == FQ) ta.template load_pass<FQ>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+        else if (f == FV) ta.template load_pass<FV>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+        else if constexpr (FV2 >= 0) ta.template load_pass<FV2>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+    };
+    const int uc_o = (min(x, a.nu - 1) * slice_o) / 32;
+    auto load_d = [&](const bx_decode_layer& Ly, int zl) {
+        tg.template load<FGU>(Ly.Wg, a.F, H, 0, UAn, dwb + zl);
+        tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, dwb + zl);
+    };
+    auto load_e_pass = [&](const bx_decode_layer& Ly, int p, int zl) {
+        if (Ly.type_down == FD) te.template load_pass<FD>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+        else if constexpr (FD2 >= 0) te.template load_pass<FD2>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
     };
 
     tile_prefetch<HD>(a, w, lt[0], pos, tile);
-    load_a(lt[0], awb + opaque_zero());
+#pragma unroll
+    for (int p = 0; p < NA; ++p) load_a_pass(lt[0], p, opaque_zero());
     pin();
 
     for (int l = 0; l < a.L; ++l) {
         const bx_decode_layer& Ly = lt[l];
+        const bx_decode_layer& Ln = lt[min(l + 1, a.L - 1)];
         const int zl = opaque_zero();
         const int sl = 1 + 9 * l;
-        // ---- A: residual, norm, q / k / v rows
+        // ---- A: residual, norm, q / k / v rows; the Wo and gate / up blocks
+        // are requested between the passes
         {
             float ss = 0.f;
             if (l > 0) {
-                if (!gather_partials<16>(a, ar, a.pdn + zl, xmask_d, tag_of(a, l - 1, 4), 1, ss)) return;
+                if (!reduce_block(a, ar, a.pdn + zl, xmask_d, x, r, tag_of(a, l - 1, 4), 1, a.hupd + zl,
+                                  tag_of(a, l - 1, 6)))
+                    return;
+                sub(a, l, 0);
+                if (!apply_update(a, ar, a.hupd + zl, x, tag_of(a, l - 1, 6), 7, ss)) return;
             } else {
                 for (int i = tidx(); i < H; i += kT) ss += ar.hv[i] * ar.hv[i];
             }
@@ -1148,7 +1214,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             norm_to_xs(ar, H, ss, Ly.in_ln, a.eps);
             stamp(a, sl + 0);
             // Wo rows stream while q / k / v are computed and travel
-            if (unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, (x * slice_o) / 32 + zl, UCn, cwb);
+            if (unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o + zl, UCn, cwb);
             pin();
             if (unit && awb < awe) {
                 auto run = [&](auto fmt_tag) {
@@ -1156,9 +1222,8 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     XRegs<F, LA, UA> xr;
                     xr.load(ar.xs, ar.xsum, UAn);
                     for (int t0 = awb; t0 < awe; t0 += RA) {
-                        if (t0 != awb) ta.template load<F>(seg == 0 ? Ly.Wq : (seg == 1 ? Ly.Wk : Ly.Wv), aN, H, 0,
-                                                           UAn, srow0 + t0 + zl);
                         float o[NA];
+                        if (t0 != awb) ta.template load<F>(a_w(Ly), aN, H, 0, UAn, srow0 + t0 + zl);
                         ta.template dot<F>(xr, UAn, o);
                         emit_rows<LA, NA>(t0, awe, o, [&](int row, float v) { ar.rows[row - arb] = v; });
                     }
@@ -1182,51 +1247,49 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             if (!combine<HD>(a, x, ar, reinterpret_cast<float*>(tile), l, pos)) return;
             stamp(a, sl + 3);
             // gate / up rows stream while the Wo partials travel
-            if (dwb < dwe) {
-                tg.template load<FGU>(Ly.Wg, a.F, H, 0, UAn, dwb + zl);
-                tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, dwb + zl);
-            }
+            load_d(Ly, zl);
             pin();
             {
                 XRegs<FO, LC, UC> xr;
                 xr.load(ar.xs, ar.xsum, UCn);
                 for (int t0 = cwb; t0 < cwe; t0 += RC) {
-                    if (t0 != cwb) tc.template load<FO>(Ly.Wo, H, a.nq * HD, (x * slice_o) / 32, UCn, t0 + zl);
+                    if (t0 != cwb) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o, UCn, t0 + zl);
                     float o[NC];
                     tc.template dot<FO>(xr, UCn, o);
                     emit_rows<LC, NC>(t0, cwe, o, [&](int row, float v) { ar.rows[row - hb] = v; });
                 }
             }
             __syncthreads();
-            emit_words<true>(ar.rows, hb, he, a.wpart, a.pwo + (int64_t)x * a.part_stride + r * a.wpart + zl,
-                             tag_of(a, l, 2));
+            emit_partial(a, ar, a.pwo + zl, x, r, tag_of(a, l, 2));
         } else {
-            if (dwb < dwe) {
-                tg.template load<FGU>(Ly.Wg, a.F, H, 0, UAn, dwb + zl);
-                tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, dwb + zl);
-            }
+            load_d(Ly, zl);
             pin();
         }
         stamp(a, sl + 4);
-        // ---- D: residual, norm, gate / up rows of the slice
+        // ---- D: residual, norm, gate / up rows of the slice; the Wd block is
+        // requested between the passes
         {
             float ss = 0.f;
-            if (!gather_partials<16>(a, ar, a.pwo + zl, xmask_o, tag_of(a, l, 2), 3, ss)) return;
+            if (!reduce_block(a, ar, a.pwo + zl, xmask_o, x, r, tag_of(a, l, 2), 3, a.hupo + zl, tag_of(a, l, 5)))
+                return;
+            sub(a, l, 10);
+            if (!apply_update(a, ar, a.hupo + zl, x, tag_of(a, l, 5), 8, ss)) return;
             __syncthreads();
             norm_to_xs(ar, H, ss, Ly.post_ln, a.eps);
             stamp(a, sl + 5);
             // Wd rows stream while gate / up are computed and travel
-            load_e(Ly, ewb + zl);
+#pragma unroll
+            for (int p = 0; p < NE; ++p) load_e_pass(Ly, p, zl);
             pin();
             if (dwb < dwe) {
                 XRegs<FGU, LD, UD> xr;
                 xr.load(ar.xs, ar.xsum, UAn);
                 for (int t0 = dwb; t0 < dwe; t0 += RD) {
+                    float og[ND], ou[ND];
                     if (t0 != dwb) {
                         tg.template load<FGU>(Ly.Wg, a.F, H, 0, UAn, t0 + zl);
                         tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, t0 + zl);
                     }
-                    float og[ND], ou[ND];
                     tg.template dot<FGU>(xr, UAn, og);
                     tu.template dot<FGU>(xr, UAn, ou);
 #pragma unroll
@@ -1238,14 +1301,15 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     emit_rows<LD, ND>(t0, dwe, og, [&](int row, float v) { ar.rows[row - gb] = v; });
                 }
             }
+            sub(a, l, 12);
             __syncthreads();
-            if (Fx > 0)
-                emit_words<false>(ar.rows, gb, ge, a.wact, a.act + (int64_t)x * a.act_stride + r * a.wact + zl,
-                                  tag_of(a, l, 3));
+            emit_words<false>(ar.rows, gb, ge, a.wact, a.act + (int64_t)x * a.act_stride + r * a.wact + zl,
+                              tag_of(a, l, 3));
         }
         stamp(a, sl + 6);
-        // ---- E: the slice's SwiGLU output, Wd partial
-        if (Fx > 0) {
+        // ---- E: the slice's SwiGLU output, Wd partial; the next layer's q / k /
+        // v block is requested between the passes
+        {
             const int nw = kR * a.wact;
             const FastDivP dwa(a.wact);
             const bool ok = poll_vec<2, kLocal>(
@@ -1268,23 +1332,24 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                 XRegs<F, LE, UE> xr;
                 xr.load(ar.xs, ar.xsum, UEn);
                 for (int t0 = ewb; t0 < ewe; t0 += RE) {
-                    if (t0 != ewb) te.template load<F>(Ly.Wd, H, a.F, fb / 32, UEn, t0 + zl);
                     float o[NE];
+                    if (t0 != ewb) te.template load<F>(Ly.Wd, H, a.F, fb / 32, UEn, t0 + zl);
                     te.template dot<F>(xr, UEn, o);
                     emit_rows<LE, NE>(t0, ewe, o, [&](int row, float v) { ar.rows[row - hb] = v; });
                 }
             };
             if (Ly.type_down == FD) run(std::integral_constant<int, FD>{});
             else if constexpr (FD2 >= 0) run(std::integral_constant<int, FD2>{});
+            sub(a, l, 30);
             __syncthreads();
-            emit_words<true>(ar.rows, hb, he, a.wpart, a.pdn + (int64_t)x * a.part_stride + r * a.wpart + zl,
-                             tag_of(a, l, 4));
+            emit_partial(a, ar, a.pdn + zl, x, r, tag_of(a, l, 4));
         }
         // the next layer's attention tile and q / k / v rows stream while the
         // down partials travel
         if (l + 1 < a.L) {
-            tile_prefetch<HD>(a, w, lt[l + 1], pos, tile);
-            load_a(lt[l + 1], awb + zl);
+            tile_prefetch<HD>(a, w, Ln, pos, tile);
+#pragma unroll
+            for (int p = 0; p < NA; ++p) load_a_pass(Ln, p, zl);
         }
         pin();
         stamp(a, sl + 8);
@@ -1318,7 +1383,9 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         if (hwb < hwe) load(b0, hwb);
         pin();
         float ss = 0.f;
-        if (!gather_partials<16>(a, ar, a.pdn, xmask_d, tag_of(a, a.L - 1, 4), 5, ss)) return;
+        if (!reduce_block(a, ar, a.pdn, xmask_d, x, r, tag_of(a, a.L - 1, 4), 5, a.hupd, tag_of(a, a.L - 1, 6)))
+            return;
+        if (!apply_update(a, ar, a.hupd, x, tag_of(a, a.L - 1, 6), 9, ss)) return;
         __syncthreads();
         norm_to_xs(ar, H, ss, a.final_norm, a.eps);
         stamp(a, sh + 0);
@@ -1444,47 +1511,56 @@ using KFn = void (*)(Args);
 struct Entry {
     int fq, fv, fv2, fo, fgu, fd, fd2, fh, hd;
     int H, slice_o, fxmax;   // K of stages A / D / head, C, E
+    bool prefer;             // run this kernel even where the first one has an instantiation (measured faster)
     KFn fn;
 };
 
-#define P2(FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE, LH, UH, NH) \
+#define P2(PREF, FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE, LH, \
+           UH, NH)                                                                                                   \
     Entry {                                                                                                         \
-        FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX,                                                           \
+        FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, PREF,                                                     \
             persist2_kernel<FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE, \
                             LH, UH, NH>                                                                             \
     }
 
 constexpr int Q4 = FMT_Q4_K, Q6 = FMT_Q6_K, Q8 = FMT_Q8_0, F16 = FMT_F16;
 
-// Shapes with an instantiation: the BASELINE widths and the test models.
+// Shapes with an instantiation: the BASELINE widths and the test models.  The
+// first argument says whether a shape runs here even where the first
+// persistent kernel has an instantiation: measured on MI355X (decode steps at
+// a 1024-token context), this kernel takes 0.80 ms at the 0.6B Q8_0 widths
+// against 0.97 ms there, but 1.07 / 2.69 / 2.62 ms at the 1.7B / 8B /
+// Llama-3-8B widths against 1.04 / 2.58 / 2.51 ms.
 // Per stage (lanes per row, units per lane, passes): a wave's first task is
 // requested one stage ahead; rows past it load in place.
 const Entry kTable[] = {
-    // Qwen3-1.7B (H 2048, F 6144, 16 / 8 heads): Q4_K with Q6_K or Q4_K v / down,
-    // untied Q6_K head or the tied FP16 head of the real Q4_K_M files
-    P2(Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 8),
-    P2(Q4, Q6, Q4, Q4, Q4, Q6, Q4, F16, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 4),
+    // Qwen3-1.7B (H 2048, F 6144, 16 / 8 heads): Q4_K with Q6_K v / down and an
+    // untied Q6_K head; the same with v / down Q6_K or
+    // Q4_K per layer and the tied FP16 head (the real Q4_K_M files)
+    P2(false, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 8),
+    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, F16, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 4),
     // Qwen3-0.6B (H 1024, F 3072): Q8_0 with the tied FP16 head
-    P2(Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1, 4),
+    P2(true, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1, 4),
     // Qwen3-8B (H 4096, F 12288, 32 / 8 heads): Q4_K, Q6_K head
-    P2(Q4, Q4, Q6, Q4, Q4, Q4, Q6, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2, 4),
+    P2(false, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2, 4),
     // Llama-3-8B widths (H 4096, F 14336): Q4_K with Q6_K v / down and head
-    P2(Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64, 2, 4),
-    // test models: H 256 / F 768 / head_dim 64 (Q4_K, Q6_K v / down / head)
-    P2(Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 64, 256, 256, 256, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1),
+    P2(false, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64, 2, 4),
+    // test models: H 256 / head_dim 64 with F 2048 (Q4_K, Q6_K or Q4_K v / down, Q6_K head)
+    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 64, 256, 256, 256, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1),
     // H 512 / F 1024 / head_dim 64, Q8_0, tied FP16 head
-    P2(Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 64, 512, 128, 128, 16, 1, 1, 4, 1, 1, 16, 1, 1, 4, 1, 1, 16, 1, 1),
+    P2(true, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 64, 512, 128, 128, 16, 1, 1, 4, 1, 1, 16, 1, 1, 4, 1, 1, 16, 1, 1),
     // H 256 / F 6144 / head_dim 128, one KV head (Mistral-shaped, Q4_K / Q6_K)
-    P2(Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 256, 512, 768, 8, 1, 1, 16, 1, 1, 8, 1, 1, 8, 3, 1, 8, 1, 1),
+    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 256, 512, 768, 8, 1, 1, 16, 1, 1, 8, 1, 1, 8, 3, 1, 8, 1, 1),
 };
 
 struct Plan {
     KFn fn = nullptr;
     int gpu = 0, nu = 0, aq = 0, ak = 0, av = 0, wq = 0, wk = 0, wv = 0, wqkv = 0, smax = 0, rec = 0, fblk = 0,
         wact = 0, wpart = 0;
-    int qkv_stride = 0, rec_stride = 0, act_stride = 0, part_stride = 0;
-    size_t ctrl = 0, qkv = 0, recw = 0, act = 0, pwo = 0, pdn = 0, cand = 0, total = 0;
+    int qkv_stride = 0, rec_stride = 0, act_stride = 0, part_stride = 0, hup_stride = 0;
+    size_t ctrl = 0, qkv = 0, recw = 0, act = 0, pwo = 0, pdn = 0, hupo = 0, hupd = 0, cand = 0, total = 0;
     size_t lds_dyn = 0;   // without the layer table
+    bool prefer = false;
 };
 
 int type_elems(int t) { return t == BX_TYPE_Q8_0 ? 32 : (t == BX_TYPE_Q4_K || t == BX_TYPE_Q6_K ? 256 : 0); }
@@ -1513,6 +1589,10 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     const int fblk = std::max(type_elems(d.down_type), type_elems(d.down_alt_type));
     if (fblk == 0 || F % fblk || H % 256) return fail(BX_EUNSUPPORTED, "persist2: widths");
     const int nbF = F / fblk, fxmax = (nbF + kX - 1) / kX * fblk;
+    // Every XCD holds an FFN slice: its E stage then waits for all 32 of its
+    // workgroups' D stages, which is what keeps an owner from overwriting an
+    // h-update word (next layer) before a slow reader of its XCD has read it.
+    if (nbF < kX) return fail(BX_EUNSUPPORTED, "persist2: FFN narrower than one block per XCD");
     const int slice_o = gpu * Gq * hd;
     const Entry* ent = nullptr;
     for (const Entry& e : kTable) {
@@ -1528,6 +1608,7 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     }
     if (!ent) return fail(BX_EUNSUPPORTED, "persist2: no instantiation for this format mix / width");
     o.fn = ent->fn;
+    o.prefer = ent->prefer;
     o.gpu = gpu;
     o.nu = nu;
     o.smax = smax;
@@ -1578,7 +1659,8 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     o.qkv_stride = (int)up(o.wqkv);
     o.rec_stride = (int)up((size_t)gpu * smax * Gq * o.rec);
     o.act_stride = (int)up((size_t)kR * o.wact);
-    o.part_stride = (int)up((size_t)kR * o.wpart);
+    o.part_stride = (int)up((size_t)H);
+    o.hup_stride = (int)up((size_t)kR * o.wpart);
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t at = off;
@@ -1591,6 +1673,8 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     o.act = take((size_t)kX * o.act_stride * 8);
     o.pwo = take((size_t)kX * o.part_stride * 8);
     o.pdn = take((size_t)kX * o.part_stride * 8);
+    o.hupo = take((size_t)kX * o.hup_stride * 8);
+    o.hupd = take((size_t)kX * o.hup_stride * 8);
     o.cand = take((size_t)2 * kG * 8);
     o.total = off;
     const int kmax = kmax_of(H, fxmax, slice_o);
@@ -1608,16 +1692,16 @@ __global__ void ws_init_kernel(uint32_t* ctrl, uint64_t* words, size_t nwords) {
     for (size_t j = i; j < nwords; j += (size_t)gridDim.x * blockDim.x) words[j] = ~0ull;
 }
 
-// Which persistent kernel runs a shape: this one where the first kernel has
-// no instantiation (per-layer attn_v / ffn_down formats, a tied FP16 head
-// over Q4_K layers) or when BROLM_PERSIST_V2 is set; BROLM_PERSIST_V1 forces
-// the first kernel.
+// Which persistent kernel runs a shape: this one where its entry prefers it
+// or the first kernel has no instantiation (per-layer attn_v / ffn_down
+// formats, a tied FP16 head over Q4_K layers); BROLM_PERSIST_V1 /
+// BROLM_PERSIST_V2 force one of the two.
 bool use_p2(const bx_decode_dims* d, Plan& o) {
     static const bool v1 = std::getenv("BROLM_PERSIST_V1") != nullptr;
     static const bool v2 = std::getenv("BROLM_PERSIST_V2") != nullptr;
     if (v1 || !d) return false;
     if (plan_of(*d, o) != BX_OK) return false;
-    if (v2) return true;
+    if (v2 || o.prefer) return true;
     const std::string err = bx_last_error();
     const bool p1_ok = p1_ws_bytes(d) != 0;
     set_error(err);
@@ -1673,9 +1757,12 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
     a.act = reinterpret_cast<uint64_t*>(base + o.act);
     a.pwo = reinterpret_cast<uint64_t*>(base + o.pwo);
     a.pdn = reinterpret_cast<uint64_t*>(base + o.pdn);
+    a.hupo = reinterpret_cast<uint64_t*>(base + o.hupo);
+    a.hupd = reinterpret_cast<uint64_t*>(base + o.hupd);
     a.cand = reinterpret_cast<uint64_t*>(base + o.cand);
     a.qkv_stride = o.qkv_stride; a.rec_stride = o.rec_stride; a.act_stride = o.act_stride;
     a.part_stride = o.part_stride;
+    a.hup_stride = o.hup_stride;
     a.trace = g_trace;
     const size_t lds = o.lds_dyn + table_bytes(n_layers);
     hipFuncAttributes attr{};

@@ -210,3 +210,49 @@ def test_cache_beyond_fused_step_uses_op_path(ba, small_gguf):
         assert margins[k] <= 2 * LOGIT_TOL
     assert m.cache_len() == len(prompt) + 7
     m.close()
+
+
+@pytest.mark.timeout(900)
+def test_q4k_m_real_layout_1p7b_widths_persistent_vs_oracle(ba, tmp_path_factory):
+    """The layout of a real Qwen3-1.7B-Q4_K_M file at its widths: tied Q6_K
+    token_embd (the lm_head is the FP16 clone of the dequantized embedding,
+    src/detail/dense_decoder.cpp:180-191, include/brolm/detail/weights.h:
+    325-339), Q4_K q / k / o / gate / up, attn_v and ffn_down Q6_K on
+    llama.cpp's use_more_bits layers (0, 3, 6, 7 of 8) and Q4_K elsewhere,
+    each dispatched on its own type (include/brolm/detail/compute.h:54-86).
+    Single-token steps run the fused persistent kernel."""
+    spec = dict(vocab=151936, hidden=2048, intermediate=6144, layers=8, n_q=16, n_kv=8, head_dim=128, tied=True,
+                embed="Q6_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K", up="Q4_K", down="Q4_K",
+                output="Q6_K", more_bits="Q6_K", seed=31)
+    path = write_synth(tmp_path_factory.mktemp("q4km17"), spec, "q4km17")
+    assert _tensor_type(path, "token_embd.weight") == 14
+    q6 = [l for l in range(8) if _tensor_type(path, f"blk.{l}.attn_v.weight") == 14]
+    assert q6 == [0, 3, 6, 7]
+    assert [l for l in range(8) if _tensor_type(path, f"blk.{l}.ffn_down.weight") == 14] == q6
+    m = _load(ba, path, cap=256)
+    assert m.decode_mode() == "persistent"
+    om = oracle.Model(str(path))
+    om.allocate_cache(256)
+    prompt = ba.prompt_ids(40, 151936, seed=42)
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    print(f"[configs] Q4_K_M layout prefill max diff {np.abs(a - b).max():.3e}", flush=True)
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    worst = 0.0
+    for _ in range(12):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        worst = max(worst, float(np.abs(a - b).max()))
+        tok = int(b.argmax())
+    print(f"[configs] Q4_K_M layout persistent steps max diff {worst:.3e}", flush=True)
+    assert worst <= LOGIT_TOL
+    want, margins = oracle.Model(str(path)).generate_greedy(prompt[:16], 24)
+    m.reset_cache()
+    first = int(m.forward_last(prompt[:16]).argmax())
+    got = [first] + m.decode_greedy(first, 23)
+    k = _first_difference(got, want)
+    print(f"[configs] Q4_K_M layout: {k} of 24 greedy tokens identical", flush=True)
+    if k < len(want):
+        assert margins[k] <= 2 * LOGIT_TOL
+    m.close()
