@@ -73,7 +73,7 @@ HIP_SYMBOLS = {
     "bx_carrier_bytes": (i64, [C.c_int, i64, i64]),
     "bx_dequant_to_f16": (C.c_int, [C.c_int, vp, vp, i64, i64, vp]),
     "bx_dequant_to_f32": (C.c_int, [C.c_int, vp, vp, i64, i64, vp]),
-    "bx_linear_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "bx_linear_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_size_t, vp]),
     "bx_embedding_f16": (C.c_int, [vp, C.c_int, C.c_int, vp, C.c_int, vp, vp]),
     "bx_embedding_f32": (C.c_int, [vp, C.c_int, C.c_int, vp, C.c_int, vp, vp]),
     "bx_rms_norm": (C.c_int, [vp, C.c_int, vp, f32, vp, C.c_int, C.c_int, vp]),
@@ -110,29 +110,31 @@ HIP_SYMBOLS = {
     "bx_argmax_f16": (C.c_int, [vp, i64, vp, vp, vp]),
     "bx_argmax_f16_noalloc": (C.c_int, [vp, i64, vp, vp]),
     "bx_linear_tiles_ok": (C.c_int, [C.c_int, C.c_int]),
+    "bx_linear_workspace_bytes": (C.c_size_t, []),
+    "bx_linear_workspace_init": (C.c_int, [vp, C.c_size_t, vp]),
     "bx_attention_varlen_f16": (C.c_int, [vp, vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp,
                                           vp]),
     "bx_sample_feed_f16": (C.c_int, [vp, C.c_int, C.c_float, C.c_int, C.c_float, vp, vp, vp, vp, vp, vp]),
     "bx_rope_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp, vp, C.c_int, vp]),
     "bx_kv_append_rows_f16": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp, vp, i64, vp]),
     "bx_linear_ss_floats": (C.c_size_t, [C.c_int]),
-    "bx_linear_residual_ss_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "bx_linear_residual_ss_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_size_t, vp]),
     "bx_linear_group_norm_f16": (C.c_int, [C.c_int, C.c_int, vp, vp, vp, vp, vp, C.c_float, vp, C.c_int, C.c_int,
-                                           vp]),
+                                           vp, C.c_size_t, vp]),
     "bx_linear_swiglu_norm_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_float, vp, vp, C.c_int, C.c_int, C.c_int,
-                                            vp]),
-    "bx_linear_group2_f16": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, vp]),
+                                            vp, C.c_size_t, vp]),
+    "bx_linear_group2_f16": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, vp, C.c_size_t, vp]),
     "bx_linear_group2_norm_f16": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, vp, vp, vp, C.c_float, vp,
-                                            C.c_int, C.c_int, vp]),
+                                            C.c_int, C.c_int, vp, C.c_size_t, vp]),
     "bx_batch_attention_workspace_bytes": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "bx_batch_attention_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
                                          C.c_int, vp, vp, C.c_int, vp, vp, i64, vp, vp, vp]),
     "bx_qk_rope_kv_rows_f16": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, vp, C.c_float, vp, vp,
                                          vp, C.c_int, vp, vp, vp, i64, vp, vp]),
     "bx_linear_group_f16": (C.c_int, [C.c_int, C.c_int, C.POINTER(vp), C.POINTER(vp), C.POINTER(C.c_int), vp, C.c_int,
-                                      C.c_int, vp]),
-    "bx_linear_residual_f16": (C.c_int, [C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
-    "bx_linear_swiglu_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+                                      C.c_int, vp, C.c_size_t, vp]),
+    "bx_linear_residual_f16": (C.c_int, [C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_size_t, vp]),
+    "bx_linear_swiglu_f16": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp, C.c_size_t, vp]),
 }
 
 # every symbol of include/brolm_c.h

@@ -1144,6 +1144,8 @@ void DenseDecoder::enqueue_batch_(int M) {
     const int width = n_kv * HD;
     const float eps = cfg_.rms_norm_eps;
     void* st = bt::stream();
+    void* const lws = hipx::linear_ws();
+    const size_t lwsb = hipx::linear_ws_bytes();
     bh_.resize(M, cfg_.hidden_size, bt::Dtype::FP32);
     battn_.resize(M, n_q * HD, bt::Dtype::FP16);
     hipx::bx(bx_embedding_f32(static_cast<const uint16_t*>(embed_tokens_.data), embed_tokens_.rows,
@@ -1183,7 +1185,7 @@ void DenseDecoder::enqueue_batch_(int M) {
         }
         return !unsupported(bx_linear_group_norm_f16(bt::dtype_to_ggml(w[0]->dtype), n, W, Y, N, hf,
                                                      static_cast<const uint16_t*>(gain.data), eps, ss, M,
-                                                     cfg_.hidden_size, st),
+                                                     cfg_.hidden_size, lws, lwsb, st),
                             "forward_batch q / k / v with the norm");
     };
     // q and k of one weight type and v of another (Q4_K and Q6_K) in one
@@ -1203,16 +1205,16 @@ void DenseDecoder::enqueue_batch_(int M) {
         const int t1 = bt::dtype_to_ggml(w[0]->dtype), t2 = bt::dtype_to_ggml(w[2]->dtype);
         const int rc = with_norm ? bx_linear_group2_norm_f16(t1, t2, 3, 2, W, Y, N, hf,
                                                              static_cast<const uint16_t*>(gain.data), eps, ss, M,
-                                                             cfg_.hidden_size, st)
+                                                             cfg_.hidden_size, lws, lwsb, st)
                                  : bx_linear_group2_f16(t1, t2, 3, 2, W, Y, N,
                                                         static_cast<const uint16_t*>(bnorm_.data), M,
-                                                        cfg_.hidden_size, st);
+                                                        cfg_.hidden_size, lws, lwsb, st);
         return !unsupported(rc, "forward_batch q / k / v");
     };
     auto residual = [&](const bt::Tensor& W, const bt::Tensor& X) {
         const int rc = bx_linear_residual_ss_f16(bt::dtype_to_ggml(W.dtype), W.data,
                                                  static_cast<const uint16_t*>(X.data), static_cast<float*>(bh_.data),
-                                                 ss, M, W.rows, W.cols, st);
+                                                 ss, M, W.rows, W.cols, lws, lwsb, st);
         have_ss = rc == BX_OK;
         if (have_ss || !unsupported(rc, "forward_batch residual projection")) return;
         if (!bt::linear_residual_forward_batched(W, X, bh_)) {
@@ -1263,7 +1265,7 @@ void DenseDecoder::enqueue_batch_(int M) {
                                                          layer.up_W.data, hf,
                                                          static_cast<const uint16_t*>(layer.post_attn_ln.data), eps,
                                                          ss, static_cast<uint16_t*>(bgate_.data), M, layer.gate_W.rows,
-                                                         layer.gate_W.cols, st),
+                                                         layer.gate_W.cols, lws, lwsb, st),
                                "forward_batch gate / up with the norm");
         }
         if (!mlp) {

@@ -22,6 +22,9 @@ inline void bx(int rc, const char* what) {
 
 hipStream_t stream();
 void sync();
+// The linear entry points' workspace for the op stream (bx_linear_workspace_bytes).
+void* linear_ws();
+std::size_t linear_ws_bytes();
 // Stream-ordered copies; the host side waits (synchronous semantics).
 void h2d(void* dst, const void* src, std::size_t n);
 void d2h(void* dst, const void* src, std::size_t n);

@@ -164,12 +164,14 @@ void linear_impl(const char* op, Dtype expect, const Tensor& W, const Tensor* bi
         const void* wf[1];
         dequant_weights(w, 1, wf);
         hipx::bx(bx_linear_f16(BX_TYPE_F16, wf[0], b, static_cast<const uint16_t*>(X.data),
-                               static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::stream()),
+                               static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::linear_ws(),
+                               hipx::linear_ws_bytes(), hipx::stream()),
                  op);
         return;
     }
     hipx::bx(bx_linear_f16(dtype_to_ggml(W.dtype), W.data, b, static_cast<const uint16_t*>(X.data),
-                           static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::stream()),
+                           static_cast<uint16_t*>(Y.data), X.rows, W.rows, W.cols, hipx::linear_ws(),
+                           hipx::linear_ws_bytes(), hipx::stream()),
              op);
 }
 
@@ -229,7 +231,7 @@ bool linear_group_forward_batched(const Tensor* const* W, Tensor* const* Y, int 
         wtype = BX_TYPE_F16;
     }
     hipx::bx(bx_linear_group_f16(wtype, n, w, y, N, static_cast<const uint16_t*>(X.data), X.rows, X.cols,
-                                 hipx::stream()),
+                                 hipx::linear_ws(), hipx::linear_ws_bytes(), hipx::stream()),
              "linear_group_forward_batched");
     return true;
 }
@@ -248,7 +250,7 @@ bool linear_residual_forward_batched(const Tensor& W, const Tensor& X, Tensor& H
         wtype = BX_TYPE_F16;
     }
     hipx::bx(bx_linear_residual_f16(wtype, w, static_cast<const uint16_t*>(X.data), static_cast<float*>(H.data), X.rows,
-                                    W.rows, W.cols, hipx::stream()),
+                                    W.rows, W.cols, hipx::linear_ws(), hipx::linear_ws_bytes(), hipx::stream()),
              "linear_residual_forward_batched");
     return true;
 }
@@ -267,7 +269,8 @@ bool linear_swiglu_forward_batched(const Tensor& Wg, const Tensor& Wu, const Ten
         wtype = BX_TYPE_F16;
     }
     hipx::bx(bx_linear_swiglu_f16(wtype, w[0], w[1], static_cast<const uint16_t*>(X.data),
-                                  static_cast<uint16_t*>(Y.data), X.rows, Wg.rows, Wg.cols, hipx::stream()),
+                                  static_cast<uint16_t*>(Y.data), X.rows, Wg.rows, Wg.cols, hipx::linear_ws(),
+                                  hipx::linear_ws_bytes(), hipx::stream()),
              "linear_swiglu_forward_batched");
     return true;
 }

@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include "brolm_hip.h"
 #include "hip_util.h"
 
 namespace {
@@ -17,6 +18,8 @@ struct RuntimeState {
     bool ready = false;
     int device = 0;
     hipStream_t stream = nullptr;
+    void* linear_ws = nullptr;           // the linear entry points' workspace, for the op stream
+    std::size_t linear_ws_bytes = 0;
     std::vector<void (*)()> releases;   // on_shutdown hooks, registration order
 };
 
@@ -40,6 +43,12 @@ hipStream_t stream() {
 }
 
 void sync() { check(hipStreamSynchronize(stream()), "hipStreamSynchronize"); }
+
+void* linear_ws() {
+    if (!state().ready) throw std::runtime_error("brotensor: init() has not been called");
+    return state().linear_ws;
+}
+std::size_t linear_ws_bytes() { return state().linear_ws_bytes; }
 
 void h2d(void* dst, const void* src, std::size_t n) {
     if (n == 0) return;
@@ -78,8 +87,18 @@ void init() {
     hipx::check(hipSetDevice(chosen), "hipSetDevice");
     hipStream_t st = nullptr;
     hipx::check(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+    // the op stream's linear workspace (split-K partials and counters of the
+    // decode-batch GEMVs), taken here once so no op allocates under graph
+    // capture
+    const std::size_t wsb = bx_linear_workspace_bytes();
+    void* ws = nullptr;
+    hipx::check(hipMalloc(&ws, wsb), "hipMalloc linear workspace");
+    hipx::bx(bx_linear_workspace_init(ws, wsb, st), "linear workspace init");
+    hipx::check(hipStreamSynchronize(st), "hipStreamSynchronize");
     s.device = chosen;
     s.stream = st;
+    s.linear_ws = ws;
+    s.linear_ws_bytes = wsb;
     s.ready = true;
 }
 
@@ -117,6 +136,9 @@ void shutdown() {
     std::lock_guard<std::mutex> lk(init_mutex());
     RuntimeState& s = state();
     (void)hipStreamSynchronize(s.stream);
+    if (s.linear_ws) (void)hipFree(s.linear_ws);
+    s.linear_ws = nullptr;
+    s.linear_ws_bytes = 0;
     (void)hipStreamDestroy(s.stream);
     s.stream = nullptr;
     s.ready = false;

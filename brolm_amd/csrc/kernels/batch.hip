@@ -178,7 +178,8 @@ struct BatchAttnArgs {
     int64_t cache_rows;
     int n_q, n_kv, S, kps, P, HPW;
     float* recs;       // (row, group) x S x G records of HD + 2 floats
-    uint32_t* cnt;     // rows x n_kv counters, zero between launches
+    uint64_t* cnt;     // rows x n_kv counter words {tag, arrivals}, zero between launches
+    uint32_t tag;      // this launch's tag (nonzero)
     uint16_t* out;     // rows x n_q HD
 };
 
@@ -425,10 +426,19 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    uint32_t* cn = a.cnt + (int64_t)r * a.n_kv + g;
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(cn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1) ? 1u
-                                                                                                               : 0u;
+    // {tag, arrivals}: a word left by another launch (one that did not
+    // finish) counts as zero arrivals; the last arrival clears the word
+    uint64_t* cn = a.cnt + (int64_t)r * a.n_kv + g;
+    if (threadIdx.x == 0) {
+        uint64_t old = __hip_atomic_load(cn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t nw;
+        do {
+            const uint32_t n = (uint32_t)(old >> 32) == a.tag ? (uint32_t)old + 1u : 1u;
+            nw = ((uint64_t)a.tag << 32) | n;
+        } while (!__hip_atomic_compare_exchange_weak(cn, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+        last = (uint32_t)nw == (uint32_t)a.S ? 1u : 0u;
+    }
     __syncthreads();
     if (!last) return;
 
@@ -487,7 +497,7 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
 #pragma unroll
         for (int i = 0; i < EPL; ++i) op[i] = f2h(acc[i] * inv);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(cn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(cn, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Split plan of the batched attention: about two workgroups per CU over all
@@ -542,7 +552,7 @@ int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int co
 size_t bx_batch_attention_workspace_bytes(int rows, int n_q, int n_kv, int hd, int max_len) {
     if (rows <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv || hd <= 0 || max_len <= 0) return 0;
     const BaPlan p = ba_plan(rows, n_q, n_kv, max_len);
-    const size_t cnt = ((size_t)rows * n_kv * 4 + 255) / 256 * 256;
+    const size_t cnt = ((size_t)rows * n_kv * 8 + 255) / 256 * 256;
     return cnt + (size_t)rows * n_q * p.S * (hd + 2) * sizeof(float);
 }
 
@@ -557,7 +567,7 @@ int bx_batch_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t*
         return fail(BX_EINVAL, "batch_attention: bad arguments");
     if (n_q / n_kv > 8) return fail(BX_EUNSUPPORTED, "batch_attention: at most 8 query heads per KV head");
     const BaPlan p = ba_plan(rows, n_q, n_kv, max_len);
-    const size_t cnt = ((size_t)rows * n_kv * 4 + 255) / 256 * 256;
+    const size_t cnt = ((size_t)rows * n_kv * 8 + 255) / 256 * 256;
     if ((size_t)rows * n_q * p.S * (hd + 2) * sizeof(float) >= (size_t)1 << 31)
         return fail(BX_EUNSUPPORTED, "batch_attention: records beyond 2 GiB");
     BatchAttnArgs a{};
@@ -567,7 +577,8 @@ int bx_batch_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t*
     a.cos_t = cos_tab; a.sin_t = sin_tab; a.tab_rows = tab_rows;
     a.Kc = Kc; a.Vc = Vc; a.cache_rows = cache_rows;
     a.n_q = n_q; a.n_kv = n_kv; a.S = p.S; a.kps = p.kps; a.P = p.P; a.HPW = p.HPW;
-    a.cnt = static_cast<uint32_t*>(workspace);
+    a.cnt = static_cast<uint64_t*>(workspace);
+    a.tag = next_launch_tag();
     a.recs = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + cnt);
     a.out = out;
     const dim3 grid((unsigned)p.S, (unsigned)n_kv, (unsigned)rows);

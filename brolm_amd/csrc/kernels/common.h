@@ -27,6 +27,11 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 int num_cus();
 // true when a rocprofiler-sdk tool (rocprofv3) is loaded into the process
 bool profiler_attached();
+
+// A new nonzero 32-bit tag per call (1, 2, ..., wrapping past 0), for
+// kernels whose workgroups count arrivals in caller memory: a counter word
+// carrying another launch's tag is treated as empty.
+uint32_t next_launch_tag();
 // Workgroups of `threads` threads and `lds` dynamic LDS bytes that one CU
 // holds at once for kernel `fn` (registers and LDS); asked of the runtime once
 // per (kernel, threads, LDS) and cached; at least 1.

@@ -19,27 +19,27 @@ int gemm_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X
 int gemm_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              hipStream_t st);
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-              hipStream_t st);
+              void* ws, size_t wsb, hipStream_t st);
 // One-row GEMV with K split over a workgroup's wavefronts (K 24576 or 32768):
 // FP16 out (+ bias), or with h non-null added into the FP32 residual h.
 int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, float* h, int N,
                    int K, hipStream_t st);
 int gemv_mfma_split(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-                    hipStream_t st);
+                    void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
-                    int M, int K, hipStream_t st);
-int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st);
+                    int M, int K, void* ws, size_t wsb, hipStream_t st);
+int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
-                     hipStream_t st);
+                     void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_resid_ss(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N, int K,
-                       hipStream_t st);
+                       void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
-                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, hipStream_t st);
+                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,
-                          const float* ss_in, uint16_t* Y, int M, int F, int K, hipStream_t st);
+                          const float* ss_in, uint16_t* Y, int M, int F, int K, void* ws, size_t wsb, hipStream_t st);
 int gemv_mfma_group2(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
                      const uint16_t* X, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
-                     int K, hipStream_t st);
+                     int K, void* ws, size_t wsb, hipStream_t st);
 
 // The fused linear forms run on the MFMA tile GEMM (M >= 128, K % 64 == 0)
 // and, for decode batches, on the MFMA GEMV (3 <= M <= 16, K % 256 == 0).
@@ -304,7 +304,7 @@ int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* 
 }
 
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-             hipStream_t st) {
+             void* ws, size_t wsb, hipStream_t st) {
     if (M == 1 && upl_for(K) <= 16) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
     // measured crossover (GEMV sweep): the per-row kernel is one launch at
     // M = 2 and 4 and faster there, except Q4_K at 4 with N >= 4096; Q8_0
@@ -312,7 +312,7 @@ int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
     const bool small_q8 = wtype == BX_TYPE_Q8_0 && M < 16 && (int64_t)N * K < (8 << 20);
     const bool mfma = K % 256 == 0 && M >= 3 && (M != 4 || (wtype == BX_TYPE_Q4_K && N >= 4096)) &&
                       !(small_q8 && (M == 8 || M <= 4));
-    if (mfma) return gemv_mfma(wtype, W, bias, X, Y, M, N, K, st);
+    if (mfma) return gemv_mfma(wtype, W, bias, X, Y, M, N, K, ws, wsb, st);
     switch (wtype) {
         case BX_TYPE_Q4_K: return gemv_dispatch<FMT_Q4_K>(M, W, X, bias, Y, N, K, st);
         case BX_TYPE_Q6_K: return gemv_dispatch<FMT_Q6_K>(M, W, X, bias, Y, N, K, st);
@@ -325,16 +325,16 @@ int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
 }  // namespace bx
 
 extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M,
-                             int N, int K, void* stream) {
+                             int N, int K, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
     if (!W || !X || !Y) return bx::fail(BX_EINVAL, "linear: null pointer");
     hipStream_t st = bx::as_stream(stream);
     // K beyond 12288 (an FFN width such as 32768) at 2..16 rows: the per-row
     // kernels' staged activations outgrow LDS; the split MFMA GEMV stages only
     // a K slice (3..16 rows, shapes it takes), else the tiled GEMM
-    if (M == 1 || (M <= 16 && K <= 12288)) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, st);
+    if (M == 1 || (M <= 16 && K <= 12288)) return bx::gemv_f16(wtype, W, bias, X, Y, M, N, K, ws, ws_bytes, st);
     if (bx::fused_gemv_ok(M, K)) {
-        const int rc = bx::gemv_mfma_split(wtype, W, bias, X, Y, M, N, K, st);
+        const int rc = bx::gemv_mfma_split(wtype, W, bias, X, Y, M, N, K, ws, ws_bytes, st);
         if (rc != BX_EUNSUPPORTED) return rc;
     }
     return bx::gemm_f16(wtype, W, bias, X, Y, M, N, K, st);
@@ -343,33 +343,35 @@ extern "C" int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, con
 extern "C" int bx_linear_tiles_ok(int M, int K) { return (bx::gemm_tiles_ok(M, K) || bx::fused_gemv_ok(M, K)) ? 1 : 0; }
 
 extern "C" int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N,
-                                   const uint16_t* X, int M, int K, void* stream) {
+                                   const uint16_t* X, int M, int K, void* ws, size_t ws_bytes, void* stream) {
     if (n < 1 || n > 3 || !W || !Y || !N || !X) return bx::fail(BX_EINVAL, "linear_group: bad arguments");
     for (int i = 0; i < n; ++i) {
         if (int rc = bx::check_linear_shape(wtype, M, N[i], K)) return rc;
         if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group: null pointer");
     }
-    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_group(wtype, n, W, Y, N, X, M, K, bx::as_stream(stream));
+    if (bx::fused_gemv_ok(M, K))
+        return bx::gemv_mfma_group(wtype, n, W, Y, N, X, M, K, ws, ws_bytes, bx::as_stream(stream));
     if (!bx::gemm_tiles_ok(M, K))
         return bx::fail(BX_EUNSUPPORTED, "linear_group: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_group_f16(wtype, n, W, Y, N, X, M, K, bx::as_stream(stream));
 }
 
 extern "C" int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K,
-                                      void* stream) {
+                                      void* ws, size_t ws_bytes, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
     if (!W || !X || !H) return bx::fail(BX_EINVAL, "linear_residual: null pointer");
-    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_resid(wtype, W, X, H, M, N, K, bx::as_stream(stream));
+    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_resid(wtype, W, X, H, M, N, K, ws, ws_bytes, bx::as_stream(stream));
     if (!bx::gemm_tiles_ok(M, K))
         return bx::fail(BX_EUNSUPPORTED, "linear_residual: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_resid_f16(wtype, W, X, H, M, N, K, bx::as_stream(stream));
 }
 
 extern "C" int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M,
-                                    int F, int K, void* stream) {
+                                    int F, int K, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, F, K)) return rc;
     if (!Wg || !Wu || !X || !Y) return bx::fail(BX_EINVAL, "linear_swiglu: null pointer");
-    if (bx::fused_gemv_ok(M, K)) return bx::gemv_mfma_swiglu(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
+    if (bx::fused_gemv_ok(M, K))
+        return bx::gemv_mfma_swiglu(wtype, Wg, Wu, X, Y, M, F, K, ws, ws_bytes, bx::as_stream(stream));
     if (!bx::gemm_tiles_ok(M, K))
         return bx::fail(BX_EUNSUPPORTED, "linear_swiglu: needs 3 <= M <= 16 with K % 256 == 0, or M >= 128 with K % 64 == 0");
     return bx::gemm_swiglu_f16(wtype, Wg, Wu, X, Y, M, F, K, bx::as_stream(stream));
@@ -381,16 +383,16 @@ extern "C" int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, c
 extern "C" size_t bx_linear_ss_floats(int N) { return N > 0 ? (size_t)(N + 63) / 64 * 16 : 0; }
 
 extern "C" int bx_linear_residual_ss_f16(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M,
-                                         int N, int K, void* stream) {
+                                         int N, int K, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, N, K)) return rc;
     if (!W || !X || !H || !ss_out) return bx::fail(BX_EINVAL, "linear_residual_ss: null pointer");
     if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_residual_ss: needs 3 <= M <= 16, K % 256 == 0");
-    return bx::gemv_mfma_resid_ss(wtype, W, X, H, ss_out, M, N, K, bx::as_stream(stream));
+    return bx::gemv_mfma_resid_ss(wtype, W, X, H, ss_out, M, N, K, ws, ws_bytes, bx::as_stream(stream));
 }
 
 extern "C" int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N,
                                         const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
-                                        int K, void* stream) {
+                                        int K, void* ws, size_t ws_bytes, void* stream) {
     if (n < 1 || n > 3 || !W || !Y || !N || !H || !gamma || !ss_in)
         return bx::fail(BX_EINVAL, "linear_group_norm: bad arguments");
     for (int i = 0; i < n; ++i) {
@@ -398,16 +400,18 @@ extern "C" int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, 
         if (!W[i] || !Y[i]) return bx::fail(BX_EINVAL, "linear_group_norm: null pointer");
     }
     if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_group_norm: needs 3 <= M <= 16, K % 256 == 0");
-    return bx::gemv_mfma_group_norm(wtype, n, W, Y, N, H, gamma, eps, ss_in, M, K, bx::as_stream(stream));
+    return bx::gemv_mfma_group_norm(wtype, n, W, Y, N, H, gamma, eps, ss_in, M, K, ws, ws_bytes,
+                                    bx::as_stream(stream));
 }
 
 extern "C" int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const float* H,
                                          const uint16_t* gamma, float eps, const float* ss_in, uint16_t* Y, int M,
-                                         int F, int K, void* stream) {
+                                         int F, int K, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = bx::check_linear_shape(wtype, M, F, K)) return rc;
     if (!Wg || !Wu || !H || !gamma || !ss_in || !Y) return bx::fail(BX_EINVAL, "linear_swiglu_norm: null pointer");
     if (!bx::fused_gemv_ok(M, K)) return bx::fail(BX_EUNSUPPORTED, "linear_swiglu_norm: needs 3 <= M <= 16, K % 256 == 0");
-    return bx::gemv_mfma_swiglu_norm(wtype, Wg, Wu, H, gamma, eps, ss_in, Y, M, F, K, bx::as_stream(stream));
+    return bx::gemv_mfma_swiglu_norm(wtype, Wg, Wu, H, gamma, eps, ss_in, Y, M, F, K, ws, ws_bytes,
+                                     bx::as_stream(stream));
 }
 
 // q / k / v in one launch when v's weight type differs (members [0, n1) of
@@ -425,18 +429,19 @@ static int group2_checks(int wtype, int wtype2, int n, int n1, const void* const
 }
 
 extern "C" int bx_linear_group2_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
-                                    const int* N, const uint16_t* X, int M, int K, void* stream) {
+                                    const int* N, const uint16_t* X, int M, int K, void* ws, size_t ws_bytes,
+                                    void* stream) {
     if (int rc = group2_checks(wtype, wtype2, n, n1, W, Y, N, M, K)) return rc;
     if (!X) return bx::fail(BX_EINVAL, "linear_group2: null X");
-    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, X, nullptr, nullptr, 0.f, nullptr, M, K,
+    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, X, nullptr, nullptr, 0.f, nullptr, M, K, ws, ws_bytes,
                                 bx::as_stream(stream));
 }
 
 extern "C" int bx_linear_group2_norm_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
                                          const int* N, const float* H, const uint16_t* gamma, float eps,
-                                         const float* ss_in, int M, int K, void* stream) {
+                                         const float* ss_in, int M, int K, void* ws, size_t ws_bytes, void* stream) {
     if (int rc = group2_checks(wtype, wtype2, n, n1, W, Y, N, M, K)) return rc;
     if (!H || !gamma || !ss_in) return bx::fail(BX_EINVAL, "linear_group2_norm: null pointer");
-    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, nullptr, H, gamma, eps, ss_in, M, K,
+    return bx::gemv_mfma_group2(wtype, wtype2, n, n1, W, Y, N, nullptr, H, gamma, eps, ss_in, M, K, ws, ws_bytes,
                                 bx::as_stream(stream));
 }

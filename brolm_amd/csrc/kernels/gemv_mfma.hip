@@ -330,6 +330,11 @@ struct MfmaJob {
     float* ss_out;
     // two-format groups: members from mem2 on have the second weight type
     int mem2;
+    // split launches: the caller's workspace (counters, then FP32 partials)
+    // and the launch's tag (nonzero, new for every launch the host makes)
+    uint64_t* cnt;
+    float* part;
+    uint32_t tag;
 };
 
 // Tile t of the launch -> (member, row tile within the member).
@@ -497,15 +502,10 @@ constexpr int kSplMaxSlices = 64;                // K up to 49152
 constexpr int64_t kSplFloats = 16ll << 20;       // partials: 64 MB
 constexpr int kSplGroups = 4096;                 // tile groups of one launch
 
+constexpr size_t kSplCntBytes = (size_t)kSplGroups * 8;
+
 }  // namespace
 }  // namespace bx
-
-// The split workspace, one copy per GPU, used by every split launch on it in
-// stream order: launches of 3 <= M <= 16 rows on one GPU must not overlap in
-// time (the library issues them on one stream).  Host code never takes these
-// names as addresses; only the kernels below touch them.
-static __device__ __align__(256) float split_part[bx::kSplFloats];
-static __device__ __align__(256) uint32_t split_cnt[bx::kSplGroups];
 
 namespace bx {
 namespace {
@@ -513,9 +513,10 @@ namespace {
 // Cache policy of the partials' buffer stores and loads: sc1, device scope.
 constexpr int kSc1 = 16;
 
-__global__ void split_clear_kernel() {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kSplGroups; i += gridDim.x * blockDim.x) split_cnt[i] = 0u;
+__global__ void split_clear_kernel(uint64_t* cnt) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kSplGroups; i += gridDim.x * blockDim.x) cnt[i] = 0ull;
 }
+
 
 // The epilogue of one tile from lane values a (and u for SwiGLU); for the
 // residual, sq[j] is the square of the lane's updated value of row 4 g + j
@@ -722,7 +723,7 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     const int Mr4 = (Mr + 3) & ~3;
     const int pl = 4 * Mr4;                             // lanes with partials
     const int64_t pstride = (int64_t)kParts * pl * 4;   // floats per (tile, slice)
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(split_part, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(job.part, 0, 0x7fffffff, 0x00020000);
     const int64_t tbase = live ? tile * S * pstride : 0;
     if (live && lane < pl) {
         const int o = (int)((tbase + s * pstride) * 4) + lane * 16;
@@ -731,11 +732,23 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(&split_cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                       (uint32_t)(S - 1)
-                   ? 1u
-                   : 0u;
+    // The group's counter word is {tag (high 32 bits), arrivals}.  A word
+    // carrying another launch's tag (one that never finished, or memory
+    // never cleared) counts as zero arrivals, so no earlier launch's count
+    // can make this launch add its partials early or never; the last
+    // arrival puts the word back to zero, which keeps replays of a captured
+    // launch (same tag every time) correct.
+    if (threadIdx.x == 0) {
+        uint64_t* c = &job.cnt[blockIdx.x];
+        uint64_t old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t nw;
+        do {
+            const uint32_t n = (uint32_t)(old >> 32) == job.tag ? (uint32_t)old + 1u : 1u;
+            nw = ((uint64_t)job.tag << 32) | n;
+        } while (!__hip_atomic_compare_exchange_weak(c, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+        last = (uint32_t)nw == (uint32_t)S ? 1u : 0u;
+    }
     __syncthreads();
     if (!last) return;
     if (live && lane < pl) {
@@ -763,7 +776,7 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
         sq = f4v{0.f, 0.f, 0.f, 0.f};
     }
     if (EPI == MEPI_RESID && job.ss_out) group_row_ss(job, Mr, wave, r, g, sq, wss);
-    if (threadIdx.x == 0) __hip_atomic_store(&split_cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(&job.cnt[blockIdx.x], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Slices of K for the split launch: up to 16 slices of as few chunks as that
@@ -774,21 +787,6 @@ int split_plan(int K, int& cps) {
     cps = min(kSplMaxCps, (nch + 15) / 16);
     const int S = (nch + cps - 1) / cps;
     return S <= kSplMaxSlices ? S : 0;
-}
-
-// The split counters start at zero: cleared once per GPU before its first
-// split launch (stream-ordered ahead of it).
-int split_ready(hipStream_t st) {
-    static std::mutex mu;
-    static std::map<int, bool> done;
-    int dev = 0;
-    if (int rc = hip_check(hipGetDevice(&dev), "gemv split: hipGetDevice")) return rc;
-    std::lock_guard<std::mutex> lk(mu);
-    if (done[dev]) return BX_OK;
-    split_clear_kernel<<<16, 256, 0, st>>>();
-    if (int rc = launch_check("gemv split clear")) return rc;
-    done[dev] = true;
-    return BX_OK;
 }
 
 size_t mfma_lds_bytes(int fmt, int Mr, int K, bool two = false) {
@@ -809,8 +807,8 @@ constexpr int64_t kSplitTiles = 2048;
 // wtype2 >= 0: a two-format group (members from job.mem2 on), Q4_K then
 // Q6_K only, split form only.
 template <int EPI>
-int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStream_t st, bool nin = false,
-                bool split_only = false, int wtype2 = -1) {
+int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, void* ws, size_t wsb, hipStream_t st,
+                bool nin = false, bool split_only = false, int wtype2 = -1) {
     if (wtype2 >= 0 && (EPI != MEPI_STORE || wtype != BX_TYPE_Q4_K || wtype2 != BX_TYPE_Q6_K))
         return fail(BX_EUNSUPPORTED, "gemv: two-format groups are Q4_K then Q6_K");
     if (wtype2 < 0) job.mem2 = job.members;
@@ -839,10 +837,18 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
     int cps = 0;
     const int S = split_plan(K, cps);
     const int64_t groups = (tiles + kSplWav - 1) / kSplWav;
-    const bool split = S > 0 && M <= 16 && tiles <= kSplitTiles && groups <= kSplGroups &&
-                       groups * kSplWav * S * (two ? 2 : 1) * M * 16 <= kSplFloats;
+    const bool fits = S > 0 && M <= 16 && tiles <= kSplitTiles && groups <= kSplGroups &&
+                      groups * kSplWav * S * (two ? 2 : 1) * M * 16 <= kSplFloats;
+    // the split form needs the caller's workspace (counters zero at entry,
+    // zero again at exit); without one the shape takes the plain launch
+    const bool split = fits && ws != nullptr && wsb >= kSplCntBytes + (size_t)kSplFloats * 4;
+    if (fits && (split_only || nin || wtype2 >= 0) && !split)
+        return fail(BX_EINVAL, "gemv: the fused-norm and two-format forms need a linear workspace "
+                               "(bx_linear_workspace_bytes)");
     if (split) {
-        if (int rc = split_ready(st)) return rc;
+        job.cnt = static_cast<uint64_t*>(ws);
+        job.tag = next_launch_tag();
+        job.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kSplCntBytes);
         const size_t lds = (size_t)(M + 1) * (128 * cps + 4) * 4 + (fmt == FMT_Q4_K ? (size_t)8 * cps * 16 * 4 : 0);
         const dim3 grid((unsigned)groups, (unsigned)S);
         if (wtype2 >= 0) {
@@ -913,31 +919,31 @@ int mfma_launch(int wtype, MfmaJob job, const uint16_t* X, int M, int K, hipStre
 
 // 1 <= M <= 16, K % 256 == 0 (the linear entry point sends 3 <= M <= 16).
 int gemv_mfma(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-              hipStream_t st) {
+              void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = W;
     job.Y[0] = Y;
     job.N[0] = N;
     job.bias = bias;
     job.members = 1;
-    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st);
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, ws, wsb, st);
 }
 
 // The split launch only (BX_EUNSUPPORTED, nothing launched, when it does not
 // take the shape): rows beyond the whole-K kernel's LDS staging.
 int gemv_mfma_split(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
-                    hipStream_t st) {
+                    void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = W;
     job.Y[0] = Y;
     job.N[0] = N;
     job.bias = bias;
     job.members = 1;
-    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st, false, true);
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, ws, wsb, st, false, true);
 }
 
 int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
-                    int M, int K, hipStream_t st) {
+                    int M, int K, void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     for (int i = 0; i < n; ++i) {
         job.W[i] = W[i];
@@ -945,31 +951,31 @@ int gemv_mfma_group(int wtype, int n, const void* const* W, uint16_t* const* Y, 
         job.N[i] = N[i];
     }
     job.members = n;
-    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st);
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, ws, wsb, st);
 }
 
-int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, hipStream_t st) {
+int gemv_mfma_resid(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = W;
     job.N[0] = N;
     job.H = H;
     job.members = 1;
-    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, st);
+    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, ws, wsb, st);
 }
 
 int gemv_mfma_resid_ss(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N, int K,
-                       hipStream_t st) {
+                       void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = W;
     job.N[0] = N;
     job.H = H;
     job.ss_out = ss_out;
     job.members = 1;
-    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, st, false, true);
+    return mfma_launch<MEPI_RESID>(wtype, job, X, M, K, ws, wsb, st, false, true);
 }
 
 int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
-                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, hipStream_t st) {
+                         const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     for (int i = 0; i < n; ++i) {
         job.W[i] = W[i];
@@ -982,12 +988,12 @@ int gemv_mfma_group_norm(int wtype, int n, const void* const* W, uint16_t* const
     job.eps = eps;
     job.ss_in = ss_in;
     job.ss_groups = (K + 63) / 64;
-    return mfma_launch<MEPI_STORE>(wtype, job, nullptr, M, K, st, true);
+    return mfma_launch<MEPI_STORE>(wtype, job, nullptr, M, K, ws, wsb, st, true);
 }
 
 int gemv_mfma_group2(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
                      const uint16_t* X, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
-                     int K, hipStream_t st) {
+                     int K, void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     for (int i = 0; i < n; ++i) {
         job.W[i] = W[i];
@@ -1004,11 +1010,11 @@ int gemv_mfma_group2(int wtype, int wtype2, int n, int n1, const void* const* W,
         job.ss_in = ss_in;
         job.ss_groups = (K + 63) / 64;
     }
-    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, st, nin, true, wtype2);
+    return mfma_launch<MEPI_STORE>(wtype, job, X, M, K, ws, wsb, st, nin, true, wtype2);
 }
 
 int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma, float eps,
-                          const float* ss_in, uint16_t* Y, int M, int F, int K, hipStream_t st) {
+                          const float* ss_in, uint16_t* Y, int M, int F, int K, void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = Wg;
     job.W[1] = Wu;
@@ -1020,18 +1026,27 @@ int gemv_mfma_swiglu_norm(int wtype, const void* Wg, const void* Wu, const float
     job.eps = eps;
     job.ss_in = ss_in;
     job.ss_groups = (K + 63) / 64;
-    return mfma_launch<MEPI_SWIGLU>(wtype, job, nullptr, M, K, st, true);
+    return mfma_launch<MEPI_SWIGLU>(wtype, job, nullptr, M, K, ws, wsb, st, true);
 }
 
 int gemv_mfma_swiglu(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F, int K,
-                     hipStream_t st) {
+                     void* ws, size_t wsb, hipStream_t st) {
     MfmaJob job{};
     job.W[0] = Wg;
     job.W[1] = Wu;
     job.Y[0] = Y;
     job.N[0] = F;
     job.members = 1;   // one tile space; each tile takes the same rows of both
-    return mfma_launch<MEPI_SWIGLU>(wtype, job, X, M, K, st);
+    return mfma_launch<MEPI_SWIGLU>(wtype, job, X, M, K, ws, wsb, st);
 }
 
 }  // namespace bx
+
+extern "C" size_t bx_linear_workspace_bytes(void) { return bx::kSplCntBytes + (size_t)bx::kSplFloats * 4; }
+
+extern "C" int bx_linear_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+    if (!ws || ws_bytes < bx_linear_workspace_bytes())
+        return bx::fail(BX_EINVAL, "linear_workspace_init: workspace smaller than bx_linear_workspace_bytes()");
+    bx::split_clear_kernel<<<16, 256, 0, bx::as_stream(stream)>>>(static_cast<uint64_t*>(ws));
+    return bx::launch_check("linear workspace init");
+}

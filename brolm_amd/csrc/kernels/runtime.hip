@@ -1,4 +1,5 @@
 // Host-side plumbing shared by every bx_* entry point: error state, device info.
+#include <atomic>
 #include "common.h"
 
 #include <link.h>
@@ -68,6 +69,15 @@ static int find_profiler_tool(struct dl_phdr_info* info, size_t, void* hit) {
         return 1;
     }
     return 0;
+}
+
+std::atomic<uint32_t> g_launch_tag{0};
+
+uint32_t next_launch_tag() {
+    uint32_t t;
+    do t = g_launch_tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    while (t == 0u);
+    return t;
 }
 
 bool profiler_attached() {

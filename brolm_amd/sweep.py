@@ -10,7 +10,10 @@ repeats come from HBM; a row whose rotation stays under 512 MB says
             the GPU-side dispatch gap, so small matrices read launch-bound);
   us_batch  100 back-to-back launches between two events / 100 (dispatch
             overlapped, the kernels' own throughput).
-GB/s counts the carrier bytes + M*(K+N)*2 activation bytes.  The comparison
+GB/s counts the carrier bytes + M*(K+N)*2 activation bytes.  Every row
+also checks the output of its last timed launch against X W^T in FP32 on the
+dequantized weights ("err_over_tol", "ok"); the run exits nonzero when a row
+fails, so a fast kernel that computes the wrong thing cannot post a number.  The comparison
 leg "ref_fp32_us" is the reference's FP32 route for a quantized weight
 (include/brolm/detail/compute.h:77-85: dequantize to FP32, then an FP32
 GEMM; here bx_dequant_to_f32 then torch.matmul in FP32) on the same case.
@@ -65,15 +68,54 @@ def make_weights(torch, t: str, n: int, k: int, copies: int, seed: int):
     return out
 
 
+_WS: dict = {}
+
+
+def workspace(torch):
+    """(pointer, bytes) of the split-K workspace handed to every timed launch,
+    allocated and cleared once (bx_linear_workspace_bytes / _init)."""
+    if "buf" not in _WS:
+        hip = _native.hip()
+        n = int(hip.bx_linear_workspace_bytes())
+        _WS["buf"] = torch.empty(n, dtype=torch.uint8, device="cuda")
+        _WS["n"] = n
+        _native.bx_check(hip.bx_linear_workspace_init(C.c_void_p(_WS["buf"].data_ptr()), C.c_size_t(n),
+                                                      C.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                         "workspace")
+    return C.c_void_p(_WS["buf"].data_ptr()), C.c_size_t(_WS["n"])
+
+
+def check_output(torch, t: str, n: int, k: int, x, y, w) -> float:
+    """Worst |y - ref| / tol over the launch's output, ref = X W^T in FP32 on
+    the exactly dequantized weights (bx_dequant_to_f32, bit-exact to the
+    block formats), tol = 2^-10 |ref| (FP16 output rounding, doubled) +
+    2^-14 sum |x||w| (FP32 accumulation order) + 1e-6.  A value above 1
+    means the timed kernel computed something else."""
+    hip = _native.hip()
+    st = torch.cuda.current_stream()
+    wf = torch.empty(n, k, device="cuda", dtype=torch.float32)
+    _native.bx_check(hip.bx_dequant_to_f32(GGML[t], C.c_void_p(w.data_ptr()), C.c_void_p(wf.data_ptr()), n, k,
+                                           C.c_void_p(st.cuda_stream)), "dequant")
+    xf = x.float()
+    ref = xf @ wf.t()
+    mass = xf.abs() @ wf.abs().t()
+    tol = 2.0 ** -10 * ref.abs() + 2.0 ** -14 * mass + 1e-6
+    worst = float(((y.float() - ref).abs() / tol).max())
+    del wf, ref, mass, tol
+    return worst
+
+
 def time_case(torch, t: str, n: int, k: int, m: int, weights, reps: int = 100) -> dict:
     hip = _native.hip()
     st = torch.cuda.current_stream()
     x = torch.randn(m, k, device="cuda", dtype=torch.float16)
     y = torch.empty(m, n, device="cuda", dtype=torch.float16)
+    wsp, wsb = workspace(torch)
 
     def launch(w):
         _native.bx_check(hip.bx_linear_f16(GGML[t], C.c_void_p(w.data_ptr()), None, C.c_void_p(x.data_ptr()),
-                                           C.c_void_p(y.data_ptr()), m, n, k, C.c_void_p(st.cuda_stream)), "linear")
+                                           C.c_void_p(y.data_ptr()), m, n, k, wsp, wsb, C.c_void_p(st.cuda_stream)),
+                         "linear")
 
     for w in weights[:4]:
         launch(w)
@@ -95,10 +137,12 @@ def time_case(torch, t: str, n: int, k: int, m: int, weights, reps: int = 100) -
     e1.record(st)
     torch.cuda.synchronize()
     batch = e0.elapsed_time(e1) * 1e3 / reps
+    worst = check_output(torch, t, n, k, x, y, weights[(reps - 1) % len(weights)])
     byts = carrier_bytes(t, n, k) + m * (k + n) * 2
     return {"type": t, "N": n, "K": k, "M": m, "us": round(med, 3), "GBps": round(byts / (med * 1e-6) / 1e9, 1),
             "frac": round(byts / (med * 1e-6) / 1e9 / HBM_PEAK, 4), "us_batch": round(batch, 3),
-            "GBps_batch": round(byts / (batch * 1e-6) / 1e9, 1), "bytes": byts}
+            "GBps_batch": round(byts / (batch * 1e-6) / 1e9, 1), "bytes": byts, "err_over_tol": round(worst, 4),
+            "ok": worst <= 1.0}
 
 
 def time_ref_fp32(torch, t: str, n: int, k: int, m: int, w, reps: int = 20) -> float:
@@ -171,6 +215,10 @@ def main(argv=None) -> int:
     if a.json:
         with open(a.json, "w") as f:
             json.dump(rows, f, indent=1)
+    bad = [r for r in rows if not r["ok"]]
+    if bad:
+        print(f"{len(bad)} row(s) failed the output check", file=sys.stderr)
+        return 1
     return 0
 
 

@@ -11,6 +11,8 @@
  *   - Nothing here allocates device memory; scratch is passed in by the
  *     caller, sized by the matching *_workspace_bytes query (except
  *     bx_argmax_f16_noalloc, whose scratch is a fixed array of the library).
+ *     Calls on different streams never share scratch unless the caller
+ *     hands them the same workspace.
  *   - Return 0 on success or a negative BX_E* code; bx_last_error() gives a
  *     thread-local message.  Shapes are validated on the host before any
  *     launch, so an invalid shape is an error return, never a device fault.
@@ -76,13 +78,29 @@ int bx_dequant_to_f32(int type, const void* carrier, float* dst, int64_t rows, i
 
 /* ------------------------------------------------------------------ linear */
 
+/* Workspace of the linear entry points below (no counterpart in the
+ * reference: brotensor's ops keep their scratch to themselves).  Decode
+ * batches of 3..16 rows over layer-sized matrices split K across
+ * workgroups; their partial sums and per-tile-group counters live in `ws`
+ * (bx_linear_workspace_bytes() bytes: 32 KB of counters, 64 MB of FP32
+ * partials), which the caller allocates and clears once with
+ * bx_linear_workspace_init before its first use.  Every launch leaves the
+ * counters at zero again, and each counter word carries its launch's tag,
+ * so a launch that did not complete cannot make a later one sum early or
+ * never.  Launches that may run at the same time (other streams, other
+ * threads) take distinct workspaces.  ws = NULL (ws_bytes 0) is accepted: those shapes then take the
+ * single-pass launch, and the forms that exist only as split launches (the
+ * _norm and _ss forms, group2) return BX_EINVAL. */
+size_t bx_linear_workspace_bytes(void);
+int bx_linear_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
 /* K1-K4: linear_forward_batched_{q4k,q6k,q8_0,}_fp16(W, bias, X, Y)
  * (include/brolm/detail/compute.h:54-86).  Y[M,N] = X[M,K] . W[N,K]^T (+bias[N]).
  * X, Y, bias FP16; FP32 accumulation.  W is a carrier of `wtype` or dense FP16
  * (wtype BX_TYPE_F16).  M <= 16 runs the GEMV kernels, larger M the prefill
- * GEMM. */
+ * GEMM.  ws / ws_bytes: the linear workspace above. */
 int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y,
-                  int M, int N, int K, void* stream);
+                  int M, int N, int K, void* ws, size_t ws_bytes, void* stream);
 
 /* Fused prefill forms of the linears of src/detail/dense_decoder.cpp:526-681
  * (the op sequence linear / silu / mul / add_inplace, with the same
@@ -98,10 +116,11 @@ int bx_linear_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t
  *   (gate / up projections, silu, mul). */
 int bx_linear_tiles_ok(int M, int K);
 int bx_linear_group_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const uint16_t* X,
-                        int M, int K, void* stream);
-int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* stream);
+                        int M, int K, void* ws, size_t ws_bytes, void* stream);
+int bx_linear_residual_f16(int wtype, const void* W, const uint16_t* X, float* H, int M, int N, int K, void* ws,
+                           size_t ws_bytes, void* stream);
 int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16_t* X, uint16_t* Y, int M, int F,
-                         int K, void* stream);
+                         int K, void* ws, size_t ws_bytes, void* stream);
 /* Decode batches (3 <= M <= 16, K % 256 == 0) with the residual RMSNorm
  * (rms_norm_forward, dense_decoder.cpp:559, :540-550) carried between
  * launches instead of run on its own: bx_linear_residual_ss_f16 is
@@ -115,11 +134,13 @@ int bx_linear_swiglu_f16(int wtype, const void* Wg, const void* Wu, const uint16
  * forms). */
 size_t bx_linear_ss_floats(int N);
 int bx_linear_residual_ss_f16(int wtype, const void* W, const uint16_t* X, float* H, float* ss_out, int M, int N,
-                              int K, void* stream);
+                              int K, void* ws, size_t ws_bytes, void* stream);
 int bx_linear_group_norm_f16(int wtype, int n, const void* const* W, uint16_t* const* Y, const int* N, const float* H,
-                             const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* stream);
+                             const uint16_t* gamma, float eps, const float* ss_in, int M, int K, void* ws,
+                             size_t ws_bytes, void* stream);
 int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const float* H, const uint16_t* gamma,
-                              float eps, const float* ss_in, uint16_t* Y, int M, int F, int K, void* stream);
+                              float eps, const float* ss_in, uint16_t* Y, int M, int F, int K, void* ws,
+                              size_t ws_bytes, void* stream);
 /* The q / k / v projections in one decode-batch launch when v's weight type
  * differs from q / k's (the per-weight dispatch of compute.h:54-86 over
  * llama.cpp's Q4_K_M mix): members [0, n1) of type wtype, [n1, n) of type
@@ -128,10 +149,10 @@ int bx_linear_swiglu_norm_f16(int wtype, const void* Wg, const void* Wu, const f
  * bx_linear_residual_ss_f16, as bx_linear_group_norm_f16.  BX_EUNSUPPORTED,
  * nothing launched, for other types or shapes outside the split GEMV. */
 int bx_linear_group2_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y, const int* N,
-                         const uint16_t* X, int M, int K, void* stream);
+                         const uint16_t* X, int M, int K, void* ws, size_t ws_bytes, void* stream);
 int bx_linear_group2_norm_f16(int wtype, int wtype2, int n, int n1, const void* const* W, uint16_t* const* Y,
                               const int* N, const float* H, const uint16_t* gamma, float eps, const float* ss_in, int M,
-                              int K, void* stream);
+                              int K, void* ws, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------- elementwise */
 
@@ -198,8 +219,9 @@ int bx_kv_append_rows_f16(const uint16_t* k, const uint16_t* v, int rows, int co
  * cache, split attention over the row's keys and the merge of the splits ->
  * out (rows, n_q*hd) FP16.  q, k, v: the raw projections.  workspace:
  * bx_batch_attention_workspace_bytes(rows, ...) bytes, zeroed once before its
- * first use (the kernel leaves its counters at zero); calls sharing one
- * workspace must not overlap.  hd: 64, 128 or 256; n_q / n_kv <= 8. */
+ * first use (the kernel leaves its counters at zero; a counter left by a
+ * launch that did not complete carries that launch's tag and is ignored);
+ * calls sharing one workspace must not overlap.  hd: 64, 128 or 256; n_q / n_kv <= 8. */
 size_t bx_batch_attention_workspace_bytes(int rows, int n_q, int n_kv, int hd, int max_len);
 int bx_batch_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, int rows, int hd, int n_q,
                            int n_kv, const uint16_t* q_gain, const uint16_t* k_gain, float eps, const int32_t* lens_dev,

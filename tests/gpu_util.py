@@ -39,6 +39,27 @@ def stream() -> C.c_void_p:
     return C.c_void_p(torch().cuda.current_stream().cuda_stream)
 
 
+_ws: dict = {}
+
+
+def new_workspace():
+    """A fresh split-K workspace for the bx_linear_* entry points: a device
+    buffer of bx_linear_workspace_bytes() bytes, counters cleared by
+    bx_linear_workspace_init on the current stream.  Returns (buffer, bytes)."""
+    n = int(hip().bx_linear_workspace_bytes())
+    buf = torch().empty(n, dtype=torch().uint8, device="cuda")
+    call("bx_linear_workspace_init", C.c_void_p(buf.data_ptr()), C.c_size_t(n), stream())
+    return buf, n
+
+
+def lws():
+    """(pointer, bytes) of the module-wide workspace the tests hand to every
+    bx_linear_* call on the default stream; made once per process."""
+    if "buf" not in _ws:
+        _ws["buf"], _ws["n"] = new_workspace()
+    return C.c_void_p(_ws["buf"].data_ptr()), C.c_size_t(_ws["n"])
+
+
 def dev(a: np.ndarray):
     return torch().from_numpy(np.ascontiguousarray(a)).to("cuda")
 

@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import spec_blocks as sb
-from gpu_util import call, carrier, dev, empty, f16_dev, f16_host, host, hip, ptr, release, stream, torch
+from gpu_util import call, carrier, dev, empty, f16_dev, f16_host, host, hip, lws, new_workspace, ptr, release, stream, torch
 
 pytestmark = pytest.mark.gpu
 
@@ -86,7 +86,7 @@ def _run_linear(t, Wdev, X, N, K, bias=None):
     x = f16_dev(X)
     y = torch().empty(M * N, dtype=torch().int16, device="cuda")
     b = f16_dev(bias) if bias is not None else None
-    call("bx_linear_f16", t, ptr(Wdev), ptr(b), ptr(x), ptr(y), M, N, K, stream())
+    call("bx_linear_f16", t, ptr(Wdev), ptr(b), ptr(x), ptr(y), M, N, K, *lws(), stream())
     return f16_host(y).reshape(M, N)
 
 
@@ -158,33 +158,93 @@ def test_fused_prefill_linears_equal_unfused_ops(t, M, K, Ns):
     W_arr = (C.c_void_p * 3)(*[ptr(w) for w in ws])
     Y_arr = (C.c_void_p * 3)(*[ptr(y) for y in ys])
     N_arr = (C.c_int * 3)(*Ns)
-    call("bx_linear_group_f16", t, 3, W_arr, Y_arr, N_arr, ptr(x), M, K, stream())
+    call("bx_linear_group_f16", t, 3, W_arr, Y_arr, N_arr, ptr(x), M, K, *lws(), stream())
     for w, y, n in zip(ws, ys, Ns):
         ref = torch().empty(M * n, dtype=torch().int16, device="cuda")
-        call("bx_linear_f16", t, ptr(w), None, ptr(x), ptr(ref), M, n, K, stream())
+        call("bx_linear_f16", t, ptr(w), None, ptr(x), ptr(ref), M, n, K, *lws(), stream())
         assert np.array_equal(host(y), host(ref))
     # residual: H (FP32) += f16(X W^T)
     H0 = rng.standard_normal((M, Ns[0])).astype(np.float32)
     Hf = dev(H0)
-    call("bx_linear_residual_f16", t, ptr(ws[0]), ptr(x), ptr(Hf), M, Ns[0], K, stream())
+    call("bx_linear_residual_f16", t, ptr(ws[0]), ptr(x), ptr(Hf), M, Ns[0], K, *lws(), stream())
     Hr = dev(H0)
     proj = torch().empty(M * Ns[0], dtype=torch().int16, device="cuda")
-    call("bx_linear_f16", t, ptr(ws[0]), None, ptr(x), ptr(proj), M, Ns[0], K, stream())
+    call("bx_linear_f16", t, ptr(ws[0]), None, ptr(x), ptr(proj), M, Ns[0], K, *lws(), stream())
     call("bx_add_inplace", ptr(Hr), 1, ptr(proj), M * Ns[0], stream())
     assert np.array_equal(host(Hf).view(np.uint32), host(Hr).view(np.uint32))
     # SwiGLU: gate = ws[1], up = ws[2] (same shape)
     act = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
-    call("bx_linear_swiglu_f16", t, ptr(ws[1]), ptr(ws[2]), ptr(x), ptr(act), M, Ns[1], K, stream())
+    call("bx_linear_swiglu_f16", t, ptr(ws[1]), ptr(ws[2]), ptr(x), ptr(act), M, Ns[1], K, *lws(), stream())
     g = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
     u = torch().empty(M * Ns[1], dtype=torch().int16, device="cuda")
-    call("bx_linear_f16", t, ptr(ws[1]), None, ptr(x), ptr(g), M, Ns[1], K, stream())
-    call("bx_linear_f16", t, ptr(ws[2]), None, ptr(x), ptr(u), M, Ns[1], K, stream())
+    call("bx_linear_f16", t, ptr(ws[1]), None, ptr(x), ptr(g), M, Ns[1], K, *lws(), stream())
+    call("bx_linear_f16", t, ptr(ws[2]), None, ptr(x), ptr(u), M, Ns[1], K, *lws(), stream())
     call("bx_silu_f16", ptr(g), ptr(g), M * Ns[1], stream())
     call("bx_mul_f16", ptr(g), ptr(u), M * Ns[1], stream())
     assert np.array_equal(host(act), host(g))
     # between the two paths: declined, nothing written
     assert h.bx_linear_tiles_ok(100, K) == 0 and h.bx_linear_tiles_ok(2, K) == 0 and h.bx_linear_tiles_ok(M, K) == 1
-    assert h.bx_linear_residual_f16(t, ptr(ws[0]), ptr(x), ptr(Hf), 100, Ns[0], K, stream()) == -3  # BX_EUNSUPPORTED
+    assert h.bx_linear_residual_f16(t, ptr(ws[0]), ptr(x), ptr(Hf), 100, Ns[0], K, *lws(), stream()) == -3  # BX_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("t", QTYPES)
+def test_linear_split_k_two_streams_own_workspaces(t):
+    """16-row split-K linears on two streams at once, each stream with its own
+    workspace: every launch matches the oracle, and each stream's result has
+    the bits of the same launch run alone (the slice order is fixed).  A
+    workspace whose counters hold a stale word of an unfinished launch (tag
+    and partial count written from the host) still gives the same bits.  No
+    workspace: the plain launch, still within the oracle's tolerance; the
+    split-only forms return BX_EINVAL with nothing written."""
+    print(f"[linear two streams] t={t}", flush=True)
+    T = torch()
+    h = hip()
+    rng = np.random.default_rng(5150 + t)
+    N, K, M, reps = 2048, 2048, 16, 6
+    raw, Wv = sb.random_matrix(rng, t, N, K)
+    car = carrier(t, raw, N, K)
+    Xs = [_f16(rng.standard_normal((M, K))) for _ in range(2)]
+    xs = [f16_dev(X) for X in Xs]
+    alone = []
+    for x in xs:
+        y = T.empty(M * N, dtype=T.int16, device="cuda")
+        call("bx_linear_f16", t, ptr(car), None, ptr(x), ptr(y), M, N, K, *lws(), stream())
+        alone.append(host(y))
+    wss = [new_workspace() for _ in range(2)]
+    T.cuda.synchronize()
+    streams = [T.cuda.Stream(), T.cuda.Stream()]
+    outs = [[T.empty(M * N, dtype=T.int16, device="cuda") for _ in range(reps)] for _ in range(2)]
+    for i in range(reps):
+        for s in range(2):
+            call("bx_linear_f16", t, ptr(car), None, ptr(xs[s]), ptr(outs[s][i]), M, N, K,
+                 C.c_void_p(wss[s][0].data_ptr()), C.c_size_t(wss[s][1]), C.c_void_p(streams[s].cuda_stream))
+    T.cuda.synchronize()
+    for s in range(2):
+        ref = oracle.linear(Wv, Xs[s])
+        tol = _linear_tol(Wv, Xs[s], ref)
+        for i in range(reps):
+            got = host(outs[s][i])
+            assert np.array_equal(got, alone[s]), (s, i)
+            assert np.all(np.abs(got.view(np.float16).astype(np.float32).reshape(M, N) - ref) <= tol), (s, i)
+    # a stale counter word: tag 0xdeadbeef with 3 arrivals, in every group
+    buf, n = wss[0]
+    stale = np.zeros(4096, np.uint64) | np.uint64((0xdeadbeef << 32) | 3)
+    buf[: stale.nbytes].copy_(T.from_numpy(stale.view(np.uint8)).to("cuda"))
+    y = T.empty(M * N, dtype=T.int16, device="cuda")
+    call("bx_linear_f16", t, ptr(car), None, ptr(xs[0]), ptr(y), M, N, K, C.c_void_p(buf.data_ptr()), C.c_size_t(n),
+         stream())
+    assert np.array_equal(host(y), alone[0])
+    # no workspace: the single-pass launch
+    y = T.empty(M * N, dtype=T.int16, device="cuda")
+    call("bx_linear_f16", t, ptr(car), None, ptr(xs[0]), ptr(y), M, N, K, None, C.c_size_t(0), stream())
+    ref = oracle.linear(Wv, Xs[0])
+    assert np.all(np.abs(f16_host(y).reshape(M, N) - ref) <= _linear_tol(Wv, Xs[0], ref))
+    H = dev(np.zeros((M, N), np.float32))
+    ss = T.zeros(h.bx_linear_ss_floats(N), dtype=T.float32, device="cuda")
+    Wo = carrier(t, sb.random_matrix(rng, t, N, K)[0], N, K)
+    assert h.bx_linear_residual_ss_f16(t, ptr(Wo), ptr(xs[0]), ptr(H), ptr(ss), M, N, K, None, C.c_size_t(0),
+                                       stream()) == -1   # BX_EINVAL
+    assert not np.any(host(H))
 
 
 @pytest.mark.parametrize("t", QTYPES)
@@ -494,9 +554,9 @@ def test_linear_rejects_bad_shapes_and_types():
     x = torch().zeros(256, dtype=torch().int16, device="cuda")
     y = torch().zeros(256, dtype=torch().int16, device="cuda")
     h = hip()
-    assert h.bx_linear_f16(12, ptr(x), None, ptr(x), ptr(y), 1, 1, 100, stream()) == -1   # K not a block multiple
-    assert h.bx_linear_f16(2, ptr(x), None, ptr(x), ptr(y), 1, 1, 256, stream()) == -3    # unsupported type
-    assert h.bx_linear_f16(12, None, None, ptr(x), ptr(y), 1, 1, 256, stream()) == -1     # null weight
+    assert h.bx_linear_f16(12, ptr(x), None, ptr(x), ptr(y), 1, 1, 100, *lws(), stream()) == -1   # K not a block multiple
+    assert h.bx_linear_f16(2, ptr(x), None, ptr(x), ptr(y), 1, 1, 256, *lws(), stream()) == -3    # unsupported type
+    assert h.bx_linear_f16(12, None, None, ptr(x), ptr(y), 1, 1, 256, *lws(), stream()) == -1     # null weight
     assert b"linear" in h.bx_last_error()
 
 
@@ -527,8 +587,8 @@ def test_linear_norm_carried_between_launches(t, M):
     ss = torch().zeros(nss, dtype=torch().float32, device="cuda")
     # residual with row sums vs the plain residual
     Hs, Hp = dev(H0), dev(H0)
-    call("bx_linear_residual_ss_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hs), ptr(ss), M, K, Ka, stream())
-    call("bx_linear_residual_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hp), M, K, Ka, stream())
+    call("bx_linear_residual_ss_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hs), ptr(ss), M, K, Ka, *lws(), stream())
+    call("bx_linear_residual_f16", t, ptr(Wo), ptr(f16_dev(X)), ptr(Hp), M, K, Ka, *lws(), stream())
     Hn = host(Hs).reshape(M, K)
     assert np.array_equal(Hn.view(np.uint32), host(Hp).reshape(M, K).view(np.uint32))
     rows = host(ss).reshape(-1, 16)[:, :M].sum(axis=0, dtype=np.float64)
@@ -542,8 +602,8 @@ def test_linear_norm_carried_between_launches(t, M):
     W_arr = (C.c_void_p * 3)(*[ptr(w[0]) for w in ws])
     N_arr = (C.c_int * 3)(*Ns)
     call("bx_linear_group_norm_f16", t, 3, W_arr, (C.c_void_p * 3)(*[ptr(y) for y in ys]), N_arr, ptr(Hs), ptr(gd),
-         C.c_float(1e-6), ptr(ss), M, K, stream())
-    call("bx_linear_group_f16", t, 3, W_arr, (C.c_void_p * 3)(*[ptr(y) for y in yr]), N_arr, ptr(xn), M, K, stream())
+         C.c_float(1e-6), ptr(ss), M, K, *lws(), stream())
+    call("bx_linear_group_f16", t, 3, W_arr, (C.c_void_p * 3)(*[ptr(y) for y in yr]), N_arr, ptr(xn), M, K, *lws(), stream())
     for (w, Wv), n, y, r in zip(ws, Ns, ys, yr):
         got, ref = f16_host(y).reshape(M, n), f16_host(r).reshape(M, n)
         # one FP16 ulp of the normalised input per element, on top of the output rounding
@@ -552,8 +612,8 @@ def test_linear_norm_carried_between_launches(t, M):
     act = torch().empty(M * F, dtype=torch().int16, device="cuda")
     act_r = torch().empty(M * F, dtype=torch().int16, device="cuda")
     call("bx_linear_swiglu_norm_f16", t, ptr(wg[0]), ptr(wu[0]), ptr(Hs), ptr(gd), C.c_float(1e-6), ptr(ss), ptr(act),
-         M, F, K, stream())
-    call("bx_linear_swiglu_f16", t, ptr(wg[0]), ptr(wu[0]), ptr(xn), ptr(act_r), M, F, K, stream())
+         M, F, K, *lws(), stream())
+    call("bx_linear_swiglu_f16", t, ptr(wg[0]), ptr(wu[0]), ptr(xn), ptr(act_r), M, F, K, *lws(), stream())
     got, ref = f16_host(act).reshape(M, F), f16_host(act_r).reshape(M, F)
     scale = (np.abs(Xn) @ np.abs(wg[1]).T) * (np.abs(Xn) @ np.abs(wu[1]).T)
     fin = np.isfinite(ref)   # products beyond FP16 overflow the same way in both
@@ -562,7 +622,7 @@ def test_linear_norm_carried_between_launches(t, M):
     # refused, nothing written
     sentinel = torch().full((M * Ns[0],), 0x1234, dtype=torch().int16, device="cuda")
     rc = h.bx_linear_group_norm_f16(t, 1, W_arr, (C.c_void_p * 3)(ptr(sentinel), None, None), N_arr, ptr(Hs), ptr(gd),
-                                    C.c_float(1e-6), ptr(ss), 2, K, stream())
+                                    C.c_float(1e-6), ptr(ss), 2, K, *lws(), stream())
     assert rc == -3 and np.all(host(sentinel) == 0x1234)
 
 
@@ -588,10 +648,10 @@ def test_linear_group_two_formats_equals_own_launches(M):
         return (C.c_void_p * 3)(*[ptr(y) for y in ys])
 
     ya, yb = outs(), outs()
-    call("bx_linear_group2_f16", 12, 14, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, stream())
-    call("bx_linear_group_f16", 12, 2, W_arr, arr(yb), N_arr, ptr(x), M, K, stream())
+    call("bx_linear_group2_f16", 12, 14, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, *lws(), stream())
+    call("bx_linear_group_f16", 12, 2, W_arr, arr(yb), N_arr, ptr(x), M, K, *lws(), stream())
     call("bx_linear_group_f16", 14, 1, (C.c_void_p * 3)(ptr(ws[2]), None, None), (C.c_void_p * 3)(ptr(yb[2]), None, None),
-         (C.c_int * 3)(Ns[2], 0, 0), ptr(x), M, K, stream())
+         (C.c_int * 3)(Ns[2], 0, 0), ptr(x), M, K, *lws(), stream())
     for a, b in zip(ya, yb):
         assert np.array_equal(host(a), host(b))
     # from RMSNorm(H), the row sums from a residual launch
@@ -600,16 +660,16 @@ def test_linear_group_two_formats_equals_own_launches(M):
     h = hip()
     ss = torch().zeros(h.bx_linear_ss_floats(K), dtype=torch().float32, device="cuda")
     call("bx_linear_residual_ss_f16", 12, ptr(Wo), ptr(f16_dev(rng.standard_normal((M, 512)))), ptr(H), ptr(ss), M, K,
-         512, stream())
+         512, *lws(), stream())
     gd = f16_dev(rng.uniform(0.5, 1.5, K))
     ya, yb = outs(), outs()
     call("bx_linear_group2_norm_f16", 12, 14, 3, 2, W_arr, arr(ya), N_arr, ptr(H), ptr(gd), C.c_float(1e-6), ptr(ss),
-         M, K, stream())
+         M, K, *lws(), stream())
     call("bx_linear_group_norm_f16", 12, 2, W_arr, arr(yb), N_arr, ptr(H), ptr(gd), C.c_float(1e-6), ptr(ss), M, K,
-         stream())
+         *lws(), stream())
     call("bx_linear_group_norm_f16", 14, 1, (C.c_void_p * 3)(ptr(ws[2]), None, None),
          (C.c_void_p * 3)(ptr(yb[2]), None, None), (C.c_int * 3)(Ns[2], 0, 0), ptr(H), ptr(gd), C.c_float(1e-6),
-         ptr(ss), M, K, stream())
+         ptr(ss), M, K, *lws(), stream())
     for a, b in zip(ya, yb):
         assert np.array_equal(host(a), host(b))
-    assert h.bx_linear_group2_f16(14, 12, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, stream()) == -3
+    assert h.bx_linear_group2_f16(14, 12, 3, 2, W_arr, arr(ya), N_arr, ptr(x), M, K, *lws(), stream()) == -3
