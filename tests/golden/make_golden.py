@@ -20,6 +20,12 @@ model_full.npz
              untied; configs[2]'s format mix), 32-token prompt, 32 tokens;
              "bf16" Qwen3-0.6B random-init BF16, tied, 32-token
              prompt, 128 tokens.  Prompts: std::mt19937_64(42) % vocab.
+model_full_logits.npz
+             the 28-layer Qwen3-1.7B of "q4k" at two contexts,
+             a 32-token prompt and a 1024-token prompt (the bench context):
+             for each of 32 teacher-forced steps on the oracle's own greedy
+             tokens, the oracle's logits at every 37th vocabulary id and at
+             its 16 largest ids, its argmax and top-2 margin.
 model_8b_width.npz
              Qwen3-8B widths (hidden 4096, FFN 12288, 32 / 8 heads of 128,
              vocab 151936; all-Q4_K layers, Q6_K output: configs[4]'s mix)
@@ -114,6 +120,44 @@ def make_full_fixture(tmp: Path) -> dict:
     return out
 
 
+FL_STEPS, FL_STRIDE, FL_TOP = 32, 37, 16
+FL_CONTEXTS = (32, 1024)
+
+
+def make_full_logits_fixture(tmp: Path) -> dict:
+    import brolm_amd as ba
+    import oracle
+    from conftest import write_synth
+
+    spec, _, _ = FULL["q4k"]
+    path = write_synth(tmp, spec, "full_q4k")
+    out = {"sha256": np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)}
+    m = oracle.Model(str(path))
+    for ctx in FL_CONTEXTS:
+        prompt = ba.prompt_ids(ctx, spec["vocab"], seed=42)
+        m.allocate_cache(ctx + FL_STEPS + 1)
+        lg = m.forward(prompt, last_only=True)[0]
+        rows, top_ids, top_vals, toks, margins = [], [], [], [], []
+        for step in range(FL_STEPS):
+            order = np.argsort(lg, kind="stable")[::-1]
+            rows.append(lg[::FL_STRIDE].copy())
+            top_ids.append(order[:FL_TOP].astype(np.int32))
+            top_vals.append(lg[order[:FL_TOP]].copy())
+            tok, _ = oracle.argmax(lg)
+            toks.append(tok)
+            margins.append(float(lg[order[0]] - lg[order[1]]))
+            if step + 1 < FL_STEPS:
+                lg = m.forward([tok], last_only=True)[0]
+        out[f"c{ctx}_prompt"] = np.asarray(prompt, np.int32)
+        out[f"c{ctx}_rows"] = np.stack(rows).astype(np.float32)
+        out[f"c{ctx}_top_ids"] = np.stack(top_ids)
+        out[f"c{ctx}_top_vals"] = np.stack(top_vals).astype(np.float32)
+        out[f"c{ctx}_tokens"] = np.asarray(toks, np.int32)
+        out[f"c{ctx}_margins"] = np.asarray(margins, np.float32)
+        print(ctx, "tokens", toks[:8], "min margin", min(margins), flush=True)
+    return out
+
+
 W8B = dict(vocab=151936, hidden=4096, intermediate=12288, layers=2, n_q=32, n_kv=8, head_dim=128, tied=False,
            embed="Q4_K", q="Q4_K", k="Q4_K", v="Q4_K", o="Q4_K", gate="Q4_K", up="Q4_K", down="Q4_K",
            output="Q6_K", seed=5)
@@ -146,7 +190,7 @@ def make_8b_width_fixture(tmp: Path) -> dict:
 
 
 def main() -> None:
-    which = sys.argv[1:] or ["blocks", "small", "full", "w8b"]
+    which = sys.argv[1:] or ["blocks", "small", "full", "w8b", "full_logits"]
     if "blocks" in which:
         np.savez_compressed(HERE / "blocks.npz", **make_blocks())
     with tempfile.TemporaryDirectory() as td:
@@ -156,6 +200,8 @@ def main() -> None:
             np.savez_compressed(HERE / "model_full.npz", **make_full_fixture(Path(td)))
         if "w8b" in which:
             np.savez_compressed(HERE / "model_8b_width.npz", **make_8b_width_fixture(Path(td)))
+        if "full_logits" in which:
+            np.savez_compressed(HERE / "model_full_logits.npz", **make_full_logits_fixture(Path(td)))
     print("wrote", which)
 
 
