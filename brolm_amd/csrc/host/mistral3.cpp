@@ -1,105 +1,149 @@
-// Mistral 3.1 text facade (reference src/mistral3_config.cpp,
-// src/mistral3_text.cpp): config from config.json / GGUF metadata, the HF ->
-// ggml tensor-name map, and the GGUF load overloads over DenseDecoder with
-// QK-norm off.
+// Mistral 3.1 text facade (reference include/brolm/mistral3_config.h:30-143,
+// include/brolm/mistral3_text.h:52-131): the configuration from config.json
+// or GGUF metadata, the HF -> ggml tensor-name map, and the GGUF loads over
+// the dense decoder with per-head QK-norm off.
+//
+// The JSON keys, the GGUF metadata keys (every model key prefixed with the
+// file's general.architecture, "llama" or "mistral"), the tensor names and
+// the error texts are the reference's contract (src/mistral3_config.cpp:
+// 36-93, :130-191, :222-246; src/mistral3_text.cpp:70-110).  Everything
+// else is tables: a JSON row per config member, the GGUF rows shared with
+// the Qwen3 facade's reader (meta_tables.h), and validation as a list of
+// (condition, message) rules.
 #include "brolm/mistral3_config.h"
 #include "brolm/mistral3_generate.h"
 #include "brolm/mistral3_text.h"
 
 #include <fstream>
-#include <sstream>
+#include <iterator>
 #include <stdexcept>
 #include <string>
 #include <string_view>
+#include <variant>
 #include <vector>
 
 #include "brolm/detail/json.h"
 #include "brolm/detail/weights.h"
 #include "brotensor/gguf.h"
+#include "meta_tables.h"
 
 namespace brolm::mistral3 {
 
 namespace gg = ::brotensor::gguf;
 namespace js = ::brolm::detail::json;
+namespace mt = ::brolm::detail::meta;
+
+using Text = Mistral3Config::Text;
 
 namespace {
 
-[[noreturn]] void cfg_fail(const std::string& msg) { throw std::runtime_error("mistral3::Mistral3Config: " + msg); }
-[[noreturn]] void model_fail(const std::string& msg) { throw std::runtime_error("mistral3::TextModel: " + msg); }
+constexpr const char* kConfigWho = "mistral3::Mistral3Config: ";
 
-int json_int(const js::Value& o, const char* key, int dflt) {
-    const js::Value* v = o.find(key);
-    if (!v || v->kind == js::Value::Kind::Null) return dflt;
-    if (!v->is_number()) cfg_fail(std::string("'") + key + "' is not a number");
-    return static_cast<int>(v->num);
-}
-float json_float(const js::Value& o, const char* key, float dflt) {
-    const js::Value* v = o.find(key);
-    if (!v || v->kind == js::Value::Kind::Null) return dflt;
-    if (!v->is_number()) cfg_fail(std::string("'") + key + "' is not a number");
-    return static_cast<float>(v->num);
-}
-bool json_bool(const js::Value& o, const char* key, bool dflt) {
-    const js::Value* v = o.find(key);
-    if (!v || v->kind == js::Value::Kind::Null) return dflt;
-    if (!v->is_bool()) cfg_fail(std::string("'") + key + "' is not a boolean");
-    return v->b;
-}
+[[noreturn]] void config_error(const std::string& msg) { throw std::runtime_error(kConfigWho + msg); }
 
-const gg::Value& need_meta(const gg::File& f, const std::string& key) {
-    const gg::Value* v = f.find_meta(key);
-    if (!v) cfg_fail("from_gguf: missing metadata '" + key + "'");
-    return *v;
-}
+// ---- config.json -------------------------------------------------------------
 
-int meta_as_int(const gg::Value& v, const std::string& key) {
-    switch (v.type) {
-        case gg::ValueType::U8: return static_cast<int>(v.scalar.u8);
-        case gg::ValueType::I8: return static_cast<int>(v.scalar.i8);
-        case gg::ValueType::U16: return static_cast<int>(v.scalar.u16);
-        case gg::ValueType::I16: return static_cast<int>(v.scalar.i16);
-        case gg::ValueType::U32: return static_cast<int>(v.scalar.u32);
-        case gg::ValueType::I32: return static_cast<int>(v.scalar.i32);
-        case gg::ValueType::U64: return static_cast<int>(v.scalar.u64);
-        case gg::ValueType::I64: return static_cast<int>(v.scalar.i64);
-        default: cfg_fail("from_gguf: metadata '" + key + "' is not an integer scalar");
+// A JSON member of object type O: its key and the member it sets.  A key that
+// is missing or null leaves the default; a value of the wrong JSON type is an
+// error naming the key.
+template <class O>
+struct JsonRow {
+    std::string_view key;
+    std::variant<int O::*, float O::*, bool O::*> field;
+};
+
+template <class O, std::size_t N>
+void apply_rows(const js::Value& obj, const JsonRow<O> (&rows)[N], O& out) {
+    for (const JsonRow<O>& r : rows) {
+        const js::Value* v = obj.find(r.key);
+        if (!v || v->kind == js::Value::Kind::Null) continue;
+        const std::string quoted = "'" + std::string(r.key) + "'";
+        if (std::holds_alternative<bool O::*>(r.field)) {
+            if (!v->is_bool()) config_error(quoted + " is not a boolean");
+            out.*std::get<bool O::*>(r.field) = v->b;
+        } else {
+            if (!v->is_number()) config_error(quoted + " is not a number");
+            if (auto p = std::get_if<int O::*>(&r.field)) out.**p = static_cast<int>(v->num);
+            else out.*std::get<float O::*>(r.field) = static_cast<float>(v->num);
+        }
     }
 }
 
-float meta_as_f32(const gg::Value& v, const std::string& key) {
-    if (v.type == gg::ValueType::F32) return v.scalar.f32;
-    if (v.type == gg::ValueType::F64) return static_cast<float>(v.scalar.f64);
-    cfg_fail("from_gguf: metadata '" + key + "' is not a float scalar");
+// Top-level multimodal glue, kept for API parity.
+const JsonRow<Mistral3Config> kTopRows[] = {
+    {"image_token_index", &Mistral3Config::image_token_index},
+    {"spatial_merge_size", &Mistral3Config::spatial_merge_size},
+    {"multimodal_projector_bias", &Mistral3Config::multimodal_projector_bias},
+};
+// text_config.
+const JsonRow<Text> kTextRows[] = {
+    {"vocab_size", &Text::vocab_size},
+    {"hidden_size", &Text::hidden_size},
+    {"intermediate_size", &Text::intermediate_size},
+    {"num_hidden_layers", &Text::num_hidden_layers},
+    {"num_attention_heads", &Text::num_attention_heads},
+    {"num_key_value_heads", &Text::num_key_value_heads},
+    {"head_dim", &Text::head_dim},
+    {"rms_norm_eps", &Text::rms_norm_eps},
+    {"rope_theta", &Text::rope_theta},
+    {"tie_word_embeddings", &Text::tie_word_embeddings},
+    {"max_position_embeddings", &Text::max_position_embeddings},
+};
+
+// sliding_window: a number turns the window on; null or absent keeps full
+// causal attention.
+void read_window(const js::Value& tc, Text& t) {
+    const js::Value* sw = tc.find("sliding_window");
+    t.has_sliding_window = sw && sw->is_number();
+    t.sliding_window = t.has_sliding_window ? static_cast<int>(sw->num) : 0;
 }
 
-bool starts_with(std::string_view s, std::string_view p) { return s.size() >= p.size() && s.compare(0, p.size(), p) == 0; }
+// ---- GGUF metadata (keys after "<general.architecture>.") ---------------------
 
-brolm::detail::DenseDecoderConfig to_core_config(const Mistral3Config::Text& c) {
-    brolm::detail::DenseDecoderConfig d;
-    d.vocab_size = c.vocab_size;
-    d.hidden_size = c.hidden_size;
-    d.intermediate_size = c.intermediate_size;
-    d.num_hidden_layers = c.num_hidden_layers;
-    d.num_attention_heads = c.num_attention_heads;
-    d.num_key_value_heads = c.num_key_value_heads;
-    d.head_dim = c.head_dim;
-    d.rms_norm_eps = c.rms_norm_eps;
-    d.rope_theta = c.rope_theta;
-    d.use_qk_norm = false;
-    d.tie_word_embeddings = c.tie_word_embeddings;
-    return d;
-}
+const mt::IntRow<Text> kGgufInts[] = {
+    {"embedding_length", &Text::hidden_size, true, nullptr},
+    {"feed_forward_length", &Text::intermediate_size, true, nullptr},
+    {"block_count", &Text::num_hidden_layers, true, nullptr},
+    {"attention.head_count", &Text::num_attention_heads, true, nullptr},
+    {"attention.head_count_kv", &Text::num_key_value_heads, false,
+     [](const Text& t) { return t.num_attention_heads; }},
+    // Mistral 3.1's head_dim (128) is not hidden / heads (160): the derived
+    // value is only for files without the key
+    {"attention.key_length", &Text::head_dim, false, [](const Text& t) { return t.hidden_size / t.num_attention_heads; }},
+    {"context_length", &Text::max_position_embeddings, false, nullptr},
+};
+const mt::RealRow<Text> kGgufReals[] = {
+    {"attention.layer_norm_rms_epsilon", &Text::rms_norm_eps},
+    {"rope.freq_base", &Text::rope_theta},
+};
+
+// ---- validation ----------------------------------------------------------------
+
+struct Rule {
+    bool (*broken)(const Mistral3Config&);
+    const char* message;
+};
+const Rule kRules[] = {
+    {[](const Mistral3Config& c) {
+         const Text& t = c.text;
+         return t.hidden_size <= 0 || t.intermediate_size <= 0 || t.num_hidden_layers <= 0 || t.vocab_size <= 0 ||
+                t.head_dim <= 0;
+     },
+     "text_config has non-positive dimension"},
+    {[](const Mistral3Config& c) { return c.text.num_attention_heads <= 0 || c.text.num_key_value_heads <= 0; },
+     "num_attention_heads / num_key_value_heads must be positive"},
+    {[](const Mistral3Config& c) { return c.text.num_attention_heads % c.text.num_key_value_heads != 0; },
+     "num_attention_heads must be a multiple of num_key_value_heads"},
+    {[](const Mistral3Config& c) { return c.text.head_dim % 2 != 0; }, "head_dim must be even (RoPE rotates pairs)"},
+    {[](const Mistral3Config& c) { return c.spatial_merge_size <= 0; }, "spatial_merge_size must be positive"},
+};
 
 }  // namespace
 
-// ---- config ---------------------------------------------------------------
-
 Mistral3Config Mistral3Config::load(const std::string& path) {
-    std::ifstream f(path, std::ios::binary);
-    if (!f) cfg_fail("cannot open '" + path + "'");
-    std::ostringstream ss;
-    ss << f.rdbuf();
-    return from_json_text(ss.str());
+    std::ifstream in(path, std::ios::binary);
+    if (!in) config_error("cannot open '" + path + "'");
+    return from_json_text(std::string(std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>()));
 }
 
 Mistral3Config Mistral3Config::from_json_text(const std::string& text) {
@@ -107,129 +151,52 @@ Mistral3Config Mistral3Config::from_json_text(const std::string& text) {
     try {
         root = js::parse(text);
     } catch (const std::exception& e) {
-        cfg_fail(std::string("json parse: ") + e.what());
+        config_error(std::string("json parse: ") + e.what());
     }
-    if (!root.is_object()) cfg_fail("root is not a JSON object");
+    if (!root.is_object()) config_error("root is not a JSON object");
     Mistral3Config cfg;
-    cfg.image_token_index = json_int(root, "image_token_index", cfg.image_token_index);
-    cfg.spatial_merge_size = json_int(root, "spatial_merge_size", cfg.spatial_merge_size);
-    cfg.multimodal_projector_bias = json_bool(root, "multimodal_projector_bias", cfg.multimodal_projector_bias);
+    apply_rows(root, kTopRows, cfg);
     const js::Value* tc = root.find("text_config");
-    if (!tc) cfg_fail("missing text_config");
-    if (!tc->is_object()) cfg_fail("text_config is not an object");
-    Text& t = cfg.text;
-    t.vocab_size = json_int(*tc, "vocab_size", t.vocab_size);
-    t.hidden_size = json_int(*tc, "hidden_size", t.hidden_size);
-    t.intermediate_size = json_int(*tc, "intermediate_size", t.intermediate_size);
-    t.num_hidden_layers = json_int(*tc, "num_hidden_layers", t.num_hidden_layers);
-    t.num_attention_heads = json_int(*tc, "num_attention_heads", t.num_attention_heads);
-    t.num_key_value_heads = json_int(*tc, "num_key_value_heads", t.num_key_value_heads);
-    t.head_dim = json_int(*tc, "head_dim", t.head_dim);
-    t.rms_norm_eps = json_float(*tc, "rms_norm_eps", t.rms_norm_eps);
-    t.rope_theta = json_float(*tc, "rope_theta", t.rope_theta);
-    t.tie_word_embeddings = json_bool(*tc, "tie_word_embeddings", t.tie_word_embeddings);
-    t.max_position_embeddings = json_int(*tc, "max_position_embeddings", t.max_position_embeddings);
-    if (const js::Value* sw = tc->find("sliding_window"); sw && sw->is_number()) {
-        t.has_sliding_window = true;
-        t.sliding_window = static_cast<int>(sw->num);
-    }
-    if (!root.find("vision_config")) cfg_fail("missing vision_config");
+    if (!tc) config_error("missing text_config");
+    if (!tc->is_object()) config_error("text_config is not an object");
+    apply_rows(*tc, kTextRows, cfg.text);
+    read_window(*tc, cfg.text);
+    // the vision tower is outside this build; its section must still exist
+    if (!root.find("vision_config")) config_error("missing vision_config");
     cfg.validate();
     return cfg;
 }
 
 Mistral3Config Mistral3Config::from_gguf(const gg::File& f) {
-    const gg::Value& arch = need_meta(f, "general.architecture");
-    if (arch.type != gg::ValueType::String) cfg_fail("from_gguf: general.architecture is not a string");
-    const std::string a = arch.str + ".";
+    const std::string who = std::string(kConfigWho) + "from_gguf: ";
+    const gg::Value* arch = f.find_meta("general.architecture");
+    if (!arch) throw std::runtime_error(who + "missing metadata 'general.architecture'");
+    if (arch->type != gg::ValueType::String) throw std::runtime_error(who + "general.architecture is not a string");
+    const mt::Reader m(f, who, arch->str + ".");
     Mistral3Config cfg;
-    Text& t = cfg.text;
-    t.hidden_size = meta_as_int(need_meta(f, a + "embedding_length"), a + "embedding_length");
-    t.intermediate_size = meta_as_int(need_meta(f, a + "feed_forward_length"), a + "feed_forward_length");
-    t.num_hidden_layers = meta_as_int(need_meta(f, a + "block_count"), a + "block_count");
-    t.num_attention_heads = meta_as_int(need_meta(f, a + "attention.head_count"), a + "attention.head_count");
-    if (const auto* v = f.find_meta(a + "attention.head_count_kv"))
-        t.num_key_value_heads = meta_as_int(*v, a + "attention.head_count_kv");
-    else
-        t.num_key_value_heads = t.num_attention_heads;
-    if (const auto* v = f.find_meta(a + "attention.key_length"))
-        t.head_dim = meta_as_int(*v, a + "attention.key_length");
-    else
-        t.head_dim = t.hidden_size / t.num_attention_heads;
-    if (const auto* v = f.find_meta(a + "attention.layer_norm_rms_epsilon"))
-        t.rms_norm_eps = meta_as_f32(*v, a + "attention.layer_norm_rms_epsilon");
-    if (const auto* v = f.find_meta(a + "rope.freq_base")) t.rope_theta = meta_as_f32(*v, a + "rope.freq_base");
-    if (const auto* v = f.find_meta(a + "context_length"))
-        t.max_position_embeddings = meta_as_int(*v, a + "context_length");
-    if (const auto* toks = f.find_meta("tokenizer.ggml.tokens"); toks && toks->type == gg::ValueType::Array)
-        t.vocab_size = static_cast<int>(toks->array.size());
-    else if (const auto* vs = f.find_meta(a + "vocab_size"))
-        t.vocab_size = meta_as_int(*vs, a + "vocab_size");
-    t.tie_word_embeddings = f.find_tensor("output.weight") == nullptr;
+    mt::read_rows(m, kGgufInts, kGgufReals, cfg.text);
+    cfg.text.vocab_size = mt::vocab_size(m, cfg.text.vocab_size);
+    // Mistral checkpoints carry their own lm_head; without one it is tied
+    cfg.text.tie_word_embeddings = f.find_tensor("output.weight") == nullptr;
     cfg.validate();
     return cfg;
 }
 
 void Mistral3Config::validate() const {
-    if (text.hidden_size <= 0 || text.intermediate_size <= 0 || text.num_hidden_layers <= 0 ||
-        text.vocab_size <= 0 || text.head_dim <= 0)
-        cfg_fail("text_config has non-positive dimension");
-    if (text.num_attention_heads <= 0 || text.num_key_value_heads <= 0)
-        cfg_fail("num_attention_heads / num_key_value_heads must be positive");
-    if (text.num_attention_heads % text.num_key_value_heads != 0)
-        cfg_fail("num_attention_heads must be a multiple of num_key_value_heads");
-    if (text.head_dim % 2 != 0) cfg_fail("head_dim must be even (RoPE rotates pairs)");
-    if (spatial_merge_size <= 0) cfg_fail("spatial_merge_size must be positive");
+    for (const Rule& r : kRules)
+        if (r.broken(*this)) config_error(r.message);
 }
 
-// ---- text model -------------------------------------------------------------
+std::string mistral3_hf_to_ggml(std::string_view hf_name) { return mt::hf_to_ggml(hf_name, /*with_qk_norm=*/false); }
 
-std::string mistral3_hf_to_ggml(std::string_view hf_name) {
-    if (hf_name == "model.embed_tokens.weight") return "token_embd.weight";
-    if (hf_name == "model.norm.weight") return "output_norm.weight";
-    if (hf_name == "lm_head.weight") return "output.weight";
-    constexpr std::string_view kLayers = "model.layers.";
-    if (!starts_with(hf_name, kLayers)) return {};
-    const auto dot = hf_name.find('.', kLayers.size());
-    if (dot == std::string_view::npos) return {};
-    const std::string_view idx = hf_name.substr(kLayers.size(), dot - kLayers.size());
-    if (idx.empty()) return {};
-    for (char ch : idx)
-        if (ch < '0' || ch > '9') return {};
-    const std::string_view tail = hf_name.substr(dot + 1);
-    static constexpr std::pair<std::string_view, std::string_view> kMap[] = {
-        {"self_attn.q_proj.weight", "attn_q.weight"},
-        {"self_attn.k_proj.weight", "attn_k.weight"},
-        {"self_attn.v_proj.weight", "attn_v.weight"},
-        {"self_attn.o_proj.weight", "attn_output.weight"},
-        {"input_layernorm.weight", "attn_norm.weight"},
-        {"post_attention_layernorm.weight", "ffn_norm.weight"},
-        {"mlp.gate_proj.weight", "ffn_gate.weight"},
-        {"mlp.up_proj.weight", "ffn_up.weight"},
-        {"mlp.down_proj.weight", "ffn_down.weight"},
-    };
-    for (const auto& [hf, ggml] : kMap) {
-        if (tail != hf) continue;
-        std::string out = "blk.";
-        out.append(idx);
-        out.push_back('.');
-        out.append(ggml);
-        return out;
-    }
-    return {};
-}
-
-TextModel::TextModel(const Mistral3Config::Text& cfg) : cfg_(cfg), core_(to_core_config(cfg)) {}
+TextModel::TextModel(const Mistral3Config::Text& cfg) : cfg_(cfg), core_(mt::decoder_config(cfg, /*qk_norm=*/false)) {}
 TextModel::~TextModel() = default;
 
-void TextModel::load_weights(const gg::File& f) {
-    const std::vector<const gg::File*> shards = {&f};
-    load_weights(shards);
-}
+void TextModel::load_weights(const gg::File& f) { load_weights(std::vector<const gg::File*>{&f}); }
 
 void TextModel::load_weights(const std::vector<const gg::File*>& shards) {
-    if (shards.empty()) model_fail("load_weights: no gguf shards");
-    brolm::detail::weights::GgufSource src(shards, [](std::string_view hf) { return mistral3_hf_to_ggml(hf); });
+    if (shards.empty()) throw std::runtime_error("mistral3::TextModel: load_weights: no gguf shards");
+    const brolm::detail::weights::GgufSource src(shards, [](std::string_view hf) { return mistral3_hf_to_ggml(hf); });
     core_.load_weights(src);
 }
 
