@@ -129,14 +129,14 @@ void File::parse_() {
         const auto t = static_cast<ValueType>(r.get<std::uint32_t>());
         Value v = read_value(r, t, 0);
         if (key == "general.alignment") {
-            // a u32 in the spec; a power of two here, since data offsets are
-            // rounded to it
+            // a u32 in the spec, which asks for a multiple of 8; offsets are
+            // rounded to it by division, so no power of two is needed
             std::uint64_t a = 0;
             if (t == ValueType::U32) a = v.scalar.u32;
             else if (t == ValueType::U64) a = v.scalar.u64;
             else bad("general.alignment is not an unsigned integer");
-            if (a == 0 || (a & (a - 1)) != 0 || a > (1u << 20)) bad("general.alignment " + std::to_string(a) +
-                                                                   " is not a power of two up to 1 MiB");
+            if (a == 0 || a % 8 != 0 || a > (1u << 20))
+                bad("general.alignment " + std::to_string(a) + " is not a nonzero multiple of 8 up to 1 MiB");
             alignment_ = static_cast<std::uint32_t>(a);
         }
         meta_.emplace_back(std::move(key), std::move(v));

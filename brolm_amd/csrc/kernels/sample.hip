@@ -23,9 +23,11 @@
 //   token = the lowest index whose p is the largest level w with M'(w) > r.
 // The host draws u from the caller's std::mt19937_64 exactly as the reference
 // does (one uniform_real_distribution<double>(0, 1) per sampled token).
-// Ties: tokens of equal probability at a top-k boundary are all kept, and
-// within a level the lowest index is chosen, where the reference's std::sort
-// leaves the order of equal probabilities unspecified.
+// Ties: equal probabilities are ordered by ascending id.  A top-k cut keeps
+// exactly k ids, as the reference does: of the ids tied at the cut level, the
+// lowest-indexed ones that fit; the top-p cut likewise ends at one id.  The
+// reference's std::sort leaves the order of equal probabilities unspecified,
+// so ascending id is one of the orders it may produce.
 #include <cmath>
 
 #include "common.h"
@@ -303,7 +305,11 @@ __device__ int select_sorted(unsigned long long* key, int n, int k, float top_p,
 // them alone.
 constexpr int kBuckets = 2048;
 constexpr int kCand = 4096;
-constexpr double kFix = 17592186044416.0;   // 2^44
+// Fixed-point scale of the per-bucket mass: each e <= 1 adds at most 2^40,
+// so even kMaxSegs * kSeg = 2^22 ids cannot carry a 64-bit total past 2^62.
+// Truncating each e only lowers the running mass, which moves the floor down
+// (more candidates), never up.
+constexpr double kFix = 1099511627776.0;   // 2^40
 
 // e in [0, 1] maps to buckets 0 .. 2032; anything else (a NaN from bad
 // logits) to the last bucket, so the histogram stays in bounds

@@ -418,7 +418,8 @@ static or_gguf* parse(or_gguf* g) {
         t->type = (int)rd_u(&r, 4);
         t->offset = rd_u(&r, 8);
     }
-    if (r.bad || alignment == 0 || (alignment & (alignment - 1)) != 0) {
+    /* the spec asks for a multiple of 8 (docs/gguf.md, general.alignment) */
+    if (r.bad || alignment == 0 || alignment % 8 != 0 || alignment > ((uint64_t)1 << 20)) {
         snprintf(g_err, sizeof g_err, "gguf: truncated or malformed header");
         or_gguf_close(g);
         return NULL;

@@ -96,15 +96,16 @@ def tensors():
             ("output.weight", GGML_Q8_0, [32, 4], blocks)]
 
 
-def pad(n: int) -> int:
-    return (n + ALIGN - 1) // ALIGN * ALIGN
+def assemble(align: int = ALIGN) -> bytes:
+    """The fixture; with another `align` (written as general.alignment) the
+    same tensors at offsets and a data section rounded to that multiple."""
+    def pad(n: int) -> int:
+        return (n + align - 1) // align * align
 
-
-def assemble() -> bytes:
     ts = tensors()
     out = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(ts), len(KV)))
     for k, t, v in KV:
-        out += gstr(k) + struct.pack("<I", t) + value(t, v)
+        out += gstr(k) + struct.pack("<I", t) + value(t, align if k == "general.alignment" else v)
     offsets, off = [], 0
     for _, _, _, data in ts:
         offsets.append(off)

@@ -120,6 +120,41 @@ def test_qwen3_config_and_dequant_from_spec_file():
     assert oracle.dequant(t, data, 32)[31] == 1.96875
 
 
+def test_alignment_24_read_by_both():
+    """general.alignment 24: a multiple of 8 (all the spec asks) and no power
+    of two.  The same tensors, assembled at offsets 0, 528, 600 of a data
+    section starting at 912 (the 911-byte header rounded up to 24), read back
+    by both readers."""
+    sys.path.insert(0, str(GOLD))
+    import make_gguf_fixture
+    b = make_gguf_fixture.assemble(align=24)
+    data0 = 912
+    offsets = [0, 528, 600]
+    assert b[data0:data0 + 4] == struct.pack("<f", -16.0)
+    from brolm_amd import _native
+    lib = _native.lib()
+    assert _product_ok(lib, b) and _oracle_ok(b)
+    buf = C.create_string_buffer(b, len(b))
+    h = oracle.lib().or_gguf_open_memory(C.cast(buf, C.c_void_p), len(b))
+    assert h
+    try:
+        for (name, gt, dims, _, nb), off in zip(TENSORS, offsets):
+            i = oracle.lib().or_gguf_find_tensor(C.c_void_p(h), name.encode())
+            assert i >= 0 and oracle.lib().or_gguf_tensor_nbytes(C.c_void_p(h), i) == nb
+            p = oracle.lib().or_gguf_tensor_data(C.c_void_p(h), i)
+            assert C.string_at(p, nb) == b[data0 + off:data0 + off + nb], name
+    finally:
+        oracle.lib().or_gguf_close(C.c_void_p(h))
+    import tempfile
+    with tempfile.NamedTemporaryFile(suffix=".gguf") as f:
+        f.write(b)
+        f.flush()
+        for (name, gt, dims, _, nb), off in zip(TENSORS, offsets):
+            out = (C.c_uint8 * nb)()
+            assert lib.brolm_gguf_tensor_data(f.name.encode(), name.encode(), out, nb) == nb
+            assert bytes(out) == b[data0 + off:data0 + off + nb], name
+
+
 # ----------------------------------------------------------------- malformed variants
 
 def _product_ok(lib, b: bytes) -> bool:
@@ -160,7 +195,8 @@ def _patched(raw: bytes, pos: int, fmt: str, value) -> bytes:
 
 
 @pytest.mark.parametrize("case", ["misaligned_offset", "offset_past_end", "offset_wraps", "dim_overflow",
-                                  "zero_dim", "array_count_huge", "alignment_zero", "alignment_not_pow2",
+                                  "zero_dim", "array_count_huge", "alignment_zero", "alignment_not_mult8",
+                                  "alignment_huge",
                                   "version_2", "bad_magic", "unknown_value_type", "too_many_dims"])
 def test_malformed_headers_are_refused(raw, lib, case):
     out_pos = _field(raw, "output.weight")          # u32 n_dims, u64 dims[2], u32 type, u64 offset
@@ -176,7 +212,8 @@ def test_malformed_headers_are_refused(raw, lib, case):
         "zero_dim": lambda: _patched(raw, emb_pos + 12, "<Q", 0),
         "array_count_huge": lambda: _patched(raw, arr_pos, "<Q", 1 << 60),
         "alignment_zero": lambda: _patched(raw, align_pos, "<I", 0),
-        "alignment_not_pow2": lambda: _patched(raw, align_pos, "<I", 48),
+        "alignment_not_mult8": lambda: _patched(raw, align_pos, "<I", 4),   # divides every offset
+        "alignment_huge": lambda: _patched(raw, align_pos, "<I", 1 << 21),
         "version_2": lambda: _patched(raw, 4, "<I", 2),
         "bad_magic": lambda: b"GGUG" + raw[4:],
         "unknown_value_type": lambda: _patched(raw, key_pos, "<I", 13),

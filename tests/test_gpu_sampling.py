@@ -7,8 +7,9 @@ Criterion: the device id equals the oracle's, except (a) an id of equal
 logit (the reference's std::sort leaves the order of equal probabilities
 unspecified) or (b) a draw within 1e-5 of the kept mass from the boundary of
 the oracle's interval (FP32 / FP64 summation order moves boundaries by ~1e-7);
-(b) is counted and printed.  Logits are distinct where the top-k / top-p cut
-falls, so the device's keep-all-ties rule at the cut never applies."""
+(b) is counted and printed.  At a top-k cut both keep exactly k ids, ties
+ordered by ascending id (the oracle's sort and the device agree on that
+order), so ties at the cut need no exception."""
 from __future__ import annotations
 
 import ctypes as C
@@ -150,8 +151,8 @@ def test_device_sampled_decode_matches_per_token_sampling(env, small_gguf, cap):
     host round trip; with a cache beyond the fused step's, the op path) picks,
     at every step, the oracle sampler's id for that step's own logits and draw
     (a second model fed the same tokens gives the logits), up to the first
-    draw within 1e-5 of an interval boundary or an FP16 tie at the top-k cut
-    (criteria as above)."""
+    draw within 1e-5 of an interval boundary (criteria as above); an FP16
+    tie where the kept set ends is checked like any other step."""
     import brolm_amd as ba
     print(f"[sample] decode_sampled cap={cap}", flush=True)
     mods = []
@@ -171,15 +172,16 @@ def test_device_sampled_decode_matches_per_token_sampling(env, small_gguf, cap):
     u = rng.random(n)
     got = a.decode_sampled(first, u, T, k, p)
     assert len(got) == n
-    checked = 0
+    checked = ties = 0
     for i in range(n):
         lg = np.asarray(b.forward_last([first if i == 0 else got[i - 1]]), dtype=np.float32).reshape(-1)
         want, margin = oracle.sample_token(lg, T, k, p, float(u[i]))
-        if margin < 1e-5 or _tie_at_cut(lg, T, k, p):
-            continue  # boundary draw, or an FP16 tie where the kept set ends (the device keeps every tie)
-        assert got[i] == want or lg[got[i]] == lg[want], (i, got[i], want)
+        if margin < 1e-5:
+            continue  # boundary draw
+        assert got[i] == want, (i, got[i], want, bool(_tie_at_cut(lg, T, k, p)))
+        ties += bool(_tie_at_cut(lg, T, k, p))
         checked += 1
-    print(f"[sample] {checked} of {n} steps checked", flush=True)
+    print(f"[sample] {checked} of {n} steps checked, {ties} with an FP16 tie at the cut", flush=True)
     assert checked >= n // 3
     assert a.cache_len() == len(prompt) + n
     for m in mods:
