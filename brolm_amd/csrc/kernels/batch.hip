@@ -178,7 +178,7 @@ struct BatchAttnArgs {
     int64_t cache_rows;
     int n_q, n_kv, S, kps, P, HPW;
     float* recs;       // (row, group) x S x G records of HD + 2 floats
-    uint64_t* cnt;     // rows x n_kv counter words {tag, arrivals}, zero between launches
+    uint64_t* cnt;     // rows x n_kv counter words (tagged_arrive), zero between launches
     uint32_t tag;      // this launch's tag (nonzero)
     uint16_t* out;     // rows x n_q HD
 };
@@ -426,19 +426,10 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // {tag, arrivals}: a word left by another launch (one that did not
-    // finish) counts as zero arrivals; the last arrival clears the word
+    // the split's arrival count (tagged_arrive: a word left by a launch that
+    // did not finish is not counted; the last arrival clears the word)
     uint64_t* cn = a.cnt + (int64_t)r * a.n_kv + g;
-    if (threadIdx.x == 0) {
-        uint64_t old = __hip_atomic_load(cn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint64_t nw;
-        do {
-            const uint32_t n = (uint32_t)(old >> 32) == a.tag ? (uint32_t)old + 1u : 1u;
-            nw = ((uint64_t)a.tag << 32) | n;
-        } while (!__hip_atomic_compare_exchange_weak(cn, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-        last = (uint32_t)nw == (uint32_t)a.S ? 1u : 0u;
-    }
+    if (threadIdx.x == 0) last = tagged_arrive(cn, a.tag) == (uint32_t)a.S ? 1u : 0u;
     __syncthreads();
     if (!last) return;
 

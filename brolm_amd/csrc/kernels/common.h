@@ -29,8 +29,7 @@ int num_cus();
 bool profiler_attached();
 
 // A new nonzero 32-bit tag per call (1, 2, ..., wrapping past 0), for
-// kernels whose workgroups count arrivals in caller memory: a counter word
-// carrying another launch's tag is treated as empty.
+// kernels whose workgroups count arrivals in caller memory (tagged_arrive).
 uint32_t next_launch_tag();
 // Workgroups of `threads` threads and `lds` dynamic LDS bytes that one CU
 // holds at once for kernel `fn` (registers and LDS); asked of the runtime once
@@ -196,6 +195,49 @@ __device__ __forceinline__ void q4k_scale_min_regs(uint32_t y, uint32_t z, uint3
         sc = (int)((bw & 0x0f) | ((by >> 6) << 4));
         m = (int)((bw >> 4) | ((bz >> 6) << 4));
     }
+}
+
+
+// One workgroup's arrival at a counter word in caller memory that the last
+// arrival of a launch puts back to zero; returns the arrival's number (1 for
+// the first).  The word is {sum of the arrivals' tags mod 2^32 (high half),
+// arrivals (low half)}, "clean" for tag T when high == low * T.  An arrival
+// adds (T, 1) in one atomic; when the word it added to was not clean for T
+// (left by a launch that never finished, or never cleared), the arrival
+// restarts the count at (T, 1) by compare-and-swap, or joins a count another
+// arrival of the same launch already restarted: a clean word stays clean, so
+// no other launch's arrivals are ever counted.  Replays of a captured launch
+// reuse one tag; each finds the word at zero.
+__device__ __forceinline__ uint32_t tagged_arrive(uint64_t* word, uint32_t tag) {
+    const uint64_t add = ((uint64_t)tag << 32) | 1u;
+    auto clean = [tag](uint64_t v) { return (uint32_t)(v >> 32) == (uint32_t)v * tag; };
+    const uint64_t old = __hip_atomic_fetch_add(word, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (clean(old)) return (uint32_t)old + 1u;
+    uint64_t cur = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nw;
+    do {
+        nw = clean(cur) ? cur + add : add;
+    } while (!__hip_atomic_compare_exchange_weak(word, &cur, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+    return (uint32_t)nw;
+}
+
+// Scales and mins of sub-blocks 2c and 2c+1 (c = 0..3) of a Q4_K block from
+// its scale dwords y (bytes 0-3), z (bytes 4-7), w (bytes 8-11): the same
+// values as q4k_scale_min_regs, as eight bit-field extracts whichever half c
+// falls in.  Sub-blocks 0-3 keep 6 bits in bytes j (scale) and j+4 (min);
+// sub-blocks 4-7 keep the low 4 bits in the nibbles of byte j+4 and the high
+// 2 bits in the top bits of bytes j-4 (scale) and j (min).  A width-0 field
+// reads as 0, which drops the high part for the first half.
+__device__ __forceinline__ void q4k_pair_scales(uint32_t y, uint32_t z, uint32_t w, int c, int& sc0, int& m0,
+                                                int& sc1, int& m1) {
+    const bool lo = c < 2;
+    const uint32_t o = 16u * (uint32_t)(c & 1);
+    const uint32_t as = lo ? y : w, am = lo ? z : w;
+    const uint32_t wl = lo ? 6u : 4u, wh = lo ? 0u : 2u, om = lo ? o : o + 4u;
+    sc0 = (int)(__builtin_amdgcn_ubfe(as, o, wl) | (__builtin_amdgcn_ubfe(y, o + 6u, wh) << 4));
+    sc1 = (int)(__builtin_amdgcn_ubfe(as, o + 8u, wl) | (__builtin_amdgcn_ubfe(y, o + 14u, wh) << 4));
+    m0 = (int)(__builtin_amdgcn_ubfe(am, om, wl) | (__builtin_amdgcn_ubfe(z, o + 6u, wh) << 4));
+    m1 = (int)(__builtin_amdgcn_ubfe(am, om + 8u, wl) | (__builtin_amdgcn_ubfe(z, o + 14u, wh) << 4));
 }
 
 }  // namespace bx

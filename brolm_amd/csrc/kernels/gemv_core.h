@@ -104,8 +104,7 @@ __device__ __forceinline__ void dot_unit(const RawQ4K& r, int u, const uint32_t*
     const int e_hi = e_lo + 32;
     const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
     int sc0, m0, sc1, m1;
-    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c, sc0, m0);
-    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c + 1, sc1, m1);
+    q4k_pair_scales(r.h.y, r.h.z, r.h.w, c, sc0, m0, sc1, m1);
     const float s_lo = d * (float)sc0, s_hi = d * (float)sc1;
     // sum x*(d*sc*q - dmin*m) with q = (q-8) + 8: s*acc + (8s - dmin*m) * X
     const float c_lo = 8.f * s_lo - dmin * (float)m0;
@@ -405,8 +404,7 @@ __device__ __forceinline__ float dot_reg(const RawQ4K& r, int u, const XU& x) {
     const int c = (u & 7) >> 1;
     const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
     int sc0, m0, sc1, m1;
-    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c, sc0, m0);
-    q4k_scale_min_regs(r.h.y, r.h.z, r.h.w, 2 * c + 1, sc1, m1);
+    q4k_pair_scales(r.h.y, r.h.z, r.h.w, c, sc0, m0, sc1, m1);
     const uint32_t mg = magic_vgpr();
     const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float al = 0.f, ah = 0.f;

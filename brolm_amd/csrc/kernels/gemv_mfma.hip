@@ -120,8 +120,7 @@ struct Chunk<FMT_Q4_K> {
         const uint32_t xm1 = x.xs2[(e0 >> 5) * 16 + (2 * g + 1) * 16 + r];
         const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
         int sc0, m0, sc1, m1;
-        q4k_scale_min_regs(hdr.y, hdr.z, hdr.w, 2 * g, sc0, m0);
-        q4k_scale_min_regs(hdr.y, hdr.z, hdr.w, 2 * g + 1, sc1, m1);
+        q4k_pair_scales(hdr.y, hdr.z, hdr.w, g, sc0, m0, sc1, m1);
         // (1024 + q) * sc - 1024 sc = sc q, one rounding of an exact integer
         const h2 s_lo = {(_Float16)sc0, (_Float16)sc0}, c_lo = {(_Float16)(-1024 * sc0), (_Float16)(-1024 * sc0)};
         const h2 s_hi = {(_Float16)sc1, (_Float16)sc1}, c_hi = {(_Float16)(-1024 * sc1), (_Float16)(-1024 * sc1)};
@@ -732,23 +731,9 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // The group's counter word is {tag (high 32 bits), arrivals}.  A word
-    // carrying another launch's tag (one that never finished, or memory
-    // never cleared) counts as zero arrivals, so no earlier launch's count
-    // can make this launch add its partials early or never; the last
-    // arrival puts the word back to zero, which keeps replays of a captured
-    // launch (same tag every time) correct.
-    if (threadIdx.x == 0) {
-        uint64_t* c = &job.cnt[blockIdx.x];
-        uint64_t old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint64_t nw;
-        do {
-            const uint32_t n = (uint32_t)(old >> 32) == job.tag ? (uint32_t)old + 1u : 1u;
-            nw = ((uint64_t)job.tag << 32) | n;
-        } while (!__hip_atomic_compare_exchange_weak(c, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-        last = (uint32_t)nw == (uint32_t)S ? 1u : 0u;
-    }
+    // the group's arrival count (a word left by a launch that never finished
+    // is not counted; the last arrival puts the word back to zero)
+    if (threadIdx.x == 0) last = tagged_arrive(&job.cnt[blockIdx.x], job.tag) == (uint32_t)S ? 1u : 0u;
     __syncthreads();
     if (!last) return;
     if (live && lane < pl) {

@@ -296,11 +296,32 @@ __device__ __forceinline__ constexpr int sum_lane(int g) {
 // ---- weight rows ---------------------------------------------------------------
 
 // One 32-element unit of any quant format in registers (48 bytes):
-//   Q4_K: a = qs, b = d / dmin / scales;  Q6_K: a = ql, b.xy = qh, b.z = d,
-//   c = scales;  Q8_0: a, b = qs, c.x = d.
+//   Q4_K: a = qs, b = d / dmin / scales;  Q6_K: a = ql, b = scales,
+//   c.xy = qh, c.z = d;  Q8_0: a, b = qs, c.x = d.
 struct RawAny {
     u4v a, b, c;
 };
+
+// A Q4_K or Q6_K unit into RawAny with the same four loads whichever the
+// format (`q6` picks the addresses).  A stage whose format is known only at
+// run time (attn_v, ffn_down) then requests its rows without a branch: with a
+// branch per format the loaded registers meet at the join, and the wave waits
+// there for its loads.  Q4_K's last two loads re-read bytes of its own unit.
+__device__ __forceinline__ void load_any_kq(RawAny& r, bool q6, const void* W, int64_t N, int64_t K, int64_t n,
+                                            int u) {
+    const uint8_t* p = static_cast<const uint8_t*>(W);
+    const int64_t nb = K / 256, s = n * nb + (u >> 3), plane = N * nb;
+    const uint8_t* pa = p + s * 128 + 16 * (u & 7);                        // qs / ql
+    const uint8_t* pb = p + plane * (q6 ? 192 : 128) + s * 16;             // header / scales
+    const uint8_t* pc = q6 ? p + plane * 128 + s * 64 + 8 * (u & 7) : pa;  // qh
+    const uint8_t* pd = q6 ? p + plane * 208 + s * 2 : pb;                 // d
+    r.a = ldg_nt16(pa);
+    r.b = ldg16(pb);
+    const u2v c = ldg_nt8(pc);
+    r.c.x = c.x;
+    r.c.y = c.y;
+    r.c.z = ldg_u16(pd);
+}
 
 template <int FMT>
 __device__ __forceinline__ void load_any(RawAny& r, const void* W, int64_t N, int64_t K, int64_t n, int u) {
@@ -311,10 +332,10 @@ __device__ __forceinline__ void load_any(RawAny& r, const void* W, int64_t N, in
     } else if constexpr (FMT == FMT_Q6_K) {
         const RawQ6K q = load_unit<FMT_Q6_K>(W, N, K, n, u);
         r.a = q.ql;
-        r.b.x = q.qh.x;
-        r.b.y = q.qh.y;
-        r.b.z = q.d;
-        r.c = q.sc;
+        r.b = q.sc;
+        r.c.x = q.qh.x;
+        r.c.y = q.qh.y;
+        r.c.z = q.d;
     } else if constexpr (FMT == FMT_Q8_0) {
         const RawQ8 q = load_unit<FMT_Q8_0>(W, N, K, n, u);
         r.a = q.q0;
@@ -332,10 +353,10 @@ __device__ __forceinline__ float dot_any(const RawAny& r, int u, const XU& x) {
     } else if constexpr (FMT == FMT_Q6_K) {
         RawQ6K q;
         q.ql = r.a;
-        q.qh.x = r.b.x;
-        q.qh.y = r.b.y;
-        q.d = r.b.z;
-        q.sc = r.c;
+        q.sc = r.b;
+        q.qh.x = r.c.x;
+        q.qh.y = r.c.y;
+        q.d = r.c.z;
         return dot_reg(q, u, x);
     } else {
         RawQ8 q;
@@ -397,6 +418,21 @@ struct Task {
     __device__ __forceinline__ void load(const void* W, int64_t N, int64_t K, int uc0, int U, int r0) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) load_pass<FMT>(W, N, K, uc0, U, r0, p);
+    }
+    // Pass p of a Q4_K or Q6_K matrix whose format is a run-time value
+    // (RawAny storage only): the same loads either way.
+    __device__ __forceinline__ void load_pass_kq(bool q6, const void* W, int64_t N, int64_t K, int uc0, int U, int r0,
+                                                 int p) {
+        static_assert(std::is_same_v<Raw, RawAny>);
+        const int lane = tidx() & 63;
+        const int slot = lane & (LPR - 1), rip = lane / LPR;
+        int64_t row = r0 + p * RPP + rip;
+        row = row < N ? row : N - 1;
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const int u = slot + LPR * i;
+            load_any_kq(raw[p][i], q6, W, N, K, row, uc0 + (u < U ? u : U - 1));
+        }
     }
 
     template <int FMT>
@@ -1159,7 +1195,12 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
     constexpr int RA = NA * (64 / LA), RC = NC * (64 / LC), RD = ND * (64 / LD), RE = NE * (64 / LE);
     const int UAn = H / 32, UCn = slice_o / 32, UEn = Fx / 32;
 
-    Task<std::conditional_t<(FV2 < 0 && FV == FQ), typename RawOf<FQ>::T, RawAny>, LA, UA, NA> ta;
+    using RawA = std::conditional_t<(FV2 < 0 && FV == FQ), typename RawOf<FQ>::T, RawAny>;
+    // run-time formats limited to Q4_K / Q6_K take the branch-free requests
+    constexpr auto kq = [](int f) { return f < 0 || f == FMT_Q4_K || f == FMT_Q6_K; };
+    constexpr bool kAnyA = std::is_same_v<RawA, RawAny> && kq(FQ) && kq(FV) && kq(FV2);
+    constexpr bool kAnyE = std::is_same_v<RawFor<FD, FD2>, RawAny> && kq(FD) && kq(FD2);
+    Task<RawA, LA, UA, NA> ta;
     Task<typename RawOf<FO>::T, LC, UC, NC> tc;
     Task<typename RawOf<FGU>::T, LD, UD, ND> tg, tu;
     Task<RawFor<FD, FD2>, LE, UE, NE> te;
@@ -1173,9 +1214,13 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
     // without rows loads harmless copies, so the loads stay unconditional)
     auto load_a_pass = [&](const bx_decode_layer& Ly, int p, int zl) {
         const int f = a_fmt(Ly);
-        if (seg != 2 || f == FQ) ta.template load_pass<FQ>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
-        else if (f == FV) ta.template load_pass<FV>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
-        else if constexpr (FV2 >= 0) ta.template load_pass<FV2>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+        if constexpr (kAnyA) {
+            ta.load_pass_kq(f == FMT_Q6_K, a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+        } else {
+            if (seg != 2 || f == FQ) ta.template load_pass<FQ>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+            else if (f == FV) ta.template load_pass<FV>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+            else if constexpr (FV2 >= 0) ta.template load_pass<FV2>(a_w(Ly), aN, H, 0, UAn, srow0 + awb + zl, p);
+        }
     };
     const int uc_o = (min(x, a.nu - 1) * slice_o) / 32;
     auto load_d = [&](const bx_decode_layer& Ly, int zl) {
@@ -1183,13 +1228,17 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, dwb + zl);
     };
     auto load_e_pass = [&](const bx_decode_layer& Ly, int p, int zl) {
-        if (Ly.type_down == FD) te.template load_pass<FD>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
-        else if constexpr (FD2 >= 0) te.template load_pass<FD2>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+        if constexpr (kAnyE) {
+            te.load_pass_kq(Ly.type_down == FMT_Q6_K, Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+        } else {
+            if (Ly.type_down == FD) te.template load_pass<FD>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+            else if constexpr (FD2 >= 0) te.template load_pass<FD2>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+        }
     };
 
-    tile_prefetch<HD>(a, w, lt[0], pos, tile);
 #pragma unroll
     for (int p = 0; p < NA; ++p) load_a_pass(lt[0], p, opaque_zero());
+    tile_prefetch<HD>(a, w, lt[0], pos, tile);
     pin();
 
     for (int l = 0; l < a.L; ++l) {
@@ -1207,6 +1256,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     return;
                 sub(a, l, 0);
                 if (!apply_update(a, ar, a.hupd + zl, x, tag_of(a, l - 1, 6), 7, ss)) return;
+                sub(a, l, 7);
             } else {
                 for (int i = tidx(); i < H; i += kT) ss += ar.hv[i] * ar.hv[i];
             }
@@ -1216,6 +1266,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             // Wo rows stream while q / k / v are computed and travel
             if (unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o + zl, UCn, cwb);
             pin();
+            sub(a, l, 8);
             if (unit && awb < awe) {
                 auto run = [&](auto fmt_tag) {
                     constexpr int F = decltype(fmt_tag)::value;
@@ -1233,6 +1284,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                 else if (f == FV) run(std::integral_constant<int, FV>{});
                 else if constexpr (FV2 >= 0) run(std::integral_constant<int, FV2>{});
             }
+            sub(a, l, 9);
             __syncthreads();
             if (unit)
                 emit_words<false>(ar.rows, arb, are, wseg, a.qkv + (int64_t)x * a.qkv_stride + woff + zl,
@@ -1249,6 +1301,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             // gate / up rows stream while the Wo partials travel
             load_d(Ly, zl);
             pin();
+            sub(a, l, 17);
             {
                 XRegs<FO, LC, UC> xr;
                 xr.load(ar.xs, ar.xsum, UCn);
@@ -1259,6 +1312,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     emit_rows<LC, NC>(t0, cwe, o, [&](int row, float v) { ar.rows[row - hb] = v; });
                 }
             }
+            sub(a, l, 18);
             __syncthreads();
             emit_partial(a, ar, a.pwo + zl, x, r, tag_of(a, l, 2));
         } else {
@@ -1274,6 +1328,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                 return;
             sub(a, l, 10);
             if (!apply_update(a, ar, a.hupo + zl, x, tag_of(a, l, 5), 8, ss)) return;
+            sub(a, l, 11);
             __syncthreads();
             norm_to_xs(ar, H, ss, Ly.post_ln, a.eps);
             stamp(a, sl + 5);
@@ -1281,6 +1336,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
 #pragma unroll
             for (int p = 0; p < NE; ++p) load_e_pass(Ly, p, zl);
             pin();
+            sub(a, l, 13);
             if (dwb < dwe) {
                 XRegs<FGU, LD, UD> xr;
                 xr.load(ar.xs, ar.xsum, UAn);
@@ -1305,6 +1361,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             __syncthreads();
             emit_words<false>(ar.rows, gb, ge, a.wact, a.act + (int64_t)x * a.act_stride + r * a.wact + zl,
                               tag_of(a, l, 3));
+            sub(a, l, 14);
         }
         stamp(a, sl + 6);
         // ---- E: the slice's SwiGLU output, Wd partial; the next layer's q / k /
@@ -1324,6 +1381,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     }
                 });
             if (!__syncthreads_and(ok)) return;
+            sub(a, l, 31);
             sums8_from_lds(ar.xs, Fx, ar.xsum);
             __syncthreads();
             stamp(a, sl + 7);
@@ -1343,15 +1401,19 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             sub(a, l, 30);
             __syncthreads();
             emit_partial(a, ar, a.pdn + zl, x, r, tag_of(a, l, 4));
+            sub(a, l, 32);
         }
-        // the next layer's attention tile and q / k / v rows stream while the
-        // down partials travel
+        // the next layer's q / k / v rows, then its attention tile, stream
+        // while the down partials travel (the tile's LDS-DMA goes last: the
+        // first LDS access after it waits for every load still outstanding,
+        // and the next poll waits for those anyway)
         if (l + 1 < a.L) {
-            tile_prefetch<HD>(a, w, Ln, pos, tile);
 #pragma unroll
             for (int p = 0; p < NA; ++p) load_a_pass(Ln, p, zl);
+            tile_prefetch<HD>(a, w, Ln, pos, tile);
         }
         pin();
+        sub(a, l, 33);
         stamp(a, sl + 8);
     }
 
