@@ -436,8 +436,7 @@ struct Task {
     }
 
     template <int FMT>
-    __device__ __forceinline__ float dot_pass(const XRegs<FMT, LPR, UPL>& xr, int U, int p) const {
-        const int slot = (tidx() & 63) & (LPR - 1);
+    __device__ __forceinline__ float dot_pass(const XRegs<FMT, LPR, UPL>& xr, int U, int p, int slot) const {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < UPL; ++i) {
@@ -456,9 +455,12 @@ struct Task {
     // between passes, so the texture unit works while the SIMD computes).
     template <int FMT, class Side>
     __device__ __forceinline__ void dot(const XRegs<FMT, LPR, UPL>& xr, int U, float (&out)[NP], Side side) const {
+        // one lane slot for every pass, so the unit-dependent values (scale
+        // positions, activation offsets) are formed once, not per pass
+        const int slot = (tidx() & 63) & (LPR - 1);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            out[p] = dot_pass<FMT>(xr, U, p);
+            out[p] = dot_pass<FMT>(xr, U, p, slot);
             side(p);
             pin();
         }
@@ -466,8 +468,9 @@ struct Task {
     }
     template <int FMT>
     __device__ __forceinline__ void dot(const XRegs<FMT, LPR, UPL>& xr, int U, float (&out)[NP]) const {
+        const int slot = (tidx() & 63) & (LPR - 1);
 #pragma unroll
-        for (int p = 0; p < NP; ++p) out[p] = dot_pass<FMT>(xr, U, p);
+        for (int p = 0; p < NP; ++p) out[p] = dot_pass<FMT>(xr, U, p, slot);
         group_sum<LPR, NP>(out);
     }
 };
@@ -477,10 +480,11 @@ template <int FMT, class Raw, int LPR, int UPL, int NP, class Side>
 __device__ __forceinline__ void dot_pair(const Task<Raw, LPR, UPL, NP>& ta, const Task<Raw, LPR, UPL, NP>& tb,
                                          const XRegs<FMT, LPR, UPL>& xr, int U, float (&oa)[NP], float (&ob)[NP],
                                          Side side) {
+    const int slot = (tidx() & 63) & (LPR - 1);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-        oa[p] = ta.template dot_pass<FMT>(xr, U, p);
-        ob[p] = tb.template dot_pass<FMT>(xr, U, p);
+        oa[p] = ta.template dot_pass<FMT>(xr, U, p, slot);
+        ob[p] = tb.template dot_pass<FMT>(xr, U, p, slot);
         side(p);
         pin();
     }
