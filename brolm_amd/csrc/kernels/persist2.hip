@@ -1594,9 +1594,10 @@ constexpr int Q4 = FMT_Q4_K, Q6 = FMT_Q6_K, Q8 = FMT_Q8_0, F16 = FMT_F16;
 // Shapes with an instantiation: the BASELINE widths and the test models.  The
 // first argument says whether a shape runs here even where the first
 // persistent kernel has an instantiation: measured on MI355X (decode steps at
-// a 1024-token context), this kernel takes 0.80 ms at the 0.6B Q8_0 widths
-// against 0.97 ms there, but 1.07 / 2.69 / 2.62 ms at the 1.7B / 8B /
-// Llama-3-8B widths against 1.04 / 2.58 / 2.51 ms.
+// a 1024-token context, ms, this kernel / the first), 0.6B Q8_0 0.788 / 0.976,
+// 8B Q4_K 2.386 / 2.469, 1.7B Q4_K 1.041 / 1.030, Llama-3-8B widths
+// 2.499 / 2.431.  The 1.7B Q4_K_M layout has no instantiation there
+// (1.073 here against 1.387 for the captured per-stage graph).
 // Per stage (lanes per row, units per lane, passes): a wave's first task is
 // requested one stage ahead; rows past it load in place.
 const Entry kTable[] = {
@@ -1608,7 +1609,7 @@ const Entry kTable[] = {
     // Qwen3-0.6B (H 1024, F 3072): Q8_0 with the tied FP16 head
     P2(true, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1, 4),
     // Qwen3-8B (H 4096, F 12288, 32 / 8 heads): Q4_K, Q6_K head
-    P2(false, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2, 4),
+    P2(true, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2, 4),
     // Llama-3-8B widths (H 4096, F 14336): Q4_K with Q6_K v / down and head
     P2(false, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64, 2, 4),
     // test models: H 256 / head_dim 64 with F 2048 (Q4_K, Q6_K or Q4_K v / down, Q6_K head)
