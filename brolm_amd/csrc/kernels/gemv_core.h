@@ -394,7 +394,16 @@ __device__ __forceinline__ uint32_t magic_vgpr() {
     asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
     return r;
 }
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
+// (x & m) | c as one v_and_or_b32, the mask in an SGPR (on gfx9 a VOP3
+// instruction reads at most one scalar operand and no literal).  Written out:
+// for two nested and-ors (Q6_K's low nibble, then its two high bits) the
+// instruction selector emits two ANDs and a three-input OR, three
+// instructions where two do.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+    return r;
+}
 
 // Q4_K unit: low nibbles (bits 0-3 of each byte) give 1024 + q, high nibbles
 // masked in place (bits 4-7) give 1024 + 16 q, so

@@ -492,34 +492,37 @@ struct WgRows {
     }
 };
 
-// lm_head rows [r0, r1): two blocks in flight per wave, the next task's loads
-// issued before the current task's math.  The first task is loaded by the
-// caller (before the final norm's input arrives).
-template <int FMT, int UPL, int R, class Epi>
-__device__ __forceinline__ void head_rows(RowBlock<FMT, UPL, R>& b0, RowBlock<FMT, UPL, R>& b1, const void* W,
-                                          int64_t N, int K, int r0, int r1, const Arena& ar, Epi epi) {
+// lm_head rows [r0, r1) with NB blocks in turn: while a task's math runs,
+// the next NB - 1 tasks' loads are in flight (a wave's tasks are r0 + wave R,
+// then every kPW R rows).  The caller loads b[0]; the requests are
+// unconditional, a task past the range re-reading the range's last rows, so
+// the compiler's wait before each task's math counts exactly the loads issued
+// after it.
+template <int FMT, int UPL, int R, int NB, class Epi>
+__device__ __forceinline__ void head_rows_nb(RowBlock<FMT, UPL, R> (&b)[NB], const void* W, int64_t N, int K,
+                                             int r0, int r1, const Arena& ar, Epi epi) {
     const int lane = tidx() & 63;
     const int step = kPW * R;
+    const int t0 = r0 + (int)(tidx() >> 6) * R;
+    auto at = [&](int t) { return t < r1 ? t : (r1 - R > r0 ? r1 - R : r0); };
+#pragma unroll
+    for (int j = 1; j < NB - 1; ++j) b[j].load(W, N, K, at(t0 + j * step));
     XCache<FMT, UPL> xu;
     xu.init(ar.xs, ar.xsum, K);
-    auto emit = [&](int t, const float (&o)[R]) {
-        if (lane == 0) {
+    for (int t = t0; t < r1; t += NB * step) {
 #pragma unroll
-            for (int rr = 0; rr < R; ++rr)
-                if (t + rr < r1) epi(t + rr, o[rr]);
+        for (int j = 0; j < NB; ++j) {
+            const int tj = t + j * step;
+            if (tj >= r1) return;
+            b[(j + NB - 1) % NB].load(W, N, K, at(tj + (NB - 1) * step));
+            float o[R];
+            b[j].dot(K, xu, o);
+            if (lane == 0) {
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr)
+                    if (tj + rr < r1) epi(tj + rr, o[rr]);
+            }
         }
-    };
-    for (int t = r0 + (int)(tidx() >> 6) * R; t < r1; t += 2 * step) {
-        const int t1 = t + step;
-        if (t1 < r1) b1.load(W, N, K, t1);
-        float o[R];
-        b0.dot(K, xu, o);
-        emit(t, o);
-        if (t1 >= r1) break;
-        const int t2 = t1 + step;
-        if (t2 < r1) b0.load(W, N, K, t2);
-        b1.dot(K, xu, o);
-        emit(t1, o);
     }
 }
 
@@ -1273,14 +1276,17 @@ __global__ __launch_bounds__(kPT, 1) void persist_kernel(PArgs a) {
     float best = -INFINITY;
     int besti = -1;
     {
-        RowBlock<FH, UH, RH> b0, b1;
-        const int first = vb + wave * RH;
-        if (first < ve) b0.load(a.lm_head, a.V, H, first);
+        // four blocks of RH / 2 rows in turn: three tasks' rows in flight
+        static_assert(RH % 2 == 0, "head tasks are RH / 2 rows");
+        constexpr int RB = RH / 2;
+        RowBlock<FH, UH, RB> hb[4];
+        const int first = vb + wave * RB;
+        hb[0].load(a.lm_head, a.V, H, first < ve ? first : vb);
         GammaRegs gam;
         gam.load(a.final_norm, H);
         if (!poll_norm(a, ar, a.hbuf, tag_of(a, a.L - 1, 4), 5, gam, a.eps)) return;
         stamp(a, sh + 0);
-        head_rows<FH, UH, RH>(b0, b1, a.lm_head, a.V, H, vb, ve, ar, [&](int r, float v) {
+        head_rows_nb<FH, UH, RB, 4>(hb, a.lm_head, a.V, H, vb, ve, ar, [&](int r, float v) {
             const uint16_t hv16 = f2h(v);
             a.logits[r] = hv16;
             const float q = h2f(hv16);
