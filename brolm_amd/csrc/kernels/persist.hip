@@ -869,8 +869,15 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? r16(__expf(sv[hb] - M)) : 0.f;
         const float L = wave_allsum(pv[0] + pv[1]);
-        // P.V: lane holds head dims 2 lane, 2 lane + 1; the probabilities come
-        // by readlane, the value rows in batches of eight LDS reads
+        // P.V: lane holds head dims 2 lane, 2 lane + 1; the value rows come in
+        // batches of eight LDS reads, the probabilities through the wave's LDS
+        // area, four per broadcast read (a readlane per key costs the wait
+        // states before its scalar result can feed the multiply; the wave's
+        // own LDS writes complete before its later reads)
+        float* pw = sc.pw();
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+            if (lane + 64 * hb < nkw) pw[lane + 64 * hb] = pv[hb];
         float o0 = 0.f, o1 = 0.f;
         const uint16_t* vcol = sc.vt + jb * HD + 2 * (2 * lane < HD ? lane : 0);
         for (int t0 = 0; t0 < nkw; t0 += 8) {
@@ -880,14 +887,11 @@ __device__ __forceinline__ bool attention_stage(const PArgs& a, const Arena& ar,
                 const int t = min(t0 + u, nkw - 1);
                 vv[u] = *reinterpret_cast<const uint32_t*>(vcol + t * HD);
             }
+            const u4v pa = *reinterpret_cast<const u4v*>(pw + t0), pc = *reinterpret_cast<const u4v*>(pw + t0 + 4);
             lds_batch();
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int t = t0 + u;   // uniform
-                float p = 0.f;
-                if (t < nkw)
-                    p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                      __builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]), t & 63));
+                const float p = t0 + u < nkw ? __uint_as_float(u < 4 ? pa[u] : pc[u - 4]) : 0.f;
                 o0 += p * h2f(vv[u] & 0xffff);
                 o1 += p * h2f(vv[u] >> 16);
             }

@@ -824,6 +824,8 @@ struct AttScratch {
     __device__ __forceinline__ uint32_t* q16() const { return reinterpret_cast<uint32_t*>(wv); }
     __device__ __forceinline__ uint32_t* kcur() const { return reinterpret_cast<uint32_t*>(wv) + HD; }
     __device__ __forceinline__ uint32_t* vcur() const { return kcur() + HD / 2; }
+    // the wave's key probabilities for P.V (2 kTile floats after q / k / v)
+    __device__ __forceinline__ float* pbuf() const { return wv + 2 * HD; }
 };
 
 // Stage B of one (group, split): a normalized partial per query head of the
@@ -934,20 +936,25 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? r16(__expf(sv[hb] - M)) : 0.f;
     const float Lw = wave_sum(pv[0] + pv[1]);
+    // the probabilities go through LDS: the P.V loop then reads four keys'
+    // worth per broadcast load, where a readlane per key costs the wait
+    // states before its scalar result can feed the multiply (the wave's own
+    // LDS writes complete before its later reads)
+    float* pb = sc.pbuf();
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+        if (lane + 64 * hb < nkw) pb[lane + 64 * hb] = pv[hb];
     float o0 = 0.f, o1 = 0.f;
     const uint16_t* vcol = vt + jb * HD + 2 * (2 * lane < HD ? lane : 0);
     for (int t0 = 0; t0 < nkw; t0 += 8) {
         uint32_t vv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) vv[u] = *reinterpret_cast<const uint32_t*>(vcol + min(t0 + u, nkw - 1) * HD);
+        const u4v pa = *reinterpret_cast<const u4v*>(pb + t0), pc = *reinterpret_cast<const u4v*>(pb + t0 + 4);
         pin();
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int t = t0 + u;
-            float p = 0.f;
-            if (t < nkw)
-                p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                  __builtin_bit_cast(int, t < 64 ? pv[0] : pv[1]), t & 63));
+            const float p = t0 + u < nkw ? __uint_as_float(u < 4 ? pa[u] : pc[u - 4]) : 0.f;
             o0 += p * h2f(vv[u] & 0xffff);
             o1 += p * h2f(vv[u] >> 16);
         }
