@@ -227,6 +227,8 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="prefill, then time only the greedy decode steps and print their throughput (for "
                          "profiler and hardware-counter runs)")
+    ap.add_argument("--kv-cap", type=int, default=0, metavar="N",
+                    help="KV cache capacity in positions (default: the config's)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (a reference dispatch of known bytes for "
                          "hardware-counter runs)")
@@ -266,7 +268,7 @@ def main() -> int:
     model.load_weights(str(path))
     log(f"loaded in {time.time() - t0:.1f} s")
     prompt = ba.prompt_ids(c["prompt"], cfg.vocab_size, seed=42)
-    cap = max(c["cap"], c["prompt"] + args.warmup + steps + 1)
+    cap = max(args.kv_cap or c["cap"], c["prompt"] + args.warmup + steps + 1)
     model.allocate_cache(cap)
 
     if args.sampled_only:

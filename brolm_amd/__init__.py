@@ -247,9 +247,10 @@ class Qwen3Model:
         return int(_native.lib().brolm_qwen3_decode_weight_bytes(self._h))
 
     def decode_mode(self) -> str:
-        """Which single-token step path runs: "persistent", "graph" or "eager"."""
+        """Which single-token step path runs: "persistent", "graph", "eager" or
+        "op" (one forward_last per token)."""
         m = check(_native.lib().brolm_qwen3_decode_mode(self._h), "decode_mode")
-        return ("eager", "graph", "persistent")[m]
+        return ("eager", "graph", "persistent", "op")[m]
 
 
 @dataclass

@@ -664,9 +664,11 @@ bx_decode_dims DenseDecoder::decode_dims_() const {
 // per-stage kernels): every layer's types are ones the step kernels read,
 // with q/k and gate/up sharing a type, and the shape fits the step's
 // workspace.  Otherwise forward_last and decode_greedy take the op path, as
-// the reference does for any weight dtype (compute.h:54-86).
+// the reference does for any weight dtype (compute.h:54-86); BROLM_OP_STEP=1
+// asks for the op path.
 bool DenseDecoder::fused_step_ok_() const {
     if (max_seq_len_ == 0 || layers_.empty() || embed_tokens_.size() == 0) return false;
+    if (env_flag("BROLM_OP_STEP")) return false;
     auto known = [](int t) {
         return t == BX_TYPE_Q4_K || t == BX_TYPE_Q6_K || t == BX_TYPE_Q8_0 || t == BX_TYPE_F16;
     };
@@ -1001,6 +1003,7 @@ double DenseDecoder::time_decode_steps(int32_t token, int n) {
 int DenseDecoder::decode_mode() {
     if (embed_tokens_.size() == 0) fail("decode_mode: weights not loaded");
     if (max_seq_len_ == 0) fail("decode_mode: cache not allocated");
+    if (!fused_step_ok_()) return 3;
     DecodeGraphSession& s = session_();
     return s.use_persist ? 2 : (s.use_graph ? 1 : 0);
 }

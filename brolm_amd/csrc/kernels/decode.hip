@@ -44,12 +44,12 @@ struct WsLayout {
     int S;
 };
 
+// Key splits per KV head: two workgroups per CU over the heads, at most the
+// combine's 512.  The cache length does not enter: a split walks its keys in
+// 64-key tiles.
 int splits_for(const bx_decode_dims& d) {
     int S = (2 * num_cus()) / (d.n_kv > 0 ? d.n_kv : 1);
-    const int need = (d.cap + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // keys per split stay <= 64
-    if (S < need) S = need;
-    if (S < 1) S = 1;
-    return S;
+    return std::max(1, std::min(S, 512));
 }
 
 WsLayout ws_layout(const bx_decode_dims& d) {
@@ -261,8 +261,14 @@ __device__ void head_norm_rope(const float* src, const uint16_t* gamma, float ep
     }
 }
 
-// 2: attention partials for (split s, KV head g) at position *pos.
-// LDS: q[G][hd] f32 | kt[64][hd+2] f16 | vt[64][hd] f16 | p[G][64] f32 | red.
+// 2: attention partials for (split s, KV head g) at position *pos.  The
+// split's keys go through LDS in tiles of kMaxKeysPerSplit, with a running
+// maximum and sum per query head (a tile's probabilities are taken against
+// the running maximum, and what came before is rescaled when it grows), so
+// the number of splits does not depend on the cache length.  A split of one
+// tile computes exactly what a single pass would.
+// LDS: q[G][hd] f32 | kt[64][hd+8] f16 | vt[64][hd] f16 | p[G][64] f32 |
+// current k, v [hd] f32 each | rescale factors [G] f32.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict__ qkv, const uint16_t* q_norm,
                                                         const uint16_t* k_norm, float eps, int n_q, int n_kv, int,
@@ -272,12 +278,15 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict_
                                                         int S, float* __restrict__ part) {
     extern __shared__ __align__(16) float sm[];
     constexpr int hd = HD;
+    constexpr int kTileKeys = kMaxKeysPerSplit;
+    constexpr int kHeadsPerWave = (kMaxGroup + kWaves - 1) / kWaves;
+    constexpr int kPairsPerThread = (kMaxGroup * HD / 2 + kThreads - 1) / kThreads;
     const int s = blockIdx.x, g = blockIdx.y;
     const int G = n_q / n_kv;
     const int pos = *pos_dev;
     int kps = (pos + 1 + S - 1) / S;
     if (kps < kMinKeysPerSplit) kps = kMinKeysPerSplit;
-    const int kb = s * kps, ke = min(pos + 1, (s + 1) * kps);
+    const int kb = (int)min((int64_t)s * kps, (int64_t)pos + 1), ke = min(pos + 1, kb + kps);
     const int nk = ke - kb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int qd = n_q * hd, kvd = n_kv * hd;
@@ -291,25 +300,42 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict_
     const int kstride = hd + 8;  // halves per K row in LDS (padding against bank conflicts)
     float* qs = sm;
     uint16_t* kt = reinterpret_cast<uint16_t*>(qs + G * hd);
-    uint16_t* vt = kt + kMaxKeysPerSplit * kstride;
-    float* pr = reinterpret_cast<float*>(vt + kMaxKeysPerSplit * hd);
-    float* ck = pr + G * kMaxKeysPerSplit;
+    uint16_t* vt = kt + kTileKeys * kstride;
+    float* pr = reinterpret_cast<float*>(vt + kTileKeys * hd);
+    float* ck = pr + G * kTileKeys;
     float* cv = ck + hd;
+    float* alpha = cv + hd;
 
-    // Issue the K/V tile loads first (16 bytes per thread per step).
-    const int chunks = nk * (hd / 8);  // 16-byte chunks per tile
-    constexpr int kMaxChunks = kMaxKeysPerSplit * HD / 8 / kThreads;
+    // K/V of keys [c0, c0 + cn) of the split into registers (16 bytes per
+    // thread per step)
+    constexpr int kMaxChunks = kTileKeys * HD / 8 / kThreads;
     u4v kreg[kMaxChunks], vreg[kMaxChunks];
+    auto load_tile = [&](int c0, int cn) {
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        if (c < chunks) {
-            const int j = c / (hd / 8), d8 = c % (hd / 8);
-            const int64_t off = (int64_t)(kb + j) * kvd + (int64_t)g * hd + 8 * d8;
-            kreg[i] = ldg16(Kc + off);
-            vreg[i] = ldg16(Vc + off);
+        for (int i = 0; i < kMaxChunks; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if (c < cn * (hd / 8)) {
+                const int j = c / (hd / 8), d8 = c % (hd / 8);
+                const int64_t off = (int64_t)(kb + c0 + j) * kvd + (int64_t)g * hd + 8 * d8;
+                kreg[i] = ldg16(Kc + off);
+                vreg[i] = ldg16(Vc + off);
+            }
         }
-    }
+    };
+    auto store_tile = [&](int cn) {
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            if (c < cn * (hd / 8)) {
+                const int j = c / (hd / 8), d8 = c % (hd / 8);
+                *reinterpret_cast<u4v*>(kt + j * kstride + 8 * d8) = kreg[i];
+                *reinterpret_cast<u4v*>(vt + j * hd + 8 * d8) = vreg[i];
+            }
+        }
+    };
+
+    // the first tile's loads are in flight while q (and the current key) are formed
+    load_tile(0, min(nk, kTileKeys));
     const float* cos_row = cos_t + (int64_t)pos * (hd / 2);
     const float* sin_row = sin_t + (int64_t)pos * (hd / 2);
     const float scale = 1.0f / sqrtf((float)hd);
@@ -321,68 +347,103 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(const float* __restrict_
         head_norm_rope(qkv + qd + (int64_t)g * hd, k_norm, eps, hd, cos_row, sin_row, ck, true, 1.0f);
         for (int d = lane; d < hd; d += 64) cv[d] = h2f(f2h(qkv[qd + kvd + (int64_t)g * hd + d]));
     }
+
+    // running maximum and sum of the heads this wave scores (h = wave + kWaves i),
+    // unnormalized outputs of the (head, dim pair)s this thread owns
+    float m_run[kHeadsPerWave], l_run[kHeadsPerWave];
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        if (c < chunks) {
-            const int j = c / (hd / 8), d8 = c % (hd / 8);
-            *reinterpret_cast<u4v*>(kt + j * kstride + 8 * d8) = kreg[i];
-            *reinterpret_cast<u4v*>(vt + j * hd + 8 * d8) = vreg[i];
-        }
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.f;
     }
-    __syncthreads();
-    if (has_cur) {
-        // the current key/value replace the (stale) cache row in the tile and go to the cache
-        for (int d = threadIdx.x; d < hd; d += kThreads) {
-            const uint16_t kh = f2h(ck[d]), vh = f2h(cv[d]);
-            kt[(nk - 1) * kstride + d] = kh;
-            vt[(nk - 1) * hd + d] = vh;
-            Kc[(int64_t)pos * kvd + (int64_t)g * hd + d] = kh;
-            Vc[(int64_t)pos * kvd + (int64_t)g * hd + d] = vh;
+    float o0[kPairsPerThread], o1[kPairsPerThread];
+#pragma unroll
+    for (int k = 0; k < kPairsPerThread; ++k) o0[k] = o1[k] = 0.f;
+
+    for (int c0 = 0; c0 < nk; c0 += kTileKeys) {
+        const int cn = min(kTileKeys, nk - c0);
+        if (c0 > 0) {
+            load_tile(c0, cn);
+            __syncthreads();  // the previous tile's readers are done
+        }
+        store_tile(cn);
+        __syncthreads();
+        if (has_cur && c0 + cn == nk) {
+            // the current key/value replace the (stale) cache row in the tile and go to the cache
+            for (int d = threadIdx.x; d < hd; d += kThreads) {
+                const uint16_t kh = f2h(ck[d]), vh = f2h(cv[d]);
+                kt[(cn - 1) * kstride + d] = kh;
+                vt[(cn - 1) * hd + d] = vh;
+                Kc[(int64_t)pos * kvd + (int64_t)g * hd + d] = kh;
+                Vc[(int64_t)pos * kvd + (int64_t)g * hd + d] = vh;
+            }
+            __syncthreads();
+        }
+        // scores: wave h handles query head h, lane j handles key j
+#pragma unroll
+        for (int i = 0; i < kHeadsPerWave; ++i) {
+            const int h = wave + kWaves * i;
+            if (h >= G) break;
+            float sc = -INFINITY;
+            if (lane < cn) {
+                const float* q = qs + h * hd;
+                const uint16_t* kr = kt + lane * kstride;
+                float a = 0.f;
+                for (int d = 0; d < hd; d += 8) {
+                    const u4v kv = *reinterpret_cast<const u4v*>(kr + d);
+                    const float4 q0 = *reinterpret_cast<const float4*>(q + d);
+                    const float4 q1 = *reinterpret_cast<const float4*>(q + d + 4);
+                    a += q0.x * h2f(kv.x & 0xffff) + q0.y * h2f(kv.x >> 16) + q0.z * h2f(kv.y & 0xffff) +
+                         q0.w * h2f(kv.y >> 16) + q1.x * h2f(kv.z & 0xffff) + q1.y * h2f(kv.z >> 16) +
+                         q1.z * h2f(kv.w & 0xffff) + q1.w * h2f(kv.w >> 16);
+                }
+                sc = a;
+            }
+            const float m = fmaxf(m_run[i], wave_max(sc));
+            const float al = m_run[i] == -INFINITY ? 0.f : __expf(m_run[i] - m);
+            const float p = lane < cn ? __expf(sc - m) : 0.f;
+            l_run[i] = l_run[i] * al + wave_allsum(p);
+            m_run[i] = m;
+            pr[h * kTileKeys + lane] = p;
+            if (lane == 0) alpha[h] = al;
         }
         __syncthreads();
-    }
-    // scores: wave h handles query head h, lane j handles key j
-    for (int h = wave; h < G; h += kWaves) {
-        float sc = -INFINITY;
-        if (lane < nk) {
-            const float* q = qs + h * hd;
-            const uint16_t* kr = kt + lane * kstride;
-            float a = 0.f;
-            for (int d = 0; d < hd; d += 8) {
-                const u4v kv = *reinterpret_cast<const u4v*>(kr + d);
-                const float4 q0 = *reinterpret_cast<const float4*>(q + d);
-                const float4 q1 = *reinterpret_cast<const float4*>(q + d + 4);
-                a += q0.x * h2f(kv.x & 0xffff) + q0.y * h2f(kv.x >> 16) + q0.z * h2f(kv.y & 0xffff) +
-                     q0.w * h2f(kv.y >> 16) + q1.x * h2f(kv.z & 0xffff) + q1.y * h2f(kv.z >> 16) +
-                     q1.z * h2f(kv.w & 0xffff) + q1.w * h2f(kv.w >> 16);
+        // o[h][d] = alpha[h] o[h][d] + sum_j p[h][j] * V[j][d]; thread -> (h, dim pair)
+#pragma unroll
+        for (int k = 0; k < kPairsPerThread; ++k) {
+            const int idx = threadIdx.x + k * kThreads;
+            if (idx >= G * (hd / 2)) break;
+            const int h = idx / (hd / 2), dp = idx % (hd / 2);
+            const float* p = pr + h * kTileKeys;
+            float a0 = 0.f, a1 = 0.f;
+            for (int j = 0; j < cn; ++j) {
+                const uint32_t v = *reinterpret_cast<const uint32_t*>(vt + j * hd + 2 * dp);
+                a0 += p[j] * h2f(v & 0xffff);
+                a1 += p[j] * h2f(v >> 16);
             }
-            sc = a;
-        }
-        const float m = wave_max(sc);
-        const float p = lane < nk ? __expf(sc - m) : 0.f;
-        const float l = wave_allsum(p);
-        if (lane < kMaxKeysPerSplit) pr[h * kMaxKeysPerSplit + lane] = p;
-        if (lane == 0) {
-            float* rec = part + ((int64_t)(g * G + h) * S + s) * (hd + 2);
-            rec[hd] = m;
-            rec[hd + 1] = l;
+            o0[k] = o0[k] * alpha[h] + a0;
+            o1[k] = o1[k] * alpha[h] + a1;
         }
     }
-    __syncthreads();
-    // o[h][d] = sum_j p[h][j] * V[j][d]; thread -> (h, dim pair)
-    for (int idx = threadIdx.x; idx < G * (hd / 2); idx += kThreads) {
+    // the record of each head: o (unnormalized), m, l
+#pragma unroll
+    for (int k = 0; k < kPairsPerThread; ++k) {
+        const int idx = threadIdx.x + k * kThreads;
+        if (idx >= G * (hd / 2)) break;
         const int h = idx / (hd / 2), dp = idx % (hd / 2);
-        const float* p = pr + h * kMaxKeysPerSplit;
-        float o0 = 0.f, o1 = 0.f;
-        for (int j = 0; j < nk; ++j) {
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(vt + j * hd + 2 * dp);
-            o0 += p[j] * h2f(v & 0xffff);
-            o1 += p[j] * h2f(v >> 16);
-        }
         float* rec = part + ((int64_t)(g * G + h) * S + s) * (hd + 2);
-        rec[2 * dp] = o0;
-        rec[2 * dp + 1] = o1;
+        rec[2 * dp] = o0[k];
+        rec[2 * dp + 1] = o1[k];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kHeadsPerWave; ++i) {
+            const int h = wave + kWaves * i;
+            if (h >= G) break;
+            float* rec = part + ((int64_t)(g * G + h) * S + s) * (hd + 2);
+            rec[hd] = m_run[i];
+            rec[hd + 1] = l_run[i];
+        }
     }
 }
 
@@ -463,7 +524,7 @@ size_t norm_lds(int K) { return (size_t)K * 2 + (size_t)(K / 8) * 4 + 64 * 4; }
 
 size_t attn_lds(int G, int hd) {
     return (size_t)G * hd * 4 + (size_t)kMaxKeysPerSplit * (hd + 8) * 2 + (size_t)kMaxKeysPerSplit * hd * 2 +
-           (size_t)G * kMaxKeysPerSplit * 4 + (size_t)2 * hd * 4 + 256;
+           (size_t)G * kMaxKeysPerSplit * 4 + (size_t)2 * hd * 4 + (size_t)G * 4 + 256;
 }
 
 bool known_type(int t) {
@@ -493,7 +554,6 @@ int check_dims(const bx_decode_dims* d) {
         return fail(BX_EUNSUPPORTED, "decode: head_dim must be 64, 128 or 256");
     if (attn_lds(d->n_q / d->n_kv, d->head_dim) > 65536)
         return fail(BX_EUNSUPPORTED, "decode: attention tile too large for LDS");
-    if (splits_for(*d) > 512) return fail(BX_EUNSUPPORTED, "decode: cache capacity too large (> 32768)");
     return BX_OK;
 }
 

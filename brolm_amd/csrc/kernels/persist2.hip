@@ -784,7 +784,7 @@ __device__ __forceinline__ void tile_prefetch(const Args& a, int w, const bx_dec
     Split sp;
     if (!split_of(a, w, pos, sp)) return;
     dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), (int64_t)a.nkv * HD,
-                 (int64_t)sp.g * HD, sp.kb, sp.ke - sp.kb, tile, tile + kTile * HD);
+                 (int64_t)sp.g * HD, sp.kb, min(sp.ke - sp.kb, kTile), tile, tile + kTile * HD);
 }
 
 // Row of word W of a unit's q / k / v vector: segment seg, segment row (or -1
@@ -844,11 +844,19 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
     const int wave = tidx() >> 6, lane = tidx() & 63;
     const int P = kW / Gq;                       // key parts per head (Gq <= kW)
     const int part = wave % P, hh = wave / P;    // head of the group this wave serves
-    const int nk = sp.ke - sp.kb, kpp = (nk + P - 1) / P;
-    const int jb = min(nk, part * kpp), je = min(nk, jb + kpp);
+    // the split's keys in chunks of one tile (chunk 0 was copied a stage
+    // ahead); the current key, when the split holds it, is the last chunk's last
+    const int nk = sp.ke - sp.kb, nch = (nk + kTile - 1) / kTile, nlast = nk - (nch - 1) * kTile;
+    auto part_of = [&](int cn, int& jb, int& je) {
+        const int kpp = (cn + P - 1) / P;
+        jb = min(cn, part * kpp);
+        je = min(cn, jb + kpp);
+    };
     const bool has_cur = sp.ke == pos + 1;
-    const int jcur = pos - sp.kb;
-    const bool mine_cur = has_cur && jcur >= jb && jcur < je;
+    const int jcur = nlast - 1;
+    int jbl, jel;
+    part_of(nlast, jbl, jel);
+    const bool mine_cur = has_cur && jcur >= jbl && jcur < jel;
     const AttScratch<HD> sc(a, ar);
     uint16_t* kt = tile;
     uint16_t* vt = tile + kTile * HD;
@@ -880,11 +888,6 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
         norm_rope_head<HD>(sc.kraw + sp.gl * HD, rr.kg, rr, a.eps, a.qk_norm != 0, kc);
         for (int p = lane; p < HD / 2; p += 64)
             vc[p] = pack16(sc.vraw[sp.gl * HD + 2 * p], sc.vraw[sp.gl * HD + 2 * p + 1]);
-        for (int d8 = lane; d8 < CPK; d8 += 64) {
-            *reinterpret_cast<u4v*>(kt + jcur * HD + 8 * (d8 ^ (jcur & (CPK - 1)))) =
-                *reinterpret_cast<const u4v*>(kc + 4 * d8);
-            *reinterpret_cast<u4v*>(vt + jcur * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vc + 4 * d8);
-        }
         if (hh == 0) {   // the KV-cache row, once per group
             const int64_t kvd = (int64_t)a.nkv * HD;
             uint16_t* Kw = static_cast<uint16_t*>(Ly.Kc) + (int64_t)pos * kvd + (int64_t)sp.g * HD;
@@ -897,78 +900,113 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
     }
 
     sub(a, layer, 3);
-    // scores of this wave's keys (lane t: keys jb + t, jb + 64 + t)
     const float scale = 1.0f / sqrtf((float)HD);
-    const int nkw = je - jb;
     const uint32_t* q = sc.q16();
-    float sv[2];
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-        const int t = lane + 64 * hb;
-        sv[hb] = -INFINITY;
-        if (64 * hb < nkw) {
-            const int jr = jb + (t < nkw ? t : nkw - 1);
-            const uint16_t* kr = kt + jr * HD;
-            float acc = 0.f, acc2 = 0.f;
-#pragma unroll
-            for (int d0 = 0; d0 < CPK; d0 += 8) {
-                u4v kk[8], qv[8];
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    kk[c] = *reinterpret_cast<const u4v*>(kr + 8 * ((d0 + c) ^ (jr & (CPK - 1))));
-                    qv[c] = *reinterpret_cast<const u4v*>(q + 4 * (d0 + c));
-                }
-                pin();
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    acc = dot2(qv[c].x, kk[c].x, acc);
-                    acc2 = dot2(qv[c].y, kk[c].y, acc2);
-                    acc = dot2(qv[c].z, kk[c].z, acc);
-                    acc2 = dot2(qv[c].w, kk[c].w, acc2);
-                }
-            }
-            if (t < nkw) sv[hb] = (acc + acc2) * scale;
-        }
-    }
-    // softmax over this wave's keys (its own max and sum), P.V with dims 2 lane, 2 lane + 1
-    const float M = wave_max(fmaxf(sv[0], sv[1]));
-    float pv[2];
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? r16(__expf(sv[hb] - M)) : 0.f;
-    const float Lw = wave_sum(pv[0] + pv[1]);
-    // the probabilities go through LDS: the P.V loop then reads four keys'
-    // worth per broadcast load, where a readlane per key costs the wait
-    // states before its scalar result can feed the multiply (the wave's own
-    // LDS writes complete before its later reads)
     float* pb = sc.pbuf();
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb)
-        if (lane + 64 * hb < nkw) pb[lane + 64 * hb] = pv[hb];
-    float o0 = 0.f, o1 = 0.f;
-    const uint16_t* vcol = vt + jb * HD + 2 * (2 * lane < HD ? lane : 0);
-    for (int t0 = 0; t0 < nkw; t0 += 8) {
-        uint32_t vv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) vv[u] = *reinterpret_cast<const uint32_t*>(vcol + min(t0 + u, nkw - 1) * HD);
-        const u4v pa = *reinterpret_cast<const u4v*>(pb + t0), pc = *reinterpret_cast<const u4v*>(pb + t0 + 4);
-        pin();
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float p = t0 + u < nkw ? __uint_as_float(u < 4 ? pa[u] : pc[u - 4]) : 0.f;
-            o0 += p * h2f(vv[u] & 0xffff);
-            o1 += p * h2f(vv[u] >> 16);
+    // this wave's running maximum and sum, and its unnormalized P.V with dims
+    // 2 lane, 2 lane + 1; a chunk's probabilities are taken against the
+    // running maximum and what came before is rescaled when it grows (one
+    // chunk: the single-pass softmax of the wave's keys)
+    float Mw = -INFINITY, Lw = 0.f, o0 = 0.f, o1 = 0.f;
+    // one chunk of cn keys in the tile; last: it holds the current key
+    auto chunk = [&](int cn, bool last) __attribute__((always_inline)) {
+        int jb, je;
+        part_of(cn, jb, je);
+        if (mine_cur && last) {
+            // the current key / value replace the (stale) cache row in the tile
+            const uint32_t* kc = sc.kcur();
+            const uint32_t* vc = sc.vcur();
+            for (int d8 = lane; d8 < CPK; d8 += 64) {
+                *reinterpret_cast<u4v*>(kt + jcur * HD + 8 * (d8 ^ (jcur & (CPK - 1)))) =
+                    *reinterpret_cast<const u4v*>(kc + 4 * d8);
+                *reinterpret_cast<u4v*>(vt + jcur * HD + 8 * d8) = *reinterpret_cast<const u4v*>(vc + 4 * d8);
+            }
         }
+        // scores of this wave's keys (lane t: keys jb + t, jb + 64 + t)
+        const int nkw = je - jb;
+        float sv[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const int t = lane + 64 * hb;
+            sv[hb] = -INFINITY;
+            if (64 * hb < nkw) {
+                const int jr = jb + (t < nkw ? t : nkw - 1);
+                const uint16_t* kr = kt + jr * HD;
+                float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+                for (int d0 = 0; d0 < CPK; d0 += 8) {
+                    u4v kk[8], qv[8];
+#pragma unroll
+                    for (int c8 = 0; c8 < 8; ++c8) {
+                        kk[c8] = *reinterpret_cast<const u4v*>(kr + 8 * ((d0 + c8) ^ (jr & (CPK - 1))));
+                        qv[c8] = *reinterpret_cast<const u4v*>(q + 4 * (d0 + c8));
+                    }
+                    pin();
+#pragma unroll
+                    for (int c8 = 0; c8 < 8; ++c8) {
+                        acc = dot2(qv[c8].x, kk[c8].x, acc);
+                        acc2 = dot2(qv[c8].y, kk[c8].y, acc2);
+                        acc = dot2(qv[c8].z, kk[c8].z, acc);
+                        acc2 = dot2(qv[c8].w, kk[c8].w, acc2);
+                    }
+                }
+                if (t < nkw) sv[hb] = (acc + acc2) * scale;
+            }
+        }
+        const float M = fmaxf(Mw, wave_max(fmaxf(sv[0], sv[1])));
+        const float al = Mw == -INFINITY ? 0.f : __expf(Mw - M);
+        float pv[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) pv[hb] = lane + 64 * hb < nkw ? r16(__expf(sv[hb] - M)) : 0.f;
+        Lw = Lw * al + wave_sum(pv[0] + pv[1]);
+        Mw = M;
+        // the probabilities go through LDS: the P.V loop then reads four keys'
+        // worth per broadcast load, where a readlane per key costs the wait
+        // states before its scalar result can feed the multiply (the wave's own
+        // LDS writes complete before its later reads)
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+            if (lane + 64 * hb < nkw) pb[lane + 64 * hb] = pv[hb];
+        o0 *= al;
+        o1 *= al;
+        const uint16_t* vcol = vt + jb * HD + 2 * (2 * lane < HD ? lane : 0);
+        for (int t0 = 0; t0 < nkw; t0 += 8) {
+            uint32_t vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vv[u] = *reinterpret_cast<const uint32_t*>(vcol + min(t0 + u, nkw - 1) * HD);
+            const u4v pa = *reinterpret_cast<const u4v*>(pb + t0), pc = *reinterpret_cast<const u4v*>(pb + t0 + 4);
+            pin();
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float p = t0 + u < nkw ? __uint_as_float(u < 4 ? pa[u] : pc[u - 4]) : 0.f;
+                o0 += p * h2f(vv[u] & 0xffff);
+                o1 += p * h2f(vv[u] >> 16);
+            }
+        }
+    };
+    // chunk 0 was copied a stage ahead (straight-line: the running state
+    // starts empty); further chunks replace it in the tile
+    chunk(nch == 1 ? nlast : kTile, nch == 1);
+    for (int c = 1; c < nch; ++c) {
+        const int cn = c == nch - 1 ? nlast : kTile;
+        __syncthreads();   // every wave is done with the previous chunk
+        dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), (int64_t)a.nkv * HD,
+                     (int64_t)sp.g * HD, sp.kb + c * kTile, cn, kt, vt);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        chunk(cn, c == nch - 1);
     }
     sub(a, layer, 4);
-    // this wave's part: o (unnormalized), m, l (an empty part has l = 0)
+    // this wave's part: o (unnormalized), m, l (a part without keys has m =
+    // -inf, l = 0)
     float* pr = sc.parts + wave * (HD + 2);
     if (2 * lane < HD) {
         pr[2 * lane] = o0;
         pr[2 * lane + 1] = o1;
     }
     if (lane == 0) {
-        pr[HD] = nkw > 0 ? M : -INFINITY;
-        pr[HD + 1] = nkw > 0 ? Lw : 0.f;
+        pr[HD] = Mw;
+        pr[HD + 1] = Lw;
     }
     __syncthreads();
     sub(a, layer, 5);
@@ -1658,7 +1696,6 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
         }
     if (gpu == 0 || d.n_kv / gpu > kX) return fail(BX_EUNSUPPORTED, "persist2: KV groups do not map onto 8 XCDs");
     const int nu = d.n_kv / gpu, smax = kR / gpu;
-    if ((int64_t)d.cap > (int64_t)smax * kTile) return fail(BX_EUNSUPPORTED, "persist2: KV cache longer than the splits' tiles");
     const int vt[2] = {d.qkv_type_v, d.v_alt_type}, dt[2] = {d.down_type, d.down_alt_type};
     const int fblk = std::max(type_elems(d.down_type), type_elems(d.down_alt_type));
     if (fblk == 0 || F % fblk || H % 256) return fail(BX_EUNSUPPORTED, "persist2: widths");

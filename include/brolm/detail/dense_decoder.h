@@ -91,8 +91,9 @@ public:
     std::int64_t decode_weight_bytes() const;
 
     // How single-token steps run: 2 = persistent single launch, 1 = replayed
-    // hipGraph of per-stage kernels, 0 = the same kernels launched eagerly.
-    // Needs loaded weights and an allocated cache (creates the step session).
+    // hipGraph of per-stage kernels, 0 = the same kernels launched eagerly,
+    // 3 = the op path (one forward_last per token).  Needs loaded weights and
+    // an allocated cache (creates the step session when one is used).
     int decode_mode();
 
     // ── Multi-sequence batched decode ──────────────────────────────────────

@@ -176,7 +176,9 @@ int brolm_qwen3_decode_sampled(brolm_qwen3* m, int32_t token, int n, const doubl
                                float top_p, int32_t* out, int eos_id);
 double brolm_qwen3_time_decode_steps(brolm_qwen3* m, int32_t token, int n);
 int64_t brolm_qwen3_decode_weight_bytes(const brolm_qwen3* m);
-/* DenseDecoder::decode_mode: 2 persistent single launch, 1 captured graph, 0 eager; -1 on error
+/* DenseDecoder::decode_mode: 2 persistent single launch, 1 captured graph, 0 eager, 3 the op path
+ * (one forward_last per token: weight types or shapes the fused step does not take, or
+ * BROLM_OP_STEP=1); -1 on error
  * (no counterpart in the reference: reports which of this build's step paths runs). */
 int brolm_qwen3_decode_mode(brolm_qwen3* m);
 

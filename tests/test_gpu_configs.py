@@ -12,9 +12,10 @@ committed fixtures of tests/golden/ (make_golden.py):
   oracle's logits sampled at every 37th vocabulary id;
 - a llama.cpp Q4_K_M-style file (attn_v / ffn_down Q6_K on use_more_bits
   layers only, Q4_K elsewhere) vs the oracle;
-- a KV cache longer than the fused step covers: single-token steps and
-  greedy decode fall back to the op path (the reference loops forward_last,
-  include/brolm/detail/generate.h:78-123).
+- the op path for single-token steps (BROLM_OP_STEP=1; the reference loops
+  forward_last, include/brolm/detail/generate.h:78-123);
+- 40960-position caches: the fused steps at contexts where every attention
+  split walks several key tiles.
 
 Greedy identity (tests/test_qwen_generate.cpp:282-323, "first 32 tokens
 identical"): free-running tokens equal the oracle's until the first step
@@ -185,10 +186,12 @@ def test_q4k_m_layer_mix_vs_oracle(ba, tmp_path_factory):
     m.close()
 
 
-def test_cache_beyond_fused_step_uses_op_path(ba, small_gguf):
-    """The fused step's workspace covers caches up to 32768 positions; with a
-    longer cache forward_last(L = 1) and decode_greedy run the op path."""
-    m = _load(ba, small_gguf, cap=33000)
+def test_op_step_path_vs_oracle(ba, small_gguf, monkeypatch):
+    """BROLM_OP_STEP=1: forward_last(L = 1) and decode_greedy run the op path,
+    the reference's loop of forward_last per token."""
+    monkeypatch.setenv("BROLM_OP_STEP", "1")
+    m = _load(ba, small_gguf, cap=64)
+    assert m.decode_mode() == "op"
     om = oracle.Model(str(small_gguf))
     om.allocate_cache(64)
     prompt = [3, 1, 4, 1, 5]
@@ -209,6 +212,51 @@ def test_cache_beyond_fused_step_uses_op_path(ba, small_gguf):
     if k < len(want):
         assert margins[k] <= 2 * LOGIT_TOL
     assert m.cache_len() == len(prompt) + 7
+    m.close()
+
+
+# Models whose attention splits walk several key tiles at a few thousand keys:
+# 32 KV heads of 64 give the persistent step 8 splits of 128-key chunks and
+# the graph step 16 splits of 64-key tiles per head; 32 of 128 (graph step
+# only) the same 16 splits; one KV head of 128 gives the persistent step 32
+# splits, so past 4096 keys a split takes two chunks.
+_TILED = {
+    "kv32_hd64": dict(SMALL, intermediate=2048, n_q=32, n_kv=32, head_dim=64, seed=21),
+    "kv32_hd128": dict(SMALL, n_q=32, n_kv=32, head_dim=128, seed=22),
+    "kv1_hd128": dict(SMALL, intermediate=6144, n_q=4, n_kv=1, head_dim=128, seed=23),
+}
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name,ctx,mode", [("kv32_hd64", 2500, "persistent"), ("kv32_hd64", 2500, "graph"),
+                                           ("kv32_hd128", 2500, "graph"), ("kv1_hd128", 4300, "persistent")])
+def test_long_cache_tiled_attention_vs_oracle(ba, tmp_path_factory, monkeypatch, name, ctx, mode):
+    """A 40960-position cache (Qwen3's context, src/qwen.cpp:126-128) runs the
+    fused step: the split count no longer follows the capacity, each split
+    walks its keys tile by tile with a running maximum and sum.  A ctx-token
+    prompt, then four single-token steps, logits against the oracle."""
+    print(f"[configs] tiled attention {name} ctx {ctx} {mode}", flush=True)
+    path = write_synth(tmp_path_factory.mktemp(f"tiled_{name}"), _TILED[name], f"tiled_{name}")
+    if mode == "graph":
+        monkeypatch.setenv("BROLM_NO_PERSIST", "1")
+    m = _load(ba, path, cap=40960)
+    assert m.decode_mode() == mode
+    om = oracle.Model(str(path))
+    om.allocate_cache(ctx + 8)
+    prompt = ba.prompt_ids(ctx, m.cfg.vocab_size, seed=ctx)
+    a = m.forward_last(prompt)
+    b = om.forward(prompt, last_only=True)[0]
+    assert np.abs(a - b).max() <= LOGIT_TOL
+    tok = int(b.argmax())
+    worst = 0.0
+    for _ in range(4):
+        a = m.forward_last([tok])
+        b = om.forward([tok], last_only=True)[0]
+        worst = max(worst, float(np.abs(a - b).max()))
+        tok = int(b.argmax())
+    print(f"[configs] tiled attention {name} {mode}: steps max diff {worst:.3e}", flush=True)
+    assert worst <= LOGIT_TOL
+    assert m.cache_len() == ctx + 4
     m.close()
 
 

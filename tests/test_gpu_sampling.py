@@ -145,16 +145,18 @@ def _tie_at_cut(lg, T, k, p):
     return m < srt.size and srt[m - 1] == srt[m]
 
 
-@pytest.mark.parametrize("cap", [64, 33000])
-def test_device_sampled_decode_matches_per_token_sampling(env, small_gguf, cap):
+@pytest.mark.parametrize("cap,op", [(64, False), (33000, False), (64, True)])
+def test_device_sampled_decode_matches_per_token_sampling(env, small_gguf, monkeypatch, cap, op):
     """decode_sampled (the fused step and the device sampler back to back, no
-    host round trip; with a cache beyond the fused step's, the op path) picks,
-    at every step, the oracle sampler's id for that step's own logits and draw
-    (a second model fed the same tokens gives the logits), up to the first
-    draw within 1e-5 of an interval boundary (criteria as above); an FP16
-    tie where the kept set ends is checked like any other step."""
+    host round trip; with BROLM_OP_STEP=1, the op path and the sampler per
+    token) picks, at every step, the oracle sampler's id for that step's own
+    logits and draw (a second model fed the same tokens gives the logits), up
+    to the first draw within 1e-5 of an interval boundary (criteria as above);
+    an FP16 tie where the kept set ends is checked like any other step."""
     import brolm_amd as ba
-    print(f"[sample] decode_sampled cap={cap}", flush=True)
+    print(f"[sample] decode_sampled cap={cap} op={op}", flush=True)
+    if op:
+        monkeypatch.setenv("BROLM_OP_STEP", "1")
     mods = []
     for _ in range(2):
         m = ba.Qwen3Model(ba.Qwen3Config.from_gguf(str(small_gguf)))
