@@ -40,7 +40,7 @@ STEP_DESC = {
 # measured at (re-measured whenever persist.hip changes):
 # profiles/persist_kernel_traffic_qwen3-1.7b-q4k.md.
 MEASURED_TRAFFIC = {
-    ("qwen3-1.7b-q4k", "persistent"): (1_602_697_659, "c5c3e17"),
+    ("qwen3-1.7b-q4k", "persistent"): (1_601_485_576, "325bded"),
 }
 KERNEL_DESC = {
     "persistent": "persist_kernel: the whole decode step (all layers, lm_head, argmax) in one launch",

@@ -512,17 +512,40 @@ namespace {
 // Cache policy of the partials' buffer stores and loads: sc1, device scope.
 constexpr int kSc1 = 16;
 
+// Workgroup barrier for LDS data only: loads of global memory still in flight
+// stay in flight (__syncthreads() would wait for every one of them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __global__ void split_clear_kernel(uint64_t* cnt) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kSplGroups; i += gridDim.x * blockDim.x) cnt[i] = 0ull;
 }
 
 
+// The residual values of the lane's rows 4 g + j (< Mr) at its column of the
+// tile, read together (the residual epilogue's input, requested early).
+__device__ __forceinline__ void resid_rows(const MfmaJob& job, int64_t tile, int r, int g, int Mr, float (&hv)[4]) {
+    int mem;
+    int64_t lt;
+    member_of(job, tile, mem, lt);
+    const int N = job.N[mem];
+    const int64_t n = lt * 16 + r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        hv[j] = 0.f;
+        if (n < N && 4 * g + j < Mr) hv[j] = job.H[(int64_t)(4 * g + j) * N + n];
+    }
+}
+
 // The epilogue of one tile from lane values a (and u for SwiGLU); for the
-// residual, sq[j] is the square of the lane's updated value of row 4 g + j
-// (0 where there is none).
+// residual, hv holds the rows' residuals (resid_rows) and sq[j] is the square
+// of the lane's updated value of row 4 g + j (0 where there is none).
 template <int EPI>
 __device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, int r, int g, int Mr, const f4v& a,
-                                              const f4v& u, f4v& sq) {
+                                              const f4v& u, const float (&hv)[4], f4v& sq) {
     sq = f4v{0.f, 0.f, 0.f, 0.f};
     int mem;
     int64_t lt;
@@ -532,11 +555,6 @@ __device__ __forceinline__ void tile_epilogue(const MfmaJob& job, int64_t tile, 
     if (n >= N) return;
     const float bv = (EPI == MEPI_STORE && job.bias) ? h2f(job.bias[n]) : 0.f;
     if constexpr (EPI == MEPI_RESID) {
-        // the rows' residuals read together, then written
-        float hv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (4 * g + j < Mr) hv[j] = job.H[(int64_t)(4 * g + j) * N + n];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (4 * g + j < Mr) {
@@ -597,12 +615,47 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     const int c0 = s * nch / S, nc = (s + 1) * nch / S - c0;   // 1 <= nc <= CPS
     const int Ks = 256 * nc;
     const int xstride = Ks / 2 + 4;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wavefront index as a scalar: the tile's member, row count and
+    // weight pointer then come from the kernel arguments by scalar loads,
+    // which the waits for the activations below do not count
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = (int64_t)blockIdx.x * kSplWav + wave;
     const bool live = tile < job.tiles;
-    // this wavefront's weights first, every load issued: a wavefront past the
-    // last tile re-reads it, chunk slots past the slice repeat its last chunk
+    // The slice's activations are requested first and this wavefront's
+    // weights right behind them: loads complete in issue order, so the
+    // staging below waits only for the activations and runs while the weights
+    // stream (its barriers wait for LDS only).  A wavefront past the last tile
+    // re-reads it, chunk slots past the slice repeat its last chunk, groups
+    // past the slice repeat its last group (all in bounds).
+    constexpr int kXG = 4 * CPS;    // 4-element groups of the slice per thread (Mr <= 16)
+    constexpr int kSsL = 8;         // row-sum partials per thread requested up front (K <= 8192)
+    const int G4 = Ks / 4, total = Mr * G4;
+    f4v hv[NIN ? kXG : 1];
+    u2v gv[NIN ? kXG : 1];
+    u2v xv[NIN ? 1 : kXG];
+    float ssv[NIN ? kSsL : 1];
+    if constexpr (NIN) {
+        // unconditional loads at clamped indices (no branch to wait at);
+        // only the partials in range are added
+        const int m = min((int)threadIdx.x & 15, Mr - 1), q0 = threadIdx.x >> 4;
+#pragma unroll
+        for (int e = 0; e < kSsL; ++e) ssv[e] = job.ss_in[min(q0 + 16 * e, job.ss_groups - 1) * 16 + m];
+#pragma unroll
+        for (int j = 0; j < kXG; ++j) {
+            const int i = min((int)threadIdx.x + kSplThr * j, total - 1);
+            const int mm = i / G4, k = 256 * c0 + 4 * (i - mm * G4);
+            hv[j] = *reinterpret_cast<const f4v*>(job.Hn + (int64_t)mm * K + k);
+            gv[j] = *reinterpret_cast<const u2v*>(job.gamma + k);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kXG; ++j) {
+            const int i = min((int)threadIdx.x + kSplThr * j, total - 1);
+            const int mm = i / G4, gg = i - mm * G4;
+            xv[j] = *reinterpret_cast<const u2v*>(X + (int64_t)mm * K + 256 * c0 + 4 * gg);
+        }
+    }
     int mem;
     int64_t lt;
     member_of(job, live ? tile : job.tiles - 1, mem, lt);
@@ -630,19 +683,6 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     uint32_t* xs2 = smem + (Mr + 1) * xstride;
     xst.xs2 = xs2;
     if constexpr (NIN) {
-        // the thread's first four 4-element groups of the slice (h and gamma)
-        // are requested before the row sums are added, so both round trips
-        // overlap; groups past the slice repeat its last one (in bounds)
-        const int G4 = Ks / 4, total = Mr * G4;
-        f4v hv[4];
-        u2v gv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = min((int)threadIdx.x + kSplThr * j, total - 1);
-            const int m = i / G4, k = 256 * c0 + 4 * (i - m * G4);
-            hv[j] = *reinterpret_cast<const f4v*>(job.Hn + (int64_t)m * K + k);
-            gv[j] = *reinterpret_cast<const u2v*>(job.gamma + k);
-        }
         // each row's 1 / rms from the producer's per-group sums of squares:
         // thread (q0, m) adds groups q0, q0 + 16, ..., then row m adds the 16
         // part sums in order
@@ -651,11 +691,15 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
         {
             const int m = threadIdx.x & 15, q0 = threadIdx.x >> 4;
             float v = 0.f;
-            if (m < Mr)
-                for (int q = q0; q < job.ss_groups; q += 16) v += job.ss_in[q * 16 + m];
+            if (m < Mr) {
+#pragma unroll
+                for (int e = 0; e < kSsL; ++e)
+                    if (q0 + 16 * e < job.ss_groups) v += ssv[e];
+                for (int q = q0 + 16 * kSsL; q < job.ss_groups; q += 16) v += job.ss_in[q * 16 + m];
+            }
             qsum[q0][m] = v;
         }
-        __syncthreads();
+        lds_barrier();
         if ((int)threadIdx.x < Mr) {
             const int m = threadIdx.x;
             float ssum = 0.f;
@@ -663,33 +707,37 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
             for (int q0 = 0; q0 < 16; ++q0) ssum += qsum[q0][m];
             row_inv[m] = 1.0f / sqrtf(ssum / (float)K + job.eps);
         }
-        __syncthreads();
+        lds_barrier();
         // the slice of the normalised rows, FP16, into LDS
-        auto put = [&](int i, const f4v& h4, const u2v& g4) {
-            const int m = i / G4, gg = i - m * G4;
-            const float inv = row_inv[m];
-            store_group<kSwz>(smem + m * xstride, gg, norm_f16(h4.x, inv, h2f(g4.x & 0xffff)),
-                              norm_f16(h4.y, inv, h2f(g4.x >> 16)), norm_f16(h4.z, inv, h2f(g4.y & 0xffff)),
-                              norm_f16(h4.w, inv, h2f(g4.y >> 16)));
-        };
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kXG; ++j) {
             const int i = threadIdx.x + kSplThr * j;
-            if (i < total) put(i, hv[j], gv[j]);
-        }
-        for (int i = threadIdx.x + 4 * kSplThr; i < total; i += kSplThr) {
-            const int m = i / G4, k = 256 * c0 + 4 * (i - m * G4);
-            put(i, *reinterpret_cast<const f4v*>(job.Hn + (int64_t)m * K + k),
-                *reinterpret_cast<const u2v*>(job.gamma + k));
+            if (i < total) {
+                const int mm = i / G4, gg = i - mm * G4;
+                const float inv = row_inv[mm];
+                const f4v& h4 = hv[j];
+                const u2v& g4 = gv[j];
+                store_group<kSwz>(smem + mm * xstride, gg, norm_f16(h4.x, inv, h2f(g4.x & 0xffff)),
+                                  norm_f16(h4.y, inv, h2f(g4.x >> 16)), norm_f16(h4.z, inv, h2f(g4.y & 0xffff)),
+                                  norm_f16(h4.w, inv, h2f(g4.y >> 16)));
+            }
         }
     } else {
-        stage_x_f16<kSwz, false>(X + 256 * c0, K, Mr, Ks, smem, xstride, nullptr, 0);
+#pragma unroll
+        for (int j = 0; j < kXG; ++j) {
+            const int i = threadIdx.x + kSplThr * j;
+            if (i < total) {
+                const int mm = i / G4, gg = i - mm * G4;
+                const u2v v = xv[j];
+                store_group<kSwz>(smem + mm * xstride, gg, v.x & 0xffff, v.x >> 16, v.y & 0xffff, v.y >> 16);
+            }
+        }
     }
     for (int i = threadIdx.x; i < xstride; i += kSplThr) smem[Mr * xstride + i] = 0u;
-    __syncthreads();
+    lds_barrier();
     if constexpr (FMT == FMT_Q4_K || FMT2 == FMT_Q4_K) {
         q4k_xsums(smem, xstride, xs2, Mr, Ks);
-        __syncthreads();
+        lds_barrier();
     }
     f4v acc = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
     if (!second) {
@@ -707,8 +755,13 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     }
     f4v sq;
     if (S == 1) {
-        if (live) tile_epilogue<EPI>(job, tile, r, g, Mr, acc, accu, sq);
-        else sq = f4v{0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            float hv[4] = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (EPI == MEPI_RESID) resid_rows(job, tile, r, g, Mr, hv);
+            tile_epilogue<EPI>(job, tile, r, g, Mr, acc, accu, hv, sq);
+        } else {
+            sq = f4v{0.f, 0.f, 0.f, 0.f};
+        }
         if (EPI == MEPI_RESID && job.ss_out) group_row_ss(job, Mr, wave, r, g, sq, wss);
         return;
     }
@@ -737,7 +790,10 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
     __syncthreads();
     if (!last) return;
     if (live && lane < pl) {
-        // all S partials requested before any is added; added in slice order
+        // the residual rows and all S partials requested before any partial
+        // is added; added in slice order
+        float hv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EPI == MEPI_RESID) resid_rows(job, tile, r, g, Mr, hv);
         f4v a = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
         for (int q0 = 0; q0 < S; q0 += 8) {
             u4v va[8], vu[kTwo ? 8 : 1];
@@ -756,7 +812,7 @@ __global__ __launch_bounds__(kSplThr) void gemv_split_kernel(MfmaJob job, const 
                 }
             }
         }
-        tile_epilogue<EPI>(job, tile, r, g, Mr, a, u, sq);
+        tile_epilogue<EPI>(job, tile, r, g, Mr, a, u, hv, sq);
     } else {
         sq = f4v{0.f, 0.f, 0.f, 0.f};
     }

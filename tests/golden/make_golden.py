@@ -33,6 +33,16 @@ model_8b_width.npz
              argmax and top-2 margin after a 2048-token prefill and after
              each of 8 greedy steps (the oracle's prefill takes about a minute
              on 8 cores, too slow to rerun inside a GPU test).
+model_full_depth_widths.npz
+             the other BASELINE.json shapes at full depth, teacher-forced on
+             the oracle's own greedy tokens: "q8" configs[1] (Qwen3-0.6B
+             widths, 28 layers, all-Q8_0, tied FP16 lm_head clone) after a
+             512-token prompt, 32 steps; "w8b" configs[4] (Qwen3-8B widths,
+             36 layers, Q4_K with Q6_K output) after a 256-token prompt
+             (the oracle's 36-layer prefill of configs[4]'s 2048 tokens
+             would take most of an hour here), 16 steps.  Per step the
+             oracle's logits at every 37th id and at its 16 largest ids,
+             its argmax and top-2 margin.
 The reference has no numeric fixtures for this path (its quant tests check
 finiteness against downloaded checkpoints only), so these are the vectors.
 """
@@ -189,8 +199,60 @@ def make_8b_width_fixture(tmp: Path) -> dict:
             "sha256": np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)}
 
 
+# Full-depth widths of configs[1] and configs[4]: name -> (spec, prompt tokens, teacher-forced steps)
+FULL_WIDTHS = {
+    "q8": (dict(vocab=151936, hidden=1024, intermediate=3072, layers=28, n_q=16, n_kv=8, head_dim=128, tied=True,
+                embed="Q8_0", q="Q8_0", k="Q8_0", v="Q8_0", o="Q8_0", gate="Q8_0", up="Q8_0", down="Q8_0",
+                output="Q8_0", seed=9), 512, 32),
+    "w8b": (dict(W8B, layers=36), 256, 16),
+}
+
+
+def teacher_forced(m, prompt, steps: int) -> dict:
+    """The oracle's logits rows (every FL_STRIDE-th id), top-FL_TOP ids and
+    values, argmax tokens and top-2 margins over `steps` teacher-forced steps
+    on its own greedy tokens after `prompt`."""
+    import oracle
+
+    m.allocate_cache(len(prompt) + steps + 1)
+    lg = m.forward(prompt, last_only=True)[0]
+    rows, top_ids, top_vals, toks, margins = [], [], [], [], []
+    for step in range(steps):
+        order = np.argsort(lg, kind="stable")[::-1]
+        rows.append(lg[::FL_STRIDE].copy())
+        top_ids.append(order[:FL_TOP].astype(np.int32))
+        top_vals.append(lg[order[:FL_TOP]].copy())
+        tok, _ = oracle.argmax(lg)
+        toks.append(tok)
+        margins.append(float(lg[order[0]] - lg[order[1]]))
+        if step + 1 < steps:
+            lg = m.forward([tok], last_only=True)[0]
+    return {"prompt": np.asarray(prompt, np.int32), "rows": np.stack(rows).astype(np.float32),
+            "top_ids": np.stack(top_ids), "top_vals": np.stack(top_vals).astype(np.float32),
+            "tokens": np.asarray(toks, np.int32), "margins": np.asarray(margins, np.float32)}
+
+
+def make_full_widths_fixture(tmp: Path) -> dict:
+    import brolm_amd as ba
+    import oracle
+    from conftest import write_synth
+
+    out = {}
+    for name, (spec, n_prompt, steps) in FULL_WIDTHS.items():
+        path = write_synth(tmp, spec, f"fw_{name}")
+        out[f"{name}_sha256"] = np.frombuffer(bytes.fromhex(checkpoint_digest(path)), np.uint8)
+        m = oracle.Model(str(path))
+        for k, v in teacher_forced(m, ba.prompt_ids(n_prompt, spec["vocab"], seed=42), steps).items():
+            out[f"{name}_{k}"] = v
+        print(name, "tokens", out[f"{name}_tokens"][:8], "min margin", float(out[f"{name}_margins"].min()),
+              flush=True)
+        del m
+        path.unlink()
+    return out
+
+
 def main() -> None:
-    which = sys.argv[1:] or ["blocks", "small", "full", "w8b", "full_logits"]
+    which = sys.argv[1:] or ["blocks", "small", "full", "w8b", "full_logits", "full_widths"]
     if "blocks" in which:
         np.savez_compressed(HERE / "blocks.npz", **make_blocks())
     with tempfile.TemporaryDirectory() as td:
@@ -202,6 +264,8 @@ def main() -> None:
             np.savez_compressed(HERE / "model_8b_width.npz", **make_8b_width_fixture(Path(td)))
         if "full_logits" in which:
             np.savez_compressed(HERE / "model_full_logits.npz", **make_full_logits_fixture(Path(td)))
+        if "full_widths" in which:
+            np.savez_compressed(HERE / "model_full_depth_widths.npz", **make_full_widths_fixture(Path(td)))
     print("wrote", which)
 
 

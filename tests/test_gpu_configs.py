@@ -6,10 +6,12 @@ committed fixtures of tests/golden/ (make_golden.py):
 - configs[0] at full depth: Qwen3-0.6B random-init BF16 (tied), 128 greedy
   tokens vs the oracle's;
 - configs[1] at its widths: Qwen3-0.6B all-Q8_0, tied (FP16 lm_head clone),
-  512-token prompt then single-token steps, vs the oracle;
+  512-token prompt then single-token steps, vs the oracle; at full depth (28
+  layers) against committed oracle logits, 32 teacher-forced steps;
 - configs[4] at its widths: Qwen3-8B shapes (H 4096, F 12288, 32/8 heads),
   Q4_K with Q6_K output, 2048-token prefill then single-token steps, vs the
-  oracle's logits sampled at every 37th vocabulary id;
+  oracle's logits sampled at every 37th vocabulary id; at full depth (36
+  layers) after a 256-token prompt, 16 teacher-forced steps;
 - a llama.cpp Q4_K_M-style file (attn_v / ffn_down Q6_K on use_more_bits
   layers only, Q4_K elsewhere) vs the oracle;
 - the op path for single-token steps (BROLM_OP_STEP=1; the reference loops
@@ -152,6 +154,43 @@ def test_q4k_8b_widths_prefill_2048(ba, tmp_path_factory):
         if step == W8B_STEPS:
             break
         lg = m.forward_last([int(d["tokens"][step])])
+    m.close()
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["q8", "w8b"])
+def test_full_depth_widths_teacher_forced_vs_oracle(ba, name, tmp_path_factory):
+    """configs[1] (Qwen3-0.6B widths, all-Q8_0, tied FP16 lm_head clone) and
+    configs[4] (Qwen3-8B widths, Q4_K with Q6_K output) at full depth, 28 and
+    36 layers: the prompt's prefill, then teacher-forced steps on the
+    persistent kernel, every step's logits within 2e-2 of the oracle's at
+    every 37th vocabulary id and at its 16 largest, and the oracle's argmax
+    wherever its top-2 margin exceeds twice that
+    (tests/golden/model_full_depth_widths.npz)."""
+    from golden.make_golden import FULL_WIDTHS
+    d = np.load(GOLD / "model_full_depth_widths.npz")
+    spec, n_prompt, steps = FULL_WIDTHS[name]
+    path = write_synth(tmp_path_factory.mktemp(f"fw_{name}"), spec, f"fw_{name}")
+    print(f"[configs] full-depth {name} checkpoint written", flush=True)
+    assert _sha256(path) == d[f"{name}_sha256"].tobytes().hex(), "synthetic generator changed; rerun make_golden.py"
+    prompt = d[f"{name}_prompt"].tolist()
+    toks, margins = d[f"{name}_tokens"], d[f"{name}_margins"]
+    rows, top_ids, top_vals = d[f"{name}_rows"], d[f"{name}_top_ids"], d[f"{name}_top_vals"]
+    assert len(prompt) == n_prompt and len(toks) == steps
+    m = _load(ba, path, cap=n_prompt + steps + 1)
+    assert m.decode_mode() == "persistent"
+    lg = m.forward_last(prompt)
+    errs = []
+    for step in range(steps):
+        errs.append(max(float(np.abs(lg[::37] - rows[step]).max()),
+                        float(np.abs(lg[top_ids[step]] - top_vals[step]).max())))
+        if margins[step] > 2 * LOGIT_TOL:
+            assert int(lg.argmax()) == int(toks[step]), step
+        if step + 1 < steps:
+            lg = m.forward_last([int(toks[step])])
+    print(f"[configs] full-depth {name} ({spec['layers']} layers, prompt {n_prompt}): per-step max-abs logit "
+          f"error {' '.join(f'{e:.2e}' for e in errs)}", flush=True)
+    assert max(errs) <= LOGIT_TOL, max(errs)
     m.close()
 
 
