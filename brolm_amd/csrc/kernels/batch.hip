@@ -66,36 +66,67 @@ __global__ void kv_rows_kernel(const uint16_t* __restrict__ k, const uint16_t* _
 // neighbouring lane.
 // One head (64 EPL elements, lane l holding elements l, l + 64, ...) of a raw
 // projection row: RMSNorm with gain (when given), FP16, RoPE by the table row
-// ps (identity when rot is false), FP16.  y[i] is element lane + 64 i.
+// ps (identity when rot is false), FP16.  y[i] is element lane + 64 i.  The
+// loads (load) and the arithmetic (apply) are apart, so a caller can request
+// the inputs of several heads before it waits for any.
+template <int EPL>
+struct NormRopeLane {
+    uint32_t x[EPL], gm[EPL];
+    float c[EPL], sn[EPL];
+    // Every load unconditional, so no branch join waits for one: without a
+    // gain the row itself is read in its place, off the table (rot false) its
+    // row 0 (launchers require a table of at least one row); apply takes the
+    // flags.
+    __device__ __forceinline__ void load(const uint16_t* src, const uint16_t* gain, int ps, bool rot,
+                                         const float* __restrict__ cos_t, const float* __restrict__ sin_t) {
+        constexpr int half = 32 * EPL;
+        const int lane = threadIdx.x & 63;
+        const uint16_t* gp = gain ? gain : src;
+        const int64_t row = rot ? ps : 0;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = lane + 64 * i;
+            x[i] = src[e];
+            gm[i] = gp[e];
+            c[i] = cos_t[row * half + (e >> 1)];
+            sn[i] = sin_t[row * half + (e >> 1)];
+        }
+    }
+    __device__ __forceinline__ void apply(bool gain, bool rot, float eps, uint16_t (&y)[EPL]) const {
+        constexpr int HD = 64 * EPL;
+        const int lane = threadIdx.x & 63;
+        float xf[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) xf[i] = h2f((uint16_t)x[i]);
+        if (gain) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) ss += xf[i] * xf[i];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) xf[i] = h2f(norm_f16(xf[i], inv, h2f((uint16_t)gm[i])));
+        }
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = lane + 64 * i;
+            const float other = __shfl_xor(xf[i], 1, 64);
+            const float cc = rot ? c[i] : 1.f, ss = rot ? sn[i] : 0.f;
+            uint16_t y0, y1;
+            if (e & 1) rope_pair(other, xf[i], cc, ss, y0, y1);
+            else rope_pair(xf[i], other, cc, ss, y0, y1);
+            y[i] = (e & 1) ? y1 : y0;
+        }
+    }
+};
+
 template <int EPL>
 __device__ __forceinline__ void norm_rope_lane(const uint16_t* src, const uint16_t* gain, float eps, int ps, bool rot,
                                                const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                                                uint16_t (&y)[EPL]) {
-    constexpr int HD = 64 * EPL, half = HD / 2;
-    const int lane = threadIdx.x & 63;
-    float x[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) x[i] = h2f(src[lane + 64 * i]);
-    if (gain) {
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) x[i] = h2f(norm_f16(x[i], inv, h2f(gain[lane + 64 * i])));
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const int e = lane + 64 * i;
-        const float other = __shfl_xor(x[i], 1, 64);
-        const float c = rot ? cos_t[(int64_t)ps * half + (e >> 1)] : 1.f;
-        const float sn = rot ? sin_t[(int64_t)ps * half + (e >> 1)] : 0.f;
-        uint16_t y0, y1;
-        if (e & 1) rope_pair(other, x[i], c, sn, y0, y1);
-        else rope_pair(x[i], other, c, sn, y0, y1);
-        y[i] = (e & 1) ? y1 : y0;
-    }
+    NormRopeLane<EPL> n;
+    n.load(src, gain, ps, rot, cos_t, sin_t);
+    n.apply(gain != nullptr, rot, eps, y);
 }
 
 template <int EPL>
@@ -159,6 +190,7 @@ struct BaShape {
     static constexpr int TK = 8192 / HD;   // keys per LDS tile (two tiles of K and V: 64 KB)
     static constexpr int CPK = HD / 8;     // 16-byte chunks per key row
     static constexpr int EPL = HD / 64;    // head elements (and output dims) per lane
+    static constexpr int INST = TK * CPK / 64;   // copy instructions of a tile (K or V), a multiple of 4
 };
 
 struct BatchAttnArgs {
@@ -195,9 +227,12 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     using SH = BaShape<HD>;
     constexpr int TK = SH::TK, CPK = SH::CPK, EPL = SH::EPL;
     extern __shared__ __align__(16) uint16_t ba_lds[];
+    // the roped q heads and the new k / v rows apart from the tiles: writes
+    // there need not wait for the tile copies in flight
+    __shared__ __align__(16) uint16_t ba_qkv[10 * HD];
     __shared__ uint32_t last;
     uint16_t* tiles = ba_lds;          // two buffers of K (TK x HD, swizzled chunks) then V (TK x HD)
-    uint16_t* qs = tiles + 4 * TK * HD;   // 8 x HD roped q heads
+    uint16_t* qs = ba_qkv;             // 8 x HD roped q heads
     uint16_t* kn = qs + 8 * HD;        // the new key row
     uint16_t* vn = kn + HD;            // the new value row
     const int s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
@@ -212,12 +247,15 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
     const uint16_t* Kg = a.Kc + row0 * kvd + (int64_t)g * HD;
     const uint16_t* Vg = a.Vc + row0 * kvd + (int64_t)g * HD;
     // tile copy of keys [c0, c0 + nk) into buffer b; slots past nk repeat key
-    // nk - 1 (in bounds)
+    // nk - 1 (in bounds).  A wavefront issues the same copies whatever nk, so
+    // the waits for the loads requested before them count exactly.
     auto copy_tile = [&](int b, int c0, int nk) {
         uint16_t* kt = tiles + 2 * b * TK * HD;
         uint16_t* vt = kt + TK * HD;
-        const int ninst = (nk * CPK + 63) / 64;
-        for (int i = wave; i < ninst; i += 4) {
+        static_assert(SH::INST % 4 == 0, "copy instructions per wavefront");
+#pragma unroll
+        for (int k4 = 0; k4 < SH::INST / 4; ++k4) {
+            const int i = wave + 4 * k4;
             const int slot = 64 * i + lane;
             int j = slot / CPK;
             const int pc = slot % CPK;
@@ -227,32 +265,54 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
             ba_dma<HD>(Vg + rowo + 8 * pc, vt + 512 * i);
         }
     };
-    if (kb < ke) copy_tile(0, kb, min(TK, ke - kb));   // lands while the prologue runs
-
-    // ---- prologue: roped q heads; the new k / v rows in the split holding them
-    for (int hh = wave; hh < G; hh += 4) {
-        uint16_t y[EPL];
-        norm_rope_lane<EPL>(a.q + ((int64_t)r * a.n_q + g * G + hh) * HD, a.q_gain, a.eps, pnew, rot, a.cos_t,
-                            a.sin_t, y);
+    // ---- prologue: the inputs of the group's q heads (at most two per
+    // wavefront) and, in the split holding the new key, of its k and v rows
+    // are requested first and the first tile's copy right behind them (loads
+    // complete in issue order); then the roped q heads and the new k / v rows
+    // (unconditional loads at clamped heads, so no branch join waits for
+    // them; only the heads that exist are used)
+    NormRopeLane<EPL> qin[2];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) qs[hh * HD + lane + 64 * i] = y[i];
+    for (int i = 0; i < 2; ++i) {
+        const int hh = min(wave + 4 * i, G - 1);
+        qin[i].load(a.q + ((int64_t)r * a.n_q + g * G + hh) * HD, a.q_gain, pnew, rot, a.cos_t, a.sin_t);
     }
-    if (has_cur && wave == 3) {
-        uint16_t y[EPL];
-        norm_rope_lane<EPL>(a.k + (int64_t)r * kvd + (int64_t)g * HD, a.k_gain, a.eps, pnew, rot, a.cos_t, a.sin_t,
-                            y);
+    const bool cur_wave = has_cur && wave == 3;
+    NormRopeLane<EPL> kin;
+    uint32_t vin[EPL];
+    kin.load(a.k + (int64_t)r * kvd + (int64_t)g * HD, a.k_gain, pnew, rot, a.cos_t, a.sin_t);
+    {
         const uint16_t* vs = a.v + (int64_t)r * kvd + (int64_t)g * HD;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) vin[i] = vs[lane + 64 * i];
+    }
+    // the first tile lands while the prologue runs; an empty split copies a
+    // row of its sequence it does not read, so every wavefront issues the
+    // same copies (the waits for the prologue's loads then count exactly)
+    copy_tile(0, max(0, min(kb, len - 1)), max(1, min(TK, ke - kb)));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int hh = wave + 4 * i;
+        if (hh < G) {
+            uint16_t y[EPL];
+            qin[i].apply(a.q_gain != nullptr, rot, a.eps, y);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) qs[hh * HD + lane + 64 * e] = y[e];
+        }
+    }
+    if (cur_wave) {
+        uint16_t y[EPL];
+        kin.apply(a.k_gain != nullptr, rot, a.eps, y);
         const int64_t d = row0 + pnew;
         const bool write = rot && d >= 0 && d < a.cache_rows;
 #pragma unroll
         for (int i = 0; i < EPL; ++i) {
             const int e = lane + 64 * i;
-            const uint16_t vv = vs[e];
             kn[e] = y[i];
-            vn[e] = vv;
+            vn[e] = (uint16_t)vin[i];
             if (write) {
                 a.Kc[d * kvd + (int64_t)g * HD + e] = y[i];
-                a.Vc[d * kvd + (int64_t)g * HD + e] = vv;
+                a.Vc[d * kvd + (int64_t)g * HD + e] = (uint16_t)vin[i];
             }
         }
     }
@@ -360,6 +420,9 @@ __global__ __launch_bounds__(256) void batch_attn_kernel(BatchAttnArgs a) {
             }
         }
     }
+    // an empty split left its one tile copy in flight: it lands before the
+    // merge area (the tile buffers) is written
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();   // all waves are done with the tiles (the merge area reuses them)
 
     // ---- the P key parts of each head merged in LDS (the tile area is free
@@ -508,7 +571,7 @@ inline BaPlan ba_plan(int rows, int n_q, int n_kv, int max_len) {
     p.S = (max_len + p.kps - 1) / p.kps;
     return p;
 }
-inline size_t ba_lds_bytes(int hd) { return (size_t)4 * 8192 * 2 + (size_t)10 * hd * 2; }
+inline size_t ba_lds_bytes(int) { return (size_t)4 * 8192 * 2; }
 
 inline unsigned blocks_of(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
