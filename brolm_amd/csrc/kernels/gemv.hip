@@ -1,6 +1,8 @@
 // Quant-carrier / FP16 batched linear (brotensor linear_forward_batched_*_fp16,
 // dispatched at include/brolm/detail/compute.h:54-86): Y[M,N] = X[M,K] W[N,K]^T.
-// M = 1: GEMV kernels (lanes across K, rows per wavefront).
+// M = 1: GEMV kernels (lanes across K, rows per wavefront); 2 <= M <= 4 over
+// lm_head-sized matrices: the same kernel with the rows' activations held per
+// lane (gemv_mr_kernel).
 // 3 <= M <= 16 with K % 256 == 0: the matrix-core GEMV (gemv_mfma.hip), except
 // M = 2 and 4 (see gemv_f16) and other K, which take the per-row GEMV kernel.
 // M > 16: the prefill GEMM (gemm.hip).
@@ -124,6 +126,48 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
     }
 }
 
+// 2 <= M <= 4 (MR rows): gemv_m1_kernel with MR activation rows staged and
+// held per lane (in registers while MR x UPL <= 4 units, otherwise re-read
+// from LDS): each weight unit is loaded once for all the rows, so a launch
+// reads the weight bytes of a one-row launch, and row m of Y equals a one-row
+// launch on row m of X bit for bit (rows_dot_mr).
+template <int FMT, int UPL, int MR>
+__global__ __launch_bounds__(kThreads) void gemv_mr_kernel(const void* __restrict__ W,
+                                                          const uint16_t* __restrict__ X,
+                                                          const uint16_t* __restrict__ bias,
+                                                          uint16_t* __restrict__ Y, int N, int K) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    uint32_t* xs = smem;                                           // MR rows of K / 2 pairs
+    float* xsum = reinterpret_cast<float*>(smem + MR * (K / 2));   // MR rows of K / 8 sums
+    stage_x_f16<true, false>(X, K, MR, K, xs, K / 2, xsum, K / 8);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) sums8_from_lds(xs + m * (K / 2), K, xsum + m * (K / 8));
+    __syncthreads();
+    constexpr int R = RowsPer<UPL>::R;
+    constexpr bool XR = UPL * MR <= 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    XCache<FMT, UPL, XR> xu[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) xu[m].init(xs + m * (K / 2), xsum + m * (K / 8), K);
+    const int64_t tasks = ((int64_t)N + R - 1) / R;
+    for (int64_t t = (int64_t)blockIdx.x * kWaves + wave; t < tasks; t += (int64_t)gridDim.x * kWaves) {
+        float o[R][MR];
+        rows_dot_mr<FMT, UPL, R, MR, XR>(W, N, K, t * R, xu, o);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int64_t row = t * R + rr;
+                if (row < N) {
+                    const float b = bias ? h2f(bias[row]) : 0.f;
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) Y[(int64_t)m * N + row] = f2h(o[rr][m] + b);
+                }
+            }
+        }
+    }
+}
+
 // M = 1 at K of 24576 or 32768 (U = K / 32 a multiple of 256): the four
 // wavefronts of a workgroup split K in quarters, so a lane owns UPW = U / 256
 // units of each row (a Q6_K row at K 32768: 4 units, where one wavefront per
@@ -211,6 +255,28 @@ int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* 
         gemv_m1_kernel<FMT_, UPL_><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
     }))
     return launch_check("gemv m1");
+}
+
+// Staged activations of the several-row GEMV: M rows of K FP16 values and
+// K / 8 sums each.
+size_t gemv_mr_lds_bytes(int M, int K) { return (size_t)M * ((size_t)K * 2 + (size_t)(K / 8) * 4); }
+bool gemv_mr_ok(int M, int K) { return M >= 2 && M <= 4 && upl_for(K) <= 6 && gemv_mr_lds_bytes(M, K) <= 65536; }
+
+int launch_gemv_mr(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int M, int N,
+                   int K, hipStream_t st) {
+    if (!gemv_mr_ok(M, K)) return fail(BX_EUNSUPPORTED, "gemv: several-row kernel shape");
+    const int upl = upl_for(K);
+    const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
+    int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
+    const int64_t cap = (int64_t)num_cus() * 8;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = gemv_mr_lds_bytes(M, K);
+    BX_DISPATCH_FMT(wtype, BX_DISPATCH_UPL(upl, {
+        if (M == 2) gemv_mr_kernel<FMT_, UPL_, 2><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
+        else if (M == 3) gemv_mr_kernel<FMT_, UPL_, 3><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
+        else gemv_mr_kernel<FMT_, UPL_, 4><<<(unsigned)blocks, kThreads, lds, st>>>(W, X, bias, Y, N, K);
+    }))
+    return launch_check("gemv mr");
 }
 
 size_t gemv_lds_bytes(int fmt, int M, int K) {
@@ -306,6 +372,14 @@ int gemv_m1_ksplit(int wtype, const void* W, const uint16_t* X, const uint16_t* 
 int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, uint16_t* Y, int M, int N, int K,
              void* ws, size_t wsb, hipStream_t st) {
     if (M == 1 && upl_for(K) <= 16) return launch_gemv_m1(wtype, W, X, bias, Y, N, K, st);
+    // measured (GEMV sweep, 151936 x 2048): the several-row kernel takes M = 2
+    // in every quant format (Q4_K 69.6 -> 54.0 us) and M = 3 / 4 in Q6_K and
+    // Q8_0 (Q8_0 at 3: 102.4 -> 73.3 us), where the matrix-core and per-row
+    // kernels pay more per weight; layer-sized matrices are launch-bound
+    // either way and keep their kernels
+    const bool big = (int64_t)N * K >= ((int64_t)32 << 20);
+    if (big && wtype != BX_TYPE_F16 && gemv_mr_ok(M, K) && (M == 2 || wtype != BX_TYPE_Q4_K))
+        return launch_gemv_mr(wtype, W, X, bias, Y, M, N, K, st);
     // measured crossover (GEMV sweep): the per-row kernel is one launch at
     // M = 2 and 4 and faster there, except Q4_K at 4 with N >= 4096; Q8_0
     // below 8 M weights keeps it up to M = 8

@@ -494,10 +494,12 @@ __device__ __forceinline__ float wave_allsum(float v) { return wave_sum(v); }
 // Dot products of rows row0 .. row0+R-1 (clamped to N-1 for loads) with the
 // activation held in xu; every lane returns the R sums.
 // Activation source for rows_dot_m1: registers when a lane owns at most two
-// units (K <= 4096), otherwise re-read from LDS per unit to stay in budget.
-template <int FMT, int UPL>
+// units (K <= 4096), otherwise re-read from LDS per unit to stay in budget
+// (REGS overrides the choice: the several-row GEMV keeps at most four units
+// of all its rows in registers).
+template <int FMT, int UPL, bool REGS = (UPL <= 2)>
 struct XCache {
-    static constexpr bool kRegs = UPL <= 2;
+    static constexpr bool kRegs = REGS;
     XU x[kRegs ? UPL : 1];
     const uint32_t* xs;
     const float* xsum;
@@ -552,15 +554,62 @@ __device__ __forceinline__ void rows_dot_m1(const void* W, int64_t N, int K, int
     for (int rr = 0; rr < R; ++rr) out[rr] = wave_allsum(a[rr]);
 }
 
-template <int FMT, int UPL>
-__device__ __forceinline__ void XCache<FMT, UPL>::init(const uint32_t* xs_, const float* xsum_, int K) {
+// rows_dot_m1 for MR activation rows: every weight unit is loaded once and
+// dotted against each row; out[rr][m] is formed exactly as rows_dot_m1 forms
+// the one-row sum of activation row m (same units, same order, same lane
+// reduction), so each row's result equals a one-row launch's bit for bit.
+template <int FMT, int UPL, int R, int MR, bool XR>
+__device__ __forceinline__ void rows_dot_mr(const void* W, int64_t N, int K, int64_t row0,
+                                            const XCache<FMT, UPL, XR> (&xu)[MR], float (&out)[R][MR]) {
+    constexpr int kB = (UPL > 8 && FMT == FMT_Q6_K) ? 4 : UPL;
+    static_assert(UPL % kB == 0, "units per lane must be a whole number of batches");
+    const int lane = threadIdx.x & 63;
+    const int U = K / 32;
+    float a[R][MR];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) a[rr][m] = 0.f;
+#pragma unroll
+    for (int b0 = 0; b0 < UPL; b0 += kB) {
+        typename RawOf<FMT>::T raw[R][kB];
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            const int64_t row = row0 + rr < N ? row0 + rr : N - 1;
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int u = lane + 64 * (b0 + i);
+                if (u < U) raw[rr][i] = load_unit<FMT>(W, N, K, row, u);
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+#pragma unroll
+            for (int i = 0; i < kB; ++i) {
+                const int u = lane + 64 * (b0 + i);
+                if (u < U) {
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) a[rr][m] += dot_reg(raw[rr][i], u, xu[m].get(b0 + i, u));
+                }
+            }
+        }
+        if constexpr (kB < UPL) asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) out[rr][m] = wave_allsum(a[rr][m]);
+}
+
+template <int FMT, int UPL, bool REGS>
+__device__ __forceinline__ void XCache<FMT, UPL, REGS>::init(const uint32_t* xs_, const float* xsum_, int K) {
     xs = xs_;
     xsum = xsum_;
     if constexpr (kRegs) load_xu_all<FMT, UPL>(xs_, xsum_, K, x);
 }
 
-template <int FMT, int UPL>
-__device__ __forceinline__ XU XCache<FMT, UPL>::get(int i, int u) const {
+template <int FMT, int UPL, bool REGS>
+__device__ __forceinline__ XU XCache<FMT, UPL, REGS>::get(int i, int u) const {
     if constexpr (kRegs) return x[i];
     else return load_xu<FMT>(xs, xsum, u);
 }

@@ -107,6 +107,32 @@ def test_linear_quant_vs_oracle(t, N, K):
         assert np.all(err <= tol), (M, float((err / tol).max()))
 
 
+@pytest.mark.parametrize("t", QTYPES)
+@pytest.mark.parametrize("N,K", [(16400, 2048), (5470, 6144)])
+def test_linear_several_rows_lm_head_sized(t, N, K):
+    """M = 2..4 over matrices of 32 M weights or more (the lm_head's class):
+    the several-row kernel (M = 2 in every format, M = 3 and 4 in Q6_K and
+    Q8_0) against the oracle within the linear tolerance, and each of its
+    output rows bit for bit equal to a one-row launch on that activation row
+    (same units per lane, same order, same lane reduction).  Q4_K at M = 3 / 4
+    runs the matrix-core kernel and is held to the tolerance only.  N leaves
+    a ragged last task; K 6144 keeps the activations in LDS."""
+    rng = np.random.default_rng(N + K + t)
+    raw, Wv = sb.random_matrix(rng, t, N, K)
+    car = carrier(t, raw, N, K)
+    for M in (2, 3, 4):
+        print(f"[linear rows] type={t} N={N} K={K} M={M}", flush=True)
+        X = _f16(rng.standard_normal((M, K)))
+        got = _run_linear(t, car, X, N, K)
+        ref = oracle.linear(Wv, X)
+        tol = _linear_tol(Wv, X, ref)
+        assert np.all(np.abs(got - ref) <= tol), (M, float((np.abs(got - ref) / tol).max()))
+        if M == 2 or t != 12:
+            for m in range(M):
+                one = _run_linear(t, car, X[m:m + 1], N, K)
+                assert np.array_equal(got[m].view(np.uint32), one[0].view(np.uint32)), (M, m)
+
+
 @pytest.mark.parametrize("t", QTYPES + [1])
 @pytest.mark.parametrize("N,K", [(128, 256), (300, 1024), (1024, 512), (4100, 256)])
 def test_linear_big_tiles_vs_oracle(t, N, K):
