@@ -64,6 +64,18 @@ void p1_set_trace(uint64_t* buf);
 namespace p2 {
 namespace {
 
+// Per-shape code options (the OPT template argument of the kernel, chosen by
+// measurement per table entry):
+//   kLate    a stage requests the next stage's weights after emitting its own
+//            output words instead of before its dot products;
+//   kAsmDma  the attention tile's LDS-DMA copies are issued from inline
+//            assembly.  The compiler's wait-count pass does not see them, so it
+//            stops making every later LDS read wait for every outstanding
+//            global load (it cannot tell the tile's DMA writes from other LDS
+//            data); the copies are waited for explicitly (s_waitcnt 0) before
+//            the barrier that publishes the tile.
+constexpr int kLate = 1, kAsmDma = 2;
+
 constexpr int kT = 256;          // threads per workgroup
 constexpr int kW = kT / 64;      // waves per workgroup
 constexpr int kX = 8;            // XCDs
@@ -734,15 +746,29 @@ __device__ __forceinline__ void norm_rope_head(const float* src, const uint32_t 
     }
 }
 
+// One 16-byte LDS-DMA copy per lane: lane i's 16 bytes land at lds + 16 i
+// (lds is wave-uniform).  ASM issues it from inline assembly (M0 = LDS base);
+// no other code in these kernels uses M0, so clobbering it is safe here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <bool ASM>
 __device__ __forceinline__ void dma16(const void* src, void* lds) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+    if constexpr (ASM) {
+        const uint32_t base = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
+                     : "memory", "m0");
+    } else {
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+    }
 }
+#pragma clang diagnostic pop
 
 // Keys [c0, c0 + nk) of one KV head into the LDS tile: K with its 16-byte
 // chunks XOR-swizzled by the key (chunk d8 of key j at d8 ^ (j mod HD/8), so
 // lanes reading consecutive keys hit distinct banks), V in natural order.
 // Slots past nk in the last copy instruction repeat key nk - 1.
-template <int HD>
+template <int HD, bool ASM>
 __device__ __forceinline__ void dma_tile(const uint16_t* Kc, const uint16_t* Vc, int64_t kvd, int64_t col0, int c0,
                                          int nk, uint16_t* kt, uint16_t* vt) {
     constexpr int CPK = HD / 8;
@@ -754,8 +780,8 @@ __device__ __forceinline__ void dma_tile(const uint16_t* Kc, const uint16_t* Vc,
         const int pc = slot % CPK;
         if (j >= nk) j = nk - 1;
         const int64_t row = (int64_t)(c0 + j) * kvd + col0;
-        dma16(Kc + row + 8 * (pc ^ (j & (CPK - 1))), kt + 512 * i);
-        dma16(Vc + row + 8 * pc, vt + 512 * i);
+        dma16<ASM>(Kc + row + 8 * (pc ^ (j & (CPK - 1))), kt + 512 * i);
+        dma16<ASM>(Vc + row + 8 * pc, vt + 512 * i);
     }
 }
 
@@ -778,13 +804,13 @@ __device__ __forceinline__ bool split_of(const Args& a, int w, int pos, Split& s
     return true;
 }
 
-template <int HD>
+template <int HD, bool ASM>
 __device__ __forceinline__ void tile_prefetch(const Args& a, int w, const bx_decode_layer& Ly, int pos,
                                               uint16_t* tile) {
     Split sp;
     if (!split_of(a, w, pos, sp)) return;
-    dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), (int64_t)a.nkv * HD,
-                 (int64_t)sp.g * HD, sp.kb, min(sp.ke - sp.kb, kTile), tile, tile + kTile * HD);
+    dma_tile<HD, ASM>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), (int64_t)a.nkv * HD,
+                      (int64_t)sp.g * HD, sp.kb, min(sp.ke - sp.kb, kTile), tile, tile + kTile * HD);
 }
 
 // Row of word W of a unit's q / k / v vector: segment seg, segment row (or -1
@@ -833,7 +859,7 @@ struct AttScratch {
 // Waves work alone: wave w takes part w mod P of the keys for head w / P
 // (P = 4 / Gq parts per head), one lane per key for the scores, P.V with two
 // head dims per lane; the parts of a head merge in LDS into its record.
-template <int HD>
+template <int HD, bool ASM>
 __device__ __forceinline__ bool attention_split(const Args& a, int w, const Arena& ar, uint16_t* tile,
                                                 const bx_decode_layer& Ly, int layer, int pos) {
     constexpr int CPK = HD / 8;
@@ -990,8 +1016,8 @@ __device__ __forceinline__ bool attention_split(const Args& a, int w, const Aren
     for (int c = 1; c < nch; ++c) {
         const int cn = c == nch - 1 ? nlast : kTile;
         __syncthreads();   // every wave is done with the previous chunk
-        dma_tile<HD>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc), (int64_t)a.nkv * HD,
-                     (int64_t)sp.g * HD, sp.kb + c * kTile, cn, kt, vt);
+        dma_tile<HD, ASM>(static_cast<const uint16_t*>(Ly.Kc), static_cast<const uint16_t*>(Ly.Vc),
+                          (int64_t)a.nkv * HD, (int64_t)sp.g * HD, sp.kb + c * kTile, cn, kt, vt);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         chunk(cn, c == nch - 1);
@@ -1171,8 +1197,9 @@ __device__ __forceinline__ uint32_t ffn_mask(const Args& a) {
 // (q / k / v, K = H), C (Wo, K = the unit's columns), D (gate / up, K = H),
 // E (Wd, K = the FFN slice), H (lm_head, K = H).
 template <int FQ, int FV, int FV2, int FO, int FGU, int FD, int FD2, int FH, int HD, int LA, int UA, int NA, int LC,
-          int UC, int NC, int LD, int UD, int ND, int LE, int UE, int NE, int LH, int UH, int NH>
+          int UC, int NC, int LD, int UD, int ND, int LE, int UE, int NE, int LH, int UH, int NH, int OPT>
 __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
+    constexpr bool kLateReq = (OPT & kLate) != 0, kAsm = (OPT & kAsmDma) != 0;
     extern __shared__ __align__(16) unsigned char dyn[];
     // The attention tile (keys then values), filled by LDS-DMA one layer ahead;
     // stage C reuses it for the split records.
@@ -1276,18 +1303,18 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         tg.template load<FGU>(Ly.Wg, a.F, H, 0, UAn, dwb + zl);
         tu.template load<FGU>(Ly.Wu, a.F, H, 0, UAn, dwb + zl);
     };
-    auto load_e_pass = [&](const bx_decode_layer& Ly, int p, int zl) {
+    auto load_e_pass = [&](const void* Wd, int type_down, int p, int zl) {
         if constexpr (kAnyE) {
-            te.load_pass_kq(Ly.type_down == FMT_Q6_K, Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+            te.load_pass_kq(type_down == FMT_Q6_K, Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
         } else {
-            if (Ly.type_down == FD) te.template load_pass<FD>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
-            else if constexpr (FD2 >= 0) te.template load_pass<FD2>(Ly.Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+            if (type_down == FD) te.template load_pass<FD>(Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
+            else if constexpr (FD2 >= 0) te.template load_pass<FD2>(Wd, H, a.F, fb / 32, UEn, ewb + zl, p);
         }
     };
 
 #pragma unroll
     for (int p = 0; p < NA; ++p) load_a_pass(lt[0], p, opaque_zero());
-    tile_prefetch<HD>(a, w, lt[0], pos, tile);
+    tile_prefetch<HD, kAsm>(a, w, lt[0], pos, tile);
     pin();
 
     for (int l = 0; l < a.L; ++l) {
@@ -1312,8 +1339,9 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             __syncthreads();
             norm_to_xs(ar, H, ss, Ly.in_ln, a.eps);
             stamp(a, sl + 0);
-            // Wo rows stream while q / k / v are computed and travel
-            if (unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o + zl, UCn, cwb);
+            // Wo rows stream while q / k / v are computed and travel (kLate:
+            // requested after the q / k / v words are out)
+            if (!kLateReq && unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o + zl, UCn, cwb);
             pin();
             sub(a, l, 8);
             if (unit && awb < awe) {
@@ -1338,17 +1366,20 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             if (unit)
                 emit_words<false>(ar.rows, arb, are, wseg, a.qkv + (int64_t)x * a.qkv_stride + woff + zl,
                                   tag_of(a, l, 0));
+            if (kLateReq && unit) tc.template load<FO>(Ly.Wo, H, a.nq * HD, uc_o + zl, UCn, cwb);
+            pin();
         }
         stamp(a, sl + 1);
         // ---- B: attention splits
-        if (!__syncthreads_and(attention_split<HD>(a, w, ar, tile, Ly, l, pos))) return;
+        if (!__syncthreads_and(attention_split<HD, kAsm>(a, w, ar, tile, Ly, l, pos))) return;
         stamp(a, sl + 2);
         // ---- C: combine, Wo partial
         if (unit) {
             if (!combine<HD>(a, x, ar, reinterpret_cast<float*>(tile), l, pos)) return;
             stamp(a, sl + 3);
-            // gate / up rows stream while the Wo partials travel
-            load_d(Ly, zl);
+            // gate / up rows stream while the Wo partials travel (before the
+            // Wo dots, or with kLate after the partials are out)
+            if (!kLateReq) load_d(Ly, zl);
             pin();
             sub(a, l, 17);
             {
@@ -1364,6 +1395,8 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             sub(a, l, 18);
             __syncthreads();
             emit_partial(a, ar, a.pwo + zl, x, r, tag_of(a, l, 2));
+            if (kLateReq) load_d(Ly, zl);
+            pin();
         } else {
             load_d(Ly, zl);
             pin();
@@ -1381,9 +1414,19 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             __syncthreads();
             norm_to_xs(ar, H, ss, Ly.post_ln, a.eps);
             stamp(a, sl + 5);
-            // Wd rows stream while gate / up are computed and travel
+            // E's matrix and format, read from the LDS table here: with global
+            // stores and loads both outstanding the compiler waits for all of
+            // them before a dependent use, so a table read just before a late
+            // request, after the SwiGLU words' stores, would wait for those
+            const void* const e_w = Ly.Wd;
+            const int e_t = Ly.type_down;
+            pin();
+            // Wd rows stream while gate / up are computed and travel (kLate:
+            // requested after the SwiGLU words are out)
+            if (!kLateReq) {
 #pragma unroll
-            for (int p = 0; p < NE; ++p) load_e_pass(Ly, p, zl);
+                for (int p = 0; p < NE; ++p) load_e_pass(e_w, e_t, p, zl);
+            }
             pin();
             sub(a, l, 13);
             if (dwb < dwe) {
@@ -1410,6 +1453,11 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             __syncthreads();
             emit_words<false>(ar.rows, gb, ge, a.wact, a.act + (int64_t)x * a.act_stride + r * a.wact + zl,
                               tag_of(a, l, 3));
+            if (kLateReq) {
+#pragma unroll
+                for (int p = 0; p < NE; ++p) load_e_pass(e_w, e_t, p, zl);
+            }
+            pin();
             sub(a, l, 14);
         }
         stamp(a, sl + 6);
@@ -1459,7 +1507,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         if (l + 1 < a.L) {
 #pragma unroll
             for (int p = 0; p < NA; ++p) load_a_pass(Ln, p, zl);
-            tile_prefetch<HD>(a, w, Ln, pos, tile);
+            tile_prefetch<HD, kAsm>(a, w, Ln, pos, tile);
         }
         pin();
         sub(a, l, 33);
@@ -1626,43 +1674,53 @@ struct Entry {
     KFn fn;
 };
 
-#define P2(PREF, FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE, LH, \
-           UH, NH)                                                                                                   \
-    Entry {                                                                                                         \
-        FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, PREF,                                                     \
-            persist2_kernel<FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE, \
-                            LH, UH, NH>                                                                             \
+#define P2(PREF, OPT, FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, \
+           NE, LH, UH, NH)                                                                                            \
+    Entry {                                                                                                          \
+        FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, H, SO, FX, PREF,                                                      \
+            persist2_kernel<FQ, FV, FV2, FO, FGU, FD, FD2, FH, HD, LA, UA, NA, LC, UC, NC, LD, UD, ND, LE, UE, NE,  \
+                            LH, UH, NH, OPT>                                                                         \
     }
 
 constexpr int Q4 = FMT_Q4_K, Q6 = FMT_Q6_K, Q8 = FMT_Q8_0, F16 = FMT_F16;
 
 // Shapes with an instantiation: the BASELINE widths and the test models.  The
 // first argument says whether a shape runs here even where the first
-// persistent kernel has an instantiation: measured on MI355X (decode steps at
-// a 1024-token context, ms, this kernel / the first), 0.6B Q8_0 0.788 / 0.976,
-// 8B Q4_K 2.386 / 2.469, 1.7B Q4_K 1.041 / 1.030, Llama-3-8B widths
-// 2.499 / 2.431.  The 1.7B Q4_K_M layout has no instantiation there
-// (1.073 here against 1.387 for the captured per-stage graph).
+// persistent kernel has an instantiation; the second holds the code options
+// (kLate, kAsmDma).  Measured on MI355X (decode steps at a 1024-token
+// context, ms; this kernel with its options / without options / the first
+// kernel): 1.7B Q4_K 0.955 / 1.024 / 1.004, 0.6B Q8_0 0.741 / 0.765 / 0.976,
+// 8B Q4_K - / 2.340 / 2.469 (kAsmDma 2.403, both 2.375), Llama-3-8B widths
+// 2.298 / 2.504 / 2.431.  The 1.7B Q4_K_M layout (1.072 / 1.071; no
+// instantiation in the first kernel, 1.387 on the captured per-stage graph)
+// takes the same options as the 1.7B.
 // Per stage (lanes per row, units per lane, passes): a wave's first task is
 // requested one stage ahead; rows past it load in place.
+constexpr int kBoth = kLate | kAsmDma;
 const Entry kTable[] = {
     // Qwen3-1.7B (H 2048, F 6144, 16 / 8 heads): Q4_K with Q6_K v / down and an
     // untied Q6_K head; the same with v / down Q6_K or
     // Q4_K per layer and the tied FP16 head (the real Q4_K_M files)
-    P2(false, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 8),
-    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, F16, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1, 4),
+    P2(true, kBoth, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1,
+       8),
+    P2(true, kBoth, Q4, Q6, Q4, Q4, Q4, Q6, Q4, F16, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1,
+       4),
     // Qwen3-0.6B (H 1024, F 3072): Q8_0 with the tied FP16 head
-    P2(true, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1, 4),
+    P2(true, kBoth, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1,
+       4),
     // Qwen3-8B (H 4096, F 12288, 32 / 8 heads): Q4_K, Q6_K head
-    P2(true, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2, 4),
+    P2(true, 0, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2,
+       4),
     // Llama-3-8B widths (H 4096, F 14336): Q4_K with Q6_K v / down and head
-    P2(false, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64, 2, 4),
+    P2(true, kBoth, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64,
+       2, 4),
     // test models: H 256 / head_dim 64 with F 2048 (Q4_K, Q6_K or Q4_K v / down, Q6_K head)
-    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 64, 256, 256, 256, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1),
+    P2(true, kBoth, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 64, 256, 256, 256, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1, 8, 1, 1),
     // H 512 / F 1024 / head_dim 64, Q8_0, tied FP16 head
-    P2(true, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 64, 512, 128, 128, 16, 1, 1, 4, 1, 1, 16, 1, 1, 4, 1, 1, 16, 1, 1),
+    P2(true, kBoth, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 64, 512, 128, 128, 16, 1, 1, 4, 1, 1, 16, 1, 1, 4, 1, 1, 16, 1,
+       1),
     // H 256 / F 6144 / head_dim 128, one KV head (Mistral-shaped, Q4_K / Q6_K)
-    P2(true, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 256, 512, 768, 8, 1, 1, 16, 1, 1, 8, 1, 1, 8, 3, 1, 8, 1, 1),
+    P2(true, kBoth, Q4, Q6, Q4, Q4, Q4, Q6, Q4, Q6, 128, 256, 512, 768, 8, 1, 1, 16, 1, 1, 8, 1, 1, 8, 3, 1, 8, 1, 1),
 };
 
 struct Plan {
