@@ -1238,6 +1238,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         return;
     }
     const int w = x + kX * r;
+    if (a.trace && tidx() == 0) a.trace[(size_t)blockIdx.x * kTraceSlots + 1000] = (uint64_t)w;   // logical id
     // embedding row -> h
     for (int i = tidx(); i < H; i += kT) ar.hv[i] = h2f(a.embed[(int64_t)tok * H + i]);
     __syncthreads();
@@ -1571,7 +1572,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             group_sum<LH, NH>(o);
             emit_rows<LH, NH>(r0, hwe, o, [&](int row, float v) {
                 const uint16_t h16 = f2h(v);
-                a.logits[row] = h16;
+                tile[row - vb] = h16;
                 const float q = h2f(h16);
                 if (besti < 0 || q > best || (q == best && row < besti)) {
                     best = q;
@@ -1579,15 +1580,27 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                 }
             });
         };
+        // Both buffers' requests are unconditional (past the wave's rows they
+        // re-read its current block, which the L2 holds): a request on one
+        // branch only would make the compiler's wait for the other buffer
+        // cover every load in flight.
         for (int t = hwb; t < hwe; t += 2 * RH) {
             const int t1 = t + RH;
-            if (t1 < hwe) load(b1, t1);
+            load(b1, t1 < hwe ? t1 : t);
+            __builtin_amdgcn_sched_barrier(0);   // the requests go out before the other buffer's math
             dot(b0, t);
             if (t1 >= hwe) break;
-            if (t1 + RH < hwe) load(b0, t1 + RH);
+            load(b0, t1 + RH < hwe ? t1 + RH : t1);
+            __builtin_amdgcn_sched_barrier(0);
             dot(b1, t1);
         }
     }
+    // The logits leave through LDS after the loop: a global store inside it
+    // would leave stores and loads outstanding together, and the compiler then
+    // makes each row block's dot wait for every load in flight, the other
+    // buffer's included.
+    __syncthreads();
+    for (int i = tidx(); i < ve - vb; i += kT) a.logits[vb + i] = tile[i];
     stamp(a, sh + 1);
     // workgroup argmax: every lane holds its best (lowest index among equals)
     {
@@ -1693,7 +1706,8 @@ constexpr int Q4 = FMT_Q4_K, Q6 = FMT_Q6_K, Q8 = FMT_Q8_0, F16 = FMT_F16;
 // 8B Q4_K - / 2.340 / 2.469 (kAsmDma 2.403, both 2.375), Llama-3-8B widths
 // 2.298 / 2.504 / 2.431.  The 1.7B Q4_K_M layout (1.072 / 1.071; no
 // instantiation in the first kernel, 1.387 on the captured per-stage graph)
-// takes the same options as the 1.7B.
+// takes the same options as the 1.7B.  The lm_head streams 4 rows per wave
+// and buffer (8 rows: 63 us for the 1.7B's 255 MB, 4 rows: 54 us).
 // Per stage (lanes per row, units per lane, passes): a wave's first task is
 // requested one stage ahead; rows past it load in place.
 constexpr int kBoth = kLate | kAsmDma;
@@ -1702,7 +1716,7 @@ const Entry kTable[] = {
     // untied Q6_K head; the same with v / down Q6_K or
     // Q4_K per layer and the tied FP16 head (the real Q4_K_M files)
     P2(true, kBoth, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1,
-       8),
+       4),
     P2(true, kBoth, Q4, Q6, Q4, Q4, Q4, Q6, Q4, F16, 128, 2048, 256, 768, 64, 1, 5, 8, 1, 2, 64, 1, 6, 8, 3, 2, 64, 1,
        4),
     // Qwen3-0.6B (H 1024, F 3072): Q8_0 with the tied FP16 head
@@ -1850,6 +1864,9 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     o.lds_dyn = arena_bytes(H, kmax, hd, gpu, Gq);
     // the combine's weights (heads x S) and the head's candidates live in the attention scratch
     if ((size_t)gpu * Gq * smax > att_floats(hd, gpu, Gq)) return fail(BX_EUNSUPPORTED, "persist2: scratch");
+    // the head's FP16 logits of a workgroup's vocabulary rows are staged in the
+    // attention tile (at least 2 kTile hd halves)
+    if ((d.vocab + kG - 1) / kG > 2 * kTile * hd) return fail(BX_EUNSUPPORTED, "persist2: vocabulary too large");
     return BX_OK;
 }
 
