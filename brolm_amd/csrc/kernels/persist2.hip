@@ -566,10 +566,26 @@ __device__ __forceinline__ void put_swz(uint32_t* xs, int e, uint32_t v) {
     reinterpret_cast<uint16_t*>(xs)[4 * (e >> 2) + 2 * (e & 1) + ((e >> 1) & 1)] = (uint16_t)v;
 }
 
+// A thread's norm gammas (8 FP16 values per 256-thread round, H <= 4096),
+// requested before the stage's input polls so that their latency hides under
+// the hand-off.  Loads past H repeat the first 8 values (issued
+// unconditionally, so the compiler counts them exactly).
+constexpr int kGammaRounds = 2;
+struct GammaRegs {
+    u4v g[kGammaRounds];
+    __device__ __forceinline__ void load(const void* gamma, int H) {
+#pragma unroll
+        for (int i = 0; i < kGammaRounds; ++i) {
+            const int c = tidx() + i * kT;
+            g[i] = gptr<u4v>(gamma)[8 * c < H ? c : 0];
+        }
+    }
+};
+
 // RMSNorm of the residual into the swizzled FP16 activation and its 8-sums:
 // x = f16(h * inv * gamma), inv = (mean(h^2) + eps)^-1/2; `ss` is this
 // thread's share of sum(h^2) (every element counted by exactly one thread).
-__device__ __forceinline__ void norm_to_xs(const Arena& ar, int H, float ss, const void* gamma, float eps) {
+__device__ __forceinline__ void norm_to_xs(const Arena& ar, int H, float ss, const GammaRegs& gr, float eps) {
     ss = wave_sum(ss);
     if ((tidx() & 63) == 0) ar.red[tidx() >> 6] = ss;
     __syncthreads();
@@ -577,8 +593,11 @@ __device__ __forceinline__ void norm_to_xs(const Arena& ar, int H, float ss, con
 #pragma unroll
     for (int i = 0; i < kW; ++i) tot += ar.red[i];
     const float inv = 1.0f / sqrtf(tot / (float)H + eps);
-    for (int c = tidx(); 8 * c < H; c += kT) {
-        const u4v gm = gptr<u4v>(gamma)[c];
+#pragma unroll
+    for (int i = 0; i < kGammaRounds; ++i) {
+        const int c = tidx() + i * kT;
+        if (8 * c >= H) break;
+        const u4v gm = gr.g[i];
         const float4 v0 = *reinterpret_cast<const float4*>(ar.hv + 8 * c);
         const float4 v1 = *reinterpret_cast<const float4*>(ar.hv + 8 * c + 4);
         const uint32_t h0 = norm_f16(v0.x, inv, h2f(gm.x & 0xffff)), h1 = norm_f16(v0.y, inv, h2f(gm.x >> 16));
@@ -1326,6 +1345,8 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         // ---- A: residual, norm, q / k / v rows; the Wo and gate / up blocks
         // are requested between the passes
         {
+            GammaRegs gr;
+            gr.load(Ly.in_ln, H);
             float ss = 0.f;
             if (l > 0) {
                 if (!reduce_block(a, ar, a.pdn + zl, xmask_d, x, r, tag_of(a, l - 1, 4), 1, a.hupd + zl,
@@ -1338,7 +1359,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                 for (int i = tidx(); i < H; i += kT) ss += ar.hv[i] * ar.hv[i];
             }
             __syncthreads();
-            norm_to_xs(ar, H, ss, Ly.in_ln, a.eps);
+            norm_to_xs(ar, H, ss, gr, a.eps);
             stamp(a, sl + 0);
             // Wo rows stream while q / k / v are computed and travel (kLate:
             // requested after the q / k / v words are out)
@@ -1406,6 +1427,8 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         // ---- D: residual, norm, gate / up rows of the slice; the Wd block is
         // requested between the passes
         {
+            GammaRegs gr;
+            gr.load(Ly.post_ln, H);
             float ss = 0.f;
             if (!reduce_block(a, ar, a.pwo + zl, xmask_o, x, r, tag_of(a, l, 2), 3, a.hupo + zl, tag_of(a, l, 5)))
                 return;
@@ -1413,7 +1436,7 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
             if (!apply_update(a, ar, a.hupo + zl, x, tag_of(a, l, 5), 8, ss)) return;
             sub(a, l, 11);
             __syncthreads();
-            norm_to_xs(ar, H, ss, Ly.post_ln, a.eps);
+            norm_to_xs(ar, H, ss, gr, a.eps);
             stamp(a, sl + 5);
             // E's matrix and format, read from the LDS table here: with global
             // stores and loads both outstanding the compiler waits for all of
@@ -1542,12 +1565,14 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
         };
         if (hwb < hwe) load(b0, hwb);
         pin();
+        GammaRegs gr;
+        gr.load(a.final_norm, H);
         float ss = 0.f;
         if (!reduce_block(a, ar, a.pdn, xmask_d, x, r, tag_of(a, a.L - 1, 4), 5, a.hupd, tag_of(a, a.L - 1, 6)))
             return;
         if (!apply_update(a, ar, a.hupd, x, tag_of(a, a.L - 1, 6), 9, ss)) return;
         __syncthreads();
-        norm_to_xs(ar, H, ss, a.final_norm, a.eps);
+        norm_to_xs(ar, H, ss, gr, a.eps);
         stamp(a, sh + 0);
         XU xu[UH];
 #pragma unroll
@@ -1770,7 +1795,8 @@ int plan_of(const bx_decode_dims& d, Plan& o) {
     const int nu = d.n_kv / gpu, smax = kR / gpu;
     const int vt[2] = {d.qkv_type_v, d.v_alt_type}, dt[2] = {d.down_type, d.down_alt_type};
     const int fblk = std::max(type_elems(d.down_type), type_elems(d.down_alt_type));
-    if (fblk == 0 || F % fblk || H % 256) return fail(BX_EUNSUPPORTED, "persist2: widths");
+    if (fblk == 0 || F % fblk || H % 256 || H > 8 * kT * kGammaRounds)
+        return fail(BX_EUNSUPPORTED, "persist2: widths");
     const int nbF = F / fblk, fxmax = (nbF + kX - 1) / kX * fblk;
     // Every XCD holds an FFN slice: its E stage then waits for all 32 of its
     // workgroups' D stages, which is what keeps an owner from overwriting an
