@@ -37,13 +37,13 @@ STEP_DESC = {
 # HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs
 # (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
 # device copy of known size in the same run), with the commit they were
-# measured at (re-measured whenever persist.hip changes):
-# profiles/persist_kernel_traffic_qwen3-1.7b-q4k.md.
+# measured at (re-measured whenever the persistent kernel changes):
+# profiles/persist2_kernel_traffic_qwen3-1.7b-q4k.md.
 MEASURED_TRAFFIC = {
-    ("qwen3-1.7b-q4k", "persistent"): (1_601_485_576, "325bded"),
+    ("qwen3-1.7b-q4k", "persistent"): (1_510_464_168, "43b4e7b"),
 }
 KERNEL_DESC = {
-    "persistent": "persist_kernel: the whole decode step (all layers, lm_head, argmax) in one launch",
+    "persistent": "persist2_kernel: the whole decode step (all layers, lm_head, argmax) in one launch",
     "graph": "captured decode step (hipGraph launch)",
     "eager": "decode step (eager kernel sequence)",
 }
