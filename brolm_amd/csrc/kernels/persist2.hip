@@ -485,6 +485,16 @@ struct Task {
         for (int p = 0; p < NP; ++p) out[p] = dot_pass<FMT>(xr, U, p, slot);
         group_sum<LPR, NP>(out);
     }
+    // The first np passes only (np wave-uniform): a wave with fewer rows than
+    // the task holds skips the products of the passes past its rows.
+    template <int FMT>
+    __device__ __forceinline__ void dot_n(const XRegs<FMT, LPR, UPL>& xr, int U, int np, float (&out)[NP]) const {
+        const int slot = (tidx() & 63) & (LPR - 1);
+        np = __builtin_amdgcn_readfirstlane(np);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) out[p] = p < np ? dot_pass<FMT>(xr, U, p, slot) : 0.f;
+        group_sum<LPR, NP>(out);
+    }
 };
 
 // Two tasks of one format and shape (gate / up) pass by pass, side(p) after each.
@@ -1374,7 +1384,10 @@ __global__ __launch_bounds__(kT, 1) void persist2_kernel(Args a) {
                     for (int t0 = awb; t0 < awe; t0 += RA) {
                         float o[NA];
                         if (t0 != awb) ta.template load<F>(a_w(Ly), aN, H, 0, UAn, srow0 + t0 + zl);
-                        ta.template dot<F>(xr, UAn, o);
+                        // a segment's rows spread over its workgroups' waves, so a
+                        // wave (v rows: Q6_K, fewer per workgroup) may hold fewer
+                        // rows than the task's passes
+                        ta.template dot_n<F>(xr, UAn, (awe - t0 + (64 / LA) - 1) / (64 / LA), o);
                         emit_rows<LA, NA>(t0, awe, o, [&](int row, float v) { ar.rows[row - arb] = v; });
                     }
                 };
