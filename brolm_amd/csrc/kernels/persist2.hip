@@ -1741,7 +1741,8 @@ constexpr int Q4 = FMT_Q4_K, Q6 = FMT_Q6_K, Q8 = FMT_Q8_0, F16 = FMT_F16;
 // (kLate, kAsmDma).  Measured on MI355X (decode steps at a 1024-token
 // context, ms; this kernel with its options / without options / the first
 // kernel): 1.7B Q4_K 0.955 / 1.024 / 1.004, 0.6B Q8_0 0.741 / 0.765 / 0.976,
-// 8B Q4_K - / 2.340 / 2.469 (kAsmDma 2.403, both 2.375), Llama-3-8B widths
+// 8B Q4_K 2.375 / 2.340 / 2.469 (kAsmDma 2.403; with the gammas requested
+// early and the head's logits staged: both 2.256, none 2.303), Llama-3-8B widths
 // 2.298 / 2.504 / 2.431.  The 1.7B Q4_K_M layout (1.072 / 1.071; no
 // instantiation in the first kernel, 1.387 on the captured per-stage graph)
 // takes the same options as the 1.7B.  The lm_head streams 4 rows per wave
@@ -1761,7 +1762,7 @@ const Entry kTable[] = {
     P2(true, kBoth, Q8, Q8, -1, Q8, Q8, Q8, -1, F16, 128, 1024, 256, 384, 32, 1, 2, 8, 1, 1, 32, 1, 2, 8, 2, 1, 32, 1,
        4),
     // Qwen3-8B (H 4096, F 12288, 32 / 8 heads): Q4_K, Q6_K head
-    P2(true, 0, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2,
+    P2(true, kBoth, Q4, Q4, -1, Q4, Q4, Q4, -1, Q6, 128, 4096, 512, 1536, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 3, 2, 64, 2,
        4),
     // Llama-3-8B widths (H 4096, F 14336): Q4_K with Q6_K v / down and head
     P2(true, kBoth, Q4, Q6, -1, Q4, Q4, Q6, -1, Q6, 128, 4096, 512, 1792, 64, 2, 4, 16, 1, 4, 64, 2, 2, 16, 4, 1, 64,
