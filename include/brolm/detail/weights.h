@@ -64,11 +64,17 @@ public:
                             const std::string& label) const override;
 
 private:
-    const brotensor::gguf::TensorInfo* find_(const std::string& ggml_name) const;
-    const brotensor::gguf::TensorInfo& need_(const std::string& hf_name, const std::string& label) const;
-    static void check_shape_(const brotensor::gguf::TensorInfo& info, int rows, int cols, const std::string& label);
-    static void upload_dense_(const brotensor::gguf::TensorInfo& info, int rows, int cols, brotensor::Tensor& dst,
-                              const std::string& label);
+    // A tensor resolved for one request: its GGUF record and the text that
+    // names it in errors ("label ('ggml name')").
+    struct Resolved {
+        const brotensor::gguf::TensorInfo* info;
+        std::string where;
+    };
+    // The record of a ggml name in the first shard that holds it, or null.
+    const brotensor::gguf::TensorInfo* lookup_ggml_(const std::string& ggml_name) const;
+    // Maps an HF name, finds it and checks that it holds rows x cols elements;
+    // throws std::runtime_error otherwise.
+    Resolved resolve_(const std::string& hf_name, int rows, int cols, const std::string& label) const;
 
     std::vector<const brotensor::gguf::File*> shards_;
     NameMap mapper_;
