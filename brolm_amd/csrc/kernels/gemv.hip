@@ -126,6 +126,89 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
     }
 }
 
+// M = 1 with one unit per lane (K <= 2048): each wavefront double-buffers its
+// row blocks (the next block's loads go out before the current block's
+// math) and keeps its sums in LDS until its last block, because a global
+// store inside the loop would make every later wait for weights a wait for
+// all loads in flight.  The row sums are formed as in gemv_m1_kernel, so Y
+// is the same bit for bit.
+constexpr int kM1pRows = 4;       // rows per block
+constexpr int kM1pMaxBlocks = 32; // blocks per wavefront at most (the grid grows past that)
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void gemv_m1p_kernel(const void* __restrict__ W,
+                                                           const uint16_t* __restrict__ X,
+                                                           const uint16_t* __restrict__ bias,
+                                                           uint16_t* __restrict__ Y, int N, int K) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    uint32_t* xs = smem;
+    float* xsum = reinterpret_cast<float*>(smem + K / 2);
+    float* sums = xsum + K / 8;   // [kWaves][kM1pMaxBlocks * kM1pRows]
+    stage_x_f16<true, false>(X, K, 1, K, xs, K / 2, xsum, K / 16);
+    __syncthreads();
+    sums8_from_lds(xs, K, xsum);
+    __syncthreads();
+    constexpr int R = kM1pRows;
+    using Raw = typename RawOf<FMT>::T;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int U = K / 32;
+    const int uc = lane < U ? lane : U - 1;
+    const XU xu = load_xu<FMT>(xs, xsum, uc);
+    const int64_t tasks = ((int64_t)N + R - 1) / R;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    const int64_t t0 = (int64_t)blockIdx.x * kWaves + wave;
+    float* ws = sums + wave * (kM1pMaxBlocks * R);
+    Raw b0[R], b1[R];
+    auto load = [&](Raw (&b)[R], int64_t t) {
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            const int64_t row = t * R + rr < N ? t * R + rr : N - 1;
+            b[rr] = load_unit<FMT>(W, N, K, row, uc);
+        }
+    };
+    int k = 0;
+    auto dot = [&](const Raw (&b)[R]) {
+        float a[R];
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            const float c = dot_reg(b[rr], uc, xu);
+            a[rr] = lane < U ? c : 0.f;
+        }
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) a[rr] = wave_allsum(a[rr]);
+        if (lane == 0) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) ws[k * R + rr] = a[rr];
+        }
+        ++k;
+    };
+    // requests are unconditional (past the wave's last block they re-read its
+    // current one): a request on one branch only would widen the other
+    // buffer's wait to every load in flight
+    if (t0 + stride >= tasks) {   // at most one block: nothing to overlap
+        if (t0 < tasks) {
+            load(b0, t0);
+            dot(b0);
+        }
+    } else {
+        load(b0, t0);
+        for (int64_t t = t0; t < tasks; t += 2 * stride) {
+            const int64_t t1 = t + stride;
+            load(b1, t1 < tasks ? t1 : t);
+            __builtin_amdgcn_sched_barrier(0);
+            dot(b0);
+            if (t1 >= tasks) break;
+            load(b0, t1 + stride < tasks ? t1 + stride : t1);
+            __builtin_amdgcn_sched_barrier(0);
+            dot(b1);
+        }
+    }
+    for (int e = lane; e < k * R; e += 64) {
+        const int j = e / R, rr = e - j * R;
+        const int64_t row = (t0 + (int64_t)j * stride) * R + rr;
+        if (row < N) Y[row] = f2h(ws[e] + (bias ? h2f(bias[row]) : 0.f));
+    }
+}
+
 // 2 <= M <= 4 (MR rows): gemv_m1_kernel with MR activation rows staged and
 // held per lane (in registers while MR x UPL <= 4 units, otherwise re-read
 // from LDS): each weight unit is loaded once for all the rows, so a launch
@@ -238,6 +321,28 @@ int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* 
     const int upl = upl_for(K);
     if (upl > 16) return fail(BX_EUNSUPPORTED, "gemv: K above 32768 at M = 1");
     if (K % 8192 == 0 && K > 16384) return gemv_m1_ksplit(wtype, W, X, bias, Y, nullptr, N, K, st);
+#ifndef EXP_M1P
+#define EXP_M1P 1
+#endif
+    if (EXP_M1P && upl == 1) {
+        // one round of resident workgroups, more where a wavefront would own
+        // more than kM1pMaxBlocks blocks
+        const int64_t tasks = ((int64_t)N + kM1pRows - 1) / kM1pRows;
+        const size_t lds1 = (size_t)K * 2 + (size_t)(K / 8) * 4 + (size_t)kWaves * kM1pMaxBlocks * kM1pRows * 4;
+        BX_DISPATCH_FMT(wtype, {
+            const void* fn = reinterpret_cast<const void*>(&gemv_m1p_kernel<FMT_>);
+            static int occ = 0;   // one per format (each case of the dispatch has its own)
+            if (occ == 0 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kThreads, lds1) != hipSuccess)
+                occ = 1;
+            if (occ < 1) occ = 1;
+            int64_t blocks = std::max<int64_t>((int64_t)num_cus() * occ,
+                                               (tasks + (int64_t)kWaves * kM1pMaxBlocks - 1) /
+                                                   ((int64_t)kWaves * kM1pMaxBlocks));
+            blocks = std::min<int64_t>(blocks, (tasks + kWaves - 1) / kWaves);
+            gemv_m1p_kernel<FMT_><<<(unsigned)blocks, kThreads, lds1, st>>>(W, X, bias, Y, N, K);
+        })
+        return launch_check("gemv m1p");
+    }
     const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
