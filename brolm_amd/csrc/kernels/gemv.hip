@@ -126,37 +126,41 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_kernel(const void* __restric
     }
 }
 
-// M = 1 with one unit per lane (K <= 2048): each wavefront double-buffers its
-// row blocks (the next block's loads go out before the current block's
-// math) and keeps its sums in LDS until its last block, because a global
-// store inside the loop would make every later wait for weights a wait for
-// all loads in flight.  The row sums are formed as in gemv_m1_kernel, so Y
-// is the same bit for bit.
+// MR <= 4 activation rows with one unit per lane (K <= 2048): each wavefront
+// double-buffers its weight-row blocks (the next block's loads go out before
+// the current block's math) and keeps its sums in LDS until its last block,
+// because a global store inside the loop would make every later wait for
+// weights a wait for all loads in flight.  Each weight unit is loaded once for
+// the MR rows, and every sum is formed as gemv_m1_kernel forms a one-row sum,
+// so row m of Y equals a one-row launch on row m of X bit for bit.
 constexpr int kM1pRows = 4;       // rows per block
 constexpr int kM1pMaxBlocks = 32; // blocks per wavefront at most (the grid grows past that)
-template <int FMT>
+template <int FMT, int MR>
 __global__ __launch_bounds__(kThreads) void gemv_m1p_kernel(const void* __restrict__ W,
                                                            const uint16_t* __restrict__ X,
                                                            const uint16_t* __restrict__ bias,
                                                            uint16_t* __restrict__ Y, int N, int K) {
     extern __shared__ __align__(16) uint32_t smem[];
-    uint32_t* xs = smem;
-    float* xsum = reinterpret_cast<float*>(smem + K / 2);
-    float* sums = xsum + K / 8;   // [kWaves][kM1pMaxBlocks * kM1pRows]
-    stage_x_f16<true, false>(X, K, 1, K, xs, K / 2, xsum, K / 16);
+    uint32_t* xs = smem;                                           // MR rows of K / 2 pairs
+    float* xsum = reinterpret_cast<float*>(smem + MR * (K / 2));   // MR rows of K / 8 sums
+    float* sums = xsum + MR * (K / 8);   // [kWaves][kM1pMaxBlocks * kM1pRows * MR]
+    stage_x_f16<true, false>(X, K, MR, K, xs, K / 2, xsum, K / 8);
     __syncthreads();
-    sums8_from_lds(xs, K, xsum);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) sums8_from_lds(xs + m * (K / 2), K, xsum + m * (K / 8));
     __syncthreads();
     constexpr int R = kM1pRows;
     using Raw = typename RawOf<FMT>::T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int U = K / 32;
     const int uc = lane < U ? lane : U - 1;
-    const XU xu = load_xu<FMT>(xs, xsum, uc);
+    XU xu[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) xu[m] = load_xu<FMT>(xs + m * (K / 2), xsum + m * (K / 8), uc);
     const int64_t tasks = ((int64_t)N + R - 1) / R;
     const int64_t stride = (int64_t)gridDim.x * kWaves;
     const int64_t t0 = (int64_t)blockIdx.x * kWaves + wave;
-    float* ws = sums + wave * (kM1pMaxBlocks * R);
+    float* ws = sums + wave * (kM1pMaxBlocks * R * MR);
     Raw b0[R], b1[R];
     auto load = [&](Raw (&b)[R], int64_t t) {
 #pragma unroll
@@ -167,17 +171,23 @@ __global__ __launch_bounds__(kThreads) void gemv_m1p_kernel(const void* __restri
     };
     int k = 0;
     auto dot = [&](const Raw (&b)[R]) {
-        float a[R];
+        float a[R][MR];
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-            const float c = dot_reg(b[rr], uc, xu);
-            a[rr] = lane < U ? c : 0.f;
-        }
+        for (int rr = 0; rr < R; ++rr)
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) a[rr] = wave_allsum(a[rr]);
+            for (int m = 0; m < MR; ++m) {
+                const float c = dot_reg(b[rr], uc, xu[m]);
+                a[rr][m] = lane < U ? c : 0.f;
+            }
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) a[rr][m] = wave_allsum(a[rr][m]);
         if (lane == 0) {
 #pragma unroll
-            for (int rr = 0; rr < R; ++rr) ws[k * R + rr] = a[rr];
+            for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) ws[(k * R + rr) * MR + m] = a[rr][m];
         }
         ++k;
     };
@@ -205,7 +215,11 @@ __global__ __launch_bounds__(kThreads) void gemv_m1p_kernel(const void* __restri
     for (int e = lane; e < k * R; e += 64) {
         const int j = e / R, rr = e - j * R;
         const int64_t row = (t0 + (int64_t)j * stride) * R + rr;
-        if (row < N) Y[row] = f2h(ws[e] + (bias ? h2f(bias[row]) : 0.f));
+        if (row < N) {
+            const float bv = bias ? h2f(bias[row]) : 0.f;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) Y[(int64_t)m * N + row] = f2h(ws[e * MR + m] + bv);
+        }
     }
 }
 
@@ -316,33 +330,51 @@ __global__ __launch_bounds__(kThreads) void gemv_m1_ksplit_kernel(const void* __
     }
 }
 
+// gemv_m1p_kernel for M (1..4) rows at K <= 2048: one round of resident
+// workgroups, more where a wavefront would own more than kM1pMaxBlocks blocks.
+int launch_gemv_m1p(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int M, int N,
+                    int K, hipStream_t st) {
+    const int64_t tasks = ((int64_t)N + kM1pRows - 1) / kM1pRows;
+    const size_t lds = (size_t)M * ((size_t)K * 2 + (size_t)(K / 8) * 4) +
+                       (size_t)kWaves * kM1pMaxBlocks * kM1pRows * M * 4;
+    auto go = [&](auto fn_kernel) -> int {
+        const void* fn = reinterpret_cast<const void*>(fn_kernel);
+        // resident workgroups per CU, asked once per kernel and LDS size
+        struct Occ {
+            const void* fn;
+            size_t lds;
+            int occ;
+        };
+        thread_local Occ cache[32];
+        thread_local int ncache = 0;
+        int occ = 0;
+        for (int i = 0; i < ncache; ++i)
+            if (cache[i].fn == fn && cache[i].lds == lds) occ = cache[i].occ;
+        if (occ == 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kThreads, lds) != hipSuccess || occ < 1) occ = 1;
+            cache[ncache < 32 ? ncache++ : 31] = Occ{fn, lds, occ};
+        }
+        int64_t blocks = std::max<int64_t>((int64_t)num_cus() * occ, (tasks + (int64_t)kWaves * kM1pMaxBlocks - 1) /
+                                                                         ((int64_t)kWaves * kM1pMaxBlocks));
+        blocks = std::min<int64_t>(blocks, (tasks + kWaves - 1) / kWaves);
+        hipLaunchKernelGGL(fn_kernel, dim3((unsigned)blocks), dim3(kThreads), lds, st, W, X, bias, Y, N, K);
+        return 0;
+    };
+    BX_DISPATCH_FMT(wtype, {
+        if (M == 1) go(gemv_m1p_kernel<FMT_, 1>);
+        else if (M == 2) go(gemv_m1p_kernel<FMT_, 2>);
+        else if (M == 3) go(gemv_m1p_kernel<FMT_, 3>);
+        else go(gemv_m1p_kernel<FMT_, 4>);
+    })
+    return launch_check("gemv m1p");
+}
+
 int launch_gemv_m1(int wtype, const void* W, const uint16_t* X, const uint16_t* bias, uint16_t* Y, int N, int K,
                    hipStream_t st) {
     const int upl = upl_for(K);
     if (upl > 16) return fail(BX_EUNSUPPORTED, "gemv: K above 32768 at M = 1");
     if (K % 8192 == 0 && K > 16384) return gemv_m1_ksplit(wtype, W, X, bias, Y, nullptr, N, K, st);
-#ifndef EXP_M1P
-#define EXP_M1P 1
-#endif
-    if (EXP_M1P && upl == 1) {
-        // one round of resident workgroups, more where a wavefront would own
-        // more than kM1pMaxBlocks blocks
-        const int64_t tasks = ((int64_t)N + kM1pRows - 1) / kM1pRows;
-        const size_t lds1 = (size_t)K * 2 + (size_t)(K / 8) * 4 + (size_t)kWaves * kM1pMaxBlocks * kM1pRows * 4;
-        BX_DISPATCH_FMT(wtype, {
-            const void* fn = reinterpret_cast<const void*>(&gemv_m1p_kernel<FMT_>);
-            static int occ = 0;   // one per format (each case of the dispatch has its own)
-            if (occ == 0 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kThreads, lds1) != hipSuccess)
-                occ = 1;
-            if (occ < 1) occ = 1;
-            int64_t blocks = std::max<int64_t>((int64_t)num_cus() * occ,
-                                               (tasks + (int64_t)kWaves * kM1pMaxBlocks - 1) /
-                                                   ((int64_t)kWaves * kM1pMaxBlocks));
-            blocks = std::min<int64_t>(blocks, (tasks + kWaves - 1) / kWaves);
-            gemv_m1p_kernel<FMT_><<<(unsigned)blocks, kThreads, lds1, st>>>(W, X, bias, Y, N, K);
-        })
-        return launch_check("gemv m1p");
-    }
+    if (upl == 1) return launch_gemv_m1p(wtype, W, X, bias, Y, 1, N, K, st);
     const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
@@ -371,6 +403,7 @@ int launch_gemv_mr(int wtype, const void* W, const uint16_t* X, const uint16_t* 
                    int K, hipStream_t st) {
     if (!gemv_mr_ok(M, K)) return fail(BX_EUNSUPPORTED, "gemv: several-row kernel shape");
     const int upl = upl_for(K);
+    if (upl == 1) return launch_gemv_m1p(wtype, W, X, bias, Y, M, N, K, st);
     const int R = upl == 1 ? 4 : (upl == 2 ? 2 : 1);
     int64_t blocks = ((int64_t)N + (int64_t)kWaves * R - 1) / ((int64_t)kWaves * R);
     const int64_t cap = (int64_t)num_cus() * 8;
@@ -480,8 +513,9 @@ int gemv_f16(int wtype, const void* W, const uint16_t* bias, const uint16_t* X, 
     // measured (GEMV sweep, 151936 x 2048): the several-row kernel takes M = 2
     // in every quant format (Q4_K 69.6 -> 54.0 us) and M = 3 / 4 in Q6_K and
     // Q8_0 (Q8_0 at 3: 102.4 -> 73.3 us), where the matrix-core and per-row
-    // kernels pay more per weight; layer-sized matrices are launch-bound
-    // either way and keep their kernels
+    // kernels pay more per weight (Q4_K at 3 / 4 stays on the matrix cores:
+    // 55 against 58-66 us on the pipelined several-row kernel); layer-sized
+    // matrices are launch-bound either way and keep their kernels
     const bool big = (int64_t)N * K >= ((int64_t)32 << 20);
     if (big && wtype != BX_TYPE_F16 && gemv_mr_ok(M, K) && (M == 2 || wtype != BX_TYPE_Q4_K))
         return launch_gemv_mr(wtype, W, X, bias, Y, M, N, K, st);
