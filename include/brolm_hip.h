@@ -358,12 +358,19 @@ int bx_persist_status(const void* ws, uint32_t* site);
 /* Debug timing (no counterpart in the reference): while buf_dev is non-null,
  * every later bx_persist_step writes the device wall clock (wall_clock64, the
  * constant-rate counter) at each stage boundary of each workgroup into
- * buf_dev[wg * 1024 + slot]: slot 0 start, 1 + 10 l + {0 A input, 1 A done,
- * 2 B done, 3 C input, 4 C done, 5 D input, 6 D done, 7 E input, 8 E done},
- * 1 + 10 L + {0 head input, 1 head rows done, 2 step done (workgroup 0)};
- * for layer 14 also the attention sub-stages (900-907) and the gate/up
- * sub-stages (910 activation cached, 911 gate dots, 912 up dots, 913 all
- * waves done).  slots_per_wg must be >= 1024.  NULL switches it off. */
+ * buf_dev[wg * 1024 + slot] (wg = the dispatch's workgroup index).  The
+ * XCD-partitioned kernel (the default where it has an instantiation): slot 0
+ * start; 1 + 9 l + {0 A normed, 1 A words out, 2 B done, 3 C records
+ * combined, 4 C partials out, 5 D normed, 6 D words out, 7 E input, 8 E done};
+ * 1 + 9 L + {0 head input normed, 1 logits written, 2 step done (logical
+ * workgroup 0)}; for layer 14 the sub-stages at 600 + k; slot 1000 the
+ * workgroup's logical id (XCD + 8 rank).  The first persistent kernel: slot 0
+ * start, 1 + 10 l + {0 A input, 1 A done, 2 B done, 3 C input, 4 C done,
+ * 5 D input, 6 D done, 7 E input, 8 E done}, 1 + 10 L + {0 head input, 1 head
+ * rows done, 2 step done (workgroup 0)}; for layer 14 also the attention
+ * sub-stages (900-907) and the gate/up sub-stages (910 activation cached,
+ * 911 gate dots, 912 up dots, 913 all waves done).  slots_per_wg must be >=
+ * 1024.  NULL switches it off. */
 int bx_persist_trace(uint64_t* buf_dev, int slots_per_wg);
 
 /* Device greedy argmax over FP16 logits, lowest index wins ties
