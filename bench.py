@@ -30,7 +30,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
 
 STEP_DESC = {
-    "persistent": "persistent cooperative kernel, one launch per token",
+    "persistent": "persistent kernel, one launch per token",
     "graph": "hipGraph of the per-stage kernels, one launch per token",
     "eager": "per-stage kernels launched one by one",
 }

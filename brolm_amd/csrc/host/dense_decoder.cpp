@@ -5,6 +5,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
@@ -73,6 +74,7 @@ struct DecodeGraphSession {
     std::size_t pws_bytes = 0;
     bx_decode_layer* layers_dev = nullptr;
     uint32_t epoch = 0;
+    bool aborted = false;  // a persistent step gave up waiting; the caller redoes its steps
     // device-side sampled decoding: the sampler's workspace and the draws
     void* sample_ws = nullptr;
     double* draws = nullptr;
@@ -782,12 +784,38 @@ static void stage_step(DecodeGraphSession& s, int32_t token, int32_t pos) {
     hipx::check(hipEventRecord(s.staged, hipx::stream()), "hipEventRecord");
 }
 
-// False when the runtime refused the cooperative launch (nothing was
-// enqueued): it does so, for one, while another process holds a context on
-// the device, since it cannot then promise that the grid is co-resident.
+// After the launches so far completed: true when a persistent step gave up
+// on a wait (its abort flag is set).  A step gives up when its workgroups
+// are not all resident together, e.g. while another process's kernels hold
+// CUs; its outputs and every later step's are then invalid.  The words are
+// re-initialized, the session runs the per-stage graph from here on, and
+// s.aborted tells the caller to redo the steps it enqueued since its last
+// check (they rewrite the same cache rows).
+static bool persist_gave_up(DecodeGraphSession& s) {
+    hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
+    uint32_t site = 0;
+    const int st = bx_persist_status(s.pws, &site);
+    if (st < 0) hipx::bx(st, "persist status");
+    if (st == 0) return false;
+    hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
+    hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
+    std::fprintf(stderr, "brolm: persistent decode step gave up waiting at site %u; the per-stage graph runs from here on\n",
+                 site);
+    s.epoch = 0;
+    s.use_persist = false;
+    s.aborted = true;
+    return true;
+}
+
+// False when nothing was enqueued: the runtime refused the launch, or a step
+// of the ending epoch cycle gave up (s.aborted).
 static bool launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const bt::Tensor& final_norm,
                            const bt::Tensor& lm_head, const bt::Tensor& cos, const bt::Tensor& sin) {
-    if (++s.epoch >= 64) {  // a cycle of 16-bit tags is used up: re-initialize the words
+    if (++s.epoch >= 64) {
+        // a cycle of 16-bit tags is used up: re-initialize the words, which
+        // also clears the abort flag, so a step of this cycle that gave up is
+        // looked for first
+        if (persist_gave_up(s)) return false;
         hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
         s.epoch = 1;
     }
@@ -804,21 +832,14 @@ static bool launch_persist(DecodeGraphSession& s, const bt::Tensor& embed, const
     return true;
 }
 
-// After the launches completed: a persistent step that gave up on a wait
-// leaves its abort flag set.
-static void check_persist(DecodeGraphSession& s) {
-    if (!s.use_persist) return;
-    hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
-    uint32_t site = 0;
-    const int st = bx_persist_status(s.pws, &site);
-    if (st < 0) hipx::bx(st, "persist status");
-    if (st == 1) {
-        // the words now hold a partial step: re-initialize them so the next step starts clean
-        hipx::bx(bx_persist_ws_init(&s.dims, s.pws, hipx::stream()), "persist ws init");
-        hipx::check(hipStreamSynchronize(hipx::stream()), "hipStreamSynchronize");
-        s.epoch = 0;
-        fail("persistent decode step aborted waiting at site " + std::to_string(site));
-    }
+// After the launches completed: false when a persistent step gave up, so
+// the caller redoes the steps it enqueued since its last check, now on the
+// per-stage graph.
+static bool check_persist(DecodeGraphSession& s) {
+    if (s.use_persist) (void)persist_gave_up(s);
+    const bool ok = !s.aborted;
+    s.aborted = false;
+    return ok;
 }
 
 static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, const bt::Tensor& final_norm,
@@ -826,7 +847,7 @@ static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, 
     if (s.use_persist) {
         int i = 0;
         while (i < n && launch_persist(s, embed, final_norm, lm_head, cos, sin)) ++i;
-        if (i == n) return;
+        if (i == n || s.aborted) return;
         // refused: this session runs the per-stage graph from here on (same
         // step, same results to the decode tolerance; decode_mode() says so)
         s.use_persist = false;
@@ -854,13 +875,14 @@ static void launch_steps(DecodeGraphSession& s, int n, const bt::Tensor& embed, 
 
 void DenseDecoder::decode_step_(int32_t token, bt::Tensor& logits_out) {
     DecodeGraphSession& s = session_();
-    stage_step(s, token, cache_len_);
-    launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
-    resize_like(logits_out, 1, cfg_.vocab_size, bt::Dtype::FP16, bt::Device::ROCm);
-    hipx::check(hipMemcpyAsync(logits_out.data, s.logits, static_cast<std::size_t>(cfg_.vocab_size) * 2,
-                               hipMemcpyDeviceToDevice, hipx::stream()),
-                "copy logits");
-    check_persist(s);
+    do {
+        stage_step(s, token, cache_len_);
+        launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+        resize_like(logits_out, 1, cfg_.vocab_size, bt::Dtype::FP16, bt::Device::ROCm);
+        hipx::check(hipMemcpyAsync(logits_out.data, s.logits, static_cast<std::size_t>(cfg_.vocab_size) * 2,
+                                   hipMemcpyDeviceToDevice, hipx::stream()),
+                    "copy logits");
+    } while (!check_persist(s));
     cache_len_ += 1;
 }
 
@@ -894,9 +916,10 @@ int DenseDecoder::decode_greedy(int32_t token, int n, int32_t* out, int eos_id) 
     int32_t cur = token;
     while (done < n) {
         const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
-        stage_step(s, cur, cache_len_);
-        launch_steps(s, chunk, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
-        check_persist(s);
+        do {
+            stage_step(s, cur, cache_len_);
+            launch_steps(s, chunk, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+        } while (!check_persist(s));
         hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
         for (int i = 0; i < chunk; ++i) {
             if (eos_id >= 0 && out[done + i] == eos_id) {
@@ -949,19 +972,20 @@ int DenseDecoder::decode_sampled(int32_t token, int n, const double* u, float te
     int32_t cur = token;
     while (done < n) {
         const int chunk = std::min(n - done, static_cast<int>(DecodeGraphSession::kHist));
-        stage_step(s, cur, cache_len_);
-        hipx::check(hipMemcpyAsync(s.draws, u + done, static_cast<std::size_t>(chunk) * sizeof(double),
-                                   hipMemcpyHostToDevice, hipx::stream()),
-                    "upload draws");
-        for (int i = 0; i < chunk; ++i) {
-            // the fused step (its argmax advances token and history), then the
-            // draw replaces that token
-            launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
-            hipx::bx(bx_sample_feed_f16(s.logits, V, temperature, top_k, top_p, s.draws, s.scal + 0, s.scal + 4,
-                                        s.scal + 3, s.sample_ws, bt::stream()),
-                     "decode_sampled");
-        }
-        check_persist(s);
+        do {
+            stage_step(s, cur, cache_len_);
+            hipx::check(hipMemcpyAsync(s.draws, u + done, static_cast<std::size_t>(chunk) * sizeof(double),
+                                       hipMemcpyHostToDevice, hipx::stream()),
+                        "upload draws");
+            for (int i = 0; i < chunk && !s.aborted; ++i) {
+                // the fused step (its argmax advances token and history), then
+                // the draw replaces that token
+                launch_steps(s, 1, embed_tokens_, final_norm_, lm_head_, rope_cos_, rope_sin_);
+                hipx::bx(bx_sample_feed_f16(s.logits, V, temperature, top_k, top_p, s.draws, s.scal + 0,
+                                            s.scal + 4, s.scal + 3, s.sample_ws, bt::stream()),
+                         "decode_sampled");
+            }
+        } while (!check_persist(s));
         hipx::d2h(out + done, s.scal + 4, static_cast<std::size_t>(chunk) * sizeof(int32_t));
         for (int i = 0; i < chunk; ++i) {
             if (eos_id >= 0 && out[done + i] == eos_id) {
@@ -995,7 +1019,7 @@ double DenseDecoder::time_decode_steps(int32_t token, int n) {
     hipx::check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    check_persist(s);
+    if (!check_persist(s)) fail("time_decode_steps: a persistent step gave up waiting; the timing is void");
     cache_len_ += n;
     return static_cast<double>(ms) / n;
 }

@@ -2,8 +2,8 @@
 //
 // The whole L = 1 step of src/detail/dense_decoder.cpp:439-496 (run_layers_,
 // :526-681, at one token) — embedding, every layer, final norm, lm_head,
-// greedy argmax and the token feedback — runs as ONE cooperative launch with
-// one workgroup per CU.  Stages that the multi-kernel step separates with a
+// greedy argmax and the token feedback — runs as ONE launch with one
+// co-resident workgroup per CU.  Stages that the multi-kernel step separates with a
 // kernel boundary are separated here by dataflow: every vector a stage hands
 // to the next is written as 64-bit words {16-bit tag, three FP16 values} (or
 // {tag, one 32-bit value} for split records and argmax candidates) with
@@ -1596,15 +1596,15 @@ int p1_step(const bx_decode_dims* d, int n_layers, const bx_decode_layer* layers
             return bx::fail(BX_ELAUNCH, "persist: cannot raise the LDS limit");
     }
     void* args[] = {&a};
-    // Plain launch of the same grid, without the cooperative API, whenever a
-    // profiler tool is loaded (rocprofv3 has ended processes whose kernels
-    // were launched cooperatively with a segmentation fault in its exit
-    // path), or when BROLM_PERSIST_PLAIN_LAUNCH is set.  The occupancy check
-    // below is the one the cooperative launch makes (one workgroup per CU,
-    // grid = CU count), so the grid is co-resident on an otherwise idle
-    // device; every wait is also bounded and raises the abort flag, so the
-    // kernel ends either way.
-    static const bool plain = std::getenv("BROLM_PERSIST_PLAIN_LAUNCH") != nullptr || bx::profiler_attached();
+    // A plain launch of the grid after the occupancy check the cooperative
+    // launch makes (one workgroup per CU, grid = CU count), so the grid is
+    // co-resident on a device no other kernel holds, without the cooperative
+    // launch's cost (about 18 us a step).  Every wait is bounded and raises
+    // the abort flag, so the kernel ends either way.  BROLM_PERSIST_COOPERATIVE=1
+    // takes the cooperative launch, except under a profiler tool (rocprofv3
+    // has ended processes whose kernels were launched cooperatively with a
+    // segmentation fault in its exit path).
+    static const bool plain = std::getenv("BROLM_PERSIST_COOPERATIVE") == nullptr || bx::profiler_attached();
     hipError_t e;
     if (plain) {
         int per_cu = 0;

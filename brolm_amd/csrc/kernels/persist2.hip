@@ -2,7 +2,7 @@
 //
 // The L = 1 step of src/detail/dense_decoder.cpp:439-496 (run_layers_,
 // :526-681, at one token): embedding, every layer, final norm, lm_head,
-// greedy argmax and the token feedback, as ONE cooperative launch of 256
+// greedy argmax and the token feedback, as ONE launch of 256 co-resident
 // workgroups, one per CU: 32 on each of the 8 XCDs, each XCD with its own L2.
 // The dispatcher deals workgroups to the XCDs in turn, starting wherever the
 // previous launch left off, so a workgroup reads its XCD from HW_REG_XCC_ID
@@ -2001,13 +2001,17 @@ extern "C" int bx_persist_step(const bx_decode_dims* d, int n_layers, const bx_d
         return bx::fail(BX_ELAUNCH, "persist: cannot raise the LDS limit");
     void* args[] = {&a};
     hipStream_t st = bx::as_stream(stream);
-    // Plain launch of the same grid when a profiler tool is loaded (rocprofv3
+    // A plain launch of the grid after the occupancy check the cooperative
+    // launch makes (one workgroup per CU, grid = CU count): on a device that
+    // no other kernel holds the grid is resident at once, and the cooperative
+    // launch's own cost (15-18 us a step on the GPU's timeline) is saved.
+    // Every wait is bounded, so a grid that is not all resident (another
+    // process's kernels on the CUs) ends with the abort flag set, and the
+    // caller redoes the step another way.  BROLM_PERSIST_COOPERATIVE=1 takes
+    // the cooperative launch instead, except under a profiler tool (rocprofv3
     // has ended processes whose kernels were launched cooperatively with a
-    // segmentation fault in its exit path) or BROLM_PERSIST_PLAIN_LAUNCH is
-    // set: the occupancy check is the one the cooperative launch makes (one
-    // workgroup per CU, grid = CU count), and every wait is bounded, so the
-    // kernel ends either way.
-    static const bool plain = std::getenv("BROLM_PERSIST_PLAIN_LAUNCH") != nullptr || bx::profiler_attached();
+    // segmentation fault in its exit path).
+    static const bool plain = std::getenv("BROLM_PERSIST_COOPERATIVE") == nullptr || bx::profiler_attached();
     hipError_t e;
     if (plain) {
         int per_cu = 0;

@@ -336,7 +336,8 @@ int bx_decode_advance(int32_t* tok_dev, int32_t* pos_dev, const int32_t* next_de
 
 /* Persistent decode step: the same single-token step (embedding, all layers,
  * final norm, lm_head, greedy argmax, the feedback of bx_decode_advance) as
- * ONE cooperative launch with one workgroup per CU; stages hand vectors to
+ * ONE launch with one workgroup per CU (a plain launch after the cooperative
+ * launch's occupancy check; a grid that is not all resident aborts); stages hand vectors to
  * each other through tagged words in `ws` instead of kernel boundaries
  * (replaces the captured step of dense_decoder.cpp:335-524 as a whole).
  * bx_persist_ws_bytes returns 0 (with a message) for shapes/format mixes it
